@@ -1,0 +1,211 @@
+/* mamba_hip.h — C ABI of the MI355X (gfx950) Mamba-1 op library libmamba_hip.so.
+ *
+ * Plain C: raw device pointers, element strides, sizes and a HIP stream passed
+ * as `void*` (a hipStream_t; NULL = the null stream). No torch types. Every
+ * entry point is asynchronous on the given stream, allocates no memory and
+ * returns MCPU_OK or an error code; mcpu_last_error() then describes it.
+ * The caller owns every buffer, including workspaces sized by the matching
+ * *_workspace_size query (the reference's caller-owns-memory rule,
+ * csrc/selective_scan.h:14-20, 42-50).
+ *
+ * Storage types: "x-group" tensors (u, delta, z, out, dout, du, ddelta, dz for
+ * the scan; x, out, states for the conv; x, dt, z, out for the state update)
+ * share one storage type given by `dtype`; everything else is float32.
+ * Arithmetic is float32 throughout.
+ */
+#ifndef MAMBA_HIP_H_
+#define MAMBA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MCPU_OK = 0,
+  MCPU_ERR_INVALID = 1,     /* bad argument: shape, stride, null pointer, size */
+  MCPU_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. dstate > 64) */
+  MCPU_ERR_DEVICE = 3,      /* current device is not gfx950 */
+  MCPU_ERR_HIP = 4          /* a HIP runtime call or launch failed */
+};
+
+enum { MCPU_F32 = 0, MCPU_BF16 = 1, MCPU_F16 = 2 };
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* mcpu_last_error(void);
+
+/* Checks that the current HIP device is gfx950. Called by every entry point
+ * (result cached per device); exported so callers can fail early. */
+int mcpu_check_device(void);
+
+/* Library version string. */
+const char* mcpu_version(void);
+
+/* sizeof() of an argument block ("scan", "conv", "conv_update",
+ * "state_update"), 0 for an unknown name; lets bindings check their layout. */
+size_t mcpu_args_size(const char* name);
+
+/* ------------------------------------------------------------------------ */
+/* Selective scan.                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* One argument block for forward and backward. Field meaning follows the
+ * reference's SelectiveScanParams / SelectiveScanBwdParams
+ * (csrc/selective_scan.h:21-38, 51-63), with these differences:
+ *   - u/delta/z/dout may be any strided (batch, dim, seqlen) view;
+ *   - B/C may be any (batch, ngroups, seqlen, dstate) view with unit dstate
+ *     stride (the reference's kernel layout is the contiguous special case);
+ *   - dA, dD and ddelta_bias come back summed over the batch (the reference
+ *     returns per-batch partials that its Python side sums,
+ *     src/mamba_cpu/ops/selective_scan_interface.py:87);
+ *   - dB/dC are written, not accumulated (no zero-fill needed).
+ * Optional inputs/outputs are NULL when absent. */
+typedef struct mcpu_scan_args {
+  /* forward inputs */
+  const void* u;            /* (batch, dim, seqlen), dtype */
+  const void* delta;        /* (batch, dim, seqlen), dtype */
+  const float* A;           /* (dim, dstate) contiguous */
+  const float* B;           /* (batch, ngroups, seqlen, dstate), unit dstate stride */
+  const float* C;           /* same as B */
+  const float* D;           /* (dim), optional */
+  const void* z;            /* (batch, dim, seqlen), dtype, optional */
+  const float* delta_bias;  /* (dim), optional */
+  int64_t batch, dim, seqlen, dstate, ngroups;
+  int32_t delta_softplus;
+  int32_t dtype;            /* MCPU_F32 / MCPU_BF16 / MCPU_F16 for the x-group */
+  int64_t u_stride[3];      /* element strides over (batch, dim, seqlen) */
+  int64_t delta_stride[3];
+  int64_t z_stride[3];
+  int64_t B_stride[3];      /* element strides over (batch, group, seqlen) */
+  int64_t C_stride[3];
+  /* forward outputs */
+  void* out;                /* (batch, dim, seqlen) contiguous, dtype; NULL = states only */
+  float* last_state;        /* (batch, dim, dstate) contiguous, optional */
+  float* ckpt;              /* optional state checkpoints, see mcpu_selective_scan_ckpt_size */
+  /* backward inputs */
+  const void* dout;         /* (batch, dim, seqlen), dtype; NULL = zeros */
+  int64_t dout_stride[3];
+  const float* dlast_state; /* (batch, dim, dstate) contiguous, optional */
+  /* backward outputs (contiguous) */
+  void* du;                 /* (batch, dim, seqlen), dtype */
+  void* ddelta;             /* (batch, dim, seqlen), dtype */
+  void* dz;                 /* (batch, dim, seqlen), dtype; required iff z != NULL */
+  float* dA;                /* (dim, dstate) */
+  float* dB;                /* (batch, ngroups, seqlen, dstate) */
+  float* dC;                /* (batch, ngroups, seqlen, dstate) */
+  float* dD;                /* (dim); required iff D != NULL */
+  float* ddelta_bias;       /* (dim); required iff delta_bias != NULL */
+} mcpu_scan_args;
+
+/* Bytes of the optional checkpoint buffer: the float32 scan state at the
+ * start of every 16-step block, (batch, dim, ceil(seqlen/16), dstate).
+ * A forward call with ckpt != NULL fills it; a backward call with the same
+ * inputs and ckpt != NULL reads it instead of recomputing it. */
+size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a);
+
+/* Forward. Replaces selective_scan_fwd_f32 (csrc/selective_scan.h:40) as bound
+ * by _C.selective_scan_fwd_f32 (csrc/bindings.cpp:23-45). */
+int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* stream);
+
+/* Workspace bytes needed by mcpu_selective_scan_bwd for these arguments. */
+size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);
+
+/* Backward. Replaces selective_scan_bwd_f32 (csrc/selective_scan.h:65) as
+ * bound by _C.selective_scan_bwd_f32 (csrc/bindings.cpp:47-84). */
+int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Causal depthwise conv1d.                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces the F.conv1d paths of causal_conv1d_fn and its autograd
+ * (src/mamba_cpu/ops/causal_conv1d.py:16-53). */
+typedef struct mcpu_conv_args {
+  const void* x;                /* (batch, dim, seqlen), dtype, any strides */
+  const float* weight;          /* (dim, width) contiguous */
+  const float* bias;            /* (dim), optional */
+  const void* initial_states;   /* (batch, dim, width-1), dtype, optional */
+  int64_t batch, dim, seqlen, width;
+  int32_t silu;                 /* 1: out = silu(conv), 0: identity */
+  int32_t dtype;
+  int64_t x_stride[3];
+  int64_t init_stride[3];
+  /* forward outputs */
+  void* out;                    /* (batch, dim, seqlen), dtype, strides out_stride */
+  int64_t out_stride[3];
+  void* final_states;           /* (batch, dim, width-1) contiguous, dtype, optional */
+  /* backward */
+  const void* dout;             /* (batch, dim, seqlen), dtype, any strides */
+  int64_t dout_stride[3];
+  const void* dfinal_states;    /* (batch, dim, width-1) contiguous, dtype, optional */
+  void* dx;                     /* (batch, dim, seqlen), dtype, strides dx_stride */
+  int64_t dx_stride[3];
+  float* dweight;               /* (dim, width) */
+  float* dbias;                 /* (dim), required iff bias != NULL */
+  void* dinitial_states;        /* (batch, dim, width-1) contiguous, dtype; optional */
+} mcpu_conv_args;
+
+int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream);
+size_t mcpu_causal_conv1d_bwd_workspace_size(const mcpu_conv_args* a);
+int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Decode step(s), conv_state updated in place. Replaces causal_conv1d_update
+ * (src/mamba_cpu/ops/causal_conv1d.py:56-85). */
+typedef struct mcpu_conv_update_args {
+  const void* x;          /* (batch, dim, seqlen), dtype, any strides */
+  void* conv_state;       /* (batch, dim, state_len), dtype, any strides, state_len >= width-1 */
+  const float* weight;    /* (dim, width) contiguous */
+  const float* bias;      /* (dim), optional */
+  void* out;              /* (batch, dim, seqlen), dtype, strides out_stride */
+  int64_t batch, dim, seqlen, width, state_len;
+  int32_t silu;
+  int32_t dtype;
+  int64_t x_stride[3];
+  int64_t state_stride[3];
+  int64_t out_stride[3];
+} mcpu_conv_update_args;
+
+int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Selective state update (one decode step).                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces selective_state_update (src/mamba_cpu/ops/selective_state_update.py:5-57).
+ * Written for the Mamba-2 head layout; the Mamba-1 layout is the special case
+ * nheads = 1, headdim = dim, ngroups = 1. Heads are split into ngroups
+ * contiguous groups that share B/C. The state is updated in place. */
+typedef struct mcpu_state_update_args {
+  void* state;             /* (batch, nheads, headdim, dstate), state_dtype, unit dstate stride */
+  const void* x;           /* (batch, nheads, headdim), dtype */
+  const void* dt;          /* (batch, nheads, headdim), dtype */
+  const float* A;          /* (nheads, headdim, dstate) contiguous */
+  const float* B;          /* (batch, ngroups, dstate), unit dstate stride */
+  const float* C;          /* (batch, ngroups, dstate), unit dstate stride */
+  const float* D;          /* (nheads, headdim), optional */
+  const void* z;           /* (batch, nheads, headdim), dtype, optional */
+  const float* dt_bias;    /* (nheads, headdim), optional */
+  void* out;               /* (batch, nheads, headdim) contiguous, dtype */
+  int64_t batch, nheads, headdim, dstate, ngroups;
+  int32_t dt_softplus;
+  int32_t dtype;           /* storage type of x, dt, z, out */
+  int32_t state_dtype;     /* storage type of state */
+  int32_t _pad;
+  int64_t state_stride[3]; /* over (batch, head, headdim) */
+  int64_t x_stride[3];
+  int64_t dt_stride[3];
+  int64_t z_stride[3];
+  int64_t B_stride[2];     /* over (batch, group) */
+  int64_t C_stride[2];
+} mcpu_state_update_args;
+
+int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MAMBA_HIP_H_ */

@@ -1,0 +1,191 @@
+// C-ABI entry points for causal conv1d (forward, backward, decode update) and
+// the selective state update: argument checks, workspace layout, launches.
+#include <cstring>
+
+#include "abi_util.h"
+#include "mcpu_common.h"
+#include "op_params.h"
+
+namespace mcpu {
+
+namespace {
+
+int check_conv(const mcpu_conv_args* a) {
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d: null argument block");
+  if (a->x == nullptr || a->weight == nullptr)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d: x and weight are required");
+  if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d: negative size");
+  if (a->width < 1 || a->width > kConvMaxW)
+    return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d: width must be in [1, %lld], got %lld",
+                (long long)kConvMaxW, (long long)a->width);
+  if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "causal_conv1d: bad dtype %d", a->dtype);
+  return MCPU_OK;
+}
+
+ConvParams make_conv(const mcpu_conv_args* a) {
+  ConvParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.x = a->x;
+  p.w = a->weight;
+  p.bias = a->bias;
+  p.init = a->initial_states;
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.seqlen = a->seqlen;
+  p.width = a->width;
+  p.nchunks = (a->seqlen + kConvT - 1) / kConvT;
+  p.R = p.nchunks < kConvRMax ? (p.nchunks < 1 ? 1 : p.nchunks) : kConvRMax;
+  for (int i = 0; i < 3; ++i) {
+    p.sx[i] = a->x_stride[i];
+    p.sinit[i] = a->init_stride[i];
+    p.sout[i] = a->out_stride[i];
+    p.sdo[i] = a->dout_stride[i];
+    p.sdx[i] = a->dx_stride[i];
+  }
+  p.silu = a->silu != 0;
+  p.channels_last = (a->x_stride[1] == 1 && a->x_stride[2] != 1) ? 1 : 0;
+  return p;
+}
+
+size_t conv_ws(const ConvParams& p) {
+  return align_up(sizeof(float) * p.batch * p.R * p.dim * (p.width + 1));
+}
+
+}  // namespace
+}  // namespace mcpu
+
+using namespace mcpu;
+
+extern "C" int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream) {
+  clear_error();
+  if (int rc = check_conv(a)) return rc;
+  if (a->out == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d_fwd: out is required");
+  if (int rc = mcpu_check_device()) return rc;
+  ConvParams p = make_conv(a);
+  p.out = a->out;
+  p.final_states = a->final_states;
+  return hip_status(conv_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
+                    "causal_conv1d_fwd launch");
+}
+
+extern "C" size_t mcpu_causal_conv1d_bwd_workspace_size(const mcpu_conv_args* a) {
+  if (check_conv(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  return conv_ws(make_conv(a));
+}
+
+extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_conv(a)) return rc;
+  if (a->dout == nullptr || a->dx == nullptr || a->dweight == nullptr)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_bwd: dout, dx and dweight are required");
+  if (a->bias != nullptr && a->dbias == nullptr)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_bwd: dbias is required when bias is given");
+  ConvParams p = make_conv(a);
+  const size_t need = conv_ws(p);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_bwd: workspace of %zu bytes needed, got %zu", need,
+                workspace_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  p.dout = a->dout;
+  p.dfinal = a->dfinal_states;
+  p.dx = a->dx;
+  p.dinit = a->dinitial_states;
+  p.dw_part = static_cast<float*>(workspace);
+  if (a->batch == 0 || a->dim == 0) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (int rc = zero_f32(a->dweight, a->dim * a->width, st)) return rc;
+    if (a->dbias) return zero_f32(a->dbias, a->dim, st);
+    return MCPU_OK;
+  }
+  return hip_status(conv_bwd_launch(p, a->dtype, a->dweight, a->dbias, static_cast<hipStream_t>(stream)),
+                    "causal_conv1d_bwd launch");
+}
+
+extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* stream) {
+  clear_error();
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d_update: null argument block");
+  if (a->x == nullptr || a->conv_state == nullptr || a->weight == nullptr || a->out == nullptr)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: x, conv_state, weight and out are required");
+  if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: negative size");
+  if (a->width < 1 || a->width > kConvMaxW)
+    return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d_update: width must be in [1, %lld]",
+                (long long)kConvMaxW);
+  if (a->state_len < a->width - 1)
+    return fail(MCPU_ERR_INVALID, "conv_state length (%lld) must be at least width - 1 (%lld)",
+                (long long)a->state_len, (long long)(a->width - 1));
+  if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "causal_conv1d_update: bad dtype");
+  if (int rc = mcpu_check_device()) return rc;
+  ConvUpdateParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.x = a->x;
+  p.state = a->conv_state;
+  p.w = a->weight;
+  p.bias = a->bias;
+  p.out = a->out;
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.seqlen = a->seqlen;
+  p.width = a->width;
+  p.state_len = a->state_len;
+  for (int i = 0; i < 3; ++i) {
+    p.sx[i] = a->x_stride[i];
+    p.sst[i] = a->state_stride[i];
+    p.sout[i] = a->out_stride[i];
+  }
+  p.silu = a->silu != 0;
+  return hip_status(conv_update_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
+                    "causal_conv1d_update launch");
+}
+
+extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream) {
+  clear_error();
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "selective_state_update: null argument block");
+  if (a->state == nullptr || a->x == nullptr || a->dt == nullptr || a->A == nullptr ||
+      a->B == nullptr || a->C == nullptr || a->out == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_state_update: state, x, dt, A, B, C and out are required");
+  if (a->batch < 0 || a->nheads < 0 || a->headdim < 0)
+    return fail(MCPU_ERR_INVALID, "selective_state_update: negative size");
+  if (a->dstate < 1 || a->dstate > 256)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_state_update: dstate must be in [1, 256]");
+  if (a->ngroups < 1 || (a->nheads > 0 && a->nheads % a->ngroups != 0))
+    return fail(MCPU_ERR_INVALID, "selective_state_update: nheads must be divisible by ngroups");
+  if (!valid_dtype(a->dtype) || !valid_dtype(a->state_dtype))
+    return fail(MCPU_ERR_INVALID, "selective_state_update: bad dtype");
+  if (int rc = mcpu_check_device()) return rc;
+  StateUpdateParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.state = a->state;
+  p.x = a->x;
+  p.dt = a->dt;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.D = a->D;
+  p.z = a->z;
+  p.dt_bias = a->dt_bias;
+  p.out = a->out;
+  p.batch = a->batch;
+  p.nheads = a->nheads;
+  p.headdim = a->headdim;
+  p.dstate = a->dstate;
+  p.ngroups = a->ngroups;
+  for (int i = 0; i < 3; ++i) {
+    p.sst[i] = a->state_stride[i];
+    p.sx[i] = a->x_stride[i];
+    p.sdt[i] = a->dt_stride[i];
+    p.sz[i] = a->z_stride[i];
+  }
+  for (int i = 0; i < 2; ++i) {
+    p.sB[i] = a->B_stride[i];
+    p.sC[i] = a->C_stride[i];
+  }
+  p.softplus = a->dt_softplus != 0;
+  return hip_status(state_update_launch(p, a->dtype, a->state_dtype, static_cast<hipStream_t>(stream)),
+                    "selective_state_update launch");
+}

@@ -1,0 +1,205 @@
+// C-ABI entry points for the selective scan: argument checks, workspace
+// layout and kernel sequencing. No allocation happens here; every buffer comes
+// from the caller.
+#include <cstdio>
+#include <cstring>
+
+#include "abi_util.h"
+#include "scan_common.h"
+
+namespace mcpu {
+hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
+hipError_t scan_bwd_launch(const ScanParams& p, int dtype, hipStream_t stream);
+hipError_t scan_reduce_bc_launch(const float* part, float* out, int64_t slices, int64_t nblk_c,
+                                 int64_t per_slice, hipStream_t stream);
+hipError_t scan_reduce_batch_launch(const float* part, float* out, int64_t batch,
+                                    int64_t per_batch, hipStream_t stream);
+
+namespace {
+
+int check_scan(const mcpu_scan_args* a) {
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "selective_scan: null argument block");
+  if (a->u == nullptr || a->delta == nullptr || a->A == nullptr || a->B == nullptr ||
+      a->C == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_scan: u, delta, A, B and C are required");
+  if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
+    return fail(MCPU_ERR_INVALID, "selective_scan: negative size");
+  if (a->ngroups < 1 || (a->dim > 0 && a->dim % a->ngroups != 0))
+    return fail(MCPU_ERR_INVALID, "selective_scan: dim (%lld) must be divisible by ngroups (%lld)",
+                (long long)a->dim, (long long)a->ngroups);
+  if (a->dstate < 1 || a->dstate > 64)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, 64], got %lld",
+                (long long)a->dstate);
+  if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "selective_scan: bad dtype %d", a->dtype);
+  const int64_t dpg = a->dim / a->ngroups;
+  const int64_t blocks = a->batch * a->ngroups * ((dpg + kScanChannelsPerWG - 1) / kScanChannelsPerWG);
+  if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
+  return MCPU_OK;
+}
+
+ScanParams make_params(const mcpu_scan_args* a) {
+  ScanParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.u = a->u;
+  p.delta = a->delta;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.D = a->D;
+  p.z = a->z;
+  p.delta_bias = a->delta_bias;
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.seqlen = a->seqlen;
+  p.dstate = a->dstate;
+  p.ngroups = a->ngroups;
+  p.dpg = a->dim / a->ngroups;
+  p.nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
+  p.nblk_c = (p.dpg + kScanChannelsPerWG - 1) / kScanChannelsPerWG;
+  for (int i = 0; i < 3; ++i) {
+    p.su[i] = a->u_stride[i];
+    p.sdl[i] = a->delta_stride[i];
+    p.sz[i] = a->z_stride[i];
+    p.sB[i] = a->B_stride[i];
+    p.sC[i] = a->C_stride[i];
+    p.sdo[i] = a->dout_stride[i];
+  }
+  p.softplus = a->delta_softplus != 0;
+  return p;
+}
+
+struct BwdLayout {
+  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, total = 0;
+  bool own_ckpt = false, part_bc = false, part_dA = false;
+};
+
+BwdLayout bwd_layout(const mcpu_scan_args* a) {
+  const ScanParams p = make_params(a);
+  BwdLayout w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.own_ckpt = a->ckpt == nullptr;
+  if (w.own_ckpt) w.ckpt = take(sizeof(float) * p.batch * p.dim * p.nblk * p.dstate);
+  w.part_bc = p.nblk_c > 1;
+  if (w.part_bc) {
+    const size_t bc = sizeof(float) * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.dstate;
+    w.dB = take(bc);
+    w.dC = take(bc);
+  }
+  w.part_dA = p.batch > 1;
+  if (w.part_dA) w.dA = take(sizeof(float) * p.batch * p.dim * p.dstate);
+  w.dD = take(sizeof(float) * p.batch * p.dim);
+  w.dbias = take(sizeof(float) * p.batch * p.dim);
+  w.total = off;
+  return w;
+}
+
+}  // namespace
+}  // namespace mcpu
+
+using namespace mcpu;
+
+extern "C" size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a) {
+  if (a == nullptr || a->batch < 0 || a->dim < 0 || a->seqlen < 0 || a->dstate < 0) return 0;
+  const int64_t nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
+  return sizeof(float) * a->batch * a->dim * nblk * a->dstate;
+}
+
+extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* stream) {
+  clear_error();
+  if (int rc = check_scan(a)) return rc;
+  if (int rc = mcpu_check_device()) return rc;
+  if (a->batch == 0 || a->dim == 0) return MCPU_OK;
+  const ScanParams p0 = make_params(a);
+  ScanParams p = p0;
+  p.out = a->out;
+  p.last_state = a->last_state;
+  p.ckpt = a->ckpt;
+  if (p.out == nullptr && p.last_state == nullptr && p.ckpt == nullptr) return MCPU_OK;
+  return hip_status(scan_fwd_launch(p, a->dtype, a->out != nullptr, static_cast<hipStream_t>(stream)),
+                    "selective_scan_fwd launch");
+}
+
+extern "C" size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a) {
+  if (check_scan(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  return bwd_layout(a).total;
+}
+
+extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_scan(a)) return rc;
+  if (a->du == nullptr || a->ddelta == nullptr || a->dA == nullptr || a->dB == nullptr ||
+      a->dC == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: du, ddelta, dA, dB and dC are required");
+  if (a->z != nullptr && a->dz == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: dz is required when z is given");
+  if (a->D != nullptr && a->dD == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: dD is required when D is given");
+  if (a->delta_bias != nullptr && a->ddelta_bias == nullptr)
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: ddelta_bias is required when delta_bias is given");
+  const BwdLayout w = bwd_layout(a);
+  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: workspace of %zu bytes needed, got %zu",
+                w.total, workspace_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->batch == 0 || a->dim == 0) {
+    // Empty batch/channel set: parameter grads are zero.
+    if (int rc = zero_f32(a->dA, a->dim * a->dstate, st)) return rc;
+    if (a->dD) if (int rc = zero_f32(a->dD, a->dim, st)) return rc;
+    if (a->ddelta_bias) if (int rc = zero_f32(a->ddelta_bias, a->dim, st)) return rc;
+    return MCPU_OK;
+  }
+  char* ws = static_cast<char*>(workspace);
+  ScanParams p = make_params(a);
+  p.ckpt = w.own_ckpt ? reinterpret_cast<float*>(ws + w.ckpt) : a->ckpt;
+  if (w.own_ckpt) {
+    ScanParams pf = p;  // states-only forward to produce the block checkpoints
+    if (int rc = hip_status(scan_fwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
+      return rc;
+  }
+  p.dout = a->dout;
+  p.dlast_state = a->dlast_state;
+  p.du = a->du;
+  p.ddelta = a->ddelta;
+  p.dz = a->dz;
+  p.dB_part = w.part_bc ? reinterpret_cast<float*>(ws + w.dB) : a->dB;
+  p.dC_part = w.part_bc ? reinterpret_cast<float*>(ws + w.dC) : a->dC;
+  p.dA_part = w.part_dA ? reinterpret_cast<float*>(ws + w.dA) : a->dA;
+  p.dD_part = reinterpret_cast<float*>(ws + w.dD);
+  p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
+  if (int rc = hip_status(scan_bwd_launch(p, a->dtype, st), "selective_scan_bwd launch")) return rc;
+  if (w.part_bc) {
+    const int64_t slices = p.batch * p.ngroups, per = p.seqlen * p.dstate;
+    if (int rc = hip_status(scan_reduce_bc_launch(p.dB_part, a->dB, slices, p.nblk_c, per, st),
+                            "selective_scan_bwd dB reduce"))
+      return rc;
+    if (int rc = hip_status(scan_reduce_bc_launch(p.dC_part, a->dC, slices, p.nblk_c, per, st),
+                            "selective_scan_bwd dC reduce"))
+      return rc;
+  }
+  if (w.part_dA) {
+    if (int rc = hip_status(scan_reduce_batch_launch(p.dA_part, a->dA, p.batch, p.dim * p.dstate, st),
+                            "selective_scan_bwd dA reduce"))
+      return rc;
+  }
+  if (a->dD != nullptr) {
+    if (int rc = hip_status(scan_reduce_batch_launch(p.dD_part, a->dD, p.batch, p.dim, st),
+                            "selective_scan_bwd dD reduce"))
+      return rc;
+  }
+  if (a->ddelta_bias != nullptr) {
+    if (int rc = hip_status(scan_reduce_batch_launch(p.dbias_part, a->ddelta_bias, p.batch, p.dim, st),
+                            "selective_scan_bwd ddelta_bias reduce"))
+      return rc;
+  }
+  return MCPU_OK;
+}

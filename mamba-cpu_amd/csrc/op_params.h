@@ -1,0 +1,68 @@
+// Kernel parameter blocks for the conv1d and state-update kernels, shared by
+// the kernels and the C-ABI layer that fills them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mcpu {
+
+constexpr int kConvT = 8;      // conv steps per chunk
+constexpr int kConvMaxW = 16;  // largest supported conv width
+constexpr int kConvRMax = 16;  // most threads walking one (batch, channel) row
+
+struct ConvParams {
+  const void* x;
+  const float* w;
+  const float* bias;
+  const void* init;
+  void* out;
+  void* final_states;
+  const void* dout;
+  const void* dfinal;
+  void* dx;
+  void* dinit;
+  float* dw_part;   // (batch, R, dim, W + 1): per-thread partial dw and dbias
+  int64_t batch, dim, seqlen, width;
+  int64_t nchunks, R;
+  int64_t sx[3], sinit[3], sout[3], sdo[3], sdx[3];
+  int silu;
+  int channels_last;  // thread index decomposed channel-fastest
+};
+
+struct ConvUpdateParams {
+  const void* x;
+  void* state;
+  const float* w;
+  const float* bias;
+  void* out;
+  int64_t batch, dim, seqlen, width, state_len;
+  int64_t sx[3], sst[3], sout[3];
+  int silu;
+};
+
+struct StateUpdateParams {
+  void* state;
+  const void* x;
+  const void* dt;
+  const float* A;
+  const float* B;
+  const float* C;
+  const float* D;
+  const void* z;
+  const float* dt_bias;
+  void* out;
+  int64_t batch, nheads, headdim, dstate, ngroups;
+  int64_t sst[3], sx[3], sdt[3], sz[3], sB[2], sC[2];
+  int softplus;
+};
+
+hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st);
+hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float* dbias,
+                           hipStream_t st);
+hipError_t conv_update_launch(const ConvUpdateParams& p, int dtype, hipStream_t st);
+hipError_t state_update_launch(const StateUpdateParams& p, int dtype, int state_dtype,
+                               hipStream_t st);
+
+}  // namespace mcpu

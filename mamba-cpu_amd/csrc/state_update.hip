@@ -1,0 +1,94 @@
+// Selective state update (one decode step) on gfx950.
+//
+// Per row (batch, head, p) and state n (reference
+// src/mamba_cpu/ops/selective_state_update.py:5-57):
+//   dt    = softplus?(dt + dt_bias)
+//   state = state * exp(dt * A) + dt * x * B[group]
+//   out   = (<state, C[group]> + D * x) * silu(z)
+// Same lane layout as the scan: 16 state lanes per row, 4 rows per wave, so a
+// 256-thread workgroup updates 16 rows; the <state, C> sum is a DPP row
+// all-reduce. The state is read and written in place.
+#include "mcpu_common.h"
+#include "op_params.h"
+
+namespace mcpu {
+
+template <typename Tx, typename Ts, int SPL>
+__global__ void __launch_bounds__(256) state_update_kernel(const StateUpdateParams p) {
+  const int j = threadIdx.x & 15;
+  const int64_t rowid = blockIdx.x * 16ll + (threadIdx.x >> 4);
+  const int64_t rows = p.batch * p.nheads * p.headdim;
+  // Whole rows of 16 lanes share the branch, so the DPP reduction below never
+  // mixes live and retired lanes of one row.
+  if (rowid >= rows) return;
+  const int64_t pp = rowid % p.headdim;
+  const int64_t h = (rowid / p.headdim) % p.nheads;
+  const int64_t b = rowid / (p.headdim * p.nheads);
+  const int64_t g = h / (p.nheads / p.ngroups);
+  const int64_t N = p.dstate;
+  const int64_t hp = h * p.headdim + pp;  // index into (nheads, headdim) parameters
+
+  const float x = ld<Tx>(p.x, b * p.sx[0] + h * p.sx[1] + pp * p.sx[2]);
+  float dt = ld<Tx>(p.dt, b * p.sdt[0] + h * p.sdt[1] + pp * p.sdt[2]);
+  if (p.dt_bias != nullptr) dt += p.dt_bias[hp];
+  if (p.softplus) dt = softplus(dt);
+  const float dtx = dt * x;
+  const int64_t sbase = b * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < SPL; ++s) {
+    const int n = j + 16 * s;
+    if (n < N) {
+      const float a = fast_exp(dt * p.A[hp * N + n]);
+      const float Bn = p.B[b * p.sB[0] + g * p.sB[1] + n];
+      const float Cn = p.C[b * p.sC[0] + g * p.sC[1] + n];
+      const float sv = fmaf(ld<Ts>(p.state, sbase + n), a, dtx * Bn);
+      st<Ts>(p.state, sbase + n, sv);
+      acc = fmaf(sv, Cn, acc);
+    }
+  }
+  float y = row_allreduce16(acc);
+  if (j == 0) {
+    if (p.D != nullptr) y = fmaf(x, p.D[hp], y);
+    if (p.z != nullptr) {
+      const float zz = ld<Tx>(p.z, b * p.sz[0] + h * p.sz[1] + pp * p.sz[2]);
+      y *= zz * sigmoid(zz);
+    }
+    st<Tx>(p.out, rowid, y);
+  }
+}
+
+template <typename Tx, typename Ts>
+static hipError_t launch_su(const StateUpdateParams& p, hipStream_t st) {
+  const int64_t rows = p.batch * p.nheads * p.headdim;
+  const unsigned blocks = static_cast<unsigned>((rows + 15) / 16);
+  if (p.dstate <= 16)
+    hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 1>), dim3(blocks), dim3(256), 0, st, p);
+  else if (p.dstate <= 32)
+    hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 2>), dim3(blocks), dim3(256), 0, st, p);
+  else if (p.dstate <= 64)
+    hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 4>), dim3(blocks), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 16>), dim3(blocks), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename Tx>
+static hipError_t launch_su_state(const StateUpdateParams& p, int state_dtype, hipStream_t st) {
+  switch (state_dtype) {
+    case MCPU_F32: return launch_su<Tx, float>(p, st);
+    case MCPU_BF16: return launch_su<Tx, bf16>(p, st);
+    default: return launch_su<Tx, f16>(p, st);
+  }
+}
+
+hipError_t state_update_launch(const StateUpdateParams& p, int dtype, int state_dtype, hipStream_t st) {
+  if (p.batch * p.nheads * p.headdim == 0) return hipSuccess;
+  switch (dtype) {
+    case MCPU_F32: return launch_su_state<float>(p, state_dtype, st);
+    case MCPU_BF16: return launch_su_state<bf16>(p, state_dtype, st);
+    default: return launch_su_state<f16>(p, state_dtype, st);
+  }
+}
+
+}  // namespace mcpu

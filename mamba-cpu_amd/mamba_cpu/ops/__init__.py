@@ -1,0 +1,10 @@
+from mamba_cpu.ops.causal_conv1d import causal_conv1d_fn, causal_conv1d_update
+from mamba_cpu.ops.selective_scan_interface import selective_scan_fn
+from mamba_cpu.ops.selective_state_update import selective_state_update
+
+__all__ = [
+    "causal_conv1d_fn",
+    "causal_conv1d_update",
+    "selective_scan_fn",
+    "selective_state_update",
+]

@@ -1,0 +1,74 @@
+"""Readable pure-PyTorch definitions of the selective scan and the causal
+conv1d, kept for API compatibility with the reference package
+(src/mamba_cpu/reference.py:10-75 exports selective_scan_ref and
+causal_conv1d_ref). They run on any device, loop over time in Python, and no op
+of this package calls them.
+"""
+
+import torch
+import torch.nn.functional as F
+
+
+def selective_scan_ref(
+    u,
+    delta,
+    A,
+    B,
+    C,
+    D=None,
+    z=None,
+    delta_bias=None,
+    delta_softplus=False,
+    return_last_state=False,
+):
+    """
+    u, delta, z: (batch, dim, seqlen)
+    A: (dim, dstate)
+    B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen)
+    D, delta_bias: (dim,)
+    Returns out: (batch, dim, seqlen) [, last_state: (batch, dim, dstate)]
+
+    h_t = exp(dt_t A) h_{t-1} + dt_t u_t B_t ; y_t = <h_t, C_t> + D u_t ;
+    out = y * silu(z), with dt = softplus?(delta + delta_bias), in float32.
+    """
+    in_dtype = u.dtype
+    u = u.float()
+    dt = delta.float()
+    if delta_bias is not None:
+        dt = dt + delta_bias.float()[:, None]
+    if delta_softplus:
+        dt = F.softplus(dt)
+    batch, dim, seqlen = u.shape
+    A = A.float()
+    Bg = B.float() if B.dim() == 4 else B.float()[:, None]
+    Cg = C.float() if C.dim() == 4 else C.float()[:, None]
+    per_group = dim // Bg.shape[1]
+    Bd = Bg.repeat_interleave(per_group, dim=1)  # (batch, dim, dstate, seqlen)
+    Cd = Cg.repeat_interleave(per_group, dim=1)
+    h = u.new_zeros(batch, dim, A.shape[1])
+    ys = []
+    for t in range(seqlen):
+        h = torch.exp(dt[:, :, t, None] * A) * h + (dt[:, :, t] * u[:, :, t])[..., None] * Bd[..., t]
+        ys.append((h * Cd[..., t]).sum(-1))
+    y = torch.stack(ys, dim=-1) if ys else u.new_zeros(batch, dim, 0)
+    if D is not None:
+        y = y + D.float()[:, None] * u
+    if z is not None:
+        y = y * F.silu(z.float())
+    y = y.to(in_dtype)
+    return (y, h) if return_last_state else y
+
+
+def causal_conv1d_ref(x, weight, bias=None, activation=None):
+    """x: (batch, dim, seqlen), weight: (dim, width). One term per tap."""
+    width = weight.shape[1]
+    seqlen = x.shape[-1]
+    xp = F.pad(x, (width - 1, 0))
+    out = torch.zeros_like(x)
+    for k in range(width):
+        out = out + weight[:, k, None] * xp[..., k:k + seqlen]
+    if bias is not None:
+        out = out + bias[:, None]
+    if activation in ("silu", "swish"):
+        out = F.silu(out)
+    return out

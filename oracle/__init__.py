@@ -1,0 +1,28 @@
+"""CPU oracle for the Mamba-1 op set — TEST INFRASTRUCTURE ONLY.
+
+Nothing in the product (`mamba-cpu_amd/`) imports, links or runs anything here.
+Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` use it, and only as the checker / the timed CPU reference.
+
+Contents
+  oracle.numerics  float64 numpy restatement of the reference's algorithms
+                   (forward and analytic backward of the selective scan,
+                   causal conv1d forward/backward/update, state update).
+  oracle.ref       ctypes loader for oracle/_ref/libmcpu_ref.so, the
+                   reference's own C++ CPU kernels compiled from the reference
+                   sources by oracle/Makefile.
+
+Pinning (how each oracle function is checked, so a plausible mistake fails):
+  scan forward      vs the compiled reference (_ref) on random inputs; closed
+                    forms (delta=0 -> out = D*u; A=-inf -> memoryless state;
+                    dstate=1 hand recurrence); NaN confinement.
+  scan backward     vs the compiled reference (_ref); vs torch.autograd through
+                    an independent float64 forward; central finite differences.
+  conv forward      vs numpy.convolve per channel (textbook routine);
+                    initial/final-state chaining invariants.
+  conv backward     vs torch.autograd through F.conv1d in float64.
+  conv update       update steps == full conv (invariant); state == last inputs.
+  state update      L single steps == full scan (whose oracle is pinned above);
+                    multi-head layout == flattened layout.
+Every function is pinned; none is "parity unpinned".
+"""

@@ -1,0 +1,276 @@
+"""Float64 numpy restatement of the reference's Mamba-1 algorithms.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Inputs may be numpy arrays
+or CPU torch tensors; everything is computed in float64 and returned as numpy
+float64 arrays.
+
+Layouts follow the reference's public API (README.md:60-67):
+  u, delta, z, dout : (batch, dim, seqlen)
+  A                 : (dim, dstate)
+  B, C              : (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen)
+  D, delta_bias     : (dim,)
+Channels are split into contiguous groups sharing B/C
+(csrc/selective_scan.cpp:99: slice = b * ngroups + d / (dim / ngroups)).
+"""
+
+import numpy as np
+
+
+def _f64(x):
+    if x is None:
+        return None
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().double().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+def softplus(x):
+    """softplus with torch's default threshold 20 (csrc/selective_scan.cpp:44-45)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return np.where(x <= 20.0, np.log1p(np.exp(np.minimum(x, 20.0))), x)
+
+
+def sigmoid(x):
+    """csrc/selective_scan.cpp:47."""
+    with np.errstate(over="ignore"):
+        return 1.0 / (1.0 + np.exp(-x))
+
+
+def _groups(X, dim):
+    """(b, n, l) | (b, g, n, l) -> (b, g, n, l) plus channels-per-group."""
+    X = _f64(X)
+    if X.ndim == 3:
+        X = X[:, None]
+    g = X.shape[1]
+    return X, dim // g
+
+
+def _dt(delta, delta_bias, delta_softplus):
+    """row_dt (csrc/selective_scan.cpp:112-115): softplus?(delta + bias)."""
+    dt = delta if delta_bias is None else delta + delta_bias[None, :, None]
+    return softplus(dt) if delta_softplus else dt
+
+
+def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False):
+    """Forward scan. Follows fwd_row_body (csrc/selective_scan.cpp:120-145) and
+    selective_scan_ref (src/mamba_cpu/reference.py:10-62):
+        dt_t = softplus?(delta_t + bias)
+        h_t  = exp(dt_t * A) * h_{t-1} + dt_t * u_t * B_t       (h_{-1} = 0)
+        y_t  = <h_t, C_t> + D * u_t ;  out_t = y_t * silu(z_t)
+    Returns (out, last_state) with last_state = h_{L-1}, shape (b, d, n)."""
+    u, delta, A = _f64(u), _f64(delta), _f64(A)
+    D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
+    batch, dim, seqlen = u.shape
+    B, dpg = _groups(B, dim)
+    C, _ = _groups(C, dim)
+    dt = _dt(delta, delta_bias, delta_softplus)
+    h = np.zeros((batch, dim, A.shape[1]))
+    y = np.zeros((batch, dim, seqlen))
+    with np.errstate(over="ignore", invalid="ignore"):
+        for t in range(seqlen):
+            Bt = np.repeat(B[:, :, :, t], dpg, axis=1)  # (b, d, n)
+            Ct = np.repeat(C[:, :, :, t], dpg, axis=1)
+            a = np.exp(dt[:, :, t, None] * A[None])
+            h = a * h + (dt[:, :, t] * u[:, :, t])[..., None] * Bt
+            y[:, :, t] = (h * Ct).sum(-1)
+        out = y if D is None else y + D[None, :, None] * u
+        if z is not None:
+            out = out * z * sigmoid(z)
+    return out, h
+
+
+def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                       dout=None, dlast_state=None):
+    """Analytic backward, restating bwd_row_body (csrc/selective_scan.cpp:168-248)
+    in float64 and vectorised over (batch, dim, dstate):
+        recompute h_t for all t (:181-190), then for t = L-1 .. 0 (:200-243)
+          y  = <h_t, C_t> + D u ; dz = dout * y * s(z) (1 + z (1 - s(z))) ; dy = dout * z * s(z)
+          g  = gh + dy C_t ; dC_t += dy h_t ; a = exp(dt A) ; ga = g h_{t-1} a
+          dA += ga dt ; ddt += ga A + g u B_t ; dB_t += g dt u ; gh = g a
+          du = dy D + dt <g, B_t> ; ddt *= sigmoid(delta + bias) if softplus
+    gh starts at dlast_state (:193-196). dA, dD and ddelta_bias are summed over
+    the batch (the reference returns per-batch partials that its Python side
+    sums, selective_scan_interface.py:87).
+    Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias) with dB/dC in B/C's
+    layout; dD / dz / ddelta_bias are None when D / z / delta_bias are None."""
+    u, delta, A = _f64(u), _f64(delta), _f64(A)
+    D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
+    dout, dlast_state = _f64(dout), _f64(dlast_state)
+    bc3 = _f64(B).ndim == 3
+    batch, dim, seqlen = u.shape
+    N = A.shape[1]
+    B, dpg = _groups(B, dim)
+    C, _ = _groups(C, dim)
+    G = B.shape[1]
+    if dout is None:
+        dout = np.zeros_like(u)
+    dt = _dt(delta, delta_bias, delta_softplus)
+    pre = delta if delta_bias is None else delta + delta_bias[None, :, None]
+    Dv = np.zeros(dim) if D is None else D
+
+    with np.errstate(over="ignore", invalid="ignore"):
+        hs = np.zeros((seqlen + 1, batch, dim, N))  # hs[t + 1] = h_t, hs[0] = 0
+        for t in range(seqlen):
+            Bt = np.repeat(B[:, :, :, t], dpg, axis=1)
+            hs[t + 1] = np.exp(dt[:, :, t, None] * A[None]) * hs[t] + \
+                (dt[:, :, t] * u[:, :, t])[..., None] * Bt
+
+        gh = np.zeros((batch, dim, N)) if dlast_state is None else dlast_state.copy()
+        du = np.zeros_like(u)
+        ddelta = np.zeros_like(u)
+        dz = None if z is None else np.zeros_like(u)
+        dA = np.zeros((batch, dim, N))
+        dB = np.zeros((batch, G, N, seqlen))
+        dC = np.zeros((batch, G, N, seqlen))
+        for t in range(seqlen - 1, -1, -1):
+            Bt = np.repeat(B[:, :, :, t], dpg, axis=1)
+            Ct = np.repeat(C[:, :, :, t], dpg, axis=1)
+            h, h_prev = hs[t + 1], hs[t]
+            ut, dtt = u[:, :, t], dt[:, :, t]
+            dy = dout[:, :, t]
+            if z is not None:
+                y = (h * Ct).sum(-1) + Dv[None] * ut
+                zt = z[:, :, t]
+                sg = sigmoid(zt)
+                dz[:, :, t] = dout[:, :, t] * y * sg * (1 + zt * (1 - sg))
+                dy = dout[:, :, t] * zt * sg
+            g = gh + dy[..., None] * Ct
+            dCc = dy[..., None] * h
+            a = np.exp(dtt[..., None] * A[None])
+            ga = g * h_prev * a
+            dA += ga * dtt[..., None]
+            ddt = (ga * A[None]).sum(-1) + ut * (g * Bt).sum(-1)
+            dBc = g * (dtt * ut)[..., None]
+            du[:, :, t] = dy * Dv[None] + dtt * (g * Bt).sum(-1)
+            if delta_softplus:
+                ddt = ddt * sigmoid(pre[:, :, t])
+            ddelta[:, :, t] = ddt
+            gh = g * a
+            dB[:, :, :, t] = dBc.reshape(batch, G, dpg, N).sum(2)
+            dC[:, :, :, t] = dCc.reshape(batch, G, dpg, N).sum(2)
+        dD_full = None
+        if D is not None:
+            dy_all = dout if z is None else dout * z * sigmoid(z)
+            dD_full = (dy_all * u).sum((0, 2))
+        ddelta_bias = None if delta_bias is None else ddelta.sum((0, 2))
+    if bc3:
+        dB, dC = dB[:, 0], dC[:, 0]
+    return du, ddelta, dA.sum(0), dB, dC, dD_full, dz, ddelta_bias
+
+
+def causal_conv1d_fwd(x, weight, bias=None, initial_states=None, activation=None):
+    """Depthwise causal conv (src/mamba_cpu/ops/causal_conv1d.py:16-53 and the
+    explicit tap loop of src/mamba_cpu/reference.py:65-75):
+        x_full = [initial_states or zeros(width-1), x]
+        out_t  = act(bias + sum_k w[k] * x_full[t + k])
+    Returns (out, final_states) with final_states = last width-1 columns of x_full."""
+    x, w, bias, init = _f64(x), _f64(weight), _f64(bias), _f64(initial_states)
+    batch, dim, seqlen = x.shape
+    width = w.shape[1]
+    if init is None:
+        init = np.zeros((batch, dim, width - 1))
+    xf = np.concatenate([init, x], axis=-1)
+    out = np.zeros((batch, dim, seqlen))
+    for k in range(width):
+        out += w[None, :, k, None] * xf[:, :, k:k + seqlen]
+    if bias is not None:
+        out += bias[None, :, None]
+    if activation in ("silu", "swish"):
+        out = out * sigmoid(out)
+    return out, xf[:, :, xf.shape[-1] - (width - 1):]
+
+
+def causal_conv1d_bwd(x, weight, bias=None, initial_states=None, dout=None, activation=None,
+                      dfinal_states=None):
+    """Backward of causal_conv1d_fwd, from the chain rule:
+        pre_t = bias + sum_k w[k] x_full[t+k] ; dpre = dout * act'(pre)
+        dx_full[s] += w[k] dpre[s-k] ; dw[k] = sum_{b,t} dpre[t] x_full[t+k] ; dbias = sum dpre
+    Returns (dx, dweight, dbias, dinitial_states); dbias / dinitial_states are
+    None when bias / initial_states are None."""
+    x, w, bias_, init = _f64(x), _f64(weight), _f64(bias), _f64(initial_states)
+    dout = _f64(dout)
+    batch, dim, seqlen = x.shape
+    width = w.shape[1]
+    init_ = np.zeros((batch, dim, width - 1)) if init is None else init
+    xf = np.concatenate([init_, x], axis=-1)
+    pre = np.zeros((batch, dim, seqlen))
+    for k in range(width):
+        pre += w[None, :, k, None] * xf[:, :, k:k + seqlen]
+    if bias_ is not None:
+        pre += bias_[None, :, None]
+    if activation in ("silu", "swish"):
+        s = sigmoid(pre)
+        dpre = dout * s * (1 + pre * (1 - s))
+    else:
+        dpre = dout
+    dxf = np.zeros_like(xf)
+    dw = np.zeros_like(w)
+    for k in range(width):
+        dxf[:, :, k:k + seqlen] += w[None, :, k, None] * dpre
+        dw[:, k] = (dpre * xf[:, :, k:k + seqlen]).sum((0, 2))
+    if dfinal_states is not None:
+        dxf[:, :, xf.shape[-1] - (width - 1):] += _f64(dfinal_states)
+    dbias = None if bias_ is None else dpre.sum((0, 2))
+    dinit = None if init is None else dxf[:, :, :width - 1]
+    return dxf[:, :, width - 1:], dw, dbias, dinit
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
+    """Decode step(s) (src/mamba_cpu/ops/causal_conv1d.py:56-85):
+        x_full = [conv_state, x] ; new_state = x_full[..., -state_len:]
+        out = conv over the last seqlen + width - 1 columns
+    x: (b, d) or (b, d, s). Returns (out shaped like x, new_state)."""
+    x, st, w, bias = _f64(x), _f64(conv_state), _f64(weight), _f64(bias)
+    single = x.ndim == 2
+    xs = x[..., None] if single else x
+    seqlen = xs.shape[-1]
+    width = w.shape[1]
+    state_len = st.shape[-1]
+    xf = np.concatenate([st, xs], axis=-1)
+    new_state = xf[..., xf.shape[-1] - state_len:].copy()
+    win = xf[..., xf.shape[-1] - (seqlen + width - 1):]
+    out = np.zeros(xs.shape)
+    for k in range(width):
+        out += w[None, :, k, None] * win[:, :, k:k + seqlen]
+    if bias is not None:
+        out += bias[None, :, None]
+    if activation in ("silu", "swish"):
+        out = out * sigmoid(out)
+    return (out[..., 0] if single else out), new_state
+
+
+def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, dt_softplus=False):
+    """One decode step (src/mamba_cpu/ops/selective_state_update.py:5-57):
+        dt = softplus?(dt + dt_bias) ; state = state * exp(dt A) + dt x B
+        out = <state, C> + D x ; out *= silu(z)
+    Mamba-1 layout: state (b, d, n), x/dt/z (b, d), A (d, n), B/C (b, n), D/dt_bias (d).
+    Mamba-2 layout: state (b, h, p, n), x/dt/z (b, h, p), A (h, p, n),
+    B/C (b, g, n), D/dt_bias (h, p); heads split into contiguous groups.
+    Returns (out shaped like x, new_state)."""
+    state, x, dt, A = _f64(state), _f64(x), _f64(dt), _f64(A)
+    B, C, D, z, dt_bias = _f64(B), _f64(C), _f64(D), _f64(z), _f64(dt_bias)
+    heads = state.ndim > 3
+    if not heads:
+        state, x, dt, A = state[:, None], x[:, None], dt[:, None], A[None]
+        B, C = B[:, None], C[:, None]
+        D = None if D is None else D[None]
+        z = None if z is None else z[:, None]
+        dt_bias = None if dt_bias is None else dt_bias[None]
+    nheads = state.shape[1]
+    if dt_bias is not None:
+        dt = dt + dt_bias[None]
+    if dt_softplus:
+        dt = softplus(dt)
+    with np.errstate(over="ignore", invalid="ignore"):
+        dA = np.exp(dt[..., None] * A[None])
+        Bh = np.repeat(B, nheads // B.shape[1], axis=1)  # (b, h, n)
+        Ch = np.repeat(C, nheads // C.shape[1], axis=1)
+        new_state = state * dA + (dt * x)[..., None] * Bh[:, :, None, :]
+        out = (new_state * Ch[:, :, None, :]).sum(-1)
+        if D is not None:
+            out = out + x * D[None]
+        if z is not None:
+            out = out * z * sigmoid(z)
+    if not heads:
+        out, new_state = out[:, 0], new_state[:, 0]
+    return out, new_state

@@ -1,0 +1,190 @@
+"""causal_conv1d_fn / causal_conv1d_update on the GPU against the float64 oracle.
+
+Mirrors the reference's tests/test_causal_conv1d.py (oracle parity over width,
+activation and bias; initial/final-state chaining; update == full conv;
+multi-token update; final_states_out buffer identity; mixed dtypes) and adds
+the backward pass (against the oracle's analytic gradients) and strided
+channel-contiguous inputs. Tolerances: float32 rtol/atol 1e-5 (forward) and
+1e-4 (gradients); bf16 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as O
+
+from mamba_cpu import causal_conv1d_fn, causal_conv1d_update
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def close(got, want, rtol, atol, name=""):
+    np.testing.assert_allclose(got.detach().float().cpu().numpy().astype(np.float64), want,
+                               rtol=rtol, atol=atol, err_msg=name)
+
+
+@pytest.mark.parametrize("width", [2, 3, 4])
+@pytest.mark.parametrize("activation", [None, "silu"])
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_matches_oracle(width, activation, has_bias):
+    torch.manual_seed(0)
+    x = torch.randn(2, 8, 37, device=DEV)
+    w = torch.randn(8, width, device=DEV)
+    b = torch.randn(8, device=DEV) if has_bias else None
+    out = causal_conv1d_fn(x, w, b, activation=activation)
+    want, _ = O.causal_conv1d_fwd(x, w, b, activation=activation)
+    close(out, want, 1e-5, 1e-5)
+
+
+def test_initial_and_final_states_chain():
+    torch.manual_seed(0)
+    x = torch.randn(2, 8, 40, device=DEV)
+    w = torch.randn(8, 4, device=DEV)
+    full = causal_conv1d_fn(x, w, activation="silu")
+    a, state = causal_conv1d_fn(x[..., :25], w, activation="silu", return_final_states=True)
+    b = causal_conv1d_fn(x[..., 25:], w, initial_states=state, activation="silu")
+    torch.testing.assert_close(torch.cat([a, b], -1), full)
+
+
+def test_update_matches_full_conv():
+    torch.manual_seed(0)
+    x = torch.randn(2, 8, 12, device=DEV)
+    w = torch.randn(8, 4, device=DEV)
+    bias = torch.randn(8, device=DEV)
+    full = causal_conv1d_fn(x, w, bias, activation="silu")
+    state = torch.zeros(2, 8, 4, device=DEV)
+    steps = [causal_conv1d_update(x[..., t], state, w, bias, "silu") for t in range(12)]
+    torch.testing.assert_close(torch.stack(steps, -1), full, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("state_len", [3, 4, 6])
+@pytest.mark.parametrize("seqlen", [1, 5])
+def test_update_multi_token_matches_full_conv(state_len, seqlen):
+    torch.manual_seed(0)
+    x = torch.randn(2, 8, 12 + seqlen, device=DEV)
+    w = torch.randn(8, 4, device=DEV)
+    full = causal_conv1d_fn(x, w, activation="silu")
+    state = torch.zeros(2, 8, state_len, device=DEV)
+    causal_conv1d_update(x[..., :12], state, w)
+    out = causal_conv1d_update(x[..., 12:], state, w, activation="silu")
+    assert out.shape == (2, 8, seqlen)
+    torch.testing.assert_close(out, full[..., 12:], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(state, x[..., -state_len:])
+
+
+@pytest.mark.parametrize("state_len", [3, 4, 7])
+@pytest.mark.parametrize("seqlen", [None, 1, 3])
+def test_update_matches_oracle(state_len, seqlen):
+    torch.manual_seed(0)
+    x = torch.randn(2, 64, device=DEV) if seqlen is None else torch.randn(2, 64, seqlen, device=DEV)
+    w, bias = torch.randn(64, 4, device=DEV), torch.randn(64, device=DEV)
+    state = torch.randn(2, 64, state_len, device=DEV)
+    want, want_state = O.causal_conv1d_update(x, state, w, bias, "silu")
+    out = causal_conv1d_update(x, state, w, bias, "silu")
+    close(out, want, 1e-5, 1e-5)
+    close(state, want_state, 0, 0)
+
+
+def test_final_states_out_buffer():
+    x = torch.randn(2, 8, 10, device=DEV)
+    w = torch.randn(8, 4, device=DEV)
+    buf = torch.empty(2, 8, 3, device=DEV)
+    _, final = causal_conv1d_fn(x, w, return_final_states=True, final_states_out=buf)
+    assert final is buf
+    torch.testing.assert_close(buf, x[..., -3:])
+
+
+def test_mixed_dtypes_return_input_dtype():
+    x = torch.randn(2, 8, 10, device=DEV).bfloat16()
+    w = torch.randn(8, 4, device=DEV)
+    out = causal_conv1d_fn(x, w, torch.randn(8, device=DEV), activation="silu")
+    assert out.dtype == torch.bfloat16
+    state = torch.zeros(2, 8, 4, dtype=torch.bfloat16, device=DEV)
+    assert causal_conv1d_update(x[..., 0], state, w).dtype == torch.bfloat16
+
+
+def test_rejects_unsupported_args():
+    x = torch.randn(2, 8, 10, device=DEV)
+    w = torch.randn(8, 4, device=DEV)
+    with pytest.raises(NotImplementedError):
+        causal_conv1d_fn(x, w, seq_idx=torch.zeros(2, 10, dtype=torch.int32, device=DEV))
+    with pytest.raises(ValueError):
+        causal_conv1d_fn(x, w, activation="relu")
+    with pytest.raises(ValueError):
+        causal_conv1d_update(x, torch.zeros(2, 8, 2, device=DEV), w)
+    with pytest.raises(NotImplementedError):
+        causal_conv1d_update(x[..., 0], torch.zeros(2, 8, 3, device=DEV), w,
+                             cache_seqlens=torch.zeros(2, dtype=torch.int32, device=DEV))
+
+
+@pytest.mark.parametrize("width", [2, 4])
+@pytest.mark.parametrize("activation", [None, "silu"])
+@pytest.mark.parametrize("with_init", [False, True])
+@pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
+def test_backward_matches_oracle(width, activation, with_init, layout):
+    torch.manual_seed(0)
+    b, d, l = 2, 24, 45
+    if layout == "contiguous":
+        x = torch.randn(b, d, l, device=DEV)
+    else:
+        x = torch.randn(b, l, d, device=DEV).transpose(1, 2)
+    x.requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    init = torch.randn(b, d, width - 1, device=DEV, requires_grad=True) if with_init else None
+    out, final = causal_conv1d_fn(x, w, bias, initial_states=init, return_final_states=True,
+                                  activation=activation)
+    want_out, want_final = O.causal_conv1d_fwd(x, w, bias, init, activation)
+    close(out, want_out, 1e-5, 1e-5, "out")
+    close(final, want_final, 0, 0, "final")
+    G = torch.randn(b, d, l, device=DEV)
+    Gf = torch.randn(b, d, width - 1, device=DEV)
+    ((out * G).sum() + (final * Gf).sum()).backward()
+    dx, dw, db, dinit = O.causal_conv1d_bwd(x, w, bias, init, G, activation, Gf)
+    close(x.grad, dx, 1e-4, 1e-4, "dx")
+    close(w.grad, dw, 1e-4, 1e-4, "dweight")
+    close(bias.grad, db, 1e-4, 1e-4, "dbias")
+    if with_init:
+        close(init.grad, dinit, 1e-4, 1e-4, "dinit")
+
+
+def test_channels_last_output_layout():
+    """A channel-contiguous x (Hugging Face's transposed view) gets a
+    channel-contiguous output, so transposing it back is free."""
+    x = torch.randn(2, 30, 16, device=DEV).transpose(1, 2)
+    w = torch.randn(16, 4, device=DEV)
+    out = causal_conv1d_fn(x, w, activation="silu")
+    assert out.transpose(1, 2).is_contiguous()
+    want, _ = O.causal_conv1d_fwd(x, w, activation="silu")
+    close(out, want, 1e-5, 1e-5)
+
+
+def test_bf16_forward_backward():
+    torch.manual_seed(0)
+    x = torch.randn(2, 16, 50, device=DEV).bfloat16().requires_grad_()
+    w = torch.randn(16, 4, device=DEV, requires_grad=True)
+    bias = torch.randn(16, device=DEV, requires_grad=True)
+    out = causal_conv1d_fn(x, w, bias, activation="silu")
+    assert out.dtype == torch.bfloat16
+    want, _ = O.causal_conv1d_fwd(x, w, bias, activation="silu")
+    close(out, want, 2e-2, 2e-2)
+    G = torch.randn(2, 16, 50, device=DEV).bfloat16()
+    (out.float() * G.float()).sum().backward()
+    dx, dw, db, _ = O.causal_conv1d_bwd(x, w, bias, None, G, "silu")
+    assert x.grad.dtype == torch.bfloat16
+    close(x.grad, dx, 2e-2, 2e-2, "dx")
+    close(w.grad / max(np.abs(dw).max(), 1), dw / max(np.abs(dw).max(), 1), 2e-2, 2e-2, "dw")
+    close(bias.grad / max(np.abs(db).max(), 1), db / max(np.abs(db).max(), 1), 2e-2, 2e-2, "db")
+
+
+def test_opcheck():
+    x = torch.randn(2, 8, 12, device=DEV, requires_grad=True)
+    w = torch.randn(8, 4, device=DEV, requires_grad=True)
+    b = torch.randn(8, device=DEV, requires_grad=True)
+    init = torch.randn(2, 8, 3, device=DEV, requires_grad=True)
+    torch.library.opcheck(torch.ops.mamba_cpu.causal_conv1d_fwd.default, (x, w, b, init, True, True))
+    torch.library.opcheck(torch.ops.mamba_cpu.causal_conv1d_bwd.default,
+                          (x.detach(), w.detach(), b.detach(), init.detach(),
+                           torch.randn(2, 8, 12, device=DEV), torch.randn(2, 8, 3, device=DEV), True))

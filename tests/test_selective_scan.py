@@ -1,0 +1,271 @@
+"""selective_scan_fn on the GPU against the float64 oracle.
+
+Mirrors the reference's tests/test_selective_scan.py case for case (shapes,
+group layouts, flag combinations, low precision, opcheck, extreme decay, exp
+accuracy, NaN confinement); the expected values come from oracle/numerics.py
+(float64) instead of the reference's pure-torch selective_scan_ref.
+Tolerances: float32 outputs rtol 1e-4 / atol 1e-5, float32 gradients rtol 1e-3
+(atol 1e-4 after scaling by the gradient's magnitude), bf16/fp16 1e-2 on
+outputs and 2e-2 on gradients, always against the oracle evaluated on the
+same (rounded) inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as O
+
+import mamba_cpu
+from mamba_cpu import selective_scan_fn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make_inputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, dtype, requires_grad=False):
+    """Same generator and distributions as the reference's make_inputs
+    (tests/test_selective_scan.py:28-45), created on the CPU, moved to the GPU."""
+    g = torch.Generator().manual_seed(0)
+
+    def rand(*shape, scale=1.0, dt=dtype):
+        return (torch.randn(*shape, generator=g) * scale).to(dt)
+
+    bc_shape = (batch, dstate, seqlen) if ngroups is None else (batch, ngroups, dstate, seqlen)
+    inp = dict(
+        u=rand(batch, dim, seqlen),
+        delta=(torch.rand(batch, dim, seqlen, generator=g) * 0.5).to(dtype),
+        A=(-torch.rand(dim, dstate, generator=g) - 0.5),
+        B=rand(*bc_shape),
+        C=rand(*bc_shape),
+        D=rand(dim, dt=torch.float32) if has_D else None,
+        z=rand(batch, dim, seqlen) if has_z else None,
+        delta_bias=(torch.rand(dim, generator=g) * 0.1) if has_bias else None,
+    )
+    return {k: None if v is None else v.to(DEV).requires_grad_(requires_grad) for k, v in inp.items()}
+
+
+def close(got, want, rtol, atol, name=""):
+    got = got.detach().float().cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=atol, err_msg=name)
+
+
+@pytest.mark.parametrize("batch,dim,seqlen,dstate", [(1, 4, 1, 1), (2, 16, 33, 16), (3, 32, 128, 8)])
+@pytest.mark.parametrize("ngroups", [None, 1, 2])
+@pytest.mark.parametrize("has_D,has_z,has_bias,softplus", [
+    (False, False, False, False),
+    (True, True, True, True),
+    (True, False, True, False),
+])
+def test_forward_matches_oracle(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, softplus):
+    inp = make_inputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, torch.float32)
+    out, last = selective_scan_fn(**inp, delta_softplus=softplus, return_last_state=True)
+    out_ref, last_ref = O.selective_scan_fwd(**inp, delta_softplus=softplus)
+    assert out.dtype == torch.float32 and last.dtype == torch.float32
+    close(out, out_ref, 1e-4, 1e-5, "out")
+    close(last, last_ref, 1e-4, 1e-5, "last_state")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_low_precision_inputs(dtype):
+    inp = make_inputs(2, 16, 64, 16, None, True, True, True, dtype)
+    out = selective_scan_fn(**inp, delta_softplus=True)
+    out_ref, _ = O.selective_scan_fwd(**inp, delta_softplus=True)
+    assert out.dtype == dtype
+    close(out, out_ref, 1e-2, 1e-2)
+
+
+def grads_of(inp, softplus, W, V):
+    """Gradients of sum(out * W) + sum(last * V) through selective_scan_fn."""
+    for v in inp.values():
+        if v is not None:
+            v.grad = None
+    out, last = selective_scan_fn(**inp, delta_softplus=softplus, return_last_state=True)
+    loss = 0
+    if W is not None:
+        loss = loss + (out.float() * W).sum()
+    if V is not None:
+        loss = loss + (last * V).sum()
+    loss.backward()
+    return {k: None if v.grad is None else v.grad.clone() for k, v in inp.items() if v is not None}
+
+
+def oracle_grads(inp, softplus, W, V):
+    du, ddelta, dA, dB, dC, dD, dz, dbias = O.selective_scan_bwd(
+        **inp, delta_softplus=softplus,
+        dout=None if W is None else W, dlast_state=None if V is None else V)
+    want = dict(u=du, delta=ddelta, A=dA, B=dB, C=dC, D=dD, z=dz, delta_bias=dbias)
+    return {k: v for k, v in want.items() if inp.get(k) is not None}
+
+
+def check_grads(got, want, rtol, atol):
+    for k, w in want.items():
+        g = got[k]
+        if g is None:
+            assert not np.any(w), k
+            continue
+        scale = max(np.abs(w).max(), 1.0)
+        close(g / scale, w / scale, rtol, atol, k)
+
+
+@pytest.mark.parametrize("batch,dim,seqlen,dstate", [(1, 4, 1, 1), (2, 8, 17, 4), (2, 64, 96, 16)])
+@pytest.mark.parametrize("ngroups", [None, 2, 4])
+@pytest.mark.parametrize("has_D,has_z,has_bias,softplus", [
+    (False, False, False, False),
+    (True, True, True, True),
+    (True, False, False, True),
+])
+@pytest.mark.parametrize("loss_on", [("out", "last"), ("out",), ("last",)])
+def test_backward_matches_oracle(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, softplus, loss_on):
+    if ngroups is not None and dim % ngroups:
+        pytest.skip("dim not divisible by ngroups")
+    inp = make_inputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, torch.float32,
+                      requires_grad=True)
+    g = torch.Generator().manual_seed(1)
+    W = torch.randn(batch, dim, seqlen, generator=g).to(DEV) if "out" in loss_on else None
+    V = torch.randn(batch, dim, dstate, generator=g).to(DEV) if "last" in loss_on else None
+    got = grads_of(inp, softplus, W, V)
+    want = oracle_grads(inp, softplus, W, V)
+    check_grads(got, want, 1e-3, 1e-4)
+
+
+def test_backward_low_precision():
+    inp = make_inputs(2, 16, 32, 8, None, True, True, True, torch.bfloat16, requires_grad=True)
+    W = torch.randn(2, 16, 32, generator=torch.Generator().manual_seed(1)).to(DEV)
+    got = grads_of(inp, True, W, None)
+    want = oracle_grads(inp, True, W, None)
+    for k in want:
+        assert got[k].dtype == inp[k].dtype, k
+    check_grads(got, want, 2e-2, 2e-2)
+
+
+def test_opcheck_bwd():
+    inp = make_inputs(2, 4, 8, 2, 2, True, True, True, torch.float32)
+    args = (
+        inp["u"], inp["delta"], inp["A"],
+        inp["B"].transpose(-1, -2).contiguous(), inp["C"].transpose(-1, -2).contiguous(),
+        inp["D"], inp["z"], inp["delta_bias"], True,
+        torch.randn(2, 4, 8, device=DEV), torch.randn(2, 4, 2, device=DEV),
+    )
+    torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_bwd.default, args)
+
+
+def test_opcheck():
+    inp = make_inputs(1, 4, 8, 2, 1, True, True, True, torch.float32, requires_grad=True)
+    args = (
+        inp["u"], inp["delta"], inp["A"],
+        inp["B"].detach().transpose(-1, -2).contiguous().requires_grad_(),
+        inp["C"].detach().transpose(-1, -2).contiguous().requires_grad_(),
+        inp["D"], inp["z"], inp["delta_bias"], True,
+    )
+    torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_fwd.default, args)
+
+
+def test_rejects_complex():
+    inp = make_inputs(1, 4, 8, 2, None, False, False, False, torch.float32)
+    inp["A"] = inp["A"].to(torch.complex64)
+    with pytest.raises(NotImplementedError):
+        selective_scan_fn(**inp)
+
+
+def decay_inputs(x, seqlen=4, dstate=8):
+    """Inputs where every step's dt*A equals x per channel (reference
+    tests/test_selective_scan.py:146-158); x: (dim,)."""
+    dim = x.shape[0]
+    g = torch.Generator().manual_seed(0)
+    delta = torch.ones(1, dim, seqlen)
+    A = x[:, None].expand(dim, dstate).contiguous()
+    inp = dict(
+        u=torch.randn(1, dim, seqlen, generator=g),
+        delta=delta,
+        A=A,
+        B=torch.randn(1, dstate, seqlen, generator=g),
+        C=torch.randn(1, dstate, seqlen, generator=g),
+    )
+    return {k: v.to(DEV) for k, v in inp.items()}
+
+
+@pytest.mark.parametrize("x", [-1e2, -1e4, -1e6, -1e8, -1e12, -1e20, -1e30, -3e38, -float("inf")])
+def test_extreme_decay_matches_oracle(x):
+    inp = decay_inputs(torch.full((16,), x))
+    out, last = selective_scan_fn(**inp, return_last_state=True)
+    out_ref, last_ref = O.selective_scan_fwd(**inp)
+    close(out, out_ref, 1e-5, 1e-5)
+    close(last, last_ref, 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("x", [-1e4, -1e12, -1e30])
+def test_extreme_decay_backward_is_finite_and_matches(x):
+    inp = decay_inputs(torch.full((16,), x))
+    for k in ("u", "B", "C"):
+        inp[k].requires_grad_()
+    out = selective_scan_fn(**inp)
+    (out * out.detach()).sum().backward()  # dout = 2 * out / 2 = out
+    _, _, _, dB, dC, _, _, _ = O.selective_scan_bwd(**inp, dout=out.detach())
+    du = O.selective_scan_bwd(**inp, dout=out.detach())[0]
+    for k, want in (("u", du), ("B", dB), ("C", dC)):
+        g = inp[k].grad
+        assert g.isfinite().all(), k
+        close(g, want, 1e-4, 1e-4, k)
+
+
+def test_exp_accuracy_across_range():
+    # Includes x > 0: dt*A is positive when delta is negative and softplus is off.
+    x = torch.cat([torch.linspace(-80, 0, 512), torch.linspace(0, 40, 128)])
+    inp = decay_inputs(x, seqlen=2)
+    inp["u"] = torch.ones_like(inp["u"])
+    inp["B"] = torch.ones_like(inp["B"])
+    inp["C"] = torch.ones_like(inp["C"])
+    out = selective_scan_fn(**inp)
+    out_ref, _ = O.selective_scan_fwd(**inp)
+    close(out, out_ref, 1e-5, 1e-6)
+
+
+def test_nan_propagates():
+    inp = decay_inputs(torch.full((16,), -1.0))
+    inp["delta"][0, 3, 1] = float("nan")
+    out = selective_scan_fn(**inp)
+    assert out[0, 3, 1:].isnan().all()
+    assert not out[0, 2].isnan().any()
+    assert not out[0, 3, :1].isnan().any()
+
+
+def test_hf_style_strided_inputs_match_contiguous():
+    """u/z channel-contiguous and B/C as (b, n, l) views of an (b, l, r + 2n)
+    projection, as Hugging Face's mixer passes them: no copies, same result."""
+    torch.manual_seed(0)
+    b, d, l, n, r = 2, 48, 70, 16, 5
+    xz = torch.randn(b, l, 2 * d, device=DEV)
+    u, z = xz[..., :d].transpose(1, 2), xz[..., d:].transpose(1, 2)
+    proj = torch.randn(b, l, r + 2 * n, device=DEV)
+    B, C = proj[..., r:r + n].transpose(1, 2), proj[..., r + n:].transpose(1, 2)
+    delta = torch.rand(b, d, l, device=DEV) - 2
+    A = -torch.rand(d, n, device=DEV) - 0.5
+    D, bias = torch.randn(d, device=DEV), torch.rand(d, device=DEV)
+    got, gl = selective_scan_fn(u, delta, A, B, C, D, z, bias, True, True)
+    want, wl = selective_scan_fn(u.contiguous(), delta, A, B.contiguous(), C.contiguous(), D,
+                                 z.contiguous(), bias, True, True)
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+    torch.testing.assert_close(gl, wl, rtol=0, atol=0)
+    out_ref, _ = O.selective_scan_fwd(u, delta, A, B, C, D, z, bias, True)
+    close(got, out_ref, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("dstate", [24, 32, 64])
+def test_larger_dstate(dstate):
+    inp = make_inputs(2, 8, 40, dstate, None, True, True, True, torch.float32, requires_grad=True)
+    W = torch.randn(2, 8, 40, generator=torch.Generator().manual_seed(1)).to(DEV)
+    out, last = selective_scan_fn(**inp, delta_softplus=True, return_last_state=True)
+    out_ref, last_ref = O.selective_scan_fwd(**inp, delta_softplus=True)
+    close(out, out_ref, 1e-4, 1e-5)
+    close(last, last_ref, 1e-4, 1e-5)
+    got = grads_of(inp, True, W, None)
+    check_grads(got, oracle_grads(inp, True, W, None), 1e-3, 1e-4)
+
+
+def test_version_and_device_check():
+    from mamba_cpu import _C
+
+    assert "gfx950" in _C.version()
+    assert _C.lib.mcpu_check_device() == 0, _C.lib.mcpu_last_error()
+    assert mamba_cpu.__version__
