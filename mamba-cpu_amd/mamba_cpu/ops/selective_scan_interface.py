@@ -98,6 +98,52 @@ def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
     return u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32)
 
 
+def _scan_bwd_impl(name, u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state,
+                   ckpt=None):
+    _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=(dout, dlast_state, ckpt))
+    if dout.shape != u.shape or dout.dtype != u.dtype:
+        raise ValueError(f"{name} expects dout shaped and typed like u")
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    if dlast_state is not None:
+        if dlast_state.dtype != torch.float32 or dlast_state.shape != (batch, dim, dstate):
+            raise ValueError(f"{name} expects float32 dlast_state (batch, dim, dstate)")
+        dlast_state = dlast_state.contiguous()
+    if ckpt is not None and (ckpt.dtype != torch.float32 or not ckpt.is_contiguous()
+                             or ckpt.shape != _ckpt_shape(u, A)):
+        raise ValueError(f"{name} expects the float32 checkpoints written by selective_scan_fwd_ckpt")
+    du = u.new_empty(u.shape)
+    ddelta = delta.new_empty(delta.shape)
+    dA = A.new_empty(A.shape)
+    dB = B.new_empty(B.shape)
+    dC = C.new_empty(C.shape)
+    dD = A.new_empty(dim)
+    dz = z.new_empty(z.shape) if z is not None else u.new_empty(0)
+    ddelta_bias = A.new_empty(dim)
+    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
+    a.dout, a.dout_stride = dout.data_ptr(), _C.strides3(dout)
+    a.dlast_state = _C.ptr(dlast_state)
+    a.ckpt = _C.ptr(ckpt)
+    a.du, a.ddelta, a.dA, a.dB, a.dC = (du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(),
+                                        dB.data_ptr(), dC.data_ptr())
+    a.dD, a.ddelta_bias = dD.data_ptr(), ddelta_bias.data_ptr()
+    a.dz = dz.data_ptr() if z is not None else 0
+    with _C.device_of(u):
+        ws_bytes = _C.lib.mcpu_selective_scan_bwd_workspace_size(a)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=u.device)
+        _C.call(_C.lib.mcpu_selective_scan_bwd, a, name, ws.data_ptr(), ws_bytes, _C.stream_of(u))
+    return du, ddelta, dA, dB, dC, dD, dz, ddelta_bias
+
+
+def _bwd_fake(u, delta, A, B, C, z):
+    dim = u.shape[1]
+    return (
+        u.new_empty(u.shape), delta.new_empty(delta.shape), A.new_empty(A.shape),
+        B.new_empty(B.shape), C.new_empty(C.shape), A.new_empty(dim),
+        z.new_empty(z.shape) if z is not None else u.new_empty(0), A.new_empty(dim),
+    )
+
+
 @torch.library.custom_op("mamba_cpu::selective_scan_bwd", mutates_args=(), device_types="cuda")
 def _selective_scan_bwd(
     u: torch.Tensor,
@@ -116,48 +162,15 @@ def _selective_scan_bwd(
     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
 ]:
     """Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias). dz is empty when z
-    is None; dD and ddelta_bias are always computed (as in the reference)."""
-    _validate("mamba_cpu::selective_scan_bwd", u, delta, A, B, C, D, z, delta_bias,
-              extra=(dout, dlast_state))
-    if dout.shape != u.shape or dout.dtype != u.dtype:
-        raise ValueError("mamba_cpu::selective_scan_bwd expects dout shaped and typed like u")
-    batch, dim, _ = u.shape
-    dstate = A.shape[1]
-    if dlast_state is not None:
-        if dlast_state.dtype != torch.float32 or dlast_state.shape != (batch, dim, dstate):
-            raise ValueError("mamba_cpu::selective_scan_bwd expects float32 dlast_state (batch, dim, dstate)")
-        dlast_state = dlast_state.contiguous()
-    du = u.new_empty(u.shape)
-    ddelta = delta.new_empty(delta.shape)
-    dA = A.new_empty(A.shape)
-    dB = B.new_empty(B.shape)
-    dC = C.new_empty(C.shape)
-    dD = A.new_empty(dim)
-    dz = z.new_empty(z.shape) if z is not None else u.new_empty(0)
-    ddelta_bias = A.new_empty(dim)
-    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
-    a.dout, a.dout_stride = dout.data_ptr(), _C.strides3(dout)
-    a.dlast_state = _C.ptr(dlast_state)
-    a.du, a.ddelta, a.dA, a.dB, a.dC = (du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(),
-                                        dB.data_ptr(), dC.data_ptr())
-    a.dD, a.ddelta_bias = dD.data_ptr(), ddelta_bias.data_ptr()
-    a.dz = dz.data_ptr() if z is not None else 0
-    with _C.device_of(u):
-        ws_bytes = _C.lib.mcpu_selective_scan_bwd_workspace_size(a)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=u.device)
-        _C.call(_C.lib.mcpu_selective_scan_bwd, a, "mamba_cpu::selective_scan_bwd",
-                ws.data_ptr(), ws_bytes, _C.stream_of(u))
-    return du, ddelta, dA, dB, dC, dD, dz, ddelta_bias
+    is None; dD and ddelta_bias are always computed (as in the reference).
+    Recomputes the forward states it needs from the inputs."""
+    return _scan_bwd_impl("mamba_cpu::selective_scan_bwd", u, delta, A, B, C, D, z, delta_bias,
+                          delta_softplus, dout, dlast_state)
 
 
 @_selective_scan_bwd.register_fake
 def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state):
-    dim = u.shape[1]
-    return (
-        u.new_empty(u.shape), delta.new_empty(delta.shape), A.new_empty(A.shape),
-        B.new_empty(B.shape), C.new_empty(C.shape), A.new_empty(dim),
-        z.new_empty(z.shape) if z is not None else u.new_empty(0), A.new_empty(dim),
-    )
+    return _bwd_fake(u, delta, A, B, C, z)
 
 
 def _setup_context(ctx, inputs, output):
@@ -184,6 +197,106 @@ def _backward(ctx, grad_out, grad_last_state):
 
 torch.library.register_autograd(
     "mamba_cpu::selective_scan_fwd", _backward, setup_context=_setup_context
+)
+
+
+# Training path: the forward also returns the scan state at the start of every
+# 16-step block, and the backward restarts from those checkpoints instead of
+# recomputing the states from the inputs. Same arithmetic as the pair above.
+
+_BLOCK_T = 16
+
+
+def _ckpt_shape(u, A):
+    batch, dim, seqlen = u.shape
+    return (batch, dim, (seqlen + _BLOCK_T - 1) // _BLOCK_T, A.shape[1])
+
+
+@torch.library.custom_op("mamba_cpu::selective_scan_fwd_ckpt", mutates_args=(), device_types="cuda")
+def _selective_scan_fwd_ckpt(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    D: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    delta_bias: Optional[torch.Tensor],
+    delta_softplus: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """selective_scan_fwd that also returns the float32 block checkpoints
+    (batch, dim, ceil(seqlen / 16), dstate) for selective_scan_bwd_ckpt."""
+    name = "mamba_cpu::selective_scan_fwd_ckpt"
+    _validate(name, u, delta, A, B, C, D, z, delta_bias)
+    batch, dim, _ = u.shape
+    out = u.new_empty(u.shape)
+    last_state = u.new_empty(batch, dim, A.shape[1], dtype=torch.float32)
+    ckpt = u.new_empty(_ckpt_shape(u, A), dtype=torch.float32)
+    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
+    a.out, a.last_state, a.ckpt = out.data_ptr(), last_state.data_ptr(), ckpt.data_ptr()
+    with _C.device_of(u):
+        _C.call(_C.lib.mcpu_selective_scan_fwd, a, name, _C.stream_of(u))
+    return out, last_state, ckpt
+
+
+@_selective_scan_fwd_ckpt.register_fake
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+    return (u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32),
+            u.new_empty(_ckpt_shape(u, A), dtype=torch.float32))
+
+
+@torch.library.custom_op("mamba_cpu::selective_scan_bwd_ckpt", mutates_args=(), device_types="cuda")
+def _selective_scan_bwd_ckpt(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    D: Optional[torch.Tensor],
+    z: Optional[torch.Tensor],
+    delta_bias: Optional[torch.Tensor],
+    delta_softplus: bool,
+    dout: torch.Tensor,
+    dlast_state: Optional[torch.Tensor],
+    ckpt: torch.Tensor,
+) -> tuple[
+    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+]:
+    """selective_scan_bwd restarting from the forward's block checkpoints."""
+    return _scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", u, delta, A, B, C, D, z, delta_bias,
+                          delta_softplus, dout, dlast_state, ckpt)
+
+
+@_selective_scan_bwd_ckpt.register_fake
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt):
+    return _bwd_fake(u, delta, A, B, C, z)
+
+
+def _setup_context_ckpt(ctx, inputs, output):
+    u, delta, A, B, C, D, z, delta_bias, delta_softplus = inputs
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[2])
+    ctx.delta_softplus = delta_softplus
+
+
+def _backward_ckpt(ctx, grad_out, grad_last_state, grad_ckpt):
+    u, delta, A, B, C, D, z, delta_bias, ckpt = ctx.saved_tensors
+    dout = torch.zeros_like(u) if grad_out is None else grad_out.to(u.dtype)
+    dlast = None if grad_last_state is None else grad_last_state.float().contiguous()
+    du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(
+        u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt
+    )
+    return (
+        du, ddelta, dA, dB, dC,
+        dD if D is not None else None,
+        dz if z is not None else None,
+        ddelta_bias if delta_bias is not None else None,
+        None,
+    )
+
+
+torch.library.register_autograd(
+    "mamba_cpu::selective_scan_fwd_ckpt", _backward_ckpt, setup_context=_setup_context_ckpt
 )
 
 
@@ -245,9 +358,15 @@ def selective_scan_fn(
     xdt = u.dtype
     if xdt not in _X_DTYPES or delta.dtype != xdt or (z is not None and z.dtype != xdt):
         xdt = torch.float32
-    out, last_state = torch.ops.mamba_cpu.selective_scan_fwd(
+    args = (
         _as_x(u, xdt), _as_x(delta, xdt), _as_f32(A), _as_kernel_bc(B), _as_kernel_bc(C),
         _as_f32(D), _as_x(z, xdt), _as_f32(delta_bias), bool(delta_softplus),
     )
+    needs_grad = torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in args)
+    if needs_grad:
+        out, last_state, _ = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
+    else:
+        out, last_state = torch.ops.mamba_cpu.selective_scan_fwd(*args)
     out = out.to(u.dtype)
     return (out, last_state) if return_last_state else out
