@@ -55,8 +55,9 @@ size_t mcpu_args_size(const char* name);
  * reference's SelectiveScanParams / SelectiveScanBwdParams
  * (csrc/selective_scan.h:21-38, 51-63), with these differences:
  *   - u/delta/z/dout may be any strided (batch, dim, seqlen) view;
- *   - B/C may be any (batch, ngroups, seqlen, dstate) view with unit dstate
- *     stride (the reference's kernel layout is the contiguous special case);
+ *   - B/C may be any strided (batch, ngroups, seqlen, dstate) view (the
+ *     reference's kernel layout is the contiguous special case, its public
+ *     (batch, ngroups, dstate, seqlen) layout the transposed one);
  *   - dA, dD and ddelta_bias come back summed over the batch (the reference
  *     returns per-batch partials that its Python side sums,
  *     src/mamba_cpu/ops/selective_scan_interface.py:87);
@@ -67,7 +68,7 @@ typedef struct mcpu_scan_args {
   const void* u;            /* (batch, dim, seqlen), dtype */
   const void* delta;        /* (batch, dim, seqlen), dtype */
   const float* A;           /* (dim, dstate) contiguous */
-  const float* B;           /* (batch, ngroups, seqlen, dstate), unit dstate stride */
+  const float* B;           /* (batch, ngroups, seqlen, dstate), any strides */
   const float* C;           /* same as B */
   const float* D;           /* (dim), optional */
   const void* z;            /* (batch, dim, seqlen), dtype, optional */
@@ -78,12 +79,15 @@ typedef struct mcpu_scan_args {
   int64_t u_stride[3];      /* element strides over (batch, dim, seqlen) */
   int64_t delta_stride[3];
   int64_t z_stride[3];
-  int64_t B_stride[3];      /* element strides over (batch, group, seqlen) */
-  int64_t C_stride[3];
+  int64_t B_stride[4];      /* element strides over (batch, group, seqlen, dstate) */
+  int64_t C_stride[4];
   /* forward outputs */
   void* out;                /* (batch, dim, seqlen) contiguous, dtype; NULL = states only */
   float* last_state;        /* (batch, dim, dstate) contiguous, optional */
   float* ckpt;              /* optional state checkpoints, see mcpu_selective_scan_ckpt_size */
+  void* ysave;              /* optional (batch, dim, seqlen) contiguous, dtype: the forward
+                               writes y = <h, C> + D u (before the z gate) here; a backward
+                               call given the same buffer reads y instead of recomputing it */
   /* backward inputs */
   const void* dout;         /* (batch, dim, seqlen), dtype; NULL = zeros */
   int64_t dout_stride[3];

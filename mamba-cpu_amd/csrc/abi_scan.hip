@@ -8,8 +8,10 @@
 #include "scan_common.h"
 
 namespace mcpu {
+int scan_fwd_waves();
+int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
-hipError_t scan_bwd_launch(const ScanParams& p, int dtype, hipStream_t stream);
+hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
 hipError_t scan_reduce_bc_launch(const float* part, float* out, int64_t slices, int64_t nblk_c,
                                  int64_t per_slice, hipStream_t stream);
 hipError_t scan_reduce_batch_launch(const float* part, float* out, int64_t batch,
@@ -32,12 +34,31 @@ int check_scan(const mcpu_scan_args* a) {
                 (long long)a->dstate);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "selective_scan: bad dtype %d", a->dtype);
   const int64_t dpg = a->dim / a->ngroups;
-  const int64_t blocks = a->batch * a->ngroups * ((dpg + kScanChannelsPerWG - 1) / kScanChannelsPerWG);
+  const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16);
   if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
+  for (int i = 0; i < 3; ++i)
+    if (a->u_stride[i] < 0 || a->delta_stride[i] < 0 || a->z_stride[i] < 0 || a->dout_stride[i] < 0)
+      return fail(MCPU_ERR_INVALID, "selective_scan: negative stride");
+  for (int i = 0; i < 4; ++i)
+    if (a->B_stride[i] < 0 || a->C_stride[i] < 0)
+      return fail(MCPU_ERR_INVALID, "selective_scan: negative stride");
+  // The kernels address a thread's element within one (channels x 16 steps)
+  // tile with a 32-bit byte offset from the tile's base.
+  const int64_t esz = dtype_size(a->dtype), ch = 4 * kScanMaxWaves - 1, T = kScanBlockT - 1;
+  const int64_t nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
+  auto x_span = [&](const int64_t (&s)[3]) { return esz * (ch * s[1] + T * s[2]); };
+  auto bc_span = [&](const int64_t (&s)[4]) { return 4 * (T * s[2] + 63 * s[3]); };
+  const int64_t spans[] = {x_span(a->u_stride), x_span(a->delta_stride), x_span(a->z_stride),
+                           x_span(a->dout_stride), bc_span(a->B_stride), bc_span(a->C_stride),
+                           4 * (ch * nblk * a->dstate + T), esz * (ch * a->seqlen + T)};
+  for (int64_t sp : spans)
+    if (sp >= 0xffffffffll)
+      return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: strides or sizes too large for 32-bit tile offsets");
   return MCPU_OK;
 }
 
-ScanParams make_params(const mcpu_scan_args* a) {
+// Kernel parameters for a launch with `waves` waves per workgroup.
+ScanParams make_params(const mcpu_scan_args* a, int waves) {
   ScanParams p;
   std::memset(&p, 0, sizeof(p));
   p.u = a->u;
@@ -55,17 +76,23 @@ ScanParams make_params(const mcpu_scan_args* a) {
   p.ngroups = a->ngroups;
   p.dpg = a->dim / a->ngroups;
   p.nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
-  p.nblk_c = (p.dpg + kScanChannelsPerWG - 1) / kScanChannelsPerWG;
+  p.nblk_c = (p.dpg + 4 * waves - 1) / (4 * waves);
   for (int i = 0; i < 3; ++i) {
     p.su[i] = a->u_stride[i];
     p.sdl[i] = a->delta_stride[i];
     p.sz[i] = a->z_stride[i];
+    p.sdo[i] = a->dout_stride[i];
+  }
+  for (int i = 0; i < 4; ++i) {
     p.sB[i] = a->B_stride[i];
     p.sC[i] = a->C_stride[i];
-    p.sdo[i] = a->dout_stride[i];
   }
   p.softplus = a->delta_softplus != 0;
   return p;
+}
+
+int bwd_waves(const mcpu_scan_args* a) {
+  return scan_bwd_waves(a->batch, a->ngroups, a->dim / a->ngroups, a->dstate);
 }
 
 struct BwdLayout {
@@ -74,7 +101,7 @@ struct BwdLayout {
 };
 
 BwdLayout bwd_layout(const mcpu_scan_args* a) {
-  const ScanParams p = make_params(a);
+  const ScanParams p = make_params(a, bwd_waves(a));
   BwdLayout w;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -114,11 +141,11 @@ extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* stream) {
   if (int rc = check_scan(a)) return rc;
   if (int rc = mcpu_check_device()) return rc;
   if (a->batch == 0 || a->dim == 0) return MCPU_OK;
-  const ScanParams p0 = make_params(a);
-  ScanParams p = p0;
+  ScanParams p = make_params(a, scan_fwd_waves());
   p.out = a->out;
   p.last_state = a->last_state;
   p.ckpt = a->ckpt;
+  p.ysave = a->out != nullptr ? a->ysave : nullptr;
   if (p.out == nullptr && p.last_state == nullptr && p.ckpt == nullptr) return MCPU_OK;
   return hip_status(scan_fwd_launch(p, a->dtype, a->out != nullptr, static_cast<hipStream_t>(stream)),
                     "selective_scan_fwd launch");
@@ -159,10 +186,13 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
     return MCPU_OK;
   }
   char* ws = static_cast<char*>(workspace);
-  ScanParams p = make_params(a);
+  const int waves = bwd_waves(a);
+  ScanParams p = make_params(a, waves);
   p.ckpt = w.own_ckpt ? reinterpret_cast<float*>(ws + w.ckpt) : a->ckpt;
+  p.ysave = (a->z != nullptr && a->ckpt != nullptr) ? a->ysave : nullptr;
   if (w.own_ckpt) {
-    ScanParams pf = p;  // states-only forward to produce the block checkpoints
+    ScanParams pf = make_params(a, scan_fwd_waves());  // states-only forward: block checkpoints
+    pf.ckpt = p.ckpt;
     if (int rc = hip_status(scan_fwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
       return rc;
   }
@@ -176,7 +206,8 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   p.dA_part = w.part_dA ? reinterpret_cast<float*>(ws + w.dA) : a->dA;
   p.dD_part = reinterpret_cast<float*>(ws + w.dD);
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
-  if (int rc = hip_status(scan_bwd_launch(p, a->dtype, st), "selective_scan_bwd launch")) return rc;
+  if (int rc = hip_status(scan_bwd_launch(p, a->dtype, waves, st), "selective_scan_bwd launch"))
+    return rc;
   if (w.part_bc) {
     const int64_t slices = p.batch * p.ngroups, per = p.seqlen * p.dstate;
     if (int rc = hip_status(scan_reduce_bc_launch(p.dB_part, a->dB, slices, p.nblk_c, per, st),

@@ -19,6 +19,7 @@ void clear_error();
 int hip_status(hipError_t e, const char* what);
 
 inline bool valid_dtype(int dt) { return dt == MCPU_F32 || dt == MCPU_BF16 || dt == MCPU_F16; }
+inline int64_t dtype_size(int dt) { return dt == MCPU_F32 ? 4 : 2; }
 inline size_t align_up(size_t bytes) { return (bytes + 255) & ~size_t(255); }
 
 // Fills n floats with zero on `stream`.

@@ -48,18 +48,26 @@ template <typename T> __device__ __forceinline__ void st(void* base, int64_t idx
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoid(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
 
-// softplus with threshold 20 (the torch default): x > 20 ? x : log1p(exp(x)).
-// NaN propagates. log1p uses the u = 1 + e correction (log(u) * e / (u - 1)),
-// accurate to a few ulp also where e is tiny.
-__device__ __forceinline__ float softplus(float x) {
-  if (x > 20.f) return x;
-  const float e = fast_exp(x);
+// softplus with threshold 20 (the torch default): x > 20 ? x : log1p(exp(x)),
+// without branches. NaN propagates. log1p(e) uses the u = 1 + e correction
+// log(u) * e / (u - 1), accurate to a few ulp also where e is tiny.
+// Also returns sigmoid(x) = e / (1 + e) from the same exponential.
+__device__ __forceinline__ float softplus_sigmoid(float x, float& sg) {
+  const bool big = !(x <= 20.f);  // also true for NaN
+  const float e = fast_exp(big ? 20.f : x);
   const float u = 1.0f + e;
   const float d = u - 1.0f;
   const float l = __builtin_amdgcn_logf(u) * kLn2;  // natural log of u
-  return d == 0.0f ? e : l * (e / d);
+  const float sp = d == 0.0f ? e : l * e * fast_rcp(d);
+  sg = big ? (x == x ? 1.0f : x) : e * fast_rcp(u);
+  return big ? x : sp;
+}
+__device__ __forceinline__ float softplus(float x) {
+  float sg;
+  return softplus_sigmoid(x, sg);
 }
 
 // ---- wave64 lane exchange ---------------------------------------------------------

@@ -4,37 +4,53 @@
 // bwd_row_body (reference csrc/selective_scan.cpp:168-248):
 //   g    = gh + dy_t C_t            (gh = dLoss/dh_t carried backwards)
 //   dC_t += dy_t h_t ;  dB_t += g dt_t u_t
-//   ga   = g h_{t-1} exp(dt_t A) ;  dA += ga dt_t
+//   gh'  = g exp(dt_t A) ;  ga = gh' h_{t-1} ;  dA += ga dt_t
 //   ddt  = <ga, A> + u_t <g, B_t> ;  du_t = dy_t D + dt_t <g, B_t>
-//   ddelta_t = ddt * sigmoid(delta_t + bias) if softplus ; gh = g exp(dt_t A)
+//   ddelta_t = ddt * sigmoid(delta_t + bias) if softplus ; gh = gh'
 // with dy_t = dout_t z_t s(z_t) and dz_t = dout_t y_t s(z_t)(1 + z_t(1 - s(z_t))).
 //
 // Instead of the reference's per-thread copy of every state (L * dstate floats
 // per row), time is walked backwards in 16-step blocks: each block restarts
 // from the checkpointed state at its start (written by the forward kernel),
 // recomputes its 16 states and decay factors in registers, then runs the
-// reverse recurrence. Sums over states use DPP row reduce-scatters; dB/dC sums
-// over channels use permlane swaps inside a wave, then LDS across the
-// workgroup's 4 waves, then one partial per workgroup that a separate kernel
-// reduces in a fixed order (deterministic, no atomics). dA/dD/ddelta_bias are
-// per-(batch, channel) partials reduced over the batch the same way.
+// reverse recurrence. y_t comes from the forward's saved copy when one is
+// given, otherwise from a recomputed <h_t, C_t>. Sums over states use DPP row
+// reduce-scatters; dB/dC sums over channels use permlane swaps inside a wave,
+// then LDS across the workgroup's W waves, then one partial per workgroup that
+// a separate kernel reduces in a fixed order (deterministic, no atomics).
+// dA/dD/ddelta_bias are per-(batch, channel) partials reduced over the batch
+// the same way. Operands of the next (earlier) block are fetched while the
+// current block computes.
+#include <cstdlib>
+
 #include "scan_common.h"
 
 namespace mcpu {
 
-template <typename Tx, int SPL, bool HAS_Z>
-__global__ void __launch_bounds__(kScanThreads) scan_bwd_kernel(const ScanParams p) {
+template <typename Tx, int W, int SPL, bool HAS_Z, bool HAS_Y>
+__global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
+  constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
-  __shared__ float lds_dB[kScanWaves][kScanBlockT][NW];
-  __shared__ float lds_dC[kScanWaves][kScanBlockT][NW];
+  constexpr int T = kScanBlockT;
+  using BC = BCStage<W, SPL>;
+  // [buffer][u, delta, dout, z, y][channel][step]
+  __shared__ __align__(16) float s_x[2][5][CH][T];
+  __shared__ __align__(16) float s_B[2][NW][kBCPad];
+  __shared__ __align__(16) float s_C[2][NW][kBCPad];
+  // [buffer][dB, dC][wave][step][state]: per-wave channel sums awaiting the
+  // cross-wave sum.
+  __shared__ float s_red[2][2][W][T][NW];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
-  const RowCtx rc = scan_row_ctx(p, wave, r);
+  const int c_local = wave * kScanRowsPerWave + r;
+  const RowCtx rc = scan_row_ctx<W>(p, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t cblk = blockIdx.x % p.nblk_c;
+  const int64_t kl = p.nblk - 1;  // last block
+  const int64_t t_last = kl * T;
 
   float Av[SPL], A2[SPL], gh[SPL], dA_acc[SPL];
 #pragma unroll
@@ -47,67 +63,165 @@ __global__ void __launch_bounds__(kScanThreads) scan_bwd_kernel(const ScanParams
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
-  const int64_t ubase = rc.b * p.su[0] + rc.d * p.su[1];
-  const int64_t dbase = rc.b * p.sdl[0] + rc.d * p.sdl[1];
-  const int64_t zbase = rc.b * p.sz[0] + rc.d * p.sz[1];
-  const int64_t obase = rc.b * p.sdo[0] + rc.d * p.sdo[1];
-  const float* Bbase = p.B + rc.b * p.sB[0] + rc.g * p.sB[1];
-  const float* Cbase = p.C + rc.b * p.sC[0] + rc.g * p.sC[1];
-  const float* ck = p.ckpt + row * p.nblk * N;
-  const int64_t part_base = ((rc.b * p.ngroups + rc.g) * p.nblk_c + cblk) * L;
+  const bool has_D = p.D != nullptr;
+  const bool softplus_on = p.softplus != 0;
   float dD_acc = 0.f, dbias_acc = 0.f;
 
-  for (int64_t k = p.nblk - 1; k >= 0; --k) {
-    const int64_t t0 = k * kScanBlockT;
-    const int64_t t = t0 + j;
-    const bool tv = t < L;
-    const int nvalid = static_cast<int>(L - t0 < kScanBlockT ? L - t0 : kScanBlockT);
-    const float uu = tv ? ld<Tx>(p.u, ubase + t * p.su[2]) : 0.f;
-    const float dl = tv ? ld<Tx>(p.delta, dbase + t * p.sdl[2]) : 0.f;
-    const float go = (tv && p.dout != nullptr) ? ld<Tx>(p.dout, obase + t * p.sdo[2]) : 0.f;
-    const float zz = (HAS_Z && tv) ? ld<Tx>(p.z, zbase + t * p.sz[2]) : 0.f;
+  // Staging cursors, all positioned on the last block and walked backwards.
+  XStage<W> xu, xd, xo, xz, xy;
+  xu.template init<Tx>(tid, p.u, p.su, p, rc, t_last);
+  xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, t_last);
+  const bool has_dout = p.dout != nullptr;
+  xo.template init<Tx>(tid, has_dout ? p.dout : p.u, p.sdo, p, rc, t_last);
+  if (HAS_Z) xz.template init<Tx>(tid, p.z, p.sz, p, rc, t_last);
+  const int64_t sy[3] = {p.dim * L, L, 1};
+  if (HAS_Y) xy.template init<Tx>(tid, p.ysave, sy, p, rc, t_last);
+  BC tb, tc;
+  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, t_last);
+  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, t_last);
 
-    float Bv[kScanBlockT][SPL], Cv[kScanBlockT][SPL], h0[SPL];
+  // Rows of the workgroup: uniform first row + per-lane offsets (rows past the
+  // slice end use the last channel for loads and store nothing).
+  const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
+  const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);  // this lane's row within the workgroup
+  // Checkpointed state lane j of the current block.
+  const char* ck_base = reinterpret_cast<const char*>(p.ckpt + (row0 * p.nblk + kl) * N);
+  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
+  // Per-lane outputs at step t0 + j of the current block; du, ddelta and dz
+  // are contiguous (batch, dim, seqlen) and share the offset.
+  const int64_t o_pos = (row0 * L + t_last) * static_cast<int64_t>(sizeof(Tx));
+  const uint32_t o_off = static_cast<uint32_t>(sizeof(Tx) * (crow * L + j));
+  char* o_du = static_cast<char*>(p.du) + o_pos;
+  char* o_dd = static_cast<char*>(p.ddelta) + o_pos;
+  char* o_dz = HAS_Z ? static_cast<char*>(p.dz) + o_pos : nullptr;
+
+  // Cross-wave dB/dC outputs of this thread: element e = (array, step, state).
+  // T * NW is a multiple of 64, so the array is uniform over a wave.
+  constexpr int NOUT = (2 * T * NW + 64 * W - 1) / (64 * W);
+  const int64_t part_row = ((rc.b * p.ngroups + rc.g) * p.nblk_c + rc.cblk) * L + t_last;
+  char* o_part[NOUT];
+  uint32_t o_poff[NOUT];
+  int o_red[NOUT], o_t[NOUT];
+  bool o_ok[NOUT];
+#pragma unroll
+  for (int q = 0; q < NOUT; ++q) {
+    const int e = tid + q * 64 * W;
+    const int arr = __builtin_amdgcn_readfirstlane(e / (T * NW));
+    const int tt = (e % (T * NW)) / NW, n = e % NW;
+    o_t[q] = tt;
+    o_red[q] = (arr * W * T + tt) * NW + n;  // index of (arr, wave 0, tt, n) in s_red[buf]
+    o_ok[q] = e < 2 * T * NW && n < N;
+    o_part[q] = reinterpret_cast<char*>((arr == 0 ? p.dB_part : p.dC_part) + part_row * N);
+    o_poff[q] = static_cast<uint32_t>(sizeof(float) * (tt * N + n));
+  }
+
+  float nu = 0.f, nd = 0.f, no = 0.f, nz = 0.f, ny = 0.f;
+  float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
+  float nh0[SPL];
+  // Loads the operands of the block at t0 (full unless GUARD) and moves every
+  // cursor one block back.
+  auto fetch = [&](auto GUARD, int64_t t0) {
+    if constexpr (decltype(GUARD)::value) {
+      nu = xu.template load_guarded<Tx>(t0, L);
+      nd = xd.template load_guarded<Tx>(t0, L);
+      no = has_dout ? xo.template load_guarded<Tx>(t0, L) : 0.f;
+      if (HAS_Z) nz = xz.template load_guarded<Tx>(t0, L);
+      if (HAS_Y) ny = xy.template load_guarded<Tx>(t0, L);
+      tb.load_guarded(t0, L, nB);
+      tc.load_guarded(t0, L, nC);
+    } else {
+      nu = xu.template load<Tx>();
+      nd = xd.template load<Tx>();
+      no = has_dout ? xo.template load<Tx>() : 0.f;
+      if (HAS_Z) nz = xz.template load<Tx>();
+      if (HAS_Y) ny = xy.template load<Tx>();
+      tb.load(nB);
+      tc.load(nC);
+    }
+#pragma unroll
+    for (int s = 0; s < SPL; ++s)
+      nh0[s] = (j + 16 * s < N) ? *reinterpret_cast<const float*>(ck_base + ck_off + 64 * s) : 0.f;
+    xu.advance(-1);
+    xd.advance(-1);
+    xo.advance(-1);
+    if (HAS_Z) xz.advance(-1);
+    if (HAS_Y) xy.advance(-1);
+    tb.advance(-1);
+    tc.advance(-1);
+    ck_base -= sizeof(float) * N;
+  };
+  auto park = [&](int buf) {
+    (&s_x[buf][0][0][0])[xu.slot] = nu;
+    (&s_x[buf][1][0][0])[xd.slot] = nd;
+    (&s_x[buf][2][0][0])[xo.slot] = no;
+    if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = nz;
+    if (HAS_Y) (&s_x[buf][4][0][0])[xy.slot] = ny;
+    tb.park(s_B[buf], nB);
+    tc.park(s_C[buf], nC);
+  };
+
+  float h0[SPL];
+  if (p.nblk > 0) {
+    fetch(std::true_type{}, t_last);
+    park(static_cast<int>(kl & 1));
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) h0[s] = nh0[s];
+  }
+  __syncthreads();
+  // Retire every load issued so far, so the loop never has to wait for the
+  // prefetch of the next block on behalf of a value loaded above.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // One block; FULL = all 16 steps exist (every block but possibly the last).
+  auto block = [&](auto FULL, int64_t k, int nvalid) {
+    constexpr bool full = decltype(FULL)::value;
+    const int buf = static_cast<int>(k & 1);
+    const int64_t t0 = k * T;
+    if (k > 0) fetch(std::false_type{}, t0 - T);
+    auto valid = [&](int i) { return full || i < nvalid; };
+
+    const bool tv = full || j < nvalid;
+    const float uu = s_x[buf][0][c_local][j];
+    const float dl = s_x[buf][1][c_local][j];
+    const float go = s_x[buf][2][c_local][j];
+    const float zz = HAS_Z ? s_x[buf][3][c_local][j] : 0.f;
+
+    float Bv[SPL][T], Cv[SPL][T];
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {
-      const int n = j + 16 * s;
-      h0[s] = n < N ? ck[k * N + n] : 0.f;
-#pragma unroll
-      for (int i = 0; i < kScanBlockT; ++i) {
-        const bool ok = i < nvalid && n < N;
-        Bv[i][s] = ok ? Bbase[(t0 + i) * p.sB[2] + n] : 0.f;
-        Cv[i][s] = ok ? Cbase[(t0 + i) * p.sC[2] + n] : 0.f;
-      }
+      read_bc_row(s_B[buf], j + 16 * s, Bv[s]);
+      read_bc_row(s_C[buf], j + 16 * s, Cv[s]);
     }
 
     const float pre = dl + bias;
-    const float dt = p.softplus ? softplus(pre) : pre;
+    float dt = pre, sg_pre = 1.f;
+    if (softplus_on) dt = softplus_sigmoid(pre, sg_pre);
     const float dtu = dt * uu;
 
     // Forward recompute of the block's states and decay factors.
-    float hs[kScanBlockT][SPL], as[kScanBlockT][SPL], pacc[kScanBlockT];
+    float hs[SPL][T], as[SPL][T], pacc[T];
     {
       float hc[SPL];
 #pragma unroll
       for (int s = 0; s < SPL; ++s) hc[s] = h0[s];
-      static_for<kScanBlockT>([&](auto I) {
+      static_for<T>([&](auto I) {
         constexpr int i = decltype(I)::value;
-        if (i < nvalid) {
+        if (valid(i)) {
           const float dti = row_bcast<i>(dt);
           const float dtui = row_bcast<i>(dtu);
           float acc = 0.f;
 #pragma unroll
           for (int s = 0; s < SPL; ++s) {
             const float a = fast_exp2(dti * A2[s]);
-            hc[s] = fmaf(a, hc[s], dtui * Bv[i][s]);
-            hs[i][s] = hc[s];
-            as[i][s] = a;
-            if (HAS_Z) acc = fmaf(hc[s], Cv[i][s], acc);
+            hc[s] = fmaf(a, hc[s], dtui * Bv[s][i]);
+            hs[s][i] = hc[s];
+            as[s][i] = a;
+            if (HAS_Z && !HAS_Y) acc = fmaf(hc[s], Cv[s][i], acc);
           }
           pacc[i] = acc;
         } else {
 #pragma unroll
-          for (int s = 0; s < SPL; ++s) hs[i][s] = as[i][s] = 0.f;
+          for (int s = 0; s < SPL; ++s) hs[s][i] = as[s][i] = 0.f;
           pacc[i] = 0.f;
         }
       });
@@ -116,33 +230,38 @@ __global__ void __launch_bounds__(kScanThreads) scan_bwd_kernel(const ScanParams
     // Output gating: dy_t and dz_t for the step this lane owns.
     float dy = go, dzv = 0.f;
     if (HAS_Z) {
-      float y = row_reduce_scatter16(pacc, j);
-      if (p.D != nullptr) y = fmaf(Dd, uu, y);
+      float y;
+      if (HAS_Y) {
+        y = s_x[buf][4][c_local][j];
+      } else {
+        y = row_reduce_scatter16(pacc, j);
+        if (has_D) y = fmaf(Dd, uu, y);
+      }
       const float sg = sigmoid(zz);
       dzv = go * y * sg * (1.f + zz * (1.f - sg));
       dy = go * zz * sg;
     }
 
     // Reverse recurrence over the block.
-    float r1[kScanBlockT], r2[kScanBlockT], dBc[SPL][kScanBlockT], dCc[SPL][kScanBlockT];
-    static_for<kScanBlockT>([&](auto I) {
-      constexpr int i = kScanBlockT - 1 - decltype(I)::value;
-      if (i < nvalid) {
+    float r1[T], r2[T], dBc[SPL][T], dCc[SPL][T];
+    static_for<T>([&](auto I) {
+      constexpr int i = T - 1 - decltype(I)::value;
+      if (valid(i)) {
         const float dyi = row_bcast<i>(dy);
         const float dti = row_bcast<i>(dt);
         const float dtui = row_bcast<i>(dtu);
         float acc1 = 0.f, acc2 = 0.f;
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
-          const float g = fmaf(dyi, Cv[i][s], gh[s]);
-          dCc[s][i] = dyi * hs[i][s];
-          const float hp = i > 0 ? hs[i > 0 ? i - 1 : 0][s] : h0[s];
-          const float ga = g * hp * as[i][s];
+          const float g = fmaf(dyi, Cv[s][i], gh[s]);
+          dCc[s][i] = dyi * hs[s][i];
+          const float hp = i > 0 ? hs[s][i > 0 ? i - 1 : 0] : h0[s];
+          gh[s] = g * as[s][i];
+          const float ga = gh[s] * hp;
           dA_acc[s] = fmaf(ga, dti, dA_acc[s]);
           acc1 = fmaf(ga, Av[s], acc1);
-          acc2 = fmaf(g, Bv[i][s], acc2);
+          acc2 = fmaf(g, Bv[s][i], acc2);
           dBc[s][i] = g * dtui;
-          gh[s] = g * as[i][s];
         }
         r1[i] = acc1;
         r2[i] = acc2;
@@ -155,51 +274,66 @@ __global__ void __launch_bounds__(kScanThreads) scan_bwd_kernel(const ScanParams
 
     const float R1 = row_reduce_scatter16(r1, j);  // <ga, A> for step t
     const float R2 = row_reduce_scatter16(r2, j);  // <g, B_t> for step t
+    float ddt = fmaf(uu, R2, R1);
+    const float duv = fmaf(dy, Dd, dt * R2);
+    if (softplus_on) ddt *= sg_pre;
     if (tv) {
-      float ddt = fmaf(uu, R2, R1);
-      const float duv = fmaf(dy, Dd, dt * R2);
-      if (p.softplus) ddt *= sigmoid(pre);
-      if (rc.active) {
-        st<Tx>(p.du, row * L + t, duv);
-        st<Tx>(p.ddelta, row * L + t, ddt);
-        if (HAS_Z) st<Tx>(p.dz, row * L + t, dzv);
-      }
       dD_acc = fmaf(dy, uu, dD_acc);
       dbias_acc += ddt;
     }
 
-    // dB/dC: sum over the workgroup's channels.
+    // dB/dC: sum over the wave's 4 channels, park for the cross-wave sum.
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {
       if (!rc.active) {
 #pragma unroll
-        for (int i = 0; i < kScanBlockT; ++i) dBc[s][i] = dCc[s][i] = 0.f;
+        for (int i = 0; i < T; ++i) dBc[s][i] = dCc[s][i] = 0.f;
       }
       float yB[4], yC[4];
       wave_rows_reduce_scatter(dBc[s], yB);
       wave_rows_reduce_scatter(dCc[s], yC);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        lds_dB[wave][4 * r + q][j + 16 * s] = yB[q];
-        lds_dC[wave][4 * r + q][j + 16 * s] = yC[q];
+        s_red[buf][0][wave][4 * r + q][j + 16 * s] = yB[q];
+        s_red[buf][1][wave][4 * r + q][j + 16 * s] = yC[q];
       }
     }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < kScanBlockT * NW; idx += kScanThreads) {
-      const int tt = idx / NW, n = idx % NW;
-      if (n < N && tt < nvalid) {
-        float sb = 0.f, sc = 0.f;
+    if (k > 0) {
+      park(buf ^ 1);
 #pragma unroll
-        for (int w = 0; w < kScanWaves; ++w) {
-          sb += lds_dB[w][tt][n];
-          sc += lds_dC[w][tt][n];
-        }
-        p.dB_part[(part_base + t0 + tt) * N + n] = sb;
-        p.dC_part[(part_base + t0 + tt) * N + n] = sc;
-      }
+      for (int s = 0; s < SPL; ++s) h0[s] = nh0[s];
     }
+    // Stores after the park, so waiting for the prefetch never waits for them.
+    if (tv && rc.active) {
+      *reinterpret_cast<Tx*>(o_du + o_off) = from_f32<Tx>(duv);
+      *reinterpret_cast<Tx*>(o_dd + o_off) = from_f32<Tx>(ddt);
+      if (HAS_Z) *reinterpret_cast<Tx*>(o_dz + o_off) = from_f32<Tx>(dzv);
+    }
+    o_du -= T * sizeof(Tx);
+    o_dd -= T * sizeof(Tx);
+    if (HAS_Z) o_dz -= T * sizeof(Tx);
     __syncthreads();
+
+    // Cross-wave sum of this block's dB/dC and the workgroup's partial.
+#pragma unroll
+    for (int q = 0; q < NOUT; ++q) {
+      if (o_ok[q] && (full || o_t[q] < nvalid)) {
+        const float* src = &s_red[buf][0][0][0][0] + o_red[q];
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc += src[w * T * NW];
+        *reinterpret_cast<float*>(o_part[q] + o_poff[q]) = acc;
+      }
+      o_part[q] -= sizeof(float) * T * N;
+    }
+  };
+
+  if (p.nblk > 0) {
+    const int nlast = static_cast<int>(L - t_last);
+    if (nlast == T) block(std::true_type{}, kl, T);
+    else block(std::false_type{}, kl, nlast);
   }
+  for (int64_t k = kl - 1; k >= 0; --k) block(std::true_type{}, k, T);
 
   if (rc.active) {
 #pragma unroll
@@ -214,10 +348,41 @@ __global__ void __launch_bounds__(kScanThreads) scan_bwd_kernel(const ScanParams
   }
 }
 
-// dB/dC: out[b, g, t, n] = sum over channel blocks of part[b, g, cblk, t, n].
+// dB/dC: out[s, e] = sum over channel blocks c of part[s, c, e], summed in
+// the order c = 0, 1, ... for every element (deterministic). Four elements per
+// thread.
 __global__ void __launch_bounds__(256) reduce_bc_kernel(const float* __restrict__ part,
                                                         float* __restrict__ out, int64_t slices,
                                                         int64_t nblk_c, int64_t per_slice) {
+  const int64_t per4 = per_slice / 4;
+  const int64_t total4 = slices * per4;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total4; i += 256ll * gridDim.x) {
+    const int64_t sl = i / per4, e = (i % per4) * 4;
+    const float* src = part + sl * nblk_c * per_slice + e;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int64_t c = 0;
+    for (; c + 4 <= nblk_c; c += 4) {
+      const float4 v0 = *reinterpret_cast<const float4*>(src + (c + 0) * per_slice);
+      const float4 v1 = *reinterpret_cast<const float4*>(src + (c + 1) * per_slice);
+      const float4 v2 = *reinterpret_cast<const float4*>(src + (c + 2) * per_slice);
+      const float4 v3 = *reinterpret_cast<const float4*>(src + (c + 3) * per_slice);
+      acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;
+      acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;
+      acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;
+      acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;
+    }
+    for (; c < nblk_c; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(src + c * per_slice);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    *reinterpret_cast<float4*>(out + sl * per_slice + e) = acc;
+  }
+}
+
+// Same, one element per thread, for sizes that are not a multiple of 4.
+__global__ void __launch_bounds__(256) reduce_bc1_kernel(const float* __restrict__ part,
+                                                         float* __restrict__ out, int64_t slices,
+                                                         int64_t nblk_c, int64_t per_slice) {
   const int64_t total = slices * per_slice;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += 256ll * gridDim.x) {
     const int64_t sl = i / per_slice, e = i % per_slice;
@@ -239,30 +404,55 @@ __global__ void __launch_bounds__(256) reduce_batch_kernel(const float* __restri
   }
 }
 
-template <typename Tx, int SPL>
-static hipError_t launch_bwd_z(const ScanParams& p, hipStream_t stream) {
-  const int64_t blocks = p.batch * p.ngroups * p.nblk_c;
-  if (p.z != nullptr)
-    hipLaunchKernelGGL((scan_bwd_kernel<Tx, SPL, true>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kScanThreads), 0, stream, p);
+template <typename Tx, int W, int SPL>
+static hipError_t launch_bwd_zy(const ScanParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c));
+  const dim3 block(64 * W);
+  if (p.z != nullptr && p.ysave != nullptr)
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, true>), grid, block, 0, stream, p);
+  else if (p.z != nullptr)
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_bwd_kernel<Tx, SPL, false>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kScanThreads), 0, stream, p);
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, false, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
+// Wider workgroups (8 or 12 waves) only for dstate <= 16, where their LDS fits.
 template <typename Tx>
-static hipError_t launch_bwd_spl(const ScanParams& p, hipStream_t stream) {
-  if (p.dstate <= 16) return launch_bwd_z<Tx, 1>(p, stream);
-  if (p.dstate <= 32) return launch_bwd_z<Tx, 2>(p, stream);
-  return launch_bwd_z<Tx, 4>(p, stream);
+static hipError_t launch_bwd_w(const ScanParams& p, int waves, hipStream_t stream) {
+  if (p.dstate <= 16) {
+    if (waves == 12) return launch_bwd_zy<Tx, 12, 1>(p, stream);
+    if (waves == 8) return launch_bwd_zy<Tx, 8, 1>(p, stream);
+    return launch_bwd_zy<Tx, 4, 1>(p, stream);
+  }
+  if (p.dstate <= 32) return launch_bwd_zy<Tx, 4, 2>(p, stream);
+  return launch_bwd_zy<Tx, 4, 4>(p, stream);
 }
 
-hipError_t scan_bwd_launch(const ScanParams& p, int dtype, hipStream_t stream) {
+// Waves per backward workgroup. More waves mean fewer dB/dC partials to
+// reduce; the choice keeps enough workgroups to fill the GPU's 256 compute
+// units in whole rounds.
+int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) {
+  if (dstate > 16) return 4;  // keeps the per-workgroup LDS small
+  // MCPU_SCAN_BWD_WAVES=4|8|12 overrides the choice (tuning).
+  if (const char* env = std::getenv("MCPU_SCAN_BWD_WAVES")) {
+    const int w = std::atoi(env);
+    if (w == 4 || w == 8 || w == 12) return w;
+  }
+  const int64_t slices = batch * ngroups;
+  for (int w : {12, 8}) {
+    const int64_t wgs = slices * ((dpg + 4 * w - 1) / (4 * w));
+    const int64_t pad = slices * ((dpg + 4 * w - 1) / (4 * w)) * 4 * w - slices * dpg;
+    if (wgs >= 256 && wgs % 256 == 0 && pad == 0) return w;
+  }
+  return 4;
+}
+
+hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream) {
   switch (dtype) {
-    case MCPU_F32: return launch_bwd_spl<float>(p, stream);
-    case MCPU_BF16: return launch_bwd_spl<bf16>(p, stream);
-    default: return launch_bwd_spl<f16>(p, stream);
+    case MCPU_F32: return launch_bwd_w<float>(p, waves, stream);
+    case MCPU_BF16: return launch_bwd_w<bf16>(p, waves, stream);
+    default: return launch_bwd_w<f16>(p, waves, stream);
   }
 }
 
@@ -274,8 +464,13 @@ static unsigned grid_for(int64_t n) {
 
 hipError_t scan_reduce_bc_launch(const float* part, float* out, int64_t slices, int64_t nblk_c,
                                  int64_t per_slice, hipStream_t stream) {
-  hipLaunchKernelGGL(reduce_bc_kernel, dim3(grid_for(slices * per_slice)), dim3(256), 0, stream,
-                     part, out, slices, nblk_c, per_slice);
+  if (per_slice % 4 == 0) {
+    hipLaunchKernelGGL(reduce_bc_kernel, dim3(grid_for(slices * per_slice / 4)), dim3(256), 0,
+                       stream, part, out, slices, nblk_c, per_slice);
+  } else {
+    hipLaunchKernelGGL(reduce_bc1_kernel, dim3(grid_for(slices * per_slice)), dim3(256), 0, stream,
+                       part, out, slices, nblk_c, per_slice);
+  }
   return hipGetLastError();
 }
 

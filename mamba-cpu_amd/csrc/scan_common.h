@@ -1,13 +1,23 @@
-// Selective-scan kernel parameters and the shared lane layout.
+// Selective-scan kernel parameters, lane layout and the LDS staging shared by
+// the forward and backward kernels.
 //
-// Lane layout (forward and backward): a workgroup is 4 waves; each wave holds
-// 4 channels (rows r = lane / 16) x 16 state lanes (j = lane % 16); lane j owns
-// states n = j + 16 * s for s < SPL (SPL = ceil(dstate / 16)). Time is walked
-// in blocks of 16 steps; within a block lane j also "owns" step t0 + j for the
-// per-step scalar work (loading u/delta/z/dout, softplus, gating, stores), and
-// the other lanes of its row read those scalars through DPP row broadcasts.
-// A workgroup covers 16 consecutive channels of one (batch, group) slice, so
-// all its rows share the same B/C rows.
+// Lane layout: a workgroup is W waves; each wave holds 4 channels (rows
+// r = lane / 16) x 16 state lanes (j = lane % 16); lane j owns states
+// n = j + 16 * s for s < SPL (SPL = ceil(dstate / 16)). A workgroup covers
+// 4W consecutive channels of one (batch, group) slice, so all its rows share
+// the same B/C rows. Time is walked in blocks of 16 steps; within a block lane
+// j also "owns" step t0 + j for the per-step scalar work (softplus, gating,
+// stores), and the other lanes of its row read those scalars through DPP row
+// broadcasts.
+//
+// Staging: every per-step input of the next block (u, delta, z, dout, y and
+// the B/C rows) is fetched into registers by the whole workgroup while the
+// current block computes, then parked in a double-buffered LDS tile, so a
+// block starts with its operands already on chip. Each tile is fetched with
+// the thread index running along whichever dimension is contiguous in memory
+// (time for (batch, dim, seqlen) tensors, channel for transposed views;
+// state or time for B/C), which keeps the global loads coalesced for both
+// the reference's layouts and Hugging Face's strided views.
 #pragma once
 
 #include "mcpu_common.h"
@@ -16,9 +26,8 @@ namespace mcpu {
 
 constexpr int kScanBlockT = 16;       // time steps per block
 constexpr int kScanRowsPerWave = 4;   // channels per wave
-constexpr int kScanWaves = 4;         // waves per workgroup
-constexpr int kScanChannelsPerWG = kScanRowsPerWave * kScanWaves;
-constexpr int kScanThreads = 64 * kScanWaves;
+constexpr int kScanMaxWaves = 12;     // widest workgroup of either kernel
+constexpr int kBCPad = 20;            // padded time stride of the B/C tiles (conflict-free b128 reads)
 
 struct ScanParams {
   const void* u;
@@ -32,6 +41,7 @@ struct ScanParams {
   void* out;
   float* last_state;
   float* ckpt;          // (batch, dim, nblk, dstate): state at the start of each block
+  void* ysave;          // (batch, dim, seqlen): y before the z gate
   const void* dout;
   const float* dlast_state;
   void* du;
@@ -44,27 +54,143 @@ struct ScanParams {
   float* dbias_part;    // (batch, dim)
   int64_t batch, dim, seqlen, dstate, ngroups, dpg;
   int64_t nblk;         // ceil(seqlen / 16)
-  int64_t nblk_c;       // ceil(dpg / 16)
-  int64_t su[3], sdl[3], sz[3], sB[3], sC[3], sdo[3];
+  int64_t nblk_c;       // channel blocks per slice: ceil(dpg / (4 W))
+  int64_t su[3], sdl[3], sz[3], sdo[3];
+  int64_t sB[4], sC[4];
   int softplus;
 };
 
 struct RowCtx {
   int64_t b, g, d;     // batch, group, channel (clamped into range)
-  bool active;         // channel exists (rows past the slice end are padding)
+  int64_t cl0;         // first channel (within the group) of the workgroup
+  int64_t cblk;        // channel block of the workgroup
+  bool active;         // this row's channel exists (rows past the slice end are padding)
 };
 
+template <int W>
 __device__ __forceinline__ RowCtx scan_row_ctx(const ScanParams& p, int wave, int r) {
   int64_t bid = blockIdx.x;
-  const int64_t cblk = bid % p.nblk_c;
-  bid /= p.nblk_c;
   RowCtx c;
+  c.cblk = bid % p.nblk_c;
+  bid /= p.nblk_c;
   c.g = bid % p.ngroups;
   c.b = bid / p.ngroups;
-  const int64_t cl = cblk * kScanChannelsPerWG + wave * kScanRowsPerWave + r;
+  c.cl0 = c.cblk * (4 * W);
+  const int64_t cl = c.cl0 + wave * kScanRowsPerWave + r;
   c.active = cl < p.dpg;
   c.d = c.g * p.dpg + (c.active ? cl : p.dpg - 1);
   return c;
+}
+
+// One (4W channels x 16 steps) tile of a (batch, dim, seqlen) tensor. A
+// thread's element is addressed as a uniform base (scalar registers), which
+// moves by one block per advance(), plus a fixed per-thread 32-bit byte offset,
+// so the loads use the scalar-base + vector-offset form and the running state
+// costs one vector register. Channel-fastest when the channel stride is 1.
+// Rows past the slice end read the slice's last channel (never out of range).
+// The host guarantees (4W - 1) * |s[1]| + 15 * |s[2]| elements fit the offset.
+template <int W>
+struct XStage {
+  const char* base;  // uniform: element (batch, first channel of the workgroup, t0)
+  int64_t step;      // uniform: bytes per block
+  uint32_t off;      // per thread: byte offset of its element from base
+  int slot;          // per thread: index c * 16 + t of its element in the LDS tile
+  int t;             // per thread: its step within the block
+  template <typename Tx>
+  __device__ __forceinline__ void init(int tid, const void* p_base, const int64_t (&s)[3],
+                                       const ScanParams& p, const RowCtx& rc, int64_t t0) {
+    int c;
+    if (s[1] == 1 && s[2] != 1) {
+      c = tid % (4 * W);
+      t = tid / (4 * W);
+    } else {
+      c = tid / kScanBlockT;
+      t = tid % kScanBlockT;
+    }
+    slot = c * kScanBlockT + t;
+    const int64_t last = p.dpg - 1 - rc.cl0;
+    const int64_t ce = c < last ? c : last;
+    constexpr int64_t sz = sizeof(Tx);
+    base = static_cast<const char*>(p_base) +
+           sz * (rc.b * s[0] + (rc.g * p.dpg + rc.cl0) * s[1] + t0 * s[2]);
+    off = static_cast<uint32_t>(sz * (ce * s[1] + t * s[2]));
+    step = sz * kScanBlockT * s[2];
+  }
+  template <typename Tx>
+  __device__ __forceinline__ float load() const {
+    return to_f32(*reinterpret_cast<const Tx*>(base + off));
+  }
+  // For a block that may extend past the sequence end.
+  template <typename Tx>
+  __device__ __forceinline__ float load_guarded(int64_t t0, int64_t L) const {
+    return t0 + t < L ? load<Tx>() : 0.f;
+  }
+  __device__ __forceinline__ void advance(int dir) { base += dir * step; }
+};
+
+// B or C rows of one block, parked transposed as [n][t] (padded) so a lane
+// reads its state's 16 steps with four 16-byte LDS reads. Addressed like
+// XStage: uniform base of the (batch, group) row at t0 + per-thread offset.
+template <int W, int SPL>
+struct BCStage {
+  static constexpr int NW = 16 * SPL;
+  static constexpr int PER_THREAD = (kScanBlockT * NW + 64 * W - 1) / (64 * W);
+  const char* base;  // uniform
+  int64_t step;      // uniform: bytes per block
+  uint32_t off[PER_THREAD];
+  int slot[PER_THREAD];  // n * kBCPad + t in the LDS tile, or -1 past the tile
+  int t[PER_THREAD];
+  bool ok[PER_THREAD];   // the state exists (n < dstate)
+  __device__ __forceinline__ void init(int tid, const float* row, const int64_t (&s)[4], int64_t N,
+                                       int64_t t0) {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int e = tid + i * 64 * W;
+      int n;
+      if (s[2] == 1 && s[3] != 1) {  // time contiguous: time-fastest
+        n = e / kScanBlockT;
+        t[i] = e % kScanBlockT;
+      } else {
+        n = e % NW;
+        t[i] = e / NW;
+      }
+      const bool in_tile = e < kScanBlockT * NW;
+      ok[i] = in_tile && n < N;
+      slot[i] = in_tile ? n * kBCPad + t[i] : -1;
+      off[i] = ok[i] ? static_cast<uint32_t>(sizeof(float) * (t[i] * s[2] + n * s[3])) : 0u;
+    }
+    base = reinterpret_cast<const char*>(row + t0 * s[2]);
+    step = static_cast<int64_t>(sizeof(float)) * kScanBlockT * s[2];
+  }
+  __device__ __forceinline__ void load(float (&v)[PER_THREAD]) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i)
+      v[i] = ok[i] ? *reinterpret_cast<const float*>(base + off[i]) : 0.f;
+  }
+  __device__ __forceinline__ void load_guarded(int64_t t0, int64_t L, float (&v)[PER_THREAD]) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i)
+      v[i] = (ok[i] && t0 + t[i] < L) ? *reinterpret_cast<const float*>(base + off[i]) : 0.f;
+  }
+  __device__ __forceinline__ void advance(int dir) { base += dir * step; }
+  __device__ __forceinline__ void park(float (*tile)[kBCPad], const float (&v)[PER_THREAD]) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i)
+      if (PER_THREAD * 64 * W == kScanBlockT * NW || slot[i] >= 0) (&tile[0][0])[slot[i]] = v[i];
+  }
+};
+
+// Reads the 16 steps of state lane n from a transposed B/C tile.
+__device__ __forceinline__ void read_bc_row(const float (*tile)[kBCPad], int n, float (&v)[kScanBlockT]) {
+  const float4* row = reinterpret_cast<const float4*>(tile[n]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 x = row[q];
+    v[4 * q + 0] = x.x;
+    v[4 * q + 1] = x.y;
+    v[4 * q + 2] = x.z;
+    v[4 * q + 3] = x.w;
+  }
 }
 
 }  // namespace mcpu

@@ -4,22 +4,37 @@
 // fwd_row_body, reference csrc/selective_scan.cpp:120-145):
 //   dt_t  = softplus?(delta_t + delta_bias)
 //   h_t   = exp(dt_t * A) * h_{t-1} + dt_t * u_t * B_t
-//   out_t = (<h_t, C_t> + D * u_t) * silu(z_t)
+//   y_t   = <h_t, C_t> + D * u_t ;  out_t = y_t * silu(z_t)
 // One state per lane (see scan_common.h); exp is v_exp_f32 on A * log2(e).
 // The <h_t, C_t> contraction over the 16 state lanes of a row is done for all
 // 16 steps of a block at once with a DPP reduce-scatter, which leaves y_t in
-// the lane that owns step t. Optional outputs: the final state, and the state
-// at the start of every 16-step block (checkpoints for the backward pass).
+// the lane that owns step t. Operands of block k+1 are fetched while block k
+// computes (double-buffered LDS). Optional outputs: the final state, the state
+// at the start of every block (checkpoints for the backward), and y before the
+// z gate (lets the backward skip recomputing it).
 #include "scan_common.h"
 
 namespace mcpu {
 
+constexpr int kFwdWaves = 4;
+
 template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT>
-__global__ void __launch_bounds__(kScanThreads) scan_fwd_kernel(const ScanParams p) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+__global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanParams p) {
+  constexpr int W = kFwdWaves;
+  constexpr int CH = 4 * W;
+  constexpr int NW = 16 * SPL;
+  using BC = BCStage<W, SPL>;
+  // [buffer][u, delta, z][channel][step]
+  __shared__ __align__(16) float s_x[2][3][CH][kScanBlockT];
+  __shared__ __align__(16) float s_B[2][NW][kBCPad];
+  __shared__ __align__(16) float s_C[2][NW][kBCPad];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
-  const RowCtx rc = scan_row_ctx(p, wave, r);
+  const int c_local = wave * kScanRowsPerWave + r;
+  const RowCtx rc = scan_row_ctx<W>(p, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
 
@@ -32,38 +47,85 @@ __global__ void __launch_bounds__(kScanThreads) scan_fwd_kernel(const ScanParams
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
-  const int64_t ubase = rc.b * p.su[0] + rc.d * p.su[1];
-  const int64_t dbase = rc.b * p.sdl[0] + rc.d * p.sdl[1];
-  const int64_t zbase = rc.b * p.sz[0] + rc.d * p.sz[1];
-  const float* Bbase = p.B + rc.b * p.sB[0] + rc.g * p.sB[1];
-  const float* Cbase = p.C + rc.b * p.sC[0] + rc.g * p.sC[1];
   float* ck = p.ckpt ? p.ckpt + row * p.nblk * N : nullptr;
 
-  for (int64_t k = 0; k < p.nblk; ++k) {
-    const int64_t t0 = k * kScanBlockT;
-    if (ck != nullptr && rc.active) {
-#pragma unroll
-      for (int s = 0; s < SPL; ++s)
-        if (j + 16 * s < N) ck[k * N + j + 16 * s] = h[s];
+  XStage<W> xu, xd, xz;
+  xu.template init<Tx>(tid, p.u, p.su, p, rc, 0);
+  xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, 0);
+  if (HAS_Z && WRITE_OUT) xz.template init<Tx>(tid, p.z, p.sz, p, rc, 0);
+  BC tb, tc;
+  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, 0);
+  if (WRITE_OUT) tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, 0);
+  // Only the last block can extend past the sequence end.
+  const int64_t t_full = L - L % kScanBlockT;
+
+  // Registers holding the next block's operands between fetch and park.
+  float nu = 0.f, nd = 0.f, nz = 0.f;
+  float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
+  auto fetch = [&](int64_t t0) {
+    if (t0 < t_full) {
+      nu = xu.template load<Tx>();
+      nd = xd.template load<Tx>();
+      if (HAS_Z && WRITE_OUT) nz = xz.template load<Tx>();
+      tb.load(nB);
+      if (WRITE_OUT) tc.load(nC);
+    } else {
+      nu = xu.template load_guarded<Tx>(t0, L);
+      nd = xd.template load_guarded<Tx>(t0, L);
+      if (HAS_Z && WRITE_OUT) nz = xz.template load_guarded<Tx>(t0, L);
+      tb.load_guarded(t0, L, nB);
+      if (WRITE_OUT) tc.load_guarded(t0, L, nC);
     }
+    xu.advance(1);
+    xd.advance(1);
+    if (HAS_Z && WRITE_OUT) xz.advance(1);
+    tb.advance(1);
+    if (WRITE_OUT) tc.advance(1);
+  };
+  auto park = [&](int buf) {
+    (&s_x[buf][0][0][0])[xu.slot] = nu;
+    (&s_x[buf][1][0][0])[xd.slot] = nd;
+    if (HAS_Z && WRITE_OUT) (&s_x[buf][2][0][0])[xz.slot] = nz;
+    tb.park(s_B[buf], nB);
+    if (WRITE_OUT) tc.park(s_C[buf], nC);
+  };
+
+  if (p.nblk > 0) {
+    fetch(0);
+    park(0);
+  }
+  __syncthreads();
+  // Retire every load issued so far. Otherwise the loop's first use of a
+  // value loaded above (bias, D, A) makes the compiler wait for all memory
+  // operations at the top of every block, which would also wait for the
+  // prefetch of the next block.
+  __builtin_amdgcn_s_waitcnt(0);
+  if (ck != nullptr && rc.active && p.nblk > 0) {
+#pragma unroll
+    for (int s = 0; s < SPL; ++s)
+      if (j + 16 * s < N) ck[j + 16 * s] = 0.f;
+  }
+
+  // Per block: prefetch the next block, compute this one, park the prefetch,
+  // then store. Stores come last so that waiting for the prefetched loads
+  // never waits for this block's stores as well.
+  for (int64_t k = 0; k < p.nblk; ++k) {
+    const int buf = static_cast<int>(k & 1);
+    const int64_t t0 = k * kScanBlockT;
+    if (k + 1 < p.nblk) fetch(t0 + kScanBlockT);
+
     const int64_t t = t0 + j;
     const bool tv = t < L;
-    const float uu = tv ? ld<Tx>(p.u, ubase + t * p.su[2]) : 0.f;
-    const float dl = tv ? ld<Tx>(p.delta, dbase + t * p.sdl[2]) : 0.f;
-    float zz = 0.f;
-    if (HAS_Z && WRITE_OUT) zz = tv ? ld<Tx>(p.z, zbase + t * p.sz[2]) : 0.f;
+    const float uu = s_x[buf][0][c_local][j];
+    const float dl = s_x[buf][1][c_local][j];
+    const float zz = (HAS_Z && WRITE_OUT) ? s_x[buf][2][c_local][j] : 0.f;
     const int nvalid = static_cast<int>(L - t0 < kScanBlockT ? L - t0 : kScanBlockT);
 
-    float Bv[kScanBlockT][SPL], Cv[kScanBlockT][SPL];
+    float Bv[SPL][kScanBlockT], Cv[SPL][kScanBlockT];
 #pragma unroll
-    for (int i = 0; i < kScanBlockT; ++i) {
-#pragma unroll
-      for (int s = 0; s < SPL; ++s) {
-        const int n = j + 16 * s;
-        const bool ok = i < nvalid && n < N;
-        Bv[i][s] = ok ? Bbase[(t0 + i) * p.sB[2] + n] : 0.f;
-        Cv[i][s] = (WRITE_OUT && ok) ? Cbase[(t0 + i) * p.sC[2] + n] : 0.f;
-      }
+    for (int s = 0; s < SPL; ++s) {
+      read_bc_row(s_B[buf], j + 16 * s, Bv[s]);
+      if (WRITE_OUT) read_bc_row(s_C[buf], j + 16 * s, Cv[s]);
     }
 
     float dt = dl + bias;
@@ -79,8 +141,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_fwd_kernel(const ScanParams
 #pragma unroll
       for (int s = 0; s < SPL; ++s) {
         const float a = fast_exp2(dti * A2[s]);
-        h[s] = fmaf(a, h[s], dtui * Bv[i][s]);
-        if (WRITE_OUT) acc = fmaf(h[s], Cv[i][s], acc);
+        h[s] = fmaf(a, h[s], dtui * Bv[s][i]);
+        if (WRITE_OUT) acc = fmaf(h[s], Cv[s][i], acc);
       }
       pacc[i] = acc;
     };
@@ -93,14 +155,25 @@ __global__ void __launch_bounds__(kScanThreads) scan_fwd_kernel(const ScanParams
       });
     }
 
+    float y = 0.f, yg = 0.f;
     if (WRITE_OUT) {
-      float y = row_reduce_scatter16(pacc, j);
-      if (tv && rc.active) {
-        if (p.D != nullptr) y = fmaf(Dd, uu, y);
-        if (HAS_Z) y *= zz * sigmoid(zz);
-        st<Tx>(p.out, row * L + t, y);
-      }
+      y = row_reduce_scatter16(pacc, j);
+      if (p.D != nullptr) y = fmaf(Dd, uu, y);
+      yg = HAS_Z ? y * (zz * sigmoid(zz)) : y;
     }
+
+    if (k + 1 < p.nblk) park(buf ^ 1);
+
+    if (WRITE_OUT && tv && rc.active) {
+      if (p.ysave != nullptr) st<Tx>(p.ysave, row * L + t, y);
+      st<Tx>(p.out, row * L + t, yg);
+    }
+    if (ck != nullptr && rc.active && k + 1 < p.nblk) {
+#pragma unroll
+      for (int s = 0; s < SPL; ++s)
+        if (j + 16 * s < N) ck[(k + 1) * N + j + 16 * s] = h[s];
+    }
+    __syncthreads();
   }
   if (p.last_state != nullptr && rc.active) {
 #pragma unroll
@@ -113,7 +186,7 @@ template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT>
 static hipError_t launch_fwd(const ScanParams& p, hipStream_t stream) {
   const int64_t blocks = p.batch * p.ngroups * p.nblk_c;
   hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, WRITE_OUT>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kScanThreads), 0, stream, p);
+                     dim3(64 * kFwdWaves), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -131,8 +204,11 @@ static hipError_t dispatch_fwd_spl(const ScanParams& p, bool write_out, hipStrea
   return dispatch_fwd_flags<Tx, 4>(p, write_out, stream);
 }
 
-// Launches the forward kernel. write_out = false computes states only
-// (checkpoints and/or last_state), skipping C, z and the outputs.
+int scan_fwd_waves() { return kFwdWaves; }
+
+// Launches the forward kernel (p.nblk_c must be computed for scan_fwd_waves()).
+// write_out = false computes states only (checkpoints and/or last_state),
+// skipping C, z and the outputs.
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream) {
   switch (dtype) {
     case MCPU_F32: return dispatch_fwd_spl<float>(p, write_out, stream);

@@ -35,6 +35,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
 _S3 = ctypes.c_int64 * 3
+_S4 = ctypes.c_int64 * 4
 _S2 = ctypes.c_int64 * 2
 
 
@@ -44,9 +45,9 @@ class ScanArgs(ctypes.Structure):
         ("delta_bias", _P),
         ("batch", _I64), ("dim", _I64), ("seqlen", _I64), ("dstate", _I64), ("ngroups", _I64),
         ("delta_softplus", _I32), ("dtype", _I32),
-        ("u_stride", _S3), ("delta_stride", _S3), ("z_stride", _S3), ("B_stride", _S3),
-        ("C_stride", _S3),
-        ("out", _P), ("last_state", _P), ("ckpt", _P),
+        ("u_stride", _S3), ("delta_stride", _S3), ("z_stride", _S3), ("B_stride", _S4),
+        ("C_stride", _S4),
+        ("out", _P), ("last_state", _P), ("ckpt", _P), ("ysave", _P),
         ("dout", _P), ("dout_stride", _S3), ("dlast_state", _P),
         ("du", _P), ("ddelta", _P), ("dz", _P), ("dA", _P), ("dB", _P), ("dC", _P), ("dD", _P),
         ("ddelta_bias", _P),

@@ -6,8 +6,8 @@ the same public function, the same custom-op names and schemas
 autograd wiring and the same exceptions. What changes is the device (ROCm GPU
 tensors instead of CPU tensors) and what the ops accept: besides the
 reference's contiguous float32 inputs they take bfloat16/float16 u/delta/z and
-strided views (unit stride along dstate for B/C), so Hugging Face's
-transposed projections reach the kernel without copies.
+strided views (B/C in the reference's kernel layout or transposed), so
+Hugging Face's transposed projections reach the kernel without copies.
 """
 
 from typing import Optional
@@ -40,8 +40,6 @@ def _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=()):
     for X in (B, C):
         if X.dim() != 4 or X.shape[0] != batch or X.shape[2] != seqlen or X.shape[3] != dstate:
             raise ValueError(f"{name} expects B and C of shape (batch, ngroups, seqlen, dstate)")
-        if X.stride(3) != 1 and dstate > 1:
-            raise ValueError(f"{name} expects B and C with unit stride along dstate")
     if B.shape[1] != C.shape[1] or dim % B.shape[1] != 0:
         raise ValueError(f"{name}: dim ({dim}) must be divisible by ngroups ({B.shape[1]})")
     for t in (D, delta_bias):
@@ -64,8 +62,8 @@ def _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
     a.u_stride = _C.strides3(u)
     a.delta_stride = _C.strides3(delta)
     a.z_stride = _C.strides3(z)
-    a.B_stride = (B.stride(0), B.stride(1), B.stride(2))
-    a.C_stride = (C.stride(0), C.stride(1), C.stride(2))
+    a.B_stride = tuple(B.stride())
+    a.C_stride = tuple(C.stride())
     return a
 
 
@@ -99,8 +97,8 @@ def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
 
 
 def _scan_bwd_impl(name, u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state,
-                   ckpt=None):
-    _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=(dout, dlast_state, ckpt))
+                   ckpt=None, ysave=None):
+    _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=(dout, dlast_state, ckpt, ysave))
     if dout.shape != u.shape or dout.dtype != u.dtype:
         raise ValueError(f"{name} expects dout shaped and typed like u")
     batch, dim, seqlen = u.shape
@@ -112,6 +110,11 @@ def _scan_bwd_impl(name, u, delta, A, B, C, D, z, delta_bias, delta_softplus, do
     if ckpt is not None and (ckpt.dtype != torch.float32 or not ckpt.is_contiguous()
                              or ckpt.shape != _ckpt_shape(u, A)):
         raise ValueError(f"{name} expects the float32 checkpoints written by selective_scan_fwd_ckpt")
+    if ysave is not None and ysave.numel() == 0:
+        ysave = None
+    if ysave is not None and (ysave.shape != u.shape or ysave.dtype != u.dtype
+                              or not ysave.is_contiguous() or z is None):
+        raise ValueError(f"{name} expects the y written by selective_scan_fwd_ckpt")
     du = u.new_empty(u.shape)
     ddelta = delta.new_empty(delta.shape)
     dA = A.new_empty(A.shape)
@@ -124,6 +127,7 @@ def _scan_bwd_impl(name, u, delta, A, B, C, D, z, delta_bias, delta_softplus, do
     a.dout, a.dout_stride = dout.data_ptr(), _C.strides3(dout)
     a.dlast_state = _C.ptr(dlast_state)
     a.ckpt = _C.ptr(ckpt)
+    a.ysave = _C.ptr(ysave)
     a.du, a.ddelta, a.dA, a.dB, a.dC = (du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(),
                                         dB.data_ptr(), dC.data_ptr())
     a.dD, a.ddelta_bias = dD.data_ptr(), ddelta_bias.data_ptr()
@@ -177,6 +181,7 @@ def _setup_context(ctx, inputs, output):
     u, delta, A, B, C, D, z, delta_bias, delta_softplus = inputs
     ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias)
     ctx.delta_softplus = delta_softplus
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, grad_out, grad_last_state):
@@ -201,8 +206,9 @@ torch.library.register_autograd(
 
 
 # Training path: the forward also returns the scan state at the start of every
-# 16-step block, and the backward restarts from those checkpoints instead of
-# recomputing the states from the inputs. Same arithmetic as the pair above.
+# 16-step block and, when z is given, y before the z gate; the backward
+# restarts from those checkpoints and reads y instead of recomputing the
+# states and y from the inputs. Same arithmetic as the pair above.
 
 _BLOCK_T = 16
 
@@ -223,26 +229,30 @@ def _selective_scan_fwd_ckpt(
     z: Optional[torch.Tensor],
     delta_bias: Optional[torch.Tensor],
     delta_softplus: bool,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """selective_scan_fwd that also returns the float32 block checkpoints
-    (batch, dim, ceil(seqlen / 16), dstate) for selective_scan_bwd_ckpt."""
+    (batch, dim, ceil(seqlen / 16), dstate) and y before the z gate (u's
+    dtype and shape; empty when z is None) for selective_scan_bwd_ckpt."""
     name = "mamba_cpu::selective_scan_fwd_ckpt"
     _validate(name, u, delta, A, B, C, D, z, delta_bias)
     batch, dim, _ = u.shape
     out = u.new_empty(u.shape)
     last_state = u.new_empty(batch, dim, A.shape[1], dtype=torch.float32)
     ckpt = u.new_empty(_ckpt_shape(u, A), dtype=torch.float32)
+    ysave = u.new_empty(u.shape) if z is not None else u.new_empty(0)
     a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
     a.out, a.last_state, a.ckpt = out.data_ptr(), last_state.data_ptr(), ckpt.data_ptr()
+    a.ysave = ysave.data_ptr() if z is not None else 0
     with _C.device_of(u):
         _C.call(_C.lib.mcpu_selective_scan_fwd, a, name, _C.stream_of(u))
-    return out, last_state, ckpt
+    return out, last_state, ckpt, ysave
 
 
 @_selective_scan_fwd_ckpt.register_fake
 def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
     return (u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32),
-            u.new_empty(_ckpt_shape(u, A), dtype=torch.float32))
+            u.new_empty(_ckpt_shape(u, A), dtype=torch.float32),
+            u.new_empty(u.shape) if z is not None else u.new_empty(0))
 
 
 @torch.library.custom_op("mamba_cpu::selective_scan_bwd_ckpt", mutates_args=(), device_types="cuda")
@@ -259,32 +269,35 @@ def _selective_scan_bwd_ckpt(
     dout: torch.Tensor,
     dlast_state: Optional[torch.Tensor],
     ckpt: torch.Tensor,
+    ysave: torch.Tensor,
 ) -> tuple[
     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
 ]:
-    """selective_scan_bwd restarting from the forward's block checkpoints."""
+    """selective_scan_bwd restarting from the forward's block checkpoints and
+    saved y (pass an empty ysave to recompute y)."""
     return _scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", u, delta, A, B, C, D, z, delta_bias,
-                          delta_softplus, dout, dlast_state, ckpt)
+                          delta_softplus, dout, dlast_state, ckpt, ysave)
 
 
 @_selective_scan_bwd_ckpt.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt):
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt, ysave):
     return _bwd_fake(u, delta, A, B, C, z)
 
 
 def _setup_context_ckpt(ctx, inputs, output):
     u, delta, A, B, C, D, z, delta_bias, delta_softplus = inputs
-    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[2])
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[2], output[3])
     ctx.delta_softplus = delta_softplus
+    ctx.set_materialize_grads(False)
 
 
-def _backward_ckpt(ctx, grad_out, grad_last_state, grad_ckpt):
-    u, delta, A, B, C, D, z, delta_bias, ckpt = ctx.saved_tensors
+def _backward_ckpt(ctx, grad_out, grad_last_state, grad_ckpt, grad_ysave):
+    u, delta, A, B, C, D, z, delta_bias, ckpt, ysave = ctx.saved_tensors
     dout = torch.zeros_like(u) if grad_out is None else grad_out.to(u.dtype)
     dlast = None if grad_last_state is None else grad_last_state.float().contiguous()
     du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(
-        u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt
+        u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt, ysave
     )
     return (
         du, ddelta, dA, dB, dC,
@@ -305,12 +318,12 @@ def _as_f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 
 
 def _as_kernel_bc(X: torch.Tensor) -> torch.Tensor:
-    """(b, n, l) or (b, g, n, l) -> float32 (b, g, l, n) view, copied only when
-    the dstate stride is not 1 (the reference always copies, :131-135)."""
+    """(b, n, l) or (b, g, n, l) -> float32 (b, g, l, n) view. The kernels take
+    any strides, so this never copies float32 input (the reference makes a
+    contiguous copy, :131-135)."""
     if X.dim() == 3:
         X = X.unsqueeze(1)
-    X = X.float().transpose(-1, -2)
-    return X if (X.stride(-1) == 1 or X.shape[-1] == 1) else X.contiguous()
+    return X.float().transpose(-1, -2)
 
 
 def _as_x(t: Optional[torch.Tensor], dtype) -> Optional[torch.Tensor]:
@@ -365,7 +378,7 @@ def selective_scan_fn(
     needs_grad = torch.is_grad_enabled() and any(
         isinstance(t, torch.Tensor) and t.requires_grad for t in args)
     if needs_grad:
-        out, last_state, _ = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
+        out, last_state, _, _ = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
     else:
         out, last_state = torch.ops.mamba_cpu.selective_scan_fwd(*args)
     out = out.to(u.dtype)

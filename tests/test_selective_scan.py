@@ -280,26 +280,30 @@ def test_opcheck_ckpt_pair():
         inp["D"], inp["z"], inp["delta_bias"], True,
     )
     torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_fwd_ckpt.default, args)
-    _, _, ckpt = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*[a.detach() if torch.is_tensor(a) else a
-                                                                for a in args])
+    _, _, ckpt, ysave = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(
+        *[a.detach() if torch.is_tensor(a) else a for a in args])
     bargs = tuple(a.detach() if torch.is_tensor(a) else a for a in args) + (
-        torch.randn(2, 4, 40, device=DEV), torch.randn(2, 4, 4, device=DEV), ckpt)
+        torch.randn(2, 4, 40, device=DEV), torch.randn(2, 4, 4, device=DEV), ckpt, ysave)
     torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_bwd_ckpt.default, bargs)
 
 
 def test_ckpt_and_recompute_backward_agree():
     """The training path (forward checkpoints) and the reference-schema
-    backward (recomputed states) give bit-identical gradients."""
+    backward (recomputed states) agree: bit-identical without the saved y,
+    within float32 rounding with it."""
     inp = make_inputs(2, 32, 77, 16, None, True, True, True, torch.float32)
     Bk = inp["B"][:, None].transpose(-1, -2).contiguous()
     Ck = inp["C"][:, None].transpose(-1, -2).contiguous()
     args = (inp["u"], inp["delta"], inp["A"], Bk, Ck, inp["D"], inp["z"], inp["delta_bias"], True)
-    out, last, ckpt = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
+    out, last, ckpt, ysave = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
     out2, last2 = torch.ops.mamba_cpu.selective_scan_fwd(*args)
     assert torch.equal(out, out2) and torch.equal(last, last2)
     dout = torch.randn_like(out)
     dlast = torch.randn_like(last)
-    g1 = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt)
+    g1 = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave)
     g2 = torch.ops.mamba_cpu.selective_scan_bwd(*args, dout, dlast)
-    for a, b in zip(g1, g2):
-        assert torch.equal(a, b)
+    g3 = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave.new_empty(0))
+    # y read back vs recomputed differ by one rounding of y; everything else is identical
+    for a, b, c in zip(g1, g2, g3):
+        assert torch.equal(b, c)
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
