@@ -8,13 +8,19 @@ The headline value is algorithmic bytes per step (every input read once, every
 output written once) divided by the measured step time, in GB/s.
 
 Also reported, on one JSON line:
-  roofline      the backward launch sequence (dominant), timed with HIP events
-                on the op's stream over the timed region, against 8 TB/s HBM;
+  roofline      the backward op (the dominant launch: scan_bwd_kernel and its
+                reduce kernels) called back to back, timed with HIP events on
+                the stream it launches on, against 8 TB/s HBM; `traffic` is the
+                HBM bytes per launch measured with rocprofv3 counters (read
+                from profiles/ when present);
   cpu_baseline  the reference's own CPU kernels (oracle/_ref, built from the
                 reference sources) on the same workload on this host's cores;
-  extra         forward-only time of the same workload, and Mamba-130M
-                (random init, 24 layers, d_model 768) prefill tokens/s for
-                4 x 1024 tokens through the patched Hugging Face model.
+  extra         forward-only time of the same workload; Mamba-130M (random
+                init) prefill 4 x 1024 tokens/s, 128-step greedy decode and a
+                4 x 256 training step through the patched Hugging Face model;
+                and every other workload of the op set (forward-only scan,
+                long-sequence bf16 scan, conv1d fp32/bf16, conv update, state
+                update), each with time, algorithmic bytes and HBM fraction.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -63,43 +69,191 @@ def make_inputs(torch, dev):
     return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, delta_bias=delta_bias), gout
 
 
-def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes):
-    """The reference's CPU kernels (csrc/selective_scan.cpp, built from source
-    into oracle/_ref) on the same workload, warm-up 1 + timed iterations as in
-    the reference's benchmarks/bench_selective_scan.py:16-22."""
+def _cpu_threads():
+    return int(os.environ.get("MCPU_BENCH_CPU_THREADS", min(os.cpu_count() or 1, 16)))
+
+
+def cpu_scan_ms(inputs, gout, softplus, fwd_only=False, iters=3):
+    """Milliseconds per call of the reference's CPU kernels
+    (csrc/selective_scan.cpp, built from source into oracle/_ref) on the same
+    inputs: forward, or forward + backward. Warm-up 1, then `iters` timed
+    calls, as the reference's benchmarks/bench_selective_scan.py:16-22 does."""
     from oracle import ref as R
 
     if not R.available():
         return None
-    threads = int(os.environ.get("MCPU_BENCH_CPU_THREADS", min(os.cpu_count() or 1, 16)))
-    a = {k: v.detach().float().cpu().numpy() for k, v in inputs.items()}
+    threads = _cpu_threads()
+    a = {k: None if v is None else v.detach().float().cpu().numpy() for k, v in inputs.items()}
     Bk, Ck = R.kernel_bc(a["B"]), R.kernel_bc(a["C"])
-    dout = gout.cpu().numpy()
+    dout = None if gout is None else gout.float().cpu().numpy()
 
     def run():
-        R.scan_fwd(a["u"], a["delta"], a["A"], Bk, Ck, a["D"], a["z"], a["delta_bias"], True, threads)
-        R.scan_bwd(a["u"], a["delta"], a["A"], Bk, Ck, a["D"], a["z"], a["delta_bias"], True, dout, None,
-                   threads)
+        R.scan_fwd(a["u"], a["delta"], a["A"], Bk, Ck, a.get("D"), a.get("z"), a.get("delta_bias"),
+                   softplus, threads)
+        if not fwd_only:
+            R.scan_bwd(a["u"], a["delta"], a["A"], Bk, Ck, a.get("D"), a.get("z"), a.get("delta_bias"),
+                       softplus, dout, None, threads)
 
     run()
-    iters = 3
     t0 = time.perf_counter()
     for _ in range(iters):
         run()
-    sec = (time.perf_counter() - t0) / iters
+    return round((time.perf_counter() - t0) / iters * 1e3, 3)
+
+
+def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes):
+    """The reference's CPU kernels on the full training-step workload."""
+    from oracle import ref as R
+
+    iters = 3
+    ms = cpu_scan_ms(inputs, gout, True, iters=iters)
+    if ms is None:
+        return None
     return {
-        "value": round((fwd_bytes + bwd_bytes) / sec / 1e9, 3),
+        "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 3),
         "unit": "GB/s",
-        "cores": threads,
+        "cores": _cpu_threads(),
         "kind": "reference",
         "sample": f"the full workload (batch {B_}, dim {D_}, seqlen {L_}, dstate {N_}, fp32, fwd+bwd), "
                   f"1 warm-up + {iters} timed iterations, {R.cpu_isa()} kernels; "
-                  f"{sec * 1e3:.1f} ms per fwd+bwd",
+                  f"{ms:.1f} ms per fwd+bwd",
     }
 
 
-def prefill_tokens_per_s(torch, dev, iters=3):
-    """Random-init Mamba-130M architecture through the patched HF model, fp32."""
+def _events_ms(torch, stream, fn, iters):
+    """Average GPU time per call of fn() over iters back-to-back calls, from
+    HIP events recorded on the stream the ops launch on."""
+    fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def _rate(nbytes, ms):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": int(nbytes)}
+
+
+def other_configs(torch, dev, stream, cpu):
+    """Every other workload of the op set, each timed on its own: absolute
+    time, algorithmic bytes (each input read once, each output written once)
+    and the fraction of the 8 TB/s HBM peak they imply."""
+    import mamba_cpu
+    from mamba_cpu import causal_conv1d_fn, causal_conv1d_update, selective_scan_fn
+
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    # Forward-only scan, fp32: batch 1, dim 1536, seqlen 2048, dstate 16, softplus, no z/bias.
+    b, d, l, n = 1, 1536, 2048, 16
+    u = torch.randn(b, d, l, generator=g, device=dev)
+    delta = torch.randn(b, d, l, generator=g, device=dev)
+    A = -torch.rand(d, n, generator=g, device=dev)
+    Bm = torch.randn(b, n, l, generator=g, device=dev)
+    Cm = torch.randn(b, n, l, generator=g, device=dev)
+    D = torch.randn(d, generator=g, device=dev)
+    nbytes = 3 * b * d * l * 4 + 2 * b * n * l * 4 + 4 * (d * n + d)
+    ms = _events_ms(torch, stream, lambda: selective_scan_fn(u, delta, A, Bm, Cm, D, delta_softplus=True), 50)
+    r = _rate(nbytes, ms)
+    r["workload"] = "selective_scan_fn forward, fp32, batch 1, dim 1536, seqlen 2048, dstate 16, softplus"
+    if cpu:
+        r["cpu_reference_ms"] = cpu_scan_ms({"u": u, "delta": delta, "A": A, "B": Bm, "C": Cm, "D": D},
+                                            None, True, fwd_only=True)
+    res["scan_fwd_b1_d1536_l2048"] = r
+    del u, delta, Bm, Cm
+
+    # Long sequence, bf16 u/delta/B/C, fp32 A/D: batch 1, dim 5120, seqlen 16384, fwd+bwd.
+    b, d, l, n = 1, 5120, 16384, 16
+    bf = torch.bfloat16
+    leaves = dict(u=torch.randn(b, d, l, generator=g, device=dev).to(bf),
+                  delta=torch.randn(b, d, l, generator=g, device=dev).to(bf),
+                  A=-torch.exp(torch.rand(d, n, generator=g, device=dev) * math.log(16)),
+                  B=torch.randn(b, n, l, generator=g, device=dev).to(bf),
+                  C=torch.randn(b, n, l, generator=g, device=dev).to(bf),
+                  D=torch.randn(d, generator=g, device=dev))
+    leaves = {k: v.requires_grad_() for k, v in leaves.items()}
+    gout = torch.randn(b, d, l, generator=g, device=dev).to(bf)
+
+    def long_step():
+        out = selective_scan_fn(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                leaves["D"], delta_softplus=True)
+        return torch.autograd.grad(out, list(leaves.values()), gout)
+
+    x, bc, prm = b * d * l * 2, b * n * l * 2, 4 * (d * n + d)
+    nbytes = (2 * x + 2 * bc + prm + x) + (3 * x + 2 * bc + prm + 2 * x + 2 * bc + prm)
+    ms = _events_ms(torch, stream, long_step, 5)
+    r = _rate(nbytes, ms)
+    r["workload"] = ("selective_scan_fn forward+backward, bf16 u/delta/B/C, fp32 A/D, batch 1, "
+                     "dim 5120, seqlen 16384, dstate 16, softplus")
+    res["scan_fwdbwd_b1_d5120_l16384_bf16"] = r
+    del leaves, gout
+
+    # Causal conv1d forward+backward: batch 8, dim 3072, seqlen 2048, width 4, silu.
+    b, d, l, w = 8, 3072, 2048, 4
+    for dt, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        x = torch.randn(b, d, l, generator=g, device=dev).to(dt).requires_grad_()
+        wt = (torch.randn(d, w, generator=g, device=dev) * 0.5).requires_grad_()
+        bias = (torch.randn(d, generator=g, device=dev) * 0.1 ** 0.5).requires_grad_()
+        go = torch.randn(b, d, l, generator=g, device=dev).to(dt)
+
+        def conv_step():
+            out = causal_conv1d_fn(x, wt, bias, activation="silu")
+            return torch.autograd.grad(out, [x, wt, bias], go)
+
+        e = x.element_size()
+        nbytes = 5 * b * d * l * e + 4 * 3 * (d * w + d)
+        ms = _events_ms(torch, stream, conv_step, 20)
+        r = _rate(nbytes, ms)
+        r["workload"] = f"causal_conv1d_fn forward+backward, {tag}, batch 8, dim 3072, seqlen 2048, width 4, silu"
+        res[f"conv_fwdbwd_b8_d3072_l2048_{tag}"] = r
+        del x, go
+
+    # Decode-time conv update: state (64, 3072, 3), 256 single-token steps.
+    b, d, w = 64, 3072, 4
+    state = torch.randn(b, d, w - 1, generator=g, device=dev)
+    xs = torch.randn(256, b, d, generator=g, device=dev)
+    wt = torch.randn(d, w, generator=g, device=dev) * 0.5
+    bias = torch.randn(d, generator=g, device=dev) * 0.1 ** 0.5
+
+    def upd():
+        for i in range(256):
+            causal_conv1d_update(xs[i], state, wt, bias, activation="silu")
+
+    ms = _events_ms(torch, stream, upd, 3) / 256
+    nbytes = (b * d + 2 * b * d * (w - 1) + b * d) * 4 + 4 * (d * w + d)
+    r = _rate(nbytes, ms)
+    r["workload"] = "causal_conv1d_update, fp32, state (64, 3072, 3), x (64, 3072), silu; per step of 256"
+    res["conv_update_b64_d3072"] = r
+
+    # Selective state update, Mamba-130M layer shape: state (4, 1536, 16).
+    b, d, n = 4, 1536, 16
+    st = torch.randn(b, d, n, generator=g, device=dev)
+    xv, dtv, zv = (torch.randn(b, d, generator=g, device=dev) for _ in range(3))
+    A = -torch.exp(torch.rand(d, n, generator=g, device=dev))
+    Bv, Cv = torch.randn(b, n, generator=g, device=dev), torch.randn(b, n, generator=g, device=dev)
+    D = torch.randn(d, generator=g, device=dev)
+    dtb = torch.randn(d, generator=g, device=dev)
+    ms = _events_ms(torch, stream, lambda: mamba_cpu.selective_state_update(
+        st, xv, dtv, A, Bv, Cv, D, zv, dtb, dt_softplus=True), 200)
+    nbytes = 2 * b * d * n * 4 + 4 * b * d * 4 + 4 * (d * n + 2 * d) + 2 * b * n * 4
+    r = _rate(nbytes, ms)
+    r["workload"] = "selective_state_update, fp32, state (4, 1536, 16), z + D + dt_bias, softplus"
+    res["state_update_b4_d1536"] = r
+    return res
+
+
+def mamba130m(torch, dev, iters=3):
+    """Random-init Mamba-1 130M architecture (24 layers, d_model 768, d_inner
+    1536, dstate 16, dt_rank 48, conv width 4, vocab 50280), fp32, through the
+    patched Hugging Face model: prefill 4 x 1024 tokens, 128 greedy decode
+    steps from a 4 x 16 prompt, and one training step (forward + backward) at
+    4 x 256 with labels = ids."""
     import transformers
 
     import mamba_cpu.hf
@@ -109,6 +263,7 @@ def prefill_tokens_per_s(torch, dev, iters=3):
     cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
                                    conv_kernel=4, vocab_size=50280)
     model = transformers.MambaForCausalLM(cfg).to(dev).eval()
+    res = {}
     ids = torch.randint(0, 50280, (4, 1024), device=dev)
     with torch.no_grad():
         model(ids)
@@ -117,10 +272,55 @@ def prefill_tokens_per_s(torch, dev, iters=3):
         for _ in range(iters):
             model(ids)
         torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / iters
+        sec = (time.perf_counter() - t0) / iters
+    res["prefill_tokens_per_s"] = round(4 * 1024 / sec, 1)
+    res["prefill_ms"] = round(sec * 1e3, 2)
+
+    prompt = ids[:, :16]
+    gen = dict(max_new_tokens=128, min_new_tokens=128, do_sample=False, pad_token_id=0)
+    with torch.no_grad():
+        model.generate(prompt, **dict(gen, max_new_tokens=4, min_new_tokens=4))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model.generate(prompt, **gen)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+    res["decode_tokens_per_s"] = round(4 * (out.shape[1] - 16) / sec, 1)
+    res["decode_ms_per_step"] = round(sec / (out.shape[1] - 16) * 1e3, 3)
+
+    model.train()
+    tids = ids[:, :256]
+    model(tids, labels=tids).loss.backward()
+    model.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        model(tids, labels=tids).loss.backward()
+        model.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    res["train_step_ms_4x256"] = round((time.perf_counter() - t0) / iters * 1e3, 2)
     del model
     torch.cuda.empty_cache()
-    return 4 * 1024 / sec, sec
+    return res
+
+
+def counter_pass(torch, dev, inputs, gout):
+    """A short fixed sequence for hardware-counter runs (rocprofv3 --pmc): the
+    training-step forward and backward ops three times, each followed by a
+    copy of 256 MiB (64 Mi floats read, 64 Mi floats written), whose counter
+    readings calibrate the byte counters against a known traffic."""
+    ops = torch.ops.mamba_cpu
+    kargs = (inputs["u"], inputs["delta"], inputs["A"], inputs["B"].transpose(-1, -2),
+             inputs["C"].transpose(-1, -2), inputs["D"], inputs["z"], inputs["delta_bias"], True)
+    src = torch.randn(64 << 20, device=dev)
+    dst = torch.empty_like(src)
+    with torch.no_grad():
+        for _ in range(3):
+            _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*kargs)
+            ops.selective_scan_bwd_ckpt(*kargs, gout, None, ckpt, ysave)
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print("counter pass done", flush=True)
 
 
 def main():
@@ -130,6 +330,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="only run 3 x (forward op, backward op, 256 MiB copy) for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
@@ -144,6 +347,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     inputs, gout = make_inputs(torch, dev)
+    if args.counter_pass:
+        counter_pass(torch, dev, inputs, gout)
+        return
     leaves = {k: v.clone().requires_grad_() for k, v in inputs.items()}
     order = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias"]
     fwd_bytes, bwd_bytes = algorithmic_bytes(B_, D_, L_, N_, G_)
@@ -189,7 +395,19 @@ def main():
         torch.cuda.synchronize()
         fwd_only_ms = e0.elapsed_time(e1) / args.steps
 
-    bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    # Dominant launch: the backward op alone (scan_bwd_kernel followed by its
+    # dB/dC/dA/dD/ddelta_bias reduce kernels), called back to back on the same
+    # stream with the forward's saved state, timed with HIP events.
+    ops = torch.ops.mamba_cpu
+    kargs = (inputs["u"], inputs["delta"], inputs["A"], inputs["B"].transpose(-1, -2),
+             inputs["C"].transpose(-1, -2), inputs["D"], inputs["z"], inputs["delta_bias"], True)
+    with torch.no_grad():
+        _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*kargs)
+        bwd_launch_ms = _events_ms(torch, stream, lambda: ops.selective_scan_bwd_ckpt(
+            *kargs, gout, None, ckpt, ysave), args.steps)
+        fwd_launch_ms = _events_ms(torch, stream, lambda: ops.selective_scan_fwd_ckpt(*kargs), args.steps)
+    del ckpt, ysave
+    bwd_gbs = bwd_bytes / (bwd_launch_ms * 1e-3) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "scan_bwd_b8_d1536_l1024_n16_traffic.json")
     if os.path.exists(tpath):
@@ -199,6 +417,8 @@ def main():
     extra = {
         "fwd_ms_in_step": round(fwd_ms, 4),
         "bwd_ms_in_step": round(bwd_ms, 4),
+        "bwd_launch_ms": round(bwd_launch_ms, 4),
+        "fwd_ckpt_launch_ms": round(fwd_launch_ms, 4),
         "fwd_only_ms": round(fwd_only_ms, 4),
         "fwd_only_GBps": round(fwd_bytes / (fwd_only_ms * 1e-3) / 1e9, 1),
         "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes},
@@ -207,11 +427,12 @@ def main():
     }
     if not args.no_prefill:
         try:
-            tps, sec = prefill_tokens_per_s(torch, dev)
-            extra["mamba130m_prefill_tokens_per_s"] = round(tps, 1)
-            extra["mamba130m_prefill_ms"] = round(sec * 1e3, 2)
+            extra["mamba130m"] = mamba130m(torch, dev)
+            extra["mamba130m_prefill_tokens_per_s"] = extra["mamba130m"]["prefill_tokens_per_s"]
         except Exception as exc:  # reported, not hidden
-            extra["mamba130m_prefill_error"] = repr(exc)
+            extra["mamba130m_error"] = repr(exc)
+    if not args.no_configs:
+        extra["workloads"] = other_configs(torch, dev, stream, not args.no_cpu_baseline)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes)
 
@@ -235,7 +456,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "selective-scan backward launch (scan_bwd_kernel + its dB/dC/dA/dD/ddelta_bias reduce kernels)",
+            "kernel": "selective-scan backward launch: scan_bwd_kernel + its dB/dC/dA/dD/ddelta_bias "
+                      "reduce kernels, algorithmic bytes of the backward / average launch time",
             "achieved": round(bwd_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

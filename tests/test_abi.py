@@ -1,0 +1,214 @@
+"""The C ABI of libmamba_hip.so, checked on the CPU (no kernel is launched).
+
+- every function include/mamba_hip.h declares is exported by the library;
+- the ctypes argument blocks have the library's sizes and field offsets;
+- argument checks reject bad calls with the documented codes and messages
+  before anything touches a device, and the Python layer maps them to the
+  reference's exception types (ValueError / NotImplementedError);
+- the Python API refuses CPU tensors instead of falling back to a CPU path.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mamba_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mcpu_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for want in ("mcpu_selective_scan_fwd", "mcpu_selective_scan_bwd",
+                 "mcpu_selective_scan_bwd_workspace_size", "mcpu_selective_scan_ckpt_size",
+                 "mcpu_causal_conv1d_fwd", "mcpu_causal_conv1d_bwd",
+                 "mcpu_causal_conv1d_bwd_workspace_size", "mcpu_causal_conv1d_update",
+                 "mcpu_selective_state_update", "mcpu_last_error", "mcpu_version",
+                 "mcpu_check_device", "mcpu_args_size"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    from mamba_cpu import _C
+
+    missing = [n for n in declared_functions() if not hasattr(_C.lib, n)]
+    assert missing == []
+
+
+def test_library_is_built_for_gfx950():
+    from mamba_cpu import _C
+
+    path = _C.LIB_PATH
+    assert os.path.exists(path)
+    blob = open(path, "rb").read()
+    assert b"gfx950" in blob
+    assert "gfx950" in _C.version()
+
+
+def test_argument_blocks_match_the_library():
+    from mamba_cpu import _C
+
+    for name, cls in (("scan", _C.ScanArgs), ("conv", _C.ConvArgs),
+                      ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs)):
+        assert _C.lib.mcpu_args_size(name.encode()) == ctypes.sizeof(cls)
+    assert _C.lib.mcpu_args_size(b"nonsense") == 0
+
+
+def _header_field_names(struct):
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        decl = re.sub(r"\[\d+\]", "", decl)
+        head, _, rest = decl.rpartition(" ")
+        names += [n.strip().lstrip("*") for n in (rest if "," not in decl else
+                                                   decl.split(None, 1)[1].replace("*", "")).split(",")]
+    return [n for n in names if n]
+
+
+@pytest.mark.parametrize("struct,cls_name", [("mcpu_scan_args", "ScanArgs"),
+                                             ("mcpu_conv_args", "ConvArgs"),
+                                             ("mcpu_conv_update_args", "ConvUpdateArgs"),
+                                             ("mcpu_state_update_args", "StateUpdateArgs")])
+def test_argument_block_fields_follow_the_header(struct, cls_name):
+    from mamba_cpu import _C
+
+    cls = getattr(_C, cls_name)
+    assert [f[0] for f in cls._fields_] == _header_field_names(struct)
+
+
+def _scan_args(**kw):
+    from mamba_cpu import _C
+
+    a = _C.ScanArgs()
+    a.u = a.delta = a.A = a.B = a.C = 16  # non-NULL placeholders: never dereferenced
+    a.batch, a.dim, a.seqlen, a.dstate, a.ngroups = 2, 8, 32, 16, 1
+    a.dtype = _C.MCPU_F32
+    a.u_stride[:] = a.delta_stride[:] = (8 * 32, 32, 1)
+    a.B_stride[:] = a.C_stride[:] = (32 * 16, 32 * 16, 16, 1)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _rc(fn, *args):
+    from mamba_cpu import _C
+
+    rc = fn(*args)
+    return rc, _C.lib.mcpu_last_error().decode()
+
+
+def test_scan_rejects_bad_arguments_before_touching_a_device():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    assert _rc(L.mcpu_selective_scan_fwd, None, None)[0] == _C.MCPU_ERR_INVALID
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(u=None)), None)
+    assert rc == _C.MCPU_ERR_INVALID and "required" in msg
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=65)), None)
+    assert rc == _C.MCPU_ERR_UNSUPPORTED and "dstate" in msg
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(ngroups=3)), None)
+    assert rc == _C.MCPU_ERR_INVALID and "ngroups" in msg
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dtype=7)), None)
+    assert rc == _C.MCPU_ERR_INVALID and "dtype" in msg
+    a = _scan_args()
+    a.u_stride[1] = -1
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None)
+    assert rc == _C.MCPU_ERR_INVALID and "stride" in msg
+    a = _scan_args()
+    a.u_stride[1] = 1 << 40  # tile offsets would not fit 32 bits
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None)
+    assert rc == _C.MCPU_ERR_UNSUPPORTED and "32-bit" in msg
+    # backward: required outputs
+    rc, msg = _rc(L.mcpu_selective_scan_bwd, ctypes.byref(_scan_args()), None, 0, None)
+    assert rc == _C.MCPU_ERR_INVALID and "du" in msg
+
+
+def test_scan_sizes():
+    from mamba_cpu import _C
+
+    a = _scan_args(seqlen=33)
+    # checkpoints: float32 state at the start of every 16-step block
+    assert _C.lib.mcpu_selective_scan_ckpt_size(ctypes.byref(a)) == 4 * 2 * 8 * 3 * 16
+    assert _C.lib.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a)) > 0
+    assert _C.lib.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(dstate=0))) == 0
+
+
+def test_scan_without_gfx950_reports_the_device():
+    """Valid arguments on a machine without a gfx950 device: a device error, no launch."""
+    from mamba_cpu import _C
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    rc, msg = _rc(_C.lib.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(out=32)), None)
+    assert rc in (_C.MCPU_ERR_DEVICE, _C.MCPU_ERR_HIP)
+    assert msg
+
+
+def test_conv_and_state_update_reject_bad_arguments():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    c = _C.ConvArgs()
+    rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
+    assert rc == _C.MCPU_ERR_INVALID and msg
+    c.x = c.weight = c.out = 16
+    c.batch, c.dim, c.seqlen, c.width = 1, 4, 8, 17
+    rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
+    assert rc in (_C.MCPU_ERR_INVALID, _C.MCPU_ERR_UNSUPPORTED) and "width" in msg
+    u = _C.ConvUpdateArgs()
+    assert _rc(L.mcpu_causal_conv1d_update, ctypes.byref(u), None)[0] == _C.MCPU_ERR_INVALID
+    s = _C.StateUpdateArgs()
+    assert _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)[0] == _C.MCPU_ERR_INVALID
+
+
+def test_status_codes_map_to_the_reference_exceptions():
+    from mamba_cpu import _C
+
+    with pytest.raises(ValueError):
+        _C.check(_C.MCPU_ERR_INVALID, "x")
+    with pytest.raises(NotImplementedError):
+        _C.check(_C.MCPU_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _C.check(_C.MCPU_ERR_HIP, "x")
+    _C.check(_C.MCPU_OK, "x")
+
+
+def test_public_api_has_no_cpu_fallback():
+    import mamba_cpu
+
+    b, d, l, n = 1, 4, 8, 4
+    u = torch.randn(b, d, l)
+    A = -torch.rand(d, n)
+    B = torch.randn(b, n, l)
+    with pytest.raises((ValueError, RuntimeError, NotImplementedError)):
+        mamba_cpu.selective_scan_fn(u, u, A, B, B)
+    with pytest.raises((ValueError, RuntimeError, NotImplementedError)):
+        mamba_cpu.causal_conv1d_fn(u, torch.randn(d, 4))
+    with pytest.raises((ValueError, RuntimeError, NotImplementedError)):
+        mamba_cpu.selective_state_update(torch.zeros(b, d, n), u[..., 0], u[..., 0], A,
+                                         B[..., 0], B[..., 0])
+
+
+def test_public_api_surface():
+    """The names the reference exports (src/mamba_cpu/__init__.py)."""
+    import mamba_cpu
+
+    for name in ("selective_scan_fn", "causal_conv1d_fn", "causal_conv1d_update",
+                 "selective_state_update", "selective_scan_ref", "causal_conv1d_ref"):
+        assert callable(getattr(mamba_cpu, name))
+    assert hasattr(torch.ops.mamba_cpu, "selective_scan_fwd")
+    assert hasattr(torch.ops.mamba_cpu, "selective_scan_bwd")
