@@ -48,8 +48,41 @@ ConvParams make_conv(const mcpu_conv_args* a) {
   return p;
 }
 
+// Launch shape of the time-contiguous fast path: 8 steps per thread; a row
+// segment is 64, 128 or 256 threads (one to four whole waves).
+void conv_vt_shape(ConvParams& p) {
+  const int64_t threads = p.seqlen / kConvVTSteps;
+  if (threads >= 256) {
+    p.tpr = 256;
+    p.nseg = (threads + 255) / 256;
+  } else {
+    p.tpr = threads <= 64 ? 64 : (threads <= 128 ? 128 : 256);
+    p.nseg = 1;
+  }
+  p.rpw = 256 / p.tpr;
+}
+
+// A (batch, dim, seqlen) operand the fast path can move in vectors: unit time
+// stride, rows starting on 4-element boundaries, an aligned base.
+bool vt_operand(const void* ptr, const int64_t (&s)[3], int dtype) {
+  const uintptr_t align = dtype == MCPU_F32 ? 16 : 8;
+  return ptr != nullptr && s[2] == 1 && s[0] % 4 == 0 && s[1] % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(ptr) % align == 0;
+}
+
+bool vt_ok(const ConvParams& p, int dtype, bool bwd) {
+  if (p.width < 2 || p.width > 5 || p.seqlen < kConvVTSteps || p.seqlen % kConvVTSteps != 0)
+    return false;
+  if (!vt_operand(p.x, p.sx, dtype)) return false;
+  if (!bwd) return vt_operand(p.out, p.sout, dtype);
+  return vt_operand(p.dout, p.sdo, dtype) && vt_operand(p.dx, p.sdx, dtype);
+}
+
 size_t conv_ws(const ConvParams& p) {
-  return align_up(sizeof(float) * p.batch * p.R * p.dim * (p.width + 1));
+  ConvParams q = p;
+  conv_vt_shape(q);
+  const int64_t parts = q.nseg > p.R ? q.nseg : p.R;
+  return align_up(sizeof(float) * p.batch * parts * p.dim * (p.width + 1));
 }
 
 }  // namespace
@@ -65,6 +98,8 @@ extern "C" int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream) {
   ConvParams p = make_conv(a);
   p.out = a->out;
   p.final_states = a->final_states;
+  p.vt = vt_ok(p, a->dtype, false);
+  if (p.vt) conv_vt_shape(p);
   return hip_status(conv_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
                     "causal_conv1d_fwd launch");
 }
@@ -96,6 +131,8 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
   p.dx = a->dx;
   p.dinit = a->dinitial_states;
   p.dw_part = static_cast<float*>(workspace);
+  p.vt = vt_ok(p, a->dtype, true);
+  if (p.vt) conv_vt_shape(p);
   if (a->batch == 0 || a->dim == 0) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (int rc = zero_f32(a->dweight, a->dim * a->width, st)) return rc;

@@ -12,10 +12,11 @@ int scan_fwd_waves();
 int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
-hipError_t scan_reduce_bc_launch(const float* part, float* out, int64_t slices, int64_t nblk_c,
-                                 int64_t per_slice, hipStream_t stream);
-hipError_t scan_reduce_batch_launch(const float* part, float* out, int64_t batch,
-                                    int64_t per_batch, hipStream_t stream);
+hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_part, float* dC,
+                              int64_t slices, int64_t nblk_c, int64_t per_slice,
+                              const float* dA_part, float* dA, int64_t nA, const float* dD_part,
+                              float* dD, const float* dbias_part, float* dbias, int64_t dim,
+                              int64_t batch, hipStream_t stream);
 
 namespace {
 
@@ -208,29 +209,13 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
   if (int rc = hip_status(scan_bwd_launch(p, a->dtype, waves, st), "selective_scan_bwd launch"))
     return rc;
-  if (w.part_bc) {
-    const int64_t slices = p.batch * p.ngroups, per = p.seqlen * p.dstate;
-    if (int rc = hip_status(scan_reduce_bc_launch(p.dB_part, a->dB, slices, p.nblk_c, per, st),
-                            "selective_scan_bwd dB reduce"))
-      return rc;
-    if (int rc = hip_status(scan_reduce_bc_launch(p.dC_part, a->dC, slices, p.nblk_c, per, st),
-                            "selective_scan_bwd dC reduce"))
-      return rc;
-  }
-  if (w.part_dA) {
-    if (int rc = hip_status(scan_reduce_batch_launch(p.dA_part, a->dA, p.batch, p.dim * p.dstate, st),
-                            "selective_scan_bwd dA reduce"))
-      return rc;
-  }
-  if (a->dD != nullptr) {
-    if (int rc = hip_status(scan_reduce_batch_launch(p.dD_part, a->dD, p.batch, p.dim, st),
-                            "selective_scan_bwd dD reduce"))
-      return rc;
-  }
-  if (a->ddelta_bias != nullptr) {
-    if (int rc = hip_status(scan_reduce_batch_launch(p.dbias_part, a->ddelta_bias, p.batch, p.dim, st),
-                            "selective_scan_bwd ddelta_bias reduce"))
-      return rc;
-  }
-  return MCPU_OK;
+  // One launch sums every partial: dB/dC over channel blocks (when there is
+  // more than one), dA/dD/ddelta_bias over the batch.
+  return hip_status(
+      scan_reduce_launch(w.part_bc ? p.dB_part : nullptr, a->dB, w.part_bc ? p.dC_part : nullptr,
+                         a->dC, p.batch * p.ngroups, p.nblk_c, p.seqlen * p.dstate,
+                         w.part_dA ? p.dA_part : nullptr, a->dA, p.dim * p.dstate,
+                         a->dD ? p.dD_part : nullptr, a->dD,
+                         a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim, p.batch, st),
+      "selective_scan_bwd reduce");
 }

@@ -237,11 +237,252 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
   }
 }
 
+// ---- Time-contiguous fast path ------------------------------------------------
+// For x, out, dout and dx with unit time stride, rows aligned to 4 elements and
+// seqlen a multiple of 8: each thread owns 8 consecutive steps of one
+// (batch, channel) row and moves them with 16-byte (fp32) or 8-byte (16-bit)
+// vector loads and stores; the W-1 inputs before its first step (and, in the
+// backward, the W-1 steps after its last) are re-read from the neighbouring
+// thread's vector, which the cache serves. A workgroup covers `rpw` rows of
+// `tpr` threads each (short rows) or one 2048-step segment of a row (long
+// rows), so a row segment never straddles a wave.
+constexpr int kConvVT = kConvVTSteps;
+
+template <typename T>
+__device__ __forceinline__ void ld4(const void* base, int64_t idx, float* v) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const T*>(base) + idx);
+    const uint32_t h[4] = {q.x & 0xffffu, q.x >> 16, q.y & 0xffffu, q.y >> 16};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (std::is_same_v<T, bf16>) v[i] = to_f32(bf16{static_cast<uint16_t>(h[i])});
+      else v[i] = to_f32(__builtin_bit_cast(f16, static_cast<uint16_t>(h[i])));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(void* base, int64_t idx, const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = __builtin_bit_cast(uint16_t, from_f32<T>(v[i]));
+    *reinterpret_cast<uint2*>(static_cast<T*>(base) + idx) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  }
+}
+
+struct ConvTile {
+  ConvRow c;      // (batch, channel) of the row
+  int64_t t0;     // first step of this thread
+  int64_t seg;    // row segment of the workgroup
+  bool active;    // the thread has steps to do
+};
+
+__device__ __forceinline__ ConvTile conv_tile(const ConvParams& p, int tid) {
+  ConvTile g;
+  const int lt = tid & (p.tpr - 1), sub = tid / p.tpr;
+  int64_t row;
+  if (p.nseg > 1) {
+    row = blockIdx.x / p.nseg;
+    g.seg = blockIdx.x % p.nseg;
+  } else {
+    row = static_cast<int64_t>(blockIdx.x) * p.rpw + sub;
+    g.seg = 0;
+  }
+  g.t0 = (g.seg * p.tpr + lt) * kConvVT;
+  const int64_t rows = p.batch * p.dim;
+  g.active = row < rows && g.t0 < p.seqlen;
+  if (row >= rows) row = rows - 1;
+  g.c.b = row / p.dim;
+  g.c.d = row % p.dim;
+  g.c.r = 0;
+  return g;
+}
+
+template <typename T, int W>
+__global__ void __launch_bounds__(256) conv_fwd_vt_kernel(const ConvParams p) {
+  const ConvTile g = conv_tile(p, threadIdx.x);
+  if (!g.active) return;
+  const ConvRow& c = g.c;
+  float w[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) w[k] = p.w[c.d * W + k];
+  const float bias = p.bias ? p.bias[c.d] : 0.f;
+  const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
+  float xv[4 + kConvVT];  // X[t0 - 4 .. t0 + 8)
+  if (g.t0 > 0) {
+    ld4<T>(p.x, xrow + g.t0 - 4, xv);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
+  }
+  ld4<T>(p.x, xrow + g.t0, xv + 4);
+  ld4<T>(p.x, xrow + g.t0 + 4, xv + 8);
+  float o[kConvVT];
+#pragma unroll
+  for (int i = 0; i < kConvVT; ++i) {
+    float acc = bias;
+#pragma unroll
+    for (int k = 0; k < W; ++k) acc = fmaf(w[k], xv[4 + i - (W - 1) + k], acc);
+    o[i] = p.silu ? acc * sigmoid(acc) : acc;
+  }
+  const int64_t orow = c.b * p.sout[0] + c.d * p.sout[1];
+  st4<T>(p.out, orow + g.t0, o);
+  st4<T>(p.out, orow + g.t0 + 4, o + 4);
+}
+
+// Sum over the 64 lanes of a wave, in a fixed order, result in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row_allreduce16(x);
+  x = swap_sum<32>(x, x);
+  return swap_sum<16>(x, x);
+}
+
+template <typename T, int W>
+__global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
+  __shared__ float s_part[4][W + 1];
+  const ConvTile g = conv_tile(p, threadIdx.x);
+  const ConvRow& c = g.c;
+  const int64_t L = p.seqlen;
+  float dwk[W + 1];  // dweight[0..W), dbias
+#pragma unroll
+  for (int k = 0; k <= W; ++k) dwk[k] = 0.f;
+  if (g.active) {
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = p.w[c.d * W + k];
+    const float bias = p.bias ? p.bias[c.d] : 0.f;
+    const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
+    const int64_t orow = c.b * p.sdo[0] + c.d * p.sdo[1];
+    const bool tail = g.t0 + kConvVT < L;  // the next 8 steps exist
+    float xv[4 + kConvVT + 4];              // X[t0 - 4 .. t0 + 12)
+    float go[kConvVT + 4];                  // dout[t0 .. t0 + 12)
+    if (g.t0 > 0) {
+      ld4<T>(p.x, xrow + g.t0 - 4, xv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
+    }
+    ld4<T>(p.x, xrow + g.t0, xv + 4);
+    ld4<T>(p.x, xrow + g.t0 + 4, xv + 8);
+    ld4<T>(p.dout, orow + g.t0, go);
+    ld4<T>(p.dout, orow + g.t0 + 4, go + 4);
+    if (tail) {
+      ld4<T>(p.x, xrow + g.t0 + 8, xv + 12);
+      ld4<T>(p.dout, orow + g.t0 + 8, go + 8);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[12 + i] = go[8 + i] = 0.f;
+    }
+    // dpre[t0 + i] for i < 8 + W - 1 (zero past the sequence end).
+    float dp[kConvVT + W - 1];
+#pragma unroll
+    for (int i = 0; i < kConvVT + W - 1; ++i) {
+      float pre = bias;
+#pragma unroll
+      for (int k = 0; k < W; ++k) pre = fmaf(w[k], xv[4 + i - (W - 1) + k], pre);
+      float v = go[i];
+      if (p.silu) {
+        const float sg = sigmoid(pre);
+        v *= sg * (1.f + pre * (1.f - sg));
+      }
+      dp[i] = (i < kConvVT || tail) ? v : 0.f;
+    }
+    float dx[kConvVT];
+    const int64_t fin0 = L - (W - 1);
+#pragma unroll
+    for (int i = 0; i < kConvVT; ++i) {
+      dwk[W] += dp[i];
+#pragma unroll
+      for (int k = 0; k < W; ++k) dwk[k] = fmaf(dp[i], xv[4 + i - (W - 1) + k], dwk[k]);
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < W; ++k) acc = fmaf(w[k], dp[i + (W - 1) - k], acc);
+      if (p.dfinal != nullptr && g.t0 + i >= fin0)
+        acc += ld<T>(p.dfinal, (c.b * p.dim + c.d) * (W - 1) + (g.t0 + i - fin0));
+      dx[i] = acc;
+    }
+    const int64_t xr = c.b * p.sdx[0] + c.d * p.sdx[1];
+    st4<T>(p.dx, xr + g.t0, dx);
+    st4<T>(p.dx, xr + g.t0 + 4, dx + 4);
+    if (g.t0 == 0 && p.dinit != nullptr) {
+      // dX[s] for s in [-(W-1), 0): the initial-state columns.
+#pragma unroll
+      for (int s = -(W - 1); s < 0; ++s) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+          if (s + (W - 1) - k >= 0) acc = fmaf(w[k], dp[s + (W - 1) - k], acc);
+        st<T>(p.dinit, (c.b * p.dim + c.d) * (W - 1) + (s + W - 1), acc);
+      }
+    }
+  }
+  // Per-segment sums of dweight/dbias: wave sums, then the segment's waves in order.
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k <= W; ++k) {
+    const float v = wave_sum(dwk[k]);
+    if ((threadIdx.x & 63) == 0) s_part[wave][k] = v;
+  }
+  __syncthreads();
+  const int wps = p.tpr / 64;  // waves per segment
+  if (threadIdx.x < p.rpw * (W + 1)) {
+    const int sg = threadIdx.x / (W + 1), k = threadIdx.x % (W + 1);
+    float acc = 0.f;
+    for (int q = 0; q < wps; ++q) acc += s_part[sg * wps + q][k];
+    const int64_t row = p.nseg > 1 ? static_cast<int64_t>(blockIdx.x) / p.nseg
+                                   : static_cast<int64_t>(blockIdx.x) * p.rpw + sg;
+    if (row < p.batch * p.dim) {
+      const int64_t b = row / p.dim, d = row % p.dim;
+      const int64_t seg = p.nseg > 1 ? blockIdx.x % p.nseg : 0;
+      p.dw_part[((b * p.nseg + seg) * p.dim + d) * (W + 1) + k] = acc;
+    }
+  }
+}
+
+template <typename T>
+static hipError_t launch_vt(const ConvParams& p, bool bwd, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>(
+      p.nseg > 1 ? p.batch * p.dim * p.nseg : (p.batch * p.dim + p.rpw - 1) / p.rpw);
+  switch (p.width) {
+#define MCPU_CONV_VT(WW)                                                                         \
+  case WW:                                                                                       \
+    if (bwd) hipLaunchKernelGGL((conv_bwd_vt_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);    \
+    else hipLaunchKernelGGL((conv_fwd_vt_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);        \
+    break;
+    MCPU_CONV_VT(2)
+    MCPU_CONV_VT(3)
+    MCPU_CONV_VT(4)
+    MCPU_CONV_VT(5)
+#undef MCPU_CONV_VT
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+static hipError_t launch_vt_dtype(const ConvParams& p, int dtype, bool bwd, hipStream_t st) {
+  switch (dtype) {
+    case MCPU_F32: return launch_vt<float>(p, bwd, st);
+    case MCPU_BF16: return launch_vt<bf16>(p, bwd, st);
+    default: return launch_vt<f16>(p, bwd, st);
+  }
+}
+
 static unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
-  if (n > 0) {
+  if (n > 0 && p.vt) {
+    if (hipError_t e = launch_vt_dtype(p, dtype, false, st)) return e;
+  } else if (n > 0) {
     switch (dtype) {
       case MCPU_F32: hipLaunchKernelGGL(conv_fwd_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
       case MCPU_BF16: hipLaunchKernelGGL(conv_fwd_kernel<bf16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
@@ -263,6 +504,13 @@ hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
 
 hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float* dbias, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
+  if (n > 0 && p.vt) {
+    if (hipError_t e = launch_vt_dtype(p, dtype, true, st)) return e;
+    const int64_t per = p.dim * (p.width + 1);
+    hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(blocks_for(per)), dim3(256), 0, st, p.dw_part,
+                       dweight, dbias, p.batch * p.nseg, p.dim, p.width);
+    return hipGetLastError();
+  }
   if (n > 0) {
     switch (dtype) {
       case MCPU_F32: hipLaunchKernelGGL(conv_bwd_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;

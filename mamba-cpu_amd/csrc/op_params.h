@@ -11,6 +11,7 @@ namespace mcpu {
 constexpr int kConvT = 8;      // conv steps per chunk
 constexpr int kConvMaxW = 16;  // largest supported conv width
 constexpr int kConvRMax = 16;  // most threads walking one (batch, channel) row
+constexpr int kConvVTSteps = 8;  // steps per thread of the time-contiguous fast path
 
 struct ConvParams {
   const void* x;
@@ -29,6 +30,11 @@ struct ConvParams {
   int64_t sx[3], sinit[3], sout[3], sdo[3], sdx[3];
   int silu;
   int channels_last;  // thread index decomposed channel-fastest
+  // Time-contiguous fast path (conv_*_vt_kernel): used when vt != 0.
+  int vt;
+  int tpr;            // threads per row segment: 64, 128 or 256
+  int rpw;            // row segments per workgroup: 256 / tpr
+  int64_t nseg;       // segments per row (rows longer than 2048 steps)
 };
 
 struct ConvUpdateParams {

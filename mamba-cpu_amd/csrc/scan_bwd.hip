@@ -348,59 +348,60 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   }
 }
 
-// dB/dC: out[s, e] = sum over channel blocks c of part[s, c, e], summed in
-// the order c = 0, 1, ... for every element (deterministic). Four elements per
-// thread.
-__global__ void __launch_bounds__(256) reduce_bc_kernel(const float* __restrict__ part,
-                                                        float* __restrict__ out, int64_t slices,
-                                                        int64_t nblk_c, int64_t per_slice) {
-  const int64_t per4 = per_slice / 4;
-  const int64_t total4 = slices * per4;
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total4; i += 256ll * gridDim.x) {
+// All reductions of one backward in one launch, as a grid-stride loop over the
+// concatenation of
+//   dB, dC:  out[s, e] = sum over channel blocks c of part[s, c, e]  (four
+//            elements per item when the slice size allows, else one)
+//   dA, dD, ddelta_bias:  out[e] = sum over the batch of part[b, e]
+// Every element is summed in the fixed order c = 0, 1, ... or b = 0, 1, ...
+// (deterministic, no atomics). A job with part == nullptr is absent.
+struct ReduceJob {
+  const float* part;
+  float* out;
+  int64_t outer;   // slices (dB/dC) or 1 (batch reductions)
+  int64_t nsum;    // terms per element: channel blocks or batch
+  int64_t per;     // elements per slice
+  int64_t items;   // work items of this job
+  int vec;         // 4: float4 items, 1: scalar items
+};
+struct ReduceJobs {
+  ReduceJob job[5];
+  int njobs;
+};
+
+__device__ __forceinline__ void reduce_item(const ReduceJob& j, int64_t i) {
+  if (j.vec == 4) {
+    const int64_t per4 = j.per / 4;
     const int64_t sl = i / per4, e = (i % per4) * 4;
-    const float* src = part + sl * nblk_c * per_slice + e;
+    const float* src = j.part + sl * j.nsum * j.per + e;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int64_t c = 0;
-    for (; c + 4 <= nblk_c; c += 4) {
-      const float4 v0 = *reinterpret_cast<const float4*>(src + (c + 0) * per_slice);
-      const float4 v1 = *reinterpret_cast<const float4*>(src + (c + 1) * per_slice);
-      const float4 v2 = *reinterpret_cast<const float4*>(src + (c + 2) * per_slice);
-      const float4 v3 = *reinterpret_cast<const float4*>(src + (c + 3) * per_slice);
-      acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;
-      acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;
-      acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;
-      acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;
+    for (int64_t c = 0; c < j.nsum; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(src + c * j.per);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
     }
-    for (; c < nblk_c; ++c) {
-      const float4 v = *reinterpret_cast<const float4*>(src + c * per_slice);
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-    }
-    *reinterpret_cast<float4*>(out + sl * per_slice + e) = acc;
+    *reinterpret_cast<float4*>(j.out + sl * j.per + e) = acc;
+  } else {
+    const int64_t sl = i / j.per, e = i % j.per;
+    const float* src = j.part + sl * j.nsum * j.per + e;
+    float acc = 0.f;
+    for (int64_t c = 0; c < j.nsum; ++c) acc += src[c * j.per];
+    j.out[sl * j.per + e] = acc;
   }
 }
 
-// Same, one element per thread, for sizes that are not a multiple of 4.
-__global__ void __launch_bounds__(256) reduce_bc1_kernel(const float* __restrict__ part,
-                                                         float* __restrict__ out, int64_t slices,
-                                                         int64_t nblk_c, int64_t per_slice) {
-  const int64_t total = slices * per_slice;
+__global__ void __launch_bounds__(256) reduce_jobs_kernel(const ReduceJobs jobs, int64_t total) {
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += 256ll * gridDim.x) {
-    const int64_t sl = i / per_slice, e = i % per_slice;
-    const float* src = part + sl * nblk_c * per_slice + e;
-    float acc = 0.f;
-    for (int64_t c = 0; c < nblk_c; ++c) acc += src[c * per_slice];
-    out[i] = acc;
-  }
-}
-
-// out[e] = sum over batch of part[b, e].
-__global__ void __launch_bounds__(256) reduce_batch_kernel(const float* __restrict__ part,
-                                                           float* __restrict__ out, int64_t batch,
-                                                           int64_t per_batch) {
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < per_batch; i += 256ll * gridDim.x) {
-    float acc = 0.f;
-    for (int64_t b = 0; b < batch; ++b) acc += part[b * per_batch + i];
-    out[i] = acc;
+    int64_t k = i;
+    for (int q = 0; q < jobs.njobs; ++q) {
+      if (k < jobs.job[q].items) {
+        reduce_item(jobs.job[q], k);
+        break;
+      }
+      k -= jobs.job[q].items;
+    }
   }
 }
 
@@ -462,22 +463,37 @@ static unsigned grid_for(int64_t n) {
   return static_cast<unsigned>(g < 1 ? 1 : g);
 }
 
-hipError_t scan_reduce_bc_launch(const float* part, float* out, int64_t slices, int64_t nblk_c,
-                                 int64_t per_slice, hipStream_t stream) {
-  if (per_slice % 4 == 0) {
-    hipLaunchKernelGGL(reduce_bc_kernel, dim3(grid_for(slices * per_slice / 4)), dim3(256), 0,
-                       stream, part, out, slices, nblk_c, per_slice);
-  } else {
-    hipLaunchKernelGGL(reduce_bc1_kernel, dim3(grid_for(slices * per_slice)), dim3(256), 0, stream,
-                       part, out, slices, nblk_c, per_slice);
-  }
-  return hipGetLastError();
-}
-
-hipError_t scan_reduce_batch_launch(const float* part, float* out, int64_t batch,
-                                    int64_t per_batch, hipStream_t stream) {
-  hipLaunchKernelGGL(reduce_batch_kernel, dim3(grid_for(per_batch)), dim3(256), 0, stream, part,
-                     out, batch, per_batch);
+// Sums the backward's partials: dB/dC over channel blocks (`slices` slices of
+// `per_slice` elements, `nblk_c` blocks each; skipped when dB_part is null),
+// and dA / dD / ddelta_bias over the batch (each skipped when its part is null).
+hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_part, float* dC,
+                              int64_t slices, int64_t nblk_c, int64_t per_slice,
+                              const float* dA_part, float* dA, int64_t nA, const float* dD_part,
+                              float* dD, const float* dbias_part, float* dbias, int64_t dim,
+                              int64_t batch, hipStream_t stream) {
+  ReduceJobs jobs{};
+  int64_t total = 0;
+  auto add = [&](const float* part, float* out, int64_t outer, int64_t nsum, int64_t per) {
+    if (part == nullptr || outer * per == 0) return;
+    ReduceJob& j = jobs.job[jobs.njobs++];
+    j.part = part;
+    j.out = out;
+    j.outer = outer;
+    j.nsum = nsum;
+    j.per = per;
+    const bool aligned = reinterpret_cast<uintptr_t>(part) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    j.vec = per % 4 == 0 && aligned ? 4 : 1;
+    j.items = outer * per / j.vec;
+    total += j.items;
+  };
+  add(dB_part, dB, slices, nblk_c, per_slice);
+  add(dC_part, dC, slices, nblk_c, per_slice);
+  add(dA_part, dA, 1, batch, nA);
+  add(dD_part, dD, 1, batch, dim);
+  add(dbias_part, dbias, 1, batch, dim);
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(reduce_jobs_kernel, dim3(grid_for(total)), dim3(256), 0, stream, jobs, total);
   return hipGetLastError();
 }
 

@@ -292,13 +292,27 @@ def _setup_context_ckpt(ctx, inputs, output):
     ctx.set_materialize_grads(False)
 
 
+def _tracing(*tensors):
+    """True under torch.compile / export / make_fx tracing (fake or
+    functional tensors, or an active dispatch mode), where the backward must
+    call the custom op rather than its body."""
+    return (torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0
+            or any(type(t) is not torch.Tensor for t in tensors))
+
+
 def _backward_ckpt(ctx, grad_out, grad_last_state, grad_ckpt, grad_ysave):
     u, delta, A, B, C, D, z, delta_bias, ckpt, ysave = ctx.saved_tensors
     dout = torch.zeros_like(u) if grad_out is None else grad_out.to(u.dtype)
     dlast = None if grad_last_state is None else grad_last_state.float().contiguous()
-    du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(
-        u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt, ysave
-    )
+    args = (u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt, ysave)
+    if _tracing(u, dout):
+        grads = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args)
+    else:
+        # Eager: the op's body directly, without a second trip through the
+        # dispatcher (the backward runs once per training step; this keeps its
+        # host cost below the kernels' time).
+        grads = _scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", *args)
+    du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = grads
     return (
         du, ddelta, dA, dB, dC,
         dD if D is not None else None,

@@ -188,3 +188,49 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.mamba_cpu.causal_conv1d_bwd.default,
                           (x.detach(), w.detach(), b.detach(), init.detach(),
                            torch.randn(2, 8, 12, device=DEV), torch.randn(2, 8, 3, device=DEV), True))
+
+
+@pytest.mark.parametrize("seqlen", [8, 64, 520, 1024, 2048, 2056])
+@pytest.mark.parametrize("width", [2, 3, 4, 5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_vector_path_forward_backward(seqlen, width, dtype):
+    """Time-contiguous x with seqlen a multiple of 8 takes the vectorised
+    kernels: rows of one to four waves (seqlen <= 2048) and rows split into
+    2048-step segments (2056). Initial/final states and their gradients ride
+    along; the chunk at t = 0 reads the initial states, the last one dfinal."""
+    torch.manual_seed(seqlen + width)
+    b, d = 2, 6
+    x = torch.randn(b, d, seqlen, device=DEV).to(dtype).requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    init = torch.randn(b, d, width - 1, device=DEV).to(dtype).requires_grad_()
+    out, final = causal_conv1d_fn(x, w, bias, initial_states=init, return_final_states=True,
+                                  activation="silu")
+    want_out, want_final = O.causal_conv1d_fwd(x, w, bias, init, "silu")
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    close(out, want_out, tol, tol, "out")
+    close(final, want_final, 0, 0, "final")
+    G = torch.randn(b, d, seqlen, device=DEV).to(dtype)
+    Gf = torch.randn(b, d, width - 1, device=DEV).to(dtype)
+    ((out.float() * G.float()).sum() + (final.float() * Gf.float()).sum()).backward()
+    dx, dw, db, dinit = O.causal_conv1d_bwd(x, w, bias, init, G, "silu", Gf)
+    gtol = 1e-4 if dtype == torch.float32 else 2e-2
+    close(x.grad, dx, gtol, gtol, "dx")
+    close(init.grad, dinit, gtol, gtol, "dinit")
+    for got, want, name in ((w.grad, dw, "dweight"), (bias.grad, db, "dbias")):
+        s = max(np.abs(want).max(), 1.0)
+        close(got / s, want / s, gtol, gtol, name)
+
+
+def test_vector_path_no_activation_no_bias():
+    torch.manual_seed(3)
+    x = torch.randn(3, 5, 128, device=DEV, requires_grad=True)
+    w = torch.randn(5, 4, device=DEV, requires_grad=True)
+    out = causal_conv1d_fn(x, w)
+    want, _ = O.causal_conv1d_fwd(x, w)
+    close(out, want, 1e-5, 1e-5)
+    G = torch.randn(3, 5, 128, device=DEV)
+    (out * G).sum().backward()
+    dx, dw, _, _ = O.causal_conv1d_bwd(x, w, None, None, G, None)
+    close(x.grad, dx, 1e-4, 1e-4, "dx")
+    close(w.grad, dw, 1e-4, 1e-4, "dweight")
