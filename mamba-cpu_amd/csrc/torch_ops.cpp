@@ -1,0 +1,666 @@
+// The mamba_cpu torch operators, in C++ over the C ABI of libmamba_hip.so.
+//
+// Same operator names and schemas as the reference's Python custom ops
+// (src/mamba_cpu/ops/selective_scan_interface.py:16-124,
+// src/mamba_cpu/ops/causal_conv1d.py, src/mamba_cpu/ops/selective_state_update.py),
+// registered for the CUDA dispatch key (ROCm GPU tensors), with their autograd
+// formulas registered for the Autograd key as torch::autograd::Functions. The
+// bodies check their arguments (ValueError / NotImplementedError, as the
+// reference raises), allocate outputs and workspaces through the torch caching
+// allocator and launch on the current stream; they never synchronise.
+// Fake (meta) implementations are registered from Python (mamba_cpu/_ops.py).
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/autograd.h>
+#include <torch/library.h>
+
+#include <cstring>
+#include <optional>
+#include <tuple>
+
+#include "mamba_hip.h"
+
+namespace mcpu_torch {
+namespace {
+
+using at::Tensor;
+using std::optional;
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+// ---- helpers ------------------------------------------------------------------
+
+void* stream_of(const Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_rc(int rc, const char* what) {
+  if (rc == MCPU_OK) return;
+  const char* msg = mcpu_last_error();
+  TORCH_CHECK_VALUE(rc != MCPU_ERR_INVALID, what, ": ", msg);
+  TORCH_CHECK_NOT_IMPLEMENTED(rc != MCPU_ERR_UNSUPPORTED, what, ": ", msg);
+  TORCH_CHECK(false, what, ": ", msg);
+}
+
+bool x_dtype(at::ScalarType s) {
+  return s == at::kFloat || s == at::kBFloat16 || s == at::kHalf;
+}
+
+int32_t dtype_tag(at::ScalarType s) {
+  return s == at::kFloat ? MCPU_F32 : (s == at::kBFloat16 ? MCPU_BF16 : MCPU_F16);
+}
+
+bool has(const optional<Tensor>& t) { return t.has_value() && t->defined(); }
+const void* ptr(const optional<Tensor>& t) { return has(t) ? t->data_ptr() : nullptr; }
+const float* fptr(const optional<Tensor>& t) {
+  return has(t) ? static_cast<const float*>(t->data_ptr()) : nullptr;
+}
+
+void strides3(int64_t (&s)[3], const Tensor& t) {
+  for (int i = 0; i < 3; ++i) s[i] = t.stride(i);
+}
+void strides3(int64_t (&s)[3], const optional<Tensor>& t) {
+  if (has(t)) strides3(s, *t);
+  else s[0] = s[1] = s[2] = 0;
+}
+
+void check_gpu(const char* name, const optional<Tensor>& t) {
+  if (has(t))
+    TORCH_CHECK_VALUE(t->is_cuda(), name, " runs on ROCm GPU tensors, got a tensor on ", t->device());
+}
+
+optional<Tensor> opt(const Tensor& t) { return t.defined() ? optional<Tensor>(t) : std::nullopt; }
+
+// A (batch, dim, seqlen) result laid out like x: channel-contiguous when x is
+// (the transposed views Hugging Face passes), contiguous otherwise.
+Tensor like_x(const Tensor& x) {
+  if (x.dim() == 3 && x.stride(1) == 1 && x.stride(2) != 1) {
+    const int64_t b = x.size(0), d = x.size(1), l = x.size(2);
+    return at::empty_strided({b, d, l}, {d * l, 1, d}, x.options());
+  }
+  return at::empty(x.sizes(), x.options());
+}
+
+// ---- selective scan -------------------------------------------------------------
+
+void validate_scan(const char* name, const Tensor& u, const Tensor& delta, const Tensor& A,
+                   const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                   const optional<Tensor>& z, const optional<Tensor>& bias,
+                   std::initializer_list<optional<Tensor>> extra = {}) {
+  for (const optional<Tensor>& t : {opt(u), opt(delta), opt(A), opt(B), opt(C), D, z, bias})
+    check_gpu(name, t);
+  for (const optional<Tensor>& t : extra) check_gpu(name, t);
+  TORCH_CHECK_VALUE(x_dtype(u.scalar_type()) && delta.scalar_type() == u.scalar_type() &&
+                        (!has(z) || z->scalar_type() == u.scalar_type()),
+                    name, " expects u, delta and z of one dtype among float32, bfloat16 and float16");
+  for (const optional<Tensor>& t : {opt(A), opt(B), opt(C), D, bias})
+    TORCH_CHECK_VALUE(!has(t) || t->scalar_type() == at::kFloat, name,
+                      " expects float32 A, B, C, D and delta_bias");
+  TORCH_CHECK_VALUE(u.dim() == 3 && delta.sizes() == u.sizes() && (!has(z) || z->sizes() == u.sizes()),
+                    name, " expects u, delta and z of shape (batch, dim, seqlen)");
+  const int64_t batch = u.size(0), dim = u.size(1), seqlen = u.size(2);
+  TORCH_CHECK_VALUE(A.dim() == 2 && A.size(0) == dim, name, " expects A of shape (dim, dstate)");
+  const int64_t dstate = A.size(1);
+  for (const Tensor* X : {&B, &C})
+    TORCH_CHECK_VALUE(X->dim() == 4 && X->size(0) == batch && X->size(2) == seqlen &&
+                          X->size(3) == dstate,
+                      name, " expects B and C of shape (batch, ngroups, seqlen, dstate)");
+  TORCH_CHECK_VALUE(B.size(1) == C.size(1) && B.size(1) > 0 && dim % B.size(1) == 0, name,
+                    ": dim (", dim, ") must be divisible by ngroups (", B.size(1), ")");
+  for (const optional<Tensor>& t : {D, bias})
+    TORCH_CHECK_VALUE(!has(t) || (t->dim() == 1 && t->size(0) == dim && t->is_contiguous()), name,
+                      " expects contiguous D and delta_bias of shape (dim,)");
+  TORCH_CHECK_VALUE(A.is_contiguous(), name, " expects a contiguous A");
+}
+
+mcpu_scan_args scan_args(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+                         const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+                         const optional<Tensor>& bias, bool softplus) {
+  mcpu_scan_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.u = u.data_ptr();
+  a.delta = delta.data_ptr();
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.B = static_cast<const float*>(B.data_ptr());
+  a.C = static_cast<const float*>(C.data_ptr());
+  a.D = fptr(D);
+  a.z = ptr(z);
+  a.delta_bias = fptr(bias);
+  a.batch = u.size(0);
+  a.dim = u.size(1);
+  a.seqlen = u.size(2);
+  a.dstate = A.size(1);
+  a.ngroups = B.size(1);
+  a.delta_softplus = softplus ? 1 : 0;
+  a.dtype = dtype_tag(u.scalar_type());
+  strides3(a.u_stride, u);
+  strides3(a.delta_stride, delta);
+  strides3(a.z_stride, z);
+  for (int i = 0; i < 4; ++i) {
+    a.B_stride[i] = B.stride(i);
+    a.C_stride[i] = C.stride(i);
+  }
+  return a;
+}
+
+constexpr int64_t kBlockT = 16;  // time steps per checkpoint block
+
+std::vector<int64_t> ckpt_shape(const Tensor& u, const Tensor& A) {
+  return {u.size(0), u.size(1), (u.size(2) + kBlockT - 1) / kBlockT, A.size(1)};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> scan_fwd_impl(
+    const char* name, const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+    const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+    const optional<Tensor>& bias, bool softplus, bool save) {
+  validate_scan(name, u, delta, A, B, C, D, z, bias);
+  c10::DeviceGuard guard(u.device());
+  const int64_t batch = u.size(0), dim = u.size(1);
+  Tensor out = at::empty(u.sizes(), u.options());
+  Tensor last = at::empty({batch, dim, A.size(1)}, u.options().dtype(at::kFloat));
+  Tensor ckpt, ysave;
+  mcpu_scan_args a = scan_args(u, delta, A, B, C, D, z, bias, softplus);
+  a.out = out.data_ptr();
+  a.last_state = static_cast<float*>(last.data_ptr());
+  if (save) {
+    ckpt = at::empty(ckpt_shape(u, A), u.options().dtype(at::kFloat));
+    ysave = has(z) ? at::empty(u.sizes(), u.options()) : at::empty({0}, u.options());
+    a.ckpt = static_cast<float*>(ckpt.data_ptr());
+    a.ysave = has(z) ? ysave.data_ptr() : nullptr;
+  }
+  check_rc(mcpu_selective_scan_fwd(&a, stream_of(u)), name);
+  return {out, last, ckpt, ysave};
+}
+
+std::tuple<Tensor, Tensor> selective_scan_fwd(const Tensor& u, const Tensor& delta, const Tensor& A,
+                                              const Tensor& B, const Tensor& C,
+                                              const optional<Tensor>& D, const optional<Tensor>& z,
+                                              const optional<Tensor>& bias, bool softplus) {
+  auto r = scan_fwd_impl("mamba_cpu::selective_scan_fwd", u, delta, A, B, C, D, z, bias, softplus,
+                         false);
+  return {std::get<0>(r), std::get<1>(r)};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> selective_scan_fwd_ckpt(
+    const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C,
+    const optional<Tensor>& D, const optional<Tensor>& z, const optional<Tensor>& bias,
+    bool softplus) {
+  return scan_fwd_impl("mamba_cpu::selective_scan_fwd_ckpt", u, delta, A, B, C, D, z, bias,
+                       softplus, true);
+}
+
+using Grads8 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>;
+
+Grads8 scan_bwd_impl(const char* name, const Tensor& u, const Tensor& delta, const Tensor& A,
+                     const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                     const optional<Tensor>& z, const optional<Tensor>& bias, bool softplus,
+                     const Tensor& dout, const optional<Tensor>& dlast_state,
+                     const optional<Tensor>& ckpt, const optional<Tensor>& ysave_in) {
+  validate_scan(name, u, delta, A, B, C, D, z, bias, {opt(dout), dlast_state, ckpt, ysave_in});
+  TORCH_CHECK_VALUE(dout.sizes() == u.sizes() && dout.scalar_type() == u.scalar_type(), name,
+                    " expects dout shaped and typed like u");
+  const int64_t batch = u.size(0), dim = u.size(1), dstate = A.size(1);
+  optional<Tensor> dlast;
+  if (has(dlast_state)) {
+    TORCH_CHECK_VALUE(dlast_state->scalar_type() == at::kFloat && dlast_state->dim() == 3 &&
+                          dlast_state->size(0) == batch && dlast_state->size(1) == dim &&
+                          dlast_state->size(2) == dstate,
+                      name, " expects float32 dlast_state (batch, dim, dstate)");
+    dlast = dlast_state->contiguous();
+  }
+  if (has(ckpt))
+    TORCH_CHECK_VALUE(ckpt->scalar_type() == at::kFloat && ckpt->is_contiguous() &&
+                          ckpt->sizes() == at::IntArrayRef(ckpt_shape(u, A)),
+                      name, " expects the float32 checkpoints written by selective_scan_fwd_ckpt");
+  optional<Tensor> ysave = (has(ysave_in) && ysave_in->numel() > 0) ? ysave_in : std::nullopt;
+  if (has(ysave))
+    TORCH_CHECK_VALUE(ysave->sizes() == u.sizes() && ysave->scalar_type() == u.scalar_type() &&
+                          ysave->is_contiguous() && has(z),
+                      name, " expects the y written by selective_scan_fwd_ckpt");
+  c10::DeviceGuard guard(u.device());
+  Tensor du = at::empty(u.sizes(), u.options());
+  Tensor ddelta = at::empty(delta.sizes(), delta.options());
+  Tensor dA = at::empty(A.sizes(), A.options());
+  Tensor dB = at::empty(B.sizes(), B.options());
+  Tensor dC = at::empty(C.sizes(), C.options());
+  Tensor dD = at::empty({dim}, A.options());
+  Tensor dz = has(z) ? at::empty(z->sizes(), z->options()) : at::empty({0}, u.options());
+  Tensor dbias = at::empty({dim}, A.options());
+  mcpu_scan_args a = scan_args(u, delta, A, B, C, D, z, bias, softplus);
+  a.dout = dout.data_ptr();
+  strides3(a.dout_stride, dout);
+  a.dlast_state = fptr(dlast);
+  a.ckpt = has(ckpt) ? static_cast<float*>(ckpt->data_ptr()) : nullptr;
+  a.ysave = has(ysave) ? ysave->data_ptr() : nullptr;
+  a.du = du.data_ptr();
+  a.ddelta = ddelta.data_ptr();
+  a.dz = has(z) ? dz.data_ptr() : nullptr;
+  a.dA = static_cast<float*>(dA.data_ptr());
+  a.dB = static_cast<float*>(dB.data_ptr());
+  a.dC = static_cast<float*>(dC.data_ptr());
+  a.dD = static_cast<float*>(dD.data_ptr());
+  a.ddelta_bias = static_cast<float*>(dbias.data_ptr());
+  const size_t ws_bytes = mcpu_selective_scan_bwd_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)},
+                        u.options().dtype(at::kByte));
+  check_rc(mcpu_selective_scan_bwd(&a, ws.data_ptr(), ws_bytes, stream_of(u)), name);
+  return {du, ddelta, dA, dB, dC, dD, dz, dbias};
+}
+
+Grads8 selective_scan_bwd(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+                          const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+                          const optional<Tensor>& bias, bool softplus, const Tensor& dout,
+                          const optional<Tensor>& dlast_state) {
+  return scan_bwd_impl("mamba_cpu::selective_scan_bwd", u, delta, A, B, C, D, z, bias, softplus,
+                       dout, dlast_state, std::nullopt, std::nullopt);
+}
+
+Grads8 selective_scan_bwd_ckpt(const Tensor& u, const Tensor& delta, const Tensor& A,
+                               const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                               const optional<Tensor>& z, const optional<Tensor>& bias,
+                               bool softplus, const Tensor& dout,
+                               const optional<Tensor>& dlast_state, const Tensor& ckpt,
+                               const Tensor& ysave) {
+  return scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", u, delta, A, B, C, D, z, bias,
+                       softplus, dout, dlast_state, ckpt, ysave);
+}
+
+// Autograd (reference selective_scan_interface.py:100-124): inputs are saved,
+// never activations; a missing output gradient is zero; gradients of absent
+// D / z / delta_bias are None.
+template <bool CKPT>
+struct ScanFn : public torch::autograd::Function<ScanFn<CKPT>> {
+  static variable_list forward(AutogradContext* ctx, const Tensor& u, const Tensor& delta,
+                               const Tensor& A, const Tensor& B, const Tensor& C,
+                               const optional<Tensor>& D, const optional<Tensor>& z,
+                               const optional<Tensor>& bias, bool softplus) {
+    at::AutoDispatchBelowADInplaceOrView below;
+    variable_list out;
+    Tensor ckpt, ysave;
+    if constexpr (CKPT) {
+      static auto op = c10::Dispatcher::singleton()
+                           .findSchemaOrThrow("mamba_cpu::selective_scan_fwd_ckpt", "")
+                           .typed<decltype(selective_scan_fwd_ckpt)>();
+      auto r = op.call(u, delta, A, B, C, D, z, bias, softplus);
+      ckpt = std::get<2>(r);
+      ysave = std::get<3>(r);
+      out = {std::get<0>(r), std::get<1>(r), ckpt, ysave};
+      ctx->mark_non_differentiable({ckpt, ysave});
+    } else {
+      static auto op = c10::Dispatcher::singleton()
+                           .findSchemaOrThrow("mamba_cpu::selective_scan_fwd", "")
+                           .typed<decltype(selective_scan_fwd)>();
+      auto r = op.call(u, delta, A, B, C, D, z, bias, softplus);
+      out = {std::get<0>(r), std::get<1>(r)};
+    }
+    ctx->save_for_backward({u, delta, A, B, C, D.value_or(Tensor()), z.value_or(Tensor()),
+                            bias.value_or(Tensor()), ckpt, ysave});
+    ctx->saved_data["softplus"] = softplus;
+    ctx->set_materialize_grads(false);
+    return out;
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const variable_list s = ctx->get_saved_variables();
+    const Tensor &u = s[0], &delta = s[1], &A = s[2], &B = s[3], &C = s[4];
+    const optional<Tensor> D = opt(s[5]), z = opt(s[6]), bias = opt(s[7]);
+    const bool softplus = ctx->saved_data["softplus"].toBool();
+    const Tensor dout = grads[0].defined() ? grads[0].to(u.scalar_type()) : at::zeros_like(u);
+    const optional<Tensor> dlast =
+        grads[1].defined() ? optional<Tensor>(grads[1].to(at::kFloat).contiguous()) : std::nullopt;
+    Grads8 g;
+    if constexpr (CKPT) {
+      static auto op = c10::Dispatcher::singleton()
+                           .findSchemaOrThrow("mamba_cpu::selective_scan_bwd_ckpt", "")
+                           .typed<decltype(selective_scan_bwd_ckpt)>();
+      g = op.call(u, delta, A, B, C, D, z, bias, softplus, dout, dlast, s[8], s[9]);
+    } else {
+      static auto op = c10::Dispatcher::singleton()
+                           .findSchemaOrThrow("mamba_cpu::selective_scan_bwd", "")
+                           .typed<decltype(selective_scan_bwd)>();
+      g = op.call(u, delta, A, B, C, D, z, bias, softplus, dout, dlast);
+    }
+    return {std::get<0>(g), std::get<1>(g), std::get<2>(g), std::get<3>(g), std::get<4>(g),
+            has(D) ? std::get<5>(g) : Tensor(), has(z) ? std::get<6>(g) : Tensor(),
+            has(bias) ? std::get<7>(g) : Tensor(), Tensor()};
+  }
+};
+
+std::tuple<Tensor, Tensor> selective_scan_fwd_autograd(
+    const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C,
+    const optional<Tensor>& D, const optional<Tensor>& z, const optional<Tensor>& bias,
+    bool softplus) {
+  auto r = ScanFn<false>::apply(u, delta, A, B, C, D, z, bias, softplus);
+  return {r[0], r[1]};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> selective_scan_fwd_ckpt_autograd(
+    const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C,
+    const optional<Tensor>& D, const optional<Tensor>& z, const optional<Tensor>& bias,
+    bool softplus) {
+  auto r = ScanFn<true>::apply(u, delta, A, B, C, D, z, bias, softplus);
+  return {r[0], r[1], r[2], r[3]};
+}
+
+// ---- causal conv1d ------------------------------------------------------------------
+
+void check_conv(const char* name, const Tensor& x, const Tensor& weight,
+                const optional<Tensor>& bias, const optional<Tensor>& init) {
+  for (const optional<Tensor>& t : {opt(x), opt(weight), bias, init}) check_gpu(name, t);
+  TORCH_CHECK_VALUE(x_dtype(x.scalar_type()), name,
+                    " expects x in float32, bfloat16 or float16, got ", x.scalar_type());
+  TORCH_CHECK_VALUE(x.dim() == 3 && weight.dim() == 2 && weight.size(0) == x.size(1), name,
+                    " expects x (batch, dim, seqlen) and weight (dim, width)");
+  TORCH_CHECK_VALUE(weight.scalar_type() == at::kFloat && weight.is_contiguous(), name,
+                    " expects a contiguous float32 weight");
+  TORCH_CHECK_VALUE(!has(bias) || (bias->scalar_type() == at::kFloat && bias->dim() == 1 &&
+                                   bias->size(0) == x.size(1)),
+                    name, " expects a float32 bias of shape (dim,)");
+  TORCH_CHECK_VALUE(!has(init) || (init->scalar_type() == x.scalar_type() && init->dim() == 3 &&
+                                   init->size(0) == x.size(0) && init->size(1) == x.size(1) &&
+                                   init->size(2) == weight.size(1) - 1),
+                    name, " expects initial_states (batch, dim, width - 1) in x's dtype");
+}
+
+mcpu_conv_args conv_args(const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
+                         const optional<Tensor>& init, bool silu) {
+  mcpu_conv_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x.data_ptr();
+  a.weight = static_cast<const float*>(weight.data_ptr());
+  a.bias = fptr(bias);
+  a.initial_states = ptr(init);
+  a.batch = x.size(0);
+  a.dim = x.size(1);
+  a.seqlen = x.size(2);
+  a.width = weight.size(1);
+  a.silu = silu ? 1 : 0;
+  a.dtype = dtype_tag(x.scalar_type());
+  strides3(a.x_stride, x);
+  strides3(a.init_stride, init);
+  return a;
+}
+
+std::tuple<Tensor, Tensor> causal_conv1d_fwd(const Tensor& x, const Tensor& weight,
+                                             const optional<Tensor>& bias,
+                                             const optional<Tensor>& init,
+                                             bool return_final_states, bool silu) {
+  const char* name = "mamba_cpu::causal_conv1d_fwd";
+  check_conv(name, x, weight, bias, init);
+  c10::DeviceGuard guard(x.device());
+  Tensor out = like_x(x);
+  const int64_t b = x.size(0), d = x.size(1), w = weight.size(1);
+  Tensor final = return_final_states ? at::empty({b, d, w - 1}, x.options())
+                                     : at::empty({0}, x.options());
+  mcpu_conv_args a = conv_args(x, weight, bias, init, silu);
+  a.out = out.data_ptr();
+  strides3(a.out_stride, out);
+  a.final_states = return_final_states ? final.data_ptr() : nullptr;
+  check_rc(mcpu_causal_conv1d_fwd(&a, stream_of(x)), name);
+  return {out, final};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
+    const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
+    const optional<Tensor>& init, const Tensor& dout, const optional<Tensor>& dfinal_states,
+    bool silu) {
+  const char* name = "mamba_cpu::causal_conv1d_bwd";
+  check_conv(name, x, weight, bias, init);
+  check_gpu(name, dout);
+  check_gpu(name, dfinal_states);
+  TORCH_CHECK_VALUE(dout.sizes() == x.sizes() && dout.scalar_type() == x.scalar_type(), name,
+                    " expects dout shaped and typed like x");
+  const int64_t b = x.size(0), d = x.size(1), w = weight.size(1);
+  optional<Tensor> dfinal;
+  if (has(dfinal_states)) {
+    TORCH_CHECK_VALUE(dfinal_states->dim() == 3 && dfinal_states->size(0) == b &&
+                          dfinal_states->size(1) == d && dfinal_states->size(2) == w - 1,
+                      name, " expects dfinal_states (batch, dim, width - 1)");
+    dfinal = dfinal_states->to(x.scalar_type()).contiguous();
+  }
+  c10::DeviceGuard guard(x.device());
+  Tensor dx = like_x(x);
+  Tensor dweight = at::empty(weight.sizes(), weight.options());
+  Tensor dbias = has(bias) ? at::empty({d}, weight.options()) : at::empty({0}, weight.options());
+  Tensor dinit = has(init) ? at::empty({b, d, w - 1}, x.options()) : at::empty({0}, x.options());
+  mcpu_conv_args a = conv_args(x, weight, bias, init, silu);
+  a.dout = dout.data_ptr();
+  strides3(a.dout_stride, dout);
+  a.dfinal_states = ptr(dfinal);
+  a.dx = dx.data_ptr();
+  strides3(a.dx_stride, dx);
+  a.dweight = static_cast<float*>(dweight.data_ptr());
+  a.dbias = has(bias) ? static_cast<float*>(dbias.data_ptr()) : nullptr;
+  a.dinitial_states = has(init) ? dinit.data_ptr() : nullptr;
+  const size_t ws_bytes = mcpu_causal_conv1d_bwd_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)},
+                        x.options().dtype(at::kByte));
+  check_rc(mcpu_causal_conv1d_bwd(&a, ws.data_ptr(), ws_bytes, stream_of(x)), name);
+  return {dx, dweight, dbias, dinit};
+}
+
+struct ConvFn : public torch::autograd::Function<ConvFn> {
+  static variable_list forward(AutogradContext* ctx, const Tensor& x, const Tensor& weight,
+                               const optional<Tensor>& bias, const optional<Tensor>& init,
+                               bool return_final_states, bool silu) {
+    at::AutoDispatchBelowADInplaceOrView below;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::causal_conv1d_fwd", "")
+                         .typed<decltype(causal_conv1d_fwd)>();
+    auto r = op.call(x, weight, bias, init, return_final_states, silu);
+    ctx->save_for_backward({x, weight, bias.value_or(Tensor()), init.value_or(Tensor())});
+    ctx->saved_data["silu"] = silu;
+    ctx->saved_data["final"] = return_final_states;
+    ctx->set_materialize_grads(false);
+    return {std::get<0>(r), std::get<1>(r)};
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const variable_list s = ctx->get_saved_variables();
+    const Tensor &x = s[0], &weight = s[1];
+    const optional<Tensor> bias = opt(s[2]), init = opt(s[3]);
+    const Tensor dout = grads[0].defined() ? grads[0].to(x.scalar_type()) : at::zeros_like(x);
+    const optional<Tensor> dfinal = (ctx->saved_data["final"].toBool() && grads[1].defined())
+                                        ? optional<Tensor>(grads[1])
+                                        : std::nullopt;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::causal_conv1d_bwd", "")
+                         .typed<decltype(causal_conv1d_bwd)>();
+    auto g = op.call(x, weight, bias, init, dout, dfinal, ctx->saved_data["silu"].toBool());
+    return {std::get<0>(g), std::get<1>(g), has(bias) ? std::get<2>(g) : Tensor(),
+            has(init) ? std::get<3>(g) : Tensor(), Tensor(), Tensor()};
+  }
+};
+
+std::tuple<Tensor, Tensor> causal_conv1d_fwd_autograd(const Tensor& x, const Tensor& weight,
+                                                      const optional<Tensor>& bias,
+                                                      const optional<Tensor>& init,
+                                                      bool return_final_states, bool silu) {
+  auto r = ConvFn::apply(x, weight, bias, init, return_final_states, silu);
+  return {r[0], r[1]};
+}
+
+Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& weight,
+                            const optional<Tensor>& bias, bool silu) {
+  const char* name = "mamba_cpu::causal_conv1d_update";
+  for (const optional<Tensor>& t : {opt(x), opt(conv_state), opt(weight), bias}) check_gpu(name, t);
+  TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && conv_state.scalar_type() == x.scalar_type(), name,
+                    " expects x and conv_state of one dtype among float32, bfloat16 and float16");
+  TORCH_CHECK_VALUE(weight.scalar_type() == at::kFloat && weight.is_contiguous() && weight.dim() == 2,
+                    name, " expects a contiguous float32 weight");
+  TORCH_CHECK_VALUE(x.dim() == 3 && conv_state.dim() == 3, name,
+                    " expects x (batch, dim, seqlen) and conv_state (batch, dim, state_len)");
+  c10::DeviceGuard guard(x.device());
+  Tensor out = at::empty(x.sizes(), x.options());
+  mcpu_conv_update_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x.data_ptr();
+  a.conv_state = conv_state.data_ptr();
+  a.weight = static_cast<const float*>(weight.data_ptr());
+  a.bias = fptr(bias);
+  a.out = out.data_ptr();
+  a.batch = x.size(0);
+  a.dim = x.size(1);
+  a.seqlen = x.size(2);
+  a.width = weight.size(1);
+  a.state_len = conv_state.size(2);
+  a.silu = silu ? 1 : 0;
+  a.dtype = dtype_tag(x.scalar_type());
+  strides3(a.x_stride, x);
+  strides3(a.state_stride, conv_state);
+  strides3(a.out_stride, out);
+  check_rc(mcpu_causal_conv1d_update(&a, stream_of(x)), name);
+  return out;
+}
+
+// ---- selective state update ---------------------------------------------------------
+
+Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, const Tensor& A,
+                              const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                              const optional<Tensor>& z, const optional<Tensor>& dt_bias,
+                              bool dt_softplus) {
+  const char* name = "mamba_cpu::selective_state_update";
+  for (const optional<Tensor>& t : {opt(state), opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias})
+    check_gpu(name, t);
+  TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && dt.scalar_type() == x.scalar_type() &&
+                        (!has(z) || z->scalar_type() == x.scalar_type()),
+                    name, " expects x, dt and z of one dtype among float32, bfloat16, float16");
+  TORCH_CHECK_VALUE(x_dtype(state.scalar_type()), name,
+                    " expects a float32, bfloat16 or float16 state");
+  TORCH_CHECK_VALUE(state.dim() == 4 && x.dim() == 3, name, " expects state (b, h, p, n) and x (b, h, p)");
+  const int64_t b = state.size(0), h = state.size(1), p = state.size(2), n = state.size(3);
+  TORCH_CHECK_VALUE(state.stride(3) == 1 || n == 1, name, " expects unit stride along dstate");
+  TORCH_CHECK_VALUE(x.size(0) == b && x.size(1) == h && x.size(2) == p && dt.sizes() == x.sizes() &&
+                        (!has(z) || z->sizes() == x.sizes()),
+                    name, " expects x, dt and z of shape (b, h, p)");
+  for (const optional<Tensor>& t : {opt(A), opt(B), opt(C), D, dt_bias})
+    TORCH_CHECK_VALUE(!has(t) || t->scalar_type() == at::kFloat, name,
+                      " expects float32 A, B, C, D and dt_bias");
+  TORCH_CHECK_VALUE(A.dim() == 3 && A.size(0) == h && A.size(1) == p && A.size(2) == n &&
+                        A.is_contiguous(),
+                    name, " expects a contiguous A of shape (nheads, headdim, dstate)");
+  const int64_t g = B.dim() == 3 ? B.size(1) : 0;
+  for (const Tensor* X : {&B, &C})
+    TORCH_CHECK_VALUE(X->dim() == 3 && X->size(0) == b && X->size(1) == g && X->size(2) == n &&
+                          (X->stride(2) == 1 || n == 1),
+                      name, " expects B and C of shape (batch, ngroups, dstate), unit dstate stride");
+  for (const optional<Tensor>& t : {D, dt_bias})
+    TORCH_CHECK_VALUE(!has(t) || (t->dim() == 2 && t->size(0) == h && t->size(1) == p &&
+                                  t->is_contiguous()),
+                      name, " expects contiguous D and dt_bias of shape (nheads, headdim)");
+  c10::DeviceGuard guard(x.device());
+  Tensor out = at::empty({b, h, p}, x.options());
+  mcpu_state_update_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.state = state.data_ptr();
+  a.x = x.data_ptr();
+  a.dt = dt.data_ptr();
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.B = static_cast<const float*>(B.data_ptr());
+  a.C = static_cast<const float*>(C.data_ptr());
+  a.D = fptr(D);
+  a.z = ptr(z);
+  a.dt_bias = fptr(dt_bias);
+  a.out = out.data_ptr();
+  a.batch = b;
+  a.nheads = h;
+  a.headdim = p;
+  a.dstate = n;
+  a.ngroups = g;
+  a.dt_softplus = dt_softplus ? 1 : 0;
+  a.dtype = dtype_tag(x.scalar_type());
+  a.state_dtype = dtype_tag(state.scalar_type());
+  for (int i = 0; i < 3; ++i) a.state_stride[i] = state.stride(i);
+  strides3(a.x_stride, x);
+  strides3(a.dt_stride, dt);
+  strides3(a.z_stride, z);
+  a.B_stride[0] = B.stride(0);
+  a.B_stride[1] = B.stride(1);
+  a.C_stride[0] = C.stride(0);
+  a.C_stride[1] = C.stride(1);
+  check_rc(mcpu_selective_state_update(&a, stream_of(x)), name);
+  return out;
+}
+
+// The two in-place ops record their mutation for autograd's version counters
+// (what torch.library does for a Python custom op with mutates_args).
+Tensor causal_conv1d_update_inplace(const Tensor& x, Tensor& conv_state, const Tensor& weight,
+                                    const optional<Tensor>& bias, bool silu) {
+  Tensor out;
+  {
+    at::AutoDispatchBelowADInplaceOrView below;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::causal_conv1d_update", "")
+                         .typed<decltype(causal_conv1d_update)>();
+    out = op.call(x, conv_state, weight, bias, silu);
+  }
+  conv_state.unsafeGetTensorImpl()->bump_version();
+  return out;
+}
+
+Tensor selective_state_update_inplace(Tensor& state, const Tensor& x, const Tensor& dt,
+                                      const Tensor& A, const Tensor& B, const Tensor& C,
+                                      const optional<Tensor>& D, const optional<Tensor>& z,
+                                      const optional<Tensor>& dt_bias, bool dt_softplus) {
+  Tensor out;
+  {
+    at::AutoDispatchBelowADInplaceOrView below;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::selective_state_update", "")
+                         .typed<decltype(selective_state_update)>();
+    out = op.call(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus);
+  }
+  state.unsafeGetTensorImpl()->bump_version();
+  return out;
+}
+
+}  // namespace
+}  // namespace mcpu_torch
+
+TORCH_LIBRARY(mamba_cpu, m) {
+  m.def("selective_scan_fwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor)");
+  m.def("selective_scan_bwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus, Tensor dout, Tensor? dlast_state) -> "
+        "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("selective_scan_fwd_ckpt(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("selective_scan_bwd_ckpt(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus, Tensor dout, Tensor? dlast_state, "
+        "Tensor ckpt, Tensor ysave) -> "
+        "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("causal_conv1d_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
+        "bool return_final_states, bool silu) -> (Tensor, Tensor)");
+  m.def("causal_conv1d_bwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
+        "Tensor dout, Tensor? dfinal_states, bool silu) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("causal_conv1d_update(Tensor x, Tensor(a!) conv_state, Tensor weight, Tensor? bias, "
+        "bool silu) -> Tensor");
+  m.def("selective_state_update(Tensor(a!) state, Tensor x, Tensor dt, Tensor A, Tensor B, "
+        "Tensor C, Tensor? D, Tensor? z, Tensor? dt_bias, bool dt_softplus) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
+  using namespace mcpu_torch;
+  m.impl("selective_scan_fwd", &selective_scan_fwd);
+  m.impl("selective_scan_bwd", &selective_scan_bwd);
+  m.impl("selective_scan_fwd_ckpt", &selective_scan_fwd_ckpt);
+  m.impl("selective_scan_bwd_ckpt", &selective_scan_bwd_ckpt);
+  m.impl("causal_conv1d_fwd", &causal_conv1d_fwd);
+  m.impl("causal_conv1d_bwd", &causal_conv1d_bwd);
+  m.impl("causal_conv1d_update", &causal_conv1d_update);
+  m.impl("selective_state_update", &selective_state_update);
+}
+
+TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
+  using namespace mcpu_torch;
+  m.impl("selective_scan_fwd", &selective_scan_fwd_autograd);
+  m.impl("selective_scan_fwd_ckpt", &selective_scan_fwd_ckpt_autograd);
+  m.impl("causal_conv1d_fwd", &causal_conv1d_fwd_autograd);
+}
+
+TORCH_LIBRARY_IMPL(mamba_cpu, ADInplaceOrView, m) {
+  using namespace mcpu_torch;
+  m.impl("causal_conv1d_update", &causal_conv1d_update_inplace);
+  m.impl("selective_state_update", &selective_state_update_inplace);
+}

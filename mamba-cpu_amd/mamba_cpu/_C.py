@@ -1,10 +1,14 @@
 """Binding of libmamba_hip.so, the gfx950 kernel library, through its C ABI.
 
 This module plays the role of the reference's nanobind module `mamba_cpu._C`
-(csrc/bindings.cpp:17-84): tensors cross the boundary as raw device pointers
-and element strides, and the library never sees a torch type. The argument
-blocks mirror include/mamba_hip.h field for field; their sizes are checked
-against the library at load time.
+(csrc/bindings.cpp:17-84). It loads the two native libraries:
+  libmamba_hip.so    the kernels behind the C ABI of include/mamba_hip.h
+                     (raw device pointers and element strides, no torch types),
+                     also bound here through ctypes: the argument blocks mirror
+                     the header field for field and their sizes are checked
+                     against the library at load time;
+  libmamba_torch.so  the torch operators mamba_cpu::* (csrc/torch_ops.cpp), C++
+                     over that C ABI, which the ops modules call.
 
 There is no fallback: if the library is missing or was built for another
 architecture, importing mamba_cpu fails or the first op raises.
@@ -25,6 +29,12 @@ if not os.path.exists(LIB_PATH):
     )
 
 lib = ctypes.CDLL(LIB_PATH)
+
+# The torch operators (mamba_cpu::*), C++ over the same C ABI.
+OPS_PATH = os.path.join(_HERE, "libmamba_torch.so")
+if not os.path.exists(OPS_PATH):
+    raise ImportError(f"mamba_cpu: {OPS_PATH} is not built. Build it with `make -C mamba-cpu_amd`.")
+torch.ops.load_library(OPS_PATH)
 
 MCPU_OK, MCPU_ERR_INVALID, MCPU_ERR_UNSUPPORTED, MCPU_ERR_DEVICE, MCPU_ERR_HIP = range(5)
 MCPU_F32, MCPU_BF16, MCPU_F16 = range(3)

@@ -1,10 +1,12 @@
-"""selective_scan_fn on MI355X: torch.library custom ops over the gfx950 kernels.
+"""selective_scan_fn on MI355X: torch operators over the gfx950 kernels.
 
 Mirrors src/mamba_cpu/ops/selective_scan_interface.py of the reference:
-the same public function, the same custom-op names and schemas
+the same public function, the same operator names and schemas
 (`mamba_cpu::selective_scan_fwd` / `mamba_cpu::selective_scan_bwd`), the same
-autograd wiring and the same exceptions. What changes is the device (ROCm GPU
-tensors instead of CPU tensors) and what the ops accept: besides the
+autograd wiring and the same exceptions. The operators are defined in C++
+(csrc/torch_ops.cpp) over the library's C ABI, so a training step spends no
+Python time below selective_scan_fn. What changes is the device (ROCm GPU
+tensors instead of CPU tensors) and what the operators accept: besides the
 reference's contiguous float32 inputs they take bfloat16/float16 u/delta/z and
 strided views (B/C in the reference's kernel layout or transposed), so
 Hugging Face's transposed projections reach the kernel without copies.
@@ -14,201 +16,19 @@ from typing import Optional
 
 import torch
 
-from mamba_cpu import _C
+from mamba_cpu import _C  # noqa: F401  (loads the operator library)
 
 _X_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
-
-def _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=()):
-    """Rejects what the kernels cannot take, with the reference's exception
-    type (ValueError, selective_scan_interface.py:28-30)."""
-    for t in (u, delta, A, B, C, D, z, delta_bias, *extra):
-        if t is not None and t.device.type != "cuda":
-            raise ValueError(f"{name} runs on ROCm GPU tensors, got a tensor on {t.device}")
-    if u.dtype not in _X_DTYPES or delta.dtype != u.dtype or (z is not None and z.dtype != u.dtype):
-        raise ValueError(f"{name} expects u, delta and z of one dtype among float32, bfloat16 "
-                         f"and float16, got {u.dtype}, {delta.dtype}, {None if z is None else z.dtype}")
-    for t in (A, B, C, D, delta_bias):
-        if t is not None and t.dtype != torch.float32:
-            raise ValueError(f"{name} expects float32 A, B, C, D and delta_bias")
-    if u.dim() != 3 or delta.shape != u.shape or (z is not None and z.shape != u.shape):
-        raise ValueError(f"{name} expects u, delta and z of shape (batch, dim, seqlen)")
-    batch, dim, seqlen = u.shape
-    if A.dim() != 2 or A.shape[0] != dim:
-        raise ValueError(f"{name} expects A of shape (dim, dstate)")
-    dstate = A.shape[1]
-    for X in (B, C):
-        if X.dim() != 4 or X.shape[0] != batch or X.shape[2] != seqlen or X.shape[3] != dstate:
-            raise ValueError(f"{name} expects B and C of shape (batch, ngroups, seqlen, dstate)")
-    if B.shape[1] != C.shape[1] or dim % B.shape[1] != 0:
-        raise ValueError(f"{name}: dim ({dim}) must be divisible by ngroups ({B.shape[1]})")
-    for t in (D, delta_bias):
-        if t is not None and (t.shape != (dim,) or not t.is_contiguous()):
-            raise ValueError(f"{name} expects contiguous D and delta_bias of shape (dim,)")
-    if not A.is_contiguous():
-        raise ValueError(f"{name} expects a contiguous A")
-
-
-def _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
-    a = _C.ScanArgs()
-    batch, dim, seqlen = u.shape
-    a.u, a.delta, a.A = u.data_ptr(), delta.data_ptr(), A.data_ptr()
-    a.B, a.C = B.data_ptr(), C.data_ptr()
-    a.D, a.z, a.delta_bias = _C.ptr(D), _C.ptr(z), _C.ptr(delta_bias)
-    a.batch, a.dim, a.seqlen = batch, dim, seqlen
-    a.dstate, a.ngroups = A.shape[1], B.shape[1]
-    a.delta_softplus = int(bool(delta_softplus))
-    a.dtype = _C.DTYPES[u.dtype]
-    a.u_stride = _C.strides3(u)
-    a.delta_stride = _C.strides3(delta)
-    a.z_stride = _C.strides3(z)
-    a.B_stride = tuple(B.stride())
-    a.C_stride = tuple(C.stride())
-    return a
-
-
-@torch.library.custom_op("mamba_cpu::selective_scan_fwd", mutates_args=(), device_types="cuda")
-def _selective_scan_fwd(
-    u: torch.Tensor,
-    delta: torch.Tensor,
-    A: torch.Tensor,
-    B: torch.Tensor,
-    C: torch.Tensor,
-    D: Optional[torch.Tensor],
-    z: Optional[torch.Tensor],
-    delta_bias: Optional[torch.Tensor],
-    delta_softplus: bool,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """Returns (out in u's dtype, last_state float32 (batch, dim, dstate))."""
-    _validate("mamba_cpu::selective_scan_fwd", u, delta, A, B, C, D, z, delta_bias)
-    batch, dim, _ = u.shape
-    out = u.new_empty(u.shape)
-    last_state = u.new_empty(batch, dim, A.shape[1], dtype=torch.float32)
-    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
-    a.out, a.last_state = out.data_ptr(), last_state.data_ptr()
-    with _C.device_of(u):
-        _C.call(_C.lib.mcpu_selective_scan_fwd, a, "mamba_cpu::selective_scan_fwd", _C.stream_of(u))
-    return out, last_state
-
-
-@_selective_scan_fwd.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
-    return u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32)
-
-
-def _scan_bwd_impl(name, u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state,
-                   ckpt=None, ysave=None):
-    _validate(name, u, delta, A, B, C, D, z, delta_bias, extra=(dout, dlast_state, ckpt, ysave))
-    if dout.shape != u.shape or dout.dtype != u.dtype:
-        raise ValueError(f"{name} expects dout shaped and typed like u")
-    batch, dim, seqlen = u.shape
-    dstate = A.shape[1]
-    if dlast_state is not None:
-        if dlast_state.dtype != torch.float32 or dlast_state.shape != (batch, dim, dstate):
-            raise ValueError(f"{name} expects float32 dlast_state (batch, dim, dstate)")
-        dlast_state = dlast_state.contiguous()
-    if ckpt is not None and (ckpt.dtype != torch.float32 or not ckpt.is_contiguous()
-                             or ckpt.shape != _ckpt_shape(u, A)):
-        raise ValueError(f"{name} expects the float32 checkpoints written by selective_scan_fwd_ckpt")
-    if ysave is not None and ysave.numel() == 0:
-        ysave = None
-    if ysave is not None and (ysave.shape != u.shape or ysave.dtype != u.dtype
-                              or not ysave.is_contiguous() or z is None):
-        raise ValueError(f"{name} expects the y written by selective_scan_fwd_ckpt")
-    du = u.new_empty(u.shape)
-    ddelta = delta.new_empty(delta.shape)
-    dA = A.new_empty(A.shape)
-    dB = B.new_empty(B.shape)
-    dC = C.new_empty(C.shape)
-    dD = A.new_empty(dim)
-    dz = z.new_empty(z.shape) if z is not None else u.new_empty(0)
-    ddelta_bias = A.new_empty(dim)
-    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
-    a.dout, a.dout_stride = dout.data_ptr(), _C.strides3(dout)
-    a.dlast_state = _C.ptr(dlast_state)
-    a.ckpt = _C.ptr(ckpt)
-    a.ysave = _C.ptr(ysave)
-    a.du, a.ddelta, a.dA, a.dB, a.dC = (du.data_ptr(), ddelta.data_ptr(), dA.data_ptr(),
-                                        dB.data_ptr(), dC.data_ptr())
-    a.dD, a.ddelta_bias = dD.data_ptr(), ddelta_bias.data_ptr()
-    a.dz = dz.data_ptr() if z is not None else 0
-    with _C.device_of(u):
-        ws_bytes = _C.lib.mcpu_selective_scan_bwd_workspace_size(a)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=u.device)
-        _C.call(_C.lib.mcpu_selective_scan_bwd, a, name, ws.data_ptr(), ws_bytes, _C.stream_of(u))
-    return du, ddelta, dA, dB, dC, dD, dz, ddelta_bias
-
-
-def _bwd_fake(u, delta, A, B, C, z):
-    dim = u.shape[1]
-    return (
-        u.new_empty(u.shape), delta.new_empty(delta.shape), A.new_empty(A.shape),
-        B.new_empty(B.shape), C.new_empty(C.shape), A.new_empty(dim),
-        z.new_empty(z.shape) if z is not None else u.new_empty(0), A.new_empty(dim),
-    )
-
-
-@torch.library.custom_op("mamba_cpu::selective_scan_bwd", mutates_args=(), device_types="cuda")
-def _selective_scan_bwd(
-    u: torch.Tensor,
-    delta: torch.Tensor,
-    A: torch.Tensor,
-    B: torch.Tensor,
-    C: torch.Tensor,
-    D: Optional[torch.Tensor],
-    z: Optional[torch.Tensor],
-    delta_bias: Optional[torch.Tensor],
-    delta_softplus: bool,
-    dout: torch.Tensor,
-    dlast_state: Optional[torch.Tensor],
-) -> tuple[
-    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-]:
-    """Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias). dz is empty when z
-    is None; dD and ddelta_bias are always computed (as in the reference).
-    Recomputes the forward states it needs from the inputs."""
-    return _scan_bwd_impl("mamba_cpu::selective_scan_bwd", u, delta, A, B, C, D, z, delta_bias,
-                          delta_softplus, dout, dlast_state)
-
-
-@_selective_scan_bwd.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state):
-    return _bwd_fake(u, delta, A, B, C, z)
-
-
-def _setup_context(ctx, inputs, output):
-    u, delta, A, B, C, D, z, delta_bias, delta_softplus = inputs
-    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias)
-    ctx.delta_softplus = delta_softplus
-    ctx.set_materialize_grads(False)
-
-
-def _backward(ctx, grad_out, grad_last_state):
-    u, delta, A, B, C, D, z, delta_bias = ctx.saved_tensors
-    dout = torch.zeros_like(u) if grad_out is None else grad_out.to(u.dtype)
-    dlast = None if grad_last_state is None else grad_last_state.float().contiguous()
-    du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = torch.ops.mamba_cpu.selective_scan_bwd(
-        u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast
-    )
-    return (
-        du, ddelta, dA, dB, dC,
-        dD if D is not None else None,
-        dz if z is not None else None,
-        ddelta_bias if delta_bias is not None else None,
-        None,
-    )
-
-
-torch.library.register_autograd(
-    "mamba_cpu::selective_scan_fwd", _backward, setup_context=_setup_context
-)
-
-
-# Training path: the forward also returns the scan state at the start of every
-# 16-step block and, when z is given, y before the z gate; the backward
-# restarts from those checkpoints and reads y instead of recomputing the
-# states and y from the inputs. Same arithmetic as the pair above.
+# The operators mamba_cpu::selective_scan_fwd / _bwd (the reference's schemas,
+# selective_scan_interface.py:16-97) and the training pair
+# mamba_cpu::selective_scan_fwd_ckpt / _bwd_ckpt are defined in C++
+# (csrc/torch_ops.cpp, loaded by mamba_cpu._C) for ROCm GPU tensors, with their
+# autograd formulas (the reference's :100-124) registered there too. The
+# _ckpt forward also returns the float32 scan state at the start of every
+# 16-step block and, when z is given, y before the z gate; its backward
+# restarts from those instead of recomputing states and y. What follows are
+# their shape functions for FakeTensor tracing (torch.compile, export, opcheck).
 
 _BLOCK_T = 16
 
@@ -218,113 +38,38 @@ def _ckpt_shape(u, A):
     return (batch, dim, (seqlen + _BLOCK_T - 1) // _BLOCK_T, A.shape[1])
 
 
-@torch.library.custom_op("mamba_cpu::selective_scan_fwd_ckpt", mutates_args=(), device_types="cuda")
-def _selective_scan_fwd_ckpt(
-    u: torch.Tensor,
-    delta: torch.Tensor,
-    A: torch.Tensor,
-    B: torch.Tensor,
-    C: torch.Tensor,
-    D: Optional[torch.Tensor],
-    z: Optional[torch.Tensor],
-    delta_bias: Optional[torch.Tensor],
-    delta_softplus: bool,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """selective_scan_fwd that also returns the float32 block checkpoints
-    (batch, dim, ceil(seqlen / 16), dstate) and y before the z gate (u's
-    dtype and shape; empty when z is None) for selective_scan_bwd_ckpt."""
-    name = "mamba_cpu::selective_scan_fwd_ckpt"
-    _validate(name, u, delta, A, B, C, D, z, delta_bias)
-    batch, dim, _ = u.shape
-    out = u.new_empty(u.shape)
-    last_state = u.new_empty(batch, dim, A.shape[1], dtype=torch.float32)
-    ckpt = u.new_empty(_ckpt_shape(u, A), dtype=torch.float32)
-    ysave = u.new_empty(u.shape) if z is not None else u.new_empty(0)
-    a = _scan_args(u, delta, A, B, C, D, z, delta_bias, delta_softplus)
-    a.out, a.last_state, a.ckpt = out.data_ptr(), last_state.data_ptr(), ckpt.data_ptr()
-    a.ysave = ysave.data_ptr() if z is not None else 0
-    with _C.device_of(u):
-        _C.call(_C.lib.mcpu_selective_scan_fwd, a, name, _C.stream_of(u))
-    return out, last_state, ckpt, ysave
+def _fwd_fake(u, A):
+    return u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32)
 
 
-@_selective_scan_fwd_ckpt.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
-    return (u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32),
-            u.new_empty(_ckpt_shape(u, A), dtype=torch.float32),
-            u.new_empty(u.shape) if z is not None else u.new_empty(0))
-
-
-@torch.library.custom_op("mamba_cpu::selective_scan_bwd_ckpt", mutates_args=(), device_types="cuda")
-def _selective_scan_bwd_ckpt(
-    u: torch.Tensor,
-    delta: torch.Tensor,
-    A: torch.Tensor,
-    B: torch.Tensor,
-    C: torch.Tensor,
-    D: Optional[torch.Tensor],
-    z: Optional[torch.Tensor],
-    delta_bias: Optional[torch.Tensor],
-    delta_softplus: bool,
-    dout: torch.Tensor,
-    dlast_state: Optional[torch.Tensor],
-    ckpt: torch.Tensor,
-    ysave: torch.Tensor,
-) -> tuple[
-    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-]:
-    """selective_scan_bwd restarting from the forward's block checkpoints and
-    saved y (pass an empty ysave to recompute y)."""
-    return _scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", u, delta, A, B, C, D, z, delta_bias,
-                          delta_softplus, dout, dlast_state, ckpt, ysave)
-
-
-@_selective_scan_bwd_ckpt.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt, ysave):
-    return _bwd_fake(u, delta, A, B, C, z)
-
-
-def _setup_context_ckpt(ctx, inputs, output):
-    u, delta, A, B, C, D, z, delta_bias, delta_softplus = inputs
-    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[2], output[3])
-    ctx.delta_softplus = delta_softplus
-    ctx.set_materialize_grads(False)
-
-
-def _tracing(*tensors):
-    """True under torch.compile / export / make_fx tracing (fake or
-    functional tensors, or an active dispatch mode), where the backward must
-    call the custom op rather than its body."""
-    return (torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0
-            or any(type(t) is not torch.Tensor for t in tensors))
-
-
-def _backward_ckpt(ctx, grad_out, grad_last_state, grad_ckpt, grad_ysave):
-    u, delta, A, B, C, D, z, delta_bias, ckpt, ysave = ctx.saved_tensors
-    dout = torch.zeros_like(u) if grad_out is None else grad_out.to(u.dtype)
-    dlast = None if grad_last_state is None else grad_last_state.float().contiguous()
-    args = (u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, dout, dlast, ckpt, ysave)
-    if _tracing(u, dout):
-        grads = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args)
-    else:
-        # Eager: the op's body directly, without a second trip through the
-        # dispatcher (the backward runs once per training step; this keeps its
-        # host cost below the kernels' time).
-        grads = _scan_bwd_impl("mamba_cpu::selective_scan_bwd_ckpt", *args)
-    du, ddelta, dA, dB, dC, dD, dz, ddelta_bias = grads
+def _bwd_fake(u, delta, A, B, C, z):
     return (
-        du, ddelta, dA, dB, dC,
-        dD if D is not None else None,
-        dz if z is not None else None,
-        ddelta_bias if delta_bias is not None else None,
-        None,
+        u.new_empty(u.shape), delta.new_empty(delta.shape), A.new_empty(A.shape),
+        B.new_empty(B.shape), C.new_empty(C.shape), A.new_empty(u.shape[1]),
+        z.new_empty(z.shape) if z is not None else u.new_empty(0), A.new_empty(u.shape[1]),
     )
 
 
-torch.library.register_autograd(
-    "mamba_cpu::selective_scan_fwd_ckpt", _backward_ckpt, setup_context=_setup_context_ckpt
-)
+@torch.library.register_fake("mamba_cpu::selective_scan_fwd")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+    return _fwd_fake(u, A)
+
+
+@torch.library.register_fake("mamba_cpu::selective_scan_bwd")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state):
+    return _bwd_fake(u, delta, A, B, C, z)
+
+
+@torch.library.register_fake("mamba_cpu::selective_scan_fwd_ckpt")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+    out, last = _fwd_fake(u, A)
+    return (out, last, u.new_empty(_ckpt_shape(u, A), dtype=torch.float32),
+            u.new_empty(u.shape) if z is not None else u.new_empty(0))
+
+
+@torch.library.register_fake("mamba_cpu::selective_scan_bwd_ckpt")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt, ysave):
+    return _bwd_fake(u, delta, A, B, C, z)
 
 
 def _as_f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
