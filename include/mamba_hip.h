@@ -109,9 +109,18 @@ typedef struct mcpu_scan_args {
  * inputs and ckpt != NULL reads it instead of recomputing it. */
 size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a);
 
+/* Workspace bytes that let mcpu_selective_scan_fwd cut the sequence into
+ * chunks scanned in parallel (0 when the rows alone fill the GPU). */
+size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a);
+
 /* Forward. Replaces selective_scan_fwd_f32 (csrc/selective_scan.h:40) as bound
- * by _C.selective_scan_fwd_f32 (csrc/bindings.cpp:23-45). */
-int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* stream);
+ * by _C.selective_scan_fwd_f32 (csrc/bindings.cpp:23-45). With a workspace of
+ * at least mcpu_selective_scan_fwd_workspace_size() bytes, short batches of
+ * long sequences are scanned in parallel time chunks; with NULL (or a smaller
+ * one) the sequence is scanned in one pass. Results agree within float32
+ * rounding either way. */
+int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* Workspace bytes needed by mcpu_selective_scan_bwd for these arguments. */
 size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);

@@ -9,6 +9,7 @@
 
 namespace mcpu {
 int scan_fwd_waves();
+void scan_fwd_chunks(ScanParams& p);
 int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
@@ -89,7 +90,23 @@ ScanParams make_params(const mcpu_scan_args* a, int waves) {
     p.sC[i] = a->C_stride[i];
   }
   p.softplus = a->delta_softplus != 0;
+  p.nchunk = 1;
+  p.chunk_blocks = p.nblk > 0 ? p.nblk : 1;
   return p;
+}
+
+// Workspace of a chunked forward: chunk-end states and chunk sums of dt.
+struct FwdLayout {
+  size_t sum_h = 0, sum_dt = 0, total = 0;
+};
+
+FwdLayout fwd_layout(const ScanParams& p) {
+  FwdLayout w;
+  if (p.nchunk <= 1) return w;
+  w.sum_h = 0;
+  w.sum_dt = align_up(sizeof(float) * p.batch * p.dim * p.nchunk * p.dstate);
+  w.total = w.sum_dt + align_up(sizeof(float) * p.batch * p.dim * p.nchunk);
+  return w;
 }
 
 int bwd_waves(const mcpu_scan_args* a) {
@@ -137,12 +154,34 @@ extern "C" size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a) {
   return sizeof(float) * a->batch * a->dim * nblk * a->dstate;
 }
 
-extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* stream) {
+extern "C" size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a) {
+  if (check_scan(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  ScanParams p = make_params(a, scan_fwd_waves());
+  scan_fwd_chunks(p);
+  return fwd_layout(p).total;
+}
+
+extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_scan(a)) return rc;
   if (int rc = mcpu_check_device()) return rc;
   if (a->batch == 0 || a->dim == 0) return MCPU_OK;
   ScanParams p = make_params(a, scan_fwd_waves());
+  scan_fwd_chunks(p);
+  const FwdLayout w = fwd_layout(p);
+  if (p.nchunk > 1 && workspace != nullptr && workspace_bytes >= w.total) {
+    char* ws = static_cast<char*>(workspace);
+    p.sum_h = reinterpret_cast<float*>(ws + w.sum_h);
+    p.sum_dt = reinterpret_cast<float*>(ws + w.sum_dt);
+  } else {
+    // Without the workspace the sequence is scanned in one chunk.
+    p.nchunk = 1;
+    p.chunk_blocks = p.nblk > 0 ? p.nblk : 1;
+  }
   p.out = a->out;
   p.last_state = a->last_state;
   p.ckpt = a->ckpt;

@@ -46,7 +46,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, wave, r);
+  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
   const int64_t kl = p.nblk - 1;  // last block

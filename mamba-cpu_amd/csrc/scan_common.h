@@ -58,6 +58,14 @@ struct ScanParams {
   int64_t su[3], sdl[3], sz[3], sdo[3];
   int64_t sB[4], sC[4];
   int softplus;
+  // Time chunks: the sequence is cut into nchunk chunks of chunk_blocks
+  // 16-step blocks, scanned in parallel; chunk c starts from the state carried
+  // over chunks 0..c-1 through their summaries (state at the chunk end when
+  // started from zero, and the chunk's sum of dt).
+  int64_t nchunk;        // 1 = unchunked
+  int64_t chunk_blocks;
+  float* sum_h;          // (batch, dim, nchunk, dstate)
+  float* sum_dt;         // (batch, dim, nchunk)
 };
 
 struct RowCtx {
@@ -67,9 +75,9 @@ struct RowCtx {
   bool active;         // this row's channel exists (rows past the slice end are padding)
 };
 
+// bid: the workgroup's index over (batch, group, channel block).
 template <int W>
-__device__ __forceinline__ RowCtx scan_row_ctx(const ScanParams& p, int wave, int r) {
-  int64_t bid = blockIdx.x;
+__device__ __forceinline__ RowCtx scan_row_ctx(const ScanParams& p, int64_t bid, int wave, int r) {
   RowCtx c;
   c.cblk = bid % p.nblk_c;
   bid /= p.nblk_c;

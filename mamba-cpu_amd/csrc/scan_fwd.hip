@@ -12,14 +12,26 @@
 // computes (double-buffered LDS). Optional outputs: the final state, the state
 // at the start of every block (checkpoints for the backward), and y before the
 // z gate (lets the backward skip recomputing it).
+//
+// Time chunks (when there are too few rows to fill the GPU): a summary pass
+// scans every chunk but the last from a zero state and records the state at
+// its end and its sum of dt; the main pass then starts chunk c from
+//   h = fold over c' < c of  exp(A * sum_dt[c']) * h + h_end[c']
+// (the recurrence is affine in h, and the decay over a chunk is the product of
+// the per-step decays, exp(A * sum of dt)).
 #include "scan_common.h"
 
 namespace mcpu {
 
 constexpr int kFwdWaves = 4;
 
-template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT>
+// MODE: outputs (out, optional ysave / ckpt / last_state), states only
+// (ckpt / last_state), or the chunk summaries of the chunked scan.
+enum FwdMode { kFwdOut = 0, kFwdStates = 1, kFwdSummary = 2 };
+
+template <typename Tx, int SPL, bool HAS_Z, int MODE>
 __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanParams p) {
+  constexpr bool WRITE_OUT = MODE == kFwdOut;
   constexpr int W = kFwdWaves;
   constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
@@ -34,9 +46,14 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, wave, r);
+  const int64_t chunk = blockIdx.x % p.nchunk;
+  // The summary pass has nothing to record for the last chunk.
+  if (MODE == kFwdSummary && chunk == p.nchunk - 1) return;
+  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
+  const int64_t kb0 = chunk * p.chunk_blocks;  // this chunk's blocks: [kb0, kb1)
+  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
 
   float A2[SPL], h[SPL];
 #pragma unroll
@@ -45,17 +62,32 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     A2[s] = n < N ? p.A[rc.d * N + n] * kLog2e : 0.f;
     h[s] = 0.f;
   }
+  if (MODE != kFwdSummary && chunk > 0) {
+    // Carry the state over the chunks before this one.
+    const float* sh = p.sum_h + row * p.nchunk * N;
+    const float* sd = p.sum_dt + row * p.nchunk;
+    for (int64_t c = 0; c < chunk; ++c) {
+      const float ds = sd[c];
+#pragma unroll
+      for (int s = 0; s < SPL; ++s) {
+        const int n = j + 16 * s;
+        if (n < N) h[s] = fmaf(fast_exp2(A2[s] * ds), h[s], sh[c * N + n]);
+      }
+    }
+  }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
-  float* ck = p.ckpt ? p.ckpt + row * p.nblk * N : nullptr;
+  float* ck = (MODE != kFwdSummary && p.ckpt) ? p.ckpt + row * p.nblk * N : nullptr;
+  float dts = 0.f;  // sum of dt over this lane's steps (summary pass)
 
+  const int64_t tb0 = kb0 * kScanBlockT;
   XStage<W> xu, xd, xz;
-  xu.template init<Tx>(tid, p.u, p.su, p, rc, 0);
-  xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, 0);
-  if (HAS_Z && WRITE_OUT) xz.template init<Tx>(tid, p.z, p.sz, p, rc, 0);
+  xu.template init<Tx>(tid, p.u, p.su, p, rc, tb0);
+  xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, tb0);
+  if (HAS_Z && WRITE_OUT) xz.template init<Tx>(tid, p.z, p.sz, p, rc, tb0);
   BC tb, tc;
-  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, 0);
-  if (WRITE_OUT) tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, 0);
+  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, tb0);
+  if (WRITE_OUT) tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, tb0);
   // Only the last block can extend past the sequence end.
   const int64_t t_full = L - L % kScanBlockT;
 
@@ -90,9 +122,9 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     if (WRITE_OUT) tc.park(s_C[buf], nC);
   };
 
-  if (p.nblk > 0) {
-    fetch(0);
-    park(0);
+  if (kb0 < kb1) {
+    fetch(tb0);
+    park(static_cast<int>(kb0 & 1));
   }
   __syncthreads();
   // Retire every load issued so far. Otherwise the loop's first use of a
@@ -100,19 +132,19 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // operations at the top of every block, which would also wait for the
   // prefetch of the next block.
   __builtin_amdgcn_s_waitcnt(0);
-  if (ck != nullptr && rc.active && p.nblk > 0) {
+  if (ck != nullptr && rc.active && kb0 < kb1) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) ck[j + 16 * s] = 0.f;
+      if (j + 16 * s < N) ck[kb0 * N + j + 16 * s] = h[s];
   }
 
   // Per block: prefetch the next block, compute this one, park the prefetch,
   // then store. Stores come last so that waiting for the prefetched loads
   // never waits for this block's stores as well.
-  for (int64_t k = 0; k < p.nblk; ++k) {
+  for (int64_t k = kb0; k < kb1; ++k) {
     const int buf = static_cast<int>(k & 1);
     const int64_t t0 = k * kScanBlockT;
-    if (k + 1 < p.nblk) fetch(t0 + kScanBlockT);
+    if (k + 1 < kb1) fetch(t0 + kScanBlockT);
 
     const int64_t t = t0 + j;
     const bool tv = t < L;
@@ -131,6 +163,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     float dt = dl + bias;
     if (p.softplus) dt = softplus(dt);
     const float dtu = dt * uu;
+    if (MODE == kFwdSummary && tv) dts += dt;
 
     float pacc[kScanBlockT];
     auto step = [&](auto I) {
@@ -162,39 +195,50 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       yg = HAS_Z ? y * (zz * sigmoid(zz)) : y;
     }
 
-    if (k + 1 < p.nblk) park(buf ^ 1);
+    if (k + 1 < kb1) park(buf ^ 1);
 
     if (WRITE_OUT && tv && rc.active) {
       if (p.ysave != nullptr) st<Tx>(p.ysave, row * L + t, y);
       st<Tx>(p.out, row * L + t, yg);
     }
-    if (ck != nullptr && rc.active && k + 1 < p.nblk) {
+    if (ck != nullptr && rc.active && k + 1 < kb1) {
 #pragma unroll
       for (int s = 0; s < SPL; ++s)
         if (j + 16 * s < N) ck[(k + 1) * N + j + 16 * s] = h[s];
     }
     __syncthreads();
   }
-  if (p.last_state != nullptr && rc.active) {
+  if (MODE == kFwdSummary) {
+    dts = row_allreduce16(dts);
+    if (rc.active) {
+#pragma unroll
+      for (int s = 0; s < SPL; ++s)
+        if (j + 16 * s < N) p.sum_h[(row * p.nchunk + chunk) * N + j + 16 * s] = h[s];
+      if (j == 0) p.sum_dt[row * p.nchunk + chunk] = dts;
+    }
+  } else if (p.last_state != nullptr && rc.active && kb1 == p.nblk) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
       if (j + 16 * s < N) p.last_state[row * N + j + 16 * s] = h[s];
   }
 }
 
-template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT>
+template <typename Tx, int SPL, bool HAS_Z, int MODE>
 static hipError_t launch_fwd(const ScanParams& p, hipStream_t stream) {
-  const int64_t blocks = p.batch * p.ngroups * p.nblk_c;
-  hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, WRITE_OUT>), dim3(static_cast<unsigned>(blocks)),
+  const int64_t blocks = p.batch * p.ngroups * p.nblk_c * p.nchunk;
+  hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, MODE>), dim3(static_cast<unsigned>(blocks)),
                      dim3(64 * kFwdWaves), 0, stream, p);
   return hipGetLastError();
 }
 
 template <typename Tx, int SPL>
 static hipError_t dispatch_fwd_flags(const ScanParams& p, bool write_out, hipStream_t stream) {
-  if (!write_out) return launch_fwd<Tx, SPL, false, false>(p, stream);
-  if (p.z != nullptr) return launch_fwd<Tx, SPL, true, true>(p, stream);
-  return launch_fwd<Tx, SPL, false, true>(p, stream);
+  if (p.nchunk > 1) {
+    if (hipError_t e = launch_fwd<Tx, SPL, false, kFwdSummary>(p, stream)) return e;
+  }
+  if (!write_out) return launch_fwd<Tx, SPL, false, kFwdStates>(p, stream);
+  if (p.z != nullptr) return launch_fwd<Tx, SPL, true, kFwdOut>(p, stream);
+  return launch_fwd<Tx, SPL, false, kFwdOut>(p, stream);
 }
 
 template <typename Tx>
@@ -205,6 +249,21 @@ static hipError_t dispatch_fwd_spl(const ScanParams& p, bool write_out, hipStrea
 }
 
 int scan_fwd_waves() { return kFwdWaves; }
+
+// Time chunks for a forward with these parameters (p.nblk_c set for
+// scan_fwd_waves()): enough chunks to give the GPU's 256 compute units about
+// four workgroups each, at least two 16-step blocks per chunk. Sets
+// p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone fill the GPU.
+void scan_fwd_chunks(ScanParams& p) {
+  const int64_t wgs = p.batch * p.ngroups * p.nblk_c;
+  int64_t n = 1;
+  if (wgs > 0 && wgs < 512 && p.nblk >= 4) {
+    n = (1024 + wgs - 1) / wgs;
+    if (n > p.nblk / 2) n = p.nblk / 2;
+  }
+  p.chunk_blocks = n > 1 ? (p.nblk + n - 1) / n : (p.nblk > 0 ? p.nblk : 1);
+  p.nchunk = n > 1 ? (p.nblk + p.chunk_blocks - 1) / p.chunk_blocks : 1;
+}
 
 // Launches the forward kernel (p.nblk_c must be computed for scan_fwd_waves()).
 // write_out = false computes states only (checkpoints and/or last_state),

@@ -8,7 +8,8 @@
 // bodies check their arguments (ValueError / NotImplementedError, as the
 // reference raises), allocate outputs and workspaces through the torch caching
 // allocator and launch on the current stream; they never synchronise.
-// Fake (meta) implementations are registered from Python (mamba_cpu/_ops.py).
+// Fake (meta) implementations are registered from Python, next to the public
+// functions (mamba_cpu/ops/*.py).
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -169,7 +170,12 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> scan_fwd_impl(
     a.ckpt = static_cast<float*>(ckpt.data_ptr());
     a.ysave = has(z) ? ysave.data_ptr() : nullptr;
   }
-  check_rc(mcpu_selective_scan_fwd(&a, stream_of(u)), name);
+  const size_t ws_bytes = mcpu_selective_scan_fwd_workspace_size(&a);
+  Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({static_cast<int64_t>(ws_bytes)}, u.options().dtype(at::kByte));
+  check_rc(mcpu_selective_scan_fwd(&a, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                                   stream_of(u)),
+           name);
   return {out, last, ckpt, ysave};
 }
 

@@ -107,7 +107,9 @@ lib.mcpu_args_size.argtypes = [ctypes.c_char_p]
 lib.mcpu_args_size.restype = ctypes.c_size_t
 lib.mcpu_selective_scan_ckpt_size.argtypes = [_ARGP["scan"]]
 lib.mcpu_selective_scan_ckpt_size.restype = ctypes.c_size_t
-lib.mcpu_selective_scan_fwd.argtypes = [_ARGP["scan"], _P]
+lib.mcpu_selective_scan_fwd_workspace_size.argtypes = [_ARGP["scan"]]
+lib.mcpu_selective_scan_fwd_workspace_size.restype = ctypes.c_size_t
+lib.mcpu_selective_scan_fwd.argtypes = [_ARGP["scan"], _P, ctypes.c_size_t, _P]
 lib.mcpu_selective_scan_fwd.restype = ctypes.c_int
 lib.mcpu_selective_scan_bwd_workspace_size.argtypes = [_ARGP["scan"]]
 lib.mcpu_selective_scan_bwd_workspace_size.restype = ctypes.c_size_t

@@ -30,6 +30,7 @@ def test_header_declares_the_entry_points():
     names = declared_functions()
     for want in ("mcpu_selective_scan_fwd", "mcpu_selective_scan_bwd",
                  "mcpu_selective_scan_bwd_workspace_size", "mcpu_selective_scan_ckpt_size",
+                 "mcpu_selective_scan_fwd_workspace_size",
                  "mcpu_causal_conv1d_fwd", "mcpu_causal_conv1d_bwd",
                  "mcpu_causal_conv1d_bwd_workspace_size", "mcpu_causal_conv1d_update",
                  "mcpu_selective_state_update", "mcpu_last_error", "mcpu_version",
@@ -115,22 +116,22 @@ def test_scan_rejects_bad_arguments_before_touching_a_device():
     from mamba_cpu import _C
 
     L = _C.lib
-    assert _rc(L.mcpu_selective_scan_fwd, None, None)[0] == _C.MCPU_ERR_INVALID
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(u=None)), None)
+    assert _rc(L.mcpu_selective_scan_fwd, None, None, 0, None)[0] == _C.MCPU_ERR_INVALID
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(u=None)), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "required" in msg
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=65)), None)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=65)), None, 0, None)
     assert rc == _C.MCPU_ERR_UNSUPPORTED and "dstate" in msg
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(ngroups=3)), None)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(ngroups=3)), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "ngroups" in msg
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dtype=7)), None)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dtype=7)), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "dtype" in msg
     a = _scan_args()
     a.u_stride[1] = -1
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "stride" in msg
     a = _scan_args()
     a.u_stride[1] = 1 << 40  # tile offsets would not fit 32 bits
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(a), None, 0, None)
     assert rc == _C.MCPU_ERR_UNSUPPORTED and "32-bit" in msg
     # backward: required outputs
     rc, msg = _rc(L.mcpu_selective_scan_bwd, ctypes.byref(_scan_args()), None, 0, None)
@@ -145,6 +146,10 @@ def test_scan_sizes():
     assert _C.lib.mcpu_selective_scan_ckpt_size(ctypes.byref(a)) == 4 * 2 * 8 * 3 * 16
     assert _C.lib.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a)) > 0
     assert _C.lib.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(dstate=0))) == 0
+    # forward chunk workspace: none when the rows fill the GPU, some for one long row
+    assert _C.lib.mcpu_selective_scan_fwd_workspace_size(ctypes.byref(_scan_args(batch=64, dim=4096))) == 0
+    assert _C.lib.mcpu_selective_scan_fwd_workspace_size(
+        ctypes.byref(_scan_args(batch=1, dim=64, seqlen=4096))) > 0
 
 
 def test_scan_without_gfx950_reports_the_device():
@@ -153,7 +158,7 @@ def test_scan_without_gfx950_reports_the_device():
 
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
-    rc, msg = _rc(_C.lib.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(out=32)), None)
+    rc, msg = _rc(_C.lib.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(out=32)), None, 0, None)
     assert rc in (_C.MCPU_ERR_DEVICE, _C.MCPU_ERR_HIP)
     assert msg
 
