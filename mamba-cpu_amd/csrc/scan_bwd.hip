@@ -118,13 +118,24 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   float nu = 0.f, nd = 0.f, no = 0.f, nz = 0.f, ny = 0.f;
   float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
   float nh0[SPL];
+  // Checkpointed state lanes past dstate load lane 0's entry and read as 0.
+  uint32_t ck_lane[SPL];
+  bool ck_ok[SPL];
+#pragma unroll
+  for (int s = 0; s < SPL; ++s) {
+    ck_ok[s] = j + 16 * s < N;
+    ck_lane[s] = ck_ok[s] ? ck_off + 64 * s : ck_off - sizeof(float) * j;
+  }
   // Loads the operands of the block at t0 (full unless GUARD) and moves every
-  // cursor one block back.
-  auto fetch = [&](auto GUARD, int64_t t0) {
+  // cursor one block back, except from block 0 (`stay`). Every iteration
+  // fetches, block 0 re-reading itself, and nothing consumes a prefetched
+  // value before park(), so no load is conditional and the loads are only
+  // waited for at the park.
+  auto fetch = [&](auto GUARD, int64_t t0, bool stay) {
     if constexpr (decltype(GUARD)::value) {
       nu = xu.template load_guarded<Tx>(t0, L);
       nd = xd.template load_guarded<Tx>(t0, L);
-      no = has_dout ? xo.template load_guarded<Tx>(t0, L) : 0.f;
+      no = xo.template load_guarded<Tx>(t0, L);
       if (HAS_Z) nz = xz.template load_guarded<Tx>(t0, L);
       if (HAS_Y) ny = xy.template load_guarded<Tx>(t0, L);
       tb.load_guarded(t0, L, nB);
@@ -132,28 +143,27 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     } else {
       nu = xu.template load<Tx>();
       nd = xd.template load<Tx>();
-      no = has_dout ? xo.template load<Tx>() : 0.f;
+      no = xo.template load<Tx>();
       if (HAS_Z) nz = xz.template load<Tx>();
       if (HAS_Y) ny = xy.template load<Tx>();
       tb.load(nB);
       tc.load(nC);
     }
 #pragma unroll
-    for (int s = 0; s < SPL; ++s)
-      nh0[s] = (j + 16 * s < N) ? *reinterpret_cast<const float*>(ck_base + ck_off + 64 * s) : 0.f;
-    xu.advance(-1);
-    xd.advance(-1);
-    xo.advance(-1);
-    if (HAS_Z) xz.advance(-1);
-    if (HAS_Y) xy.advance(-1);
-    tb.advance(-1);
-    tc.advance(-1);
-    ck_base -= sizeof(float) * N;
+    for (int s = 0; s < SPL; ++s) nh0[s] = *reinterpret_cast<const float*>(ck_base + ck_lane[s]);
+    xu.advance_unless(-1, stay);
+    xd.advance_unless(-1, stay);
+    xo.advance_unless(-1, stay);
+    if (HAS_Z) xz.advance_unless(-1, stay);
+    if (HAS_Y) xy.advance_unless(-1, stay);
+    tb.advance_unless(-1, stay);
+    tc.advance_unless(-1, stay);
+    ck_base -= stay ? 0 : sizeof(float) * N;
   };
   auto park = [&](int buf) {
     (&s_x[buf][0][0][0])[xu.slot] = nu;
     (&s_x[buf][1][0][0])[xd.slot] = nd;
-    (&s_x[buf][2][0][0])[xo.slot] = no;
+    (&s_x[buf][2][0][0])[xo.slot] = has_dout ? no : 0.f;
     if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = nz;
     if (HAS_Y) (&s_x[buf][4][0][0])[xy.slot] = ny;
     tb.park(s_B[buf], nB);
@@ -162,10 +172,10 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
 
   float h0[SPL];
   if (p.nblk > 0) {
-    fetch(std::true_type{}, t_last);
+    fetch(std::true_type{}, t_last, kl == 0);
     park(static_cast<int>(kl & 1));
 #pragma unroll
-    for (int s = 0; s < SPL; ++s) h0[s] = nh0[s];
+    for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
   }
   __syncthreads();
   // Retire every load issued so far, so the loop never has to wait for the
@@ -177,7 +187,10 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     constexpr bool full = decltype(FULL)::value;
     const int buf = static_cast<int>(k & 1);
     const int64_t t0 = k * T;
-    if (k > 0) fetch(std::false_type{}, t0 - T);
+    // The block before this one (always full), or this block again from
+    // block 0 (guarded like this block).
+    if (k > 0) fetch(std::false_type{}, t0 - T, k <= 1);
+    else fetch(std::integral_constant<bool, !full>{}, t0, true);
     auto valid = [&](int i) { return full || i < nvalid; };
 
     const bool tv = full || j < nvalid;
@@ -298,11 +311,9 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
         s_red[buf][1][wave][4 * r + q][j + 16 * s] = yC[q];
       }
     }
-    if (k > 0) {
-      park(buf ^ 1);
+    park(buf ^ 1);  // from block 0 a harmless copy into the idle buffer
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) h0[s] = nh0[s];
-    }
+    for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
     // Stores after the park, so waiting for the prefetch never waits for them.
     if (tv && rc.active) {
       *reinterpret_cast<Tx*>(o_du + o_off) = from_f32<Tx>(duv);

@@ -128,12 +128,20 @@ struct XStage {
   __device__ __forceinline__ float load() const {
     return to_f32(*reinterpret_cast<const Tx*>(base + off));
   }
-  // For a block that may extend past the sequence end.
+  // For a block that may extend past the sequence end: steps past the end
+  // load the tile's first element (always in range) and read as 0. The load
+  // itself is unconditional, so no prefetch register is written under a
+  // lane mask (which would make the compiler drain every outstanding memory
+  // operation before reusing it).
   template <typename Tx>
   __device__ __forceinline__ float load_guarded(int64_t t0, int64_t L) const {
-    return t0 + t < L ? load<Tx>() : 0.f;
+    const bool ok = t0 + t < L;
+    const float x = to_f32(*reinterpret_cast<const Tx*>(base + (ok ? off : 0u)));
+    return ok ? x : 0.f;
   }
   __device__ __forceinline__ void advance(int dir) { base += dir * step; }
+  // Moves one block in direction dir unless `stay` (uniform).
+  __device__ __forceinline__ void advance_unless(int dir, bool stay) { base += stay ? 0 : dir * step; }
 };
 
 // B or C rows of one block, parked transposed as [n][t] (padded) so a lane
@@ -170,21 +178,30 @@ struct BCStage {
     base = reinterpret_cast<const char*>(row + t0 * s[2]);
     step = static_cast<int64_t>(sizeof(float)) * kScanBlockT * s[2];
   }
+  // Unconditional loads: elements outside the tile load the row's first
+  // element (off = 0) and are zeroed by park(), after the block's compute, so
+  // nothing consumes a prefetched value before then.
   __device__ __forceinline__ void load(float (&v)[PER_THREAD]) const {
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i)
-      v[i] = ok[i] ? *reinterpret_cast<const float*>(base + off[i]) : 0.f;
+    for (int i = 0; i < PER_THREAD; ++i) v[i] = *reinterpret_cast<const float*>(base + off[i]);
   }
+  // Also zeroes the steps past the sequence end (see XStage::load_guarded).
+  // Used for the sequence's last block only.
   __device__ __forceinline__ void load_guarded(int64_t t0, int64_t L, float (&v)[PER_THREAD]) const {
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i)
-      v[i] = (ok[i] && t0 + t[i] < L) ? *reinterpret_cast<const float*>(base + off[i]) : 0.f;
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const bool in = ok[i] && t0 + t[i] < L;
+      const float x = *reinterpret_cast<const float*>(base + (in ? off[i] : 0u));
+      v[i] = in ? x : 0.f;
+    }
   }
   __device__ __forceinline__ void advance(int dir) { base += dir * step; }
+  __device__ __forceinline__ void advance_unless(int dir, bool stay) { base += stay ? 0 : dir * step; }
   __device__ __forceinline__ void park(float (*tile)[kBCPad], const float (&v)[PER_THREAD]) const {
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i)
-      if (PER_THREAD * 64 * W == kScanBlockT * NW || slot[i] >= 0) (&tile[0][0])[slot[i]] = v[i];
+      if (PER_THREAD * 64 * W == kScanBlockT * NW || slot[i] >= 0)
+        (&tile[0][0])[slot[i]] = ok[i] ? v[i] : 0.f;
   }
 };
 

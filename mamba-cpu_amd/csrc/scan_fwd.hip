@@ -94,7 +94,11 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // Registers holding the next block's operands between fetch and park.
   float nu = 0.f, nd = 0.f, nz = 0.f;
   float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
-  auto fetch = [&](int64_t t0) {
+  // Loads the block at t0 and moves the cursors to the next block, except
+  // from the chunk's last block (`last`), where they stay: the loop fetches
+  // in every iteration, the last one re-reading its own block, so no load or
+  // park is ever conditional.
+  auto fetch = [&](int64_t t0, bool last) {
     if (t0 < t_full) {
       nu = xu.template load<Tx>();
       nd = xd.template load<Tx>();
@@ -108,11 +112,11 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       tb.load_guarded(t0, L, nB);
       if (WRITE_OUT) tc.load_guarded(t0, L, nC);
     }
-    xu.advance(1);
-    xd.advance(1);
-    if (HAS_Z && WRITE_OUT) xz.advance(1);
-    tb.advance(1);
-    if (WRITE_OUT) tc.advance(1);
+    xu.advance_unless(1, last);
+    xd.advance_unless(1, last);
+    if (HAS_Z && WRITE_OUT) xz.advance_unless(1, last);
+    tb.advance_unless(1, last);
+    if (WRITE_OUT) tc.advance_unless(1, last);
   };
   auto park = [&](int buf) {
     (&s_x[buf][0][0][0])[xu.slot] = nu;
@@ -123,7 +127,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   };
 
   if (kb0 < kb1) {
-    fetch(tb0);
+    fetch(tb0, kb0 + 1 >= kb1);
     park(static_cast<int>(kb0 & 1));
   }
   __syncthreads();
@@ -144,7 +148,8 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   for (int64_t k = kb0; k < kb1; ++k) {
     const int buf = static_cast<int>(k & 1);
     const int64_t t0 = k * kScanBlockT;
-    if (k + 1 < kb1) fetch(t0 + kScanBlockT);
+    const bool has_next = k + 1 < kb1;
+    fetch(has_next ? t0 + kScanBlockT : t0, k + 2 >= kb1);
 
     const int64_t t = t0 + j;
     const bool tv = t < L;
@@ -195,7 +200,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       yg = HAS_Z ? y * (zz * sigmoid(zz)) : y;
     }
 
-    if (k + 1 < kb1) park(buf ^ 1);
+    park(buf ^ 1);  // in the last iteration a harmless copy into the idle buffer
 
     if (WRITE_OUT && tv && rc.active) {
       if (p.ysave != nullptr) st<Tx>(p.ysave, row * L + t, y);
