@@ -56,6 +56,13 @@ int check_scan(const mcpu_scan_args* a) {
   for (int64_t sp : spans)
     if (sp >= 0xffffffffll)
       return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: strides or sizes too large for 32-bit tile offsets");
+  // The staging cursors move by one 16-step block as a signed 32-bit byte step.
+  const int64_t steps[] = {esz * kScanBlockT * a->u_stride[2], esz * kScanBlockT * a->delta_stride[2],
+                           esz * kScanBlockT * a->z_stride[2], esz * kScanBlockT * a->dout_stride[2],
+                           4 * kScanBlockT * a->B_stride[2], 4 * kScanBlockT * a->C_stride[2]};
+  for (int64_t st : steps)
+    if (st > 0x7fffffffll)
+      return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: time stride too large for 32-bit block steps");
   return MCPU_OK;
 }
 

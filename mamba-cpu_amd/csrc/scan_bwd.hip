@@ -210,6 +210,11 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     float dt = pre, sg_pre = 1.f;
     if (softplus_on) dt = softplus_sigmoid(pre, sg_pre);
     const float dtu = dt * uu;
+    // The reverse pass broadcasts its own copies of dt and dt*u: the compiler
+    // folds a DPP broadcast into its multiplies only when they follow it
+    // closely, so one broadcast shared by the recompute and the reverse pass
+    // (which identical values would be merged into) costs a move per step.
+    const float dt_r = dt + 0.0f, dtu_r = dtu + 0.0f;
 
     // Forward recompute of the block's states and decay factors.
     float hs[SPL][T], as[SPL][T], pacc[T];
@@ -261,8 +266,8 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
       constexpr int i = T - 1 - decltype(I)::value;
       if (valid(i)) {
         const float dyi = row_bcast<i>(dy);
-        const float dti = row_bcast<i>(dt);
-        const float dtui = row_bcast<i>(dtu);
+        const float dti = row_bcast<i>(dt_r);
+        const float dtui = row_bcast<i>(dtu_r);
         float acc1 = 0.f, acc2 = 0.f;
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {

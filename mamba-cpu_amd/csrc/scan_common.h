@@ -100,7 +100,7 @@ __device__ __forceinline__ RowCtx scan_row_ctx(const ScanParams& p, int64_t bid,
 template <int W>
 struct XStage {
   const char* base;  // uniform: element (batch, first channel of the workgroup, t0)
-  int64_t step;      // uniform: bytes per block
+  int32_t step;      // uniform: bytes per block (|16 * time stride| fits the 32-bit tile offsets)
   uint32_t off;      // per thread: byte offset of its element from base
   int slot;          // per thread: index c * 16 + t of its element in the LDS tile
   int t;             // per thread: its step within the block
@@ -122,7 +122,7 @@ struct XStage {
     base = static_cast<const char*>(p_base) +
            sz * (rc.b * s[0] + (rc.g * p.dpg + rc.cl0) * s[1] + t0 * s[2]);
     off = static_cast<uint32_t>(sz * (ce * s[1] + t * s[2]));
-    step = sz * kScanBlockT * s[2];
+    step = static_cast<int32_t>(sz * kScanBlockT * s[2]);
   }
   template <typename Tx>
   __device__ __forceinline__ float load() const {
@@ -152,7 +152,7 @@ struct BCStage {
   static constexpr int NW = 16 * SPL;
   static constexpr int PER_THREAD = (kScanBlockT * NW + 64 * W - 1) / (64 * W);
   const char* base;  // uniform
-  int64_t step;      // uniform: bytes per block
+  int32_t step;      // uniform: bytes per block
   uint32_t off[PER_THREAD];
   int slot[PER_THREAD];  // n * kBCPad + t in the LDS tile, or -1 past the tile
   int t[PER_THREAD];
@@ -176,7 +176,7 @@ struct BCStage {
       off[i] = ok[i] ? static_cast<uint32_t>(sizeof(float) * (t[i] * s[2] + n * s[3])) : 0u;
     }
     base = reinterpret_cast<const char*>(row + t0 * s[2]);
-    step = static_cast<int64_t>(sizeof(float)) * kScanBlockT * s[2];
+    step = static_cast<int32_t>(sizeof(float) * kScanBlockT * s[2]);
   }
   // Unconditional loads: elements outside the tile load the row's first
   // element (off = 0) and are zeroed by park(), after the block's compute, so
