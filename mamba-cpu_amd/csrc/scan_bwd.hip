@@ -385,25 +385,44 @@ struct ReduceJobs {
   int njobs;
 };
 
+// The terms are loaded eight at a time (eight loads in flight instead of a
+// load-add chain) and added in the same fixed order c = 0, 1, ...
 __device__ __forceinline__ void reduce_item(const ReduceJob& j, int64_t i) {
+  constexpr int U = 8;
   if (j.vec == 4) {
     const int64_t per4 = j.per / 4;
     const int64_t sl = i / per4, e = (i % per4) * 4;
     const float* src = j.part + sl * j.nsum * j.per + e;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int64_t c = 0; c < j.nsum; ++c) {
-      const float4 v = *reinterpret_cast<const float4*>(src + c * j.per);
+    auto add = [&](const float4 v) {
       acc.x += v.x;
       acc.y += v.y;
       acc.z += v.z;
       acc.w += v.w;
+    };
+    int64_t c = 0;
+    for (; c + U <= j.nsum; c += U) {
+      float4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = *reinterpret_cast<const float4*>(src + (c + u) * j.per);
+#pragma unroll
+      for (int u = 0; u < U; ++u) add(v[u]);
     }
+    for (; c < j.nsum; ++c) add(*reinterpret_cast<const float4*>(src + c * j.per));
     *reinterpret_cast<float4*>(j.out + sl * j.per + e) = acc;
   } else {
     const int64_t sl = i / j.per, e = i % j.per;
     const float* src = j.part + sl * j.nsum * j.per + e;
     float acc = 0.f;
-    for (int64_t c = 0; c < j.nsum; ++c) acc += src[c * j.per];
+    int64_t c = 0;
+    for (; c + U <= j.nsum; c += U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = src[(c + u) * j.per];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += v[u];
+    }
+    for (; c < j.nsum; ++c) acc += src[c * j.per];
     j.out[sl * j.per + e] = acc;
   }
 }
