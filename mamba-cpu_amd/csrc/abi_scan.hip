@@ -52,7 +52,7 @@ int check_scan(const mcpu_scan_args* a) {
   auto bc_span = [&](const int64_t (&s)[4]) { return 4 * (T * s[2] + 63 * s[3]); };
   const int64_t spans[] = {x_span(a->u_stride), x_span(a->delta_stride), x_span(a->z_stride),
                            x_span(a->dout_stride), bc_span(a->B_stride), bc_span(a->C_stride),
-                           4 * (ch * nblk * a->dstate + T), esz * (ch * a->seqlen + T)};
+                           4 * (ch * nblk * a->dstate + 63), esz * (ch * a->seqlen + T)};
   for (int64_t sp : spans)
     if (sp >= 0xffffffffll)
       return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: strides or sizes too large for 32-bit tile offsets");

@@ -44,6 +44,37 @@ template <typename T> __device__ __forceinline__ void st(void* base, int64_t idx
   static_cast<T*>(base)[idx] = from_f32<T>(v);
 }
 
+// ---- buffer loads ---------------------------------------------------------------
+// Loads through a raw buffer descriptor built from a wave-uniform base pointer
+// (scalar registers) and a 32-bit per-lane byte offset: the address
+// arithmetic stays in the scalar unit instead of a 64-bit add per lane. The
+// descriptor spans 4 GiB (no range check is relied on); 0x00020000 is the
+// gfx9 raw-buffer format word.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wave_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+template <typename T> __device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ float buf_ld<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ float buf_ld<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return to_f32(bf16{static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0))});
+}
+template <> __device__ __forceinline__ float buf_ld<f16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return to_f32(__builtin_bit_cast(f16, static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0))));
+}
+
+template <typename T> __device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v);
+template <> __device__ __forceinline__ void buf_st<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+template <> __device__ __forceinline__ void buf_st<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(from_f32<bf16>(v).bits, r, off, 0, 0);
+}
+template <> __device__ __forceinline__ void buf_st<f16>(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<f16>(v)), r, off, 0, 0);
+}
+
 // ---- scalar math ----------------------------------------------------------------
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
       tc.load(nC);
     }
 #pragma unroll
-    for (int s = 0; s < SPL; ++s) nh0[s] = *reinterpret_cast<const float*>(ck_base + ck_lane[s]);
+    for (int s = 0; s < SPL; ++s) nh0[s] = buf_ld<float>(wave_rsrc(ck_base), ck_lane[s]);
     xu.advance_unless(-1, stay);
     xd.advance_unless(-1, stay);
     xo.advance_unless(-1, stay);
@@ -321,9 +321,9 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
     // Stores after the park, so waiting for the prefetch never waits for them.
     if (tv && rc.active) {
-      *reinterpret_cast<Tx*>(o_du + o_off) = from_f32<Tx>(duv);
-      *reinterpret_cast<Tx*>(o_dd + o_off) = from_f32<Tx>(ddt);
-      if (HAS_Z) *reinterpret_cast<Tx*>(o_dz + o_off) = from_f32<Tx>(dzv);
+      buf_st<Tx>(wave_rsrc(o_du), o_off, duv);
+      buf_st<Tx>(wave_rsrc(o_dd), o_off, ddt);
+      if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), o_off, dzv);
     }
     o_du -= T * sizeof(Tx);
     o_dd -= T * sizeof(Tx);
@@ -338,7 +338,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < W; ++w) acc += src[w * T * NW];
-        *reinterpret_cast<float*>(o_part[q] + o_poff[q]) = acc;
+        buf_st<float>(wave_rsrc(o_part[q]), o_poff[q], acc);
       }
       o_part[q] -= sizeof(float) * T * N;
     }

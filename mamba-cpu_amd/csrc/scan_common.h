@@ -126,7 +126,7 @@ struct XStage {
   }
   template <typename Tx>
   __device__ __forceinline__ float load() const {
-    return to_f32(*reinterpret_cast<const Tx*>(base + off));
+    return buf_ld<Tx>(wave_rsrc(base), off);
   }
   // For a block that may extend past the sequence end: steps past the end
   // load the tile's first element (always in range) and read as 0. The load
@@ -136,7 +136,7 @@ struct XStage {
   template <typename Tx>
   __device__ __forceinline__ float load_guarded(int64_t t0, int64_t L) const {
     const bool ok = t0 + t < L;
-    const float x = to_f32(*reinterpret_cast<const Tx*>(base + (ok ? off : 0u)));
+    const float x = buf_ld<Tx>(wave_rsrc(base), ok ? off : 0u);
     return ok ? x : 0.f;
   }
   __device__ __forceinline__ void advance(int dir) { base += dir * step; }
@@ -183,7 +183,7 @@ struct BCStage {
   // nothing consumes a prefetched value before then.
   __device__ __forceinline__ void load(float (&v)[PER_THREAD]) const {
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i) v[i] = *reinterpret_cast<const float*>(base + off[i]);
+    for (int i = 0; i < PER_THREAD; ++i) v[i] = buf_ld<float>(wave_rsrc(base), off[i]);
   }
   // Also zeroes the steps past the sequence end (see XStage::load_guarded).
   // Used for the sequence's last block only.
@@ -191,7 +191,7 @@ struct BCStage {
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
       const bool in = ok[i] && t0 + t[i] < L;
-      const float x = *reinterpret_cast<const float*>(base + (in ? off[i] : 0u));
+      const float x = buf_ld<float>(wave_rsrc(base), in ? off[i] : 0u);
       v[i] = in ? x : 0.f;
     }
   }

@@ -78,6 +78,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
   float* ck = (MODE != kFwdSummary && p.ckpt) ? p.ckpt + row * p.nblk * N : nullptr;
+  // Per-step outputs and checkpoints as a uniform base (the workgroup's first
+  // row, moved one block at a time) plus a fixed 32-bit per-lane offset.
+  const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
+  const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);
+  const uint32_t o_off = static_cast<uint32_t>(sizeof(Tx) * (crow * L + j));
+  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
   float dts = 0.f;  // sum of dt over this lane's steps (summary pass)
 
   const int64_t tb0 = kb0 * kScanBlockT;
@@ -203,13 +209,15 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     park(buf ^ 1);  // in the last iteration a harmless copy into the idle buffer
 
     if (WRITE_OUT && tv && rc.active) {
-      if (p.ysave != nullptr) st<Tx>(p.ysave, row * L + t, y);
-      st<Tx>(p.out, row * L + t, yg);
+      const int64_t o_pos = (row0 * L + t0) * static_cast<int64_t>(sizeof(Tx));
+      if (p.ysave != nullptr) buf_st<Tx>(wave_rsrc(static_cast<char*>(p.ysave) + o_pos), o_off, y);
+      buf_st<Tx>(wave_rsrc(static_cast<char*>(p.out) + o_pos), o_off, yg);
     }
     if (ck != nullptr && rc.active && k + 1 < kb1) {
 #pragma unroll
       for (int s = 0; s < SPL; ++s)
-        if (j + 16 * s < N) ck[(k + 1) * N + j + 16 * s] = h[s];
+        if (j + 16 * s < N)
+          buf_st<float>(wave_rsrc(p.ckpt + (row0 * p.nblk + k + 1) * N), ck_off + 64 * s, h[s]);
     }
     __syncthreads();
   }
