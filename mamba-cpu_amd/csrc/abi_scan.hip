@@ -13,6 +13,7 @@ void scan_fwd_chunks(ScanParams& p);
 int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
+hipError_t scan_bwd_summary_launch(const ScanParams& p, int dtype, hipStream_t stream);
 hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_part, float* dC,
                               int64_t slices, int64_t nblk_c, int64_t per_slice,
                               const float* dA_part, float* dA, int64_t nA, const float* dD_part,
@@ -120,14 +121,35 @@ int bwd_waves(const mcpu_scan_args* a) {
   return scan_bwd_waves(a->batch, a->ngroups, a->dim / a->ngroups, a->dstate);
 }
 
+// Time chunks of a backward with these parameters: when the rows give fewer
+// than two waves per SIMD of the GPU's 1024, the sequence is cut into chunks
+// (at least four 16-step blocks each) so that about three waves per SIMD run,
+// the most that fit at the backward's register use. Only with the 4-wave
+// workgroups, which the summary pass shares. Sets p.nchunk / p.chunk_blocks.
+void bwd_chunks(ScanParams& p, int waves) {
+  int64_t n = 1;
+  const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves;
+  if (waves == kScanSumWaves && wv > 0 && wv < 2048 && p.nblk >= 8) {
+    n = 3072 / wv;
+    if (n > p.nblk / 4) n = p.nblk / 4;
+    if (n < 1) n = 1;
+  }
+  p.chunk_blocks = n > 1 ? (p.nblk + n - 1) / n : (p.nblk > 0 ? p.nblk : 1);
+  p.nchunk = n > 1 ? (p.nblk + p.chunk_blocks - 1) / p.chunk_blocks : 1;
+}
+
 struct BwdLayout {
-  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, total = 0;
+  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, sum_h = 0, sum_dt = 0, total = 0;
   bool own_ckpt = false, part_bc = false, part_dA = false;
+  int64_t nchunk = 1, chunk_blocks = 1;
 };
 
 BwdLayout bwd_layout(const mcpu_scan_args* a) {
-  const ScanParams p = make_params(a, bwd_waves(a));
+  ScanParams p = make_params(a, bwd_waves(a));
+  bwd_chunks(p, bwd_waves(a));
   BwdLayout w;
+  w.nchunk = p.nchunk;
+  w.chunk_blocks = p.chunk_blocks;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
@@ -142,10 +164,16 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
     w.dB = take(bc);
     w.dC = take(bc);
   }
-  w.part_dA = p.batch > 1;
-  if (w.part_dA) w.dA = take(sizeof(float) * p.batch * p.dim * p.dstate);
-  w.dD = take(sizeof(float) * p.batch * p.dim);
-  w.dbias = take(sizeof(float) * p.batch * p.dim);
+  // dA, dD and ddelta_bias partials per (chunk, batch).
+  const int64_t parts = p.batch * p.nchunk;
+  w.part_dA = parts > 1;
+  if (w.part_dA) w.dA = take(sizeof(float) * parts * p.dim * p.dstate);
+  w.dD = take(sizeof(float) * parts * p.dim);
+  w.dbias = take(sizeof(float) * parts * p.dim);
+  if (p.nchunk > 1) {
+    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nchunk * p.dstate);
+    w.sum_dt = take(sizeof(float) * p.batch * p.dim * p.nchunk);
+  }
   w.total = off;
   return w;
 }
@@ -253,6 +281,15 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   p.dA_part = w.part_dA ? reinterpret_cast<float*>(ws + w.dA) : a->dA;
   p.dD_part = reinterpret_cast<float*>(ws + w.dD);
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
+  p.nchunk = w.nchunk;
+  p.chunk_blocks = w.chunk_blocks;
+  if (p.nchunk > 1) {
+    // Chunked: the adjoint summaries of chunks 1.. first.
+    p.sum_h = reinterpret_cast<float*>(ws + w.sum_h);
+    p.sum_dt = reinterpret_cast<float*>(ws + w.sum_dt);
+    if (int rc = hip_status(scan_bwd_summary_launch(p, a->dtype, st), "selective_scan_bwd summary launch"))
+      return rc;
+  }
   if (int rc = hip_status(scan_bwd_launch(p, a->dtype, waves, st), "selective_scan_bwd launch"))
     return rc;
   // One launch sums every partial: dB/dC over channel blocks (when there is
@@ -262,6 +299,7 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
                          a->dC, p.batch * p.ngroups, p.nblk_c, p.seqlen * p.dstate,
                          w.part_dA ? p.dA_part : nullptr, a->dA, p.dim * p.dstate,
                          a->dD ? p.dD_part : nullptr, a->dD,
-                         a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim, p.batch, st),
+                         a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim,
+                         p.batch * p.nchunk, st),
       "selective_scan_bwd reduce");
 }

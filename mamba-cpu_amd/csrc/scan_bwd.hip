@@ -46,11 +46,17 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x, wave, r);
+  // Time chunk of this workgroup: blocks [kb0, kb1), walked from kb1 - 1 down.
+  const int64_t chunk = blockIdx.x % p.nchunk;
+  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t kl = p.nblk - 1;  // last block
+  const int64_t kb0 = chunk * p.chunk_blocks;
+  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
+  const int64_t kl = kb1 - 1;  // the chunk's last block
   const int64_t t_last = kl * T;
+  // Row of the per-(chunk, batch, channel) partials of dA, dD, ddelta_bias.
+  const int64_t prow = (chunk * p.batch + rc.b) * p.dim + rc.d;
 
   float Av[SPL], A2[SPL], gh[SPL], dA_acc[SPL];
 #pragma unroll
@@ -60,6 +66,21 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     A2[s] = Av[s] * kLog2e;
     gh[s] = (n < N && p.dlast_state != nullptr) ? p.dlast_state[row * N + n] : 0.f;
     dA_acc[s] = 0.f;
+  }
+  if (chunk < p.nchunk - 1) {
+    // Carry the adjoint state over the later chunks: through chunk c it maps
+    // gh to exp(A * sum_dt[c]) * gh + sum_h[c] (sum_h[c] = the adjoint at
+    // chunk c's start from a zero adjoint at its end).
+    const float* sh = p.sum_h + row * p.nchunk * N;
+    const float* sd = p.sum_dt + row * p.nchunk;
+    for (int64_t c = p.nchunk - 1; c > chunk; --c) {
+      const float ds = sd[c];
+#pragma unroll
+      for (int s = 0; s < SPL; ++s) {
+        const int n = j + 16 * s;
+        if (n < N) gh[s] = fmaf(fast_exp2(A2[s] * ds), gh[s], sh[c * N + n]);
+      }
+    }
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
@@ -171,8 +192,8 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   };
 
   float h0[SPL];
-  if (p.nblk > 0) {
-    fetch(std::true_type{}, t_last, kl == 0);
+  if (kb0 < kb1) {
+    fetch(std::true_type{}, t_last, kl == kb0);
     park(static_cast<int>(kl & 1));
 #pragma unroll
     for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
@@ -187,9 +208,9 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     constexpr bool full = decltype(FULL)::value;
     const int buf = static_cast<int>(k & 1);
     const int64_t t0 = k * T;
-    // The block before this one (always full), or this block again from
-    // block 0 (guarded like this block).
-    if (k > 0) fetch(std::false_type{}, t0 - T, k <= 1);
+    // The block before this one (always full), or this block again from the
+    // chunk's first block (guarded like this block).
+    if (k > kb0) fetch(std::false_type{}, t0 - T, k - 1 <= kb0);
     else fetch(std::integral_constant<bool, !full>{}, t0, true);
     auto valid = [&](int i) { return full || i < nvalid; };
 
@@ -316,7 +337,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
         s_red[buf][1][wave][4 * r + q][j + 16 * s] = yC[q];
       }
     }
-    park(buf ^ 1);  // from block 0 a harmless copy into the idle buffer
+    park(buf ^ 1);  // from the chunk's first block a harmless copy into the idle buffer
 #pragma unroll
     for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
     // Stores after the park, so waiting for the prefetch never waits for them.
@@ -344,23 +365,150 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     }
   };
 
-  if (p.nblk > 0) {
-    const int nlast = static_cast<int>(L - t_last);
+  if (kb0 < kb1) {
+    const int nlast = static_cast<int>(L - t_last < T ? L - t_last : T);
     if (nlast == T) block(std::true_type{}, kl, T);
     else block(std::false_type{}, kl, nlast);
   }
-  for (int64_t k = kl - 1; k >= 0; --k) block(std::true_type{}, k, T);
+  for (int64_t k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
 
   if (rc.active) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) p.dA_part[row * N + j + 16 * s] = dA_acc[s];
+      if (j + 16 * s < N) p.dA_part[prow * N + j + 16 * s] = dA_acc[s];
   }
   dD_acc = row_allreduce16(dD_acc);
   dbias_acc = row_allreduce16(dbias_acc);
   if (rc.active && j == 0) {
-    p.dD_part[row] = dD_acc;
-    p.dbias_part[row] = dbias_acc;
+    p.dD_part[prow] = dD_acc;
+    p.dbias_part[prow] = dbias_acc;
+  }
+}
+
+// Adjoint summaries of a time-chunked backward. For every chunk c > 0, runs
+// the adjoint recurrence g = gh + dy_t C_t, gh = g exp(dt_t A) backwards over
+// the chunk from gh = 0 at its end and records gh at the chunk's start
+// (sum_h) and the chunk's sum of dt (sum_dt). The recurrence is affine in gh,
+// so the backward kernel rebuilds the adjoint entering chunk c from these and
+// dlast_state alone. Needs only delta, dout, z and C: no states, no B.
+template <typename Tx, int SPL, bool HAS_Z>
+__global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(const ScanParams p) {
+  constexpr int W = kScanSumWaves;
+  constexpr int CH = 4 * W;
+  constexpr int NW = 16 * SPL;
+  constexpr int T = kScanBlockT;
+  using BC = BCStage<W, SPL>;
+  __shared__ __align__(16) float s_x[2][3][CH][T];  // delta, dout, z
+  __shared__ __align__(16) float s_C[2][NW][kBCPad];
+
+  const int64_t chunk = blockIdx.x % p.nchunk;
+  if (chunk == 0) return;  // no chunk precedes chunk 0
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r = lane >> 4, j = lane & 15;
+  const int c_local = wave * kScanRowsPerWave + r;
+  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
+  const int64_t N = p.dstate, L = p.seqlen;
+  const int64_t row = rc.b * p.dim + rc.d;
+  const int64_t kb0 = chunk * p.chunk_blocks;
+  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
+  const int64_t kl = kb1 - 1;
+  const int64_t t_last = kl * T;
+
+  float A2[SPL], gh[SPL];
+#pragma unroll
+  for (int s = 0; s < SPL; ++s) {
+    const int n = j + 16 * s;
+    A2[s] = n < N ? p.A[rc.d * N + n] * kLog2e : 0.f;
+    gh[s] = 0.f;
+  }
+  const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
+  const bool softplus_on = p.softplus != 0;
+  const bool has_dout = p.dout != nullptr;
+  float dts = 0.f;
+
+  XStage<W> xd, xo, xz;
+  xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, t_last);
+  xo.template init<Tx>(tid, has_dout ? p.dout : p.delta, p.sdo, p, rc, t_last);
+  if (HAS_Z) xz.template init<Tx>(tid, p.z, p.sz, p, rc, t_last);
+  BC tc;
+  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, t_last);
+
+  float nd = 0.f, no = 0.f, nz = 0.f, nC[BC::PER_THREAD];
+  auto fetch = [&](auto GUARD, int64_t t0, bool stay) {
+    if constexpr (decltype(GUARD)::value) {
+      nd = xd.template load_guarded<Tx>(t0, L);
+      no = xo.template load_guarded<Tx>(t0, L);
+      if (HAS_Z) nz = xz.template load_guarded<Tx>(t0, L);
+      tc.load_guarded(t0, L, nC);
+    } else {
+      nd = xd.template load<Tx>();
+      no = xo.template load<Tx>();
+      if (HAS_Z) nz = xz.template load<Tx>();
+      tc.load(nC);
+    }
+    xd.advance_unless(-1, stay);
+    xo.advance_unless(-1, stay);
+    if (HAS_Z) xz.advance_unless(-1, stay);
+    tc.advance_unless(-1, stay);
+  };
+  auto park = [&](int buf) {
+    (&s_x[buf][0][0][0])[xd.slot] = nd;
+    (&s_x[buf][1][0][0])[xo.slot] = has_dout ? no : 0.f;
+    if (HAS_Z) (&s_x[buf][2][0][0])[xz.slot] = nz;
+    tc.park(s_C[buf], nC);
+  };
+
+  fetch(std::true_type{}, t_last, kl == kb0);
+  park(static_cast<int>(kl & 1));
+  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+
+  auto block = [&](auto FULL, int64_t k, int nvalid) {
+    constexpr bool full = decltype(FULL)::value;
+    const int buf = static_cast<int>(k & 1);
+    const int64_t t0 = k * T;
+    if (k > kb0) fetch(std::false_type{}, t0 - T, k - 1 <= kb0);
+    else fetch(std::integral_constant<bool, !full>{}, t0, true);
+    const float dl = s_x[buf][0][c_local][j];
+    const float go = s_x[buf][1][c_local][j];
+    const float zz = HAS_Z ? s_x[buf][2][c_local][j] : 0.f;
+    float Cv[SPL][T];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) read_bc_row(s_C[buf], j + 16 * s, Cv[s]);
+    float dt = dl + bias;
+    if (softplus_on) dt = softplus(dt);
+    float dy = go;
+    if (HAS_Z) dy = go * zz * sigmoid(zz);
+    if (full || j < nvalid) dts += dt;
+    static_for<T>([&](auto I) {
+      constexpr int i = T - 1 - decltype(I)::value;
+      if (full || i < nvalid) {
+        const float dti = row_bcast<i>(dt);
+        const float dyi = row_bcast<i>(dy);
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+          const float a = fast_exp2(dti * A2[s]);
+          gh[s] = fmaf(dyi, Cv[s][i], gh[s]) * a;
+        }
+      }
+    });
+    park(buf ^ 1);
+    __syncthreads();
+  };
+
+  const int nlast = static_cast<int>(L - t_last < T ? L - t_last : T);
+  if (nlast == T) block(std::true_type{}, kl, T);
+  else block(std::false_type{}, kl, nlast);
+  for (int64_t k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
+
+  dts = row_allreduce16(dts);
+  if (rc.active) {
+#pragma unroll
+    for (int s = 0; s < SPL; ++s)
+      if (j + 16 * s < N) p.sum_h[(row * p.nchunk + chunk) * N + j + 16 * s] = gh[s];
+    if (j == 0) p.sum_dt[row * p.nchunk + chunk] = dts;
   }
 }
 
@@ -442,7 +590,7 @@ __global__ void __launch_bounds__(256) reduce_jobs_kernel(const ReduceJobs jobs,
 
 template <typename Tx, int W, int SPL>
 static hipError_t launch_bwd_zy(const ScanParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c));
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nchunk));
   const dim3 block(64 * W);
   if (p.z != nullptr && p.ysave != nullptr)
     hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, true>), grid, block, 0, stream, p);
@@ -482,6 +630,34 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) 
     if (wgs >= 256 && wgs % 256 == 0 && pad == 0) return w;
   }
   return 4;
+}
+
+template <typename Tx, int SPL>
+static hipError_t launch_bwd_summary(const ScanParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nchunk));
+  const dim3 block(64 * kScanSumWaves);
+  if (p.z != nullptr)
+    hipLaunchKernelGGL((scan_bwd_summary_kernel<Tx, SPL, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((scan_bwd_summary_kernel<Tx, SPL, false>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename Tx>
+static hipError_t launch_bwd_summary_spl(const ScanParams& p, hipStream_t stream) {
+  if (p.dstate <= 16) return launch_bwd_summary<Tx, 1>(p, stream);
+  if (p.dstate <= 32) return launch_bwd_summary<Tx, 2>(p, stream);
+  return launch_bwd_summary<Tx, 4>(p, stream);
+}
+
+// Adjoint summaries of a chunked backward (p.nchunk > 1, p.nblk_c for
+// kScanSumWaves waves, p.sum_h / p.sum_dt set).
+hipError_t scan_bwd_summary_launch(const ScanParams& p, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case MCPU_F32: return launch_bwd_summary_spl<float>(p, stream);
+    case MCPU_BF16: return launch_bwd_summary_spl<bf16>(p, stream);
+    default: return launch_bwd_summary_spl<f16>(p, stream);
+  }
 }
 
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream) {

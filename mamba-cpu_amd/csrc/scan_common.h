@@ -28,6 +28,7 @@ constexpr int kScanBlockT = 16;       // time steps per block
 constexpr int kScanRowsPerWave = 4;   // channels per wave
 constexpr int kScanMaxWaves = 12;     // widest workgroup of either kernel
 constexpr int kBCPad = 20;            // padded time stride of the B/C tiles (conflict-free b128 reads)
+constexpr int kScanSumWaves = 4;      // waves per workgroup of the backward's chunk-summary pass
 
 struct ScanParams {
   const void* u;
