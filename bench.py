@@ -304,6 +304,53 @@ def mamba130m(torch, dev, iters=3):
     return res
 
 
+def cpu_prefill(torch, batch=4, seqlen=1024):
+    """The same random-init Mamba-130M prefill on this host's cores the way
+    mamba-cpu runs it: the reference's hf.py routes transformers'
+    `mamba_selective_scan` to its native CPU kernels (here the reference's own
+    csrc/selective_scan.cpp, built into oracle/_ref) and keeps the ATen
+    F.conv1d conv (src/mamba_cpu/ops/causal_conv1d.py:41-46, which transformers'
+    own causal_conv1d_fn also is). One warm-up pass, one timed pass, at
+    `_cpu_threads()` threads. Returns (tokens/s, seconds, threads) or None."""
+    import importlib
+
+    import transformers
+
+    from oracle import ref as R
+
+    if not R.available():
+        return None
+    threads = _cpu_threads()
+    mod = importlib.import_module("transformers.models.mamba.modeling_mamba")
+    saved = mod.mamba_selective_scan
+
+    def ref_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                 return_last_state=False, **kwargs):
+        out, last = R.scan_fwd(u, delta, A, R.kernel_bc(B), R.kernel_bc(C), D, z, delta_bias,
+                               delta_softplus, threads)
+        out = torch.from_numpy(out)
+        return (out, torch.from_numpy(last)) if return_last_state else out
+
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    mod.mamba_selective_scan = ref_scan
+    try:
+        torch.manual_seed(0)
+        cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
+                                       conv_kernel=4, vocab_size=50280)
+        model = transformers.MambaForCausalLM(cfg).eval()
+        ids = torch.randint(0, 50280, (batch, seqlen))
+        with torch.no_grad():
+            model(ids)
+            t0 = time.perf_counter()
+            model(ids)
+            sec = time.perf_counter() - t0
+    finally:
+        mod.mamba_selective_scan = saved
+        torch.set_num_threads(prev_threads)
+    return round(batch * seqlen / sec, 1), round(sec, 3), threads
+
+
 def counter_pass(torch, dev, inputs, gout):
     """A short fixed sequence for hardware-counter runs (rocprofv3 --pmc): the
     training-step forward and backward ops three times, each followed by a
@@ -431,6 +478,18 @@ def main():
             extra["mamba130m_prefill_tokens_per_s"] = extra["mamba130m"]["prefill_tokens_per_s"]
         except Exception as exc:  # reported, not hidden
             extra["mamba130m_error"] = repr(exc)
+        if not args.no_cpu_baseline and "mamba130m" in extra:
+            try:
+                cpu = cpu_prefill(torch)
+                if cpu is not None:
+                    tps, sec, threads = cpu
+                    m = extra["mamba130m"]
+                    m["cpu_reference_prefill_tokens_per_s"] = tps
+                    m["cpu_reference_prefill_s"] = sec
+                    m["cpu_reference_threads"] = threads
+                    m["prefill_speedup_vs_cpu_reference"] = round(m["prefill_tokens_per_s"] / tps, 1)
+            except Exception as exc:  # reported, not hidden
+                extra["mamba130m_cpu_error"] = repr(exc)
     if not args.no_configs:
         extra["workloads"] = other_configs(torch, dev, stream, not args.no_cpu_baseline)
 
