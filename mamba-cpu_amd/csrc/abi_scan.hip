@@ -136,12 +136,27 @@ void bwd_chunks(ScanParams& p, int waves) {
   }
   p.chunk_blocks = n > 1 ? (p.nblk + n - 1) / n : (p.nblk > 0 ? p.nblk : 1);
   p.nchunk = n > 1 ? (p.nblk + p.chunk_blocks - 1) / p.chunk_blocks : 1;
+  p.nsum = p.nchunk;
+  p.sum_blocks = p.chunk_blocks;
+  p.sum_per_chunk = 1;
+  if (p.nchunk > 1) {
+    // Summary units: enough of them after the first chunk for about four
+    // waves per SIMD in the summary pass; chunks are whole units.
+    int64_t m = (4096 + wv * (p.nchunk - 1) - 1) / (wv * (p.nchunk - 1));
+    if (m > p.chunk_blocks) m = p.chunk_blocks;
+    if (m < 1) m = 1;
+    p.sum_blocks = (p.chunk_blocks + m - 1) / m;
+    p.chunk_blocks = p.sum_blocks * m;
+    p.nchunk = (p.nblk + p.chunk_blocks - 1) / p.chunk_blocks;
+    p.nsum = (p.nblk + p.sum_blocks - 1) / p.sum_blocks;
+    p.sum_per_chunk = m;
+  }
 }
 
 struct BwdLayout {
   size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, sum_h = 0, sum_dt = 0, total = 0;
   bool own_ckpt = false, part_bc = false, part_dA = false;
-  int64_t nchunk = 1, chunk_blocks = 1;
+  int64_t nchunk = 1, chunk_blocks = 1, nsum = 1, sum_blocks = 1, sum_per_chunk = 1;
 };
 
 BwdLayout bwd_layout(const mcpu_scan_args* a) {
@@ -150,6 +165,9 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
   BwdLayout w;
   w.nchunk = p.nchunk;
   w.chunk_blocks = p.chunk_blocks;
+  w.nsum = p.nsum;
+  w.sum_blocks = p.sum_blocks;
+  w.sum_per_chunk = p.sum_per_chunk;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
@@ -171,8 +189,8 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
   w.dD = take(sizeof(float) * parts * p.dim);
   w.dbias = take(sizeof(float) * parts * p.dim);
   if (p.nchunk > 1) {
-    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nchunk * p.dstate);
-    w.sum_dt = take(sizeof(float) * p.batch * p.dim * p.nchunk);
+    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nsum * p.dstate);
+    w.sum_dt = take(sizeof(float) * p.batch * p.dim * p.nsum);
   }
   w.total = off;
   return w;
@@ -283,6 +301,9 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
   p.nchunk = w.nchunk;
   p.chunk_blocks = w.chunk_blocks;
+  p.nsum = w.nsum;
+  p.sum_blocks = w.sum_blocks;
+  p.sum_per_chunk = w.sum_per_chunk;
   if (p.nchunk > 1) {
     // Chunked: the adjoint summaries of chunks 1.. first.
     p.sum_h = reinterpret_cast<float*>(ws + w.sum_h);

@@ -68,12 +68,12 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     dA_acc[s] = 0.f;
   }
   if (chunk < p.nchunk - 1) {
-    // Carry the adjoint state over the later chunks: through chunk c it maps
-    // gh to exp(A * sum_dt[c]) * gh + sum_h[c] (sum_h[c] = the adjoint at
-    // chunk c's start from a zero adjoint at its end).
-    const float* sh = p.sum_h + row * p.nchunk * N;
-    const float* sd = p.sum_dt + row * p.nchunk;
-    for (int64_t c = p.nchunk - 1; c > chunk; --c) {
+    // Carry the adjoint state over the summary units after this chunk:
+    // through unit u it maps gh to exp(A * sum_dt[u]) * gh + sum_h[u]
+    // (sum_h[u] = the adjoint at u's start from a zero adjoint at its end).
+    const float* sh = p.sum_h + row * p.nsum * N;
+    const float* sd = p.sum_dt + row * p.nsum;
+    for (int64_t c = p.nsum - 1; c >= (chunk + 1) * p.sum_per_chunk; --c) {
       const float ds = sd[c];
 #pragma unroll
       for (int s = 0; s < SPL; ++s) {
@@ -385,12 +385,14 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   }
 }
 
-// Adjoint summaries of a time-chunked backward. For every chunk c > 0, runs
-// the adjoint recurrence g = gh + dy_t C_t, gh = g exp(dt_t A) backwards over
-// the chunk from gh = 0 at its end and records gh at the chunk's start
-// (sum_h) and the chunk's sum of dt (sum_dt). The recurrence is affine in gh,
-// so the backward kernel rebuilds the adjoint entering chunk c from these and
-// dlast_state alone. Needs only delta, dout, z and C: no states, no B.
+// Adjoint summaries of a time-chunked backward. For every summary unit u
+// after the first chunk, runs the adjoint recurrence g = gh + dy_t C_t,
+// gh = g exp(dt_t A) backwards over the unit from gh = 0 at its end and
+// records gh at the unit's start (sum_h) and the unit's sum of dt (sum_dt).
+// The recurrence is affine in gh, so the backward kernel rebuilds the adjoint
+// entering chunk c from these and dlast_state alone. Needs only delta, dout,
+// z and C: no states, no B. Units are finer than chunks so that this pass,
+// which skips the first chunk, still fills the GPU.
 template <typename Tx, int SPL, bool HAS_Z>
 __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(const ScanParams p) {
   constexpr int W = kScanSumWaves;
@@ -401,18 +403,18 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   __shared__ __align__(16) float s_x[2][3][CH][T];  // delta, dout, z
   __shared__ __align__(16) float s_C[2][NW][kBCPad];
 
-  const int64_t chunk = blockIdx.x % p.nchunk;
-  if (chunk == 0) return;  // no chunk precedes chunk 0
+  const int64_t unit = blockIdx.x % p.nsum;
+  if (unit < p.sum_per_chunk) return;  // the first chunk's units feed no carry
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
+  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nsum, wave, r);
   const int64_t N = p.dstate, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t kb0 = chunk * p.chunk_blocks;
-  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
+  const int64_t kb0 = unit * p.sum_blocks;
+  const int64_t kb1 = kb0 + p.sum_blocks < p.nblk ? kb0 + p.sum_blocks : p.nblk;
   const int64_t kl = kb1 - 1;
   const int64_t t_last = kl * T;
 
@@ -507,8 +509,8 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   if (rc.active) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) p.sum_h[(row * p.nchunk + chunk) * N + j + 16 * s] = gh[s];
-    if (j == 0) p.sum_dt[row * p.nchunk + chunk] = dts;
+      if (j + 16 * s < N) p.sum_h[(row * p.nsum + unit) * N + j + 16 * s] = gh[s];
+    if (j == 0) p.sum_dt[row * p.nsum + unit] = dts;
   }
 }
 
@@ -634,7 +636,7 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) 
 
 template <typename Tx, int SPL>
 static hipError_t launch_bwd_summary(const ScanParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nchunk));
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nsum));
   const dim3 block(64 * kScanSumWaves);
   if (p.z != nullptr)
     hipLaunchKernelGGL((scan_bwd_summary_kernel<Tx, SPL, true>), grid, block, 0, stream, p);

@@ -65,8 +65,13 @@ struct ScanParams {
   // started from zero, and the chunk's sum of dt).
   int64_t nchunk;        // 1 = unchunked
   int64_t chunk_blocks;
-  float* sum_h;          // (batch, dim, nchunk, dstate)
-  float* sum_dt;         // (batch, dim, nchunk)
+  float* sum_h;          // (batch, dim, nchunk, dstate); backward: (batch, dim, nsum, dstate)
+  float* sum_dt;         // (batch, dim, nchunk); backward: (batch, dim, nsum)
+  // Backward: adjoint summaries are kept per unit of sum_blocks blocks (nsum
+  // units); a chunk is sum_per_chunk whole units.
+  int64_t nsum;
+  int64_t sum_blocks;
+  int64_t sum_per_chunk;
 };
 
 struct RowCtx {
