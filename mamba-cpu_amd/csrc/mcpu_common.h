@@ -121,6 +121,30 @@ constexpr int kQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
 // Value of x held by lane N of the caller's row.
 template <int N> __device__ __forceinline__ float row_bcast(float x) { return dpp<0x150 + N>(x); }
 
+// One VOP2 instruction whose first operand is x as held by lane N of the
+// caller's row (row_newbcast), for the uses the compiler cannot fold a DPP
+// move into (v_fmac, or a multiply far from the broadcast). Each statement
+// starts with the two wait states a DPP instruction needs after a vector ALU
+// write of any of its operands, so it is safe wherever it is scheduled; the
+// wait stalls only the issuing wave. Nothing the compiler emits reads their
+// results through DPP.
+
+// acc + bcast_N(x) * m
+template <int N> __device__ __forceinline__ float fmac_bcast(float acc, float x, float m) {
+  asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "+v"(acc)
+      : "v"(x), "v"(m), "n"(N));
+  return acc;
+}
+// bcast_N(x) * m
+template <int N> __device__ __forceinline__ float mul_bcast(float x, float m) {
+  float r;
+  asm("s_nop 1\n\tv_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "=v"(r)
+      : "v"(x), "v"(m), "n"(N));
+  return r;
+}
+
 // Sum over the 16 lanes of a row, result in every lane of the row.
 __device__ __forceinline__ float row_allreduce16(float x) {
   x += dpp<kQuadXor1>(x);
@@ -131,25 +155,50 @@ __device__ __forceinline__ float row_allreduce16(float x) {
 }
 
 // Reduce-scatter over a row: lane j of every row returns sum_{lanes of row} p[j].
-// Butterfly with partner masks 15 (row_mirror), 7 (row_half_mirror), 3 and 1
-// (quad_perm); they span all four lane bits, and at each step the lane keeps
-// the half selected by bits 3, 2, 1, 0 of j in turn.
+// The first two halvings split the row by DPP bank masks (a bank is 4 lanes):
+// one v_add_f32_dpp per half writes only the lanes that keep that half, so a
+// halving costs one instruction per output and no selects. Partners are
+// lane j ^ 8 (row_ror:8; banks 0-1 keep steps 0-7, banks 2-3 steps 8-15) and
+// lane j ^ 7 (row_half_mirror; banks 0, 2 keep the lower four, banks 1, 3 the
+// upper four), so lane j then holds steps i + 4 b2 + 8 b3 (i < 4) summed over
+// lanes {j, j^8, j^7, j^15}. The last two halvings pair j with j ^ 3 and
+// j ^ 1 within the quad (quad_perm) and select by bits 1 and 0. The 24 adds are
+// one statement with the two wait states a DPP read needs after the vector ALU
+// wrote its operand at its head; inside it no instruction reads a register
+// written fewer than seven instructions earlier.
 __device__ __forceinline__ float row_reduce_scatter16(const float (&p)[16], int j) {
-  const bool b3 = j & 8, b2 = j & 4, b1 = j & 2, b0 = j & 1;
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float keep = b3 ? p[i + 8] : p[i];
-    const float send = b3 ? p[i] : p[i + 8];
-    q[i] = keep + dpp<kRowMirror>(send);
-  }
-  float r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float keep = b2 ? q[i + 4] : q[i];
-    const float send = b2 ? q[i] : q[i + 4];
-    r[i] = keep + dpp<kRowHalfMirror>(send);
-  }
+  const bool b1 = j & 2, b0 = j & 1;
+  float t0, t1, t2, t3, t4, t5, t6, t7;
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %8, %8 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %16, %16 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %1, %9, %9 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %1, %17, %17 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %2, %10, %10 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %18, %18 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %3, %11, %11 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %3, %19, %19 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %4, %12, %12 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %4, %20, %20 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %5, %13, %13 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %5, %21, %21 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %6, %14, %14 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %6, %22, %22 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %7, %15, %15 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %7, %23, %23 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %4, %4 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %1, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %2, %2, %2 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %2, %6, %6 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %3, %3, %3 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %3, %7, %7 row_half_mirror row_mask:0xf bank_mask:0xa"
+      : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+      : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7]),
+        "v"(p[8]), "v"(p[9]), "v"(p[10]), "v"(p[11]), "v"(p[12]), "v"(p[13]), "v"(p[14]), "v"(p[15]));
+  const float r[4] = {t0, t1, t2, t3};
   float s[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {

@@ -286,21 +286,21 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     static_for<T>([&](auto I) {
       constexpr int i = T - 1 - decltype(I)::value;
       if (valid(i)) {
+        // dt, dt*u and dy of step i from its owner lane: fused into the
+        // instructions that consume them (DPP row broadcasts).
         const float dyi = row_bcast<i>(dy);
-        const float dti = row_bcast<i>(dt_r);
-        const float dtui = row_bcast<i>(dtu_r);
         float acc1 = 0.f, acc2 = 0.f;
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
-          const float g = fmaf(dyi, Cv[s][i], gh[s]);
+          const float g = fmac_bcast<i>(gh[s], dy, Cv[s][i]);
           dCc[s][i] = dyi * hs[s][i];
           const float hp = i > 0 ? hs[s][i > 0 ? i - 1 : 0] : h0[s];
           gh[s] = g * as[s][i];
           const float ga = gh[s] * hp;
-          dA_acc[s] = fmaf(ga, dti, dA_acc[s]);
+          dA_acc[s] = fmac_bcast<i>(dA_acc[s], dt_r, ga);
           acc1 = fmaf(ga, Av[s], acc1);
           acc2 = fmaf(g, Bv[s][i], acc2);
-          dBc[s][i] = g * dtui;
+          dBc[s][i] = mul_bcast<i>(dtu_r, g);
         }
         r1[i] = acc1;
         r2[i] = acc2;
