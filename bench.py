@@ -134,10 +134,59 @@ def _events_ms(torch, stream, fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
+def _cpu_ms(fn, iters):
+    """Milliseconds per call of fn() on the host: one warm-up call, then
+    `iters` timed calls."""
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    return (time.perf_counter() - t0) / iters * 1e3
+
+
+def _attach_cpu(r, cpu_ms, sample):
+    """Adds the CPU reference time of a workload and the GPU's speedup over it."""
+    r["cpu_reference_ms"] = round(cpu_ms, 3)
+    r["cpu_reference_threads"] = _cpu_threads()
+    r["cpu_reference_sample"] = sample
+    r["speedup_vs_cpu_reference"] = round(cpu_ms / r["ms"], 1)
+
+
 def _rate(nbytes, ms):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "algorithmic_bytes": int(nbytes)}
+
+
+class _torch_threads:
+    """Sets torch's intra-op thread count to the CPU baseline's for a block."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __enter__(self):
+        self.prev = self.torch.get_num_threads()
+        self.torch.set_num_threads(_cpu_threads())
+
+    def __exit__(self, *exc):
+        self.torch.set_num_threads(self.prev)
+
+
+def cpu_conv_ms(torch, x, wt, bias, go, iters=2):
+    """Milliseconds per forward+backward of the reference's conv path on the
+    host (ATen depthwise F.conv1d + silu, autograd through ATen), same inputs."""
+    from oracle import cpu_torch as CT
+
+    cx = x.detach().cpu().requires_grad_()
+    cw, cb = wt.detach().cpu().requires_grad_(), bias.detach().cpu().requires_grad_()
+    cgo = go.cpu()
+
+    def step():
+        out = CT.causal_conv1d_fn(cx, cw, cb, activation="silu")
+        return torch.autograd.grad(out, [cx, cw, cb], cgo)
+
+    with _torch_threads(torch):
+        return _cpu_ms(step, iters)
 
 
 def other_configs(torch, dev, stream, cpu):
@@ -163,8 +212,10 @@ def other_configs(torch, dev, stream, cpu):
     r = _rate(nbytes, ms)
     r["workload"] = "selective_scan_fn forward, fp32, batch 1, dim 1536, seqlen 2048, dstate 16, softplus"
     if cpu:
-        r["cpu_reference_ms"] = cpu_scan_ms({"u": u, "delta": delta, "A": A, "B": Bm, "C": Cm, "D": D},
-                                            None, True, fwd_only=True)
+        cms = cpu_scan_ms({"u": u, "delta": delta, "A": A, "B": Bm, "C": Cm, "D": D}, None, True,
+                          fwd_only=True)
+        if cms is not None:
+            _attach_cpu(r, cms, "the full workload on the reference's C++ kernels, 1 warm-up + 3 timed calls")
     res["scan_fwd_b1_d1536_l2048"] = r
     del u, delta, Bm, Cm
 
@@ -191,6 +242,13 @@ def other_configs(torch, dev, stream, cpu):
     r = _rate(nbytes, ms)
     r["workload"] = ("selective_scan_fn forward+backward, bf16 u/delta/B/C, fp32 A/D, batch 1, "
                      "dim 5120, seqlen 16384, dstate 16, softplus")
+    if cpu:
+        # The reference computes in fp32: its interface casts bf16 inputs up
+        # (selective_scan_interface.py:127-135), so the CPU leg takes them in fp32.
+        cms = cpu_scan_ms({k: v.detach() for k, v in leaves.items()}, gout, True, iters=1)
+        if cms is not None:
+            _attach_cpu(r, cms, "the full workload (fp32 copies of the bf16 inputs) on the reference's "
+                                "C++ kernels, 1 warm-up + 1 timed fwd+bwd")
     res["scan_fwdbwd_b1_d5120_l16384_bf16"] = r
     del leaves, gout
 
@@ -211,6 +269,10 @@ def other_configs(torch, dev, stream, cpu):
         ms = _events_ms(torch, stream, conv_step, 20)
         r = _rate(nbytes, ms)
         r["workload"] = f"causal_conv1d_fn forward+backward, {tag}, batch 8, dim 3072, seqlen 2048, width 4, silu"
+        if cpu:
+            cms = cpu_conv_ms(torch, x, wt, bias, go)
+            _attach_cpu(r, cms, "the full workload through the reference's ATen conv path "
+                                "(ops/causal_conv1d.py:16-53) with autograd, 1 warm-up + 2 timed")
         res[f"conv_fwdbwd_b8_d3072_l2048_{tag}"] = r
         del x, go
 
@@ -229,6 +291,19 @@ def other_configs(torch, dev, stream, cpu):
     nbytes = (b * d + 2 * b * d * (w - 1) + b * d) * 4 + 4 * (d * w + d)
     r = _rate(nbytes, ms)
     r["workload"] = "causal_conv1d_update, fp32, state (64, 3072, 3), x (64, 3072), silu; per step of 256"
+    if cpu:
+        from oracle import cpu_torch as CT
+
+        cst, cxs, cw, cb = state.cpu(), xs.cpu(), wt.cpu(), bias.cpu()
+
+        def cupd():
+            for i in range(256):
+                CT.causal_conv1d_update(cxs[i], cst, cw, cb, activation="silu")
+
+        with _torch_threads(torch):
+            cms = _cpu_ms(cupd, 1) / 256
+        _attach_cpu(r, cms, "256 steps through the reference's ATen update path "
+                            "(ops/causal_conv1d.py:56-85), 1 warm-up + 1 timed pass")
     res["conv_update_b64_d3072"] = r
 
     # Selective state update, Mamba-130M layer shape: state (4, 1536, 16).
@@ -244,6 +319,19 @@ def other_configs(torch, dev, stream, cpu):
     nbytes = 2 * b * d * n * 4 + 4 * b * d * 4 + 4 * (d * n + 2 * d) + 2 * b * n * 4
     r = _rate(nbytes, ms)
     r["workload"] = "selective_state_update, fp32, state (4, 1536, 16), z + D + dt_bias, softplus"
+    if cpu:
+        from oracle import cpu_torch as CT
+
+        c = [t.cpu() for t in (st, xv, dtv, A, Bv, Cv, D, zv, dtb)]
+
+        def cst():
+            for _ in range(200):
+                CT.selective_state_update(*c[:7], c[7], c[8], True)
+
+        with _torch_threads(torch):
+            cms = _cpu_ms(cst, 1) / 200
+        _attach_cpu(r, cms, "200 calls through the reference's ATen path "
+                            "(ops/selective_state_update.py:5-57), 1 warm-up + 1 timed pass")
     res["state_update_b4_d1536"] = r
     return res
 
@@ -288,6 +376,20 @@ def mamba130m(torch, dev, iters=3):
     res["decode_tokens_per_s"] = round(4 * (out.shape[1] - 16) / sec, 1)
     res["decode_ms_per_step"] = round(sec / (out.shape[1] - 16) * 1e3, 3)
 
+    # The same 128 greedy steps with each token's step replayed from a HIP
+    # graph (mamba_cpu.decode); the graph's capture is inside the timed region.
+    import mamba_cpu.decode
+
+    mamba_cpu.decode.greedy_generate(model, prompt, 4)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gout = mamba_cpu.decode.greedy_generate(model, prompt, 128)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    res["decode_graph_ms_per_step"] = round(sec / 128 * 1e3, 3)
+    res["decode_graph_tokens_per_s"] = round(4 * 128 / sec, 1)
+    res["decode_graph_tokens_match_generate"] = bool(torch.equal(gout, out))
+
     model.train()
     tids = ids[:, :256]
     model(tids, labels=tids).loss.backward()
@@ -304,37 +406,27 @@ def mamba130m(torch, dev, iters=3):
     return res
 
 
-def cpu_prefill(torch, batch=4, seqlen=1024):
-    """The same random-init Mamba-130M prefill on this host's cores the way
-    mamba-cpu runs it: the reference's hf.py routes transformers'
-    `mamba_selective_scan` to its native CPU kernels (here the reference's own
-    csrc/selective_scan.cpp, built into oracle/_ref) and keeps the ATen
-    F.conv1d conv (src/mamba_cpu/ops/causal_conv1d.py:41-46, which transformers'
-    own causal_conv1d_fn also is). One warm-up pass, one timed pass, at
-    `_cpu_threads()` threads. Returns (tokens/s, seconds, threads) or None."""
-    import importlib
-
+def cpu_mamba130m(torch, batch=4, seqlen=1024, decode_steps=16):
+    """The same random-init Mamba-130M on this host's cores the way mamba-cpu
+    runs it: transformers' Mamba ops routed as the reference's hf.py routes
+    CPU tensors (the scan to the reference's own C++ kernels, built from its
+    csrc/selective_scan.cpp into oracle/_ref, with their backward for
+    training; conv, conv update and state update through the reference's ATen
+    paths; mamba_inner_fn -> None). Prefill: one warm-up pass, one timed pass.
+    Decode: `decode_steps` greedy tokens from the same 4 x 16 prompt as the
+    GPU leg (a sample of its 128). Train: one warm-up step, one timed step at
+    4 x 256. All at `_cpu_threads()` threads. Returns a dict, or None when the
+    reference kernels are not built."""
     import transformers
 
+    from oracle import cpu_torch as CT
     from oracle import ref as R
 
     if not R.available():
         return None
     threads = _cpu_threads()
-    mod = importlib.import_module("transformers.models.mamba.modeling_mamba")
-    saved = mod.mamba_selective_scan
-
-    def ref_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                 return_last_state=False, **kwargs):
-        out, last = R.scan_fwd(u, delta, A, R.kernel_bc(B), R.kernel_bc(C), D, z, delta_bias,
-                               delta_softplus, threads)
-        out = torch.from_numpy(out)
-        return (out, torch.from_numpy(last)) if return_last_state else out
-
-    prev_threads = torch.get_num_threads()
-    torch.set_num_threads(threads)
-    mod.mamba_selective_scan = ref_scan
-    try:
+    res = {"cpu_reference_threads": threads}
+    with CT.route_transformers(threads):
         torch.manual_seed(0)
         cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
                                        conv_kernel=4, vocab_size=50280)
@@ -345,10 +437,29 @@ def cpu_prefill(torch, batch=4, seqlen=1024):
             t0 = time.perf_counter()
             model(ids)
             sec = time.perf_counter() - t0
-    finally:
-        mod.mamba_selective_scan = saved
-        torch.set_num_threads(prev_threads)
-    return round(batch * seqlen / sec, 1), round(sec, 3), threads
+        res["cpu_reference_prefill_tokens_per_s"] = round(batch * seqlen / sec, 1)
+        res["cpu_reference_prefill_s"] = round(sec, 3)
+
+        prompt = ids[:, :16]
+        gen = dict(max_new_tokens=decode_steps, min_new_tokens=decode_steps, do_sample=False,
+                   pad_token_id=0)
+        with torch.no_grad():
+            model.generate(prompt, **dict(gen, max_new_tokens=2, min_new_tokens=2))
+            t0 = time.perf_counter()
+            out = model.generate(prompt, **gen)
+            sec = time.perf_counter() - t0
+        res["cpu_reference_decode_ms_per_step"] = round(sec / (out.shape[1] - 16) * 1e3, 3)
+        res["cpu_reference_decode_sample"] = f"{out.shape[1] - 16} greedy steps from the 4 x 16 prompt"
+
+        model.train()
+        tids = ids[:, :256]
+        for i in range(2):
+            t0 = time.perf_counter()
+            model(tids, labels=tids).loss.backward()
+            model.zero_grad(set_to_none=True)
+            sec = time.perf_counter() - t0
+        res["cpu_reference_train_step_ms_4x256"] = round(sec * 1e3, 1)
+    return res
 
 
 def counter_pass(torch, dev, inputs, gout):
@@ -480,14 +591,18 @@ def main():
             extra["mamba130m_error"] = repr(exc)
         if not args.no_cpu_baseline and "mamba130m" in extra:
             try:
-                cpu = cpu_prefill(torch)
+                cpu = cpu_mamba130m(torch)
                 if cpu is not None:
-                    tps, sec, threads = cpu
                     m = extra["mamba130m"]
-                    m["cpu_reference_prefill_tokens_per_s"] = tps
-                    m["cpu_reference_prefill_s"] = sec
-                    m["cpu_reference_threads"] = threads
-                    m["prefill_speedup_vs_cpu_reference"] = round(m["prefill_tokens_per_s"] / tps, 1)
+                    m.update(cpu)
+                    m["prefill_speedup_vs_cpu_reference"] = round(
+                        m["prefill_tokens_per_s"] / cpu["cpu_reference_prefill_tokens_per_s"], 1)
+                    m["decode_speedup_vs_cpu_reference"] = round(
+                        cpu["cpu_reference_decode_ms_per_step"] / m["decode_ms_per_step"], 1)
+                    m["decode_graph_speedup_vs_cpu_reference"] = round(
+                        cpu["cpu_reference_decode_ms_per_step"] / m["decode_graph_ms_per_step"], 1)
+                    m["train_speedup_vs_cpu_reference"] = round(
+                        cpu["cpu_reference_train_step_ms_4x256"] / m["train_step_ms_4x256"], 1)
             except Exception as exc:  # reported, not hidden
                 extra["mamba130m_cpu_error"] = repr(exc)
     if not args.no_configs:

@@ -11,6 +11,9 @@ Contents
   oracle.ref       ctypes loader for oracle/_ref/libmcpu_ref.so, the
                    reference's own C++ CPU kernels compiled from the reference
                    sources by oracle/Makefile.
+  oracle.cpu_torch the reference's CPU execution path for timing (its ATen
+                   conv / state-update code paths, an autograd wrapper around
+                   oracle.ref's kernels, and its transformers routing).
 
 Pinning (how each oracle function is checked, so a plausible mistake fails):
   scan forward      vs the compiled reference (_ref) on random inputs; closed
@@ -24,5 +27,7 @@ Pinning (how each oracle function is checked, so a plausible mistake fails):
   conv update       update steps == full conv (invariant); state == last inputs.
   state update      L single steps == full scan (whose oracle is pinned above);
                     multi-head layout == flattened layout.
+  cpu_torch         each function vs the pinned float64 functions above
+                    (tests/test_cpu_baseline.py).
 Every function is pinned; none is "parity unpinned".
 """
