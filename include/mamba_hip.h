@@ -82,7 +82,7 @@ typedef struct mcpu_scan_args {
   int64_t B_stride[4];      /* element strides over (batch, group, seqlen, dstate) */
   int64_t C_stride[4];
   /* forward outputs */
-  void* out;                /* (batch, dim, seqlen) contiguous, dtype; NULL = states only */
+  void* out;                /* (batch, dim, seqlen), dtype, strides out_stride; NULL = states only */
   float* last_state;        /* (batch, dim, dstate) contiguous, optional */
   float* ckpt;              /* optional state checkpoints, see mcpu_selective_scan_ckpt_size */
   void* ysave;              /* optional (batch, dim, seqlen) contiguous, dtype: the forward
@@ -92,15 +92,23 @@ typedef struct mcpu_scan_args {
   const void* dout;         /* (batch, dim, seqlen), dtype; NULL = zeros */
   int64_t dout_stride[3];
   const float* dlast_state; /* (batch, dim, dstate) contiguous, optional */
-  /* backward outputs (contiguous) */
-  void* du;                 /* (batch, dim, seqlen), dtype */
-  void* ddelta;             /* (batch, dim, seqlen), dtype */
-  void* dz;                 /* (batch, dim, seqlen), dtype; required iff z != NULL */
+  /* backward outputs */
+  void* du;                 /* (batch, dim, seqlen), dtype, strides du_stride */
+  void* ddelta;             /* (batch, dim, seqlen), dtype, strides ddelta_stride */
+  void* dz;                 /* (batch, dim, seqlen), dtype, strides dz_stride; required iff z != NULL */
   float* dA;                /* (dim, dstate) */
   float* dB;                /* (batch, ngroups, seqlen, dstate) */
   float* dC;                /* (batch, ngroups, seqlen, dstate) */
   float* dD;                /* (dim); required iff D != NULL */
   float* ddelta_bias;       /* (dim); required iff delta_bias != NULL */
+  /* Element strides over (batch, dim, seqlen) of out, du, ddelta and dz; all
+     three zero = contiguous. A channel-contiguous layout (dim stride 1, the
+     transposed views Hugging Face's mixer passes) lets a caller hand the
+     result to a (batch, seqlen, dim) consumer without a copy. */
+  int64_t out_stride[3];
+  int64_t du_stride[3];
+  int64_t ddelta_stride[3];
+  int64_t dz_stride[3];
 } mcpu_scan_args;
 
 /* Bytes of the optional checkpoint buffer: the float32 scan state at the

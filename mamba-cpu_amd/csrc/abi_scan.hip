@@ -22,6 +22,14 @@ hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_p
 
 namespace {
 
+// An output's strides as given, or contiguous (batch, dim, seqlen) when all zero.
+void out_strides(const int64_t (&given)[3], int64_t dim, int64_t seqlen, int64_t (&s)[3]) {
+  const bool none = given[0] == 0 && given[1] == 0 && given[2] == 0;
+  s[0] = none ? dim * seqlen : given[0];
+  s[1] = none ? seqlen : given[1];
+  s[2] = none ? 1 : given[2];
+}
+
 int check_scan(const mcpu_scan_args* a) {
   if (a == nullptr) return fail(MCPU_ERR_INVALID, "selective_scan: null argument block");
   if (a->u == nullptr || a->delta == nullptr || a->A == nullptr || a->B == nullptr ||
@@ -40,8 +48,14 @@ int check_scan(const mcpu_scan_args* a) {
   const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16);
   if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
   for (int i = 0; i < 3; ++i)
-    if (a->u_stride[i] < 0 || a->delta_stride[i] < 0 || a->z_stride[i] < 0 || a->dout_stride[i] < 0)
+    if (a->u_stride[i] < 0 || a->delta_stride[i] < 0 || a->z_stride[i] < 0 || a->dout_stride[i] < 0 ||
+        a->out_stride[i] < 0 || a->du_stride[i] < 0 || a->ddelta_stride[i] < 0 || a->dz_stride[i] < 0)
       return fail(MCPU_ERR_INVALID, "selective_scan: negative stride");
+  int64_t so[3], sdu[3], sdd[3], sdz[3];
+  out_strides(a->out_stride, a->dim, a->seqlen, so);
+  out_strides(a->du_stride, a->dim, a->seqlen, sdu);
+  out_strides(a->ddelta_stride, a->dim, a->seqlen, sdd);
+  out_strides(a->dz_stride, a->dim, a->seqlen, sdz);
   for (int i = 0; i < 4; ++i)
     if (a->B_stride[i] < 0 || a->C_stride[i] < 0)
       return fail(MCPU_ERR_INVALID, "selective_scan: negative stride");
@@ -53,14 +67,17 @@ int check_scan(const mcpu_scan_args* a) {
   auto bc_span = [&](const int64_t (&s)[4]) { return 4 * (T * s[2] + 63 * s[3]); };
   const int64_t spans[] = {x_span(a->u_stride), x_span(a->delta_stride), x_span(a->z_stride),
                            x_span(a->dout_stride), bc_span(a->B_stride), bc_span(a->C_stride),
-                           4 * (ch * nblk * a->dstate + 63), esz * (ch * a->seqlen + T)};
+                           4 * (ch * nblk * a->dstate + 63), esz * (ch * a->seqlen + T),
+                           x_span(so), x_span(sdu), x_span(sdd), x_span(sdz)};
   for (int64_t sp : spans)
     if (sp >= 0xffffffffll)
       return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: strides or sizes too large for 32-bit tile offsets");
   // The staging cursors move by one 16-step block as a signed 32-bit byte step.
   const int64_t steps[] = {esz * kScanBlockT * a->u_stride[2], esz * kScanBlockT * a->delta_stride[2],
                            esz * kScanBlockT * a->z_stride[2], esz * kScanBlockT * a->dout_stride[2],
-                           4 * kScanBlockT * a->B_stride[2], 4 * kScanBlockT * a->C_stride[2]};
+                           4 * kScanBlockT * a->B_stride[2], 4 * kScanBlockT * a->C_stride[2],
+                           esz * kScanBlockT * so[2], esz * kScanBlockT * sdu[2],
+                           esz * kScanBlockT * sdd[2], esz * kScanBlockT * sdz[2]};
   for (int64_t st : steps)
     if (st > 0x7fffffffll)
       return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: time stride too large for 32-bit block steps");
@@ -93,6 +110,10 @@ ScanParams make_params(const mcpu_scan_args* a, int waves) {
     p.sz[i] = a->z_stride[i];
     p.sdo[i] = a->dout_stride[i];
   }
+  out_strides(a->out_stride, a->dim, a->seqlen, p.sout);
+  out_strides(a->du_stride, a->dim, a->seqlen, p.sdu);
+  out_strides(a->ddelta_stride, a->dim, a->seqlen, p.sdd);
+  out_strides(a->dz_stride, a->dim, a->seqlen, p.sdz);
   for (int i = 0; i < 4; ++i) {
     p.sB[i] = a->B_stride[i];
     p.sC[i] = a->C_stride[i];

@@ -45,21 +45,25 @@ __device__ __forceinline__ float conv_x(const ConvParams& p, const ConvRow& c, i
   return ld<T>(p.init, c.b * p.sinit[0] + c.d * p.sinit[1] + (p.width - 1 + s) * p.sinit[2]);
 }
 
-template <typename T>
+// WT: the width as a compile-time constant (2..5), or 0 for any width up to
+// kConvMaxW read from the parameters. With a fixed width the window and tap
+// loops unroll to exactly the taps that exist.
+template <typename T, int WT>
 __global__ void __launch_bounds__(256) conv_fwd_kernel(const ConvParams p) {
+  constexpr int MW = WT > 0 ? WT : kConvMaxW;
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
   if (tid >= p.batch * p.dim * p.R) return;
   const ConvRow c = conv_row(p, tid);
-  const int W = static_cast<int>(p.width);
-  float w[kConvMaxW];
+  const int W = WT > 0 ? WT : static_cast<int>(p.width);
+  float w[MW];
 #pragma unroll
-  for (int k = 0; k < kConvMaxW; ++k) w[k] = k < W ? p.w[c.d * W + k] : 0.f;
+  for (int k = 0; k < MW; ++k) w[k] = k < W ? p.w[c.d * W + k] : 0.f;
   const float bias = p.bias ? p.bias[c.d] : 0.f;
   for (int64_t ch = c.r; ch < p.nchunks; ch += p.R) {
     const int64_t t0 = ch * kConvT;
-    float win[kConvT + kConvMaxW - 1];
+    float win[kConvT + MW - 1];
 #pragma unroll
-    for (int i = 0; i < kConvT + kConvMaxW - 1; ++i) {
+    for (int i = 0; i < kConvT + MW - 1; ++i) {
       const int64_t s = t0 - (W - 1) + i;
       win[i] = (i < kConvT + W - 1 && s < p.seqlen) ? conv_x<T>(p, c, s) : 0.f;
     }
@@ -69,7 +73,7 @@ __global__ void __launch_bounds__(256) conv_fwd_kernel(const ConvParams p) {
       if (t >= p.seqlen) break;
       float acc = bias;
 #pragma unroll
-      for (int k = 0; k < kConvMaxW; ++k)
+      for (int k = 0; k < MW; ++k)
         if (k < W) acc = fmaf(w[k], win[i + k], acc);
       if (p.silu) acc = acc * sigmoid(acc);
       st<T>(p.out, c.b * p.sout[0] + c.d * p.sout[1] + t * p.sout[2], acc);
@@ -98,16 +102,17 @@ __global__ void __launch_bounds__(256) conv_final_states_kernel(const ConvParams
 // dX[s] goes to dx for s >= 0 and to dinitial_states for s < 0 (handled by the
 // thread of chunk 0). dw/dbias accumulate dpre[t] X[t-(W-1)+k] over this
 // thread's steps and are written as one partial per thread.
-template <typename T>
+template <typename T, int WT>
 __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
+  constexpr int MW = WT > 0 ? WT : kConvMaxW;
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
   if (tid >= p.batch * p.dim * p.R) return;
   const ConvRow c = conv_row(p, tid);
-  const int W = static_cast<int>(p.width);
+  const int W = WT > 0 ? WT : static_cast<int>(p.width);
   const int64_t L = p.seqlen;
-  float w[kConvMaxW], dw[kConvMaxW];
+  float w[MW], dw[MW];
 #pragma unroll
-  for (int k = 0; k < kConvMaxW; ++k) {
+  for (int k = 0; k < MW; ++k) {
     w[k] = k < W ? p.w[c.d * W + k] : 0.f;
     dw[k] = 0.f;
   }
@@ -123,21 +128,21 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
     const int nout = pre_chunk ? W - 1 : kConvT;
     // dpre for t in [s0, s0 + nout + W - 1), which needs X on
     // [s0 - (W-1), s0 + nout + W - 1).
-    float xw[kConvT + 2 * (kConvMaxW - 1)];
-    float dp[kConvT + kConvMaxW - 1];
+    float xw[kConvT + 2 * (MW - 1)];
+    float dp[kConvT + MW - 1];
 #pragma unroll
-    for (int i = 0; i < kConvT + 2 * (kConvMaxW - 1); ++i) {
+    for (int i = 0; i < kConvT + 2 * (MW - 1); ++i) {
       const int64_t s = s0 - (W - 1) + i;
       xw[i] = (i < nout + 2 * (W - 1) && s < L) ? conv_x<T>(p, c, s) : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < kConvT + kConvMaxW - 1; ++i) {
+    for (int i = 0; i < kConvT + MW - 1; ++i) {
       const int64_t t = s0 + i;
       float v = 0.f;
       if (i < nout + W - 1 && t >= 0 && t < L) {
         float pre = bias;
 #pragma unroll
-        for (int k = 0; k < kConvMaxW; ++k)
+        for (int k = 0; k < MW; ++k)
           if (k < W) pre = fmaf(w[k], xw[i + k], pre);
         const float go = ld<T>(p.dout, c.b * p.sdo[0] + c.d * p.sdo[1] + t * p.sdo[2]);
         if (p.silu) {
@@ -156,7 +161,7 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
         if (i < nout && s0 + i < L) {
           dbias += dp[i];
 #pragma unroll
-          for (int k = 0; k < kConvMaxW; ++k)
+          for (int k = 0; k < MW; ++k)
             if (k < W) dw[k] = fmaf(dp[i], xw[i + k], dw[k]);
         }
       }
@@ -168,7 +173,7 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
       if (i >= nout || s >= L) break;
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < kConvMaxW; ++k)
+      for (int k = 0; k < MW; ++k)
         if (k < W) acc = fmaf(w[k], dp[i + (W - 1) - k], acc);
       if (p.dfinal != nullptr && s >= fin0)
         acc += ld<T>(p.dfinal, (c.b * p.dim + c.d) * (W - 1) + (s - fin0));
@@ -181,25 +186,41 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
   }
   float* part = p.dw_part + ((c.b * p.R + c.r) * p.dim + c.d) * (W + 1);
 #pragma unroll
-  for (int k = 0; k < kConvMaxW; ++k)
+  for (int k = 0; k < MW; ++k)
     if (k < W) part[k] = dw[k];
   part[W] = dbias;
 }
 
-// dweight[d, k] / dbias[d] = sum over (batch, R) partials.
+// dweight[d, k] / dbias[d] = sum over the (batch, R or segment) partials.
+// A workgroup covers 64 consecutive (d, k) entries; its four waves each sum
+// every fourth partial (four loads in flight per lane), then combine in LDS.
 __global__ void __launch_bounds__(256) conv_reduce_dw_kernel(const float* __restrict__ part,
                                                              float* __restrict__ dw,
                                                              float* __restrict__ dbias,
                                                              int64_t nparts, int64_t dim,
                                                              int64_t width) {
-  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  __shared__ float s_acc[4][64];
+  const int lane = threadIdx.x & 63, q0 = threadIdx.x >> 6;
   const int64_t per = dim * (width + 1);
-  if (i >= per) return;
+  const int64_t i = blockIdx.x * 64ll + lane;
   float acc = 0.f;
-  for (int64_t q = 0; q < nparts; ++q) acc += part[q * per + i];
-  const int64_t d = i / (width + 1), k = i % (width + 1);
-  if (k < width) dw[d * width + k] = acc;
-  else if (dbias != nullptr) dbias[d] = acc;
+  if (i < per) {
+    int64_t q = q0;
+    for (; q + 12 < nparts; q += 16) {
+      const float a0 = part[q * per + i], a1 = part[(q + 4) * per + i];
+      const float a2 = part[(q + 8) * per + i], a3 = part[(q + 12) * per + i];
+      acc += (a0 + a1) + (a2 + a3);
+    }
+    for (; q < nparts; q += 4) acc += part[q * per + i];
+  }
+  s_acc[q0][lane] = acc;
+  __syncthreads();
+  if (q0 == 0 && i < per) {
+    const float total = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
+    const int64_t d = i / (width + 1), k = i % (width + 1);
+    if (k < width) dw[d * width + k] = total;
+    else if (dbias != nullptr) dbias[d] = total;
+  }
 }
 
 // Decode update (reference src/mamba_cpu/ops/causal_conv1d.py:56-85): one
@@ -478,17 +499,42 @@ static hipError_t launch_vt_dtype(const ConvParams& p, int dtype, bool bwd, hipS
 
 static unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
+// The chunked kernels, specialised for widths 2..5 (Mamba's is 4).
+template <typename T>
+static hipError_t launch_generic(const ConvParams& p, bool bwd, unsigned grid, hipStream_t st) {
+  switch (p.width) {
+#define MCPU_CONV_GEN(WW)                                                                     \
+  case WW:                                                                                    \
+    if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);  \
+    else hipLaunchKernelGGL((conv_fwd_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);      \
+    break;
+    MCPU_CONV_GEN(2)
+    MCPU_CONV_GEN(3)
+    MCPU_CONV_GEN(4)
+    MCPU_CONV_GEN(5)
+#undef MCPU_CONV_GEN
+    default:
+      if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, 0>), dim3(grid), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((conv_fwd_kernel<T, 0>), dim3(grid), dim3(256), 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+static hipError_t launch_generic_dtype(const ConvParams& p, int dtype, bool bwd, unsigned grid,
+                                       hipStream_t st) {
+  switch (dtype) {
+    case MCPU_F32: return launch_generic<float>(p, bwd, grid, st);
+    case MCPU_BF16: return launch_generic<bf16>(p, bwd, grid, st);
+    default: return launch_generic<f16>(p, bwd, grid, st);
+  }
+}
+
 hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
   if (n > 0 && p.vt) {
     if (hipError_t e = launch_vt_dtype(p, dtype, false, st)) return e;
   } else if (n > 0) {
-    switch (dtype) {
-      case MCPU_F32: hipLaunchKernelGGL(conv_fwd_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-      case MCPU_BF16: hipLaunchKernelGGL(conv_fwd_kernel<bf16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-      default: hipLaunchKernelGGL(conv_fwd_kernel<f16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-    }
-    if (hipError_t e = hipGetLastError()) return e;
+    if (hipError_t e = launch_generic_dtype(p, dtype, false, blocks_for(n), st)) return e;
   }
   const int64_t nf = p.final_states ? p.batch * p.dim * (p.width - 1) : 0;
   if (nf > 0) {
@@ -507,21 +553,16 @@ hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float
   if (n > 0 && p.vt) {
     if (hipError_t e = launch_vt_dtype(p, dtype, true, st)) return e;
     const int64_t per = p.dim * (p.width + 1);
-    hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(blocks_for(per)), dim3(256), 0, st, p.dw_part,
-                       dweight, dbias, p.batch * p.nseg, p.dim, p.width);
+    hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(static_cast<unsigned>((per + 63) / 64)), dim3(256),
+                       0, st, p.dw_part, dweight, dbias, p.batch * p.nseg, p.dim, p.width);
     return hipGetLastError();
   }
   if (n > 0) {
-    switch (dtype) {
-      case MCPU_F32: hipLaunchKernelGGL(conv_bwd_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-      case MCPU_BF16: hipLaunchKernelGGL(conv_bwd_kernel<bf16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-      default: hipLaunchKernelGGL(conv_bwd_kernel<f16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-    }
-    if (hipError_t e = hipGetLastError()) return e;
+    if (hipError_t e = launch_generic_dtype(p, dtype, true, blocks_for(n), st)) return e;
   }
   const int64_t per = p.dim * (p.width + 1);
-  hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(blocks_for(per)), dim3(256), 0, st, p.dw_part,
-                     dweight, dbias, p.batch * p.R, p.dim, p.width);
+  hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(static_cast<unsigned>((per + 63) / 64)), dim3(256), 0,
+                     st, p.dw_part, dweight, dbias, p.batch * p.R, p.dim, p.width);
   return hipGetLastError();
 }
 

@@ -108,13 +108,18 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   // Checkpointed state lane j of the current block.
   const char* ck_base = reinterpret_cast<const char*>(p.ckpt + (row0 * p.nblk + kl) * N);
   const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
-  // Per-lane outputs at step t0 + j of the current block; du, ddelta and dz
-  // are contiguous (batch, dim, seqlen) and share the offset.
-  const int64_t o_pos = (row0 * L + t_last) * static_cast<int64_t>(sizeof(Tx));
-  const uint32_t o_off = static_cast<uint32_t>(sizeof(Tx) * (crow * L + j));
-  char* o_du = static_cast<char*>(p.du) + o_pos;
-  char* o_dd = static_cast<char*>(p.ddelta) + o_pos;
-  char* o_dz = HAS_Z ? static_cast<char*>(p.dz) + o_pos : nullptr;
+  // Per-lane outputs at step t0 + j of the current block, each with its own
+  // strides: a uniform base (the workgroup's first channel at t0, moved one
+  // block back per block) plus a fixed per-lane offset.
+  constexpr int64_t esz = sizeof(Tx);
+  const int64_t cl = rc.g * p.dpg + rc.cl0;
+  char* o_du = static_cast<char*>(p.du) + esz * (rc.b * p.sdu[0] + cl * p.sdu[1] + t_last * p.sdu[2]);
+  char* o_dd = static_cast<char*>(p.ddelta) + esz * (rc.b * p.sdd[0] + cl * p.sdd[1] + t_last * p.sdd[2]);
+  char* o_dz = HAS_Z ? static_cast<char*>(p.dz) + esz * (rc.b * p.sdz[0] + cl * p.sdz[1] + t_last * p.sdz[2])
+                     : nullptr;
+  const uint32_t off_du = static_cast<uint32_t>(esz * (crow * p.sdu[1] + j * p.sdu[2]));
+  const uint32_t off_dd = static_cast<uint32_t>(esz * (crow * p.sdd[1] + j * p.sdd[2]));
+  const uint32_t off_dz = HAS_Z ? static_cast<uint32_t>(esz * (crow * p.sdz[1] + j * p.sdz[2])) : 0u;
 
   // Cross-wave dB/dC outputs of this thread: element e = (array, step, state).
   // T * NW is a multiple of 64, so the array is uniform over a wave.
@@ -342,13 +347,13 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     for (int s = 0; s < SPL; ++s) h0[s] = ck_ok[s] ? nh0[s] : 0.f;
     // Stores after the park, so waiting for the prefetch never waits for them.
     if (tv && rc.active) {
-      buf_st<Tx>(wave_rsrc(o_du), o_off, duv);
-      buf_st<Tx>(wave_rsrc(o_dd), o_off, ddt);
-      if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), o_off, dzv);
+      buf_st<Tx>(wave_rsrc(o_du), off_du, duv);
+      buf_st<Tx>(wave_rsrc(o_dd), off_dd, ddt);
+      if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), off_dz, dzv);
     }
-    o_du -= T * sizeof(Tx);
-    o_dd -= T * sizeof(Tx);
-    if (HAS_Z) o_dz -= T * sizeof(Tx);
+    o_du -= T * esz * p.sdu[2];
+    o_dd -= T * esz * p.sdd[2];
+    if (HAS_Z) o_dz -= T * esz * p.sdz[2];
     __syncthreads();
 
     // Cross-wave sum of this block's dB/dC and the workgroup's partial.

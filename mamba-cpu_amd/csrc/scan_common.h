@@ -57,6 +57,7 @@ struct ScanParams {
   int64_t nblk;         // ceil(seqlen / 16)
   int64_t nblk_c;       // channel blocks per slice: ceil(dpg / (4 W))
   int64_t su[3], sdl[3], sz[3], sdo[3];
+  int64_t sout[3], sdu[3], sdd[3], sdz[3];  // output strides (contiguous when the caller gave none)
   int64_t sB[4], sC[4];
   int softplus;
   // Time chunks: the sequence is cut into nchunk chunks of chunk_blocks

@@ -82,7 +82,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // row, moved one block at a time) plus a fixed 32-bit per-lane offset.
   const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
   const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);
-  const uint32_t o_off = static_cast<uint32_t>(sizeof(Tx) * (crow * L + j));
+  const uint32_t o_off = static_cast<uint32_t>(sizeof(Tx) * (crow * L + j));  // ysave (contiguous)
+  // out: strides p.sout, uniform base per block + per-lane offset.
+  char* const out0 = static_cast<char*>(p.out) +
+      static_cast<int64_t>(sizeof(Tx)) * (rc.b * p.sout[0] + (rc.g * p.dpg + rc.cl0) * p.sout[1]);
+  const int64_t out_ts = static_cast<int64_t>(sizeof(Tx)) * p.sout[2];
+  const uint32_t out_off = static_cast<uint32_t>(sizeof(Tx) * (crow * p.sout[1] + j * p.sout[2]));
   const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
   float dts = 0.f;  // sum of dt over this lane's steps (summary pass)
 
@@ -211,7 +216,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     if (WRITE_OUT && tv && rc.active) {
       const int64_t o_pos = (row0 * L + t0) * static_cast<int64_t>(sizeof(Tx));
       if (p.ysave != nullptr) buf_st<Tx>(wave_rsrc(static_cast<char*>(p.ysave) + o_pos), o_off, y);
-      buf_st<Tx>(wave_rsrc(static_cast<char*>(p.out) + o_pos), o_off, yg);
+      buf_st<Tx>(wave_rsrc(out0 + t0 * out_ts), out_off, yg);
     }
     if (ck != nullptr && rc.active && k + 1 < kb1) {
 #pragma unroll

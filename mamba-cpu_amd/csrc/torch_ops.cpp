@@ -158,11 +158,12 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> scan_fwd_impl(
   validate_scan(name, u, delta, A, B, C, D, z, bias);
   c10::DeviceGuard guard(u.device());
   const int64_t batch = u.size(0), dim = u.size(1);
-  Tensor out = at::empty(u.sizes(), u.options());
+  Tensor out = like_x(u);
   Tensor last = at::empty({batch, dim, A.size(1)}, u.options().dtype(at::kFloat));
   Tensor ckpt, ysave;
   mcpu_scan_args a = scan_args(u, delta, A, B, C, D, z, bias, softplus);
   a.out = out.data_ptr();
+  strides3(a.out_stride, out);
   a.last_state = static_cast<float*>(last.data_ptr());
   if (save) {
     ckpt = at::empty(ckpt_shape(u, A), u.options().dtype(at::kFloat));
@@ -225,13 +226,14 @@ Grads8 scan_bwd_impl(const char* name, const Tensor& u, const Tensor& delta, con
                           ysave->is_contiguous() && has(z),
                       name, " expects the y written by selective_scan_fwd_ckpt");
   c10::DeviceGuard guard(u.device());
-  Tensor du = at::empty(u.sizes(), u.options());
-  Tensor ddelta = at::empty(delta.sizes(), delta.options());
+  // Gradients take their input's layout (channel-contiguous stays so).
+  Tensor du = like_x(u);
+  Tensor ddelta = like_x(delta);
   Tensor dA = at::empty(A.sizes(), A.options());
   Tensor dB = at::empty(B.sizes(), B.options());
   Tensor dC = at::empty(C.sizes(), C.options());
   Tensor dD = at::empty({dim}, A.options());
-  Tensor dz = has(z) ? at::empty(z->sizes(), z->options()) : at::empty({0}, u.options());
+  Tensor dz = has(z) ? like_x(*z) : at::empty({0}, u.options());
   Tensor dbias = at::empty({dim}, A.options());
   mcpu_scan_args a = scan_args(u, delta, A, B, C, D, z, bias, softplus);
   a.dout = dout.data_ptr();
@@ -242,6 +244,9 @@ Grads8 scan_bwd_impl(const char* name, const Tensor& u, const Tensor& delta, con
   a.du = du.data_ptr();
   a.ddelta = ddelta.data_ptr();
   a.dz = has(z) ? dz.data_ptr() : nullptr;
+  strides3(a.du_stride, du);
+  strides3(a.ddelta_stride, ddelta);
+  if (has(z)) strides3(a.dz_stride, dz);
   a.dA = static_cast<float*>(dA.data_ptr());
   a.dB = static_cast<float*>(dB.data_ptr());
   a.dC = static_cast<float*>(dC.data_ptr());

@@ -38,15 +38,24 @@ def _ckpt_shape(u, A):
     return (batch, dim, (seqlen + _BLOCK_T - 1) // _BLOCK_T, A.shape[1])
 
 
+def _like_x(x):
+    """A (batch, dim, seqlen) result laid out like x, as the operators allocate
+    it: channel-contiguous when x is, contiguous otherwise."""
+    if x.dim() == 3 and x.stride(1) == 1 and x.stride(2) != 1:
+        b, d, l = x.shape
+        return torch.empty_strided((b, d, l), (d * l, 1, d), dtype=x.dtype, device=x.device)
+    return x.new_empty(x.shape)
+
+
 def _fwd_fake(u, A):
-    return u.new_empty(u.shape), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32)
+    return _like_x(u), u.new_empty(u.shape[0], u.shape[1], A.shape[1], dtype=torch.float32)
 
 
 def _bwd_fake(u, delta, A, B, C, z):
     return (
-        u.new_empty(u.shape), delta.new_empty(delta.shape), A.new_empty(A.shape),
+        _like_x(u), _like_x(delta), A.new_empty(A.shape),
         B.new_empty(B.shape), C.new_empty(C.shape), A.new_empty(u.shape[1]),
-        z.new_empty(z.shape) if z is not None else u.new_empty(0), A.new_empty(u.shape[1]),
+        _like_x(z) if z is not None else u.new_empty(0), A.new_empty(u.shape[1]),
     )
 
 

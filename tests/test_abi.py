@@ -217,3 +217,74 @@ def test_public_api_surface():
         assert callable(getattr(mamba_cpu, name))
     assert hasattr(torch.ops.mamba_cpu, "selective_scan_fwd")
     assert hasattr(torch.ops.mamba_cpu, "selective_scan_bwd")
+
+
+@pytest.mark.gpu
+def test_scan_writes_outputs_through_their_strides():
+    """out, du, ddelta and dz land at the strides the caller gives: here
+    interleaved halves of (batch, seqlen, 2 dim) buffers, as a fused mixer
+    writes dz next to the conv's dx. Compared with the contiguous results of
+    the same call."""
+    from mamba_cpu import _C
+
+    torch.manual_seed(3)
+    b, d, l, n = 2, 40, 53, 16
+    dev = "cuda"
+    u, delta, z, dout = (torch.randn(b, d, l, device=dev) for _ in range(4))
+    delta = delta.abs() * 0.1
+    A = -torch.rand(d, n, device=dev) - 0.5
+    Bk, Ck = torch.randn(b, 1, l, n, device=dev), torch.randn(b, 1, l, n, device=dev)
+    D = torch.randn(d, device=dev)
+
+    def args():
+        a = _C.ScanArgs()
+        a.u, a.delta, a.A, a.B, a.C, a.D, a.z = (t.data_ptr() for t in (u, delta, A, Bk, Ck, D, z))
+        a.batch, a.dim, a.seqlen, a.dstate, a.ngroups = b, d, l, n, 1
+        a.delta_softplus, a.dtype = 1, _C.MCPU_F32
+        a.u_stride[:] = a.delta_stride[:] = a.z_stride[:] = a.dout_stride[:] = u.stride()
+        a.B_stride[:], a.C_stride[:] = Bk.stride(), Ck.stride()
+        a.dout = dout.data_ptr()
+        return a
+
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(fwd, a):
+        if fwd:
+            ws_n = _C.lib.mcpu_selective_scan_fwd_workspace_size(ctypes.byref(a))
+        else:
+            ws_n = _C.lib.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a))
+        ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device=dev)
+        fn = _C.lib.mcpu_selective_scan_fwd if fwd else _C.lib.mcpu_selective_scan_bwd
+        rc = fn(ctypes.byref(a), ws.data_ptr(), ws_n, stream)
+        assert rc == 0, _C.lib.mcpu_last_error().decode()
+        torch.cuda.synchronize()
+
+    small = dict(dA=torch.empty(d, n, device=dev), dB=torch.zeros(b, 1, l, n, device=dev),
+                 dC=torch.zeros(b, 1, l, n, device=dev), dD=torch.empty(d, device=dev))
+    # Contiguous reference results.
+    ref = {k: torch.empty(b, d, l, device=dev) for k in ("out", "du", "ddelta", "dz")}
+    a = args()
+    a.out = ref["out"].data_ptr()
+    call(True, a)
+    a = args()
+    a.du, a.ddelta, a.dz = ref["du"].data_ptr(), ref["ddelta"].data_ptr(), ref["dz"].data_ptr()
+    for k, t in small.items():
+        setattr(a, k, t.data_ptr())
+    call(False, a)
+    # Strided: each output is one half of a (b, l, 2d) buffer, the other half a sentinel.
+    bufs = {k: torch.full((b, l, 2 * d), 7.0, device=dev) for k in ref}
+    views = {k: bufs[k][..., d:].transpose(1, 2) for k in ref}
+    a = args()
+    a.out = views["out"].data_ptr()
+    a.out_stride[:] = views["out"].stride()
+    call(True, a)
+    a = args()
+    for k, f in (("du", "du"), ("ddelta", "ddelta"), ("dz", "dz")):
+        setattr(a, f, views[k].data_ptr())
+        getattr(a, f + "_stride")[:] = views[k].stride()
+    for k, t in small.items():
+        setattr(a, k, t.data_ptr())
+    call(False, a)
+    for k in ref:
+        torch.testing.assert_close(views[k], ref[k], rtol=0, atol=0, msg=lambda m: f"{k}: {m}")
+        assert (bufs[k][..., :d] == 7.0).all(), f"{k} wrote outside its view"

@@ -25,7 +25,7 @@ def close(got, want, rtol, atol, name=""):
                                rtol=rtol, atol=atol, err_msg=name)
 
 
-@pytest.mark.parametrize("width", [2, 3, 4])
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7])
 @pytest.mark.parametrize("activation", [None, "silu"])
 @pytest.mark.parametrize("has_bias", [False, True])
 def test_matches_oracle(width, activation, has_bias):
@@ -119,7 +119,7 @@ def test_rejects_unsupported_args():
                              cache_seqlens=torch.zeros(2, dtype=torch.int32, device=DEV))
 
 
-@pytest.mark.parametrize("width", [2, 4])
+@pytest.mark.parametrize("width", [1, 2, 4, 7])
 @pytest.mark.parametrize("activation", [None, "silu"])
 @pytest.mark.parametrize("with_init", [False, True])
 @pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
@@ -234,3 +234,21 @@ def test_vector_path_no_activation_no_bias():
     dx, dw, _, _ = O.causal_conv1d_bwd(x, w, None, None, G, None)
     close(x.grad, dx, 1e-4, 1e-4, "dx")
     close(w.grad, dw, 1e-4, 1e-4, "dweight")
+
+
+@pytest.mark.parametrize("batch,parts_per_row", [(1, 1), (3, 9), (5, 16)])
+def test_dweight_reduction_over_many_partials(batch, parts_per_row):
+    """dweight/dbias sum one partial per (batch, time chunk): every count of
+    partials, including ones not a multiple of the reduction's unroll."""
+    torch.manual_seed(1)
+    d, width = 70, 4
+    l = 8 * parts_per_row + 3  # ragged last chunk, off the vector path
+    x = torch.randn(batch, l, d, device=DEV).transpose(1, 2).requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    out = causal_conv1d_fn(x, w, bias, activation="silu")
+    G = torch.randn(batch, d, l, device=DEV)
+    (out * G).sum().backward()
+    _, dw, db, _ = O.causal_conv1d_bwd(x, w, bias, None, G, "silu")
+    close(w.grad, dw, 1e-4, 1e-4, "dweight")
+    close(bias.grad, db, 1e-4, 1e-4, "dbias")

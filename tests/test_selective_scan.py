@@ -251,6 +251,44 @@ def test_hf_style_strided_inputs_match_contiguous():
     close(got, out_ref, 1e-4, 1e-5)
 
 
+@pytest.mark.parametrize("b,l", [(2, 70), (1, 4000)])
+def test_channel_contiguous_outputs_and_gradients(b, l):
+    """Channel-contiguous u and z (Hugging Face's transposed views) give a
+    channel-contiguous out, du and dz, so the (b, l, d) consumers downstream
+    need no copy; values equal the contiguous path's exactly (same kernels,
+    only the addresses differ). (1, 4000) takes the time-chunked passes."""
+    torch.manual_seed(0)
+    d, n, r = 48, 16, 5
+    xz = torch.randn(b, l, 2 * d, device=DEV)
+    proj = torch.randn(b, l, r + 2 * n, device=DEV)
+    delta0 = torch.rand(b, d, l, device=DEV) - 2
+    A0 = -torch.rand(d, n, device=DEV) - 0.5
+    D0, bias0 = torch.randn(d, device=DEV), torch.rand(d, device=DEV)
+    G = torch.randn(b, d, l, device=DEV)
+
+    def run(strided):
+        xz_, proj_ = xz.clone().requires_grad_(), proj.clone().requires_grad_()
+        delta, A, D, bias = (t.clone().requires_grad_() for t in (delta0, A0, D0, bias0))
+        u, z = xz_[..., :d].transpose(1, 2), xz_[..., d:].transpose(1, 2)
+        B, C = proj_[..., r:r + n].transpose(1, 2), proj_[..., r + n:].transpose(1, 2)
+        if not strided:
+            u, z, B, C = (t.contiguous() for t in (u, z, B, C))
+        out = selective_scan_fn(u, delta, A, B, C, D, z, bias, True)
+        (out * G).sum().backward()
+        return out, xz_.grad, proj_.grad, delta.grad, A.grad, D.grad, bias.grad
+
+    got, want = run(True), run(False)
+    assert got[0].transpose(1, 2).is_contiguous()
+    for name, g, w in zip(["out", "dxz", "dproj", "ddelta", "dA", "dD", "dbias"], got, want):
+        torch.testing.assert_close(g, w, rtol=0, atol=0, msg=lambda m: f"{name}: {m}")
+    # The operator itself returns du and dz in their inputs' layout.
+    u, z = xz[..., :d].transpose(1, 2), xz[..., d:].transpose(1, 2)
+    Bk, Ck = proj[..., r:r + n][:, None], proj[..., r + n:][:, None]
+    grads = torch.ops.mamba_cpu.selective_scan_bwd(u, delta0, A0, Bk, Ck, D0, z, bias0, True, G, None)
+    assert grads[0].stride(1) == 1 and grads[6].stride(1) == 1
+    assert grads[1].is_contiguous()
+
+
 @pytest.mark.parametrize("dstate", [24, 32, 64])
 def test_larger_dstate(dstate):
     inp = make_inputs(2, 8, 40, dstate, None, True, True, True, torch.float32, requires_grad=True)
