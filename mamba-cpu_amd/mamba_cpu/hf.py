@@ -10,8 +10,10 @@ transformers (>= 5) resolves `mamba_selective_scan`,
 `mamba_inner_fn` from module globals at call time, and patch_transformers()
 wraps those globals. The wrappers route calls whose first tensor is on a ROCm
 GPU ("cuda" device type) to this package's gfx950 custom ops; tensors on other
-devices keep transformers' own path. `mamba_inner_fn` answers None so the
-mixer takes its unfused path, which calls the four ops above.
+devices keep transformers' own path. `mamba_inner_fn`, which the reference
+answers with None (so its mixers always take their unfused path), is the
+fused mixer of mamba_cpu.ops.mamba_inner for float32 models on the GPU, and
+None otherwise.
 """
 
 import functools
@@ -23,6 +25,7 @@ from mamba_cpu.ops import (
     selective_scan_fn,
     selective_state_update,
 )
+from mamba_cpu.ops.mamba_inner import fused_path_supported, mamba_inner_fn
 
 SUPPORTED_MODELS = ("mamba", "falcon_mamba", "jamba")
 _DEVICE_TYPE = "cuda"  # ROCm GPUs report the "cuda" device type in PyTorch
@@ -58,8 +61,26 @@ def _conv_update(x, conv_state, weight, bias=None, activation=None, **kwargs):
     return causal_conv1d_update(x, conv_state, weight, bias, activation)
 
 
-def _no_fused_path(*args, **kwargs):
-    return None  # the mixer takes its unfused path when mamba_inner_fn returns None
+def _inner(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+           out_proj_bias, A, B=None, C=None, D=None, delta_bias=None, delta_softplus=True,
+           b_rms_weight=None, c_rms_weight=None, dt_rms_weight=None, b_c_dt_rms_eps=1e-6, **kwargs):
+    # The fused mixer (mamba_cpu.ops.mamba_inner) where it applies; None
+    # otherwise, and the mixer takes its unfused path, which calls the four
+    # ops above (the reference always answers None, hf.py:59-60).
+    # FalconMamba passes norm weights: its unfused path normalises dt before
+    # dt_proj and ignores the weights, where mamba_inner_fn's norms (as in
+    # mamba_ssm) normalise delta after it, so that model keeps the unfused
+    # path, which is the computation the reference runs.
+    if any(w is not None for w in (b_rms_weight, c_rms_weight, dt_rms_weight)):
+        return None
+    if not fused_path_supported(xz, conv1d_weight, x_proj_weight, delta_proj_weight, out_proj_weight,
+                                A, B, C):
+        return None
+    return mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                          out_proj_weight, out_proj_bias, A, D=D, delta_bias=delta_bias,
+                          delta_softplus=delta_softplus, b_rms_weight=b_rms_weight,
+                          c_rms_weight=c_rms_weight, dt_rms_weight=dt_rms_weight,
+                          b_c_dt_rms_eps=b_c_dt_rms_eps)
 
 
 _OPS = {
@@ -67,7 +88,7 @@ _OPS = {
     "mamba_selective_state_update": _state_update,
     "causal_conv1d_fn": _conv,
     "causal_conv1d_update": _conv_update,
-    "mamba_inner_fn": _no_fused_path,
+    "mamba_inner_fn": _inner,
 }
 
 

@@ -61,9 +61,15 @@ def patched(monkeypatch):
 
 @pytest.fixture
 def scan_calls(monkeypatch):
+    """Counts scans through this package: the scan op, or the fused mixer
+    (mamba_inner_fn) that transformers' Mamba mixers call in training."""
     calls = []
     monkeypatch.setattr(
         mamba_cpu.hf, "selective_scan_fn", lambda *a: calls.append(1) or selective_scan_fn(*a)
+    )
+    fused = mamba_cpu.hf.mamba_inner_fn
+    monkeypatch.setattr(
+        mamba_cpu.hf, "mamba_inner_fn", lambda *a, **k: calls.append(2) or fused(*a, **k)
     )
     return calls
 
@@ -130,6 +136,8 @@ def test_training_gradients_match(name, patched, scan_calls):
 
     got, want = patched(grads)
     assert scan_calls and got.keys() == want.keys()
+    if name == "mamba":  # FalconMamba keeps its unfused path (its norms differ from the fused ones)
+        assert 2 in scan_calls, "the fused mixer was not used"
     for k in want:
         torch.testing.assert_close(got[k], want[k], rtol=1e-3, atol=1e-4, msg=lambda m: f"{k}: {m}")
 

@@ -1,0 +1,100 @@
+"""The fused mixer (mamba_cpu.ops.mamba_inner_fn) against the same mixer
+composed from the pure-torch reference functions in float64 on the CPU
+(mamba_cpu.reference: the reference's reference.py restated), forward and
+every gradient, with and without mamba_ssm's optional RMS norms (B and C
+over dstate, delta over dim).
+Tolerances: output rtol 1e-4; gradients rtol 1e-3 after scaling by the
+gradient's magnitude."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mamba_cpu import mamba_inner_fn
+from mamba_cpu.reference import causal_conv1d_ref, selective_scan_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rms(x, w, eps):
+    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+
+def reference_inner(xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, out_proj_b, A, D, delta_bias,
+                    rms_w=None, eps=1e-6):
+    d = xz.shape[1] // 2
+    R, N = dt_proj_w.shape[1], A.shape[1]
+    x, z = xz[:, :d], xz[:, d:]
+    conv = causal_conv1d_ref(x, conv_w.reshape(d, -1), conv_b, activation="silu")
+    dt, B, C = F.linear(conv.transpose(1, 2), x_proj_w).split([R, N, N], dim=-1)
+    delta = F.linear(dt, dt_proj_w)
+    if rms_w is not None:  # mamba_ssm's norms: B, C over dstate, delta over dim
+        delta, B, C = _rms(delta, rms_w[2], eps), _rms(B, rms_w[0], eps), _rms(C, rms_w[1], eps)
+    delta = delta.transpose(1, 2)
+    y = selective_scan_ref(conv, delta, A, B.transpose(1, 2), C.transpose(1, 2), D, z, delta_bias, True)
+    return F.linear(y.transpose(1, 2), out_proj_w, out_proj_b)
+
+
+def make(b, d, l, N, R, Dm, width, rms, bias, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s, sc=1.0: torch.randn(*s, generator=g, dtype=torch.float64) * sc  # noqa: E731
+    p = dict(
+        xz=r(b, l, 2 * d).transpose(1, 2),  # transformers' transposed view of in_proj's output
+        conv_w=r(d, 1, width, sc=0.5), conv_b=r(d, sc=0.3) if bias else None,
+        x_proj_w=r(R + 2 * N, d, sc=d ** -0.5), dt_proj_w=r(d, R, sc=R ** -0.5),
+        out_proj_w=r(Dm, d, sc=d ** -0.5), out_proj_b=r(Dm, sc=0.1) if bias else None,
+        A=-torch.exp(torch.rand(d, N, generator=g, dtype=torch.float64) * 2),
+        D=r(d), delta_bias=torch.rand(d, generator=g, dtype=torch.float64) - 3,
+    )
+    rms_w = [1 + 0.1 * r(N), 1 + 0.1 * r(N), 1 + 0.1 * r(d)] if rms else None
+    return p, rms_w
+
+
+@pytest.mark.parametrize("b,d,l,rms,bias", [(2, 24, 37, False, True), (2, 40, 64, True, True),
+                                            (3, 16, 19, False, False), (1, 64, 3000, False, True)])
+def test_fused_mixer_matches_reference(b, d, l, rms, bias):
+    N, R, Dm, width = 8, 4, 16, 4
+    p, rms_w = make(b, d, l, N, R, Dm, width, rms, bias)
+    names = [k for k, v in p.items() if v is not None]
+    cpu = {k: (v.clone().requires_grad_() if v is not None else None) for k, v in p.items()}
+    cpu_rms = [w.clone().requires_grad_() for w in rms_w] if rms else None
+    want = reference_inner(**cpu, rms_w=cpu_rms)
+    G = torch.randn(want.shape, generator=torch.Generator().manual_seed(9), dtype=torch.float64)
+    (want * G).sum().backward()
+
+    gpu = {}
+    for k, v in p.items():
+        if v is None:
+            gpu[k] = None
+        elif k == "xz":  # keep the transposed-view layout on the GPU
+            gpu[k] = v.transpose(1, 2).float().to(DEV).transpose(1, 2).detach().requires_grad_()
+        else:
+            gpu[k] = v.float().to(DEV).requires_grad_()
+    gpu_rms = [w.float().to(DEV).requires_grad_() for w in rms_w] if rms else [None] * 3
+    got = mamba_inner_fn(gpu["xz"], gpu["conv_w"], gpu["conv_b"], gpu["x_proj_w"], gpu["dt_proj_w"],
+                         gpu["out_proj_w"], gpu["out_proj_b"], gpu["A"], None, None, gpu["D"],
+                         gpu["delta_bias"], delta_softplus=True, b_rms_weight=gpu_rms[0],
+                         c_rms_weight=gpu_rms[1], dt_rms_weight=gpu_rms[2])
+    (got * G.float().to(DEV)).sum().backward()
+    np.testing.assert_allclose(got.detach().cpu().double().numpy(), want.detach().numpy(),
+                               rtol=1e-4, atol=1e-4)
+    pairs = [(k, gpu[k], cpu[k]) for k in names]
+    if rms:
+        pairs += [(f"rms{i}", gpu_rms[i], cpu_rms[i]) for i in range(3)]
+    for k, g_, c_ in pairs:
+        gg, cg = g_.grad.detach().cpu().double(), c_.grad
+        scale = max(1.0, float(cg.abs().max()))
+        np.testing.assert_allclose((gg / scale).numpy(), (cg / scale).numpy(), rtol=1e-3, atol=1e-4,
+                                   err_msg=k)
+    # in_proj's gradient comes back in (batch, seqlen, 2 dim) order: no copy before in_proj.
+    assert gpu["xz"].grad.transpose(1, 2).is_contiguous()
+
+
+def test_rejects_input_independent_bc():
+    p, _ = make(1, 8, 5, 4, 2, 8, 4, False, True)
+    g = {k: v.float().to(DEV) if v is not None else None for k, v in p.items()}
+    with pytest.raises(NotImplementedError):
+        mamba_inner_fn(g["xz"], g["conv_w"], g["conv_b"], g["x_proj_w"], g["dt_proj_w"], g["out_proj_w"],
+                       g["out_proj_b"], g["A"], torch.zeros(8, 4, device=DEV), None, g["D"])
