@@ -481,6 +481,35 @@ def counter_pass(torch, dev, inputs, gout):
     print("counter pass done", flush=True)
 
 
+def model_pass(torch, dev, what):
+    """A short fixed run of the Mamba-130M architecture for kernel traces
+    (rocprofv3 --kernel-trace): `train` = 3 warm-up + 5 training steps at
+    4 x 256; `decode` = the 4 x 16 prompt, then 64 graph-replayed greedy
+    steps."""
+    import transformers
+
+    import mamba_cpu.decode
+    import mamba_cpu.hf
+
+    mamba_cpu.hf.patch_transformers()
+    torch.manual_seed(0)
+    cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
+                                   conv_kernel=4, vocab_size=50280)
+    model = transformers.MambaForCausalLM(cfg).to(dev)
+    if what == "train":
+        model.train()
+        ids = torch.randint(0, 50280, (4, 256), device=dev)
+        for _ in range(8):
+            model(ids, labels=ids).loss.backward()
+            model.zero_grad(set_to_none=True)
+    else:
+        model.eval()
+        ids = torch.randint(0, 50280, (4, 16), device=dev)
+        mamba_cpu.decode.greedy_generate(model, ids, 64)
+    torch.cuda.synchronize()
+    print(f"model pass ({what}) done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -491,6 +520,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
     ap.add_argument("--counter-pass", action="store_true",
                     help="only run 3 x (forward op, backward op, 256 MiB copy) for rocprofv3 --pmc")
+    ap.add_argument("--model-pass", choices=["train", "decode"],
+                    help="only run a short Mamba-130M train or graph-decode sequence for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
@@ -504,6 +535,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.model_pass:
+        model_pass(torch, dev, args.model_pass)
+        return
     inputs, gout = make_inputs(torch, dev)
     if args.counter_pass:
         counter_pass(torch, dev, inputs, gout)
