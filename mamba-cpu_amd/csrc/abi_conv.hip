@@ -48,10 +48,13 @@ ConvParams make_conv(const mcpu_conv_args* a) {
   return p;
 }
 
-// Launch shape of the time-contiguous fast path: 8 steps per thread; a row
-// segment is 64, 128 or 256 threads (one to four whole waves).
-void conv_vt_shape(ConvParams& p) {
-  const int64_t threads = p.seqlen / kConvVTSteps;
+// Steps per thread of the time-contiguous fast path: 32 bytes of each tensor.
+int conv_vt_steps(int dtype) { return dtype == MCPU_F32 ? kConvVTSteps : 2 * kConvVTSteps; }
+
+// Launch shape of the time-contiguous fast path: `steps` steps per thread; a
+// row segment is 64, 128 or 256 threads (one to four whole waves).
+void conv_vt_shape(ConvParams& p, int steps) {
+  const int64_t threads = p.seqlen / steps;
   if (threads >= 256) {
     p.tpr = 256;
     p.nseg = (threads + 255) / 256;
@@ -71,8 +74,8 @@ bool vt_operand(const void* ptr, const int64_t (&s)[3], int dtype) {
 }
 
 bool vt_ok(const ConvParams& p, int dtype, bool bwd) {
-  if (p.width < 2 || p.width > 5 || p.seqlen < kConvVTSteps || p.seqlen % kConvVTSteps != 0)
-    return false;
+  const int steps = conv_vt_steps(dtype);
+  if (p.width < 2 || p.width > 5 || p.seqlen < steps || p.seqlen % steps != 0) return false;
   if (!vt_operand(p.x, p.sx, dtype)) return false;
   if (!bwd) return vt_operand(p.out, p.sout, dtype);
   return vt_operand(p.dout, p.sdo, dtype) && vt_operand(p.dx, p.sdx, dtype);
@@ -80,7 +83,7 @@ bool vt_ok(const ConvParams& p, int dtype, bool bwd) {
 
 size_t conv_ws(const ConvParams& p) {
   ConvParams q = p;
-  conv_vt_shape(q);
+  conv_vt_shape(q, kConvVTSteps);  // the fewest steps per thread: the most segments
   const int64_t parts = q.nseg > p.R ? q.nseg : p.R;
   return align_up(sizeof(float) * p.batch * parts * p.dim * (p.width + 1));
 }
@@ -99,7 +102,7 @@ extern "C" int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream) {
   p.out = a->out;
   p.final_states = a->final_states;
   p.vt = vt_ok(p, a->dtype, false);
-  if (p.vt) conv_vt_shape(p);
+  if (p.vt) conv_vt_shape(p, conv_vt_steps(a->dtype));
   return hip_status(conv_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
                     "causal_conv1d_fwd launch");
 }
@@ -132,7 +135,7 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
   p.dinit = a->dinitial_states;
   p.dw_part = static_cast<float*>(workspace);
   p.vt = vt_ok(p, a->dtype, true);
-  if (p.vt) conv_vt_shape(p);
+  if (p.vt) conv_vt_shape(p, conv_vt_steps(a->dtype));
   if (a->batch == 0 || a->dim == 0) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (int rc = zero_f32(a->dweight, a->dim * a->width, st)) return rc;

@@ -260,14 +260,16 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
 
 // ---- Time-contiguous fast path ------------------------------------------------
 // For x, out, dout and dx with unit time stride, rows aligned to 4 elements and
-// seqlen a multiple of 8: each thread owns 8 consecutive steps of one
-// (batch, channel) row and moves them with 16-byte (fp32) or 8-byte (16-bit)
-// vector loads and stores; the W-1 inputs before its first step (and, in the
-// backward, the W-1 steps after its last) are re-read from the neighbouring
-// thread's vector, which the cache serves. A workgroup covers `rpw` rows of
-// `tpr` threads each (short rows) or one 2048-step segment of a row (long
-// rows), so a row segment never straddles a wave.
-constexpr int kConvVT = kConvVTSteps;
+// seqlen a multiple of VT: each thread owns VT consecutive steps of one
+// (batch, channel) row (VT = 8 for fp32, 16 for 16-bit types, so a thread
+// moves 32 bytes of each tensor either way) with 16-byte (fp32) or 8-byte
+// (16-bit) vector loads and stores; the W-1 inputs before its first step (and,
+// in the backward, the W-1 steps after its last) are re-read from the
+// neighbouring thread's vector, which the cache serves. A workgroup covers
+// `rpw` rows of `tpr` threads each (short rows) or one 256 * VT-step segment of
+// a row (long rows), so a row segment never straddles a wave.
+template <typename T>
+constexpr int conv_vt_of() { return sizeof(T) == 4 ? 8 : 16; }
 
 template <typename T>
 __device__ __forceinline__ void ld4(const void* base, int64_t idx, float* v) {
@@ -292,6 +294,9 @@ template <typename T>
 __device__ __forceinline__ void st4(void* base, int64_t idx, const float* v) {
   if constexpr (sizeof(T) == 4) {
     *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (std::is_same_v<T, bf16>) {
+    *reinterpret_cast<uint2*>(static_cast<T*>(base) + idx) =
+        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   } else {
     uint32_t h[4];
 #pragma unroll
@@ -307,9 +312,13 @@ struct ConvTile {
   bool active;    // the thread has steps to do
 };
 
+template <int VT>
 __device__ __forceinline__ ConvTile conv_tile(const ConvParams& p, int tid) {
   ConvTile g;
-  const int lt = tid & (p.tpr - 1), sub = tid / p.tpr;
+  // A row segment is whole waves (tpr >= 64), so the row is wave-uniform and
+  // its (batch, channel) split stays in the scalar unit.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lt = tid & (p.tpr - 1), sub = (wave * 64) / p.tpr;
   int64_t row;
   if (p.nseg > 1) {
     row = blockIdx.x / p.nseg;
@@ -318,7 +327,7 @@ __device__ __forceinline__ ConvTile conv_tile(const ConvParams& p, int tid) {
     row = static_cast<int64_t>(blockIdx.x) * p.rpw + sub;
     g.seg = 0;
   }
-  g.t0 = (g.seg * p.tpr + lt) * kConvVT;
+  g.t0 = (g.seg * p.tpr + lt) * VT;
   const int64_t rows = p.batch * p.dim;
   g.active = row < rows && g.t0 < p.seqlen;
   if (row >= rows) row = rows - 1;
@@ -330,7 +339,8 @@ __device__ __forceinline__ ConvTile conv_tile(const ConvParams& p, int tid) {
 
 template <typename T, int W>
 __global__ void __launch_bounds__(256) conv_fwd_vt_kernel(const ConvParams p) {
-  const ConvTile g = conv_tile(p, threadIdx.x);
+  constexpr int VT = conv_vt_of<T>();
+  const ConvTile g = conv_tile<VT>(p, threadIdx.x);
   if (!g.active) return;
   const ConvRow& c = g.c;
   float w[W];
@@ -338,26 +348,26 @@ __global__ void __launch_bounds__(256) conv_fwd_vt_kernel(const ConvParams p) {
   for (int k = 0; k < W; ++k) w[k] = p.w[c.d * W + k];
   const float bias = p.bias ? p.bias[c.d] : 0.f;
   const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
-  float xv[4 + kConvVT];  // X[t0 - 4 .. t0 + 8)
+  float xv[4 + VT];  // X[t0 - 4 .. t0 + VT)
   if (g.t0 > 0) {
     ld4<T>(p.x, xrow + g.t0 - 4, xv);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
   }
-  ld4<T>(p.x, xrow + g.t0, xv + 4);
-  ld4<T>(p.x, xrow + g.t0 + 4, xv + 8);
-  float o[kConvVT];
 #pragma unroll
-  for (int i = 0; i < kConvVT; ++i) {
+  for (int q = 0; q < VT; q += 4) ld4<T>(p.x, xrow + g.t0 + q, xv + 4 + q);
+  float o[VT];
+#pragma unroll
+  for (int i = 0; i < VT; ++i) {
     float acc = bias;
 #pragma unroll
     for (int k = 0; k < W; ++k) acc = fmaf(w[k], xv[4 + i - (W - 1) + k], acc);
     o[i] = p.silu ? acc * sigmoid(acc) : acc;
   }
   const int64_t orow = c.b * p.sout[0] + c.d * p.sout[1];
-  st4<T>(p.out, orow + g.t0, o);
-  st4<T>(p.out, orow + g.t0 + 4, o + 4);
+#pragma unroll
+  for (int q = 0; q < VT; q += 4) st4<T>(p.out, orow + g.t0 + q, o + q);
 }
 
 // Sum over the 64 lanes of a wave, in a fixed order, result in every lane.
@@ -369,8 +379,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 template <typename T, int W>
 __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
+  constexpr int VT = conv_vt_of<T>();
   __shared__ float s_part[4][W + 1];
-  const ConvTile g = conv_tile(p, threadIdx.x);
+  const ConvTile g = conv_tile<VT>(p, threadIdx.x);
   const ConvRow& c = g.c;
   const int64_t L = p.seqlen;
   float dwk[W + 1];  // dweight[0..W), dbias
@@ -383,30 +394,31 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
     const float bias = p.bias ? p.bias[c.d] : 0.f;
     const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
     const int64_t orow = c.b * p.sdo[0] + c.d * p.sdo[1];
-    const bool tail = g.t0 + kConvVT < L;  // the next 8 steps exist
-    float xv[4 + kConvVT + 4];              // X[t0 - 4 .. t0 + 12)
-    float go[kConvVT + 4];                  // dout[t0 .. t0 + 12)
+    const bool tail = g.t0 + VT < L;  // the next VT steps exist
+    float xv[4 + VT + 4];              // X[t0 - 4 .. t0 + VT + 4)
+    float go[VT + 4];                  // dout[t0 .. t0 + VT + 4)
     if (g.t0 > 0) {
       ld4<T>(p.x, xrow + g.t0 - 4, xv);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
     }
-    ld4<T>(p.x, xrow + g.t0, xv + 4);
-    ld4<T>(p.x, xrow + g.t0 + 4, xv + 8);
-    ld4<T>(p.dout, orow + g.t0, go);
-    ld4<T>(p.dout, orow + g.t0 + 4, go + 4);
+#pragma unroll
+    for (int q = 0; q < VT; q += 4) {
+      ld4<T>(p.x, xrow + g.t0 + q, xv + 4 + q);
+      ld4<T>(p.dout, orow + g.t0 + q, go + q);
+    }
     if (tail) {
-      ld4<T>(p.x, xrow + g.t0 + 8, xv + 12);
-      ld4<T>(p.dout, orow + g.t0 + 8, go + 8);
+      ld4<T>(p.x, xrow + g.t0 + VT, xv + 4 + VT);
+      ld4<T>(p.dout, orow + g.t0 + VT, go + VT);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xv[12 + i] = go[8 + i] = 0.f;
+      for (int i = 0; i < 4; ++i) xv[4 + VT + i] = go[VT + i] = 0.f;
     }
-    // dpre[t0 + i] for i < 8 + W - 1 (zero past the sequence end).
-    float dp[kConvVT + W - 1];
+    // dpre[t0 + i] for i < VT + W - 1 (zero past the sequence end).
+    float dp[VT + W - 1];
 #pragma unroll
-    for (int i = 0; i < kConvVT + W - 1; ++i) {
+    for (int i = 0; i < VT + W - 1; ++i) {
       float pre = bias;
 #pragma unroll
       for (int k = 0; k < W; ++k) pre = fmaf(w[k], xv[4 + i - (W - 1) + k], pre);
@@ -415,12 +427,12 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
         const float sg = sigmoid(pre);
         v *= sg * (1.f + pre * (1.f - sg));
       }
-      dp[i] = (i < kConvVT || tail) ? v : 0.f;
+      dp[i] = (i < VT || tail) ? v : 0.f;
     }
-    float dx[kConvVT];
+    float dx[VT];
     const int64_t fin0 = L - (W - 1);
 #pragma unroll
-    for (int i = 0; i < kConvVT; ++i) {
+    for (int i = 0; i < VT; ++i) {
       dwk[W] += dp[i];
 #pragma unroll
       for (int k = 0; k < W; ++k) dwk[k] = fmaf(dp[i], xv[4 + i - (W - 1) + k], dwk[k]);
@@ -432,8 +444,8 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
       dx[i] = acc;
     }
     const int64_t xr = c.b * p.sdx[0] + c.d * p.sdx[1];
-    st4<T>(p.dx, xr + g.t0, dx);
-    st4<T>(p.dx, xr + g.t0 + 4, dx + 4);
+#pragma unroll
+    for (int q = 0; q < VT; q += 4) st4<T>(p.dx, xr + g.t0 + q, dx + q);
     if (g.t0 == 0 && p.dinit != nullptr) {
       // dX[s] for s in [-(W-1), 0): the initial-state columns.
 #pragma unroll

@@ -29,12 +29,17 @@ __device__ __forceinline__ float to_f32(f16 x) { return static_cast<float>(x); }
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return static_cast<f16>(x); }
-// Round to nearest even; NaN stays a (quiet) NaN.
+// Round to nearest even; NaN stays a (quiet) NaN. gfx950 converts in hardware
+// (v_cvt_pk_bf16_f32, two values per instruction when neighbours convert together).
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) {
-  uint32_t u = __builtin_bit_cast(uint32_t, x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{static_cast<uint16_t>((u >> 16) | 0x40)};
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bf16{static_cast<uint16_t>(u >> 16)};
+  return bf16{__builtin_bit_cast(uint16_t, static_cast<__bf16>(x))};
+}
+// Two values rounded to bf16 by one v_cvt_pk_bf16_f32; lo in bits 0-15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 template <typename T> __device__ __forceinline__ float ld(const void* base, int64_t idx) {

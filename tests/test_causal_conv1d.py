@@ -190,14 +190,16 @@ def test_opcheck():
                            torch.randn(2, 8, 12, device=DEV), torch.randn(2, 8, 3, device=DEV), True))
 
 
-@pytest.mark.parametrize("seqlen", [8, 64, 520, 1024, 2048, 2056])
+@pytest.mark.parametrize("seqlen", [8, 16, 64, 520, 1024, 2048, 2056, 4112])
 @pytest.mark.parametrize("width", [2, 3, 4, 5])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_vector_path_forward_backward(seqlen, width, dtype):
-    """Time-contiguous x with seqlen a multiple of 8 takes the vectorised
-    kernels: rows of one to four waves (seqlen <= 2048) and rows split into
-    2048-step segments (2056). Initial/final states and their gradients ride
-    along; the chunk at t = 0 reads the initial states, the last one dfinal."""
+    """Time-contiguous x with seqlen a multiple of the vector tile (8 steps
+    per thread in fp32, 16 in bf16) takes the vectorised kernels: rows of one
+    to four waves and rows split into 256-thread segments (2056 and 4112 in
+    fp32, 4112 in bf16); other lengths take the chunked kernels. Initial/final
+    states and their gradients ride along; the chunk at t = 0 reads the
+    initial states, the last one dfinal."""
     torch.manual_seed(seqlen + width)
     b, d = 2, 6
     x = torch.randn(b, d, seqlen, device=DEV).to(dtype).requires_grad_()
