@@ -261,15 +261,12 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
 // ---- Time-contiguous fast path ------------------------------------------------
 // For x, out, dout and dx with unit time stride, rows aligned to 4 elements and
 // seqlen a multiple of VT: each thread owns VT consecutive steps of one
-// (batch, channel) row (VT = 8 for fp32, 16 for 16-bit types, so a thread
-// moves 32 bytes of each tensor either way) with 16-byte (fp32) or 8-byte
-// (16-bit) vector loads and stores; the W-1 inputs before its first step (and,
+// (batch, channel) row (VT = 16 where seqlen allows, else 8) with 16-byte
+// (fp32) or 8-byte (16-bit) vector loads and stores; the W-1 inputs before its first step (and,
 // in the backward, the W-1 steps after its last) are re-read from the
 // neighbouring thread's vector, which the cache serves. A workgroup covers
 // `rpw` rows of `tpr` threads each (short rows) or one 256 * VT-step segment of
 // a row (long rows), so a row segment never straddles a wave.
-template <typename T>
-constexpr int conv_vt_of() { return sizeof(T) == 4 ? 8 : 16; }
 
 template <typename T>
 __device__ __forceinline__ void ld4(const void* base, int64_t idx, float* v) {
@@ -337,9 +334,8 @@ __device__ __forceinline__ ConvTile conv_tile(const ConvParams& p, int tid) {
   return g;
 }
 
-template <typename T, int W>
+template <typename T, int W, int VT>
 __global__ void __launch_bounds__(256) conv_fwd_vt_kernel(const ConvParams p) {
-  constexpr int VT = conv_vt_of<T>();
   const ConvTile g = conv_tile<VT>(p, threadIdx.x);
   if (!g.active) return;
   const ConvRow& c = g.c;
@@ -377,9 +373,8 @@ __device__ __forceinline__ float wave_sum(float x) {
   return swap_sum<16>(x, x);
 }
 
-template <typename T, int W>
+template <typename T, int W, int VT>
 __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
-  constexpr int VT = conv_vt_of<T>();
   __shared__ float s_part[4][W + 1];
   const ConvTile g = conv_tile<VT>(p, threadIdx.x);
   const ConvRow& c = g.c;
@@ -486,10 +481,15 @@ static hipError_t launch_vt(const ConvParams& p, bool bwd, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(
       p.nseg > 1 ? p.batch * p.dim * p.nseg : (p.batch * p.dim + p.rpw - 1) / p.rpw);
   switch (p.width) {
-#define MCPU_CONV_VT(WW)                                                                         \
-  case WW:                                                                                       \
-    if (bwd) hipLaunchKernelGGL((conv_bwd_vt_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);    \
-    else hipLaunchKernelGGL((conv_fwd_vt_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);        \
+#define MCPU_CONV_VT(WW)                                                                             \
+  case WW:                                                                                           \
+    if (p.vt == 16) {                                                                                \
+      if (bwd) hipLaunchKernelGGL((conv_bwd_vt_kernel<T, WW, 16>), dim3(grid), dim3(256), 0, st, p);  \
+      else hipLaunchKernelGGL((conv_fwd_vt_kernel<T, WW, 16>), dim3(grid), dim3(256), 0, st, p);      \
+    } else {                                                                                         \
+      if (bwd) hipLaunchKernelGGL((conv_bwd_vt_kernel<T, WW, 8>), dim3(grid), dim3(256), 0, st, p);   \
+      else hipLaunchKernelGGL((conv_fwd_vt_kernel<T, WW, 8>), dim3(grid), dim3(256), 0, st, p);       \
+    }                                                                                                \
     break;
     MCPU_CONV_VT(2)
     MCPU_CONV_VT(3)

@@ -30,7 +30,8 @@ struct ConvParams {
   int64_t sx[3], sinit[3], sout[3], sdo[3], sdx[3];
   int silu;
   int channels_last;  // thread index decomposed channel-fastest
-  // Time-contiguous fast path (conv_*_vt_kernel): used when vt != 0.
+  // Time-contiguous fast path (conv_*_vt_kernel): vt = steps per thread (8 or
+  // 16), 0 when the path does not apply.
   int vt;
   int tpr;            // threads per row segment: 64, 128 or 256
   int rpw;            // row segments per workgroup: 256 / tpr

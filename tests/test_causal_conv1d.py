@@ -194,12 +194,12 @@ def test_opcheck():
 @pytest.mark.parametrize("width", [2, 3, 4, 5])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_vector_path_forward_backward(seqlen, width, dtype):
-    """Time-contiguous x with seqlen a multiple of the vector tile (8 steps
-    per thread in fp32, 16 in bf16) takes the vectorised kernels: rows of one
-    to four waves and rows split into 256-thread segments (2056 and 4112 in
-    fp32, 4112 in bf16); other lengths take the chunked kernels. Initial/final
-    states and their gradients ride along; the chunk at t = 0 reads the
-    initial states, the last one dfinal."""
+    """Time-contiguous x with seqlen a multiple of 8 takes the vectorised
+    kernels (8 steps per thread in fp32; 16 in bf16 when seqlen is a multiple
+    of 16, else 8): rows of one to four waves and rows split into 256-thread
+    segments (2056 and 4112 in fp32, 2056 (8 steps) and 4112 in bf16).
+    Initial/final states and their gradients ride along; the chunk at t = 0
+    reads the initial states, the last one dfinal."""
     torch.manual_seed(seqlen + width)
     b, d = 2, 6
     x = torch.randn(b, d, seqlen, device=DEV).to(dtype).requires_grad_()
