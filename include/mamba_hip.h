@@ -188,6 +188,19 @@ typedef struct mcpu_conv_update_args {
   int64_t x_stride[3];
   int64_t state_stride[3];
   int64_t out_stride[3];
+  /* Continuous batching (no counterpart in the reference, which raises
+     NotImplementedError for both, ops/causal_conv1d.py:66-67; the semantics
+     of the upstream causal_conv1d package):
+     conv_state_indices (batch) int32, optional: batch row b uses
+       conv_state[conv_state_indices[b]]; rows outside [0, state_batch) are
+       skipped (out = 0, no state written). Indices must be distinct.
+     cache_seqlens (batch) int32, optional: conv_state is a ring buffer; the
+       W-1 inputs before x are at (cache_seqlens[b] - (W-1) + k) mod state_len
+       and x[s] is written at (cache_seqlens[b] + s) mod state_len.
+     state_batch: rows of conv_state (0 = batch). */
+  const int32_t* cache_seqlens;
+  const int32_t* conv_state_indices;
+  int64_t state_batch;
 } mcpu_conv_update_args;
 
 int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* stream);
@@ -222,6 +235,14 @@ typedef struct mcpu_state_update_args {
   int64_t z_stride[3];
   int64_t B_stride[2];     /* over (batch, group) */
   int64_t C_stride[2];
+  /* state_batch_indices (batch) int32, optional: batch row b updates
+     state[state_batch_indices[b]]; rows outside [0, state_batch) are skipped
+     (out = 0, no state written). Indices must be distinct. No counterpart in
+     the reference, which raises NotImplementedError for it
+     (ops/selective_state_update.py:24-25); the semantics of mamba_ssm's
+     selective_state_update. state_batch: rows of state (0 = batch). */
+  const int32_t* state_batch_indices;
+  int64_t state_batch;
 } mcpu_state_update_args;
 
 int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream);

@@ -185,6 +185,12 @@ extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* s
     p.sout[i] = a->out_stride[i];
   }
   p.silu = a->silu != 0;
+  p.cache_seqlens = a->cache_seqlens;
+  p.state_idx = a->conv_state_indices;
+  p.state_batch = a->state_batch > 0 ? a->state_batch : a->batch;
+  if (a->state_batch < 0) return fail(MCPU_ERR_INVALID, "causal_conv1d_update: negative state_batch");
+  if (a->conv_state_indices == nullptr && p.state_batch < a->batch)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: conv_state has fewer rows than the batch");
   return hip_status(conv_update_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
                     "causal_conv1d_update launch");
 }
@@ -231,6 +237,11 @@ extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void
     p.sB[i] = a->B_stride[i];
     p.sC[i] = a->C_stride[i];
   }
+  if (a->state_batch < 0) return fail(MCPU_ERR_INVALID, "selective_state_update: negative state_batch");
+  p.state_idx = a->state_batch_indices;
+  p.state_batch = a->state_batch > 0 ? a->state_batch : a->batch;
+  if (a->state_batch_indices == nullptr && p.state_batch < a->batch)
+    return fail(MCPU_ERR_INVALID, "selective_state_update: state has fewer rows than the batch");
   p.softplus = a->dt_softplus != 0;
   return hip_status(state_update_launch(p, a->dtype, a->state_dtype, static_cast<hipStream_t>(stream)),
                     "selective_state_update launch");

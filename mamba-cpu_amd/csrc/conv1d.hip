@@ -226,6 +226,11 @@ __global__ void __launch_bounds__(256) conv_reduce_dw_kernel(const float* __rest
 // Decode update (reference src/mamba_cpu/ops/causal_conv1d.py:56-85): one
 // thread per (batch, channel). x_full = [state, x]; out[s] = act(bias +
 // sum_k w[k] x_full[state_len-(W-1)+s+k]); state <- last state_len columns.
+// With conv_state_indices, batch row b works on state row state_idx[b] (rows
+// out of range are skipped: out = 0, state untouched). With cache_seqlens the
+// state is a ring buffer (the upstream causal_conv1d package's semantics): the
+// W-1 inputs before x sit at (cs - (W-1) + k) mod state_len, and x[s] is
+// written at (cs + s) mod state_len after every output has been computed.
 template <typename T>
 __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams p) {
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
@@ -234,9 +239,24 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
   const int W = static_cast<int>(p.width);
   const int64_t S = p.state_len, L = p.seqlen;
   const int64_t xb = b * p.sx[0] + d * p.sx[1];
-  const int64_t sb = b * p.sst[0] + d * p.sst[1];
-  auto full = [&](int64_t i) -> float {  // x_full[i], i in [0, S + L)
-    return i < S ? ld<T>(p.state, sb + i * p.sst[2]) : ld<T>(p.x, xb + (i - S) * p.sx[2]);
+  const int64_t ob = b * p.sout[0] + d * p.sout[1];
+  int64_t srow = b;
+  if (p.state_idx != nullptr) {
+    srow = p.state_idx[b];
+    if (srow < 0 || srow >= p.state_batch) {
+      for (int64_t s = 0; s < L; ++s) st<T>(p.out, ob + s * p.sout[2], 0.f);
+      return;
+    }
+  }
+  const int64_t sb = srow * p.sst[0] + d * p.sst[1];
+  const bool ring = p.cache_seqlens != nullptr;
+  const int64_t cs = ring ? p.cache_seqlens[b] : 0;
+  auto wrap = [&](int64_t i) { const int64_t r = i % S; return r < 0 ? r + S : r; };
+  // x_full[i] for i in [S - (W-1), S + L): the W-1 inputs before x, then x.
+  auto full = [&](int64_t i) -> float {
+    if (i >= S) return ld<T>(p.x, xb + (i - S) * p.sx[2]);
+    const int64_t pos = ring ? wrap(cs - S + i) : i;
+    return ld<T>(p.state, sb + pos * p.sst[2]);
   };
   float w[kConvMaxW];
 #pragma unroll
@@ -248,7 +268,11 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
     for (int k = 0; k < kConvMaxW; ++k)
       if (k < W) acc = fmaf(w[k], full(S - (W - 1) + s + k), acc);
     if (p.silu) acc = acc * sigmoid(acc);
-    st<T>(p.out, b * p.sout[0] + d * p.sout[1] + s * p.sout[2], acc);
+    st<T>(p.out, ob + s * p.sout[2], acc);
+  }
+  if (ring) {
+    for (int64_t s = 0; s < L; ++s) st<T>(p.state, sb + wrap(cs + s) * p.sst[2], full(S + s));
+    return;
   }
   // Shift: new_state[i] = x_full[L + i]; ascending i never reads a slot it
   // has already overwritten (reads are at index L + i >= i).

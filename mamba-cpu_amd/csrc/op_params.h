@@ -47,6 +47,9 @@ struct ConvUpdateParams {
   int64_t batch, dim, seqlen, width, state_len;
   int64_t sx[3], sst[3], sout[3];
   int silu;
+  const int32_t* cache_seqlens;  // ring-buffer write positions, or null
+  const int32_t* state_idx;      // conv_state row per batch row, or null
+  int64_t state_batch;           // rows of conv_state
 };
 
 struct StateUpdateParams {
@@ -63,6 +66,8 @@ struct StateUpdateParams {
   int64_t batch, nheads, headdim, dstate, ngroups;
   int64_t sst[3], sx[3], sdt[3], sz[3], sB[2], sC[2];
   int softplus;
+  const int32_t* state_idx;  // state row per batch row, or null
+  int64_t state_batch;       // rows of state
 };
 
 hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st);

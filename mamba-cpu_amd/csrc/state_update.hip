@@ -33,7 +33,16 @@ __global__ void __launch_bounds__(256) state_update_kernel(const StateUpdatePara
   if (p.dt_bias != nullptr) dt += p.dt_bias[hp];
   if (p.softplus) dt = softplus(dt);
   const float dtx = dt * x;
-  const int64_t sbase = b * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
+  int64_t srow = b;
+  if (p.state_idx != nullptr) {
+    // Rows of one (batch, head, p) share b, so the whole 16-lane row leaves.
+    srow = p.state_idx[b];
+    if (srow < 0 || srow >= p.state_batch) {
+      if (j == 0) st<Tx>(p.out, rowid, 0.f);
+      return;
+    }
+  }
+  const int64_t sbase = srow * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
   float acc = 0.f;
 #pragma unroll
   for (int s = 0; s < SPL; ++s) {

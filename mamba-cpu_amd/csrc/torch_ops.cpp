@@ -492,16 +492,33 @@ std::tuple<Tensor, Tensor> causal_conv1d_fwd_autograd(const Tensor& x, const Ten
   return {r[0], r[1]};
 }
 
+// An optional (batch,) int32 index / length vector of the decode ops.
+void check_index(const char* name, const char* what, const optional<Tensor>& t, int64_t batch) {
+  if (!has(t)) return;
+  check_gpu(name, t);
+  TORCH_CHECK_VALUE(t->scalar_type() == at::kInt && t->dim() == 1 && t->size(0) == batch &&
+                        t->is_contiguous(),
+                    name, " expects ", what, " as a contiguous int32 tensor of shape (batch,)");
+}
+
 Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& weight,
-                            const optional<Tensor>& bias, bool silu) {
+                            const optional<Tensor>& bias, bool silu,
+                            const optional<Tensor>& cache_seqlens,
+                            const optional<Tensor>& conv_state_indices) {
   const char* name = "mamba_cpu::causal_conv1d_update";
   for (const optional<Tensor>& t : {opt(x), opt(conv_state), opt(weight), bias}) check_gpu(name, t);
+  check_index(name, "cache_seqlens", cache_seqlens, x.size(0));
+  check_index(name, "conv_state_indices", conv_state_indices, x.size(0));
   TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && conv_state.scalar_type() == x.scalar_type(), name,
                     " expects x and conv_state of one dtype among float32, bfloat16 and float16");
   TORCH_CHECK_VALUE(weight.scalar_type() == at::kFloat && weight.is_contiguous() && weight.dim() == 2,
                     name, " expects a contiguous float32 weight");
   TORCH_CHECK_VALUE(x.dim() == 3 && conv_state.dim() == 3, name,
                     " expects x (batch, dim, seqlen) and conv_state (batch, dim, state_len)");
+  TORCH_CHECK_VALUE(conv_state.size(1) == x.size(1) &&
+                        (has(conv_state_indices) || conv_state.size(0) == x.size(0)),
+                    name, " expects conv_state (batch, dim, state_len), or (rows, dim, state_len) "
+                    "with conv_state_indices");
   c10::DeviceGuard guard(x.device());
   Tensor out = at::empty(x.sizes(), x.options());
   mcpu_conv_update_args a;
@@ -521,6 +538,10 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
   strides3(a.x_stride, x);
   strides3(a.state_stride, conv_state);
   strides3(a.out_stride, out);
+  a.cache_seqlens = has(cache_seqlens) ? static_cast<const int32_t*>(cache_seqlens->data_ptr()) : nullptr;
+  a.conv_state_indices =
+      has(conv_state_indices) ? static_cast<const int32_t*>(conv_state_indices->data_ptr()) : nullptr;
+  a.state_batch = conv_state.size(0);
   check_rc(mcpu_causal_conv1d_update(&a, stream_of(x)), name);
   return out;
 }
@@ -530,8 +551,9 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
 Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, const Tensor& A,
                               const Tensor& B, const Tensor& C, const optional<Tensor>& D,
                               const optional<Tensor>& z, const optional<Tensor>& dt_bias,
-                              bool dt_softplus) {
+                              bool dt_softplus, const optional<Tensor>& state_batch_indices) {
   const char* name = "mamba_cpu::selective_state_update";
+  check_index(name, "state_batch_indices", state_batch_indices, x.size(0));
   for (const optional<Tensor>& t : {opt(state), opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias})
     check_gpu(name, t);
   TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && dt.scalar_type() == x.scalar_type() &&
@@ -540,7 +562,9 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
   TORCH_CHECK_VALUE(x_dtype(state.scalar_type()), name,
                     " expects a float32, bfloat16 or float16 state");
   TORCH_CHECK_VALUE(state.dim() == 4 && x.dim() == 3, name, " expects state (b, h, p, n) and x (b, h, p)");
-  const int64_t b = state.size(0), h = state.size(1), p = state.size(2), n = state.size(3);
+  TORCH_CHECK_VALUE(has(state_batch_indices) || state.size(0) == x.size(0), name,
+                    " expects state and x of one batch, or state_batch_indices");
+  const int64_t b = x.size(0), h = state.size(1), p = state.size(2), n = state.size(3);
   TORCH_CHECK_VALUE(state.stride(3) == 1 || n == 1, name, " expects unit stride along dstate");
   TORCH_CHECK_VALUE(x.size(0) == b && x.size(1) == h && x.size(2) == p && dt.sizes() == x.sizes() &&
                         (!has(z) || z->sizes() == x.sizes()),
@@ -590,6 +614,9 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
   a.B_stride[1] = B.stride(1);
   a.C_stride[0] = C.stride(0);
   a.C_stride[1] = C.stride(1);
+  a.state_batch_indices =
+      has(state_batch_indices) ? static_cast<const int32_t*>(state_batch_indices->data_ptr()) : nullptr;
+  a.state_batch = state.size(0);
   check_rc(mcpu_selective_state_update(&a, stream_of(x)), name);
   return out;
 }
@@ -597,14 +624,16 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
 // The two in-place ops record their mutation for autograd's version counters
 // (what torch.library does for a Python custom op with mutates_args).
 Tensor causal_conv1d_update_inplace(const Tensor& x, Tensor& conv_state, const Tensor& weight,
-                                    const optional<Tensor>& bias, bool silu) {
+                                    const optional<Tensor>& bias, bool silu,
+                                    const optional<Tensor>& cache_seqlens,
+                                    const optional<Tensor>& conv_state_indices) {
   Tensor out;
   {
     at::AutoDispatchBelowADInplaceOrView below;
     static auto op = c10::Dispatcher::singleton()
                          .findSchemaOrThrow("mamba_cpu::causal_conv1d_update", "")
                          .typed<decltype(causal_conv1d_update)>();
-    out = op.call(x, conv_state, weight, bias, silu);
+    out = op.call(x, conv_state, weight, bias, silu, cache_seqlens, conv_state_indices);
   }
   conv_state.unsafeGetTensorImpl()->bump_version();
   return out;
@@ -613,14 +642,15 @@ Tensor causal_conv1d_update_inplace(const Tensor& x, Tensor& conv_state, const T
 Tensor selective_state_update_inplace(Tensor& state, const Tensor& x, const Tensor& dt,
                                       const Tensor& A, const Tensor& B, const Tensor& C,
                                       const optional<Tensor>& D, const optional<Tensor>& z,
-                                      const optional<Tensor>& dt_bias, bool dt_softplus) {
+                                      const optional<Tensor>& dt_bias, bool dt_softplus,
+                                      const optional<Tensor>& state_batch_indices) {
   Tensor out;
   {
     at::AutoDispatchBelowADInplaceOrView below;
     static auto op = c10::Dispatcher::singleton()
                          .findSchemaOrThrow("mamba_cpu::selective_state_update", "")
                          .typed<decltype(selective_state_update)>();
-    out = op.call(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus);
+    out = op.call(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus, state_batch_indices);
   }
   state.unsafeGetTensorImpl()->bump_version();
   return out;
@@ -646,9 +676,10 @@ TORCH_LIBRARY(mamba_cpu, m) {
   m.def("causal_conv1d_bwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
         "Tensor dout, Tensor? dfinal_states, bool silu) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("causal_conv1d_update(Tensor x, Tensor(a!) conv_state, Tensor weight, Tensor? bias, "
-        "bool silu) -> Tensor");
+        "bool silu, Tensor? cache_seqlens=None, Tensor? conv_state_indices=None) -> Tensor");
   m.def("selective_state_update(Tensor(a!) state, Tensor x, Tensor dt, Tensor A, Tensor B, "
-        "Tensor C, Tensor? D, Tensor? z, Tensor? dt_bias, bool dt_softplus) -> Tensor");
+        "Tensor C, Tensor? D, Tensor? z, Tensor? dt_bias, bool dt_softplus, "
+        "Tensor? state_batch_indices=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {

@@ -83,6 +83,7 @@ class ConvUpdateArgs(ctypes.Structure):
         ("batch", _I64), ("dim", _I64), ("seqlen", _I64), ("width", _I64), ("state_len", _I64),
         ("silu", _I32), ("dtype", _I32),
         ("x_stride", _S3), ("state_stride", _S3), ("out_stride", _S3),
+        ("cache_seqlens", _P), ("conv_state_indices", _P), ("state_batch", _I64),
     ]
 
 
@@ -94,6 +95,7 @@ class StateUpdateArgs(ctypes.Structure):
         ("dt_softplus", _I32), ("dtype", _I32), ("state_dtype", _I32), ("_pad", _I32),
         ("state_stride", _S3), ("x_stride", _S3), ("dt_stride", _S3), ("z_stride", _S3),
         ("B_stride", _S2), ("C_stride", _S2),
+        ("state_batch_indices", _P), ("state_batch", _I64),
     ]
 
 

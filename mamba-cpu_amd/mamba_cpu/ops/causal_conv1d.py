@@ -57,8 +57,17 @@ def _(x, weight, bias, initial_states, dout, dfinal_states, silu):
 
 
 @torch.library.register_fake("mamba_cpu::causal_conv1d_update")
-def _(x, conv_state, weight, bias, silu):
+def _(x, conv_state, weight, bias, silu, cache_seqlens=None, conv_state_indices=None):
     return x.new_empty(x.shape)
+
+
+def _index(t, name, batch, device):
+    """An optional (batch,) integer vector as the int32 the kernels read."""
+    if t is None:
+        return None
+    if t.dtype not in (torch.int32, torch.int64) or t.dim() != 1 or t.shape[0] != batch:
+        raise ValueError(f"{name} must be an integer tensor of shape ({batch},)")
+    return t.to(device=device, dtype=torch.int32).contiguous()
 
 
 def causal_conv1d_fn(
@@ -109,10 +118,19 @@ def causal_conv1d_update(
     x: (batch, dim) or (batch, dim, seqlen)
     conv_state: (batch, dim, state_len), state_len >= width - 1
     weight: (dim, width)
+    cache_seqlens: optional (batch,) int; conv_state is then a ring buffer
+        (the upstream causal_conv1d package's semantics): the width - 1 inputs
+        before x are at (cache_seqlens - (width - 1) + k) % state_len and x is
+        written from cache_seqlens % state_len on.
+    conv_state_indices: optional (batch,) int; batch row b then uses
+        conv_state[conv_state_indices[b]] (conv_state may have more rows than
+        the batch; rows whose index is out of range are skipped and get a zero
+        output). Indices must be distinct.
     Returns out shaped like x.
+
+    The reference raises NotImplementedError for the last two
+    (ops/causal_conv1d.py:66-67); they serve continuous batching.
     """
-    if cache_seqlens is not None or conv_state_indices is not None:
-        raise NotImplementedError("cache_seqlens and conv_state_indices are not supported yet")
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
     silu = _silu_flag(activation)
@@ -127,12 +145,14 @@ def causal_conv1d_update(
         x_seq = x_seq.float()
     w = weight.float().contiguous()
     bb = None if bias is None else bias.float().contiguous()
+    cs = _index(cache_seqlens, "cache_seqlens", x_seq.shape[0], x.device)
+    idx = _index(conv_state_indices, "conv_state_indices", x_seq.shape[0], x.device)
     if conv_state.dtype == x_seq.dtype:
-        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, conv_state, w, bb, silu)
+        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, conv_state, w, bb, silu, cs, idx)
     else:
         # The reference mixes dtypes through conv_state.to(x.dtype) and a copy back.
         tmp = conv_state.to(x_seq.dtype)
-        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, tmp, w, bb, silu)
+        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, tmp, w, bb, silu, cs, idx)
         conv_state.copy_(tmp)
     out = out.to(in_dtype)
     return out.squeeze(-1) if single_step else out

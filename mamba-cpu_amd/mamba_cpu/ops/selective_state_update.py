@@ -21,8 +21,8 @@ _X_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
 @torch.library.register_fake("mamba_cpu::selective_state_update")
-def _(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus):
-    return x.new_empty(state.shape[:3])
+def _(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus, state_batch_indices=None):
+    return x.new_empty(x.shape)
 
 
 def selective_state_update(
@@ -42,10 +42,13 @@ def selective_state_update(
         A: (nheads, headdim, dstate)
         B, C: (batch, ngroups, dstate)
         D, dt_bias: (nheads, headdim)
+    state_batch_indices: optional (batch,) int; batch row b then updates
+        state[state_batch_indices[b]] (state may have more rows than the batch;
+        rows whose index is out of range are skipped and get a zero output).
+        Indices must be distinct. mamba_ssm's semantics; the reference raises
+        NotImplementedError for it (ops/selective_state_update.py:24-25).
     Returns out shaped like x.
     """
-    if state_batch_indices is not None:
-        raise NotImplementedError("state_batch_indices is not supported yet")
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
     has_heads = state.dim() > 3
@@ -75,9 +78,15 @@ def selective_state_update(
     st = state
     if st.dtype not in _X_DTYPES or (st.stride(-1) != 1 and st.shape[-1] > 1):
         st = state.float().contiguous()
+    idx = None
+    if state_batch_indices is not None:
+        if (state_batch_indices.dtype not in (torch.int32, torch.int64)
+                or state_batch_indices.shape != (x.shape[0],)):
+            raise ValueError(f"state_batch_indices must be an integer tensor of shape ({x.shape[0]},)")
+        idx = state_batch_indices.to(device=x.device, dtype=torch.int32).contiguous()
     out = torch.ops.mamba_cpu.selective_state_update(
         st, x.to(xdt), dt.to(xdt), f32(A), bc(B), bc(C), f32(D),
-        None if z is None else z.to(xdt), f32(dt_bias), bool(dt_softplus),
+        None if z is None else z.to(xdt), f32(dt_bias), bool(dt_softplus), idx,
     )
     if st is not state:
         state.copy_(st)

@@ -215,38 +215,76 @@ def causal_conv1d_bwd(x, weight, bias=None, initial_states=None, dout=None, acti
     return dxf[:, :, width - 1:], dw, dbias, dinit
 
 
-def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None, cache_seqlens=None,
+                         conv_state_indices=None):
     """Decode step(s) (src/mamba_cpu/ops/causal_conv1d.py:56-85):
         x_full = [conv_state, x] ; new_state = x_full[..., -state_len:]
         out = conv over the last seqlen + width - 1 columns
-    x: (b, d) or (b, d, s). Returns (out shaped like x, new_state)."""
+    x: (b, d) or (b, d, s). Returns (out shaped like x, new conv_state).
+
+    The continuous-batching arguments the reference rejects (:66-67) follow
+    the upstream causal_conv1d package's published semantics:
+      conv_state_indices (b,): row b uses conv_state[conv_state_indices[b]]
+        (conv_state may have more rows); an index out of range skips the row
+        (zero output, state untouched);
+      cache_seqlens (b,): conv_state is a ring buffer; the width - 1 inputs
+        before x are at (cache_seqlens - (width - 1) + k) % state_len, and x[s]
+        is written at (cache_seqlens + s) % state_len."""
     x, st, w, bias = _f64(x), _f64(conv_state), _f64(weight), _f64(bias)
     single = x.ndim == 2
     xs = x[..., None] if single else x
-    seqlen = xs.shape[-1]
+    batch, _, seqlen = xs.shape
     width = w.shape[1]
     state_len = st.shape[-1]
-    xf = np.concatenate([st, xs], axis=-1)
-    new_state = xf[..., xf.shape[-1] - state_len:].copy()
-    win = xf[..., xf.shape[-1] - (seqlen + width - 1):]
+    new_state = st.copy()
     out = np.zeros(xs.shape)
-    for k in range(width):
-        out += w[None, :, k, None] * win[:, :, k:k + seqlen]
-    if bias is not None:
-        out += bias[None, :, None]
-    if activation in ("silu", "swish"):
-        out = out * sigmoid(out)
+    for b in range(batch):
+        row = b if conv_state_indices is None else int(conv_state_indices[b])
+        if not 0 <= row < st.shape[0]:
+            continue
+        if cache_seqlens is None:
+            xf = np.concatenate([st[row], xs[b]], axis=-1)
+            new_state[row] = xf[:, xf.shape[-1] - state_len:]
+            hist = st[row][:, state_len - (width - 1):]
+        else:
+            cs = int(cache_seqlens[b])
+            hist = st[row][:, [(cs - (width - 1) + k) % state_len for k in range(width - 1)]]
+            for t in range(seqlen):
+                new_state[row][:, (cs + t) % state_len] = xs[b][:, t]
+        win = np.concatenate([hist, xs[b]], axis=-1)  # (d, width - 1 + seqlen)
+        for k in range(width):
+            out[b] += w[:, k, None] * win[:, k:k + seqlen]
+        if bias is not None:
+            out[b] += bias[:, None]
+        if activation in ("silu", "swish"):
+            out[b] = out[b] * sigmoid(out[b])
     return (out[..., 0] if single else out), new_state
 
 
-def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, dt_softplus=False):
+def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, dt_softplus=False,
+                           state_batch_indices=None):
     """One decode step (src/mamba_cpu/ops/selective_state_update.py:5-57):
         dt = softplus?(dt + dt_bias) ; state = state * exp(dt A) + dt x B
         out = <state, C> + D x ; out *= silu(z)
     Mamba-1 layout: state (b, d, n), x/dt/z (b, d), A (d, n), B/C (b, n), D/dt_bias (d).
     Mamba-2 layout: state (b, h, p, n), x/dt/z (b, h, p), A (h, p, n),
     B/C (b, g, n), D/dt_bias (h, p); heads split into contiguous groups.
-    Returns (out shaped like x, new_state)."""
+    state_batch_indices (b,), which the reference rejects (:24-25), follows
+    mamba_ssm's semantics: row b updates state[state_batch_indices[b]] (state
+    may have more rows); an index out of range skips the row (zero output).
+    Returns (out shaped like x, new state)."""
+    if state_batch_indices is not None:
+        full = _f64(state).copy()
+        idx = [int(i) for i in state_batch_indices]
+        ok = [0 <= i < full.shape[0] for i in idx]
+        rows = [i if k else 0 for i, k in zip(idx, ok)]
+        out, upd = selective_state_update(full[rows], x, dt, A, B, C, D, z, dt_bias, dt_softplus)
+        for b, (i, k) in enumerate(zip(idx, ok)):
+            if k:
+                full[i] = upd[b]
+            else:
+                out[b] = 0.0
+        return out, full
     state, x, dt, A = _f64(state), _f64(x), _f64(dt), _f64(A)
     B, C, D, z, dt_bias = _f64(B), _f64(C), _f64(D), _f64(z), _f64(dt_bias)
     heads = state.ndim > 3

@@ -114,9 +114,41 @@ def test_rejects_unsupported_args():
         causal_conv1d_fn(x, w, activation="relu")
     with pytest.raises(ValueError):
         causal_conv1d_update(x, torch.zeros(2, 8, 2, device=DEV), w)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):  # one index per batch row
         causal_conv1d_update(x[..., 0], torch.zeros(2, 8, 3, device=DEV), w,
-                             cache_seqlens=torch.zeros(2, dtype=torch.int32, device=DEV))
+                             cache_seqlens=torch.zeros(3, dtype=torch.int32, device=DEV))
+
+
+@pytest.mark.parametrize("seqlen", [None, 1, 3])
+@pytest.mark.parametrize("state_len", [3, 6])
+@pytest.mark.parametrize("mode", ["indices", "ring", "both"])
+def test_update_continuous_batching_matches_oracle(seqlen, state_len, mode):
+    """conv_state_indices (rows of a larger state, one out of range) and
+    cache_seqlens (ring buffer), which the reference rejects, against the
+    oracle's restatement of the upstream semantics; several steps in a row so
+    the ring wraps."""
+    torch.manual_seed(7)
+    b, d, width, rows = 3, 20, 4, 6
+    w = torch.randn(d, width, device=DEV)
+    bias = torch.randn(d, device=DEV)
+    state = torch.randn(rows, d, state_len, device=DEV)
+    idx = torch.tensor([4, 0, 9], dtype=torch.int32, device=DEV) if mode != "ring" else None
+    want_state = state.cpu().double().numpy()
+    if mode == "ring":
+        state = state[:b].clone()
+        want_state = want_state[:b]
+    cs = torch.tensor([0, 5, 2], dtype=torch.int64, device=DEV) if mode != "indices" else None
+    for step in range(4):
+        x = torch.randn(b, d, device=DEV) if seqlen is None else torch.randn(b, d, seqlen, device=DEV)
+        out = causal_conv1d_update(x, state, w, bias, "silu", cache_seqlens=cs, conv_state_indices=idx)
+        want, want_state = O.causal_conv1d_update(
+            x, want_state, w, bias, "silu",
+            cache_seqlens=None if cs is None else cs.cpu().numpy(),
+            conv_state_indices=None if idx is None else idx.cpu().numpy())
+        close(out, want, 1e-5, 1e-5, f"out step {step}")
+        close(state, want_state, 0, 0, f"state step {step}")
+        if cs is not None:
+            cs = cs + (1 if seqlen is None else seqlen)
 
 
 @pytest.mark.parametrize("width", [1, 2, 4, 7])

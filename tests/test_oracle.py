@@ -323,3 +323,69 @@ def test_planted_mistakes_are_caught():
     out, _ = O.causal_conv1d_fwd(x, w[:, ::-1])
     xf = np.concatenate([np.zeros(2), x[0, 0]])
     assert not np.allclose(out[0, 0], np.convolve(xf, w[0][::-1], mode="valid"))
+
+
+def test_conv_update_indices_and_ring_buffer_invariants():
+    """Pins the continuous-batching arguments of the conv update oracle:
+    identity indices change nothing; permuted indices update the selected rows
+    only; an out-of-range index skips its row; a ring buffer stepped with
+    cache_seqlens = t gives the linear update's outputs, and its contents are
+    the linear state rotated by t."""
+    rng = np.random.default_rng(21)
+    b, d, w, S, T = 3, 4, 4, 5, 11
+    x = rng.standard_normal((b, d, T))
+    wt, bias = rng.standard_normal((d, w)), rng.standard_normal(d)
+    st0 = rng.standard_normal((b, d, S))
+    o1, s1 = O.causal_conv1d_update(x[..., 0], st0, wt, bias, "silu")
+    o2, s2 = O.causal_conv1d_update(x[..., 0], st0, wt, bias, "silu", conv_state_indices=np.arange(b))
+    np.testing.assert_array_equal(o1, o2)
+    np.testing.assert_array_equal(s1, s2)
+    big = rng.standard_normal((6, d, S))
+    idx = np.array([4, 0, 2])
+    o3, s3 = O.causal_conv1d_update(x[..., :2], big, wt, bias, "silu", conv_state_indices=idx)
+    o4, s4 = O.causal_conv1d_update(x[..., :2], big[idx], wt, bias, "silu")
+    np.testing.assert_allclose(o3, o4, rtol=1e-13)
+    np.testing.assert_allclose(s3[idx], s4, rtol=1e-13)
+    untouched = [i for i in range(6) if i not in idx]
+    np.testing.assert_array_equal(s3[untouched], big[untouched])
+    o5, s5 = O.causal_conv1d_update(x[..., :2], big, wt, bias, "silu", conv_state_indices=np.array([4, -1, 9]))
+    np.testing.assert_allclose(o5[0], o4[0], rtol=1e-13)
+    assert (o5[1:] == 0).all()
+    np.testing.assert_array_equal(s5[[0, 1, 2, 3, 5]], big[[0, 1, 2, 3, 5]])
+    # Ring buffer vs linear, one token at a time, then two tokens at once.
+    lin, ring = st0.copy(), np.zeros((b, d, S))
+    ring[..., :] = st0  # ring slots 0..S-1 hold the state with cache_seqlens = 0 meaning "next write at 0"
+    outs_l, outs_r = [], []
+    for t in range(T):
+        ol, lin = O.causal_conv1d_update(x[..., t], lin, wt, bias, "silu")
+        orr, ring = O.causal_conv1d_update(x[..., t], ring, wt, bias, "silu",
+                                           cache_seqlens=np.full(b, t))
+        outs_l.append(ol)
+        outs_r.append(orr)
+    np.testing.assert_allclose(np.stack(outs_r, -1), np.stack(outs_l, -1), rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(lin, np.roll(ring, -(T % S), axis=-1), rtol=0, atol=0)
+    o6, r6 = O.causal_conv1d_update(x[..., :2], ring, wt, bias, "silu", cache_seqlens=np.full(b, T))
+    o7, l7 = O.causal_conv1d_update(x[..., :2], lin, wt, bias, "silu")
+    np.testing.assert_allclose(o6, o7, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(l7, np.roll(r6, -((T + 2) % S), axis=-1), rtol=0, atol=0)
+
+
+def test_state_update_batch_indices_invariants():
+    rng = np.random.default_rng(22)
+    b, d, n = 3, 5, 4
+    x, dt, z = rng.standard_normal((b, d)), rng.random((b, d)), rng.standard_normal((b, d))
+    A, D, dtb = -rng.random((d, n)), rng.standard_normal(d), rng.random(d)
+    B, C = rng.standard_normal((b, n)), rng.standard_normal((b, n))
+    big = rng.standard_normal((7, d, n))
+    idx = np.array([6, 1, 3])
+    o1, s1 = O.selective_state_update(big, x, dt, A, B, C, D, z, dtb, True, state_batch_indices=idx)
+    o2, s2 = O.selective_state_update(big[idx], x, dt, A, B, C, D, z, dtb, True)
+    np.testing.assert_array_equal(o1, o2)
+    np.testing.assert_array_equal(s1[idx], s2)
+    rest = [0, 2, 4, 5]
+    np.testing.assert_array_equal(s1[rest], big[rest])
+    o3, s3 = O.selective_state_update(big, x, dt, A, B, C, D, z, dtb, True,
+                                      state_batch_indices=np.array([6, 7, -2]))
+    np.testing.assert_array_equal(o3[0], o2[0])
+    assert (o3[1:] == 0).all()
+    np.testing.assert_array_equal(s3[:6], big[:6])

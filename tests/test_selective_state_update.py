@@ -3,7 +3,8 @@
 Mirrors the reference's tests/test_selective_state_update.py (L single steps
 equal the full scan; Mamba-2 head layout equals the flattened Mamba-1 layout)
 and adds direct comparisons with the float64 oracle for both layouts, grouped
-B/C, a bf16 state and the rejected argument. Tolerance rtol/atol 1e-5 (float32).
+B/C, a bf16 state and state_batch_indices (which the reference rejects).
+Tolerance rtol/atol 1e-5 (float32).
 """
 
 import numpy as np
@@ -107,10 +108,34 @@ def test_bf16_state_and_inputs():
     close(state, want_state, 2e-2, 2e-2)
 
 
-def test_rejects_state_batch_indices():
+@pytest.mark.parametrize("heads", [False, True])
+def test_state_batch_indices_match_oracle(heads):
+    """state_batch_indices (rows of a larger state, one out of range), which
+    the reference rejects, against the oracle's restatement of mamba_ssm's
+    semantics."""
+    torch.manual_seed(5)
+    b, h, p, n, rows = 3, 2, 8, 16, 7
+    lead = (b, h, p) if heads else (b, h * p)
+    prm = (h, p) if heads else (h * p,)
+    state = torch.randn((rows,) + lead[1:] + (n,), device=DEV)
+    x, z = torch.randn(lead, device=DEV), torch.randn(lead, device=DEV)
+    dt = torch.rand(lead, device=DEV)
+    A = -torch.rand(prm + (n,), device=DEV) - 0.5
+    B = torch.randn((b, 1, n) if heads else (b, n), device=DEV)
+    C = torch.randn((b, 1, n) if heads else (b, n), device=DEV)
+    D, dtb = torch.randn(prm, device=DEV), torch.rand(prm, device=DEV) * 0.1
+    idx = torch.tensor([5, 1, -1], dtype=torch.int32, device=DEV)
+    want, want_state = O.selective_state_update(state, x, dt, A, B, C, D, z, dtb, True,
+                                                state_batch_indices=idx.cpu().numpy())
+    out = selective_state_update(state, x, dt, A, B, C, D, z, dtb, True, state_batch_indices=idx)
+    close(out, want, 1e-5, 1e-5, "out")
+    close(state, want_state, 1e-5, 1e-5, "state")
+
+
+def test_rejects_malformed_state_batch_indices():
     s = torch.zeros(1, 4, 2, device=DEV)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):
         selective_state_update(s, torch.zeros(1, 4, device=DEV), torch.zeros(1, 4, device=DEV),
                                torch.zeros(4, 2, device=DEV), torch.zeros(1, 2, device=DEV),
                                torch.zeros(1, 2, device=DEV),
-                               state_batch_indices=torch.zeros(1, dtype=torch.int32, device=DEV))
+                               state_batch_indices=torch.zeros(2, dtype=torch.int32, device=DEV))
