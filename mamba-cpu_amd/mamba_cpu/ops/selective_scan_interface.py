@@ -14,6 +14,8 @@ Hugging Face's transposed projections reach the kernel without copies.
 
 from typing import Optional
 
+import math
+
 import torch
 
 from mamba_cpu import _C  # noqa: F401  (loads the operator library)
@@ -94,6 +96,19 @@ def _as_kernel_bc(X: torch.Tensor) -> torch.Tensor:
     return X.float().transpose(-1, -2)
 
 
+def _kernel_bc_groups(X: torch.Tensor, ngroups: int, batch: int, seqlen: int) -> torch.Tensor:
+    """B or C as the kernels' float32 (b, ngroups, l, n) operand. A 2-D
+    (dim, dstate) tensor is one group per channel, constant in time: a
+    stride-0 view. Fewer groups than ngroups are repeated (a copy of the small
+    B/C tensor); autograd sums the gradient back."""
+    if X.dim() == 2:
+        return X.float()[None, :, None, :].expand(batch, X.shape[0], seqlen, X.shape[1])
+    Xk = _as_kernel_bc(X)
+    if Xk.shape[1] != ngroups:
+        Xk = Xk.repeat_interleave(ngroups // Xk.shape[1], dim=1)
+    return Xk
+
+
 def _as_x(t: Optional[torch.Tensor], dtype) -> Optional[torch.Tensor]:
     return None if t is None else t.to(dtype)
 
@@ -115,7 +130,8 @@ def selective_scan_fn(
 
     u, delta, z: (batch, dim, seqlen), float32 / bfloat16 / float16
     A: (dim, dstate), real-valued
-    B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen)
+    B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen), input-dependent,
+          with their own group counts; or (dim, dstate), input-independent
     D, delta_bias: (dim,)
     Returns out: (batch, dim, seqlen) in u's dtype [, last_state: (batch, dim, dstate) float32]
     Arithmetic and the scan state are float32 for every input dtype.
@@ -124,15 +140,20 @@ def selective_scan_fn(
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {u.device}")
     if A.is_complex():
         raise NotImplementedError("complex A is not supported yet")
-    if B.dim() < 3 or C.dim() < 3:
-        raise NotImplementedError("input-independent (2D) B/C is not supported yet")
-    dim = u.shape[1]
+    batch, dim, seqlen = u.shape
+
+    def groups(X):
+        return dim if X.dim() == 2 else (1 if X.dim() == 3 else X.shape[1])
+
     for name, X in (("B", B), ("C", C)):
-        ngroups = 1 if X.dim() == 3 else X.shape[1]
-        if dim % ngroups != 0:
-            raise ValueError(f"dim ({dim}) must be divisible by {name}'s ngroups ({ngroups})")
-    if B.dim() != C.dim() or (B.dim() == 4 and B.shape[1] != C.shape[1]):
-        raise NotImplementedError("B and C must have the same number of groups")
+        if X.dim() == 2 and X.shape[0] != dim:
+            raise ValueError(f"an input-independent {name} must be (dim, dstate), got {tuple(X.shape)}")
+        if dim % groups(X) != 0:
+            raise ValueError(f"dim ({dim}) must be divisible by {name}'s ngroups ({groups(X)})")
+    # The kernels take one group count for B and C. Unequal counts (and 2-D,
+    # input-independent B/C, which are one group per channel) run at their
+    # least common multiple; the reference rejects both (:160-170).
+    ngroups = math.lcm(groups(B), groups(C))
 
     # u/delta/z keep their storage type when they share a supported one;
     # mixed or other types are computed from float32 copies.
@@ -140,8 +161,9 @@ def selective_scan_fn(
     if xdt not in _X_DTYPES or delta.dtype != xdt or (z is not None and z.dtype != xdt):
         xdt = torch.float32
     args = (
-        _as_x(u, xdt), _as_x(delta, xdt), _as_f32(A), _as_kernel_bc(B), _as_kernel_bc(C),
-        _as_f32(D), _as_x(z, xdt), _as_f32(delta_bias), bool(delta_softplus),
+        _as_x(u, xdt), _as_x(delta, xdt), _as_f32(A), _kernel_bc_groups(B, ngroups, batch, seqlen),
+        _kernel_bc_groups(C, ngroups, batch, seqlen), _as_f32(D), _as_x(z, xdt), _as_f32(delta_bias),
+        bool(delta_softplus),
     )
     needs_grad = torch.is_grad_enabled() and any(
         isinstance(t, torch.Tensor) and t.requires_grad for t in args)

@@ -24,7 +24,8 @@ def selective_scan_ref(
     """
     u, delta, z: (batch, dim, seqlen)
     A: (dim, dstate)
-    B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen)
+    B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen) (each
+          with its own group count), or (dim, dstate) input-independent
     D, delta_bias: (dim,)
     Returns out: (batch, dim, seqlen) [, last_state: (batch, dim, dstate)]
 
@@ -40,11 +41,14 @@ def selective_scan_ref(
         dt = F.softplus(dt)
     batch, dim, seqlen = u.shape
     A = A.float()
-    Bg = B.float() if B.dim() == 4 else B.float()[:, None]
-    Cg = C.float() if C.dim() == 4 else C.float()[:, None]
-    per_group = dim // Bg.shape[1]
-    Bd = Bg.repeat_interleave(per_group, dim=1)  # (batch, dim, dstate, seqlen)
-    Cd = Cg.repeat_interleave(per_group, dim=1)
+
+    def per_channel(X):  # (batch, dim, dstate, seqlen); B and C group independently
+        if X.dim() == 2:  # input-independent (dim, dstate)
+            return X.float()[None, :, :, None].expand(batch, dim, X.shape[1], seqlen)
+        Xg = X.float() if X.dim() == 4 else X.float()[:, None]
+        return Xg.repeat_interleave(dim // Xg.shape[1], dim=1)
+
+    Bd, Cd = per_channel(B), per_channel(C)
     h = u.new_zeros(batch, dim, A.shape[1])
     ys = []
     for t in range(seqlen):

@@ -45,6 +45,16 @@ def _groups(X, dim):
     return X, dim // g
 
 
+def _input_independent(X, batch, seqlen):
+    """A 2-D (dim, dstate) B or C (input-independent, mamba_ssm's
+    `is_variable_B = False` case) as the equivalent (b, dim, n, l) tensor:
+    one group per channel, the same values at every step; None for 3-/4-D."""
+    X = _f64(X)
+    if X.ndim != 2:
+        return None
+    return np.broadcast_to(X[None, :, :, None], (batch, X.shape[0], X.shape[1], seqlen))
+
+
 def _dt(delta, delta_bias, delta_softplus):
     """row_dt (csrc/selective_scan.cpp:112-115): softplus?(delta + bias)."""
     dt = delta if delta_bias is None else delta + delta_bias[None, :, None]
@@ -57,19 +67,25 @@ def selective_scan_fwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
         dt_t = softplus?(delta_t + bias)
         h_t  = exp(dt_t * A) * h_{t-1} + dt_t * u_t * B_t       (h_{-1} = 0)
         y_t  = <h_t, C_t> + D * u_t ;  out_t = y_t * silu(z_t)
+    B and C may have different group counts, and either may be 2-D
+    (dim, dstate), input-independent (mamba_ssm's selective_scan_ref).
     Returns (out, last_state) with last_state = h_{L-1}, shape (b, d, n)."""
     u, delta, A = _f64(u), _f64(delta), _f64(A)
     D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
     batch, dim, seqlen = u.shape
+    for name in ("B", "C"):
+        X = _input_independent(B if name == "B" else C, batch, seqlen)
+        if X is not None:
+            B, C = (X, C) if name == "B" else (B, X)
     B, dpg = _groups(B, dim)
-    C, _ = _groups(C, dim)
+    C, dpgC = _groups(C, dim)
     dt = _dt(delta, delta_bias, delta_softplus)
     h = np.zeros((batch, dim, A.shape[1]))
     y = np.zeros((batch, dim, seqlen))
     with np.errstate(over="ignore", invalid="ignore"):
         for t in range(seqlen):
             Bt = np.repeat(B[:, :, :, t], dpg, axis=1)  # (b, d, n)
-            Ct = np.repeat(C[:, :, :, t], dpg, axis=1)
+            Ct = np.repeat(C[:, :, :, t], dpgC, axis=1)
             a = np.exp(dt[:, :, t, None] * A[None])
             h = a * h + (dt[:, :, t] * u[:, :, t])[..., None] * Bt
             y[:, :, t] = (h * Ct).sum(-1)
@@ -96,12 +112,15 @@ def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     u, delta, A = _f64(u), _f64(delta), _f64(A)
     D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
     dout, dlast_state = _f64(dout), _f64(dlast_state)
-    bc3 = _f64(B).ndim == 3
     batch, dim, seqlen = u.shape
     N = A.shape[1]
+    ndimB, ndimC = _f64(B).ndim, _f64(C).ndim
+    B2, C2 = _input_independent(B, batch, seqlen), _input_independent(C, batch, seqlen)
+    B = B if B2 is None else B2
+    C = C if C2 is None else C2
     B, dpg = _groups(B, dim)
-    C, _ = _groups(C, dim)
-    G = B.shape[1]
+    C, dpgC = _groups(C, dim)
+    G, GC = B.shape[1], C.shape[1]
     if dout is None:
         dout = np.zeros_like(u)
     dt = _dt(delta, delta_bias, delta_softplus)
@@ -121,10 +140,10 @@ def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
         dz = None if z is None else np.zeros_like(u)
         dA = np.zeros((batch, dim, N))
         dB = np.zeros((batch, G, N, seqlen))
-        dC = np.zeros((batch, G, N, seqlen))
+        dC = np.zeros((batch, GC, N, seqlen))
         for t in range(seqlen - 1, -1, -1):
             Bt = np.repeat(B[:, :, :, t], dpg, axis=1)
-            Ct = np.repeat(C[:, :, :, t], dpg, axis=1)
+            Ct = np.repeat(C[:, :, :, t], dpgC, axis=1)
             h, h_prev = hs[t + 1], hs[t]
             ut, dtt = u[:, :, t], dt[:, :, t]
             dy = dout[:, :, t]
@@ -147,14 +166,15 @@ def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
             ddelta[:, :, t] = ddt
             gh = g * a
             dB[:, :, :, t] = dBc.reshape(batch, G, dpg, N).sum(2)
-            dC[:, :, :, t] = dCc.reshape(batch, G, dpg, N).sum(2)
+            dC[:, :, :, t] = dCc.reshape(batch, GC, dpgC, N).sum(2)
         dD_full = None
         if D is not None:
             dy_all = dout if z is None else dout * z * sigmoid(z)
             dD_full = (dy_all * u).sum((0, 2))
         ddelta_bias = None if delta_bias is None else ddelta.sum((0, 2))
-    if bc3:
-        dB, dC = dB[:, 0], dC[:, 0]
+    # dB/dC in B's and C's own shapes: (b, n, l), (b, g, n, l) or (dim, n).
+    dB = dB.sum((0, 3)) if ndimB == 2 else (dB[:, 0] if ndimB == 3 else dB)
+    dC = dC.sum((0, 3)) if ndimC == 2 else (dC[:, 0] if ndimC == 3 else dC)
     return du, ddelta, dA.sum(0), dB, dC, dD_full, dz, ddelta_bias
 
 

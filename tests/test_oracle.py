@@ -389,3 +389,42 @@ def test_state_update_batch_indices_invariants():
     np.testing.assert_array_equal(o3[0], o2[0])
     assert (o3[1:] == 0).all()
     np.testing.assert_array_equal(s3[:6], big[:6])
+
+
+def test_scan_unequal_groups_and_2d_bc_equal_expanded():
+    """Pins the oracle's extensions beyond the reference's kernels (which take
+    one group count for both B and C, and no 2-D B/C): B and C with different
+    group counts equal both repeated to a common count; a 2-D (dim, dstate)
+    B or C equals the (batch, dim, dstate, seqlen) tensor repeating it at
+    every step, and its gradient is that tensor's gradient summed over batch
+    and time."""
+    inp = scan_case(2, 12, 9, 4, None, True, seed=31)
+    rng = np.random.default_rng(32)
+    B1 = rng.standard_normal((2, 1, 4, 9))
+    C3 = rng.standard_normal((2, 3, 4, 9))
+    G = rng.standard_normal((2, 12, 9))
+    base = {k: inp[k] for k in ("u", "delta", "A", "D", "z", "delta_bias")}
+    out_u, last_u = O.selective_scan_fwd(**base, B=B1, C=C3, delta_softplus=True)
+    out_e, last_e = O.selective_scan_fwd(**base, B=np.repeat(B1, 3, axis=1), C=C3, delta_softplus=True)
+    np.testing.assert_allclose(out_u, out_e, rtol=1e-13)
+    np.testing.assert_allclose(last_u, last_e, rtol=1e-13)
+    gu = O.selective_scan_bwd(**base, B=B1, C=C3, delta_softplus=True, dout=G)
+    ge = O.selective_scan_bwd(**base, B=np.repeat(B1, 3, axis=1), C=C3, delta_softplus=True, dout=G)
+    for i in (0, 1, 2, 4, 5, 6, 7):
+        np.testing.assert_allclose(gu[i], ge[i], rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(gu[3], ge[3].reshape(2, 1, 3, 4, 9).sum(2), rtol=1e-12)
+    # 2-D B and C
+    B2, C2 = rng.standard_normal((12, 4)), rng.standard_normal((12, 4))
+    B4 = np.broadcast_to(B2[None, :, :, None], (2, 12, 4, 9)).copy()
+    C4 = np.broadcast_to(C2[None, :, :, None], (2, 12, 4, 9)).copy()
+    for Bx, Cx, Be, Ce in ((B2, C3, B4, C3), (B1, C2, B1, C4), (B2, C2, B4, C4)):
+        o2, _ = O.selective_scan_fwd(**base, B=Bx, C=Cx, delta_softplus=True)
+        o4, _ = O.selective_scan_fwd(**base, B=Be, C=Ce, delta_softplus=True)
+        np.testing.assert_allclose(o2, o4, rtol=1e-13)
+        g2 = O.selective_scan_bwd(**base, B=Bx, C=Cx, delta_softplus=True, dout=G)
+        g4 = O.selective_scan_bwd(**base, B=Be, C=Ce, delta_softplus=True, dout=G)
+        for i in (0, 1, 2, 5, 6, 7):
+            np.testing.assert_allclose(g2[i], g4[i], rtol=1e-12, atol=1e-14)
+        for i, X in ((3, Bx), (4, Cx)):
+            want = g4[i].sum((0, 3)) if X.ndim == 2 else g4[i]
+            np.testing.assert_allclose(g2[i], want, rtol=1e-12, atol=1e-14)

@@ -168,6 +168,36 @@ def test_rejects_complex():
         selective_scan_fn(**inp)
 
 
+@pytest.mark.parametrize("case", ["groups_1_3", "groups_2_1", "B_2d", "C_2d", "both_2d"])
+def test_unequal_groups_and_input_independent_bc(case):
+    """B and C with their own group counts, and 2-D (dim, dstate)
+    input-independent B/C (both rejected by the reference,
+    selective_scan_interface.py:160-170): forward and every gradient against
+    the oracle."""
+    torch.manual_seed(11)
+    b, d, l, n = 2, 24, 37, 8
+    shapes = {"groups_1_3": ((b, n, l), (b, 3, n, l)), "groups_2_1": ((b, 2, n, l), (b, n, l)),
+              "B_2d": ((d, n), (b, 2, n, l)), "C_2d": ((b, n, l), (d, n)), "both_2d": ((d, n), (d, n))}[case]
+    u = torch.randn(b, d, l, device=DEV, requires_grad=True)
+    delta = (torch.rand(b, d, l, device=DEV) * 0.5).requires_grad_()
+    A = (-torch.rand(d, n, device=DEV) - 0.5).requires_grad_()
+    B = torch.randn(shapes[0], device=DEV, requires_grad=True)
+    C = torch.randn(shapes[1], device=DEV, requires_grad=True)
+    D = torch.randn(d, device=DEV, requires_grad=True)
+    z = torch.randn(b, d, l, device=DEV, requires_grad=True)
+    bias = (torch.rand(d, device=DEV) * 0.1).requires_grad_()
+    out = selective_scan_fn(u, delta, A, B, C, D, z, bias, True)
+    want, _ = O.selective_scan_fwd(u, delta, A, B, C, D, z, bias, True)
+    close(out, want, 1e-4, 1e-5, "out")
+    G = torch.randn(b, d, l, device=DEV)
+    (out * G).sum().backward()
+    grads = O.selective_scan_bwd(u, delta, A, B, C, D, z, bias, True, dout=G)
+    for name, t, g in zip(["u", "delta", "A", "B", "C", "D", "z", "delta_bias"],
+                          [u, delta, A, B, C, D, z, bias], grads):
+        scale = max(1.0, float(np.abs(g).max()))
+        close(t.grad / scale, g / scale, 1e-3, 1e-4, name)
+
+
 def decay_inputs(x, seqlen=4, dstate=8):
     """Inputs where every step's dt*A equals x per channel (reference
     tests/test_selective_scan.py:146-158); x: (dim,)."""
