@@ -167,6 +167,12 @@ typedef struct mcpu_conv_args {
   float* dweight;               /* (dim, width) */
   float* dbias;                 /* (dim), required iff bias != NULL */
   void* dinitial_states;        /* (batch, dim, width-1) contiguous, dtype; optional */
+  /* (batch, seqlen) contiguous int32, optional: packed sequences; a tap
+     reading an input of another sequence counts as zero (the upstream
+     causal_conv1d package's semantics; the reference rejects seq_idx,
+     ops/causal_conv1d.py:34-35). Excludes initial_states, final_states and
+     dfinal_states. */
+  const int32_t* seq_idx;
 } mcpu_conv_args;
 
 int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream);

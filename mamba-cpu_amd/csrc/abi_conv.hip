@@ -20,6 +20,10 @@ int check_conv(const mcpu_conv_args* a) {
     return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d: width must be in [1, %lld], got %lld",
                 (long long)kConvMaxW, (long long)a->width);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "causal_conv1d: bad dtype %d", a->dtype);
+  if (a->seq_idx != nullptr &&
+      (a->initial_states != nullptr || a->final_states != nullptr || a->dfinal_states != nullptr ||
+       a->dinitial_states != nullptr))
+    return fail(MCPU_ERR_INVALID, "causal_conv1d: seq_idx excludes initial and final states");
   return MCPU_OK;
 }
 
@@ -44,6 +48,7 @@ ConvParams make_conv(const mcpu_conv_args* a) {
     p.sdx[i] = a->dx_stride[i];
   }
   p.silu = a->silu != 0;
+  p.seq_idx = a->seq_idx;
   p.channels_last = (a->x_stride[1] == 1 && a->x_stride[2] != 1) ? 1 : 0;
   return p;
 }
@@ -79,6 +84,7 @@ bool vt_operand(const void* ptr, const int64_t (&s)[3], int dtype) {
 
 // The fast path's steps per thread (8 or 16), or 0 where it does not apply.
 int vt_ok(const ConvParams& p, int dtype, bool bwd) {
+  if (p.seq_idx != nullptr) return 0;  // the chunked kernels mask the taps
   const int steps = conv_vt_steps(dtype, p.seqlen);
   if (p.width < 2 || p.width > 5 || p.seqlen < steps || p.seqlen % steps != 0) return 0;
   if (!vt_operand(p.x, p.sx, dtype)) return 0;

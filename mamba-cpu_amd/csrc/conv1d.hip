@@ -45,10 +45,17 @@ __device__ __forceinline__ float conv_x(const ConvParams& p, const ConvRow& c, i
   return ld<T>(p.init, c.b * p.sinit[0] + c.d * p.sinit[1] + (p.width - 1 + s) * p.sinit[2]);
 }
 
+// Packed-sequence id of step s of row b, or a value no id equals outside the
+// sequence (the taps there read zeros anyway: seq_idx excludes initial states).
+__device__ __forceinline__ int64_t conv_seq(const ConvParams& p, int64_t b, int64_t s) {
+  return (s >= 0 && s < p.seqlen) ? static_cast<int64_t>(p.seq_idx[b * p.seqlen + s]) : INT64_MIN;
+}
+
 // WT: the width as a compile-time constant (2..5), or 0 for any width up to
 // kConvMaxW read from the parameters. With a fixed width the window and tap
-// loops unroll to exactly the taps that exist.
-template <typename T, int WT>
+// loops unroll to exactly the taps that exist. SEQ: packed sequences (seq_idx);
+// a tap reading another sequence's input counts as zero.
+template <typename T, int WT, bool SEQ>
 __global__ void __launch_bounds__(256) conv_fwd_kernel(const ConvParams p) {
   constexpr int MW = WT > 0 ? WT : kConvMaxW;
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
@@ -62,10 +69,12 @@ __global__ void __launch_bounds__(256) conv_fwd_kernel(const ConvParams p) {
   for (int64_t ch = c.r; ch < p.nchunks; ch += p.R) {
     const int64_t t0 = ch * kConvT;
     float win[kConvT + MW - 1];
+    int64_t sq[SEQ ? kConvT + MW - 1 : 1];
 #pragma unroll
     for (int i = 0; i < kConvT + MW - 1; ++i) {
       const int64_t s = t0 - (W - 1) + i;
       win[i] = (i < kConvT + W - 1 && s < p.seqlen) ? conv_x<T>(p, c, s) : 0.f;
+      if constexpr (SEQ) sq[i] = conv_seq(p, c.b, s);
     }
 #pragma unroll
     for (int i = 0; i < kConvT; ++i) {
@@ -73,8 +82,12 @@ __global__ void __launch_bounds__(256) conv_fwd_kernel(const ConvParams p) {
       if (t >= p.seqlen) break;
       float acc = bias;
 #pragma unroll
-      for (int k = 0; k < MW; ++k)
-        if (k < W) acc = fmaf(w[k], win[i + k], acc);
+      for (int k = 0; k < MW; ++k) {
+        if (k >= W) continue;
+        float xk = win[i + k];
+        if constexpr (SEQ) xk = sq[i + k] == sq[i + W - 1] ? xk : 0.f;
+        acc = fmaf(w[k], xk, acc);
+      }
       if (p.silu) acc = acc * sigmoid(acc);
       st<T>(p.out, c.b * p.sout[0] + c.d * p.sout[1] + t * p.sout[2], acc);
     }
@@ -102,7 +115,7 @@ __global__ void __launch_bounds__(256) conv_final_states_kernel(const ConvParams
 // dX[s] goes to dx for s >= 0 and to dinitial_states for s < 0 (handled by the
 // thread of chunk 0). dw/dbias accumulate dpre[t] X[t-(W-1)+k] over this
 // thread's steps and are written as one partial per thread.
-template <typename T, int WT>
+template <typename T, int WT, bool SEQ>
 __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
   constexpr int MW = WT > 0 ? WT : kConvMaxW;
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
@@ -130,10 +143,14 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
     // [s0 - (W-1), s0 + nout + W - 1).
     float xw[kConvT + 2 * (MW - 1)];
     float dp[kConvT + MW - 1];
+    int64_t sq[SEQ ? kConvT + 2 * (MW - 1) : 1];  // ids of the xw positions
+    // Tap mask: input at xw index a feeds the output whose own xw index is o.
+    auto same = [&](int a, int o) { if constexpr (SEQ) return sq[a] == sq[o]; else return true; };
 #pragma unroll
     for (int i = 0; i < kConvT + 2 * (MW - 1); ++i) {
       const int64_t s = s0 - (W - 1) + i;
       xw[i] = (i < nout + 2 * (W - 1) && s < L) ? conv_x<T>(p, c, s) : 0.f;
+      if constexpr (SEQ) sq[i] = conv_seq(p, c.b, s);
     }
 #pragma unroll
     for (int i = 0; i < kConvT + MW - 1; ++i) {
@@ -143,7 +160,7 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
         float pre = bias;
 #pragma unroll
         for (int k = 0; k < MW; ++k)
-          if (k < W) pre = fmaf(w[k], xw[i + k], pre);
+          if (k < W) pre = fmaf(w[k], same(i + k, i + W - 1) ? xw[i + k] : 0.f, pre);
         const float go = ld<T>(p.dout, c.b * p.sdo[0] + c.d * p.sdo[1] + t * p.sdo[2]);
         if (p.silu) {
           const float sg = sigmoid(pre);
@@ -162,7 +179,7 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
           dbias += dp[i];
 #pragma unroll
           for (int k = 0; k < MW; ++k)
-            if (k < W) dw[k] = fmaf(dp[i], xw[i + k], dw[k]);
+            if (k < W) dw[k] = fmaf(same(i + k, i + W - 1) ? dp[i] : 0.f, xw[i + k], dw[k]);
         }
       }
     }
@@ -174,7 +191,8 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < MW; ++k)
-        if (k < W) acc = fmaf(w[k], dp[i + (W - 1) - k], acc);
+        if (k < W)
+          acc = fmaf(w[k], same(i + W - 1, i + 2 * (W - 1) - k) ? dp[i + (W - 1) - k] : 0.f, acc);
       if (p.dfinal != nullptr && s >= fin0)
         acc += ld<T>(p.dfinal, (c.b * p.dim + c.d) * (W - 1) + (s - fin0));
       if (s >= 0) {
@@ -536,13 +554,13 @@ static hipError_t launch_vt_dtype(const ConvParams& p, int dtype, bool bwd, hipS
 static unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 // The chunked kernels, specialised for widths 2..5 (Mamba's is 4).
-template <typename T>
-static hipError_t launch_generic(const ConvParams& p, bool bwd, unsigned grid, hipStream_t st) {
+template <typename T, bool SEQ>
+static hipError_t launch_generic_seq(const ConvParams& p, bool bwd, unsigned grid, hipStream_t st) {
   switch (p.width) {
-#define MCPU_CONV_GEN(WW)                                                                     \
-  case WW:                                                                                    \
-    if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);  \
-    else hipLaunchKernelGGL((conv_fwd_kernel<T, WW>), dim3(grid), dim3(256), 0, st, p);      \
+#define MCPU_CONV_GEN(WW)                                                                          \
+  case WW:                                                                                         \
+    if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, WW, SEQ>), dim3(grid), dim3(256), 0, st, p);  \
+    else hipLaunchKernelGGL((conv_fwd_kernel<T, WW, SEQ>), dim3(grid), dim3(256), 0, st, p);      \
     break;
     MCPU_CONV_GEN(2)
     MCPU_CONV_GEN(3)
@@ -550,10 +568,16 @@ static hipError_t launch_generic(const ConvParams& p, bool bwd, unsigned grid, h
     MCPU_CONV_GEN(5)
 #undef MCPU_CONV_GEN
     default:
-      if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, 0>), dim3(grid), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((conv_fwd_kernel<T, 0>), dim3(grid), dim3(256), 0, st, p);
+      if (bwd) hipLaunchKernelGGL((conv_bwd_kernel<T, 0, SEQ>), dim3(grid), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((conv_fwd_kernel<T, 0, SEQ>), dim3(grid), dim3(256), 0, st, p);
   }
   return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_generic(const ConvParams& p, bool bwd, unsigned grid, hipStream_t st) {
+  return p.seq_idx != nullptr ? launch_generic_seq<T, true>(p, bwd, grid, st)
+                              : launch_generic_seq<T, false>(p, bwd, grid, st);
 }
 
 static hipError_t launch_generic_dtype(const ConvParams& p, int dtype, bool bwd, unsigned grid,

@@ -29,6 +29,7 @@ struct ConvParams {
   int64_t nchunks, R;
   int64_t sx[3], sinit[3], sout[3], sdo[3], sdx[3];
   int silu;
+  const int32_t* seq_idx;  // (batch, seqlen) packed-sequence ids, or null
   int channels_last;  // thread index decomposed channel-fastest
   // Time-contiguous fast path (conv_*_vt_kernel): vt = steps per thread (8 or
   // 16), 0 when the path does not apply.

@@ -374,10 +374,22 @@ void check_conv(const char* name, const Tensor& x, const Tensor& weight,
                     name, " expects initial_states (batch, dim, width - 1) in x's dtype");
 }
 
+// Optional (batch, seqlen) packed-sequence ids of the conv.
+void check_seq_idx(const char* name, const optional<Tensor>& seq_idx, const Tensor& x) {
+  if (!has(seq_idx)) return;
+  check_gpu(name, seq_idx);
+  TORCH_CHECK_VALUE(seq_idx->scalar_type() == at::kInt && seq_idx->dim() == 2 &&
+                        seq_idx->size(0) == x.size(0) && seq_idx->size(1) == x.size(2) &&
+                        seq_idx->is_contiguous(),
+                    name, " expects seq_idx as a contiguous int32 tensor of shape (batch, seqlen)");
+}
+
 mcpu_conv_args conv_args(const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
-                         const optional<Tensor>& init, bool silu) {
+                         const optional<Tensor>& init, bool silu,
+                         const optional<Tensor>& seq_idx = std::nullopt) {
   mcpu_conv_args a;
   std::memset(&a, 0, sizeof(a));
+  a.seq_idx = has(seq_idx) ? static_cast<const int32_t*>(seq_idx->data_ptr()) : nullptr;
   a.x = x.data_ptr();
   a.weight = static_cast<const float*>(weight.data_ptr());
   a.bias = fptr(bias);
@@ -396,7 +408,8 @@ mcpu_conv_args conv_args(const Tensor& x, const Tensor& weight, const optional<T
 std::tuple<Tensor, Tensor> causal_conv1d_fwd(const Tensor& x, const Tensor& weight,
                                              const optional<Tensor>& bias,
                                              const optional<Tensor>& init,
-                                             bool return_final_states, bool silu) {
+                                             bool return_final_states, bool silu,
+                                             const optional<Tensor>& seq_idx) {
   const char* name = "mamba_cpu::causal_conv1d_fwd";
   check_conv(name, x, weight, bias, init);
   c10::DeviceGuard guard(x.device());
@@ -404,7 +417,8 @@ std::tuple<Tensor, Tensor> causal_conv1d_fwd(const Tensor& x, const Tensor& weig
   const int64_t b = x.size(0), d = x.size(1), w = weight.size(1);
   Tensor final = return_final_states ? at::empty({b, d, w - 1}, x.options())
                                      : at::empty({0}, x.options());
-  mcpu_conv_args a = conv_args(x, weight, bias, init, silu);
+  check_seq_idx("mamba_cpu::causal_conv1d_fwd", seq_idx, x);
+  mcpu_conv_args a = conv_args(x, weight, bias, init, silu, seq_idx);
   a.out = out.data_ptr();
   strides3(a.out_stride, out);
   a.final_states = return_final_states ? final.data_ptr() : nullptr;
@@ -415,8 +429,9 @@ std::tuple<Tensor, Tensor> causal_conv1d_fwd(const Tensor& x, const Tensor& weig
 std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
     const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
     const optional<Tensor>& init, const Tensor& dout, const optional<Tensor>& dfinal_states,
-    bool silu) {
+    bool silu, const optional<Tensor>& seq_idx) {
   const char* name = "mamba_cpu::causal_conv1d_bwd";
+  check_seq_idx(name, seq_idx, x);
   check_conv(name, x, weight, bias, init);
   check_gpu(name, dout);
   check_gpu(name, dfinal_states);
@@ -435,7 +450,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
   Tensor dweight = at::empty(weight.sizes(), weight.options());
   Tensor dbias = has(bias) ? at::empty({d}, weight.options()) : at::empty({0}, weight.options());
   Tensor dinit = has(init) ? at::empty({b, d, w - 1}, x.options()) : at::empty({0}, x.options());
-  mcpu_conv_args a = conv_args(x, weight, bias, init, silu);
+  mcpu_conv_args a = conv_args(x, weight, bias, init, silu, seq_idx);
   a.dout = dout.data_ptr();
   strides3(a.dout_stride, dout);
   a.dfinal_states = ptr(dfinal);
@@ -454,13 +469,15 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
 struct ConvFn : public torch::autograd::Function<ConvFn> {
   static variable_list forward(AutogradContext* ctx, const Tensor& x, const Tensor& weight,
                                const optional<Tensor>& bias, const optional<Tensor>& init,
-                               bool return_final_states, bool silu) {
+                               bool return_final_states, bool silu,
+                               const optional<Tensor>& seq_idx) {
     at::AutoDispatchBelowADInplaceOrView below;
     static auto op = c10::Dispatcher::singleton()
                          .findSchemaOrThrow("mamba_cpu::causal_conv1d_fwd", "")
                          .typed<decltype(causal_conv1d_fwd)>();
-    auto r = op.call(x, weight, bias, init, return_final_states, silu);
-    ctx->save_for_backward({x, weight, bias.value_or(Tensor()), init.value_or(Tensor())});
+    auto r = op.call(x, weight, bias, init, return_final_states, silu, seq_idx);
+    ctx->save_for_backward({x, weight, bias.value_or(Tensor()), init.value_or(Tensor()),
+                            seq_idx.value_or(Tensor())});
     ctx->saved_data["silu"] = silu;
     ctx->saved_data["final"] = return_final_states;
     ctx->set_materialize_grads(false);
@@ -470,7 +487,7 @@ struct ConvFn : public torch::autograd::Function<ConvFn> {
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     const variable_list s = ctx->get_saved_variables();
     const Tensor &x = s[0], &weight = s[1];
-    const optional<Tensor> bias = opt(s[2]), init = opt(s[3]);
+    const optional<Tensor> bias = opt(s[2]), init = opt(s[3]), seq_idx = opt(s[4]);
     const Tensor dout = grads[0].defined() ? grads[0].to(x.scalar_type()) : at::zeros_like(x);
     const optional<Tensor> dfinal = (ctx->saved_data["final"].toBool() && grads[1].defined())
                                         ? optional<Tensor>(grads[1])
@@ -478,17 +495,18 @@ struct ConvFn : public torch::autograd::Function<ConvFn> {
     static auto op = c10::Dispatcher::singleton()
                          .findSchemaOrThrow("mamba_cpu::causal_conv1d_bwd", "")
                          .typed<decltype(causal_conv1d_bwd)>();
-    auto g = op.call(x, weight, bias, init, dout, dfinal, ctx->saved_data["silu"].toBool());
+    auto g = op.call(x, weight, bias, init, dout, dfinal, ctx->saved_data["silu"].toBool(), seq_idx);
     return {std::get<0>(g), std::get<1>(g), has(bias) ? std::get<2>(g) : Tensor(),
-            has(init) ? std::get<3>(g) : Tensor(), Tensor(), Tensor()};
+            has(init) ? std::get<3>(g) : Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
 
 std::tuple<Tensor, Tensor> causal_conv1d_fwd_autograd(const Tensor& x, const Tensor& weight,
                                                       const optional<Tensor>& bias,
                                                       const optional<Tensor>& init,
-                                                      bool return_final_states, bool silu) {
-  auto r = ConvFn::apply(x, weight, bias, init, return_final_states, silu);
+                                                      bool return_final_states, bool silu,
+                                                      const optional<Tensor>& seq_idx) {
+  auto r = ConvFn::apply(x, weight, bias, init, return_final_states, silu, seq_idx);
   return {r[0], r[1]};
 }
 
@@ -672,9 +690,10 @@ TORCH_LIBRARY(mamba_cpu, m) {
         "Tensor ckpt, Tensor ysave) -> "
         "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("causal_conv1d_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
-        "bool return_final_states, bool silu) -> (Tensor, Tensor)");
+        "bool return_final_states, bool silu, Tensor? seq_idx=None) -> (Tensor, Tensor)");
   m.def("causal_conv1d_bwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
-        "Tensor dout, Tensor? dfinal_states, bool silu) -> (Tensor, Tensor, Tensor, Tensor)");
+        "Tensor dout, Tensor? dfinal_states, bool silu, Tensor? seq_idx=None) -> "
+        "(Tensor, Tensor, Tensor, Tensor)");
   m.def("causal_conv1d_update(Tensor x, Tensor(a!) conv_state, Tensor weight, Tensor? bias, "
         "bool silu, Tensor? cache_seqlens=None, Tensor? conv_state_indices=None) -> Tensor");
   m.def("selective_state_update(Tensor(a!) state, Tensor x, Tensor dt, Tensor A, Tensor B, "

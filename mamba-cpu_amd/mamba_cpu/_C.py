@@ -74,6 +74,7 @@ class ConvArgs(ctypes.Structure):
         ("out", _P), ("out_stride", _S3), ("final_states", _P),
         ("dout", _P), ("dout_stride", _S3), ("dfinal_states", _P),
         ("dx", _P), ("dx_stride", _S3), ("dweight", _P), ("dbias", _P), ("dinitial_states", _P),
+        ("seq_idx", _P),
     ]
 
 

@@ -40,14 +40,14 @@ def _like_x(x):
 
 
 @torch.library.register_fake("mamba_cpu::causal_conv1d_fwd")
-def _(x, weight, bias, initial_states, return_final_states, silu):
+def _(x, weight, bias, initial_states, return_final_states, silu, seq_idx=None):
     b, d, _ = x.shape
     final = x.new_empty(b, d, weight.shape[1] - 1) if return_final_states else x.new_empty(0)
     return _like_x(x), final
 
 
 @torch.library.register_fake("mamba_cpu::causal_conv1d_bwd")
-def _(x, weight, bias, initial_states, dout, dfinal_states, silu):
+def _(x, weight, bias, initial_states, dout, dfinal_states, silu, seq_idx=None):
     b, d, _ = x.shape
     return (
         _like_x(x), weight.new_empty(weight.shape),
@@ -84,12 +84,14 @@ def causal_conv1d_fn(
     x: (batch, dim, seqlen)
     weight: (dim, width)
     bias: (dim,)
+    seq_idx: optional (batch, seqlen) int: packed sequences; a tap reading an
+        input of another sequence counts as zero (the upstream causal_conv1d
+        package's semantics; the reference raises NotImplementedError,
+        ops/causal_conv1d.py:34-35). Excludes initial_states and final states.
     initial_states: (batch, dim, width - 1)
     final_states_out: optional (batch, dim, width - 1) buffer for the final states
     Returns out: (batch, dim, seqlen) in x's dtype [, final_states: (batch, dim, width - 1)]
     """
-    if seq_idx is not None:
-        raise NotImplementedError("seq_idx is not supported yet")
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
     silu = _silu_flag(activation)
@@ -97,9 +99,15 @@ def causal_conv1d_fn(
     if in_dtype not in _X_DTYPES:
         x = x.float()
     init = None if initial_states is None else initial_states.to(x.dtype)
+    if seq_idx is not None:
+        if initial_states is not None or return_final_states:
+            raise ValueError("seq_idx cannot be combined with initial_states or return_final_states")
+        if seq_idx.dtype not in (torch.int32, torch.int64) or seq_idx.shape != (x.shape[0], x.shape[2]):
+            raise ValueError(f"seq_idx must be an integer tensor of shape ({x.shape[0]}, {x.shape[2]})")
+        seq_idx = seq_idx.to(device=x.device, dtype=torch.int32).contiguous()
     out, final = torch.ops.mamba_cpu.causal_conv1d_fwd(
         x, weight.float().contiguous(), None if bias is None else bias.float().contiguous(), init,
-        bool(return_final_states), silu,
+        bool(return_final_states), silu, seq_idx,
     )
     out = out.to(in_dtype)
     if not return_final_states:

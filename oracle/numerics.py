@@ -178,11 +178,29 @@ def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     return du, ddelta, dA.sum(0), dB, dC, dD_full, dz, ddelta_bias
 
 
-def causal_conv1d_fwd(x, weight, bias=None, initial_states=None, activation=None):
+def _tap_mask(seq_idx, width, seqlen):
+    """(b, 1, width, seqlen) 0/1: tap k of output t reads x[t - (width-1) + k],
+    which counts only inside t's own sequence (seq_idx equal, position >= 0),
+    the upstream causal_conv1d package's seq_idx semantics. None without
+    seq_idx."""
+    if seq_idx is None:
+        return None
+    sq = np.asarray(seq_idx)
+    m = np.zeros((sq.shape[0], 1, width, seqlen))
+    for k in range(width):
+        src = np.arange(seqlen) - (width - 1) + k
+        ok = src >= 0
+        m[:, 0, k, ok] = (sq[:, src[ok]] == sq[:, ok]).astype(np.float64)
+    return m
+
+
+def causal_conv1d_fwd(x, weight, bias=None, initial_states=None, activation=None, seq_idx=None):
     """Depthwise causal conv (src/mamba_cpu/ops/causal_conv1d.py:16-53 and the
     explicit tap loop of src/mamba_cpu/reference.py:65-75):
         x_full = [initial_states or zeros(width-1), x]
         out_t  = act(bias + sum_k w[k] * x_full[t + k])
+    seq_idx (b, seqlen), which the reference rejects (:34-35): packed
+    sequences; a tap reading another sequence's input counts as zero.
     Returns (out, final_states) with final_states = last width-1 columns of x_full."""
     x, w, bias, init = _f64(x), _f64(weight), _f64(bias), _f64(initial_states)
     batch, dim, seqlen = x.shape
@@ -190,9 +208,11 @@ def causal_conv1d_fwd(x, weight, bias=None, initial_states=None, activation=None
     if init is None:
         init = np.zeros((batch, dim, width - 1))
     xf = np.concatenate([init, x], axis=-1)
+    mask = _tap_mask(seq_idx, width, seqlen)
     out = np.zeros((batch, dim, seqlen))
     for k in range(width):
-        out += w[None, :, k, None] * xf[:, :, k:k + seqlen]
+        tap = w[None, :, k, None] * xf[:, :, k:k + seqlen]
+        out += tap if mask is None else tap * mask[:, :, k]
     if bias is not None:
         out += bias[None, :, None]
     if activation in ("silu", "swish"):
@@ -201,7 +221,7 @@ def causal_conv1d_fwd(x, weight, bias=None, initial_states=None, activation=None
 
 
 def causal_conv1d_bwd(x, weight, bias=None, initial_states=None, dout=None, activation=None,
-                      dfinal_states=None):
+                      dfinal_states=None, seq_idx=None):
     """Backward of causal_conv1d_fwd, from the chain rule:
         pre_t = bias + sum_k w[k] x_full[t+k] ; dpre = dout * act'(pre)
         dx_full[s] += w[k] dpre[s-k] ; dw[k] = sum_{b,t} dpre[t] x_full[t+k] ; dbias = sum dpre
@@ -213,9 +233,11 @@ def causal_conv1d_bwd(x, weight, bias=None, initial_states=None, dout=None, acti
     width = w.shape[1]
     init_ = np.zeros((batch, dim, width - 1)) if init is None else init
     xf = np.concatenate([init_, x], axis=-1)
+    mask = _tap_mask(seq_idx, width, seqlen)
+    one = np.ones((1, 1, seqlen))
     pre = np.zeros((batch, dim, seqlen))
     for k in range(width):
-        pre += w[None, :, k, None] * xf[:, :, k:k + seqlen]
+        pre += w[None, :, k, None] * xf[:, :, k:k + seqlen] * (one if mask is None else mask[:, :, k])
     if bias_ is not None:
         pre += bias_[None, :, None]
     if activation in ("silu", "swish"):
@@ -226,8 +248,9 @@ def causal_conv1d_bwd(x, weight, bias=None, initial_states=None, dout=None, acti
     dxf = np.zeros_like(xf)
     dw = np.zeros_like(w)
     for k in range(width):
-        dxf[:, :, k:k + seqlen] += w[None, :, k, None] * dpre
-        dw[:, k] = (dpre * xf[:, :, k:k + seqlen]).sum((0, 2))
+        dpk = dpre if mask is None else dpre * mask[:, :, k]
+        dxf[:, :, k:k + seqlen] += w[None, :, k, None] * dpk
+        dw[:, k] = (dpk * xf[:, :, k:k + seqlen]).sum((0, 2))
     if dfinal_states is not None:
         dxf[:, :, xf.shape[-1] - (width - 1):] += _f64(dfinal_states)
     dbias = None if bias_ is None else dpre.sum((0, 2))

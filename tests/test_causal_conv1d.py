@@ -108,8 +108,9 @@ def test_mixed_dtypes_return_input_dtype():
 def test_rejects_unsupported_args():
     x = torch.randn(2, 8, 10, device=DEV)
     w = torch.randn(8, 4, device=DEV)
-    with pytest.raises(NotImplementedError):
-        causal_conv1d_fn(x, w, seq_idx=torch.zeros(2, 10, dtype=torch.int32, device=DEV))
+    with pytest.raises(ValueError):  # seq_idx excludes initial states
+        causal_conv1d_fn(x, w, seq_idx=torch.zeros(2, 10, dtype=torch.int32, device=DEV),
+                         initial_states=torch.zeros(2, 8, 3, device=DEV))
     with pytest.raises(ValueError):
         causal_conv1d_fn(x, w, activation="relu")
     with pytest.raises(ValueError):
@@ -286,3 +287,36 @@ def test_dweight_reduction_over_many_partials(batch, parts_per_row):
     _, dw, db, _ = O.causal_conv1d_bwd(x, w, bias, None, G, "silu")
     close(w.grad, dw, 1e-4, 1e-4, "dweight")
     close(bias.grad, db, 1e-4, 1e-4, "dbias")
+
+
+@pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
+@pytest.mark.parametrize("width", [2, 4, 7])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_seq_idx_matches_oracle(layout, width, dtype):
+    """Packed sequences (seq_idx, which the reference rejects): forward and
+    every gradient against the oracle, with boundaries inside and across the
+    8-step chunks and a one-step sequence."""
+    torch.manual_seed(width)
+    b, d, l = 2, 24, 45
+    xs = torch.randn(b, d, l, device=DEV) if layout == "contiguous" else \
+        torch.randn(b, l, d, device=DEV).transpose(1, 2)
+    x = xs.to(dtype).requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    seq = torch.zeros(b, l, dtype=torch.int32)
+    for bi, cuts in enumerate([[0, 3, 4, 16, 30, 45], [0, 45]]):
+        for si, (lo, hi) in enumerate(zip(cuts[:-1], cuts[1:])):
+            seq[bi, lo:hi] = si + 7 * bi
+    seq = seq.to(DEV)
+    out = causal_conv1d_fn(x, w, bias, seq_idx=seq, activation="silu")
+    want, _ = O.causal_conv1d_fwd(x, w, bias, None, "silu", seq_idx=seq.cpu().numpy())
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    close(out, want, tol, tol, "out")
+    G = torch.randn(b, d, l, device=DEV).to(dtype)
+    (out.float() * G.float()).sum().backward()
+    dx, dw, db, _ = O.causal_conv1d_bwd(x, w, bias, None, G, "silu", seq_idx=seq.cpu().numpy())
+    gtol = 1e-4 if dtype == torch.float32 else 2e-2
+    close(x.grad, dx, gtol, gtol, "dx")
+    for got, want_, name in ((w.grad, dw, "dweight"), (bias.grad, db, "dbias")):
+        sc = max(np.abs(want_).max(), 1.0)
+        close(got / sc, want_ / sc, gtol, gtol, name)

@@ -428,3 +428,33 @@ def test_scan_unequal_groups_and_2d_bc_equal_expanded():
         for i, X in ((3, Bx), (4, Cx)):
             want = g4[i].sum((0, 3)) if X.ndim == 2 else g4[i]
             np.testing.assert_allclose(g2[i], want, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("activation", [None, "silu"])
+def test_conv_seq_idx_equals_separate_sequences(activation):
+    """Pins the seq_idx extension of the conv oracle: packed sequences give the
+    outputs and input gradients of each sequence convolved on its own (zero
+    history), and the weight/bias gradients are the sums over them."""
+    rng = np.random.default_rng(41)
+    b, d, l, w = 2, 3, 17, 4
+    x, wt, bias = rng.standard_normal((b, d, l)), rng.standard_normal((d, w)), rng.standard_normal(d)
+    G = rng.standard_normal((b, d, l))
+    cuts = [[0, 5, 6, 17], [0, 11, 17]]
+    seq = np.zeros((b, l), dtype=np.int32)
+    for bi, c in enumerate(cuts):
+        for si in range(len(c) - 1):
+            seq[bi, c[si]:c[si + 1]] = si + 3 * bi
+    out, _ = O.causal_conv1d_fwd(x, wt, bias, activation=activation, seq_idx=seq)
+    dx, dw, db, _ = O.causal_conv1d_bwd(x, wt, bias, dout=G, activation=activation, seq_idx=seq)
+    dw_sum, db_sum = np.zeros_like(dw), np.zeros_like(db)
+    for bi, c in enumerate(cuts):
+        for lo, hi in zip(c[:-1], c[1:]):
+            o1, _ = O.causal_conv1d_fwd(x[bi:bi + 1, :, lo:hi], wt, bias, activation=activation)
+            np.testing.assert_allclose(out[bi:bi + 1, :, lo:hi], o1, rtol=1e-13)
+            g1 = O.causal_conv1d_bwd(x[bi:bi + 1, :, lo:hi], wt, bias, dout=G[bi:bi + 1, :, lo:hi],
+                                     activation=activation)
+            np.testing.assert_allclose(dx[bi:bi + 1, :, lo:hi], g1[0], rtol=1e-12, atol=1e-14)
+            dw_sum += g1[1]
+            db_sum += g1[2]
+    np.testing.assert_allclose(dw, dw_sum, rtol=1e-12)
+    np.testing.assert_allclose(db, db_sum, rtol=1e-12)
