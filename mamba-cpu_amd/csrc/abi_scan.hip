@@ -151,7 +151,7 @@ void bwd_chunks(ScanParams& p, int waves) {
   int64_t n = 1;
   const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves;
   if (waves == kScanSumWaves && wv > 0 && wv < 2048 && p.nblk >= 8) {
-    n = 3072 / wv;
+    n = 4096 / wv;  // about four waves per SIMD, the register limit of the kernel
     if (n > p.nblk / 4) n = p.nblk / 4;
     if (n < 1) n = 1;
   }
