@@ -150,7 +150,7 @@ int bwd_waves(const mcpu_scan_args* a) {
 void bwd_chunks(ScanParams& p, int waves) {
   int64_t n = 1;
   const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves;
-  if (waves == kScanSumWaves && wv > 0 && wv < 2048 && p.nblk >= 8) {
+  if (wv > 0 && wv < 2048 && p.nblk >= 8) {
     n = 4096 / wv;  // about four waves per SIMD, the register limit of the kernel
     if (n > p.nblk / 4) n = p.nblk / 4;
     if (n < 1) n = 1;
@@ -329,7 +329,11 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
     // Chunked: the adjoint summaries of chunks 1.. first.
     p.sum_h = reinterpret_cast<float*>(ws + w.sum_h);
     p.sum_dt = reinterpret_cast<float*>(ws + w.sum_dt);
-    if (int rc = hip_status(scan_bwd_summary_launch(p, a->dtype, st), "selective_scan_bwd summary launch"))
+    // The summary kernel's workgroups are kScanSumWaves waves (channel blocks
+    // of 4 * kScanSumWaves), whatever the main kernel's width.
+    ScanParams ps = p;
+    ps.nblk_c = (p.dpg + 4 * kScanSumWaves - 1) / (4 * kScanSumWaves);
+    if (int rc = hip_status(scan_bwd_summary_launch(ps, a->dtype, st), "selective_scan_bwd summary launch"))
       return rc;
   }
   if (int rc = hip_status(scan_bwd_launch(p, a->dtype, waves, st), "selective_scan_bwd launch"))

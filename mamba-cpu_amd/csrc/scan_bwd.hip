@@ -636,6 +636,10 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) 
     const int64_t pad = slices * ((dpg + 4 * w - 1) / (4 * w)) * 4 * w - slices * dpg;
     if (wgs >= 256 && wgs % 256 == 0 && pad == 0) return w;
   }
+  // Time-chunked shapes with many channels per slice: 8 waves halve the
+  // per-channel-block dB/dC partials (measured: batch 1, dim 5120, seqlen
+  // 16384 bf16 is 3 % faster than with 4 waves).
+  if (dpg >= 4096 && dpg % 32 == 0) return 8;
   return 4;
 }
 

@@ -434,11 +434,12 @@ def test_chunked_forward_matches_single_pass():
     torch.testing.assert_close(outs[1][1], outs[0][1], rtol=1e-4, atol=1e-5)
 
 
-def test_chunked_backward_matches_single_pass(monkeypatch):
-    """Batch 1, 48 channels, 4000 steps: with 4-wave workgroups the backward
-    cuts time into chunks (adjoint summaries carried across them); with
-    12-wave workgroups it walks the whole sequence. Same gradients within
-    float32 rounding (the carried decay is exp(A * sum dt))."""
+def test_chunked_backward_matches_oracle(monkeypatch):
+    """Batch 1, 48 channels, 4000 steps: the backward cuts time into chunks
+    (adjoint summaries carried across them, the carried decay being
+    exp(A * sum dt)) with 4-, 8- and 12-wave workgroups; the summary pass keeps
+    its own 4-wave channel blocks. Every width against the float64 oracle and
+    against the others."""
     inp = make_inputs(1, 48, 4000, 16, None, True, True, True, torch.float32)
     ops = torch.ops.mamba_cpu
     args = (inp["u"], inp["delta"], inp["A"], inp["B"][:, None].transpose(-1, -2),
@@ -448,10 +449,18 @@ def test_chunked_backward_matches_single_pass(monkeypatch):
     dlast = torch.randn(1, 48, 16, generator=g).to(DEV)
     _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*args)
     grads = []
-    for waves in ("12", "4"):
+    for waves in ("4", "8", "12"):
         monkeypatch.setenv("MCPU_SCAN_BWD_WAVES", waves)
         grads.append(ops.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave))
     torch.cuda.synchronize()
-    for name, a, b in zip("u delta A B C D z delta_bias".split(), grads[1], grads[0]):
-        scale = max(b.abs().max().item(), 1.0)
-        torch.testing.assert_close(a / scale, b / scale, rtol=1e-4, atol=1e-5, msg=name)
+    want = O.selective_scan_bwd(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                inp["z"], inp["delta_bias"], True, dout=dout, dlast_state=dlast)
+    names = "u delta A B C D z delta_bias".split()
+    for waves, got in zip((4, 8, 12), grads):
+        for name, a, w in zip(names, got, want):
+            w = w.swapaxes(-1, -2)[:, None] if name in ("B", "C") else w  # kernel layout (b, 1, l, n)
+            scale = max(float(np.abs(w).max()), 1.0)
+            close(a / scale, w / scale, 1e-3, 1e-4, f"{name} ({waves} waves)")
+        for name, a, b in zip(names, got, grads[0]):
+            scale = max(b.abs().max().item(), 1.0)
+            torch.testing.assert_close(a / scale, b / scale, rtol=1e-4, atol=1e-5, msg=name)
