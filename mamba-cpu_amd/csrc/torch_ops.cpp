@@ -83,6 +83,11 @@ Tensor like_x(const Tensor& x) {
   return at::empty(x.sizes(), x.options());
 }
 
+// Float32 copy of a parameter tensor when it is not already float32 and
+// contiguous (the reference computes in float32 whatever they are stored in).
+Tensor f32c(const Tensor& t) { return t.scalar_type() == at::kFloat && t.is_contiguous() ? t : t.to(at::kFloat).contiguous(); }
+optional<Tensor> f32c(const optional<Tensor>& t) { return has(t) ? optional<Tensor>(f32c(*t)) : std::nullopt; }
+
 // ---- selective scan -------------------------------------------------------------
 
 void validate_scan(const char* name, const Tensor& u, const Tensor& delta, const Tensor& A,
@@ -519,24 +524,28 @@ void check_index(const char* name, const char* what, const optional<Tensor>& t, 
                     name, " expects ", what, " as a contiguous int32 tensor of shape (batch,)");
 }
 
-Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& weight,
-                            const optional<Tensor>& bias, bool silu,
+// Decode step(s) of the conv (ops/causal_conv1d.py:56-85): x (b, dim) for one
+// step or (b, dim, seqlen); the output is shaped like x.
+Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& weight_in,
+                            const optional<Tensor>& bias_in, bool silu,
                             const optional<Tensor>& cache_seqlens,
                             const optional<Tensor>& conv_state_indices) {
   const char* name = "mamba_cpu::causal_conv1d_update";
-  for (const optional<Tensor>& t : {opt(x), opt(conv_state), opt(weight), bias}) check_gpu(name, t);
+  for (const optional<Tensor>& t : {opt(x), opt(conv_state), opt(weight_in), bias_in}) check_gpu(name, t);
   check_index(name, "cache_seqlens", cache_seqlens, x.size(0));
   check_index(name, "conv_state_indices", conv_state_indices, x.size(0));
   TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && conv_state.scalar_type() == x.scalar_type(), name,
                     " expects x and conv_state of one dtype among float32, bfloat16 and float16");
-  TORCH_CHECK_VALUE(weight.scalar_type() == at::kFloat && weight.is_contiguous() && weight.dim() == 2,
-                    name, " expects a contiguous float32 weight");
-  TORCH_CHECK_VALUE(x.dim() == 3 && conv_state.dim() == 3, name,
-                    " expects x (batch, dim, seqlen) and conv_state (batch, dim, state_len)");
+  TORCH_CHECK_VALUE(weight_in.dim() == 2, name, " expects weight (dim, width)");
+  const bool single = x.dim() == 2;
+  TORCH_CHECK_VALUE((single || x.dim() == 3) && conv_state.dim() == 3, name,
+                    " expects x (batch, dim[, seqlen]) and conv_state (batch, dim, state_len)");
   TORCH_CHECK_VALUE(conv_state.size(1) == x.size(1) &&
                         (has(conv_state_indices) || conv_state.size(0) == x.size(0)),
                     name, " expects conv_state (batch, dim, state_len), or (rows, dim, state_len) "
                     "with conv_state_indices");
+  const Tensor weight = f32c(weight_in);
+  const optional<Tensor> bias = f32c(bias_in);
   c10::DeviceGuard guard(x.device());
   Tensor out = at::empty(x.sizes(), x.options());
   mcpu_conv_update_args a;
@@ -548,14 +557,19 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
   a.out = out.data_ptr();
   a.batch = x.size(0);
   a.dim = x.size(1);
-  a.seqlen = x.size(2);
+  a.seqlen = single ? 1 : x.size(2);
   a.width = weight.size(1);
   a.state_len = conv_state.size(2);
   a.silu = silu ? 1 : 0;
   a.dtype = dtype_tag(x.scalar_type());
-  strides3(a.x_stride, x);
+  auto s3 = [&](int64_t (&d)[3], const Tensor& t) {
+    d[0] = t.stride(0);
+    d[1] = t.stride(1);
+    d[2] = single ? 0 : t.stride(2);
+  };
+  s3(a.x_stride, x);
   strides3(a.state_stride, conv_state);
-  strides3(a.out_stride, out);
+  s3(a.out_stride, out);
   a.cache_seqlens = has(cache_seqlens) ? static_cast<const int32_t*>(cache_seqlens->data_ptr()) : nullptr;
   a.conv_state_indices =
       has(conv_state_indices) ? static_cast<const int32_t*>(conv_state_indices->data_ptr()) : nullptr;
@@ -566,44 +580,59 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
 
 // ---- selective state update ---------------------------------------------------------
 
-Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, const Tensor& A,
-                              const Tensor& B, const Tensor& C, const optional<Tensor>& D,
-                              const optional<Tensor>& z, const optional<Tensor>& dt_bias,
+// One decode step in either layout of the reference
+// (ops/selective_state_update.py:5-57): Mamba-1 state (b, dim, n), x/dt/z
+// (b, dim), A (dim, n), B/C (b, n), D/dt_bias (dim); or Mamba-2 state
+// (b, h, p, n), x/dt/z (b, h, p), A (h, p, n), B/C (b, g, n), D/dt_bias (h, p).
+// The Mamba-1 layout is the head layout with one head, passed through strides
+// without any reshaping op.
+Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, const Tensor& A_in,
+                              const Tensor& B_in, const Tensor& C_in, const optional<Tensor>& D_in,
+                              const optional<Tensor>& z, const optional<Tensor>& dt_bias_in,
                               bool dt_softplus, const optional<Tensor>& state_batch_indices) {
   const char* name = "mamba_cpu::selective_state_update";
   check_index(name, "state_batch_indices", state_batch_indices, x.size(0));
-  for (const optional<Tensor>& t : {opt(state), opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias})
+  for (const optional<Tensor>& t : {opt(state), opt(x), opt(dt), opt(A_in), opt(B_in), opt(C_in), D_in,
+                                    z, dt_bias_in})
     check_gpu(name, t);
   TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && dt.scalar_type() == x.scalar_type() &&
                         (!has(z) || z->scalar_type() == x.scalar_type()),
                     name, " expects x, dt and z of one dtype among float32, bfloat16, float16");
   TORCH_CHECK_VALUE(x_dtype(state.scalar_type()), name,
                     " expects a float32, bfloat16 or float16 state");
-  TORCH_CHECK_VALUE(state.dim() == 4 && x.dim() == 3, name, " expects state (b, h, p, n) and x (b, h, p)");
+  const bool heads = state.dim() == 4;
+  TORCH_CHECK_VALUE((heads && x.dim() == 3) || (state.dim() == 3 && x.dim() == 2), name,
+                    " expects state (b, dim, n) with x (b, dim), or state (b, h, p, n) with x (b, h, p)");
   TORCH_CHECK_VALUE(has(state_batch_indices) || state.size(0) == x.size(0), name,
                     " expects state and x of one batch, or state_batch_indices");
-  const int64_t b = x.size(0), h = state.size(1), p = state.size(2), n = state.size(3);
-  TORCH_CHECK_VALUE(state.stride(3) == 1 || n == 1, name, " expects unit stride along dstate");
-  TORCH_CHECK_VALUE(x.size(0) == b && x.size(1) == h && x.size(2) == p && dt.sizes() == x.sizes() &&
-                        (!has(z) || z->sizes() == x.sizes()),
-                    name, " expects x, dt and z of shape (b, h, p)");
-  for (const optional<Tensor>& t : {opt(A), opt(B), opt(C), D, dt_bias})
-    TORCH_CHECK_VALUE(!has(t) || t->scalar_type() == at::kFloat, name,
-                      " expects float32 A, B, C, D and dt_bias");
-  TORCH_CHECK_VALUE(A.dim() == 3 && A.size(0) == h && A.size(1) == p && A.size(2) == n &&
-                        A.is_contiguous(),
-                    name, " expects a contiguous A of shape (nheads, headdim, dstate)");
-  const int64_t g = B.dim() == 3 ? B.size(1) : 0;
-  for (const Tensor* X : {&B, &C})
-    TORCH_CHECK_VALUE(X->dim() == 3 && X->size(0) == b && X->size(1) == g && X->size(2) == n &&
-                          (X->stride(2) == 1 || n == 1),
-                      name, " expects B and C of shape (batch, ngroups, dstate), unit dstate stride");
+  const int64_t b = x.size(0), h = heads ? state.size(1) : 1, p = heads ? state.size(2) : state.size(1);
+  const int64_t n = state.size(-1);
+  TORCH_CHECK_VALUE(state.stride(-1) == 1 || n == 1, name, " expects unit stride along dstate");
+  const bool x_ok = heads ? (x.size(1) == h && x.size(2) == p) : x.size(1) == p;
+  TORCH_CHECK_VALUE(x_ok && dt.sizes() == x.sizes() && (!has(z) || z->sizes() == x.sizes()), name,
+                    " expects x, dt and z shaped like the state without dstate");
+  auto unit_last = [](const Tensor& t) {
+    const Tensor f = t.to(at::kFloat);
+    return (f.stride(-1) == 1 || f.size(-1) == 1) ? f : f.contiguous();
+  };
+  const Tensor A = f32c(A_in), B = unit_last(B_in), C = unit_last(C_in);
+  const optional<Tensor> D = f32c(D_in), dt_bias = f32c(dt_bias_in);
+  TORCH_CHECK_VALUE(heads ? (A.dim() == 3 && A.size(0) == h && A.size(1) == p && A.size(2) == n)
+                          : (A.dim() == 2 && A.size(0) == p && A.size(1) == n),
+                    name, " expects A of shape (dim, dstate) or (nheads, headdim, dstate)");
+  const int64_t g = heads ? B.size(1) : 1;
+  for (const Tensor* X : {&B, &C}) {
+    const bool ok = heads ? (X->dim() == 3 && X->size(0) == b && X->size(1) == g && X->size(2) == n)
+                          : (X->dim() == 2 && X->size(0) == b && X->size(1) == n);
+    TORCH_CHECK_VALUE(ok && (X->stride(-1) == 1 || n == 1), name,
+                      " expects B and C of shape (batch, [ngroups,] dstate), unit dstate stride");
+  }
   for (const optional<Tensor>& t : {D, dt_bias})
-    TORCH_CHECK_VALUE(!has(t) || (t->dim() == 2 && t->size(0) == h && t->size(1) == p &&
-                                  t->is_contiguous()),
-                      name, " expects contiguous D and dt_bias of shape (nheads, headdim)");
+    TORCH_CHECK_VALUE(!has(t) || (heads ? (t->dim() == 2 && t->size(0) == h && t->size(1) == p)
+                                        : (t->dim() == 1 && t->size(0) == p)),
+                      name, " expects D and dt_bias of shape (dim,) or (nheads, headdim)");
   c10::DeviceGuard guard(x.device());
-  Tensor out = at::empty({b, h, p}, x.options());
+  Tensor out = at::empty(x.sizes(), x.options());
   mcpu_state_update_args a;
   std::memset(&a, 0, sizeof(a));
   a.state = state.data_ptr();
@@ -624,14 +653,20 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
   a.dt_softplus = dt_softplus ? 1 : 0;
   a.dtype = dtype_tag(x.scalar_type());
   a.state_dtype = dtype_tag(state.scalar_type());
-  for (int i = 0; i < 3; ++i) a.state_stride[i] = state.stride(i);
-  strides3(a.x_stride, x);
-  strides3(a.dt_stride, dt);
-  strides3(a.z_stride, z);
+  // Strides over (batch, head, headdim); the Mamba-1 layout has one head.
+  auto s3 = [&](int64_t (&d)[3], const Tensor& t) {
+    d[0] = t.stride(0);
+    d[1] = heads ? t.stride(1) : 0;
+    d[2] = t.stride(heads ? 2 : 1);
+  };
+  s3(a.state_stride, state);
+  s3(a.x_stride, x);
+  s3(a.dt_stride, dt);
+  if (has(z)) s3(a.z_stride, *z);
   a.B_stride[0] = B.stride(0);
-  a.B_stride[1] = B.stride(1);
+  a.B_stride[1] = heads ? B.stride(1) : 0;
   a.C_stride[0] = C.stride(0);
-  a.C_stride[1] = C.stride(1);
+  a.C_stride[1] = heads ? C.stride(1) : 0;
   a.state_batch_indices =
       has(state_batch_indices) ? static_cast<const int32_t*>(state_batch_indices->data_ptr()) : nullptr;
   a.state_batch = state.size(0);

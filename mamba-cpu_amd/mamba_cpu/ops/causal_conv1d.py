@@ -142,25 +142,20 @@ def causal_conv1d_update(
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
     silu = _silu_flag(activation)
-    single_step = x.dim() == 2
-    x_seq = x.unsqueeze(-1) if single_step else x
     width = weight.shape[1]
     state_len = conv_state.shape[-1]
     if state_len < width - 1:
         raise ValueError(f"conv_state length ({state_len}) must be at least width - 1 ({width - 1})")
-    in_dtype = x.dtype
-    if in_dtype not in _X_DTYPES:
-        x_seq = x_seq.float()
-    w = weight.float().contiguous()
-    bb = None if bias is None else bias.float().contiguous()
-    cs = _index(cache_seqlens, "cache_seqlens", x_seq.shape[0], x.device)
-    idx = _index(conv_state_indices, "conv_state_indices", x_seq.shape[0], x.device)
-    if conv_state.dtype == x_seq.dtype:
-        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, conv_state, w, bb, silu, cs, idx)
-    else:
-        # The reference mixes dtypes through conv_state.to(x.dtype) and a copy back.
-        tmp = conv_state.to(x_seq.dtype)
-        out = torch.ops.mamba_cpu.causal_conv1d_update(x_seq, tmp, w, bb, silu, cs, idx)
-        conv_state.copy_(tmp)
-    out = out.to(in_dtype)
-    return out.squeeze(-1) if single_step else out
+    batch = x.shape[0]
+    cs = _index(cache_seqlens, "cache_seqlens", batch, x.device)
+    idx = _index(conv_state_indices, "conv_state_indices", batch, x.device)
+    if x.dtype in _X_DTYPES and conv_state.dtype == x.dtype:
+        # The operator takes (b, dim) or (b, dim, seqlen) as they are: one dispatch.
+        return torch.ops.mamba_cpu.causal_conv1d_update(x, conv_state, weight, bias, silu, cs, idx)
+    # Mixed or other dtypes: the reference mixes them through conv_state.to(x.dtype)
+    # and a copy back; unsupported x dtypes are computed in float32.
+    xw = x if x.dtype in _X_DTYPES else x.float()
+    tmp = conv_state.to(xw.dtype)
+    out = torch.ops.mamba_cpu.causal_conv1d_update(xw, tmp, weight, bias, silu, cs, idx)
+    conv_state.copy_(tmp)
+    return out.to(x.dtype)

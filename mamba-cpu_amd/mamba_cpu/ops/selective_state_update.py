@@ -51,44 +51,28 @@ def selective_state_update(
     """
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
-    has_heads = state.dim() > 3
-    if not has_heads:
-        # Mamba-1 is the head layout with one head of headdim = dim.
-        state = state.unsqueeze(1)
-        x = x.unsqueeze(1)
-        dt = dt.unsqueeze(1)
-        A = A.unsqueeze(0)
-        B = B.unsqueeze(1)
-        C = C.unsqueeze(1)
-        D = None if D is None else D.unsqueeze(0)
-        z = None if z is None else z.unsqueeze(1)
-        dt_bias = None if dt_bias is None else dt_bias.unsqueeze(0)
-    in_dtype = x.dtype
-    xdt = in_dtype
-    if xdt not in _X_DTYPES or dt.dtype != xdt or (z is not None and z.dtype != xdt):
-        xdt = torch.float32
-
-    def f32(t):
-        return None if t is None else t.float().contiguous()
-
-    def bc(t):
-        t = t.float()
-        return t if (t.stride(-1) == 1 or t.shape[-1] == 1) else t.contiguous()
-
-    st = state
-    if st.dtype not in _X_DTYPES or (st.stride(-1) != 1 and st.shape[-1] > 1):
-        st = state.float().contiguous()
     idx = None
     if state_batch_indices is not None:
         if (state_batch_indices.dtype not in (torch.int32, torch.int64)
                 or state_batch_indices.shape != (x.shape[0],)):
             raise ValueError(f"state_batch_indices must be an integer tensor of shape ({x.shape[0]},)")
         idx = state_batch_indices.to(device=x.device, dtype=torch.int32).contiguous()
+    xdt = x.dtype
+    if (xdt in _X_DTYPES and dt.dtype == xdt and (z is None or z.dtype == xdt)
+            and state.dtype in _X_DTYPES and (state.stride(-1) == 1 or state.shape[-1] == 1)):
+        # The operator takes both layouts as they are and casts the float32
+        # parameters itself: the common decode call is one dispatch.
+        return torch.ops.mamba_cpu.selective_state_update(
+            state, x, dt, A, B, C, D, z, dt_bias, bool(dt_softplus), idx)
+    # Mixed or other dtypes: computed in float32, state written back.
+    if xdt not in _X_DTYPES or dt.dtype != xdt or (z is not None and z.dtype != xdt):
+        xdt = torch.float32
+    st = state
+    if state.dtype not in _X_DTYPES or (state.stride(-1) != 1 and state.shape[-1] > 1):
+        st = state.float().contiguous()
     out = torch.ops.mamba_cpu.selective_state_update(
-        st, x.to(xdt), dt.to(xdt), f32(A), bc(B), bc(C), f32(D),
-        None if z is None else z.to(xdt), f32(dt_bias), bool(dt_softplus), idx,
-    )
+        st, x.to(xdt), dt.to(xdt), A, B, C, D, None if z is None else z.to(xdt), dt_bias,
+        bool(dt_softplus), idx)
     if st is not state:
         state.copy_(st)
-    out = out.to(in_dtype)
-    return out if has_heads else out.squeeze(1)
+    return out.to(x.dtype)
