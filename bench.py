@@ -252,6 +252,37 @@ def other_configs(torch, dev, stream, cpu):
     res["scan_fwdbwd_b1_d5120_l16384_bf16"] = r
     del leaves, gout
 
+    # Complex A (mamba_ssm's complex-A scan, which the reference rejects): the
+    # training-step shape, fp32, batch 8, dim 1536, seqlen 1024, dstate 16
+    # complex, z + D + delta_bias, softplus, fwd+bwd. B/C real (b, n, 2 l).
+    b, d, l, n = 8, 1536, 1024, 16
+    leaves = dict(u=torch.randn(b, d, l, generator=g, device=dev),
+                  delta=torch.randn(b, d, l, generator=g, device=dev),
+                  A=torch.complex(-torch.exp(torch.rand(d, n, generator=g, device=dev) * math.log(16)),
+                                  torch.randn(d, n, generator=g, device=dev) * math.pi),
+                  B=torch.randn(b, n, 2 * l, generator=g, device=dev),
+                  C=torch.randn(b, n, 2 * l, generator=g, device=dev),
+                  D=torch.randn(d, generator=g, device=dev),
+                  z=torch.randn(b, d, l, generator=g, device=dev),
+                  delta_bias=torch.rand(d, generator=g, device=dev) * 2 - 4)
+    leaves = {k: v.requires_grad_() for k, v in leaves.items()}
+    gout = torch.randn(b, d, l, generator=g, device=dev)
+
+    def complex_step():
+        out = selective_scan_fn(**leaves, delta_softplus=True)
+        return torch.autograd.grad(out, list(leaves.values()), gout)
+
+    x, bc, prm = b * d * l * 4, b * n * l * 8, 8 * d * n + 8 * d
+    nbytes = (3 * x + 2 * bc + prm + x) + (4 * x + 2 * bc + prm + 3 * x + 2 * bc + prm)
+    ms = _events_ms(torch, stream, complex_step, 10)
+    r = _rate(nbytes, ms)
+    r["workload"] = ("selective_scan_fn forward+backward with complex A, fp32, batch 8, dim 1536, "
+                     "seqlen 1024, dstate 16 (complex), z + D + delta_bias, softplus")
+    r["cpu_baseline"] = None
+    r["cpu_note"] = "the reference rejects complex A (ops/selective_scan_interface.py:160-161)"
+    res["scan_fwdbwd_complex_b8_d1536_l1024"] = r
+    del leaves, gout
+
     # Causal conv1d forward+backward: batch 8, dim 3072, seqlen 2048, width 4, silu.
     b, d, l, w = 8, 3072, 2048, 4
     for dt, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):

@@ -109,10 +109,21 @@ typedef struct mcpu_scan_args {
   int64_t du_stride[3];
   int64_t ddelta_stride[3];
   int64_t dz_stride[3];
+  /* Nonzero: complex A (mamba_ssm's complex-A scan, y = 2 Re(<h, C>) + D u;
+     the reference rejects complex A, ops/selective_scan_interface.py:160-161).
+     Then A, dA are (dim, dstate) complex64 as (re, im) float pairs; B/C
+     strides locate the real part of element (batch, group, seqlen, dstate)
+     and the imaginary part is the next float (mamba_ssm's real
+     (batch, ngroups, dstate, 2 seqlen) layout, or a complex tensor's view);
+     last_state, dlast_state and the checkpoints hold complex pairs; dB/dC are
+     (batch, ngroups, seqlen, dstate, 2) contiguous. dstate <= 32; ysave and
+     the forward workspace are not used. */
+  int32_t complex_a;
 } mcpu_scan_args;
 
 /* Bytes of the optional checkpoint buffer: the float32 scan state at the
- * start of every 16-step block, (batch, dim, ceil(seqlen/16), dstate).
+ * start of every 16-step block, (batch, dim, ceil(seqlen/16), dstate)
+ * (twice that with complex_a: (re, im) pairs).
  * A forward call with ckpt != NULL fills it; a backward call with the same
  * inputs and ckpt != NULL reads it instead of recomputing it. */
 size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a);

@@ -14,6 +14,9 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
 hipError_t scan_bwd_summary_launch(const ScanParams& p, int dtype, hipStream_t stream);
+int scan_complex_waves();
+hipError_t scan_cfwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
+hipError_t scan_cbwd_launch(const ScanParams& p, int dtype, hipStream_t stream);
 hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_part, float* dC,
                               int64_t slices, int64_t nblk_c, int64_t per_slice,
                               const float* dA_part, float* dA, int64_t nA, const float* dD_part,
@@ -40,9 +43,10 @@ int check_scan(const mcpu_scan_args* a) {
   if (a->ngroups < 1 || (a->dim > 0 && a->dim % a->ngroups != 0))
     return fail(MCPU_ERR_INVALID, "selective_scan: dim (%lld) must be divisible by ngroups (%lld)",
                 (long long)a->dim, (long long)a->ngroups);
-  if (a->dstate < 1 || a->dstate > 64)
-    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, 64], got %lld",
-                (long long)a->dstate);
+  const int64_t max_dstate = a->complex_a ? 32 : 64;
+  if (a->dstate < 1 || a->dstate > max_dstate)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, %lld]%s, got %lld",
+                (long long)max_dstate, a->complex_a ? " with complex A" : "", (long long)a->dstate);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "selective_scan: bad dtype %d", a->dtype);
   const int64_t dpg = a->dim / a->ngroups;
   const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16);
@@ -64,10 +68,11 @@ int check_scan(const mcpu_scan_args* a) {
   const int64_t esz = dtype_size(a->dtype), ch = 4 * kScanMaxWaves - 1, T = kScanBlockT - 1;
   const int64_t nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
   auto x_span = [&](const int64_t (&s)[3]) { return esz * (ch * s[1] + T * s[2]); };
-  auto bc_span = [&](const int64_t (&s)[4]) { return 4 * (T * s[2] + 63 * s[3]); };
+  const int64_t cw = a->complex_a ? 2 : 1;  // floats per state element
+  auto bc_span = [&](const int64_t (&s)[4]) { return 4 * (T * s[2] + 63 * s[3] + cw - 1); };
   const int64_t spans[] = {x_span(a->u_stride), x_span(a->delta_stride), x_span(a->z_stride),
                            x_span(a->dout_stride), bc_span(a->B_stride), bc_span(a->C_stride),
-                           4 * (ch * nblk * a->dstate + 63), esz * (ch * a->seqlen + T),
+                           4 * cw * (ch * nblk * a->dstate + 63), esz * (ch * a->seqlen + T),
                            x_span(so), x_span(sdu), x_span(sdd), x_span(sdz)};
   for (int64_t sp : spans)
     if (sp >= 0xffffffffll)
@@ -217,6 +222,88 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
   return w;
 }
 
+// Complex A: one time chunk, 4-wave workgroups, states as (re, im) pairs.
+struct CBwdLayout {
+  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, total = 0;
+  bool own_ckpt = false, part_bc = false, part_dA = false;
+};
+
+CBwdLayout cbwd_layout(const mcpu_scan_args* a) {
+  const ScanParams p = make_params(a, scan_complex_waves());
+  CBwdLayout w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.own_ckpt = a->ckpt == nullptr;
+  if (w.own_ckpt) w.ckpt = take(sizeof(float) * 2 * p.batch * p.dim * p.nblk * p.dstate);
+  w.part_bc = p.nblk_c > 1;
+  if (w.part_bc) {
+    const size_t bc = sizeof(float) * 2 * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.dstate;
+    w.dB = take(bc);
+    w.dC = take(bc);
+  }
+  w.part_dA = p.batch > 1;
+  if (w.part_dA) w.dA = take(sizeof(float) * 2 * p.batch * p.dim * p.dstate);
+  w.dD = take(sizeof(float) * p.batch * p.dim);
+  w.dbias = take(sizeof(float) * p.batch * p.dim);
+  w.total = off;
+  return w;
+}
+
+int complex_fwd(const mcpu_scan_args* a, hipStream_t st) {
+  ScanParams p = make_params(a, scan_complex_waves());
+  p.out = a->out;
+  p.last_state = a->last_state;
+  p.ckpt = a->ckpt;
+  if (p.out == nullptr && p.last_state == nullptr && p.ckpt == nullptr) return MCPU_OK;
+  return hip_status(scan_cfwd_launch(p, a->dtype, a->out != nullptr, st), "selective_scan_fwd launch");
+}
+
+int complex_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  const CBwdLayout w = cbwd_layout(a);
+  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+    return fail(MCPU_ERR_INVALID, "selective_scan_bwd: workspace of %zu bytes needed, got %zu",
+                w.total, workspace_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  if (a->batch == 0 || a->dim == 0 || a->seqlen == 0) {
+    // Nothing to scan: parameter grads are zero (dB/dC, du, ... are empty
+    // unless seqlen is 0 with a nonempty batch, where they have no elements).
+    if (int rc = zero_f32(a->dA, 2 * a->dim * a->dstate, st)) return rc;
+    if (a->dD) if (int rc = zero_f32(a->dD, a->dim, st)) return rc;
+    if (a->ddelta_bias) if (int rc = zero_f32(a->ddelta_bias, a->dim, st)) return rc;
+    return MCPU_OK;
+  }
+  char* ws = static_cast<char*>(workspace);
+  ScanParams p = make_params(a, scan_complex_waves());
+  p.ckpt = w.own_ckpt ? reinterpret_cast<float*>(ws + w.ckpt) : a->ckpt;
+  if (w.own_ckpt) {
+    ScanParams pf = p;  // states-only forward: block checkpoints
+    if (int rc = hip_status(scan_cfwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
+      return rc;
+  }
+  p.dout = a->dout;
+  p.dlast_state = a->dlast_state;
+  p.du = a->du;
+  p.ddelta = a->ddelta;
+  p.dz = a->dz;
+  p.dB_part = w.part_bc ? reinterpret_cast<float*>(ws + w.dB) : a->dB;
+  p.dC_part = w.part_bc ? reinterpret_cast<float*>(ws + w.dC) : a->dC;
+  p.dA_part = w.part_dA ? reinterpret_cast<float*>(ws + w.dA) : a->dA;
+  p.dD_part = reinterpret_cast<float*>(ws + w.dD);
+  p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
+  if (int rc = hip_status(scan_cbwd_launch(p, a->dtype, st), "selective_scan_bwd launch")) return rc;
+  return hip_status(
+      scan_reduce_launch(w.part_bc ? p.dB_part : nullptr, a->dB, w.part_bc ? p.dC_part : nullptr,
+                         a->dC, p.batch * p.ngroups, p.nblk_c, 2 * p.seqlen * p.dstate,
+                         w.part_dA ? p.dA_part : nullptr, a->dA, 2 * p.dim * p.dstate,
+                         a->dD ? p.dD_part : nullptr, a->dD,
+                         a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim, p.batch, st),
+      "selective_scan_bwd reduce");
+}
+
 }  // namespace
 }  // namespace mcpu
 
@@ -225,7 +312,7 @@ using namespace mcpu;
 extern "C" size_t mcpu_selective_scan_ckpt_size(const mcpu_scan_args* a) {
   if (a == nullptr || a->batch < 0 || a->dim < 0 || a->seqlen < 0 || a->dstate < 0) return 0;
   const int64_t nblk = (a->seqlen + kScanBlockT - 1) / kScanBlockT;
-  return sizeof(float) * a->batch * a->dim * nblk * a->dstate;
+  return sizeof(float) * a->batch * a->dim * nblk * a->dstate * (a->complex_a ? 2 : 1);
 }
 
 extern "C" size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a) {
@@ -233,6 +320,7 @@ extern "C" size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a
     clear_error();
     return 0;
   }
+  if (a->complex_a) return 0;
   ScanParams p = make_params(a, scan_fwd_waves());
   scan_fwd_chunks(p);
   return fwd_layout(p).total;
@@ -244,6 +332,7 @@ extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
   if (int rc = check_scan(a)) return rc;
   if (int rc = mcpu_check_device()) return rc;
   if (a->batch == 0 || a->dim == 0) return MCPU_OK;
+  if (a->complex_a) return complex_fwd(a, static_cast<hipStream_t>(stream));
   ScanParams p = make_params(a, scan_fwd_waves());
   scan_fwd_chunks(p);
   const FwdLayout w = fwd_layout(p);
@@ -270,7 +359,7 @@ extern "C" size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a
     clear_error();
     return 0;
   }
-  return bwd_layout(a).total;
+  return a->complex_a ? cbwd_layout(a).total : bwd_layout(a).total;
 }
 
 extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
@@ -286,6 +375,7 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
     return fail(MCPU_ERR_INVALID, "selective_scan_bwd: dD is required when D is given");
   if (a->delta_bias != nullptr && a->ddelta_bias == nullptr)
     return fail(MCPU_ERR_INVALID, "selective_scan_bwd: ddelta_bias is required when delta_bias is given");
+  if (a->complex_a) return complex_bwd(a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   const BwdLayout w = bwd_layout(a);
   if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
     return fail(MCPU_ERR_INVALID, "selective_scan_bwd: workspace of %zu bytes needed, got %zu",

@@ -164,13 +164,18 @@ struct BCStage {
   int slot[PER_THREAD];  // n * kBCPad + t in the LDS tile, or -1 past the tile
   int t[PER_THREAD];
   bool ok[PER_THREAD];   // the state exists (n < dstate)
+  // pairs: the row holds one part of (re, im) float pairs (complex B/C),
+  // whose time stride is 2 in mamba_ssm's (.., dstate, 2 seqlen) layout;
+  // the thread index then runs along time whenever time has the smaller
+  // nonzero stride.
   __device__ __forceinline__ void init(int tid, const float* row, const int64_t (&s)[4], int64_t N,
-                                       int64_t t0) {
+                                       int64_t t0, bool pairs = false) {
+    const bool time_fastest = pairs ? (s[2] > 0 && s[2] < s[3]) : (s[2] == 1 && s[3] != 1);
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
       const int e = tid + i * 64 * W;
       int n;
-      if (s[2] == 1 && s[3] != 1) {  // time contiguous: time-fastest
+      if (time_fastest) {  // time contiguous: time-fastest
         n = e / kScanBlockT;
         t[i] = e % kScanBlockT;
       } else {

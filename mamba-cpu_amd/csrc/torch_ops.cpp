@@ -359,6 +359,155 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> selective_scan_fwd_ckpt_autograd(
   return {r[0], r[1], r[2], r[3]};
 }
 
+// ---- selective scan, complex A ------------------------------------------------------
+//
+// mamba_ssm's complex-A scan (the reference rejects complex A,
+// selective_scan_interface.py:160-161). A is complex64 (dim, dstate); B and C
+// reach the operators as float32 (batch, ngroups, seqlen, dstate, 2) views
+// whose last dim is the (re, im) pair (unit stride), so both mamba_ssm's real
+// (batch, ngroups, dstate, 2 seqlen) layout and a complex tensor's
+// view_as_real pass without copies. The forward also returns the block
+// checkpoints its backward restarts from; autograd is wired in Python.
+
+void validate_cscan(const char* name, const Tensor& u, const Tensor& delta, const Tensor& A,
+                    const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                    const optional<Tensor>& z, const optional<Tensor>& bias,
+                    std::initializer_list<optional<Tensor>> extra = {}) {
+  for (const optional<Tensor>& t : {opt(u), opt(delta), opt(A), opt(B), opt(C), D, z, bias})
+    check_gpu(name, t);
+  for (const optional<Tensor>& t : extra) check_gpu(name, t);
+  TORCH_CHECK_VALUE(x_dtype(u.scalar_type()) && delta.scalar_type() == u.scalar_type() &&
+                        (!has(z) || z->scalar_type() == u.scalar_type()),
+                    name, " expects u, delta and z of one dtype among float32, bfloat16 and float16");
+  TORCH_CHECK_VALUE(u.dim() == 3 && delta.sizes() == u.sizes() && (!has(z) || z->sizes() == u.sizes()),
+                    name, " expects u, delta and z of shape (batch, dim, seqlen)");
+  const int64_t batch = u.size(0), dim = u.size(1), seqlen = u.size(2);
+  TORCH_CHECK_VALUE(A.scalar_type() == at::kComplexFloat && A.dim() == 2 && A.size(0) == dim &&
+                        A.is_contiguous(),
+                    name, " expects a contiguous complex64 A of shape (dim, dstate)");
+  const int64_t dstate = A.size(1);
+  for (const Tensor* X : {&B, &C})
+    TORCH_CHECK_VALUE(X->scalar_type() == at::kFloat && X->dim() == 5 && X->size(0) == batch &&
+                          X->size(2) == seqlen && X->size(3) == dstate && X->size(4) == 2 &&
+                          X->stride(4) == 1,
+                      name, " expects float32 B and C of shape (batch, ngroups, seqlen, dstate, 2) "
+                      "with (re, im) pairs in the unit-stride last dim");
+  TORCH_CHECK_VALUE(B.size(1) == C.size(1) && B.size(1) > 0 && dim % B.size(1) == 0, name,
+                    ": dim (", dim, ") must be divisible by ngroups (", B.size(1), ")");
+  for (const optional<Tensor>& t : {D, bias})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == at::kFloat && t->dim() == 1 &&
+                                  t->size(0) == dim && t->is_contiguous()),
+                      name, " expects contiguous float32 D and delta_bias of shape (dim,)");
+}
+
+mcpu_scan_args cscan_args(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+                          const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+                          const optional<Tensor>& bias, bool softplus) {
+  mcpu_scan_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.complex_a = 1;
+  a.u = u.data_ptr();
+  a.delta = delta.data_ptr();
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.B = static_cast<const float*>(B.data_ptr());
+  a.C = static_cast<const float*>(C.data_ptr());
+  a.D = fptr(D);
+  a.z = ptr(z);
+  a.delta_bias = fptr(bias);
+  a.batch = u.size(0);
+  a.dim = u.size(1);
+  a.seqlen = u.size(2);
+  a.dstate = A.size(1);
+  a.ngroups = B.size(1);
+  a.delta_softplus = softplus ? 1 : 0;
+  a.dtype = dtype_tag(u.scalar_type());
+  strides3(a.u_stride, u);
+  strides3(a.delta_stride, delta);
+  strides3(a.z_stride, z);
+  for (int i = 0; i < 4; ++i) {
+    a.B_stride[i] = B.stride(i);
+    a.C_stride[i] = C.stride(i);
+  }
+  return a;
+}
+
+std::vector<int64_t> cckpt_shape(const Tensor& u, const Tensor& A) {
+  return {u.size(0), u.size(1), (u.size(2) + kBlockT - 1) / kBlockT, A.size(1), 2};
+}
+
+std::tuple<Tensor, Tensor, Tensor> selective_scan_cfwd(const Tensor& u, const Tensor& delta,
+                                                       const Tensor& A, const Tensor& B,
+                                                       const Tensor& C, const optional<Tensor>& D,
+                                                       const optional<Tensor>& z,
+                                                       const optional<Tensor>& bias, bool softplus) {
+  const char* name = "mamba_cpu::selective_scan_cfwd";
+  validate_cscan(name, u, delta, A, B, C, D, z, bias);
+  c10::DeviceGuard guard(u.device());
+  Tensor out = like_x(u);
+  Tensor last = at::empty({u.size(0), u.size(1), A.size(1)}, u.options().dtype(at::kComplexFloat));
+  Tensor ckpt = at::empty(cckpt_shape(u, A), u.options().dtype(at::kFloat));
+  mcpu_scan_args a = cscan_args(u, delta, A, B, C, D, z, bias, softplus);
+  a.out = out.data_ptr();
+  strides3(a.out_stride, out);
+  a.last_state = static_cast<float*>(last.data_ptr());
+  a.ckpt = static_cast<float*>(ckpt.data_ptr());
+  check_rc(mcpu_selective_scan_fwd(&a, nullptr, 0, stream_of(u)), name);
+  return {out, last, ckpt};
+}
+
+Grads8 selective_scan_cbwd(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+                           const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+                           const optional<Tensor>& bias, bool softplus, const Tensor& dout,
+                           const optional<Tensor>& dlast_state, const optional<Tensor>& ckpt) {
+  const char* name = "mamba_cpu::selective_scan_cbwd";
+  validate_cscan(name, u, delta, A, B, C, D, z, bias, {opt(dout), dlast_state, ckpt});
+  TORCH_CHECK_VALUE(dout.sizes() == u.sizes() && dout.scalar_type() == u.scalar_type(), name,
+                    " expects dout shaped and typed like u");
+  const int64_t batch = u.size(0), dim = u.size(1), dstate = A.size(1);
+  optional<Tensor> dlast;
+  if (has(dlast_state)) {
+    TORCH_CHECK_VALUE(dlast_state->scalar_type() == at::kComplexFloat && dlast_state->dim() == 3 &&
+                          dlast_state->size(0) == batch && dlast_state->size(1) == dim &&
+                          dlast_state->size(2) == dstate,
+                      name, " expects complex64 dlast_state (batch, dim, dstate)");
+    dlast = dlast_state->contiguous();
+  }
+  if (has(ckpt))
+    TORCH_CHECK_VALUE(ckpt->scalar_type() == at::kFloat && ckpt->is_contiguous() &&
+                          ckpt->sizes() == at::IntArrayRef(cckpt_shape(u, A)),
+                      name, " expects the checkpoints written by selective_scan_cfwd");
+  c10::DeviceGuard guard(u.device());
+  Tensor du = like_x(u);
+  Tensor ddelta = like_x(delta);
+  Tensor dA = at::empty(A.sizes(), A.options());
+  Tensor dB = at::empty(B.sizes(), B.options());
+  Tensor dC = at::empty(C.sizes(), C.options());
+  Tensor dD = at::empty({dim}, B.options());
+  Tensor dz = has(z) ? like_x(*z) : at::empty({0}, u.options());
+  Tensor dbias = at::empty({dim}, B.options());
+  mcpu_scan_args a = cscan_args(u, delta, A, B, C, D, z, bias, softplus);
+  a.dout = dout.data_ptr();
+  strides3(a.dout_stride, dout);
+  a.dlast_state = has(dlast) ? static_cast<const float*>(dlast->data_ptr()) : nullptr;
+  a.ckpt = has(ckpt) ? static_cast<float*>(ckpt->data_ptr()) : nullptr;
+  a.du = du.data_ptr();
+  a.ddelta = ddelta.data_ptr();
+  a.dz = has(z) ? dz.data_ptr() : nullptr;
+  strides3(a.du_stride, du);
+  strides3(a.ddelta_stride, ddelta);
+  if (has(z)) strides3(a.dz_stride, dz);
+  a.dA = static_cast<float*>(dA.data_ptr());
+  a.dB = static_cast<float*>(dB.data_ptr());
+  a.dC = static_cast<float*>(dC.data_ptr());
+  a.dD = static_cast<float*>(dD.data_ptr());
+  a.ddelta_bias = static_cast<float*>(dbias.data_ptr());
+  const size_t ws_bytes = mcpu_selective_scan_bwd_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)},
+                        u.options().dtype(at::kByte));
+  check_rc(mcpu_selective_scan_bwd(&a, ws.data_ptr(), ws_bytes, stream_of(u)), name);
+  return {du, ddelta, dA, dB, dC, dD, dz, dbias};
+}
+
 // ---- causal conv1d ------------------------------------------------------------------
 
 void check_conv(const char* name, const Tensor& x, const Tensor& weight,
@@ -724,6 +873,11 @@ TORCH_LIBRARY(mamba_cpu, m) {
         "Tensor? z, Tensor? delta_bias, bool delta_softplus, Tensor dout, Tensor? dlast_state, "
         "Tensor ckpt, Tensor ysave) -> "
         "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("selective_scan_cfwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor, Tensor)");
+  m.def("selective_scan_cbwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
+        "Tensor? z, Tensor? delta_bias, bool delta_softplus, Tensor dout, Tensor? dlast_state, "
+        "Tensor? ckpt) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("causal_conv1d_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
         "bool return_final_states, bool silu, Tensor? seq_idx=None) -> (Tensor, Tensor)");
   m.def("causal_conv1d_bwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
@@ -742,6 +896,8 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("selective_scan_bwd", &selective_scan_bwd);
   m.impl("selective_scan_fwd_ckpt", &selective_scan_fwd_ckpt);
   m.impl("selective_scan_bwd_ckpt", &selective_scan_bwd_ckpt);
+  m.impl("selective_scan_cfwd", &selective_scan_cfwd);
+  m.impl("selective_scan_cbwd", &selective_scan_cbwd);
   m.impl("causal_conv1d_fwd", &causal_conv1d_fwd);
   m.impl("causal_conv1d_bwd", &causal_conv1d_bwd);
   m.impl("causal_conv1d_update", &causal_conv1d_update);

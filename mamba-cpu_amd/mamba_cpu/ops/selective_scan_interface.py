@@ -83,6 +83,95 @@ def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ck
     return _bwd_fake(u, delta, A, B, C, z)
 
 
+@torch.library.register_fake("mamba_cpu::selective_scan_cfwd")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+    batch, dim, seqlen = u.shape
+    nblk = (seqlen + _BLOCK_T - 1) // _BLOCK_T
+    return (_like_x(u), u.new_empty(batch, dim, A.shape[1], dtype=torch.complex64),
+            u.new_empty(batch, dim, nblk, A.shape[1], 2, dtype=torch.float32))
+
+
+@torch.library.register_fake("mamba_cpu::selective_scan_cbwd")
+def _(u, delta, A, B, C, D, z, delta_bias, delta_softplus, dout, dlast_state, ckpt):
+    return (
+        _like_x(u), _like_x(delta), A.new_empty(A.shape), B.new_empty(B.shape), C.new_empty(C.shape),
+        B.new_empty(u.shape[1]), _like_x(z) if z is not None else u.new_empty(0), B.new_empty(u.shape[1]),
+    )
+
+
+class _ComplexScan(torch.autograd.Function):
+    """Autograd of the complex-A scan: the forward keeps its block
+    checkpoints, the backward restarts from them."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, softplus):
+        out, last, ckpt = torch.ops.mamba_cpu.selective_scan_cfwd(u, delta, A, B, C, D, z, delta_bias,
+                                                                  softplus)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, ckpt)
+        ctx.softplus = softplus
+        ctx.set_materialize_grads(False)
+        return out, last
+
+    @staticmethod
+    def backward(ctx, dout, dlast):
+        u, delta, A, B, C, D, z, delta_bias, ckpt = ctx.saved_tensors
+        dout = torch.zeros_like(u) if dout is None else dout.to(u.dtype)
+        dlast = None if dlast is None else dlast.to(torch.complex64)
+        du, ddelta, dA, dB, dC, dD, dz, dbias = torch.ops.mamba_cpu.selective_scan_cbwd(
+            u, delta, A, B, C, D, z, delta_bias, ctx.softplus, dout, dlast, ckpt)
+        return (du, ddelta, dA, dB, dC, dD if D is not None else None, dz if z is not None else None,
+                dbias if delta_bias is not None else None, None)
+
+
+def _complex_kernel_bc(X: torch.Tensor, ngroups: int, batch: int, seqlen: int) -> torch.Tensor:
+    """B or C of a complex-A scan as the kernels' float32 (b, ngroups, l, n, 2)
+    operand, (re, im) in the unit-stride last dim. Input-dependent B/C are real
+    (b, n, 2 l) or (b, g, n, 2 l) with the pairs interleaved along the last dim
+    (mamba_ssm's layout): a view. A (dim, dstate) B/C, complex or real, is
+    input-independent, one group per channel: a stride-0 view of
+    view_as_real. Fewer groups than ngroups are repeated (a copy)."""
+    if X.dim() == 2:
+        Xr = torch.view_as_real(X.to(torch.complex64))
+        return Xr[None, :, None].expand(batch, X.shape[0], seqlen, X.shape[1], 2)
+    X = X if X.dim() == 4 else X.unsqueeze(1)
+    Xk = X.float().unflatten(-1, (seqlen, 2)).transpose(2, 3)
+    if Xk.stride(-1) != 1:
+        Xk = Xk.contiguous()
+    if Xk.shape[1] != ngroups:
+        Xk = Xk.repeat_interleave(ngroups // Xk.shape[1], dim=1)
+    return Xk
+
+
+def _complex_scan(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state, xdt):
+    """selective_scan_fn for complex A (mamba_ssm's semantics, which the
+    reference rejects: selective_scan_interface.py:160-161)."""
+    batch, dim, seqlen = u.shape
+    for name, X in (("B", B), ("C", C)):
+        if X.is_complex() or X.dim() == 2:
+            if X.dim() != 2 or X.shape[0] != dim or X.shape[1] != A.shape[1]:
+                raise ValueError(f"a complex {name} must be input-independent, (dim, dstate), "
+                                 f"got {tuple(X.shape)}")
+        elif X.dim() not in (3, 4) or X.shape[-1] != 2 * seqlen or X.shape[-2] != A.shape[1]:
+            raise ValueError(f"with complex A, an input-dependent {name} is real (batch, [ngroups,] dstate, "
+                             f"2 * seqlen) holding (re, im) pairs, got {tuple(X.shape)}")
+
+    def groups(X):
+        return dim if X.dim() == 2 else (1 if X.dim() == 3 else X.shape[1])
+
+    for name, X in (("B", B), ("C", C)):
+        if dim % groups(X) != 0:
+            raise ValueError(f"dim ({dim}) must be divisible by {name}'s ngroups ({groups(X)})")
+    ngroups = math.lcm(groups(B), groups(C))
+    args = (
+        _as_x(u, xdt), _as_x(delta, xdt), A.to(torch.complex64).contiguous(),
+        _complex_kernel_bc(B, ngroups, batch, seqlen), _complex_kernel_bc(C, ngroups, batch, seqlen),
+        _as_f32(D), _as_x(z, xdt), _as_f32(delta_bias), bool(delta_softplus),
+    )
+    out, last_state = _ComplexScan.apply(*args)
+    out = out.to(u.dtype)
+    return (out, last_state) if return_last_state else out
+
+
 def _as_f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return None if t is None else t.float().contiguous()
 
@@ -129,18 +218,27 @@ def selective_scan_fn(
     ROCm GPU tensors.
 
     u, delta, z: (batch, dim, seqlen), float32 / bfloat16 / float16
-    A: (dim, dstate), real-valued
+    A: (dim, dstate), real-valued, or complex (dstate <= 32)
     B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen), input-dependent,
-          with their own group counts; or (dim, dstate), input-independent
+          with their own group counts; or (dim, dstate), input-independent.
+          With complex A (mamba_ssm's convention): input-dependent B/C are real
+          (batch, [ngroups,] dstate, 2 * seqlen) with (re, im) pairs along the
+          last dim, input-independent ones complex (dim, dstate); y = 2 Re(<h, C>) + D u
     D, delta_bias: (dim,)
-    Returns out: (batch, dim, seqlen) in u's dtype [, last_state: (batch, dim, dstate) float32]
+    Returns out: (batch, dim, seqlen) in u's dtype [, last_state: (batch, dim, dstate) float32,
+    complex64 with complex A]
     Arithmetic and the scan state are float32 for every input dtype.
     """
     if u.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {u.device}")
-    if A.is_complex():
-        raise NotImplementedError("complex A is not supported yet")
     batch, dim, seqlen = u.shape
+    # u/delta/z keep their storage type when they share a supported one;
+    # mixed or other types are computed from float32 copies.
+    xdt = u.dtype
+    if xdt not in _X_DTYPES or delta.dtype != xdt or (z is not None and z.dtype != xdt):
+        xdt = torch.float32
+    if A.is_complex():
+        return _complex_scan(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state, xdt)
 
     def groups(X):
         return dim if X.dim() == 2 else (1 if X.dim() == 3 else X.shape[1])
@@ -154,12 +252,6 @@ def selective_scan_fn(
     # input-independent B/C, which are one group per channel) run at their
     # least common multiple; the reference rejects both (:160-170).
     ngroups = math.lcm(groups(B), groups(C))
-
-    # u/delta/z keep their storage type when they share a supported one;
-    # mixed or other types are computed from float32 copies.
-    xdt = u.dtype
-    if xdt not in _X_DTYPES or delta.dtype != xdt or (z is not None and z.dtype != xdt):
-        xdt = torch.float32
     args = (
         _as_x(u, xdt), _as_x(delta, xdt), _as_f32(A), _kernel_bc_groups(B, ngroups, batch, seqlen),
         _kernel_bc_groups(C, ngroups, batch, seqlen), _as_f32(D), _as_x(z, xdt), _as_f32(delta_bias),

@@ -21,6 +21,10 @@ Pinning (how each oracle function is checked, so a plausible mistake fails):
                     dstate=1 hand recurrence); NaN confinement.
   scan backward     vs the compiled reference (_ref); vs torch.autograd through
                     an independent float64 forward; central finite differences.
+  complex-A scan    (mamba_ssm's semantics; the reference has no complex path)
+                    forward vs a closed-form direct sum and vs the real scan
+                    (Im A = 0); a phase invariance of B/C; backward vs
+                    torch.autograd through the direct sum in complex128.
   conv forward      vs numpy.convolve per channel (textbook routine);
                     initial/final-state chaining invariants.
   conv backward     vs torch.autograd through F.conv1d in float64.

@@ -178,6 +178,149 @@ def selective_scan_bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     return du, ddelta, dA.sum(0), dB, dC, dD_full, dz, ddelta_bias
 
 
+def _is_complex(x):
+    return x.is_complex() if hasattr(x, "is_complex") else np.iscomplexobj(x)
+
+
+def _c128(x):
+    if x is None:
+        return None
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().numpy()
+    return np.asarray(x, dtype=np.complex128)
+
+
+def _complex_bc(X, dim, batch, seqlen):
+    """B or C of a complex-A scan as complex (b, g, n, l) plus channels per
+    group. Input-dependent B/C are real (b, n, 2l) or (b, g, n, 2l) holding
+    (re, im) pairs along the last dim (mamba_ssm's selective_scan_ref:
+    view_as_complex over "... (L two) -> ... L two"); a 2-D (dim, dstate)
+    B/C is complex and input-independent (one group per channel)."""
+    if _is_complex(X):
+        X = _c128(X)
+        if X.ndim != 2:
+            raise ValueError("complex B/C must be 2-D (dim, dstate)")
+        return np.broadcast_to(X[None, :, :, None], (batch, X.shape[0], X.shape[1], seqlen)), 1
+    X = _f64(X)
+    if X.ndim == 3:
+        X = X[:, None]
+    Xc = X[..., 0::2] + 1j * X[..., 1::2]
+    return Xc, dim // Xc.shape[1]
+
+
+def selective_scan_fwd_complex(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                               delta_softplus=False):
+    """Forward scan with complex A (mamba_ssm's selective_scan_ref semantics;
+    the reference rejects complex A, src/mamba_cpu/ops/selective_scan_interface.py:160-161):
+        h_t = exp(dt_t * A) * h_{t-1} + dt_t * u_t * B_t      (complex, h_{-1} = 0)
+        y_t = 2 * Re(sum_n h_t C_t) + D * u_t ;  out_t = y_t * silu(z_t)
+    A: complex (dim, dstate). B/C: see _complex_bc. Returns (out, last_state)
+    with last_state complex (b, d, n)."""
+    u, delta, A = _f64(u), _f64(delta), _c128(A)
+    D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
+    batch, dim, seqlen = u.shape
+    B, dpg = _complex_bc(B, dim, batch, seqlen)
+    C, dpgC = _complex_bc(C, dim, batch, seqlen)
+    dt = _dt(delta, delta_bias, delta_softplus)
+    h = np.zeros((batch, dim, A.shape[1]), dtype=np.complex128)
+    y = np.zeros((batch, dim, seqlen))
+    with np.errstate(over="ignore", invalid="ignore"):
+        for t in range(seqlen):
+            Bt = np.repeat(B[:, :, :, t], dpg, axis=1)
+            Ct = np.repeat(C[:, :, :, t], dpgC, axis=1)
+            h = np.exp(dt[:, :, t, None] * A[None]) * h + (dt[:, :, t] * u[:, :, t])[..., None] * Bt
+            y[:, :, t] = 2.0 * (h * Ct).sum(-1).real
+        out = y if D is None else y + D[None, :, None] * u
+        if z is not None:
+            out = out * z * sigmoid(z)
+    return out, h
+
+
+def _complex_bc_grad(G, X, dpg):
+    """dLoss/dB for B = X from the per-channel complex gradient G (b, d, n, l)
+    (real part: dLoss/dRe, imaginary part: dLoss/dIm), in X's own layout."""
+    b, d, n, l = G.shape
+    Gg = G.reshape(b, d // dpg, dpg, n, l).sum(2)
+    if _is_complex(X):
+        return G.sum((0, 3))
+    out = np.stack([Gg.real, Gg.imag], axis=-1).reshape(b, d // dpg, n, 2 * l)
+    return out[:, 0] if _f64(X).ndim == 3 else out
+
+
+def selective_scan_bwd_complex(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                               delta_softplus=False, dout=None, dlast_state=None):
+    """Backward of selective_scan_fwd_complex by the chain rule on the real and
+    imaginary parts. A complex gradient holds dLoss/dRe + i dLoss/dIm (torch's
+    convention for complex leaves). For t = L-1 .. 0, with gh = dLoss/dh_t
+    carried backwards from dlast_state:
+        g  = gh + 2 dy conj(C_t) ;  dC_t = 2 dy conj(h_t) ;  dB_t = g dt u
+        gh = g conj(a_t)  (a_t = exp(dt A)) ;  q = gh conj(h_{t-1}) ;  dA += dt q
+        ddt = sum_n Re(q conj(A)) + u sum_n Re(g conj(B_t))
+        du  = dy D + dt sum_n Re(g conj(B_t))
+    (dy, dz, the softplus factor and dD / ddelta_bias as in the real scan).
+    Returns (du, ddelta, dA, dB, dC, dD, dz, ddelta_bias); dA complex (d, n),
+    dB/dC in B's and C's layouts."""
+    u, delta, A = _f64(u), _f64(delta), _c128(A)
+    D, z, delta_bias = _f64(D), _f64(z), _f64(delta_bias)
+    dout = _f64(dout)
+    dlast_state = _c128(dlast_state)
+    batch, dim, seqlen = u.shape
+    N = A.shape[1]
+    Bc, dpg = _complex_bc(B, dim, batch, seqlen)
+    Cc, dpgC = _complex_bc(C, dim, batch, seqlen)
+    if dout is None:
+        dout = np.zeros_like(u)
+    dt = _dt(delta, delta_bias, delta_softplus)
+    pre = delta if delta_bias is None else delta + delta_bias[None, :, None]
+    Dv = np.zeros(dim) if D is None else D
+    with np.errstate(over="ignore", invalid="ignore"):
+        hs = np.zeros((seqlen + 1, batch, dim, N), dtype=np.complex128)
+        for t in range(seqlen):
+            Bt = np.repeat(Bc[:, :, :, t], dpg, axis=1)
+            hs[t + 1] = np.exp(dt[:, :, t, None] * A[None]) * hs[t] + \
+                (dt[:, :, t] * u[:, :, t])[..., None] * Bt
+        gh = np.zeros((batch, dim, N), dtype=np.complex128) if dlast_state is None else dlast_state.copy()
+        du = np.zeros_like(u)
+        ddelta = np.zeros_like(u)
+        dz = None if z is None else np.zeros_like(u)
+        dA = np.zeros((batch, dim, N), dtype=np.complex128)
+        dBf = np.zeros((batch, dim, N, seqlen), dtype=np.complex128)
+        dCf = np.zeros((batch, dim, N, seqlen), dtype=np.complex128)
+        for t in range(seqlen - 1, -1, -1):
+            Bt = np.repeat(Bc[:, :, :, t], dpg, axis=1)
+            Ct = np.repeat(Cc[:, :, :, t], dpgC, axis=1)
+            h, h_prev = hs[t + 1], hs[t]
+            ut, dtt = u[:, :, t], dt[:, :, t]
+            dy = dout[:, :, t]
+            if z is not None:
+                y = 2.0 * (h * Ct).sum(-1).real + Dv[None] * ut
+                zt = z[:, :, t]
+                sg = sigmoid(zt)
+                dz[:, :, t] = dout[:, :, t] * y * sg * (1 + zt * (1 - sg))
+                dy = dout[:, :, t] * zt * sg
+            g = gh + 2.0 * dy[..., None] * np.conj(Ct)
+            dCf[:, :, :, t] = 2.0 * dy[..., None] * np.conj(h)
+            a = np.exp(dtt[..., None] * A[None])
+            gh = g * np.conj(a)
+            q = gh * np.conj(h_prev)
+            dA += dtt[..., None] * q
+            gB = (g * np.conj(Bt)).real.sum(-1)
+            ddt = (q * np.conj(A[None])).real.sum(-1) + ut * gB
+            dBf[:, :, :, t] = g * (dtt * ut)[..., None]
+            du[:, :, t] = dy * Dv[None] + dtt * gB
+            if delta_softplus:
+                ddt = ddt * sigmoid(pre[:, :, t])
+            ddelta[:, :, t] = ddt
+        dD_full = None
+        if D is not None:
+            dy_all = dout if z is None else dout * z * sigmoid(z)
+            dD_full = (dy_all * u).sum((0, 2))
+        ddelta_bias = None if delta_bias is None else ddelta.sum((0, 2))
+    dB = _complex_bc_grad(dBf, B, dpg)
+    dC = _complex_bc_grad(dCf, C, dpgC)
+    return du, ddelta, dA.sum(0), dB, dC, dD_full, dz, ddelta_bias
+
+
 def _tap_mask(seq_idx, width, seqlen):
     """(b, 1, width, seqlen) 0/1: tap k of output t reads x[t - (width-1) + k],
     which counts only inside t's own sequence (seq_idx equal, position >= 0),

@@ -458,3 +458,133 @@ def test_conv_seq_idx_equals_separate_sequences(activation):
             db_sum += g1[2]
     np.testing.assert_allclose(dw, dw_sum, rtol=1e-12)
     np.testing.assert_allclose(db, db_sum, rtol=1e-12)
+
+
+# ---- complex A (mamba_ssm's semantics; the reference rejects complex A) ----
+
+def complex_case(batch, dim, seqlen, dstate, ngroups, seed=0, bc2d=False):
+    """Complex-A inputs: A complex (dim, dstate) with negative real parts;
+    B/C real (b[, g], n, 2 l) with (re, im) pairs along the last dim, or
+    complex (dim, dstate) when bc2d."""
+    rng = np.random.default_rng(seed)
+    bc = (batch, dstate, 2 * seqlen) if ngroups is None else (batch, ngroups, dstate, 2 * seqlen)
+    cplx = lambda *s: rng.standard_normal(s) + 1j * rng.standard_normal(s)  # noqa: E731
+    return dict(
+        u=rng.standard_normal((batch, dim, seqlen)),
+        delta=rng.random((batch, dim, seqlen)) * 0.5,
+        A=-(rng.random((dim, dstate)) + 0.5) + 1j * rng.standard_normal((dim, dstate)) * 3,
+        B=cplx(dim, dstate) if bc2d else rng.standard_normal(bc),
+        C=rng.standard_normal(bc),
+        D=rng.standard_normal(dim),
+        z=rng.standard_normal((batch, dim, seqlen)),
+        delta_bias=rng.random(dim) * 0.1,
+    )
+
+
+def _complex_direct_sum(u, delta, A, B, C, D, z, delta_bias, softplus):
+    """Torch float64/complex128 forward in closed form, no recurrence:
+    h_t = sum_{s<=t} exp(A (S_t - S_s)) dt_s u_s B_s with S_t = sum_{r<=t} dt_r,
+    out = (2 Re <h_t, C_t> + D u) silu(z). B/C as in complex_case (real
+    interleaved pairs, or complex (dim, dstate)). Returns (out, last_state)."""
+    b, d, l = u.shape
+    dt = delta + delta_bias[None, :, None]
+    dt = F.softplus(dt) if softplus else dt
+
+    def per_channel(X):
+        if X.is_complex():
+            return X[None, :, :, None].expand(b, d, X.shape[1], l)
+        X = X if X.dim() == 4 else X[:, None]
+        Xc = torch.view_as_complex(X.reshape(*X.shape[:-1], l, 2).contiguous())
+        return Xc.repeat_interleave(d // Xc.shape[1], dim=1)  # (b, d, n, l)
+
+    Bf, Cf = per_channel(B), per_channel(C)
+    S = torch.cumsum(dt, -1)
+    diff = S[..., :, None] - S[..., None, :]  # (b, d, t, s)
+    mask = torch.tril(torch.ones(l, l, dtype=torch.float64))
+    K = torch.exp(diff[..., None] * A[None, :, None, None, :]) * mask[..., None]  # (b, d, t, s, n)
+    x = (dt * u)[:, :, None, :, None] * Bf.permute(0, 1, 3, 2)[:, :, None]  # (b, d, 1, s, n)
+    h = (K * x).sum(3)  # (b, d, t, n)
+    y = 2 * (h * Cf.permute(0, 1, 3, 2)).sum(-1).real + D[None, :, None] * u
+    return y * F.silu(z), h[:, :, -1]
+
+
+@pytest.mark.parametrize("ngroups,bc2d", [(None, False), (2, False), (None, True)])
+def test_complex_scan_fwd_equals_direct_sum(ngroups, bc2d):
+    inp = complex_case(2, 4, 9, 3, ngroups, seed=51, bc2d=bc2d)
+    out, last = O.selective_scan_fwd_complex(**inp, delta_softplus=True)
+    t = {k: torch.from_numpy(v) for k, v in inp.items()}
+    want, want_last = _complex_direct_sum(**t, softplus=True)
+    np.testing.assert_allclose(out, want.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(last, want_last.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_complex_scan_real_case_and_phase_invariance():
+    """A with zero imaginary part and real B, C reduce to the real scan with C
+    doubled (y = 2 Re <h, C>); rotating state n's B by exp(i phi_n) and C by
+    exp(-i phi_n) leaves the output unchanged."""
+    rng = np.random.default_rng(52)
+    r = scan_case(2, 4, 11, 3, None, True, seed=52)
+    inter = lambda X: np.stack([X, np.zeros_like(X)], -1).reshape(*X.shape[:-1], -1)  # noqa: E731
+    out, last = O.selective_scan_fwd_complex(r["u"], r["delta"], r["A"] + 0j, inter(r["B"]), inter(r["C"]),
+                                             r["D"], r["z"], r["delta_bias"], True)
+    want, want_last = O.selective_scan_fwd(r["u"], r["delta"], r["A"], r["B"], 2 * r["C"], r["D"], r["z"],
+                                           r["delta_bias"], True)
+    np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(last.real, want_last, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(last.imag, 0, atol=0)
+
+    inp = complex_case(2, 4, 11, 3, None, seed=53)
+    phi = rng.random(3) * 2 * np.pi
+
+    def rotate(X, sign):
+        Xc = X[..., 0::2] + 1j * X[..., 1::2]
+        Xc = Xc * np.exp(sign * 1j * phi)[:, None]
+        return np.stack([Xc.real, Xc.imag], -1).reshape(X.shape)
+
+    out0, _ = O.selective_scan_fwd_complex(**inp, delta_softplus=True)
+    out1, _ = O.selective_scan_fwd_complex(**{**inp, "B": rotate(inp["B"], 1), "C": rotate(inp["C"], -1)},
+                                           delta_softplus=True)
+    np.testing.assert_allclose(out1, out0, rtol=1e-11, atol=1e-12)
+    # the same rotation of B and C together is not an invariance
+    out2, _ = O.selective_scan_fwd_complex(**{**inp, "B": rotate(inp["B"], 1), "C": rotate(inp["C"], 1)},
+                                           delta_softplus=True)
+    assert not np.allclose(out2, out0, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("ngroups,bc2d", [(None, False), (2, False), (None, True)])
+def test_complex_scan_bwd_matches_autograd(ngroups, bc2d):
+    """The analytic complex backward against torch.autograd through the
+    closed-form forward (complex gradients: dLoss/dRe + i dLoss/dIm), with a
+    gradient on the last state too."""
+    inp = complex_case(2, 4, 8, 3, ngroups, seed=54, bc2d=bc2d)
+    rng = np.random.default_rng(55)
+    W = rng.standard_normal(inp["u"].shape)
+    W2 = rng.standard_normal((2, 4, 3)) + 1j * rng.standard_normal((2, 4, 3))
+    got = O.selective_scan_bwd_complex(**inp, delta_softplus=True, dout=W, dlast_state=W2)
+    names = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias"]
+    t = {k: torch.from_numpy(np.ascontiguousarray(v)).requires_grad_() for k, v in inp.items()}
+    out, last = _complex_direct_sum(**t, softplus=True)
+    loss = (out * torch.from_numpy(W)).sum() + (torch.conj(torch.from_numpy(W2)) * last).real.sum()
+    want = torch.autograd.grad(loss, [t[k] for k in names])
+    for k, g, w in zip(names, got, want):
+        np.testing.assert_allclose(g, w.numpy(), rtol=1e-9, atol=1e-10, err_msg=k)
+
+
+def test_complex_scan_planted_mistakes_are_caught():
+    """Copies of the complex oracle with a plausible mistake fail the checks above:
+    B's (re, im) pairs swapped, the factor 2 of y dropped, dA conjugated."""
+    inp = complex_case(1, 3, 7, 2, None, seed=56)
+    t = {k: torch.from_numpy(v) for k, v in inp.items()}
+    want, _ = _complex_direct_sum(**t, softplus=True)
+    swapped = inp["B"].reshape(1, 2, 7, 2)[..., ::-1].reshape(1, 2, 14)
+    out, _ = O.selective_scan_fwd_complex(**{**inp, "B": swapped}, delta_softplus=True)
+    assert not np.allclose(out, want.numpy(), rtol=1e-4, atol=1e-5)
+    half, _ = O.selective_scan_fwd_complex(**{**inp, "C": inp["C"] / 2}, delta_softplus=True)
+    assert not np.allclose(half, want.numpy(), rtol=1e-4, atol=1e-5)
+    W = np.random.default_rng(57).standard_normal(inp["u"].shape)
+    dA = O.selective_scan_bwd_complex(**inp, delta_softplus=True, dout=W)[2]
+    tt = {k: torch.from_numpy(v).requires_grad_() for k, v in inp.items()}
+    out, _ = _complex_direct_sum(**tt, softplus=True)
+    (gA,) = torch.autograd.grad((out * torch.from_numpy(W)).sum(), [tt["A"]])
+    np.testing.assert_allclose(dA, gA.numpy(), rtol=1e-9, atol=1e-10)
+    assert not np.allclose(np.conj(dA), gA.numpy(), rtol=1e-4, atol=1e-5)

@@ -161,10 +161,13 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_fwd.default, args)
 
 
-def test_rejects_complex():
+def test_complex_a_layout_checks():
+    # The reference rejects complex A (test_rejects_non_cpu_and_complex); here
+    # it runs (tests/test_selective_scan_complex.py) with mamba_ssm's B/C
+    # layout, and B/C in the real-A layout are rejected with a ValueError.
     inp = make_inputs(1, 4, 8, 2, None, False, False, False, torch.float32)
     inp["A"] = inp["A"].to(torch.complex64)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="2 \\* seqlen"):
         selective_scan_fn(**inp)
 
 
