@@ -270,13 +270,18 @@ int scan_fwd_waves() { return kFwdWaves; }
 
 // Time chunks for a forward with these parameters (p.nblk_c set for
 // scan_fwd_waves()): enough chunks to give the GPU's 256 compute units about
-// four workgroups each, at least two 16-step blocks per chunk. Sets
-// p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone fill the GPU.
+// five workgroups each (the kernel's occupancy), and chunks of at most 64
+// 16-step blocks, at least two blocks per chunk. Measured: batch 1, dim 1536,
+// seqlen 2048 fp32 runs fastest at 13 chunks (40 us against 44 us at 11);
+// batch 1, dim 5120, seqlen 16384 bf16 at 16-24 chunks (0.73 ms against
+// 0.83 ms at 4), although the summary pass then covers 15/16 of the sequence.
+// Sets p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone fill the GPU.
 void scan_fwd_chunks(ScanParams& p) {
   const int64_t wgs = p.batch * p.ngroups * p.nblk_c;
   int64_t n = 1;
   if (wgs > 0 && wgs < 512 && p.nblk >= 4) {
-    n = (1024 + wgs - 1) / wgs;
+    n = (1280 + wgs - 1) / wgs;
+    if (n < p.nblk / 64) n = p.nblk / 64;
     if (n > p.nblk / 2) n = p.nblk / 2;
   }
   p.chunk_blocks = n > 1 ? (p.nblk + n - 1) / n : (p.nblk > 0 ? p.nblk : 1);
