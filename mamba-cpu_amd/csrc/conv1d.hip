@@ -300,6 +300,54 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
   }
 }
 
+// Single-step update without a ring buffer (the decode step): a 2-D grid of
+// channel tiles x batch rows, so no per-thread 64-bit division. The whole old
+// state row (state_len <= kUpd1MaxS entries) and x are loaded together, the
+// output is computed, and the shifted state is stored from registers, so no
+// store waits on a reload of a slot it depends on.
+constexpr int kUpd1MaxS = 8;
+
+template <typename T, int W>
+__global__ void __launch_bounds__(256) conv_update1_kernel(const ConvUpdateParams p) {
+  const int64_t d = blockIdx.x * 256ll + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (d >= p.dim) return;
+  const int S = static_cast<int>(p.state_len);
+  const int64_t ob = b * p.sout[0] + d * p.sout[1];
+  int64_t srow = b;
+  if (p.state_idx != nullptr) {
+    srow = p.state_idx[b];
+    if (srow < 0 || srow >= p.state_batch) {
+      st<T>(p.out, ob, 0.f);
+      return;
+    }
+  }
+  const int64_t sb = srow * p.sst[0] + d * p.sst[1];
+  float old[kUpd1MaxS];
+#pragma unroll
+  for (int i = 0; i < kUpd1MaxS; ++i) old[i] = i < S ? ld<T>(p.state, sb + i * p.sst[2]) : 0.f;
+  const float xv = ld<T>(p.x, b * p.sx[0] + d * p.sx[1]);
+  float w[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) w[k] = p.w[d * W + k];
+  float acc = p.bias ? p.bias[d] : 0.f;
+  // Taps 0 .. W-2 read the newest W-1 state entries, tap W-1 reads x.
+#pragma unroll
+  for (int k = 0; k < W - 1; ++k) {
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < kUpd1MaxS; ++i)
+      if (i == S - (W - 1) + k) v = old[i];
+    acc = fmaf(w[k], v, acc);
+  }
+  acc = fmaf(w[W - 1], xv, acc);
+  if (p.silu) acc = acc * sigmoid(acc);
+  st<T>(p.out, ob, acc);
+#pragma unroll
+  for (int i = 0; i < kUpd1MaxS; ++i)
+    if (i < S) st<T>(p.state, sb + i * p.sst[2], i + 1 < S ? old[i + 1 < kUpd1MaxS ? i + 1 : 0] : xv);
+}
+
 // ---- Time-contiguous fast path ------------------------------------------------
 // For x, out, dout and dx with unit time stride, rows aligned to 4 elements and
 // seqlen a multiple of VT: each thread owns VT consecutive steps of one
@@ -626,9 +674,29 @@ hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float
   return hipGetLastError();
 }
 
+template <typename T>
+static bool launch_update1(const ConvUpdateParams& p, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((p.dim + 255) / 256), static_cast<unsigned>(p.batch));
+  switch (p.width) {
+    case 2: hipLaunchKernelGGL((conv_update1_kernel<T, 2>), grid, dim3(256), 0, st, p); return true;
+    case 3: hipLaunchKernelGGL((conv_update1_kernel<T, 3>), grid, dim3(256), 0, st, p); return true;
+    case 4: hipLaunchKernelGGL((conv_update1_kernel<T, 4>), grid, dim3(256), 0, st, p); return true;
+    default: return false;
+  }
+}
+
 hipError_t conv_update_launch(const ConvUpdateParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim;
   if (n == 0) return hipSuccess;
+  if (p.seqlen == 1 && p.cache_seqlens == nullptr && p.state_len <= kUpd1MaxS && p.batch <= 65535) {
+    bool done = false;
+    switch (dtype) {
+      case MCPU_F32: done = launch_update1<float>(p, st); break;
+      case MCPU_BF16: done = launch_update1<bf16>(p, st); break;
+      default: done = launch_update1<f16>(p, st); break;
+    }
+    if (done) return hipGetLastError();
+  }
   switch (dtype) {
     case MCPU_F32: hipLaunchKernelGGL(conv_update_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
     case MCPU_BF16: hipLaunchKernelGGL(conv_update_kernel<bf16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;

@@ -87,6 +87,32 @@ def test_update_matches_oracle(state_len, seqlen):
     close(state, want_state, 0, 0)
 
 
+@pytest.mark.parametrize("width", [2, 3, 4, 5])
+@pytest.mark.parametrize("extra", [0, 1, "max", "over"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
+def test_single_step_update_matches_oracle(width, extra, dtype, layout):
+    """The single-token decode step (its own kernel for widths 2-4 and state
+    lengths up to 8, the general one otherwise) over several steps, with state
+    lengths width-1, width, 8 and 9, in both state layouts."""
+    torch.manual_seed(3)
+    b, d = 3, 300
+    S = {0: width - 1, 1: width, "max": 8, "over": 9}[extra]
+    w, bias = torch.randn(d, width, device=DEV), torch.randn(d, device=DEV)
+    if layout == "contiguous":
+        state = torch.randn(b, d, S, device=DEV).to(dtype)
+    else:
+        state = torch.randn(b, S, d, device=DEV).to(dtype).transpose(1, 2)
+    want_state = state.cpu().double().numpy()
+    for step in range(3):
+        x = torch.randn(b, d, device=DEV).to(dtype)
+        out = causal_conv1d_update(x, state, w, bias, "silu")
+        want, want_state = O.causal_conv1d_update(x, want_state, w, bias, "silu")
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        close(out, want, tol, tol, f"out step {step}")
+        close(state, want_state, 0, 0, f"state step {step}")
+
+
 def test_final_states_out_buffer():
     x = torch.randn(2, 8, 10, device=DEV)
     w = torch.randn(8, 4, device=DEV)
