@@ -215,6 +215,8 @@ extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void
     return fail(MCPU_ERR_INVALID, "selective_state_update: nheads must be divisible by ngroups");
   if (!valid_dtype(a->dtype) || !valid_dtype(a->state_dtype))
     return fail(MCPU_ERR_INVALID, "selective_state_update: bad dtype");
+  if (a->nheads * a->headdim > 0xffff0000ll)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_state_update: nheads * headdim too large");
   if (int rc = mcpu_check_device()) return rc;
   StateUpdateParams p;
   std::memset(&p, 0, sizeof(p));

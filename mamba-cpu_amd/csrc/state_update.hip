@@ -6,8 +6,10 @@
 //   state = state * exp(dt * A) + dt * x * B[group]
 //   out   = (<state, C[group]> + D * x) * silu(z)
 // Same lane layout as the scan: 16 state lanes per row, 4 rows per wave, so a
-// 256-thread workgroup updates 16 rows; the <state, C> sum is a DPP row
-// all-reduce. The state is read and written in place.
+// 256-thread workgroup updates 16 rows of one batch entry (grid: row tiles of
+// the (nheads, headdim) rows x batch, so the row decode is one 32-bit
+// division); the <state, C> sum is a DPP row all-reduce. The state is read
+// and written in place.
 #include "mcpu_common.h"
 #include "op_params.h"
 
@@ -16,61 +18,59 @@ namespace mcpu {
 template <typename Tx, typename Ts, int SPL>
 __global__ void __launch_bounds__(256) state_update_kernel(const StateUpdateParams p) {
   const int j = threadIdx.x & 15;
-  const int64_t rowid = blockIdx.x * 16ll + (threadIdx.x >> 4);
-  const int64_t rows = p.batch * p.nheads * p.headdim;
-  // Whole rows of 16 lanes share the branch, so the DPP reduction below never
-  // mixes live and retired lanes of one row.
-  if (rowid >= rows) return;
-  const int64_t pp = rowid % p.headdim;
-  const int64_t h = (rowid / p.headdim) % p.nheads;
-  const int64_t b = rowid / (p.headdim * p.nheads);
-  const int64_t g = h / (p.nheads / p.ngroups);
+  const uint32_t hp = blockIdx.x * 16u + (threadIdx.x >> 4);  // row within (nheads, headdim)
+  // Whole rows of 16 lanes share every branch, so the DPP reduction below
+  // never mixes live and retired lanes of one row.
+  if (hp >= static_cast<uint32_t>(p.nheads * p.headdim)) return;
+  const uint32_t hd = static_cast<uint32_t>(p.headdim);
+  const uint32_t h = hp / hd, pp = hp - h * hd;
+  const int64_t g = h / static_cast<uint32_t>(p.nheads / p.ngroups);
   const int64_t N = p.dstate;
-  const int64_t hp = h * p.headdim + pp;  // index into (nheads, headdim) parameters
-
-  const float x = ld<Tx>(p.x, b * p.sx[0] + h * p.sx[1] + pp * p.sx[2]);
-  float dt = ld<Tx>(p.dt, b * p.sdt[0] + h * p.sdt[1] + pp * p.sdt[2]);
-  if (p.dt_bias != nullptr) dt += p.dt_bias[hp];
-  if (p.softplus) dt = softplus(dt);
-  const float dtx = dt * x;
-  int64_t srow = b;
-  if (p.state_idx != nullptr) {
-    // Rows of one (batch, head, p) share b, so the whole 16-lane row leaves.
-    srow = p.state_idx[b];
-    if (srow < 0 || srow >= p.state_batch) {
-      if (j == 0) st<Tx>(p.out, rowid, 0.f);
-      return;
+  for (int64_t b = blockIdx.y; b < p.batch; b += gridDim.y) {
+    const int64_t rowid = b * p.nheads * p.headdim + hp;
+    const float x = ld<Tx>(p.x, b * p.sx[0] + h * p.sx[1] + pp * p.sx[2]);
+    float dt = ld<Tx>(p.dt, b * p.sdt[0] + h * p.sdt[1] + pp * p.sdt[2]);
+    if (p.dt_bias != nullptr) dt += p.dt_bias[hp];
+    if (p.softplus) dt = softplus(dt);
+    const float dtx = dt * x;
+    int64_t srow = b;
+    if (p.state_idx != nullptr) {
+      srow = p.state_idx[b];
+      if (srow < 0 || srow >= p.state_batch) {
+        if (j == 0) st<Tx>(p.out, rowid, 0.f);
+        continue;
+      }
     }
-  }
-  const int64_t sbase = srow * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
-  float acc = 0.f;
+    const int64_t sbase = srow * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
+    float acc = 0.f;
 #pragma unroll
-  for (int s = 0; s < SPL; ++s) {
-    const int n = j + 16 * s;
-    if (n < N) {
-      const float a = fast_exp(dt * p.A[hp * N + n]);
-      const float Bn = p.B[b * p.sB[0] + g * p.sB[1] + n];
-      const float Cn = p.C[b * p.sC[0] + g * p.sC[1] + n];
-      const float sv = fmaf(ld<Ts>(p.state, sbase + n), a, dtx * Bn);
-      st<Ts>(p.state, sbase + n, sv);
-      acc = fmaf(sv, Cn, acc);
+    for (int s = 0; s < SPL; ++s) {
+      const int n = j + 16 * s;
+      if (n < N) {
+        const float a = fast_exp(dt * p.A[hp * N + n]);
+        const float Bn = p.B[b * p.sB[0] + g * p.sB[1] + n];
+        const float Cn = p.C[b * p.sC[0] + g * p.sC[1] + n];
+        const float sv = fmaf(ld<Ts>(p.state, sbase + n), a, dtx * Bn);
+        st<Ts>(p.state, sbase + n, sv);
+        acc = fmaf(sv, Cn, acc);
+      }
     }
-  }
-  float y = row_allreduce16(acc);
-  if (j == 0) {
-    if (p.D != nullptr) y = fmaf(x, p.D[hp], y);
-    if (p.z != nullptr) {
-      const float zz = ld<Tx>(p.z, b * p.sz[0] + h * p.sz[1] + pp * p.sz[2]);
-      y *= zz * sigmoid(zz);
+    float y = row_allreduce16(acc);
+    if (j == 0) {
+      if (p.D != nullptr) y = fmaf(x, p.D[hp], y);
+      if (p.z != nullptr) {
+        const float zz = ld<Tx>(p.z, b * p.sz[0] + h * p.sz[1] + pp * p.sz[2]);
+        y *= zz * sigmoid(zz);
+      }
+      st<Tx>(p.out, rowid, y);
     }
-    st<Tx>(p.out, rowid, y);
   }
 }
 
 template <typename Tx, typename Ts>
 static hipError_t launch_su(const StateUpdateParams& p, hipStream_t st) {
-  const int64_t rows = p.batch * p.nheads * p.headdim;
-  const unsigned blocks = static_cast<unsigned>((rows + 15) / 16);
+  const dim3 blocks(static_cast<unsigned>((p.nheads * p.headdim + 15) / 16),
+                    static_cast<unsigned>(p.batch < 65535 ? p.batch : 65535));
   if (p.dstate <= 16)
     hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 1>), dim3(blocks), dim3(256), 0, st, p);
   else if (p.dstate <= 32)
