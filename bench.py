@@ -322,6 +322,32 @@ def other_configs(torch, dev, stream, cpu):
     nbytes = (b * d + 2 * b * d * (w - 1) + b * d) * 4 + 4 * (d * w + d)
     r = _rate(nbytes, ms)
     r["workload"] = "causal_conv1d_update, fp32, state (64, 3072, 3), x (64, 3072), silu; per step of 256"
+    # The same 256 steps replayed from one HIP graph: the per-step time
+    # without the host's per-call dispatch (what a graph-captured decoder
+    # sees). The replayed state must equal the eager one.
+    try:
+        st0 = state.clone()
+        gph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            upd()
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(gph):
+            upd()
+        state.copy_(st0)
+        upd()
+        want = state.clone()
+        state.copy_(st0)
+        gph.replay()
+        torch.cuda.synchronize()
+        if torch.equal(state, want):
+            r["graph_us_per_step"] = round(_events_ms(torch, stream, gph.replay, 5) / 256 * 1e3, 2)
+        else:
+            r["graph_error"] = "replayed state differs from the eager state"
+        del gph
+    except Exception as exc:  # noqa: BLE001
+        r["graph_error"] = repr(exc)
     if cpu:
         from oracle import cpu_torch as CT
 
