@@ -257,6 +257,17 @@ __device__ __forceinline__ void wave_rows_reduce_scatter(const float (&x)[16], f
   }
 }
 
+// The same over 8 per-lane values x[i] (i = 0..7): y[k] (k = 0..1) in lane
+// (row, j) holds the sum over the 4 rows of x[2 * row + k] of lane j.
+__device__ __forceinline__ void wave_rows_reduce_scatter8(const float (&x)[8], float (&y)[2]) {
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = swap_sum<32>(x[i], x[i + 4]);
+  // rows 0,1 now hold values 0..3 summed over rows {r, r+2}; rows 2,3 hold 4..7.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) y[i] = swap_sum<16>(s[i], s[i + 2]);
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0 .. N-1.
 template <int... Is, typename F>
 __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F&& f) {

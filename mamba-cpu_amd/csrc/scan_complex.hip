@@ -242,9 +242,8 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
   }
 }
 
-template <typename Tx, int SPL, bool HAS_Z>
-__global__ void __launch_bounds__(64 * kCWaves) scan_cbwd_kernel(const ScanParams p) {
-  constexpr int W = kCWaves;
+template <typename Tx, int W, int SPL, bool HAS_Z>
+__global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
   constexpr int T = kScanBlockT;
@@ -482,14 +481,44 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cbwd_kernel(const ScanParam
       dy = go * zz * sg;
     }
 
-    // Reverse recurrence over the block.
+    // Padding rows (channels past the slice end) add nothing to dB/dC: their
+    // dy and dt u are zero in the terms dC = 2 dy conj(h), dB = g dt u.
+    const float dy_b = rc.active ? dy : 0.f;
+    const float dtu_b = rc.active ? dtu : 0.f;
+    // Reverse recurrence over the block. The dB/dC terms of steps 15..8 are
+    // summed over the wave's 4 channel rows and parked for the cross-wave sum
+    // as soon as step 8 is done, those of 7..0 at the end, which halves the
+    // registers they hold.
+    constexpr int TH = T / 2;
     float r1[T], r2[T], dBr[SPL][T], dBi[SPL][T], dCr[SPL][T], dCi[SPL][T];
+    auto flush = [&](auto LO) {
+      constexpr int i0 = decltype(LO)::value;
+#pragma unroll
+      for (int s = 0; s < SPL; ++s) {
+        float xs[4][TH];
+#pragma unroll
+        for (int i = 0; i < TH; ++i) {
+          xs[0][i] = dBr[s][i0 + i];
+          xs[1][i] = dBi[s][i0 + i];
+          xs[2][i] = dCr[s][i0 + i];
+          xs[3][i] = dCi[s][i0 + i];
+        }
+
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          float y2[2];
+          wave_rows_reduce_scatter8(xs[a], y2);
+          s_red[buf][a][wave][i0 + 2 * r][j + 16 * s] = y2[0];
+          s_red[buf][a][wave][i0 + 2 * r + 1][j + 16 * s] = y2[1];
+        }
+      }
+    };
     static_for<T>([&](auto I) {
       constexpr int i = T - 1 - decltype(I)::value;
       if (valid(i)) {
-        const float dy2 = 2.f * row_bcast<i>(dy);
+        const float dy2 = 2.f * row_bcast<i>(dy_b);
         const float dti = row_bcast<i>(dt);
-        const float dtui = row_bcast<i>(dtu);
+        const float dtui = row_bcast<i>(dtu_b);
         float acc1 = 0.f, acc2 = 0.f;
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
@@ -520,6 +549,8 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cbwd_kernel(const ScanParam
 #pragma unroll
         for (int s = 0; s < SPL; ++s) dBr[s][i] = dBi[s][i] = dCr[s][i] = dCi[s][i] = 0.f;
       }
+      if constexpr (i == TH) flush(std::integral_constant<int, TH>{});
+      if constexpr (i == 0) flush(std::integral_constant<int, 0>{});
     });
 
     const float R1 = row_reduce_scatter16(r1, j);  // sum_n Re(q conj(A)) for step t
@@ -532,23 +563,6 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cbwd_kernel(const ScanParam
       dbias_acc += ddt;
     }
 
-    // dB/dC: sum over the wave's 4 channels, park for the cross-wave sum.
-#pragma unroll
-    for (int s = 0; s < SPL; ++s) {
-      if (!rc.active) {
-#pragma unroll
-        for (int i = 0; i < T; ++i) dBr[s][i] = dBi[s][i] = dCr[s][i] = dCi[s][i] = 0.f;
-      }
-      float y4[4][4];
-      wave_rows_reduce_scatter(dBr[s], y4[0]);
-      wave_rows_reduce_scatter(dBi[s], y4[1]);
-      wave_rows_reduce_scatter(dCr[s], y4[2]);
-      wave_rows_reduce_scatter(dCi[s], y4[3]);
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) s_red[buf][a][wave][4 * r + q][j + 16 * s] = y4[a][q];
-    }
     park(buf ^ 1);  // from block 0 a harmless copy into the idle buffer
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {
@@ -613,14 +627,14 @@ static hipError_t launch_cfwd(const ScanParams& p, bool write_out, hipStream_t s
   return hipGetLastError();
 }
 
-template <typename Tx, int SPL>
+template <typename Tx, int W, int SPL>
 static hipError_t launch_cbwd(const ScanParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c));
-  const dim3 block(64 * kCWaves);
+  const dim3 block(64 * W);
   if (p.z != nullptr)
-    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, SPL, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, SPL, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
@@ -630,10 +644,12 @@ static hipError_t cfwd_spl(const ScanParams& p, bool write_out, hipStream_t stre
   return launch_cfwd<Tx, 2>(p, write_out, stream);
 }
 
+// 4-wave workgroups for the backward too: 8 waves halve the dB/dC partials
+// but their LDS leaves one workgroup per CU, and the kernel ran 25 % slower.
 template <typename Tx>
 static hipError_t cbwd_spl(const ScanParams& p, hipStream_t stream) {
-  if (p.dstate <= 16) return launch_cbwd<Tx, 1>(p, stream);
-  return launch_cbwd<Tx, 2>(p, stream);
+  if (p.dstate <= 16) return launch_cbwd<Tx, kCWaves, 1>(p, stream);
+  return launch_cbwd<Tx, kCWaves, 2>(p, stream);
 }
 
 int scan_complex_waves() { return kCWaves; }
