@@ -204,11 +204,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> selective_scan_fwd_ckpt(
 
 using Grads8 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>;
 
+// dz_into: an existing (batch, dim, seqlen) view to write dz into (any
+// strides), instead of a new tensor.
 Grads8 scan_bwd_impl(const char* name, const Tensor& u, const Tensor& delta, const Tensor& A,
                      const Tensor& B, const Tensor& C, const optional<Tensor>& D,
                      const optional<Tensor>& z, const optional<Tensor>& bias, bool softplus,
                      const Tensor& dout, const optional<Tensor>& dlast_state,
-                     const optional<Tensor>& ckpt, const optional<Tensor>& ysave_in) {
+                     const optional<Tensor>& ckpt, const optional<Tensor>& ysave_in,
+                     const Tensor* dz_into = nullptr) {
   validate_scan(name, u, delta, A, B, C, D, z, bias, {opt(dout), dlast_state, ckpt, ysave_in});
   TORCH_CHECK_VALUE(dout.sizes() == u.sizes() && dout.scalar_type() == u.scalar_type(), name,
                     " expects dout shaped and typed like u");
@@ -238,7 +241,7 @@ Grads8 scan_bwd_impl(const char* name, const Tensor& u, const Tensor& delta, con
   Tensor dB = at::empty(B.sizes(), B.options());
   Tensor dC = at::empty(C.sizes(), C.options());
   Tensor dD = at::empty({dim}, A.options());
-  Tensor dz = has(z) ? like_x(*z) : at::empty({0}, u.options());
+  Tensor dz = has(z) ? (dz_into != nullptr ? *dz_into : like_x(*z)) : at::empty({0}, u.options());
   Tensor dbias = at::empty({dim}, A.options());
   mcpu_scan_args a = scan_args(u, delta, A, B, C, D, z, bias, softplus);
   a.dout = dout.data_ptr();
@@ -580,10 +583,12 @@ std::tuple<Tensor, Tensor> causal_conv1d_fwd(const Tensor& x, const Tensor& weig
   return {out, final};
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
+// dx_into: an existing (batch, dim, seqlen) view to write dx into (any
+// strides), instead of a new tensor.
+std::tuple<Tensor, Tensor, Tensor, Tensor> conv_bwd_impl(
     const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
     const optional<Tensor>& init, const Tensor& dout, const optional<Tensor>& dfinal_states,
-    bool silu, const optional<Tensor>& seq_idx) {
+    bool silu, const optional<Tensor>& seq_idx, const Tensor* dx_into) {
   const char* name = "mamba_cpu::causal_conv1d_bwd";
   check_seq_idx(name, seq_idx, x);
   check_conv(name, x, weight, bias, init);
@@ -600,7 +605,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
     dfinal = dfinal_states->to(x.scalar_type()).contiguous();
   }
   c10::DeviceGuard guard(x.device());
-  Tensor dx = like_x(x);
+  Tensor dx = dx_into != nullptr ? *dx_into : like_x(x);
   Tensor dweight = at::empty(weight.sizes(), weight.options());
   Tensor dbias = has(bias) ? at::empty({d}, weight.options()) : at::empty({0}, weight.options());
   Tensor dinit = has(init) ? at::empty({b, d, w - 1}, x.options()) : at::empty({0}, x.options());
@@ -618,6 +623,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
                         x.options().dtype(at::kByte));
   check_rc(mcpu_causal_conv1d_bwd(&a, ws.data_ptr(), ws_bytes, stream_of(x)), name);
   return {dx, dweight, dbias, dinit};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> causal_conv1d_bwd(
+    const Tensor& x, const Tensor& weight, const optional<Tensor>& bias,
+    const optional<Tensor>& init, const Tensor& dout, const optional<Tensor>& dfinal_states,
+    bool silu, const optional<Tensor>& seq_idx) {
+  return conv_bwd_impl(x, weight, bias, init, dout, dfinal_states, silu, seq_idx, nullptr);
 }
 
 struct ConvFn : public torch::autograd::Function<ConvFn> {
@@ -725,6 +737,110 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
   a.state_batch = conv_state.size(0);
   check_rc(mcpu_causal_conv1d_update(&a, stream_of(x)), name);
   return out;
+}
+
+// ---- fused Mamba-1 mixer (mamba_inner_fn) --------------------------------------------
+//
+// The forward and backward of mamba_inner_fn (without the optional RMS norms)
+// as two operators, so that a training step issues its conv, scan and GEMM
+// calls from C++ instead of one Python call each. Everything between in_proj
+// and out_proj stays in the (batch, seqlen, channels) layout of in_proj's
+// output: xz is the transposed view transformers passes, the conv and scan
+// read and write those views through their strides, and the backward writes
+// dx and dz straight into the two halves of one (batch, seqlen, 2 dim)
+// gradient.
+
+void check_inner(const char* name, const Tensor& xz, const Tensor& conv_w, const Tensor& x_proj_w,
+                 const Tensor& dt_proj_w, const Tensor& out_proj_w, const Tensor& A) {
+  for (const Tensor* t : {&xz, &conv_w, &x_proj_w, &dt_proj_w, &out_proj_w, &A}) {
+    check_gpu(name, opt(*t));
+    TORCH_CHECK_VALUE(t->scalar_type() == at::kFloat, name, " runs float32 tensors");
+  }
+  TORCH_CHECK_VALUE(xz.dim() == 3 && xz.size(1) % 2 == 0, name, " expects xz (batch, 2 dim, seqlen)");
+  const int64_t d = xz.size(1) / 2;
+  TORCH_CHECK_VALUE(A.dim() == 2 && A.size(0) == d, name, " expects A (dim, dstate)");
+  const int64_t R = dt_proj_w.size(1), N = A.size(1);
+  TORCH_CHECK_VALUE(conv_w.numel() % d == 0 && conv_w.size(0) == d, name, " expects conv1d_weight (dim, [1,] width)");
+  TORCH_CHECK_VALUE(x_proj_w.dim() == 2 && x_proj_w.size(0) == R + 2 * N && x_proj_w.size(1) == d, name,
+                    " expects x_proj_weight (dt_rank + 2 dstate, dim)");
+  TORCH_CHECK_VALUE(dt_proj_w.dim() == 2 && dt_proj_w.size(0) == d, name, " expects delta_proj_weight (dim, dt_rank)");
+  TORCH_CHECK_VALUE(out_proj_w.dim() == 2 && out_proj_w.size(1) == d, name, " expects out_proj_weight (d_model, dim)");
+}
+
+// Returns (out, conv_out, x_dbl, delta, ckpt, ysave, y): out (batch, seqlen,
+// d_model) and what the backward restarts from.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> mamba_inner_fwd(
+    const Tensor& xz, const Tensor& conv_w, const optional<Tensor>& conv_b, const Tensor& x_proj_w,
+    const Tensor& dt_proj_w, const Tensor& out_proj_w, const optional<Tensor>& out_proj_b,
+    const Tensor& A, const optional<Tensor>& D, const optional<Tensor>& delta_bias, bool softplus) {
+  const char* name = "mamba_cpu::mamba_inner_fwd";
+  check_inner(name, xz, conv_w, x_proj_w, dt_proj_w, out_proj_w, A);
+  c10::DeviceGuard guard(xz.device());
+  const int64_t d = xz.size(1) / 2, R = dt_proj_w.size(1), N = A.size(1);
+  const Tensor x = xz.narrow(1, 0, d), z = xz.narrow(1, d, d);
+  const Tensor w2 = conv_w.reshape({d, -1}).contiguous();
+  const Tensor conv_out = std::get<0>(causal_conv1d_fwd(x, w2, f32c(conv_b), std::nullopt, false, true,
+                                                        std::nullopt));
+  const Tensor x_dbl = at::linear(conv_out.transpose(1, 2), x_proj_w);  // (b, l, R + 2N)
+  const Tensor delta = at::linear(x_dbl.narrow(-1, 0, R), dt_proj_w).transpose(1, 2);  // (b, d, l) view
+  const Tensor Bk = x_dbl.narrow(-1, R, N).unsqueeze(1), Ck = x_dbl.narrow(-1, R + N, N).unsqueeze(1);
+  auto r = scan_fwd_impl(name, conv_out, delta, A.contiguous(), Bk, Ck, f32c(D), opt(z),
+                         f32c(delta_bias), softplus, true);
+  const Tensor& y = std::get<0>(r);
+  const Tensor out = at::linear(y.transpose(1, 2), out_proj_w, f32c(out_proj_b));
+  return {out, conv_out, x_dbl, delta, std::get<2>(r), std::get<3>(r), y};
+}
+
+// Gradients (dxz, dconv_w, dconv_b, dx_proj_w, ddt_proj_w, dout_proj_w,
+// dout_proj_b, dA, dD, ddelta_bias); those of absent optional inputs are
+// empty tensors.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>
+mamba_inner_bwd(const Tensor& dout, const Tensor& xz, const Tensor& conv_w, const optional<Tensor>& conv_b,
+                const Tensor& x_proj_w, const Tensor& dt_proj_w, const Tensor& out_proj_w,
+                bool has_out_b, const Tensor& A, const optional<Tensor>& D,
+                const optional<Tensor>& delta_bias, bool softplus, const Tensor& conv_out,
+                const Tensor& x_dbl, const Tensor& delta, const Tensor& ckpt, const Tensor& ysave,
+                const Tensor& y) {
+  const char* name = "mamba_cpu::mamba_inner_bwd";
+  check_inner(name, xz, conv_w, x_proj_w, dt_proj_w, out_proj_w, A);
+  c10::DeviceGuard guard(xz.device());
+  const int64_t b = xz.size(0), d2 = xz.size(1), l = xz.size(2), d = d2 / 2;
+  const int64_t R = dt_proj_w.size(1), N = A.size(1);
+  const Tensor x = xz.narrow(1, 0, d), z = xz.narrow(1, d, d);
+  const Tensor w2 = conv_w.reshape({d, -1}).contiguous();
+  const Tensor g = dout.contiguous();
+  const Tensor g2 = g.reshape({-1, g.size(-1)});
+  // out_proj
+  const Tensor d_out_proj_w = g2.t().mm(y.transpose(1, 2).reshape({-1, d}));
+  const Tensor d_out_proj_b = has_out_b ? g2.sum(0) : at::empty({0}, g.options());
+  const Tensor dy = g.matmul(out_proj_w).transpose(1, 2);  // (b, d, l), channel-contiguous
+  // scan; dz goes straight into its half of the (b, l, 2d) input gradient
+  Tensor dxz = at::empty({b, l, d2}, xz.options());
+  const Tensor dz_view = dxz.narrow(2, d, d).transpose(1, 2);
+  const Tensor Bk = x_dbl.narrow(-1, R, N).unsqueeze(1), Ck = x_dbl.narrow(-1, R + N, N).unsqueeze(1);
+  Grads8 gs = scan_bwd_impl(name, conv_out, delta, A.contiguous(), Bk, Ck, f32c(D), opt(z),
+                            f32c(delta_bias), softplus, dy, std::nullopt, ckpt, ysave, &dz_view);
+  const Tensor& du = std::get<0>(gs);
+  const Tensor ddelta_bl = std::get<1>(gs).transpose(1, 2);  // (b, l, d)
+  // dt_proj: delta = dt_in @ dt_proj_w^T
+  const Tensor ddelta2 = ddelta_bl.reshape({-1, d});
+  const Tensor dt_in2 = x_dbl.narrow(-1, 0, R).reshape({-1, R});
+  const Tensor d_dt_proj_w = ddelta2.t().mm(dt_in2);
+  // x_proj output gradient (b * l, R + 2N): d_dt_in, dB, dC side by side
+  Tensor dx_dbl = at::empty({b * l, R + 2 * N}, xz.options());
+  Tensor d_dt_in = dx_dbl.narrow(1, 0, R);
+  at::mm_out(d_dt_in, ddelta2, dt_proj_w);
+  dx_dbl.narrow(1, R, N).copy_(std::get<3>(gs).select(1, 0).reshape({-1, N}));
+  dx_dbl.narrow(1, R + N, N).copy_(std::get<4>(gs).select(1, 0).reshape({-1, N}));
+  const Tensor conv2 = conv_out.transpose(1, 2).reshape({-1, d});
+  const Tensor d_x_proj_w = dx_dbl.t().mm(conv2);
+  const Tensor dconv = at::addmm(du.transpose(1, 2).reshape({-1, d}), dx_dbl, x_proj_w).view({b, l, d});
+  // conv; dx goes straight into its half of the input gradient
+  const Tensor dx_view = dxz.narrow(2, 0, d).transpose(1, 2);
+  auto cg = conv_bwd_impl(x, w2, f32c(conv_b), std::nullopt, dconv.transpose(1, 2), std::nullopt, true,
+                          std::nullopt, &dx_view);
+  return {dxz.transpose(1, 2), std::get<1>(cg).view(conv_w.sizes()), std::get<2>(cg), d_x_proj_w,
+          d_dt_proj_w, d_out_proj_w, d_out_proj_b, std::get<2>(gs), std::get<5>(gs), std::get<7>(gs)};
 }
 
 // ---- selective state update ---------------------------------------------------------
@@ -878,6 +994,14 @@ TORCH_LIBRARY(mamba_cpu, m) {
   m.def("selective_scan_cbwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
         "Tensor? z, Tensor? delta_bias, bool delta_softplus, Tensor dout, Tensor? dlast_state, "
         "Tensor? ckpt) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("mamba_inner_fwd(Tensor xz, Tensor conv1d_weight, Tensor? conv1d_bias, Tensor x_proj_weight, "
+        "Tensor delta_proj_weight, Tensor out_proj_weight, Tensor? out_proj_bias, Tensor A, Tensor? D, "
+        "Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("mamba_inner_bwd(Tensor dout, Tensor xz, Tensor conv1d_weight, Tensor? conv1d_bias, "
+        "Tensor x_proj_weight, Tensor delta_proj_weight, Tensor out_proj_weight, bool has_out_proj_bias, "
+        "Tensor A, Tensor? D, Tensor? delta_bias, bool delta_softplus, Tensor conv_out, Tensor x_dbl, "
+        "Tensor delta, Tensor ckpt, Tensor ysave, Tensor y) -> (Tensor, Tensor, Tensor, Tensor, Tensor, "
+        "Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("causal_conv1d_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
         "bool return_final_states, bool silu, Tensor? seq_idx=None) -> (Tensor, Tensor)");
   m.def("causal_conv1d_bwd(Tensor x, Tensor weight, Tensor? bias, Tensor? initial_states, "
@@ -898,6 +1022,8 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("selective_scan_bwd_ckpt", &selective_scan_bwd_ckpt);
   m.impl("selective_scan_cfwd", &selective_scan_cfwd);
   m.impl("selective_scan_cbwd", &selective_scan_cbwd);
+  m.impl("mamba_inner_fwd", &mamba_inner_fwd);
+  m.impl("mamba_inner_bwd", &mamba_inner_bwd);
   m.impl("causal_conv1d_fwd", &causal_conv1d_fwd);
   m.impl("causal_conv1d_bwd", &causal_conv1d_bwd);
   m.impl("causal_conv1d_update", &causal_conv1d_update);

@@ -24,7 +24,11 @@ unfused path instead makes contiguous copies for every GEMM and concatenates
 the input gradient through a transposing copy.
 
 The backward keeps the forward's scan checkpoints and pre-gate y
-(selective_scan_fwd_ckpt), so it does not recompute the states.
+(selective_scan_fwd_ckpt), so it does not recompute the states. Without the
+RMS norms (transformers' Mamba mixers) the forward and the backward are one
+C++ operator each, mamba_cpu::mamba_inner_fwd / mamba_inner_bwd, which issue
+the conv, scan and GEMM calls themselves; with them, MambaInnerFn composes
+the same operators from Python around the norms' autograd graph.
 """
 
 import torch
@@ -129,6 +133,65 @@ class MambaInnerFn(torch.autograd.Function):
                 None)
 
 
+def _like_channels(x):
+    """(batch, dim, seqlen) result laid out like the operators allocate it for
+    a channel-contiguous input view."""
+    b, d, l = x.shape
+    return torch.empty_strided((b, d, l), (d * l, 1, d), dtype=x.dtype, device=x.device)
+
+
+@torch.library.register_fake("mamba_cpu::mamba_inner_fwd")
+def _(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight, out_proj_bias,
+      A, D, delta_bias, delta_softplus):
+    b, d2, l = xz.shape
+    d, N, R = d2 // 2, A.shape[1], delta_proj_weight.shape[1]
+    x = xz[:, :d]
+    conv_out = _like_channels(x) if x.stride(1) == 1 and x.stride(2) != 1 else x.new_empty(x.shape)
+    return (xz.new_empty(b, l, out_proj_weight.shape[0]), conv_out, xz.new_empty(b, l, R + 2 * N),
+            xz.new_empty(b, l, d).transpose(1, 2), xz.new_empty(b, d, (l + 15) // 16, N),
+            xz.new_empty(b, d, l),
+            torch.empty_strided(conv_out.shape, conv_out.stride(), dtype=xz.dtype, device=xz.device))
+
+
+@torch.library.register_fake("mamba_cpu::mamba_inner_bwd")
+def _(dout, xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+      has_out_proj_bias, A, D, delta_bias, delta_softplus, conv_out, x_dbl, delta, ckpt, ysave, y):
+    b, d2, l = xz.shape
+    d = d2 // 2
+    f = A.new_empty
+    return (xz.new_empty(b, l, d2).transpose(1, 2), f(conv1d_weight.shape),
+            f(d) if conv1d_bias is not None else f(0), f(x_proj_weight.shape), f(delta_proj_weight.shape),
+            f(out_proj_weight.shape), f(out_proj_weight.shape[0]) if has_out_proj_bias else f(0), f(A.shape),
+            f(d), f(d))
+
+
+class MambaInnerOpsFn(torch.autograd.Function):
+    """mamba_inner_fn without the RMS norms: one C++ operator for the forward
+    (conv, x_proj, dt_proj, scan, out_proj) and one for the backward, so a
+    training step makes one Python call each way per layer."""
+
+    @staticmethod
+    def forward(ctx, xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, out_proj_b, A, D, delta_bias,
+                softplus):
+        out, conv_out, x_dbl, delta, ckpt, ysave, y = _ops.mamba_inner_fwd(
+            xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, out_proj_b, A, D, delta_bias, softplus)
+        ctx.save_for_backward(xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, A, D, delta_bias,
+                              conv_out, x_dbl, delta, ckpt, ysave, y)
+        ctx.softplus, ctx.has_out_b = softplus, out_proj_b is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, A, D, delta_bias, conv_out, x_dbl, delta,
+         ckpt, ysave, y) = ctx.saved_tensors
+        dxz, dcw, dcb, dxp, ddtp, dop, dopb, dA, dD, ddb = _ops.mamba_inner_bwd(
+            dout, xz, conv_w, conv_b, x_proj_w, dt_proj_w, out_proj_w, ctx.has_out_b, A, D, delta_bias,
+            ctx.softplus, conv_out, x_dbl, delta, ckpt, ysave, y)
+        return (dxz, dcw, dcb if conv_b is not None else None, dxp, ddtp, dop,
+                dopb if ctx.has_out_b else None, dA, dD if D is not None else None,
+                ddb if delta_bias is not None else None, None)
+
+
 def fused_path_supported(xz, conv1d_weight, x_proj_weight, delta_proj_weight, out_proj_weight, A, B, C):
     """The shapes and dtypes the fused path runs: float32 xz and weights on a
     ROCm GPU, input-dependent B/C (B = C = None), a real A."""
@@ -167,6 +230,10 @@ def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
     if any(w is not None for w in norms) and not all(w is not None for w in norms):
         raise ValueError("mamba_inner_fn: b_rms_weight, c_rms_weight and dt_rms_weight go together")
     f32 = lambda t: None if t is None else t.float()  # noqa: E731
+    if dt_rms_weight is None:
+        return MambaInnerOpsFn.apply(xz, conv1d_weight, f32(conv1d_bias), x_proj_weight, delta_proj_weight,
+                                     out_proj_weight, f32(out_proj_bias), A.float().contiguous(), f32(D),
+                                     f32(delta_bias), bool(delta_softplus))
     return MambaInnerFn.apply(xz, conv1d_weight, f32(conv1d_bias), x_proj_weight, delta_proj_weight,
                               out_proj_weight, f32(out_proj_bias), A.float().contiguous(), f32(D),
                               f32(delta_bias), bool(delta_softplus), b_rms_weight, c_rms_weight,

@@ -98,3 +98,17 @@ def test_rejects_input_independent_bc():
     with pytest.raises(NotImplementedError):
         mamba_inner_fn(g["xz"], g["conv_w"], g["conv_b"], g["x_proj_w"], g["dt_proj_w"], g["out_proj_w"],
                        g["out_proj_b"], g["A"], torch.zeros(8, 4, device=DEV), None, g["D"])
+
+
+def test_opcheck_inner_ops():
+    """Schemas and shape functions of the two C++ operators behind the
+    norm-free mixer."""
+    p, _ = make(2, 16, 20, 4, 3, 12, 4, False, True, seed=5)
+    t = {k: v.float().to(DEV) for k, v in p.items()}
+    args = (t["xz"], t["conv_w"], t["conv_b"], t["x_proj_w"], t["dt_proj_w"], t["out_proj_w"], t["out_proj_b"],
+            t["A"], t["D"], t["delta_bias"], True)
+    torch.library.opcheck(torch.ops.mamba_cpu.mamba_inner_fwd.default, args)
+    res = torch.ops.mamba_cpu.mamba_inner_fwd(*args)
+    bargs = ((torch.randn_like(res[0]), t["xz"], t["conv_w"], t["conv_b"], t["x_proj_w"], t["dt_proj_w"],
+              t["out_proj_w"], True, t["A"], t["D"], t["delta_bias"], True) + tuple(res[1:]))
+    torch.library.opcheck(torch.ops.mamba_cpu.mamba_inner_bwd.default, bargs)
