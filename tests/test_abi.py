@@ -152,6 +152,25 @@ def test_scan_sizes():
         ctypes.byref(_scan_args(batch=1, dim=64, seqlen=4096))) > 0
 
 
+def test_complex_scan_sizes_and_limits():
+    """complex_a: checkpoints hold (re, im) pairs, the forward uses no
+    workspace, dstate is at most 32, and the imaginary part of the last B/C
+    element counts in the 32-bit offset check."""
+    from mamba_cpu import _C
+
+    L = _C.lib
+    a = _scan_args(seqlen=33, complex_a=1)
+    a.B_stride[:] = a.C_stride[:] = (32 * 16 * 2, 32 * 16 * 2, 2, 2 * 33)
+    assert L.mcpu_selective_scan_ckpt_size(ctypes.byref(a)) == 2 * 4 * 2 * 8 * 3 * 16
+    assert L.mcpu_selective_scan_fwd_workspace_size(
+        ctypes.byref(_scan_args(batch=1, dim=64, seqlen=4096, complex_a=1))) == 0
+    assert L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a)) > \
+        L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(seqlen=33)))
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=33, complex_a=1)), None, 0, None)
+    assert rc == _C.MCPU_ERR_UNSUPPORTED and "complex" in msg
+    assert L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(dstate=33, complex_a=1))) == 0
+
+
 def test_scan_without_gfx950_reports_the_device():
     """Valid arguments on a machine without a gfx950 device: a device error, no launch."""
     from mamba_cpu import _C

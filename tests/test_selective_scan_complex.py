@@ -194,3 +194,25 @@ def test_opcheck_complex_ops():
     dlast = torch.complex(torch.randn(2, 4, 2), torch.randn(2, 4, 2)).to(DEV)
     bwd_args = fwd_args + (torch.randn(2, 4, 8, device=DEV), dlast, ckpt)
     torch.library.opcheck(torch.ops.mamba_cpu.selective_scan_cbwd.default, bwd_args)
+
+
+def test_complex_channel_contiguous_inputs():
+    """u, delta and z as channel-contiguous views (Hugging Face's transposed
+    projections): same results as the oracle, the output and du / ddelta /
+    dz keep that layout."""
+    inp = make_cinputs(2, 32, 45, 8, None, True, True, True, seed=11)
+    cc = {k: (v.transpose(1, 2).contiguous().transpose(1, 2) if k in ("u", "delta", "z") else v.clone())
+          for k, v in inp.items()}
+    for v in cc.values():
+        v.requires_grad_()
+    out = selective_scan_fn(**cc, delta_softplus=True)
+    want, _ = O.selective_scan_fwd_complex(**inp, delta_softplus=True)
+    close(out, want, 1e-4, 2e-5, "out")
+    assert out.stride(1) == 1
+    W = torch.randn(2, 32, 45, generator=torch.Generator().manual_seed(12)).to(DEV)
+    (out * W).sum().backward()
+    wants = O.selective_scan_bwd_complex(**inp, delta_softplus=True, dout=W)
+    for k, w in zip(["u", "delta", "A", "B", "C", "D", "z", "delta_bias"], wants):
+        scale = max(np.abs(w).max(), 1.0)
+        close(cc[k].grad / scale, w / scale, 1e-3, 1e-4, k)
+    assert cc["u"].grad.stride(1) == 1 and cc["z"].grad.stride(1) == 1
