@@ -200,6 +200,33 @@ def fused_path_supported(xz, conv1d_weight, x_proj_weight, delta_proj_weight, ou
             all(t.dtype == torch.float32 and t.device.type == "cuda" for t in tensors))
 
 
+def _mamba_inner_complex(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                         out_proj_weight, out_proj_bias, A, D, delta_bias, delta_softplus):
+    """mamba_inner_fn with complex A, composed from this package's ops (autograd
+    through them): mamba_ssm's layout, where x_proj's output holds dt_rank
+    columns, then B and C as 2 dstate columns each, the (re, im) pairs of each
+    state side by side ("(b l) (dstate two) -> b 1 dstate (l two)")."""
+    from mamba_cpu.ops.causal_conv1d import causal_conv1d_fn
+    from mamba_cpu.ops.selective_scan_interface import selective_scan_fn
+
+    b, d2, l = xz.shape
+    d, R, N = d2 // 2, delta_proj_weight.shape[1], A.shape[1]
+    if x_proj_weight.shape[0] != R + 4 * N:
+        raise ValueError(f"with complex A, x_proj_weight has dt_rank + 4 dstate = {R + 4 * N} rows, "
+                         f"got {x_proj_weight.shape[0]}")
+    x, z = xz[:, :d], xz[:, d:]
+    conv = causal_conv1d_fn(x, conv1d_weight.reshape(d, -1), conv1d_bias, activation="silu")
+    x_dbl = F.linear(conv.transpose(1, 2), x_proj_weight)  # (b, l, R + 4N)
+    dt_in, Bp, Cp = x_dbl.split([R, 2 * N, 2 * N], dim=-1)
+    delta = F.linear(dt_in, delta_proj_weight).transpose(1, 2)
+
+    def pairs(X):  # (b, l, N * 2) -> (b, N, l * 2)
+        return X.unflatten(-1, (N, 2)).permute(0, 2, 1, 3).reshape(b, N, 2 * l)
+
+    y = selective_scan_fn(conv, delta, A, pairs(Bp), pairs(Cp), D, z, delta_bias, delta_softplus)
+    return F.linear(y.transpose(1, 2), out_proj_weight, out_proj_bias)
+
+
 def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                    out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
                    B_proj_bias=None, C_proj_bias=None, delta_softplus=True, checkpoint_lvl=1,
@@ -211,7 +238,9 @@ def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
     xz: (batch, 2 dim, seqlen) float32 (any strides; transformers passes the
     transposed view of in_proj's output). conv1d_weight: (dim, 1, width) or
     (dim, width). x_proj_weight: (dt_rank + 2 dstate, dim). delta_proj_weight:
-    (dim, dt_rank). out_proj_weight: (d_model, dim). A: (dim, dstate) real.
+    (dim, dt_rank). out_proj_weight: (d_model, dim). A: (dim, dstate) real,
+    or complex (mamba_ssm's layout: x_proj_weight then has dt_rank + 4 dstate
+    rows, B and C as (re, im) pairs; composed from the ops, no RMS norms).
     D, delta_bias: (dim,). b_rms_weight / c_rms_weight (dstate,) and
     dt_rms_weight (dim,): RMS norms on B, C and delta, all or none.
 
@@ -222,7 +251,10 @@ def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
     if B is not None or C is not None or B_proj_bias is not None or C_proj_bias is not None:
         raise NotImplementedError("mamba_inner_fn: input-independent B/C are not supported")
     if A.is_complex():
-        raise NotImplementedError("complex A is not supported yet")
+        if dt_rms_weight is not None or b_rms_weight is not None or c_rms_weight is not None:
+            raise NotImplementedError("mamba_inner_fn: RMS norms with complex A are not supported")
+        return _mamba_inner_complex(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                                    out_proj_weight, out_proj_bias, A, D, delta_bias, bool(delta_softplus))
     if not fused_path_supported(xz, conv1d_weight, x_proj_weight, delta_proj_weight, out_proj_weight,
                                 A, B, C):
         raise NotImplementedError("mamba_inner_fn runs float32 tensors on a ROCm GPU")

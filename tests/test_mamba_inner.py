@@ -112,3 +112,48 @@ def test_opcheck_inner_ops():
     bargs = ((torch.randn_like(res[0]), t["xz"], t["conv_w"], t["conv_b"], t["x_proj_w"], t["dt_proj_w"],
               t["out_proj_w"], True, t["A"], t["D"], t["delta_bias"], True) + tuple(res[1:]))
     torch.library.opcheck(torch.ops.mamba_cpu.mamba_inner_bwd.default, bargs)
+
+
+def test_complex_a_mixer_matches_reference():
+    """Complex A through mamba_inner_fn (mamba_ssm's layout: B and C as 2 dstate
+    columns of (re, im) pairs each) against the same mixer in float64 on the
+    CPU, with the scan as the closed-form direct sum that tests/test_oracle.py
+    pins the complex oracle with. Output and every gradient."""
+    from test_oracle import _complex_direct_sum
+
+    b, d, l, N, R, Dm, W = 2, 16, 12, 4, 3, 10, 4
+    g = torch.Generator().manual_seed(21)
+    r = lambda *s, sc=1.0: torch.randn(*s, generator=g, dtype=torch.float64) * sc  # noqa: E731
+    p = dict(xz=r(b, l, 2 * d).transpose(1, 2), conv_w=r(d, 1, W, sc=0.5), conv_b=r(d, sc=0.3),
+             x_proj_w=r(R + 4 * N, d, sc=d ** -0.5), dt_proj_w=r(d, R, sc=R ** -0.5),
+             out_proj_w=r(Dm, d, sc=d ** -0.5),
+             A=torch.complex(-torch.exp(torch.rand(d, N, generator=g, dtype=torch.float64)), r(d, N)),
+             D=r(d), delta_bias=torch.rand(d, generator=g, dtype=torch.float64) - 3)
+    G = r(b, l, Dm)
+
+    def pairs(X):
+        return X.unflatten(-1, (N, 2)).permute(0, 2, 1, 3).reshape(b, N, 2 * l)
+
+    ref = {k: v.clone().requires_grad_() for k, v in p.items()}
+    x, z = ref["xz"][:, :d], ref["xz"][:, d:]
+    conv = causal_conv1d_ref(x, ref["conv_w"].reshape(d, -1), ref["conv_b"], activation="silu")
+    dt, Bp, Cp = F.linear(conv.transpose(1, 2), ref["x_proj_w"]).split([R, 2 * N, 2 * N], -1)
+    delta = F.linear(dt, ref["dt_proj_w"]).transpose(1, 2)
+    y, _ = _complex_direct_sum(conv, delta, ref["A"], pairs(Bp), pairs(Cp), ref["D"], z, ref["delta_bias"], True)
+    want = F.linear(y.transpose(1, 2), ref["out_proj_w"])
+    (want * G).sum().backward()
+
+    gpu = {k: (v.to(torch.complex64) if v.is_complex() else v.float()).to(DEV).requires_grad_()
+           for k, v in p.items()}
+    out = mamba_inner_fn(gpu["xz"], gpu["conv_w"], gpu["conv_b"], gpu["x_proj_w"], gpu["dt_proj_w"],
+                         gpu["out_proj_w"], None, gpu["A"], None, None, gpu["D"], gpu["delta_bias"],
+                         delta_softplus=True)
+    np.testing.assert_allclose(out.detach().cpu().double().numpy(), want.detach().numpy(), rtol=1e-4, atol=1e-5)
+    (out * G.float().to(DEV)).sum().backward()
+    for k in p:
+        got, w = gpu[k].grad.cpu(), ref[k].grad
+        if w.is_complex():
+            got, w = torch.view_as_real(got.to(torch.complex128)), torch.view_as_real(w)
+        scale = max(w.abs().max().item(), 1.0)
+        np.testing.assert_allclose(got.double().numpy() / scale, w.numpy() / scale, rtol=1e-3, atol=1e-4,
+                                   err_msg=k)
