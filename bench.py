@@ -307,6 +307,28 @@ def other_configs(torch, dev, stream, cpu):
         res[f"conv_fwdbwd_b8_d3072_l2048_{tag}"] = r
         del x, go
 
+    # Packed sequences (seq_idx), the layout upstream causal_conv1d requires
+    # for them: x channel-contiguous, (batch, seqlen, dim) in memory, each row
+    # eight sequences of ragged lengths. Timed beside the same layout without
+    # seq_idx, so the cost of the per-tap sequence mask shows. The reference
+    # rejects seq_idx, so there is no CPU leg.
+    x = torch.randn(b, l, d, generator=g, device=dev).transpose(1, 2).requires_grad_()
+    go = torch.randn(b, l, d, generator=g, device=dev).transpose(1, 2)
+    cuts = torch.sort(torch.randint(1, l, (b, 7), generator=g, device=dev), dim=1).values
+    seq = (torch.arange(l, device=dev)[None, :, None] >= cuts[:, None, :]).sum(-1).to(torch.int32)
+
+    def packed_step(si):
+        out = causal_conv1d_fn(x, wt, bias, seq_idx=si, activation="silu")
+        return torch.autograd.grad(out, [x, wt, bias], go)
+
+    nbytes = 5 * b * d * l * 4 + 2 * b * l * 4 + 4 * 3 * (d * w + d)
+    r = _rate(nbytes, _events_ms(torch, stream, lambda: packed_step(seq), 20))
+    r["workload"] = ("causal_conv1d_fn forward+backward with seq_idx, fp32, batch 8, dim 3072, "
+                     "seqlen 2048, width 4, silu, channel-contiguous x, 8 packed sequences per row")
+    r["same_layout_without_seq_idx_ms"] = round(_events_ms(torch, stream, lambda: packed_step(None), 20), 4)
+    res["conv_fwdbwd_seqidx_b8_d3072_l2048_f32"] = r
+    del x, go, seq
+
     # Decode-time conv update: state (64, 3072, 3), 256 single-token steps.
     b, d, w = 64, 3072, 4
     state = torch.randn(b, d, w - 1, generator=g, device=dev)
@@ -362,6 +384,29 @@ def other_configs(torch, dev, stream, cpu):
         _attach_cpu(r, cms, "256 steps through the reference's ATen update path "
                             "(ops/causal_conv1d.py:56-85), 1 warm-up + 1 timed pass")
     res["conv_update_b64_d3072"] = r
+
+    # The same update through the decode indexers the reference rejects: a
+    # pool of 128 ring-buffer states of length 8 (cache_seqlens), of which the
+    # 64 batch rows use every other one (conv_state_indices). 256 steps, the
+    # sequence positions advancing by one per step.
+    pool = torch.randn(2 * b, d, 8, generator=g, device=dev)
+    rows = torch.arange(0, 2 * b, 2, device=dev, dtype=torch.int32)
+    pos = [torch.full((b,), 5 + i, device=dev, dtype=torch.int32) for i in range(256)]
+
+    def upd_ring():
+        for i in range(256):
+            causal_conv1d_update(xs[i], pool, wt, bias, activation="silu",
+                                 cache_seqlens=pos[i], conv_state_indices=rows)
+
+    ms = _events_ms(torch, stream, upd_ring, 3) / 256
+    # Per step: x, the width-1 taps read and one tap written per row, the
+    # out, the two index vectors, weight and bias.
+    nbytes = (b * d + b * d * (w - 1) + b * d + b * d) * 4 + 2 * b * 4 + 4 * (d * w + d)
+    r = _rate(nbytes, ms)
+    r["workload"] = ("causal_conv1d_update with cache_seqlens and conv_state_indices, fp32, pool "
+                     "(128, 3072, 8) of ring buffers, x (64, 3072), silu; per step of 256")
+    res["conv_update_ring_indexed_b64_d3072"] = r
+    del pool, pos
 
     # Selective state update, Mamba-130M layer shape: state (4, 1536, 16).
     b, d, n = 4, 1536, 16

@@ -93,10 +93,45 @@ int vt_ok(const ConvParams& p, int dtype, bool bwd) {
   return ok ? steps : 0;
 }
 
+// Launch shape of the channel-contiguous fast path: time segments of 64, 32,
+// 16 or 8 steps per wave, the longest that still gives 8192 waves (or 8).
+void conv_cl_shape(ConvParams& p) {
+  const int64_t tiles = p.batch * ((p.dim + 255) / 256);
+  int ng = 8;
+  while (ng > 1 && tiles * ((p.seqlen + kConvClG * ng - 1) / (kConvClG * ng)) < 8192) ng /= 2;
+  p.cl_ng = ng;
+  const int64_t nseg = (p.seqlen + kConvClG * ng - 1) / (kConvClG * ng);
+  p.cl_gy = (nseg + 3) / 4;
+}
+
+// A (batch, dim, seqlen) operand the channel-contiguous path can move in
+// four-channel vectors: unit channel stride, batch and time strides on
+// 4-element boundaries, an aligned base.
+bool cl_operand(const void* ptr, const int64_t (&s)[3], int dtype) {
+  const uintptr_t align = dtype == MCPU_F32 ? 16 : 8;
+  return ptr != nullptr && s[1] == 1 && s[0] % 4 == 0 && s[2] % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(ptr) % align == 0;
+}
+
+// Whether the channel-contiguous path applies (after conv_cl_shape): widths
+// 2..5, whole four-channel vectors, no initial states (forward) and no
+// initial- or final-state gradients (backward); seq_idx is allowed.
+bool cl_ok(const ConvParams& p, int dtype, bool bwd) {
+  if (p.width < 2 || p.width > 5 || p.dim % 4 != 0 || p.seqlen < 1) return false;
+  if (!p.channels_last || p.batch > 65535 || p.cl_gy > 65535) return false;
+  if (!cl_operand(p.x, p.sx, dtype)) return false;
+  if (bwd)
+    return p.dinit == nullptr && p.dfinal == nullptr && cl_operand(p.dout, p.sdo, dtype) &&
+           cl_operand(p.dx, p.sdx, dtype);
+  return p.init == nullptr && cl_operand(p.out, p.sout, dtype);
+}
+
 size_t conv_ws(const ConvParams& p) {
   ConvParams q = p;
   conv_vt_shape(q, kConvVTSteps);  // the fewest steps per thread: the most segments
-  const int64_t parts = q.nseg > p.R ? q.nseg : p.R;
+  conv_cl_shape(q);
+  int64_t parts = q.nseg > p.R ? q.nseg : p.R;
+  if (q.cl_gy > parts) parts = q.cl_gy;
   return align_up(sizeof(float) * p.batch * parts * p.dim * (p.width + 1));
 }
 
@@ -115,6 +150,8 @@ extern "C" int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream) {
   p.final_states = a->final_states;
   p.vt = vt_ok(p, a->dtype, false);
   if (p.vt) conv_vt_shape(p, p.vt);
+  conv_cl_shape(p);
+  p.cl = !p.vt && cl_ok(p, a->dtype, false);
   return hip_status(conv_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)),
                     "causal_conv1d_fwd launch");
 }
@@ -148,6 +185,8 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
   p.dw_part = static_cast<float*>(workspace);
   p.vt = vt_ok(p, a->dtype, true);
   if (p.vt) conv_vt_shape(p, p.vt);
+  conv_cl_shape(p);
+  p.cl = !p.vt && cl_ok(p, a->dtype, true);
   if (a->batch == 0 || a->dim == 0) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (int rc = zero_f32(a->dweight, a->dim * a->width, st)) return rc;

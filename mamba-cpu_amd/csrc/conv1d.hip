@@ -392,6 +392,12 @@ __device__ __forceinline__ void st4(void* base, int64_t idx, const float* v) {
   }
 }
 
+struct ConvClTile {
+  int64_t b, d0, t0, S;  // batch row, first of the lane's 4 channels, segment start and length
+  bool wave_on;          // the wave's segment starts inside the sequence
+  bool active;           // ... and the lane's channels exist
+};
+
 struct ConvTile {
   ConvRow c;      // (batch, channel) of the row
   int64_t t0;     // first step of this thread
@@ -566,6 +572,327 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Channel-contiguous fast path: x (and out, or dout and dx) with unit channel
+// stride, as Hugging Face's transposed (batch, seqlen, dim) views and the
+// fused mixer's halves of xz are. A lane owns four neighbouring channels and
+// moves them as one 16-byte (fp32) or 8-byte (16-bit) vector per step; a wave
+// covers 256 channels of one batch row over one time segment of
+// kConvClG * cl_ng steps, so the step index and the packed-sequence ids are
+// wave-uniform. Each lane walks its segment with a rolling window of the last
+// W inputs (and, backward, the last W output gradients) in registers; the W-1
+// inputs before the segment, and backward the W-1 steps after it, are re-read
+// from the neighbouring segments. A workgroup is four waves: four consecutive
+// segments of the same 256 channels (grid: channel tiles, segment groups,
+// batch). Packed sequences cost only where a segment holds a boundary: a wave
+// vote over its ids picks the masked body for those segments alone.
+
+__device__ __forceinline__ ConvClTile conv_cl_tile(const ConvParams& p) {
+  ConvClTile g;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  g.S = static_cast<int64_t>(p.cl_ng) * kConvClG;
+  g.b = blockIdx.z;
+  g.t0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * g.S;
+  g.d0 = (static_cast<int64_t>(blockIdx.x) * 64 + (threadIdx.x & 63)) * 4;
+  g.wave_on = g.t0 < p.seqlen;
+  g.active = g.wave_on && g.d0 < p.dim;
+  return g;
+}
+
+// Sequence id of step s of row b, s clamped to the sequence: positions
+// outside it read zeros (seq_idx excludes initial states), so any id serves.
+__device__ __forceinline__ int32_t conv_cl_id(const ConvParams& p, int64_t b, int64_t s) {
+  s = s < 0 ? 0 : (s >= p.seqlen ? p.seqlen - 1 : s);
+  return __builtin_amdgcn_readfirstlane(p.seq_idx[b * p.seqlen + s]);
+}
+
+// Whether the ids over steps [lo, hi] (hi - lo < 128) are not all equal.
+// Wave-uniform; every lane of the wave must be active.
+__device__ __forceinline__ bool conv_cl_breaks(const ConvParams& p, int64_t b, int64_t lo, int64_t hi) {
+  const int lane = threadIdx.x & 63;
+  const int32_t first = conv_cl_id(p, b, lo);
+  const int32_t* ids = p.seq_idx + b * p.seqlen;
+  auto at = [&](int64_t s) { return ids[s < 0 ? 0 : (s >= p.seqlen ? p.seqlen - 1 : s)]; };
+  const bool d1 = lo + lane <= hi && at(lo + lane) != first;
+  const bool d2 = lo + 64 + lane <= hi && at(lo + 64 + lane) != first;
+  return __ballot(d1 || d2) != 0;
+}
+
+// M: mask the taps by sequence id. TAIL: the segment runs past the sequence
+// end (steps there load nothing and store nothing).
+template <typename T, int W, bool M, bool TAIL>
+__device__ __forceinline__ void conv_fwd_cl_body(const ConvParams& p, const ConvClTile& g,
+                                                 const float (&w)[4][W], const float (&bias)[4]) {
+  const int64_t L = p.seqlen;
+  const int64_t xb = g.b * p.sx[0] + g.d0, ob = g.b * p.sout[0] + g.d0;
+  float xw[W][4];  // X[t-(W-1) .. t], four channels each
+  int32_t iw[W];   // their sequence ids (M)
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) {
+    const int64_t s = g.t0 - (W - 1) + j;
+    if (s >= 0) {
+      ld4<T>(p.x, xb + s * p.sx[2], xw[j]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xw[j][c] = 0.f;
+    }
+    if constexpr (M) iw[j] = conv_cl_id(p, g.b, s);
+  }
+  // Unrolled groups of G steps; the masked body (segments with a sequence
+  // boundary) unrolls less, so the register budget it sets for the kernel
+  // stays near the unmasked body's.
+  constexpr int G = M ? 2 : kConvClG;
+  for (int64_t tg = g.t0; tg < g.t0 + g.S; tg += G) {
+    if (TAIL && tg >= L) break;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int64_t t = tg + i;
+      const bool in = !TAIL || t < L;
+      if (in) {
+        ld4<T>(p.x, xb + t * p.sx[2], xw[W - 1]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xw[W - 1][c] = 0.f;
+      }
+      if constexpr (M) iw[W - 1] = conv_cl_id(p, g.b, t);
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float acc = bias[c];
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          float xk = xw[k][c];
+          if constexpr (M) xk = iw[k] == iw[W - 1] ? xk : 0.f;
+          acc = fmaf(w[c][k], xk, acc);
+        }
+        o[c] = p.silu ? acc * sigmoid(acc) : acc;
+      }
+      if (in) st4<T>(p.out, ob + t * p.sout[2], o);
+#pragma unroll
+      for (int k = 0; k < W - 1; ++k) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xw[k][c] = xw[k + 1][c];
+        if constexpr (M) iw[k] = iw[k + 1];
+      }
+    }
+  }
+}
+
+template <typename T, int W, bool SEQ>
+__global__ void __launch_bounds__(256) conv_fwd_cl_kernel(const ConvParams p) {
+  const ConvClTile g = conv_cl_tile(p);
+  if (!g.wave_on) return;
+  bool masked = false;
+  if constexpr (SEQ) masked = conv_cl_breaks(p, g.b, g.t0 - (W - 1), g.t0 + g.S - 1);
+  if (!g.active) return;
+  float w[4][W], bias[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[c][k] = p.w[(g.d0 + c) * W + k];
+    bias[c] = p.bias ? p.bias[g.d0 + c] : 0.f;
+  }
+  const bool tail = g.t0 + g.S > p.seqlen;
+  if (SEQ && masked) {
+    if (tail) conv_fwd_cl_body<T, W, SEQ, true>(p, g, w, bias);
+    else conv_fwd_cl_body<T, W, SEQ, false>(p, g, w, bias);
+  } else {
+    if (tail) conv_fwd_cl_body<T, W, false, true>(p, g, w, bias);
+    else conv_fwd_cl_body<T, W, false, false>(p, g, w, bias);
+  }
+}
+
+// One step t of the backward walk. OWN: t is one of the segment's steps (its
+// dweight/dbias terms are this segment's); otherwise it is one of the W-1
+// look-ahead steps past the segment. dx is emitted for s = t - (W-1) once s
+// is inside the segment.
+template <typename T, int W, bool M, bool TAIL, bool OWN>
+__device__ __forceinline__ void conv_bwd_cl_step(const ConvParams& p, const ConvClTile& g, int64_t t,
+                                                 const float (&w)[4][W], const float (&bias)[4],
+                                                 float (&xw)[W][4], float (&dpw)[W][4], int32_t (&iw)[W],
+                                                 float (&dw)[4][W], float (&db)[4]) {
+  const int64_t L = p.seqlen;
+  const bool in = !TAIL || t < L;
+  float go[4];
+  if (in) {
+    ld4<T>(p.x, g.b * p.sx[0] + g.d0 + t * p.sx[2], xw[W - 1]);
+    ld4<T>(p.dout, g.b * p.sdo[0] + g.d0 + t * p.sdo[2], go);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xw[W - 1][c] = go[c] = 0.f;
+  }
+  if constexpr (M) iw[W - 1] = conv_cl_id(p, g.b, t);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float xm[W];
+    float pre = bias[c];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      xm[k] = xw[k][c];
+      if constexpr (M) xm[k] = iw[k] == iw[W - 1] ? xm[k] : 0.f;
+      pre = fmaf(w[c][k], xm[k], pre);
+    }
+    float v = go[c];
+    if (p.silu) {
+      const float sg = sigmoid(pre);
+      v *= sg * (1.f + pre * (1.f - sg));
+    }
+    dpw[W - 1][c] = v;
+    if constexpr (OWN) {
+      db[c] += v;
+#pragma unroll
+      for (int k = 0; k < W; ++k) dw[c][k] = fmaf(v, xm[k], dw[c][k]);
+    }
+  }
+  // dx[s] = sum_k w[k] dpre[s + (W-1) - k], the tap of output s + (W-1) - k
+  // that reads input s; dpre[s + (W-1) - k] sits in dpw[W-1-k].
+  const int64_t s = t - (W - 1);
+  if (s >= g.t0 && (!TAIL || s < L)) {
+    float dx[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        float d = dpw[W - 1 - k][c];
+        if constexpr (M) d = iw[0] == iw[W - 1 - k] ? d : 0.f;
+        acc = fmaf(w[c][k], d, acc);
+      }
+      dx[c] = acc;
+    }
+    st4<T>(p.dx, g.b * p.sdx[0] + g.d0 + s * p.sdx[2], dx);
+  }
+#pragma unroll
+  for (int k = 0; k < W - 1; ++k) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      xw[k][c] = xw[k + 1][c];
+      dpw[k][c] = dpw[k + 1][c];
+    }
+    if constexpr (M) iw[k] = iw[k + 1];
+  }
+}
+
+template <typename T, int W, bool M, bool TAIL>
+__device__ __forceinline__ void conv_bwd_cl_body(const ConvParams& p, const ConvClTile& g,
+                                                 const float (&w)[4][W], const float (&bias)[4],
+                                                 float (&dw)[4][W], float (&db)[4]) {
+  float xw[W][4], dpw[W][4];
+  int32_t iw[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xw[j][c] = dpw[j][c] = 0.f;
+    iw[j] = 0;
+  }
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) {
+    const int64_t s = g.t0 - (W - 1) + j;
+    if (s >= 0) ld4<T>(p.x, g.b * p.sx[0] + g.d0 + s * p.sx[2], xw[j]);
+    if constexpr (M) iw[j] = conv_cl_id(p, g.b, s);
+  }
+  // The segment's own steps, in unrolled groups of G (as in the forward); a
+  // tail segment stops after the group holding the sequence's last step.
+  constexpr int G = M ? 2 : kConvClG;
+  const int64_t own_end = TAIL && p.seqlen < g.t0 + g.S ? p.seqlen : g.t0 + g.S;
+  int64_t tg = g.t0;
+  for (; tg < own_end; tg += G) {
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      conv_bwd_cl_step<T, W, M, TAIL, true>(p, g, tg + i, w, bias, xw, dpw, iw, dw, db);
+  }
+  // W-1 more steps right after the last one walked (the windows roll one
+  // step per call), for the dx of the segment's last W-1 steps.
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i)
+    conv_bwd_cl_step<T, W, M, TAIL, false>(p, g, tg + i, w, bias, xw, dpw, iw, dw, db);
+}
+
+template <typename T, int W, bool SEQ>
+__global__ void __launch_bounds__(256) conv_bwd_cl_kernel(const ConvParams p) {
+  __shared__ float s_part[4][W + 1][256];
+  const ConvClTile g = conv_cl_tile(p);
+  float dw[4][W], db[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    db[c] = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) dw[c][k] = 0.f;
+  }
+  if (g.wave_on) {
+    bool masked = false;
+    if constexpr (SEQ) masked = conv_cl_breaks(p, g.b, g.t0 - (W - 1), g.t0 + g.S + W - 2);
+    if (g.active) {
+      float w[4][W], bias[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int k = 0; k < W; ++k) w[c][k] = p.w[(g.d0 + c) * W + k];
+        bias[c] = p.bias ? p.bias[g.d0 + c] : 0.f;
+      }
+      const bool tail = g.t0 + g.S + (W - 1) > p.seqlen;
+      if (SEQ && masked) {
+        if (tail) conv_bwd_cl_body<T, W, SEQ, true>(p, g, w, bias, dw, db);
+        else conv_bwd_cl_body<T, W, SEQ, false>(p, g, w, bias, dw, db);
+      } else {
+        if (tail) conv_bwd_cl_body<T, W, false, true>(p, g, w, bias, dw, db);
+        else conv_bwd_cl_body<T, W, false, false>(p, g, w, bias, dw, db);
+      }
+    }
+  }
+  // The workgroup's four segments summed in order: one partial per
+  // (batch, segment group, channel).
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) s_part[wave][k][lane * 4 + c] = dw[c][k];
+    s_part[wave][W][lane * 4 + c] = db[c];
+  }
+  __syncthreads();
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (d < p.dim) {
+    float* part = p.dw_part + ((g.b * p.cl_gy + blockIdx.y) * p.dim + d) * (W + 1);
+#pragma unroll
+    for (int k = 0; k <= W; ++k)
+      part[k] = (s_part[0][k][threadIdx.x] + s_part[1][k][threadIdx.x]) +
+                (s_part[2][k][threadIdx.x] + s_part[3][k][threadIdx.x]);
+  }
+}
+
+template <typename T, bool SEQ>
+static hipError_t launch_cl_seq(const ConvParams& p, bool bwd, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((p.dim + 255) / 256), static_cast<unsigned>(p.cl_gy),
+                  static_cast<unsigned>(p.batch));
+  switch (p.width) {
+#define MCPU_CONV_CL(WW)                                                                         \
+  case WW:                                                                                       \
+    if (bwd) hipLaunchKernelGGL((conv_bwd_cl_kernel<T, WW, SEQ>), grid, dim3(256), 0, st, p);   \
+    else hipLaunchKernelGGL((conv_fwd_cl_kernel<T, WW, SEQ>), grid, dim3(256), 0, st, p);       \
+    break;
+    MCPU_CONV_CL(2)
+    MCPU_CONV_CL(3)
+    MCPU_CONV_CL(4)
+    MCPU_CONV_CL(5)
+#undef MCPU_CONV_CL
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_cl(const ConvParams& p, bool bwd, hipStream_t st) {
+  return p.seq_idx != nullptr ? launch_cl_seq<T, true>(p, bwd, st) : launch_cl_seq<T, false>(p, bwd, st);
+}
+
+static hipError_t launch_cl_dtype(const ConvParams& p, int dtype, bool bwd, hipStream_t st) {
+  switch (dtype) {
+    case MCPU_F32: return launch_cl<float>(p, bwd, st);
+    case MCPU_BF16: return launch_cl<bf16>(p, bwd, st);
+    default: return launch_cl<f16>(p, bwd, st);
+  }
+}
+
 template <typename T>
 static hipError_t launch_vt(const ConvParams& p, bool bwd, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(
@@ -641,6 +968,8 @@ hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
   if (n > 0 && p.vt) {
     if (hipError_t e = launch_vt_dtype(p, dtype, false, st)) return e;
+  } else if (n > 0 && p.cl) {
+    if (hipError_t e = launch_cl_dtype(p, dtype, false, st)) return e;
   } else if (n > 0) {
     if (hipError_t e = launch_generic_dtype(p, dtype, false, blocks_for(n), st)) return e;
   }
@@ -663,6 +992,13 @@ hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float
     const int64_t per = p.dim * (p.width + 1);
     hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(static_cast<unsigned>((per + 63) / 64)), dim3(256),
                        0, st, p.dw_part, dweight, dbias, p.batch * p.nseg, p.dim, p.width);
+    return hipGetLastError();
+  }
+  if (n > 0 && p.cl) {
+    if (hipError_t e = launch_cl_dtype(p, dtype, true, st)) return e;
+    const int64_t per = p.dim * (p.width + 1);
+    hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(static_cast<unsigned>((per + 63) / 64)), dim3(256),
+                       0, st, p.dw_part, dweight, dbias, p.batch * p.cl_gy, p.dim, p.width);
     return hipGetLastError();
   }
   if (n > 0) {

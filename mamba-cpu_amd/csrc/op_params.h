@@ -12,6 +12,7 @@ constexpr int kConvT = 8;      // conv steps per chunk
 constexpr int kConvMaxW = 16;  // largest supported conv width
 constexpr int kConvRMax = 16;  // most threads walking one (batch, channel) row
 constexpr int kConvVTSteps = 8;  // steps per thread of the time-contiguous fast path
+constexpr int kConvClG = 8;      // unrolled steps per group of the channel-contiguous fast path
 
 struct ConvParams {
   const void* x;
@@ -37,6 +38,11 @@ struct ConvParams {
   int tpr;            // threads per row segment: 64, 128 or 256
   int rpw;            // row segments per workgroup: 256 / tpr
   int64_t nseg;       // segments per row (rows longer than 2048 steps)
+  // Channel-contiguous fast path (conv_*_cl_kernel): cl = 1 when it applies;
+  // a wave's time segment is cl_ng groups of kConvClG steps; cl_gy segment
+  // groups of four per row (the grid's y).
+  int cl, cl_ng;
+  int64_t cl_gy;
 };
 
 struct ConvUpdateParams {

@@ -346,3 +346,75 @@ def test_seq_idx_matches_oracle(layout, width, dtype):
     for got, want_, name in ((w.grad, dw, "dweight"), (bias.grad, db, "dbias")):
         sc = max(np.abs(want_).max(), 1.0)
         close(got / sc, want_ / sc, gtol, gtol, name)
+
+
+def _packed_ids(b, l, cuts_per_row, device):
+    """(b, l) int32 sequence ids, row r cut at cuts_per_row[r]."""
+    seq = torch.zeros(b, l, dtype=torch.int32)
+    for bi, cuts in enumerate(cuts_per_row):
+        edges = [0] + sorted(c for c in cuts if 0 < c < l) + [l]
+        for si, (lo, hi) in enumerate(zip(edges[:-1], edges[1:])):
+            seq[bi, lo:hi] = si + 11 * bi
+    return seq.to(device)
+
+
+@pytest.mark.parametrize("width", [2, 3, 4, 5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("seqlen", [1, 7, 45, 130])
+@pytest.mark.parametrize("packed", [False, True])
+def test_channel_contiguous_path_matches_oracle(width, dtype, seqlen, packed):
+    """x, out, dout and dx all channel-contiguous (the fused mixer's and
+    Hugging Face's layout) take the four-channels-per-lane kernels: 264
+    channels (a second, partly filled 256-channel tile), 8-step segments with
+    a ragged last one, and packed sequences with boundaries inside segments,
+    on segment starts and a one-step sequence."""
+    torch.manual_seed(width * 100 + seqlen)
+    b, d = 3, 264
+    x = torch.randn(b, seqlen, d, device=DEV).to(dtype).transpose(1, 2).requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    seq = _packed_ids(b, seqlen, [[3, 4, 16, 40, 41], [8, 24, 100], [1]], DEV) if packed else None
+    out = causal_conv1d_fn(x, w, bias, seq_idx=seq, activation="silu")
+    assert out.transpose(1, 2).is_contiguous()
+    sq = None if seq is None else seq.cpu().numpy()
+    want, _ = O.causal_conv1d_fwd(x, w, bias, None, "silu", seq_idx=sq)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    close(out, want, tol, tol, "out")
+    G = torch.randn(b, seqlen, d, device=DEV).to(dtype).transpose(1, 2)
+    dx_, dw_, db_ = torch.autograd.grad(out, [x, w, bias], G)
+    dx, dw, db, _ = O.causal_conv1d_bwd(x, w, bias, None, G, "silu", seq_idx=sq)
+    gtol = 1e-4 if dtype == torch.float32 else 2e-2
+    close(dx_, dx, gtol, gtol, "dx")
+    for got, want_, name in ((dw_, dw, "dweight"), (db_, db, "dbias")):
+        sc = max(np.abs(want_).max(), 1.0)
+        close(got / sc, want_ / sc, gtol, gtol, name)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_channel_contiguous_long_segments_match_time_contiguous(packed):
+    """A long sequence gives the channel-contiguous kernels 16-step segments
+    walked in two unrolled groups (one group when a segment holds a sequence
+    boundary) and a ragged last segment. The outputs and input gradients are
+    the same sums in the same order as the time-contiguous kernels': the
+    outputs match bitwise, the input gradients to rounding (the activation's
+    derivative is associated differently); the weight gradients sum the
+    partials in another order."""
+    torch.manual_seed(5)
+    b, d, l, width = 8, 256, 16384 + 5, 4
+    xt = torch.randn(b, l, d, device=DEV)
+    w = torch.randn(d, width, device=DEV) * 0.5
+    bias = torch.randn(d, device=DEV) * 0.3
+    Gt = torch.randn(b, l, d, device=DEV)
+    cuts = [[16, 17, 4000, 9999], [5], [], [8192, 8193, 8194], [16], [1, 2, 3], [16384], [777]]
+    seq = _packed_ids(b, l, cuts, DEV) if packed else None
+    res = []
+    for x, G in ((xt.transpose(1, 2), Gt.transpose(1, 2)),
+                 (xt.transpose(1, 2).contiguous(), Gt.transpose(1, 2).contiguous())):
+        xx, ww, bb = x.clone().requires_grad_(), w.clone().requires_grad_(), bias.clone().requires_grad_()
+        out = causal_conv1d_fn(xx, ww, bb, seq_idx=seq, activation="silu")
+        res.append((out, *torch.autograd.grad(out, [xx, ww, bb], G)))
+    (o1, dx1, dw1, db1), (o2, dx2, dw2, db2) = res
+    assert torch.equal(o1, o2)
+    torch.testing.assert_close(dx1, dx2, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(dw1, dw2, rtol=1e-5, atol=1e-2)
+    torch.testing.assert_close(db1, db2, rtol=1e-5, atol=1e-2)
