@@ -19,8 +19,10 @@ Also reported, on one JSON line:
                 init) prefill 4 x 1024 tokens/s, 128-step greedy decode and a
                 4 x 256 training step through the patched Hugging Face model;
                 and every other workload of the op set (forward-only scan,
-                long-sequence bf16 scan, conv1d fp32/bf16, conv update, state
-                update), each with time, algorithmic bytes and HBM fraction.
+                long-sequence bf16 scan, complex-A scan, conv1d fp32/bf16,
+                conv1d over packed sequences, conv update, conv update through
+                ring buffers and state indices, state update), each with time,
+                algorithmic bytes and HBM fraction.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -170,6 +172,35 @@ class _torch_threads:
 
     def __exit__(self, *exc):
         self.torch.set_num_threads(self.prev)
+
+
+def _attach_graph(torch, stream, r, fn, state, steps):
+    """Adds the per-step time of `fn` (`steps` in-place steps on `state`)
+    replayed from one HIP graph, once the replayed state is checked equal to
+    the eager one; or the reason it is missing."""
+    try:
+        st0 = state.clone()
+        gph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(gph):
+            fn()
+        state.copy_(st0)
+        fn()
+        want = state.clone()
+        state.copy_(st0)
+        gph.replay()
+        torch.cuda.synchronize()
+        if torch.equal(state, want):
+            r["graph_us_per_step"] = round(_events_ms(torch, stream, gph.replay, 5) / steps * 1e3, 2)
+        else:
+            r["graph_error"] = "replayed state differs from the eager state"
+        del gph
+    except Exception as exc:  # noqa: BLE001
+        r["graph_error"] = repr(exc)
 
 
 def cpu_conv_ms(torch, x, wt, bias, go, iters=2):
@@ -347,29 +378,7 @@ def other_configs(torch, dev, stream, cpu):
     # The same 256 steps replayed from one HIP graph: the per-step time
     # without the host's per-call dispatch (what a graph-captured decoder
     # sees). The replayed state must equal the eager one.
-    try:
-        st0 = state.clone()
-        gph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            upd()
-        torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(gph):
-            upd()
-        state.copy_(st0)
-        upd()
-        want = state.clone()
-        state.copy_(st0)
-        gph.replay()
-        torch.cuda.synchronize()
-        if torch.equal(state, want):
-            r["graph_us_per_step"] = round(_events_ms(torch, stream, gph.replay, 5) / 256 * 1e3, 2)
-        else:
-            r["graph_error"] = "replayed state differs from the eager state"
-        del gph
-    except Exception as exc:  # noqa: BLE001
-        r["graph_error"] = repr(exc)
+    _attach_graph(torch, stream, r, upd, state, 256)
     if cpu:
         from oracle import cpu_torch as CT
 
@@ -405,6 +414,7 @@ def other_configs(torch, dev, stream, cpu):
     r = _rate(nbytes, ms)
     r["workload"] = ("causal_conv1d_update with cache_seqlens and conv_state_indices, fp32, pool "
                      "(128, 3072, 8) of ring buffers, x (64, 3072), silu; per step of 256")
+    _attach_graph(torch, stream, r, upd_ring, pool, 256)
     res["conv_update_ring_indexed_b64_d3072"] = r
     del pool, pos
 

@@ -300,14 +300,17 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
   }
 }
 
-// Single-step update without a ring buffer (the decode step): a 2-D grid of
-// channel tiles x batch rows, so no per-thread 64-bit division. The whole old
+// Single-step update (the decode step): a 2-D grid of channel tiles x batch
+// rows, so no per-thread 64-bit division. Without a ring buffer the whole old
 // state row (state_len <= kUpd1MaxS entries) and x are loaded together, the
 // output is computed, and the shifted state is stored from registers, so no
-// store waits on a reload of a slot it depends on.
+// store waits on a reload of a slot it depends on. With a ring buffer (RING,
+// any state_len) the W-1 taps are read at (cs - (W-1) + k) mod state_len and x
+// is written at cs mod state_len; cs is the batch row's, so the wrap runs once
+// per wave in 32-bit scalar arithmetic.
 constexpr int kUpd1MaxS = 8;
 
-template <typename T, int W>
+template <typename T, int W, bool RING>
 __global__ void __launch_bounds__(256) conv_update1_kernel(const ConvUpdateParams p) {
   const int64_t d = blockIdx.x * 256ll + threadIdx.x;
   const int64_t b = blockIdx.y;
@@ -323,14 +326,26 @@ __global__ void __launch_bounds__(256) conv_update1_kernel(const ConvUpdateParam
     }
   }
   const int64_t sb = srow * p.sst[0] + d * p.sst[1];
-  float old[kUpd1MaxS];
-#pragma unroll
-  for (int i = 0; i < kUpd1MaxS; ++i) old[i] = i < S ? ld<T>(p.state, sb + i * p.sst[2]) : 0.f;
   const float xv = ld<T>(p.x, b * p.sx[0] + d * p.sx[1]);
   float w[W];
 #pragma unroll
   for (int k = 0; k < W; ++k) w[k] = p.w[d * W + k];
   float acc = p.bias ? p.bias[d] : 0.f;
+  if constexpr (RING) {
+    const int cs = __builtin_amdgcn_readfirstlane(p.cache_seqlens[b]);
+    auto wrap = [&](int i) { const int r = i % S; return r < 0 ? r + S : r; };
+#pragma unroll
+    for (int k = 0; k < W - 1; ++k)
+      acc = fmaf(w[k], ld<T>(p.state, sb + wrap(cs - (W - 1) + k) * p.sst[2]), acc);
+    acc = fmaf(w[W - 1], xv, acc);
+    if (p.silu) acc = acc * sigmoid(acc);
+    st<T>(p.out, ob, acc);
+    st<T>(p.state, sb + wrap(cs) * p.sst[2], xv);
+    return;
+  }
+  float old[kUpd1MaxS];
+#pragma unroll
+  for (int i = 0; i < kUpd1MaxS; ++i) old[i] = i < S ? ld<T>(p.state, sb + i * p.sst[2]) : 0.f;
   // Taps 0 .. W-2 read the newest W-1 state entries, tap W-1 reads x.
 #pragma unroll
   for (int k = 0; k < W - 1; ++k) {
@@ -1010,21 +1025,27 @@ hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float
   return hipGetLastError();
 }
 
-template <typename T>
-static bool launch_update1(const ConvUpdateParams& p, hipStream_t st) {
+template <typename T, bool RING>
+static bool launch_update1_ring(const ConvUpdateParams& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((p.dim + 255) / 256), static_cast<unsigned>(p.batch));
   switch (p.width) {
-    case 2: hipLaunchKernelGGL((conv_update1_kernel<T, 2>), grid, dim3(256), 0, st, p); return true;
-    case 3: hipLaunchKernelGGL((conv_update1_kernel<T, 3>), grid, dim3(256), 0, st, p); return true;
-    case 4: hipLaunchKernelGGL((conv_update1_kernel<T, 4>), grid, dim3(256), 0, st, p); return true;
+    case 2: hipLaunchKernelGGL((conv_update1_kernel<T, 2, RING>), grid, dim3(256), 0, st, p); return true;
+    case 3: hipLaunchKernelGGL((conv_update1_kernel<T, 3, RING>), grid, dim3(256), 0, st, p); return true;
+    case 4: hipLaunchKernelGGL((conv_update1_kernel<T, 4, RING>), grid, dim3(256), 0, st, p); return true;
     default: return false;
   }
+}
+
+template <typename T>
+static bool launch_update1(const ConvUpdateParams& p, hipStream_t st) {
+  return p.cache_seqlens != nullptr ? launch_update1_ring<T, true>(p, st) : launch_update1_ring<T, false>(p, st);
 }
 
 hipError_t conv_update_launch(const ConvUpdateParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim;
   if (n == 0) return hipSuccess;
-  if (p.seqlen == 1 && p.cache_seqlens == nullptr && p.state_len <= kUpd1MaxS && p.batch <= 65535) {
+  const bool fits = p.cache_seqlens != nullptr ? p.state_len <= INT32_MAX : p.state_len <= kUpd1MaxS;
+  if (p.seqlen == 1 && fits && p.batch <= 65535) {
     bool done = false;
     switch (dtype) {
       case MCPU_F32: done = launch_update1<float>(p, st); break;

@@ -147,15 +147,18 @@ def test_rejects_unsupported_args():
 
 
 @pytest.mark.parametrize("seqlen", [None, 1, 3])
-@pytest.mark.parametrize("state_len", [3, 6])
+@pytest.mark.parametrize("state_len", [3, 6, 11])
 @pytest.mark.parametrize("mode", ["indices", "ring", "both"])
-def test_update_continuous_batching_matches_oracle(seqlen, state_len, mode):
+@pytest.mark.parametrize("width", [2, 4])
+def test_update_continuous_batching_matches_oracle(seqlen, state_len, mode, width):
     """conv_state_indices (rows of a larger state, one out of range) and
     cache_seqlens (ring buffer), which the reference rejects, against the
     oracle's restatement of the upstream semantics; several steps in a row so
-    the ring wraps."""
-    torch.manual_seed(7)
-    b, d, width, rows = 3, 20, 4, 6
+    the ring wraps. Single steps take the 2-D single-step kernel (ring
+    positions wrapped per batch row, any state length), longer ones the
+    general kernel."""
+    torch.manual_seed(7 + width)
+    b, d, rows = 3, 20, 6
     w = torch.randn(d, width, device=DEV)
     bias = torch.randn(d, device=DEV)
     state = torch.randn(rows, d, state_len, device=DEV)
@@ -164,7 +167,7 @@ def test_update_continuous_batching_matches_oracle(seqlen, state_len, mode):
     if mode == "ring":
         state = state[:b].clone()
         want_state = want_state[:b]
-    cs = torch.tensor([0, 5, 2], dtype=torch.int64, device=DEV) if mode != "indices" else None
+    cs = torch.tensor([0, 5, 100003], dtype=torch.int64, device=DEV) if mode != "indices" else None
     for step in range(4):
         x = torch.randn(b, d, device=DEV) if seqlen is None else torch.randn(b, d, seqlen, device=DEV)
         out = causal_conv1d_update(x, state, w, bias, "silu", cache_seqlens=cs, conv_state_indices=idx)
