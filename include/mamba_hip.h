@@ -187,6 +187,10 @@ typedef struct mcpu_conv_args {
 } mcpu_conv_args;
 
 int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream);
+/* Bytes of device workspace the backward needs: the dweight/dbias partials,
+   float32 (batch, parts, dim, width+1). It depends only on batch, dim, seqlen
+   and width (the largest of the three kernel paths' partial counts), so one
+   workspace serves every layout of a shape. 0 for invalid arguments. */
 size_t mcpu_causal_conv1d_bwd_workspace_size(const mcpu_conv_args* a);
 int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace, size_t workspace_bytes,
                            void* stream);

@@ -199,6 +199,31 @@ def test_conv_and_state_update_reject_bad_arguments():
     assert _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)[0] == _C.MCPU_ERR_INVALID
 
 
+def test_conv_workspace_depends_only_on_the_shape():
+    """The backward's partials workspace is sized from batch, dim, seqlen and
+    width alone (host arithmetic, no device): a time-contiguous and a
+    channel-contiguous x of one shape need the same bytes, and that covers the
+    channel-contiguous path's partials (one per four 8- to 64-step segments)
+    as well as the chunked kernels' (up to 16 threads per row)."""
+    from mamba_cpu import _C
+
+    L = _C.lib
+    for b, d, l, w in ((8, 3072, 2048, 4), (1, 8, 5, 2), (3, 264, 130, 5), (2, 1536, 100000, 4)):
+        sizes = []
+        for strides in ((d * l, l, 1), (l * d, 1, d)):
+            c = _C.ConvArgs()
+            c.x = c.weight = 4096
+            c.batch, c.dim, c.seqlen, c.width = b, d, l, w
+            c.x_stride[:] = strides
+            sizes.append(L.mcpu_causal_conv1d_bwd_workspace_size(ctypes.byref(c)))
+        assert sizes[0] == sizes[1] > 0
+        tiles, ng = b * ((d + 255) // 256), 8
+        while ng > 1 and tiles * -(-l // (8 * ng)) < 8192:
+            ng //= 2
+        gy = -(-(-(-l // (8 * ng))) // 4)
+        assert sizes[0] >= 4 * b * max(gy, min(-(-l // 8), 16)) * d * (w + 1)
+
+
 def test_status_codes_map_to_the_reference_exceptions():
     from mamba_cpu import _C
 
