@@ -119,6 +119,11 @@ typedef struct mcpu_scan_args {
      (batch, ngroups, seqlen, dstate, 2) contiguous. dstate <= 32; ysave and
      the forward workspace are not used. */
   int32_t complex_a;
+  /* Backward workgroup width in waves: 0 = chosen by the library from the
+     shape (the production setting); 4, 8 or 12 pins it (dstate <= 16, real A
+     only), so tests can cover every width on one shape. The workspace size
+     query must see the same value as the call. */
+  int32_t bwd_waves;
 } mcpu_scan_args;
 
 /* Bytes of the optional checkpoint buffer: the float32 scan state at the
@@ -148,6 +153,7 @@ size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);
  * bound by _C.selective_scan_bwd_f32 (csrc/bindings.cpp:47-84). */
 int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
                             void* stream);
+
 
 /* ------------------------------------------------------------------------ */
 /* Causal depthwise conv1d.                                                  */

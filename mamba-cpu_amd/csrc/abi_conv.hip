@@ -114,16 +114,17 @@ bool cl_operand(const void* ptr, const int64_t (&s)[3], int dtype) {
 }
 
 // Whether the channel-contiguous path applies (after conv_cl_shape): widths
-// 2..5, whole four-channel vectors, no initial states (forward) and no
-// initial- or final-state gradients (backward); seq_idx is allowed.
+// 2..5, whole four-channel vectors, no initial states (its kernels read zeros
+// before step 0) and, in the backward, no initial- or final-state gradients;
+// seq_idx is allowed.
 bool cl_ok(const ConvParams& p, int dtype, bool bwd) {
   if (p.width < 2 || p.width > 5 || p.dim % 4 != 0 || p.seqlen < 1) return false;
   if (!p.channels_last || p.batch > 65535 || p.cl_gy > 65535) return false;
-  if (!cl_operand(p.x, p.sx, dtype)) return false;
+  if (p.init != nullptr || !cl_operand(p.x, p.sx, dtype)) return false;
   if (bwd)
     return p.dinit == nullptr && p.dfinal == nullptr && cl_operand(p.dout, p.sdo, dtype) &&
            cl_operand(p.dx, p.sdx, dtype);
-  return p.init == nullptr && cl_operand(p.out, p.sout, dtype);
+  return cl_operand(p.out, p.sout, dtype);
 }
 
 size_t conv_ws(const ConvParams& p) {
@@ -210,6 +211,8 @@ extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* s
   if (a->state_len < a->width - 1)
     return fail(MCPU_ERR_INVALID, "conv_state length (%lld) must be at least width - 1 (%lld)",
                 (long long)a->state_len, (long long)(a->width - 1));
+  if (a->cache_seqlens != nullptr && a->state_len < 1)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: cache_seqlens needs a conv_state of at least one slot");
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "causal_conv1d_update: bad dtype");
   if (int rc = mcpu_check_device()) return rc;
   ConvUpdateParams p;

@@ -48,6 +48,10 @@ int check_scan(const mcpu_scan_args* a) {
     return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, %lld]%s, got %lld",
                 (long long)max_dstate, a->complex_a ? " with complex A" : "", (long long)a->dstate);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "selective_scan: bad dtype %d", a->dtype);
+  if (a->bwd_waves != 0 &&
+      (a->complex_a || a->dstate > 16 || (a->bwd_waves != 4 && a->bwd_waves != 8 && a->bwd_waves != 12)))
+    return fail(MCPU_ERR_INVALID, "selective_scan: bwd_waves must be 0, or 4, 8 or 12 with real A "
+                "and dstate <= 16, got %d", a->bwd_waves);
   const int64_t dpg = a->dim / a->ngroups;
   const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16);
   if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
@@ -143,7 +147,10 @@ FwdLayout fwd_layout(const ScanParams& p) {
   return w;
 }
 
+// The backward's workgroup width: pinned by the caller (bwd_waves, checked by
+// check_scan) or chosen from the shape.
 int bwd_waves(const mcpu_scan_args* a) {
+  if (a->bwd_waves != 0) return a->bwd_waves;
   return scan_bwd_waves(a->batch, a->ngroups, a->dim / a->ngroups, a->dstate);
 }
 
@@ -441,3 +448,4 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
                          p.batch * p.nchunk, st),
       "selective_scan_bwd reduce");
 }
+

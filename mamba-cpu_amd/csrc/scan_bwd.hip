@@ -21,8 +21,6 @@
 // dA/dD/ddelta_bias are per-(batch, channel) partials reduced over the batch
 // the same way. Operands of the next (earlier) block are fetched while the
 // current block computes.
-#include <cstdlib>
-
 #include "scan_common.h"
 
 namespace mcpu {
@@ -625,11 +623,6 @@ static hipError_t launch_bwd_w(const ScanParams& p, int waves, hipStream_t strea
 // units in whole rounds.
 int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) {
   if (dstate > 16) return 4;  // keeps the per-workgroup LDS small
-  // MCPU_SCAN_BWD_WAVES=4|8|12 overrides the choice (tuning).
-  if (const char* env = std::getenv("MCPU_SCAN_BWD_WAVES")) {
-    const int w = std::atoi(env);
-    if (w == 4 || w == 8 || w == 12) return w;
-  }
   const int64_t slices = batch * ngroups;
   for (int w : {12, 8}) {
     const int64_t wgs = slices * ((dpg + 4 * w - 1) / (4 * w));

@@ -701,14 +701,19 @@ Tensor causal_conv1d_update(const Tensor& x, Tensor& conv_state, const Tensor& w
   check_index(name, "conv_state_indices", conv_state_indices, x.size(0));
   TORCH_CHECK_VALUE(x_dtype(x.scalar_type()) && conv_state.scalar_type() == x.scalar_type(), name,
                     " expects x and conv_state of one dtype among float32, bfloat16 and float16");
-  TORCH_CHECK_VALUE(weight_in.dim() == 2, name, " expects weight (dim, width)");
   const bool single = x.dim() == 2;
+  TORCH_CHECK_VALUE(weight_in.dim() == 2 && x.dim() >= 2 && weight_in.size(0) == x.size(1), name,
+                    " expects weight (dim, width) with dim = x.size(1)");
+  TORCH_CHECK_VALUE(!has(bias_in) || (bias_in->dim() == 1 && bias_in->size(0) == x.size(1)), name,
+                    " expects bias of shape (dim,)");
   TORCH_CHECK_VALUE((single || x.dim() == 3) && conv_state.dim() == 3, name,
                     " expects x (batch, dim[, seqlen]) and conv_state (batch, dim, state_len)");
   TORCH_CHECK_VALUE(conv_state.size(1) == x.size(1) &&
                         (has(conv_state_indices) || conv_state.size(0) == x.size(0)),
                     name, " expects conv_state (batch, dim, state_len), or (rows, dim, state_len) "
                     "with conv_state_indices");
+  TORCH_CHECK_VALUE(!has(cache_seqlens) || conv_state.size(2) >= 1, name,
+                    " expects a conv_state of at least one slot when cache_seqlens is given");
   const Tensor weight = f32c(weight_in);
   const optional<Tensor> bias = f32c(bias_in);
   c10::DeviceGuard guard(x.device());

@@ -62,7 +62,7 @@ class ScanArgs(ctypes.Structure):
         ("du", _P), ("ddelta", _P), ("dz", _P), ("dA", _P), ("dB", _P), ("dC", _P), ("dD", _P),
         ("ddelta_bias", _P),
         ("out_stride", _S3), ("du_stride", _S3), ("ddelta_stride", _S3), ("dz_stride", _S3),
-        ("complex_a", _I32),
+        ("complex_a", _I32), ("bwd_waves", _I32),
     ]
 
 

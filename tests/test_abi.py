@@ -263,6 +263,66 @@ def test_public_api_surface():
     assert hasattr(torch.ops.mamba_cpu, "selective_scan_bwd")
 
 
+def test_public_signatures_equal_the_reference():
+    """inspect.signature of each public function equals the reference's
+    (parameter names, order and defaults), as the reference pins its ops
+    against upstream's (tests/test_upstream.py:21-28). The expected text comes
+    from the reference's sources, read with `ast` by
+    tests/golden/make_signatures.py into tests/golden/signatures.json."""
+    import inspect
+    import json
+
+    import mamba_cpu
+
+    with open(os.path.join(ROOT, "tests", "golden", "signatures.json")) as f:
+        want = json.load(f)
+    assert set(want) == {"selective_scan_fn", "causal_conv1d_fn", "causal_conv1d_update",
+                         "selective_state_update", "selective_scan_ref", "causal_conv1d_ref"}
+    for name, entry in want.items():
+        got = str(inspect.signature(getattr(mamba_cpu, name)))
+        assert got == entry["signature"], f"{name}: {got} != {entry['signature']} ({entry['source']})"
+
+
+def test_scan_bwd_waves_is_checked_and_sizes_the_workspace():
+    """bwd_waves = 0 lets the library choose; 4, 8 or 12 pin the backward's
+    workgroup width (fewer channel blocks, so a smaller dB/dC partial
+    workspace, the wider it is); anything else, complex A or dstate > 16 is
+    rejected before any device work."""
+    from mamba_cpu import _C
+
+    L = _C.lib
+
+    def ws(**kw):
+        a = _scan_args(batch=8, dim=1536, seqlen=1024, ckpt=64, **kw)
+        a.u_stride[:] = a.delta_stride[:] = (1536 * 1024, 1024, 1)
+        a.B_stride[:] = a.C_stride[:] = (1024 * 16, 1024 * 16, 16, 1)
+        return L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a))
+
+    w4, w8, w12 = ws(bwd_waves=4), ws(bwd_waves=8), ws(bwd_waves=12)
+    assert w4 > w8 > w12 > 0
+    # the shape of the training-step workload chooses 12 waves by itself
+    assert ws() == w12
+    for bad in (3, 16, -4):
+        rc, msg = _rc(L.mcpu_selective_scan_bwd, ctypes.byref(_scan_args(bwd_waves=bad)), None, 0, None)
+        assert rc == _C.MCPU_ERR_INVALID and "bwd_waves" in msg
+        assert ws(bwd_waves=bad) == 0
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(bwd_waves=8, dstate=32)), None, 0, None)
+    assert rc == _C.MCPU_ERR_INVALID and "bwd_waves" in msg
+
+
+def test_conv_update_ring_buffer_needs_a_slot():
+    """cache_seqlens with a zero-length conv_state (possible at width 1) would
+    index the ring modulo 0: rejected before any device work."""
+    from mamba_cpu import _C
+
+    L = _C.lib
+    u = _C.ConvUpdateArgs()
+    u.x = u.conv_state = u.weight = u.out = u.cache_seqlens = 16
+    u.batch, u.dim, u.seqlen, u.width, u.state_len = 1, 4, 1, 1, 0
+    rc, msg = _rc(L.mcpu_causal_conv1d_update, ctypes.byref(u), None)
+    assert rc == _C.MCPU_ERR_INVALID and "cache_seqlens" in msg
+
+
 @pytest.mark.gpu
 def test_scan_writes_outputs_through_their_strides():
     """out, du, ddelta and dz land at the strides the caller gives: here

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from conftest import GRAD_ATOL, GRAD_RTOL
 from oracle import numerics as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -41,8 +42,9 @@ def close(got, want, rtol, atol, name):
 
 
 def close_grad(got, want, name):
-    scale = max(float(np.abs(want).max()), 1.0)
-    close(np.asarray(got, np.float64) / scale, want / scale, 1e-3, 1e-4, name)
+    """Unscaled: rtol 1e-3 and the per-gradient atol of conftest.GRAD_ATOL
+    (name is the gradient's, e.g. "dA" -> A)."""
+    close(np.asarray(got, np.float64), want, GRAD_RTOL, GRAD_ATOL[name[1:]], name)
 
 
 GRADS = ("du", "ddelta", "dA", "dB", "dC", "dD", "dz", "ddelta_bias")

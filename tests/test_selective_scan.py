@@ -1,19 +1,22 @@
 """selective_scan_fn on the GPU against the float64 oracle.
 
-Mirrors the reference's tests/test_selective_scan.py case for case (shapes,
+Covers the cases of the reference's tests/test_selective_scan.py (its shapes,
 group layouts, flag combinations, low precision, opcheck, extreme decay, exp
 accuracy, NaN confinement); the expected values come from oracle/numerics.py
 (float64) instead of the reference's pure-torch selective_scan_ref.
-Tolerances: float32 outputs rtol 1e-4 / atol 1e-5, float32 gradients rtol 1e-3
-(atol 1e-4 after scaling by the gradient's magnitude), bf16/fp16 1e-2 on
-outputs and 2e-2 on gradients, always against the oracle evaluated on the
-same (rounded) inputs.
+Tolerances, unscaled (|got - want| <= atol + rtol |want|): float32 outputs
+rtol 1e-4 / atol 1e-5; float32 gradients at the reference's shapes and loss
+rtol 1e-4 / atol 1e-4 (its own bound, tests/test_selective_scan.py:85),
+elsewhere rtol 1e-3 with the atol of conftest.GRAD_ATOL; bf16/fp16 1e-2 on
+outputs and 2e-2 on gradients. The oracle always sees the same (rounded)
+inputs as the GPU.
 """
 
 import numpy as np
 import pytest
 import torch
 
+from conftest import GRAD_ATOL, GRAD_RTOL, assert_close_report
 from oracle import numerics as O
 
 import mamba_cpu
@@ -24,30 +27,31 @@ DEV = "cuda"
 
 
 def make_inputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, dtype, requires_grad=False):
-    """Same generator and distributions as the reference's make_inputs
-    (tests/test_selective_scan.py:28-45), created on the CPU, moved to the GPU."""
-    g = torch.Generator().manual_seed(0)
-
-    def rand(*shape, scale=1.0, dt=dtype):
-        return (torch.randn(*shape, generator=g) * scale).to(dt)
-
-    bc_shape = (batch, dstate, seqlen) if ngroups is None else (batch, ngroups, dstate, seqlen)
-    inp = dict(
-        u=rand(batch, dim, seqlen),
-        delta=(torch.rand(batch, dim, seqlen, generator=g) * 0.5).to(dtype),
-        A=(-torch.rand(dim, dstate, generator=g) - 0.5),
-        B=rand(*bc_shape),
-        C=rand(*bc_shape),
-        D=rand(dim, dt=torch.float32) if has_D else None,
-        z=rand(batch, dim, seqlen) if has_z else None,
-        delta_bias=(torch.rand(dim, generator=g) * 0.1) if has_bias else None,
-    )
-    return {k: None if v is None else v.to(DEV).requires_grad_(requires_grad) for k, v in inp.items()}
+    """A scan case drawn on the CPU from one seed-0 generator, then moved to
+    the GPU. The draws (and their order) are the reference's test inputs
+    (tests/test_selective_scan.py:9-26): u, B, C, D, z ~ N(0, 1); delta ~
+    U(0, 0.5); A ~ -U(0.5, 1.5); delta_bias ~ U(0, 0.1). B/C are
+    (batch, dstate, seqlen), or (batch, ngroups, dstate, seqlen) when ngroups
+    is given."""
+    gen = torch.Generator().manual_seed(0)
+    normal = lambda *shape: torch.randn(*shape, generator=gen)  # noqa: E731
+    uniform = lambda *shape: torch.rand(*shape, generator=gen)  # noqa: E731
+    bc = (batch, dstate, seqlen) if ngroups is None else (batch, ngroups, dstate, seqlen)
+    draws = [
+        ("u", normal(batch, dim, seqlen).to(dtype)),
+        ("delta", (0.5 * uniform(batch, dim, seqlen)).to(dtype)),
+        ("A", -0.5 - uniform(dim, dstate)),
+        ("B", normal(*bc).to(dtype)),
+        ("C", normal(*bc).to(dtype)),
+        ("D", normal(dim) if has_D else None),
+        ("z", normal(batch, dim, seqlen).to(dtype) if has_z else None),
+        ("delta_bias", 0.1 * uniform(dim) if has_bias else None),
+    ]
+    return {k: None if v is None else v.to(DEV).requires_grad_(requires_grad) for k, v in draws}
 
 
 def close(got, want, rtol, atol, name=""):
-    got = got.detach().float().cpu().numpy().astype(np.float64)
-    np.testing.assert_allclose(got, want, rtol=rtol, atol=atol, err_msg=name)
+    assert_close_report(got, want, rtol, atol, name)
 
 
 @pytest.mark.parametrize("batch,dim,seqlen,dstate", [(1, 4, 1, 1), (2, 16, 33, 16), (3, 32, 128, 8)])
@@ -98,14 +102,15 @@ def oracle_grads(inp, softplus, W, V):
     return {k: v for k, v in want.items() if inp.get(k) is not None}
 
 
-def check_grads(got, want, rtol, atol):
+def check_grads(got, want, rtol=GRAD_RTOL, atol=None):
+    """Unscaled elementwise check of every gradient; atol per gradient from
+    conftest.GRAD_ATOL unless one value is given."""
     for k, w in want.items():
         g = got[k]
         if g is None:
             assert not np.any(w), k
             continue
-        scale = max(np.abs(w).max(), 1.0)
-        close(g / scale, w / scale, rtol, atol, k)
+        close(g, w, rtol, GRAD_ATOL[k] if atol is None else atol, k)
 
 
 @pytest.mark.parametrize("batch,dim,seqlen,dstate", [(1, 4, 1, 1), (2, 8, 17, 4), (2, 64, 96, 16)])
@@ -117,23 +122,40 @@ def check_grads(got, want, rtol, atol):
 ])
 @pytest.mark.parametrize("loss_on", [("out", "last"), ("out",), ("last",)])
 def test_backward_matches_oracle(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, softplus, loss_on):
+    """The reference's backward cases with its loss, sum((out * ramp)^2) over a
+    ramp from -1 to 1 along the sequence plus sum(last * sign(last))
+    (tests/test_selective_scan.py:52-65), at its tolerance rtol 1e-4 /
+    atol 1e-4, unscaled. The oracle gets the upstream gradients its own
+    float64 forward implies."""
     if ngroups is not None and dim % ngroups:
         pytest.skip("dim not divisible by ngroups")
     inp = make_inputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, torch.float32,
                       requires_grad=True)
-    g = torch.Generator().manual_seed(1)
-    W = torch.randn(batch, dim, seqlen, generator=g).to(DEV) if "out" in loss_on else None
-    V = torch.randn(batch, dim, dstate, generator=g).to(DEV) if "last" in loss_on else None
-    got = grads_of(inp, softplus, W, V)
-    want = oracle_grads(inp, softplus, W, V)
-    check_grads(got, want, 1e-3, 1e-4)
+    for v in inp.values():
+        if v is not None:
+            v.grad = None
+    out, last = selective_scan_fn(**inp, delta_softplus=softplus, return_last_state=True)
+    ramp = torch.linspace(-1, 1, seqlen, device=DEV)
+    loss = 0
+    if "out" in loss_on:
+        loss = loss + (out * ramp).square().sum()
+    if "last" in loss_on:
+        loss = loss + (last * last.detach().sign()).sum()
+    loss.backward()
+    got = {k: None if v.grad is None else v.grad for k, v in inp.items() if v is not None}
+    out64, last64 = O.selective_scan_fwd(**inp, delta_softplus=softplus)
+    r = np.linspace(-1, 1, seqlen)
+    W = 2 * out64 * r * r if "out" in loss_on else None
+    V = np.sign(last64) if "last" in loss_on else None
+    check_grads(got, oracle_grads(inp, softplus, W, V), 1e-4, 1e-4)
 
 
 def test_backward_low_precision():
     inp = make_inputs(2, 16, 32, 8, None, True, True, True, torch.bfloat16, requires_grad=True)
     W = torch.randn(2, 16, 32, generator=torch.Generator().manual_seed(1)).to(DEV)
     got = grads_of(inp, True, W, None)
-    want = oracle_grads(inp, True, W, None)
+    # the GPU's upstream gradient of a bf16 out is W rounded to bf16
+    want = oracle_grads(inp, True, W.bfloat16().float(), None)
     for k in want:
         assert got[k].dtype == inp[k].dtype, k
     check_grads(got, want, 2e-2, 2e-2)
@@ -197,8 +219,7 @@ def test_unequal_groups_and_input_independent_bc(case):
     grads = O.selective_scan_bwd(u, delta, A, B, C, D, z, bias, True, dout=G)
     for name, t, g in zip(["u", "delta", "A", "B", "C", "D", "z", "delta_bias"],
                           [u, delta, A, B, C, D, z, bias], grads):
-        scale = max(1.0, float(np.abs(g).max()))
-        close(t.grad / scale, g / scale, 1e-3, 1e-4, name)
+        close(t.grad, g, GRAD_RTOL, GRAD_ATOL[name], name)
 
 
 def decay_inputs(x, seqlen=4, dstate=8):
@@ -331,7 +352,7 @@ def test_larger_dstate(dstate):
     close(out, out_ref, 1e-4, 1e-5)
     close(last, last_ref, 1e-4, 1e-5)
     got = grads_of(inp, True, W, None)
-    check_grads(got, oracle_grads(inp, True, W, None), 1e-3, 1e-4)
+    check_grads(got, oracle_grads(inp, True, W, None))
 
 
 def test_version_and_device_check():
@@ -396,8 +417,12 @@ def test_long_sequence_time_chunks(seqlen, dtype):
     close(out, out_ref, *tol, "out")
     close(last, last_ref, 1e-4 if dtype == torch.float32 else 1e-2, 1e-5, "last_state")
     got = grads_of(inp, True, W, V)
-    want = oracle_grads(inp, True, W, V)
-    check_grads(got, want, *((1e-3, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)))
+    # the GPU's upstream gradient of a bf16 out is W rounded to bf16
+    want = oracle_grads(inp, True, W.to(dtype).float(), V)
+    if dtype == torch.float32:
+        check_grads(got, want)
+    else:
+        check_grads(got, want, 2e-2, 2e-2)
 
 
 def test_chunked_forward_matches_single_pass():
@@ -437,24 +462,25 @@ def test_chunked_forward_matches_single_pass():
     torch.testing.assert_close(outs[1][1], outs[0][1], rtol=1e-4, atol=1e-5)
 
 
-def test_chunked_backward_matches_oracle(monkeypatch):
-    """Batch 1, 48 channels, 4000 steps: the backward cuts time into chunks
-    (adjoint summaries carried across them, the carried decay being
-    exp(A * sum dt)) with 4-, 8- and 12-wave workgroups; the summary pass keeps
-    its own 4-wave channel blocks. Every width against the float64 oracle and
-    against the others."""
-    inp = make_inputs(1, 48, 4000, 16, None, True, True, True, torch.float32)
+@pytest.mark.parametrize("batch,dim,seqlen", [(1, 48, 4000), (2, 96, 160)])
+def test_backward_every_workgroup_width_matches_oracle(batch, dim, seqlen):
+    """The backward with 4-, 8- and 12-wave workgroups, pinned through the C
+    ABI's bwd_waves. Batch 1, 48 channels, 4000 steps is time-chunked
+    (adjoint summaries carried across chunks, the carried decay being
+    exp(A * sum dt); the summary pass keeps its own 4-wave channel blocks);
+    batch 2, 96 channels, 160 steps runs in one chunk, like the training-step
+    shape. Every width against the float64 oracle and against the others."""
+    from scan_abi import bwd as abi_bwd
+
+    inp = make_inputs(batch, dim, seqlen, 16, None, True, True, True, torch.float32)
     ops = torch.ops.mamba_cpu
     args = (inp["u"], inp["delta"], inp["A"], inp["B"][:, None].transpose(-1, -2),
             inp["C"][:, None].transpose(-1, -2), inp["D"], inp["z"], inp["delta_bias"], True)
     g = torch.Generator().manual_seed(11)
-    dout = torch.randn(1, 48, 4000, generator=g).to(DEV)
-    dlast = torch.randn(1, 48, 16, generator=g).to(DEV)
+    dout = torch.randn(batch, dim, seqlen, generator=g).to(DEV)
+    dlast = torch.randn(batch, dim, 16, generator=g).to(DEV)
     _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*args)
-    grads = []
-    for waves in ("4", "8", "12"):
-        monkeypatch.setenv("MCPU_SCAN_BWD_WAVES", waves)
-        grads.append(ops.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave))
+    grads = [abi_bwd(*args, dout, dlast, ckpt, ysave, waves=w) for w in (4, 8, 12)]
     torch.cuda.synchronize()
     want = O.selective_scan_bwd(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"],
                                 inp["z"], inp["delta_bias"], True, dout=dout, dlast_state=dlast)
@@ -462,8 +488,6 @@ def test_chunked_backward_matches_oracle(monkeypatch):
     for waves, got in zip((4, 8, 12), grads):
         for name, a, w in zip(names, got, want):
             w = w.swapaxes(-1, -2)[:, None] if name in ("B", "C") else w  # kernel layout (b, 1, l, n)
-            scale = max(float(np.abs(w).max()), 1.0)
-            close(a / scale, w / scale, 1e-3, 1e-4, f"{name} ({waves} waves)")
+            assert_close_report(a, w, GRAD_RTOL, GRAD_ATOL[name], f"{name} ({waves} waves)")
         for name, a, b in zip(names, got, grads[0]):
-            scale = max(b.abs().max().item(), 1.0)
-            torch.testing.assert_close(a / scale, b / scale, rtol=1e-4, atol=1e-5, msg=name)
+            assert_close_report(a, b, GRAD_RTOL, GRAD_ATOL[name], f"{name} ({waves} vs 4 waves)")
