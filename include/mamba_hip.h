@@ -154,6 +154,25 @@ size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);
 int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* Bytes of the per-device scratch array behind mcpu_selective_scan_bwd_noalloc. */
+#define MCPU_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* Backward that allocates nothing and takes no workspace. No counterpart in
+ * the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid allocation). It runs
+ * the kernels of mcpu_selective_scan_bwd with their scratch (partial sums,
+ * chunk summaries, and block checkpoints when ckpt is NULL) in a fixed
+ * library array of MCPU_NOALLOC_SCRATCH_BYTES per device, which each device
+ * holds from the first call on it until the process ends. Results equal
+ * mcpu_selective_scan_bwd's. Returns MCPU_ERR_UNSUPPORTED, before any device
+ * work, when mcpu_selective_scan_bwd_workspace_size(a) exceeds the array
+ * (the training-step shape batch 8, dim 1536, seqlen 1024, dstate 16 needs
+ * 35 MB with the forward's checkpoints given). Every call on one device
+ * shares that device's array: calls that overlap on one device (other
+ * streams, other threads) race and must be serialised by the caller. The
+ * first call on each device looks up the array's address; make it outside
+ * graph capture. */
+int mcpu_selective_scan_bwd_noalloc(const mcpu_scan_args* a, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Causal depthwise conv1d.                                                  */

@@ -3,6 +3,7 @@
 // from the caller.
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "abi_util.h"
 #include "scan_common.h"
@@ -449,3 +450,56 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
       "selective_scan_bwd reduce");
 }
 
+// ---- backward without allocation ------------------------------------------
+
+namespace mcpu {
+
+// Scratch of mcpu_selective_scan_bwd_noalloc, in place of a caller workspace.
+// Each device holds its own copy; host code must use the address
+// hipGetSymbolAddress returns for the current device, never this name.
+static __device__ __align__(256) unsigned char scratch[MCPU_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices];  // device address of `scratch` per device, once looked up
+
+// The current device's copy of `scratch`, looked up on the first call on
+// that device (with it current) and kept for the process.
+int scratch_address(void** out) {
+  int dev = 0;
+  if (int rc = hip_status(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan_bwd_noalloc: device index %d beyond %d", dev,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (int rc = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                            "selective_scan_bwd_noalloc: hipGetSymbolAddress"))
+      return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MCPU_OK;
+}
+
+}  // namespace
+}  // namespace mcpu
+
+extern "C" int mcpu_selective_scan_bwd_noalloc(const mcpu_scan_args* a, void* stream) {
+  clear_error();
+  if (int rc = check_scan(a)) return rc;
+  const size_t need = a->complex_a ? cbwd_layout(a).total : bwd_layout(a).total;
+  if (need > MCPU_NOALLOC_SCRATCH_BYTES)
+    return fail(MCPU_ERR_UNSUPPORTED,
+                "selective_scan_bwd_noalloc: needs %zu bytes of scratch, the library's array holds %zu; "
+                "use mcpu_selective_scan_bwd with a workspace",
+                need, (size_t)MCPU_NOALLOC_SCRATCH_BYTES);
+  if (int rc = mcpu_check_device()) return rc;
+  void* ws = nullptr;
+  if (need > 0)
+    if (int rc = scratch_address(&ws)) return rc;
+  return mcpu_selective_scan_bwd(a, ws, need > 0 ? (size_t)MCPU_NOALLOC_SCRATCH_BYTES : 0, stream);
+}

@@ -120,6 +120,8 @@ lib.mcpu_selective_scan_bwd_workspace_size.argtypes = [_ARGP["scan"]]
 lib.mcpu_selective_scan_bwd_workspace_size.restype = ctypes.c_size_t
 lib.mcpu_selective_scan_bwd.argtypes = [_ARGP["scan"], _P, ctypes.c_size_t, _P]
 lib.mcpu_selective_scan_bwd.restype = ctypes.c_int
+lib.mcpu_selective_scan_bwd_noalloc.argtypes = [_ARGP["scan"], _P]
+lib.mcpu_selective_scan_bwd_noalloc.restype = ctypes.c_int
 lib.mcpu_causal_conv1d_fwd.argtypes = [_ARGP["conv"], _P]
 lib.mcpu_causal_conv1d_fwd.restype = ctypes.c_int
 lib.mcpu_causal_conv1d_bwd_workspace_size.argtypes = [_ARGP["conv"]]
