@@ -1,23 +1,29 @@
-"""Run Hugging Face transformers Mamba models on mamba_cpu's MI355X ops.
+"""Hugging Face transformers' Mamba-family models on this package's GPU ops.
 
     import mamba_cpu.hf
     mamba_cpu.hf.patch_transformers()
     model = transformers.MambaForCausalLM(config).to("cuda")
 
-Same mechanism and surface as the reference's src/mamba_cpu/hf.py:26-112:
-transformers (>= 5) resolves `mamba_selective_scan`,
-`mamba_selective_state_update`, `causal_conv1d_fn`, `causal_conv1d_update` and
-`mamba_inner_fn` from module globals at call time, and patch_transformers()
-wraps those globals. The wrappers route calls whose first tensor is on a ROCm
-GPU ("cuda" device type) to this package's gfx950 custom ops; tensors on other
-devices keep transformers' own path. `mamba_inner_fn`, which the reference
-answers with None (so its mixers always take their unfused path), is the
-fused mixer of mamba_cpu.ops.mamba_inner for float32 models on the GPU, and
-None otherwise.
+How transformers (>= 5) reaches its kernels: each Mamba-family modeling
+module defines five kernel functions as module globals (mamba_selective_scan,
+mamba_selective_state_update, causal_conv1d_fn, causal_conv1d_update,
+mamba_inner_fn) and its mixers look them up by name on every call. The
+reference hooks the same five globals (src/mamba_cpu/hf.py:63-112), which is
+why the hook points, the three public names and the parameter lists below are
+what they are.
+
+patch_transformers() puts a DeviceRoute in each global: a call whose leading
+tensor is on a ROCm GPU (torch's "cuda" device type) runs this package's op,
+any other call the function the route replaced, so CPU models keep
+transformers' own path. mamba_inner_fn, which the reference answers with
+None so that mixers take their unfused path, is the fused mixer of
+mamba_cpu.ops.mamba_inner for float32 Mamba models in training, and None
+where that mixer does not apply.
 """
 
-import functools
 import importlib
+
+import torch
 
 from mamba_cpu.ops import (
     causal_conv1d_fn,
@@ -28,106 +34,119 @@ from mamba_cpu.ops import (
 from mamba_cpu.ops.mamba_inner import fused_path_supported, mamba_inner_fn
 
 SUPPORTED_MODELS = ("mamba", "falcon_mamba", "jamba")
-_DEVICE_TYPE = "cuda"  # ROCm GPUs report the "cuda" device type in PyTorch
 
 
-def _scan(
-    hidden_states,
-    dt,
-    A,
-    B,
-    C,
-    D=None,
-    z=None,
-    delta_bias=None,
-    delta_softplus=False,
-    return_last_state=False,
-    **kwargs,  # use_mambapy, use_associative_scan select transformers' own fallbacks
-):
-    return selective_scan_fn(
-        hidden_states, dt, A, B, C, D, z, delta_bias, delta_softplus, return_last_state
-    )
+# GPU bodies of transformers' kernel globals. Each takes the parameter list of
+# the function it stands in for (transformers' modeling_mamba.py defines
+# them); keywords that only choose among transformers' own torch fallbacks
+# (use_mambapy, use_associative_scan, ...) arrive in **options and are moot
+# here.
 
 
-def _state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, dt_softplus=False, **kwargs):
-    return selective_state_update(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus)
+def gpu_selective_scan(hidden_states, dt, A, B, C, D=None, z=None, delta_bias=None,
+                       delta_softplus=False, return_last_state=False, **options):
+    return selective_scan_fn(hidden_states, dt, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                             delta_softplus=delta_softplus, return_last_state=return_last_state)
 
 
-def _conv(x, weight, bias=None, activation=None, **kwargs):
-    return causal_conv1d_fn(x, weight, bias, activation=activation)
+def gpu_selective_state_update(state, hidden_states, dt, A, B, C, D=None, dt_bias=None,
+                               dt_softplus=False, z=None, **options):
+    # transformers orders (D, dt_bias, dt_softplus, z); the op's own order is (D, z, dt_bias, dt_softplus)
+    return selective_state_update(state, hidden_states, dt, A, B, C, D=D, z=z, dt_bias=dt_bias,
+                                  dt_softplus=dt_softplus)
 
 
-def _conv_update(x, conv_state, weight, bias=None, activation=None, **kwargs):
-    return causal_conv1d_update(x, conv_state, weight, bias, activation)
+def gpu_causal_conv1d(hidden_states, weight, bias=None, activation=None, **options):
+    return causal_conv1d_fn(hidden_states, weight, bias, activation=activation)
 
 
-def _inner(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
-           out_proj_bias, A, B=None, C=None, D=None, delta_bias=None, delta_softplus=True,
-           b_rms_weight=None, c_rms_weight=None, dt_rms_weight=None, b_c_dt_rms_eps=1e-6, **kwargs):
-    # The fused mixer (mamba_cpu.ops.mamba_inner) where it applies; None
-    # otherwise, and the mixer takes its unfused path, which calls the four
-    # ops above (the reference always answers None, hf.py:59-60).
-    # FalconMamba passes norm weights: its unfused path normalises dt before
-    # dt_proj and ignores the weights, where mamba_inner_fn's norms (as in
-    # mamba_ssm) normalise delta after it, so that model keeps the unfused
-    # path, which is the computation the reference runs.
-    if any(w is not None for w in (b_rms_weight, c_rms_weight, dt_rms_weight)):
+def gpu_causal_conv1d_update(hidden_states, conv_state, weight, bias=None, activation=None, **options):
+    return causal_conv1d_update(hidden_states, conv_state, weight, bias, activation=activation)
+
+
+def gpu_mamba_inner(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                    out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
+                    delta_softplus=True, b_rms_weight=None, c_rms_weight=None, dt_rms_weight=None,
+                    b_c_dt_rms_eps=1e-6, **options):
+    """The fused mixer where it applies; None otherwise, which sends the mixer
+    down its unfused path (through the four ops above).
+
+    FalconMamba passes RMS-norm weights: its unfused path normalises dt
+    before dt_proj, where the fused mixer's norms (mamba_ssm's) normalise
+    delta after it. Such calls answer None, so that model computes what the
+    reference computes."""
+    if b_rms_weight is not None or c_rms_weight is not None or dt_rms_weight is not None:
         return None
     if not fused_path_supported(xz, conv1d_weight, x_proj_weight, delta_proj_weight, out_proj_weight,
                                 A, B, C):
         return None
     return mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                           out_proj_weight, out_proj_bias, A, D=D, delta_bias=delta_bias,
-                          delta_softplus=delta_softplus, b_rms_weight=b_rms_weight,
-                          c_rms_weight=c_rms_weight, dt_rms_weight=dt_rms_weight,
-                          b_c_dt_rms_eps=b_c_dt_rms_eps)
+                          delta_softplus=delta_softplus)
 
 
-_OPS = {
-    "mamba_selective_scan": _scan,
-    "mamba_selective_state_update": _state_update,
-    "causal_conv1d_fn": _conv,
-    "causal_conv1d_update": _conv_update,
-    "mamba_inner_fn": _inner,
+# transformers global -> the GPU body that routes take for it
+KERNEL_GLOBALS = {
+    "mamba_selective_scan": gpu_selective_scan,
+    "mamba_selective_state_update": gpu_selective_state_update,
+    "causal_conv1d_fn": gpu_causal_conv1d,
+    "causal_conv1d_update": gpu_causal_conv1d_update,
+    "mamba_inner_fn": gpu_mamba_inner,
 }
 
 
-def _dispatch(original, native):
-    @functools.wraps(original)
-    def wrapper(first, *args, **kwargs):
-        fn = native if first.device.type == _DEVICE_TYPE else original
-        return fn(first, *args, **kwargs)
+class DeviceRoute:
+    """Stands in for one of transformers' kernel globals. A call whose first
+    positional argument is a tensor on a ROCm GPU goes to `gpu`; every other
+    call goes to `fallback`, the function this route replaced (reachable as
+    __wrapped__ too)."""
 
-    wrapper._mamba_cpu_original = original
-    return wrapper
+    def __init__(self, fallback, gpu):
+        self.fallback = fallback
+        self.gpu = gpu
+        self.__wrapped__ = fallback
+        self.__name__ = getattr(fallback, "__name__", gpu.__name__)
+        self.__doc__ = getattr(fallback, "__doc__", None)
+
+    def __call__(self, *args, **kwargs):
+        lead = args[0] if args else None
+        on_gpu = isinstance(lead, torch.Tensor) and lead.device.type == "cuda"
+        return (self.gpu if on_gpu else self.fallback)(*args, **kwargs)
+
+    def __repr__(self):
+        return f"DeviceRoute({self.__name__}: ROCm GPU -> mamba_cpu, else -> transformers)"
 
 
-def _modeling_module(name):
-    return importlib.import_module(f"transformers.models.{name}.modeling_{name}")
+def _modeling(family):
+    return importlib.import_module(f".modeling_{family}", f"transformers.models.{family}")
 
 
 def patch_transformers(models=SUPPORTED_MODELS):
-    """Route ROCm-GPU execution of the given transformers model families
-    through mamba_cpu. Safe to call repeatedly."""
-    modules = [_modeling_module(name) for name in models]
+    """Route ROCm-GPU calls of the given model families' kernels to this
+    package. Calling it again changes nothing. Raises RuntimeError, and
+    patches nothing, if a family's modeling module lacks one of the five
+    globals (transformers older than 5)."""
+    modules = [_modeling(family) for family in models]
+    gaps = []
     for module in modules:
-        missing = [op for op in _OPS if not hasattr(module, op)]
-        if missing:
-            raise RuntimeError(
-                f"{module.__name__} has no {', '.join(missing)}; mamba_cpu.hf needs transformers >= 5"
-            )
+        absent = [name for name in KERNEL_GLOBALS if not hasattr(module, name)]
+        if absent:
+            gaps.append(f"{module.__name__} ({', '.join(absent)})")
+    if gaps:
+        raise RuntimeError("mamba_cpu.hf works with transformers >= 5, whose Mamba modeling modules "
+                           "define the kernel globals it routes; missing in " + "; ".join(gaps))
     for module in modules:
-        for op, native in _OPS.items():
-            original = getattr(module, op)
-            if not hasattr(original, "_mamba_cpu_original"):
-                setattr(module, op, _dispatch(original, native))
+        for name, body in KERNEL_GLOBALS.items():
+            current = getattr(module, name)
+            if not isinstance(current, DeviceRoute):
+                setattr(module, name, DeviceRoute(current, body))
 
 
 def unpatch_transformers(models=SUPPORTED_MODELS):
-    """Undo patch_transformers."""
-    for name in models:
-        module = _modeling_module(name)
-        for op in _OPS:
-            original = getattr(getattr(module, op), "_mamba_cpu_original", None)
-            if original is not None:
-                setattr(module, op, original)
+    """Put back the functions patch_transformers() replaced."""
+    for family in models:
+        module = _modeling(family)
+        for name in KERNEL_GLOBALS:
+            current = getattr(module, name, None)
+            if isinstance(current, DeviceRoute):
+                setattr(module, name, current.fallback)

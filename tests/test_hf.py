@@ -1,11 +1,20 @@
-"""mamba_cpu.hf against transformers' own pure-torch fallbacks, on small random
-models (the cases of the reference's tests/test_hf.py, on the GPU), and the
-graph-replayed greedy decoder (mamba_cpu.decode) against model.generate.
+"""mamba_cpu.hf on small random Mamba, FalconMamba and Jamba models.
 
-The baseline runs the same model on the same GPU through transformers'
-fallback functions (pinned through `__wrapped__`, as the reference's tests
-pin them); the patched run goes through this package's HIP ops."""
+Each check runs one model twice on the GPU: first on transformers' own
+pure-torch kernel functions (the functions the routes replace, reached
+through __wrapped__), then with patch_transformers() routing the kernels to
+this package's HIP ops, and compares the two. The cases are those of the
+reference's tests/test_hf.py: logits, greedy generation, a padded batch,
+training gradients, patching twice and undoing it, models on other devices
+left alone, a patched model used as installed. Beyond them: the
+graph-replayed greedy decoder (mamba_cpu.decode) against model.generate, and
+a two-layer model of the Mamba-130M width (d_model 768, vocabulary 50280)
+checked with the reference's model-level measures (largest logit
+difference, top-1 agreement, greedy identity, per-tensor gradient error:
+benchmarks/check_hf_model.py:105-121).
+"""
 
+import contextlib
 import importlib
 
 import pytest
@@ -16,147 +25,178 @@ pytest.importorskip("transformers", minversion="5.0")
 import transformers
 
 import mamba_cpu.hf
-from mamba_cpu import selective_scan_fn
 
-SMALL = dict(vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=8, conv_kernel=4, expand=2)
+FAMILIES = mamba_cpu.hf.SUPPORTED_MODELS
 DEV = "cuda"
+TINY = dict(vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=8, conv_kernel=4, expand=2)
 
 
-def build(name, dev=DEV):
+def tiny_model(family, device=DEV):
     torch.manual_seed(0)
-    if name == "mamba":
-        model = transformers.MambaForCausalLM(transformers.MambaConfig(**SMALL))
-    elif name == "falcon_mamba":
-        model = transformers.FalconMambaForCausalLM(transformers.FalconMambaConfig(**SMALL))
-    else:
-        config = transformers.JambaConfig(
-            vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
-            num_key_value_heads=2, num_experts=1, attn_layer_period=2, attn_layer_offset=1,
-            expert_layer_period=2, expert_layer_offset=1, mamba_d_state=8, mamba_dt_rank=4,
-            use_mamba_kernels=False,
-        )
-        model = transformers.JambaForCausalLM(config)
-    return model.to(dev).eval()
+    if family == "mamba":
+        model = transformers.MambaForCausalLM(transformers.MambaConfig(**TINY))
+    elif family == "falcon_mamba":
+        model = transformers.FalconMambaForCausalLM(transformers.FalconMambaConfig(**TINY))
+    else:  # a Mamba layer then an attention layer, one expert
+        model = transformers.JambaForCausalLM(transformers.JambaConfig(
+            vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=2,
+            num_attention_heads=2, num_key_value_heads=2, num_experts=1, attn_layer_period=2,
+            attn_layer_offset=1, expert_layer_period=2, expert_layer_offset=1, mamba_d_state=8,
+            mamba_dt_rank=4, use_mamba_kernels=False))
+    return model.to(device).eval()
 
 
-@pytest.fixture
-def patched(monkeypatch):
-    """Runs fn on transformers' pure-torch fallbacks, then on mamba_cpu."""
+def token_ids(shape, device=DEV, vocab=64, seed=1):
+    return torch.randint(0, vocab, shape, generator=torch.Generator().manual_seed(seed)).to(device)
+
+
+def _modules():
+    return [importlib.import_module(f".modeling_{f}", f"transformers.models.{f}") for f in FAMILIES]
+
+
+@contextlib.contextmanager
+def torch_kernels():
+    """transformers' pure-torch kernel functions in every family's globals
+    (the plain functions its hub/fallback decorator wraps), restored after."""
     mamba_cpu.hf.unpatch_transformers()
-    for name in mamba_cpu.hf.SUPPORTED_MODELS:
-        module = importlib.import_module(f"transformers.models.{name}.modeling_{name}")
-        for op in mamba_cpu.hf._OPS:
-            monkeypatch.setattr(module, op, getattr(module, op).__wrapped__)
+    saved = []
+    for module in _modules():
+        for name in mamba_cpu.hf.KERNEL_GLOBALS:
+            fn = getattr(module, name)
+            saved.append((module, name, fn))
+            setattr(module, name, getattr(fn, "__wrapped__", fn))
+    try:
+        yield
+    finally:
+        for module, name, fn in saved:
+            setattr(module, name, fn)
 
-    def run_both(fn):
-        want = fn()
+
+@contextlib.contextmanager
+def gpu_kernels():
+    """Those same globals routed to this package (patched over the pure-torch
+    functions, so nothing but this package's ops can run on the GPU)."""
+    with torch_kernels():
         mamba_cpu.hf.patch_transformers()
         try:
-            return fn(), want
+            yield
         finally:
             mamba_cpu.hf.unpatch_transformers()
 
-    return run_both
+
+def torch_then_gpu(fn):
+    """(fn() on this package's ops, fn() on transformers' torch kernels)."""
+    with torch_kernels():
+        want = fn()
+    with gpu_kernels():
+        got = fn()
+    return got, want
 
 
 @pytest.fixture
-def scan_calls(monkeypatch):
-    """Counts scans through this package: the scan op, or the fused mixer
-    (mamba_inner_fn) that transformers' Mamba mixers call in training."""
-    calls = []
-    monkeypatch.setattr(
-        mamba_cpu.hf, "selective_scan_fn", lambda *a: calls.append(1) or selective_scan_fn(*a)
-    )
-    fused = mamba_cpu.hf.mamba_inner_fn
-    monkeypatch.setattr(
-        mamba_cpu.hf, "mamba_inner_fn", lambda *a, **k: calls.append(2) or fused(*a, **k)
-    )
-    return calls
+def calls(monkeypatch):
+    """Names of the GPU bodies the routes ran, in order."""
+    seen = []
+
+    def counted(name, body):
+        def run(*args, **kwargs):
+            seen.append(name)
+            return body(*args, **kwargs)
+        return run
+
+    for name, body in list(mamba_cpu.hf.KERNEL_GLOBALS.items()):
+        monkeypatch.setitem(mamba_cpu.hf.KERNEL_GLOBALS, name, counted(name, body))
+    return seen
 
 
-models = pytest.mark.parametrize("name", mamba_cpu.hf.SUPPORTED_MODELS)
+def used_the_scan(seen):
+    # the scan itself, or the fused mixer (which runs it) in training
+    return "mamba_selective_scan" in seen or "mamba_inner_fn" in seen
 
 
-def _ids(shape, dev=DEV):
-    g = torch.Generator().manual_seed(1)
-    return torch.randint(0, 64, shape, generator=g).to(dev)
+per_family = pytest.mark.parametrize("family", FAMILIES)
 
 
 @pytest.mark.gpu
-@models
-def test_logits_match(name, patched, scan_calls):
-    model = build(name)
-    ids = _ids((2, 37))
-
-    def logits():
-        with torch.no_grad():
-            return model(ids).logits
-
-    got, want = patched(logits)
-    assert scan_calls, "patched scan was not used"
+@per_family
+def test_logits_match(family, calls):
+    model = tiny_model(family)
+    ids = token_ids((2, 37))
+    got, want = torch_then_gpu(lambda: model(ids).logits.detach())
+    assert used_the_scan(calls)
     torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
 
 
 @pytest.mark.gpu
-@models
-def test_generate_matches(name, patched, scan_calls):
-    model = build(name)
-    ids = _ids((2, 11))
-    got, want = patched(lambda: model.generate(ids, max_new_tokens=12, do_sample=False))
-    assert scan_calls
+@per_family
+def test_greedy_generation_matches(family, calls):
+    model = tiny_model(family)
+    ids = token_ids((2, 11))
+    got, want = torch_then_gpu(lambda: model.generate(ids, max_new_tokens=12, do_sample=False))
+    assert used_the_scan(calls) and "mamba_selective_state_update" in calls
     assert torch.equal(got, want)
 
 
 @pytest.mark.gpu
-@models
-def test_padded_batch_matches(name, patched):
-    model = build(name)
-    ids = _ids((2, 16))
+@per_family
+def test_left_padded_batch_matches(family):
+    model = tiny_model(family)
+    ids = token_ids((2, 16))
     mask = torch.ones_like(ids)
     mask[1, :5] = 0
-
-    def logits():
-        with torch.no_grad():
-            return model(ids, attention_mask=mask).logits
-
-    got, want = patched(logits)
+    got, want = torch_then_gpu(lambda: model(ids, attention_mask=mask).logits.detach())
     torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
 
 
 @pytest.mark.gpu
-@models
-def test_training_gradients_match(name, patched, scan_calls):
-    model = build(name).train()
-    ids = _ids((2, 24))
+@per_family
+def test_training_gradients_match(family, calls):
+    model = tiny_model(family).train()
+    ids = token_ids((2, 24))
 
     def grads():
         model.zero_grad()
         model(ids, labels=ids).loss.backward()
         return {k: p.grad.clone() for k, p in model.named_parameters() if p.grad is not None}
 
-    got, want = patched(grads)
-    assert scan_calls and got.keys() == want.keys()
-    if name == "mamba":  # FalconMamba keeps its unfused path (its norms differ from the fused ones)
-        assert 2 in scan_calls, "the fused mixer was not used"
-    for k in want:
-        torch.testing.assert_close(got[k], want[k], rtol=1e-3, atol=1e-4, msg=lambda m: f"{k}: {m}")
+    got, want = torch_then_gpu(grads)
+    assert got.keys() == want.keys() and used_the_scan(calls)
+    if family == "mamba":
+        # float32 Mamba in training takes the fused mixer; FalconMamba keeps
+        # its unfused path (its norms differ from the fused mixer's)
+        assert "mamba_inner_fn" in calls and "mamba_selective_scan" not in calls
+    for k, w in want.items():
+        torch.testing.assert_close(got[k], w, rtol=1e-3, atol=1e-4, msg=lambda m: f"{k}: {m}")
 
 
-def test_patch_is_idempotent_and_reversible():
+def test_patching_twice_changes_nothing_and_unpatch_restores():
     module = importlib.import_module("transformers.models.mamba.modeling_mamba")
-    original = module.mamba_selective_scan
+    before = {name: getattr(module, name) for name in mamba_cpu.hf.KERNEL_GLOBALS}
     mamba_cpu.hf.patch_transformers()
-    patched_fn = module.mamba_selective_scan
-    mamba_cpu.hf.patch_transformers()
-    assert module.mamba_selective_scan is patched_fn is not original
-    mamba_cpu.hf.unpatch_transformers()
-    assert module.mamba_selective_scan is original
+    try:
+        first = {name: getattr(module, name) for name in before}
+        assert all(isinstance(r, mamba_cpu.hf.DeviceRoute) for r in first.values())
+        mamba_cpu.hf.patch_transformers()
+        assert all(getattr(module, name) is first[name] for name in before)
+        assert all(first[name].fallback is before[name] for name in before)
+    finally:
+        mamba_cpu.hf.unpatch_transformers()
+    assert all(getattr(module, name) is fn for name, fn in before.items())
 
 
-def test_cpu_tensors_keep_transformers_path(scan_calls):
-    # The routing predicate: tensors on other devices keep transformers' own ops.
-    model = build("mamba", dev="cpu")
-    ids = _ids((1, 9), dev="cpu")
+def test_patch_refuses_modules_without_the_kernel_globals(monkeypatch):
+    module = importlib.import_module("transformers.models.mamba.modeling_mamba")
+    monkeypatch.delattr(module, "mamba_inner_fn")
+    falcon = importlib.import_module("transformers.models.falcon_mamba.modeling_falcon_mamba")
+    before = falcon.mamba_selective_scan
+    with pytest.raises(RuntimeError, match="transformers >= 5"):
+        mamba_cpu.hf.patch_transformers()
+    assert falcon.mamba_selective_scan is before  # nothing was patched
+
+
+def test_models_on_other_devices_keep_transformers_kernels(calls):
+    model = tiny_model("mamba", device="cpu")
+    ids = token_ids((1, 9), device="cpu")
     with torch.no_grad():
         want = model(ids).logits
     mamba_cpu.hf.patch_transformers()
@@ -165,15 +205,18 @@ def test_cpu_tensors_keep_transformers_path(scan_calls):
             got = model(ids).logits
     finally:
         mamba_cpu.hf.unpatch_transformers()
-    assert not scan_calls
-    torch.testing.assert_close(got, want, rtol=0, atol=0)
+    assert calls == []
+    assert torch.equal(got, want)
 
 
 @pytest.mark.gpu
-@models
-def test_patched_model_runs_as_installed(name, scan_calls):
-    model = build(name)
-    ids = _ids((1, 9))
+@per_family
+def test_patched_model_used_as_installed(family, calls):
+    """patch_transformers() over whatever transformers installed (no pinning
+    of its fallbacks): generation and a training step run through this
+    package."""
+    model = tiny_model(family)
+    ids = token_ids((1, 9))
     mamba_cpu.hf.patch_transformers()
     try:
         model.generate(ids, max_new_tokens=3, do_sample=False)
@@ -181,49 +224,78 @@ def test_patched_model_runs_as_installed(name, scan_calls):
         model(ids, labels=ids).loss.backward()
     finally:
         mamba_cpu.hf.unpatch_transformers()
-    assert scan_calls
+    assert used_the_scan(calls)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["mamba", "falcon_mamba"])
-def test_graphed_greedy_matches_generate(name):
+@pytest.mark.parametrize("family", ["mamba", "falcon_mamba"])
+def test_graph_replayed_greedy_equals_generate(family):
     import mamba_cpu.decode
 
-    model = build(name)
-    ids = _ids((3, 7))
-    mamba_cpu.hf.patch_transformers()
-    try:
+    model = tiny_model(family)
+    ids = token_ids((3, 7))
+    with gpu_kernels():
         want = model.generate(ids, max_new_tokens=20, min_new_tokens=20, do_sample=False)
         got = mamba_cpu.decode.greedy_generate(model, ids, 20)
-    finally:
-        mamba_cpu.hf.unpatch_transformers()
     assert torch.equal(got, want)
 
 
 @pytest.mark.gpu
-def test_graph_replays_match_eager_steps():
-    # Every replay against the eager step on the same token and cache, with
-    # eager work and synchronisations between the replays.
+def test_each_graph_replay_equals_the_eager_step():
+    """Every replay of the captured decode step against the eager step on the
+    same token and cache, with eager work and synchronisations between
+    replays."""
     import mamba_cpu.decode
 
-    model = build("mamba")
-    ids = _ids((2, 9))
-    toks = _ids((2, 12))
-    mamba_cpu.hf.patch_transformers()
-    try:
-        with torch.no_grad():
-            cache = model(ids, use_cache=True).cache_params
-            eager = []
-            for i in range(toks.shape[1]):
-                eager.append(model(input_ids=toks[:, i:i + 1], cache_params=cache, use_cache=True)
-                             .logits[:, -1].clone())
-            cache = model(ids, use_cache=True).cache_params
-            step = mamba_cpu.decode.GraphedDecodeStep(model, cache, 2)
-            for i in range(toks.shape[1]):
-                step.token.copy_(toks[:, i:i + 1])
-                got = step.replay().clone()
-                if i % 3 == 0:
-                    torch.cuda.synchronize()
-                torch.testing.assert_close(got, eager[i], rtol=0, atol=0, msg=lambda m: f"step {i}: {m}")
-    finally:
-        mamba_cpu.hf.unpatch_transformers()
+    model = tiny_model("mamba")
+    prompt, steps = token_ids((2, 9)), token_ids((2, 12), seed=2)
+    with gpu_kernels(), torch.no_grad():
+        cache = model(prompt, use_cache=True).cache_params
+        eager = [model(input_ids=steps[:, i:i + 1], cache_params=cache, use_cache=True).logits[:, -1].clone()
+                 for i in range(steps.shape[1])]
+        graphed = mamba_cpu.decode.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 2)
+        for i in range(steps.shape[1]):
+            graphed.token.copy_(steps[:, i:i + 1])
+            got = graphed.replay().clone()
+            if i % 3 == 0:
+                torch.cuda.synchronize()
+            assert torch.equal(got, eager[i]), f"replay {i}"
+
+
+@pytest.mark.gpu
+def test_mamba_130m_width_two_layers_agrees_with_transformers():
+    """Two layers of the Mamba-130M architecture (d_model 768, d_inner 1536,
+    dstate 16, dt_rank 48, conv width 4, vocabulary 50280), random init,
+    float32: prefill logits of 2 x 256 random tokens, 16 greedy steps, and a
+    training step of 2 x 128, on this package against transformers' torch
+    kernels. Bounds: largest |logit difference| 1e-3 (logits reach a few
+    units), top-1 agreement at every position, identical greedy tokens, and a
+    worst per-tensor gradient error max|dg| / max|g| of 1e-4."""
+    torch.manual_seed(0)
+    cfg = transformers.MambaConfig(num_hidden_layers=2, hidden_size=768, state_size=16, expand=2,
+                                   conv_kernel=4, vocab_size=50280)
+    model = transformers.MambaForCausalLM(cfg).to(DEV).eval()
+    ids = token_ids((2, 256), vocab=50280)
+    got, want = torch_then_gpu(lambda: model(ids).logits.detach())
+    dlogit = (got - want).abs().max().item()
+    top1 = (got.argmax(-1) == want.argmax(-1)).float().mean().item()
+    print(f"  max|dlogit| {dlogit:.3g} (max|logit| {want.abs().max().item():.3g}), top-1 agreement {top1}")
+    assert dlogit < 1e-3 and top1 == 1.0
+    gen, gen_want = torch_then_gpu(lambda: model.generate(ids[:, :32], max_new_tokens=16,
+                                                          min_new_tokens=16, do_sample=False))
+    assert torch.equal(gen, gen_want)
+    model.train()
+    train_ids = ids[:, :128]
+
+    def step():
+        model.zero_grad()
+        loss = model(train_ids, labels=train_ids).loss
+        loss.backward()
+        return loss.item(), {k: p.grad.clone() for k, p in model.named_parameters() if p.grad is not None}
+
+    (loss, grads), (loss_want, grads_want) = torch_then_gpu(step)
+    worst = max(((grads[k] - g).abs().max() / g.abs().max().clamp_min(1e-12)).item()
+                for k, g in grads_want.items())
+    print(f"  train loss {loss:.6f} vs {loss_want:.6f}, worst per-tensor gradient error {worst:.3g}")
+    assert abs(loss - loss_want) <= 1e-5 * abs(loss_want)
+    assert worst < 1e-4
