@@ -40,6 +40,12 @@ for _p in (os.path.join(ROOT, "mamba-cpu_amd"), ROOT):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+# Vector-ALU issue peak: one wave64 VALU instruction per CU per cycle (four
+# 16-lane SIMDs, four cycles each), 256 CUs at the 2.4 GHz peak clock.
+VALU_PEAK_G = 256 * 2.4
+# Counter readings of the training-step backward launch (rocprofv3 --pmc),
+# summarised in profiles/.
+COUNTERS_JSON = "scan_bwd_b8_d1536_l1024_n16_counters.json"
 METRIC = "selective_scan fwd+bwd HBM GB/s & % peak; Mamba-130M prefill tokens/s"
 B_, D_, L_, N_, G_ = 8, 1536, 1024, 16, 1
 
@@ -75,16 +81,17 @@ def _cpu_threads():
     return int(os.environ.get("MCPU_BENCH_CPU_THREADS", min(os.cpu_count() or 1, 16)))
 
 
-def cpu_scan_ms(inputs, gout, softplus, fwd_only=False, iters=3):
+def cpu_scan_ms(inputs, gout, softplus, fwd_only=False, iters=3, threads=None):
     """Milliseconds per call of the reference's CPU kernels
     (csrc/selective_scan.cpp, built from source into oracle/_ref) on the same
-    inputs: forward, or forward + backward. Warm-up 1, then `iters` timed
-    calls, as the reference's benchmarks/bench_selective_scan.py:16-22 does."""
+    inputs: forward, or forward + backward, at `threads` threads
+    (_cpu_threads() by default). Warm-up 1, then `iters` timed calls, as the
+    reference's benchmarks/bench_selective_scan.py:16-22 does."""
     from oracle import ref as R
 
     if not R.available():
         return None
-    threads = _cpu_threads()
+    threads = threads or _cpu_threads()
     a = {k: None if v is None else v.detach().float().cpu().numpy() for k, v in inputs.items()}
     Bk, Ck = R.kernel_bc(a["B"]), R.kernel_bc(a["C"])
     dout = None if gout is None else gout.float().cpu().numpy()
@@ -103,14 +110,29 @@ def cpu_scan_ms(inputs, gout, softplus, fwd_only=False, iters=3):
     return round((time.perf_counter() - t0) / iters * 1e3, 3)
 
 
-def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes):
-    """The reference's CPU kernels on the full training-step workload."""
+def host_cpus():
+    """Logical CPUs of the host, and those this process may run on."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"logical": os.cpu_count(), "usable": usable}
+
+
+def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes, extra):
+    """The reference's CPU kernels on the full training-step workload, at
+    _cpu_threads() threads; also at 8 threads (the reference README's
+    comparison point, README.md:33-39) into extra["cpu_reference_8_threads"]."""
     from oracle import ref as R
 
     iters = 3
     ms = cpu_scan_ms(inputs, gout, True, iters=iters)
     if ms is None:
         return None
+    ms8 = cpu_scan_ms(inputs, gout, True, iters=iters, threads=8)
+    extra["cpu_reference_8_threads"] = {
+        "ms_per_fwd_bwd": ms8, "GBps": round((fwd_bytes + bwd_bytes) / (ms8 * 1e-3) / 1e9, 3),
+        "threads": 8}
     return {
         "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 3),
         "unit": "GB/s",
@@ -119,6 +141,31 @@ def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes):
         "sample": f"the full workload (batch {B_}, dim {D_}, seqlen {L_}, dstate {N_}, fp32, fwd+bwd), "
                   f"1 warm-up + {iters} timed iterations, {R.cpu_isa()} kernels; "
                   f"{ms:.1f} ms per fwd+bwd",
+    }
+
+
+def valu_roofline(launch_ms, counters):
+    """The vector-ALU ceiling of the backward launch: the issue slots it
+    needs per launch (VALU wave-instructions from the committed counters,
+    plus one more slot per v_exp_f32, which issues at half rate) over the
+    launch time measured in this run, against VALU_PEAK_G. Also the slots per
+    (batch, channel, step, state) element. None without committed counters."""
+    slots = counters.get("valu_issue_slots_per_launch")
+    if not slots:
+        return None
+    rate = slots / (launch_ms * 1e-3) / 1e9
+    return {
+        "issue_slots": slots,
+        "valu_wave_instructions": counters.get("valu_wave_instructions_per_launch"),
+        "achieved": round(rate, 1),
+        "peak": VALU_PEAK_G,
+        "unit": "G wave-instructions/s",
+        "frac": round(rate / VALU_PEAK_G, 4),
+        "per_state_step": round(counters.get("valu_wave_instructions_per_launch", 0) * 64
+                                / (B_ * D_ * L_ * N_), 2),
+        "note": "peak at the 2.4 GHz peak clock; the chip runs at about 2.1 GHz under this load, "
+                "so the attainable fraction is about 0.88",
+        "source": "profiles/" + COUNTERS_JSON,
     }
 
 
@@ -448,25 +495,42 @@ def other_configs(torch, dev, stream, cpu):
     return res
 
 
-def mamba130m(torch, dev, iters=3):
+MAMBA130M = dict(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2, conv_kernel=4,
+                 vocab_size=50280)
+
+
+def _mamba130m_model(torch):
+    """The random-init Mamba-130M architecture, built on the CPU from seed 0,
+    so the GPU and CPU legs hold the same weights."""
+    import transformers
+
+    torch.manual_seed(0)
+    return transformers.MambaForCausalLM(transformers.MambaConfig(**MAMBA130M))
+
+
+def _mamba130m_ids(torch):
+    """Prefill ids (4, 1024), uniform over the vocabulary, seed 1, on the CPU:
+    both legs use these; the decode prompt is their first 16 columns and the
+    training batch their first 256."""
+    return torch.randint(0, MAMBA130M["vocab_size"], (4, 1024), generator=torch.Generator().manual_seed(1))
+
+
+def mamba130m(torch, dev, keep, iters=3):
     """Random-init Mamba-1 130M architecture (24 layers, d_model 768, d_inner
     1536, dstate 16, dt_rank 48, conv width 4, vocab 50280), fp32, through the
     patched Hugging Face model: prefill 4 x 1024 tokens, 128 greedy decode
     steps from a 4 x 16 prompt, and one training step (forward + backward) at
-    4 x 256 with labels = ids."""
-    import transformers
-
+    4 x 256 with labels = ids. `keep` receives the prefill logits, the greedy
+    tokens, the training loss and gradients (on the host) for the agreement
+    check against the CPU leg."""
     import mamba_cpu.hf
 
     mamba_cpu.hf.patch_transformers()
-    torch.manual_seed(0)
-    cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
-                                   conv_kernel=4, vocab_size=50280)
-    model = transformers.MambaForCausalLM(cfg).to(dev).eval()
+    model = _mamba130m_model(torch).to(dev).eval()
     res = {}
-    ids = torch.randint(0, 50280, (4, 1024), device=dev)
+    ids = _mamba130m_ids(torch).to(dev)
     with torch.no_grad():
-        model(ids)
+        keep["logits"] = model(ids).logits.cpu()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(iters):
@@ -485,6 +549,7 @@ def mamba130m(torch, dev, iters=3):
         out = model.generate(prompt, **gen)
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
+    keep["tokens"] = out.cpu()
     res["decode_tokens_per_s"] = round(4 * (out.shape[1] - 16) / sec, 1)
     res["decode_ms_per_step"] = round(sec / (out.shape[1] - 16) * 1e3, 3)
 
@@ -504,7 +569,11 @@ def mamba130m(torch, dev, iters=3):
 
     model.train()
     tids = ids[:, :256]
-    model(tids, labels=tids).loss.backward()
+    model.zero_grad(set_to_none=True)
+    loss = model(tids, labels=tids).loss
+    loss.backward()
+    keep["loss"] = loss.item()
+    keep["grads"] = {k: p.grad.cpu() for k, p in model.named_parameters() if p.grad is not None}
     model.zero_grad(set_to_none=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -518,19 +587,23 @@ def mamba130m(torch, dev, iters=3):
     return res
 
 
-def cpu_mamba130m(torch, batch=4, seqlen=1024, decode_steps=16):
-    """The same random-init Mamba-130M on this host's cores the way mamba-cpu
-    runs it: transformers' Mamba ops routed as the reference's hf.py routes
-    CPU tensors (the scan to the reference's own C++ kernels, built from its
-    csrc/selective_scan.cpp into oracle/_ref, with their backward for
-    training; conv, conv update and state update through the reference's ATen
-    paths; mamba_inner_fn -> None). Prefill: one warm-up pass, one timed pass.
-    Decode: `decode_steps` greedy tokens from the same 4 x 16 prompt as the
-    GPU leg (a sample of its 128). Train: one warm-up step, one timed step at
-    4 x 256. All at `_cpu_threads()` threads. Returns a dict, or None when the
-    reference kernels are not built."""
-    import transformers
+def cpu_mamba130m(torch, keep, decode_steps=16):
+    """The same random-init Mamba-130M (same weights, same ids) on this host's
+    cores the way mamba-cpu runs it: transformers' Mamba ops routed as the
+    reference's hf.py routes CPU tensors (the scan to the reference's own C++
+    kernels, built from its csrc/selective_scan.cpp into oracle/_ref, with
+    their backward for training; conv, conv update and state update through
+    the reference's ATen paths; mamba_inner_fn -> None). Prefill: one warm-up
+    pass, one timed pass. Decode: `decode_steps` greedy tokens from the same
+    4 x 16 prompt as the GPU leg (a sample of its 128). Train: one warm-up
+    step, one timed step at 4 x 256. All at `_cpu_threads()` threads.
 
+    Agreement with the GPU leg (`keep`), the measures of the reference's
+    benchmarks/check_hf_model.py:105-121: largest |logit difference| and
+    top-1 agreement over all 4 x 1024 prefill positions, whether the sampled
+    greedy tokens are identical, the two training losses and the worst
+    per-tensor gradient error max|dg| / max|g|. Returns a dict, or None when
+    the reference kernels are not built."""
     from oracle import cpu_torch as CT
     from oracle import ref as R
 
@@ -539,18 +612,22 @@ def cpu_mamba130m(torch, batch=4, seqlen=1024, decode_steps=16):
     threads = _cpu_threads()
     res = {"cpu_reference_threads": threads}
     with CT.route_transformers(threads):
-        torch.manual_seed(0)
-        cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
-                                       conv_kernel=4, vocab_size=50280)
-        model = transformers.MambaForCausalLM(cfg).eval()
-        ids = torch.randint(0, 50280, (batch, seqlen))
+        model = _mamba130m_model(torch).eval()
+        ids = _mamba130m_ids(torch)
         with torch.no_grad():
-            model(ids)
+            logits = model(ids).logits
             t0 = time.perf_counter()
             model(ids)
             sec = time.perf_counter() - t0
-        res["cpu_reference_prefill_tokens_per_s"] = round(batch * seqlen / sec, 1)
+        res["cpu_reference_prefill_tokens_per_s"] = round(4 * 1024 / sec, 1)
         res["cpu_reference_prefill_s"] = round(sec, 3)
+        agree = {}
+        if "logits" in keep:
+            agree["max_abs_logit_diff"] = float((keep["logits"] - logits).abs().max())
+            agree["max_abs_logit"] = float(logits.abs().max())
+            agree["top1_agreement"] = float((keep["logits"].argmax(-1) == logits.argmax(-1)).float().mean())
+            agree["positions"] = int(logits.shape[0] * logits.shape[1])
+        del logits
 
         prompt = ids[:, :16]
         gen = dict(max_new_tokens=decode_steps, min_new_tokens=decode_steps, do_sample=False,
@@ -562,35 +639,87 @@ def cpu_mamba130m(torch, batch=4, seqlen=1024, decode_steps=16):
             sec = time.perf_counter() - t0
         res["cpu_reference_decode_ms_per_step"] = round(sec / (out.shape[1] - 16) * 1e3, 3)
         res["cpu_reference_decode_sample"] = f"{out.shape[1] - 16} greedy steps from the 4 x 16 prompt"
+        if "tokens" in keep:
+            agree["greedy_tokens_identical"] = bool(torch.equal(keep["tokens"][:, :out.shape[1]], out))
+            agree["greedy_steps_compared"] = int(out.shape[1] - 16)
 
         model.train()
         tids = ids[:, :256]
         for i in range(2):
             t0 = time.perf_counter()
-            model(tids, labels=tids).loss.backward()
-            model.zero_grad(set_to_none=True)
+            loss = model(tids, labels=tids).loss
+            loss.backward()
             sec = time.perf_counter() - t0
+            if i == 0 and "grads" in keep:
+                agree["train_loss"] = keep["loss"]
+                agree["train_loss_cpu_reference"] = loss.item()
+                worst, where = 0.0, None
+                for k, p in model.named_parameters():
+                    if p.grad is None:
+                        continue
+                    e = float((keep["grads"][k] - p.grad).abs().max() / p.grad.abs().max().clamp_min(1e-12))
+                    if e > worst:
+                        worst, where = e, k
+                agree["worst_per_tensor_grad_error"] = worst
+                agree["worst_grad_tensor"] = where
+            model.zero_grad(set_to_none=True)
         res["cpu_reference_train_step_ms_4x256"] = round(sec * 1e3, 1)
+        res["agreement_with_cpu_reference"] = agree
     return res
 
 
-def counter_pass(torch, dev, inputs, gout):
-    """A short fixed sequence for hardware-counter runs (rocprofv3 --pmc): the
-    training-step forward and backward ops three times, each followed by a
-    copy of 256 MiB (64 Mi floats read, 64 Mi floats written), whose counter
-    readings calibrate the byte counters against a known traffic."""
-    ops = torch.ops.mamba_cpu
-    kargs = (inputs["u"], inputs["delta"], inputs["A"], inputs["B"].transpose(-1, -2),
-             inputs["C"].transpose(-1, -2), inputs["D"], inputs["z"], inputs["delta_bias"], True)
+def counter_pass(torch, dev, inputs, gout, which):
+    """A short fixed sequence for hardware-counter runs (rocprofv3 --pmc),
+    three repetitions, each followed by a copy of 256 MiB (64 Mi floats read,
+    64 Mi floats written) whose counter readings calibrate the byte counters
+    against a known traffic. `which`: "train" = the training-step forward
+    and backward ops; "fwd" = the forward-only workload (batch 1, dim 1536,
+    seqlen 2048); "long" = the long bf16 workload's forward and backward
+    (batch 1, dim 5120, seqlen 16384)."""
+    from mamba_cpu import selective_scan_fn
+
     src = torch.randn(64 << 20, device=dev)
     dst = torch.empty_like(src)
-    with torch.no_grad():
-        for _ in range(3):
-            _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*kargs)
-            ops.selective_scan_bwd_ckpt(*kargs, gout, None, ckpt, ysave)
-            dst.copy_(src)
+    g = torch.Generator(device=dev).manual_seed(0)
+    if which == "train":
+        ops = torch.ops.mamba_cpu
+        kargs = (inputs["u"], inputs["delta"], inputs["A"], inputs["B"].transpose(-1, -2),
+                 inputs["C"].transpose(-1, -2), inputs["D"], inputs["z"], inputs["delta_bias"], True)
+
+        def run():
+            with torch.no_grad():
+                _, _, ckpt, ysave = ops.selective_scan_fwd_ckpt(*kargs)
+                ops.selective_scan_bwd_ckpt(*kargs, gout, None, ckpt, ysave)
+    elif which == "fwd":
+        b, d, l, n = 1, 1536, 2048, 16
+        u, delta = (torch.randn(b, d, l, generator=g, device=dev) for _ in range(2))
+        A = -torch.rand(d, n, generator=g, device=dev)
+        Bm, Cm = (torch.randn(b, n, l, generator=g, device=dev) for _ in range(2))
+        D = torch.randn(d, generator=g, device=dev)
+
+        def run():
+            with torch.no_grad():
+                selective_scan_fn(u, delta, A, Bm, Cm, D, delta_softplus=True)
+    else:
+        b, d, l, n = 1, 5120, 16384, 16
+        bf = torch.bfloat16
+        leaves = dict(u=torch.randn(b, d, l, generator=g, device=dev).to(bf),
+                      delta=torch.randn(b, d, l, generator=g, device=dev).to(bf),
+                      A=-torch.exp(torch.rand(d, n, generator=g, device=dev) * math.log(16)),
+                      B=torch.randn(b, n, l, generator=g, device=dev).to(bf),
+                      C=torch.randn(b, n, l, generator=g, device=dev).to(bf),
+                      D=torch.randn(d, generator=g, device=dev))
+        leaves = {k: v.requires_grad_() for k, v in leaves.items()}
+        lgout = torch.randn(b, d, l, generator=g, device=dev).to(bf)
+
+        def run():
+            out = selective_scan_fn(**leaves, delta_softplus=True)
+            torch.autograd.grad(out, list(leaves.values()), lgout)
+    for _ in range(3):
+        run()
+        dst.copy_(src)
     torch.cuda.synchronize()
-    print("counter pass done", flush=True)
+    print(f"counter pass ({which}) done", flush=True)
 
 
 def model_pass(torch, dev, what):
@@ -630,8 +759,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
-    ap.add_argument("--counter-pass", action="store_true",
-                    help="only run 3 x (forward op, backward op, 256 MiB copy) for rocprofv3 --pmc")
+    ap.add_argument("--counter-pass", nargs="?", const="train", choices=["train", "fwd", "long"],
+                    help="only run 3 x (one workload's scan ops, 256 MiB copy) for rocprofv3 --pmc: "
+                         "train (default), fwd or long")
     ap.add_argument("--model-pass", choices=["train", "decode"],
                     help="only run a short Mamba-130M train or graph-decode sequence for kernel traces")
     args = ap.parse_args()
@@ -652,7 +782,7 @@ def main():
         return
     inputs, gout = make_inputs(torch, dev)
     if args.counter_pass:
-        counter_pass(torch, dev, inputs, gout)
+        counter_pass(torch, dev, inputs, gout, args.counter_pass)
         return
     leaves = {k: v.clone().requires_grad_() for k, v in inputs.items()}
     order = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias"]
@@ -719,11 +849,12 @@ def main():
         fwd_launch_ms = _events_ms(torch, stream, lambda: ops.selective_scan_fwd_ckpt(*kargs), args.steps)
     del ckpt, ysave
     bwd_gbs = bwd_bytes / (bwd_launch_ms * 1e-3) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "scan_bwd_b8_d1536_l1024_n16_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    counters = {}
+    cpath = os.path.join(ROOT, "profiles", COUNTERS_JSON)
+    if os.path.exists(cpath):
+        with open(cpath) as f:
+            counters = json.load(f)
+    traffic = counters.get("hbm_bytes_per_launch")
 
     extra = {
         "fwd_ms_in_step": round(fwd_ms, 4),
@@ -737,14 +868,15 @@ def main():
         "library": mamba_cpu._C.version(),
     }
     if not args.no_prefill:
+        keep = {}
         try:
-            extra["mamba130m"] = mamba130m(torch, dev)
+            extra["mamba130m"] = mamba130m(torch, dev, keep)
             extra["mamba130m_prefill_tokens_per_s"] = extra["mamba130m"]["prefill_tokens_per_s"]
         except Exception as exc:  # reported, not hidden
             extra["mamba130m_error"] = repr(exc)
         if not args.no_cpu_baseline and "mamba130m" in extra:
             try:
-                cpu = cpu_mamba130m(torch)
+                cpu = cpu_mamba130m(torch, keep)
                 if cpu is not None:
                     m = extra["mamba130m"]
                     m.update(cpu)
@@ -758,10 +890,13 @@ def main():
                         cpu["cpu_reference_train_step_ms_4x256"] / m["train_step_ms_4x256"], 1)
             except Exception as exc:  # reported, not hidden
                 extra["mamba130m_cpu_error"] = repr(exc)
+        del keep
     if not args.no_configs:
         extra["workloads"] = other_configs(torch, dev, stream, not args.no_cpu_baseline)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes, extra)
+    extra["host_cpus"] = host_cpus()
+    valu = valu_roofline(bwd_launch_ms, counters)
 
     line = {
         "metric": METRIC,
@@ -782,7 +917,9 @@ def main():
             "batch": B_, "dim": D_, "seqlen": L_, "dstate": N_, "ngroups": G_,
         },
         "roofline": {
-            "bound": "hbm",
+            # The kernel is issue-bound on the vector ALUs (valu below, from
+            # committed counters); achieved / peak / frac are its HBM figures.
+            "bound": "valu" if valu else "hbm",
             "kernel": "selective-scan backward launch: scan_bwd_kernel + its dB/dC/dA/dD/ddelta_bias "
                       "reduce kernels, algorithmic bytes of the backward / average launch time",
             "achieved": round(bwd_gbs, 2),
@@ -790,6 +927,7 @@ def main():
             "unit": "GB/s",
             "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "valu": valu,
         },
         "cpu_baseline": cpu,
         "extra": extra,

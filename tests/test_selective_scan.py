@@ -222,66 +222,70 @@ def test_unequal_groups_and_input_independent_bc(case):
         close(t.grad, g, GRAD_RTOL, GRAD_ATOL[name], name)
 
 
-def decay_inputs(x, seqlen=4, dstate=8):
-    """Inputs where every step's dt*A equals x per channel (reference
-    tests/test_selective_scan.py:146-158); x: (dim,)."""
-    dim = x.shape[0]
-    g = torch.Generator().manual_seed(0)
-    delta = torch.ones(1, dim, seqlen)
-    A = x[:, None].expand(dim, dstate).contiguous()
-    inp = dict(
-        u=torch.randn(1, dim, seqlen, generator=g),
-        delta=delta,
-        A=A,
-        B=torch.randn(1, dstate, seqlen, generator=g),
-        C=torch.randn(1, dstate, seqlen, generator=g),
-    )
-    return {k: v.to(DEV) for k, v in inp.items()}
+def fixed_decay_case(log_decay, seqlen=4, dstate=8, ones=False):
+    """A batch-1 case whose per-step decay exponent dt*A is log_decay[d] on
+    channel d at every step and state: dt = 1 (no softplus), A[d, :] =
+    log_decay[d]. u, B, C are seeded normals, or all ones with `ones` (then
+    the exact answer is a geometric sum of exp(log_decay)). The extreme-decay,
+    exp-accuracy and NaN cases of the reference's tests use such inputs
+    (tests/test_selective_scan.py:146-183)."""
+    dim = log_decay.shape[0]
+    gen = torch.Generator().manual_seed(0)
+    draw = (lambda *s: torch.ones(*s)) if ones else (lambda *s: torch.randn(*s, generator=gen))
+    case = {"u": draw(1, dim, seqlen), "delta": torch.ones(1, dim, seqlen),
+            "A": log_decay.reshape(dim, 1).repeat(1, dstate),
+            "B": draw(1, dstate, seqlen), "C": draw(1, dstate, seqlen)}
+    return {k: v.to(DEV) for k, v in case.items()}
 
 
 @pytest.mark.parametrize("x", [-1e2, -1e4, -1e6, -1e8, -1e12, -1e20, -1e30, -3e38, -float("inf")])
 def test_extreme_decay_matches_oracle(x):
-    inp = decay_inputs(torch.full((16,), x))
-    out, last = selective_scan_fn(**inp, return_last_state=True)
-    out_ref, last_ref = O.selective_scan_fwd(**inp)
-    close(out, out_ref, 1e-5, 1e-5)
-    close(last, last_ref, 1e-5, 1e-5)
+    """Decay exponents down to -inf: the state forgets everything at each
+    step (h_t = dt u_t B_t), with no NaN from inf * 0."""
+    case = fixed_decay_case(torch.full((16,), x))
+    out, last = selective_scan_fn(**case, return_last_state=True)
+    want, want_last = O.selective_scan_fwd(**case)
+    close(out, want, 1e-5, 1e-5)
+    close(last, want_last, 1e-5, 1e-5)
 
 
 @pytest.mark.parametrize("x", [-1e4, -1e12, -1e30])
 def test_extreme_decay_backward_is_finite_and_matches(x):
-    inp = decay_inputs(torch.full((16,), x))
-    for k in ("u", "B", "C"):
-        inp[k].requires_grad_()
-    out = selective_scan_fn(**inp)
-    (out * out.detach()).sum().backward()  # dout = 2 * out / 2 = out
-    _, _, _, dB, dC, _, _, _ = O.selective_scan_bwd(**inp, dout=out.detach())
-    du = O.selective_scan_bwd(**inp, dout=out.detach())[0]
-    for k, want in (("u", du), ("B", dB), ("C", dC)):
-        g = inp[k].grad
-        assert g.isfinite().all(), k
-        close(g, want, 1e-4, 1e-4, k)
+    case = fixed_decay_case(torch.full((16,), x))
+    leaves = ("u", "B", "C")
+    for k in leaves:
+        case[k].requires_grad_()
+    out = selective_scan_fn(**case)
+    upstream = 2 * out.detach()  # the gradient of sum(out ** 2)
+    out.backward(upstream)
+    want = dict(zip(("u", "delta", "A", "B", "C"), O.selective_scan_bwd(**case, dout=upstream)))
+    for k in leaves:
+        assert case[k].grad.isfinite().all(), k
+        close(case[k].grad, want[k], 1e-4, 1e-4, k)
 
 
 def test_exp_accuracy_across_range():
-    # Includes x > 0: dt*A is positive when delta is negative and softplus is off.
+    """Two steps of all-ones inputs: out_1 = exp(x) + 1 per channel, over
+    exponents from -80 to 40 (positive ones occur when delta is negative
+    without softplus), against float64."""
     x = torch.cat([torch.linspace(-80, 0, 512), torch.linspace(0, 40, 128)])
-    inp = decay_inputs(x, seqlen=2)
-    inp["u"] = torch.ones_like(inp["u"])
-    inp["B"] = torch.ones_like(inp["B"])
-    inp["C"] = torch.ones_like(inp["C"])
-    out = selective_scan_fn(**inp)
-    out_ref, _ = O.selective_scan_fwd(**inp)
-    close(out, out_ref, 1e-5, 1e-6)
+    case = fixed_decay_case(x, seqlen=2, ones=True)
+    out = selective_scan_fn(**case)
+    want, _ = O.selective_scan_fwd(**case)
+    close(out, want, 1e-5, 1e-6)
+    # the closed form: y_0 = dstate, y_1 = dstate (exp(x) + 1)
+    close(out[0, :, 1], 8 * (np.exp(x.double().numpy()) + 1), 1e-5, 1e-6, "closed form")
 
 
 def test_nan_propagates():
-    inp = decay_inputs(torch.full((16,), -1.0))
-    inp["delta"][0, 3, 1] = float("nan")
-    out = selective_scan_fn(**inp)
-    assert out[0, 3, 1:].isnan().all()
-    assert not out[0, 2].isnan().any()
-    assert not out[0, 3, :1].isnan().any()
+    """A NaN delta at (channel 3, step 1) poisons that channel from step 1
+    on, and nothing else."""
+    case = fixed_decay_case(torch.full((16,), -1.0))
+    case["delta"][0, 3, 1] = float("nan")
+    out = selective_scan_fn(**case)[0]
+    assert out[3, 1:].isnan().all()
+    others = torch.cat([out[:3], out[4:]])
+    assert not others.isnan().any() and not out[3, :1].isnan().any()
 
 
 def test_hf_style_strided_inputs_match_contiguous():
