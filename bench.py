@@ -22,7 +22,9 @@ Also reported, on one JSON line:
                 long-sequence bf16 scan, complex-A scan, conv1d fp32/bf16,
                 conv1d over packed sequences, conv update, conv update through
                 ring buffers and state indices, state update), each with time,
-                algorithmic bytes and HBM fraction.
+                algorithmic bytes and HBM fraction; and Mamba-2's SSD scan
+                (mamba_chunk_scan_combined, bf16 and fp32 storage) with its
+                matrix-core TFLOP/s against the fp32 MFMA peak.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -495,6 +497,106 @@ def other_configs(torch, dev, stream, cpu):
     return res
 
 
+# Mamba-2 SSD scan (mamba_chunk_scan_combined) at the layer shape of Mamba-2
+# 2.7B: d_inner 5120 as 80 heads of headdim 64, one B/C group, dstate 128.
+SSD_SHAPE = dict(batch=4, seqlen=2048, nheads=80, headdim=64, ngroups=1, dstate=128)
+MFMA_F32_PEAK_TFS = 157.3
+
+
+def _ssd_inputs(torch, dev, xdt, shape, seed=0):
+    b, l, h, p, g, n = (shape[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate"))
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen, device=dev)  # noqa: E731
+    return dict(x=r(b, l, h, p).to(xdt), dt=r(b, l, h) * 0.5 - 1.0,
+                A=-torch.exp(torch.rand(h, generator=gen, device=dev) * math.log(16)),
+                B=r(b, l, g, n).to(xdt), C=r(b, l, g, n).to(xdt), D=r(h), z=r(b, l, h, p).to(xdt),
+                dt_bias=torch.rand(h, generator=gen, device=dev) * 0.5)
+
+
+def ssd_bytes(shape, e):
+    """Algorithmic bytes of the SSD scan: forward reads x, z, dt, B, C (and
+    the per-head vectors) and writes out; the backward reads them again with
+    dout and writes dx, dz, ddt, dB, dC (and the per-head gradients)."""
+    b, l, h, p, g, n = (shape[k] for k in ("batch", "seqlen", "nheads", "headdim", "ngroups", "dstate"))
+    xs, bc, dts, vec = b * l * h * p * e, b * l * g * n * e, b * l * h * 4, 3 * h * 4
+    fwd = 3 * xs + 2 * bc + dts + vec
+    bwd = (3 * xs + 2 * bc + dts + vec) + (2 * xs + 2 * bc + dts + vec)
+    return fwd, bwd
+
+
+def ssd_workloads(torch, dev, stream, cpu):
+    """mamba_chunk_scan_combined forward and forward+backward at the Mamba-2
+    2.7B layer shape, bf16 and fp32 storage: time, matrix-core TFLOP/s against
+    the fp32 MFMA peak (the kernels multiply in fp32 for every storage type)
+    and algorithmic GB/s against HBM."""
+    from mamba_cpu import mamba_chunk_scan_combined
+    from mamba_cpu.ops.ssd_combined import ssd_flops
+
+    sh = SSD_SHAPE
+    res = {}
+    for name, xdt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        t = _ssd_inputs(torch, dev, xdt, sh)
+        kw = dict(D=t["D"], z=t["z"], dt_bias=t["dt_bias"], dt_softplus=True)
+        with torch.no_grad():
+            fwd_ms = _events_ms(torch, stream, lambda: mamba_chunk_scan_combined(
+                t["x"], t["dt"], t["A"], t["B"], t["C"], 256, **kw), 20)
+        leaves = {k: v.clone().requires_grad_() for k, v in t.items()}
+        gout = torch.randn(t["x"].shape, device=dev).to(xdt)
+        order = ["x", "dt", "A", "B", "C", "D", "z", "dt_bias"]
+
+        def fb():
+            out = mamba_chunk_scan_combined(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"],
+                                            256, D=leaves["D"], z=leaves["z"], dt_bias=leaves["dt_bias"],
+                                            dt_softplus=True)
+            return torch.autograd.grad(out, [leaves[k] for k in order], gout)
+
+        fb_ms = _events_ms(torch, stream, fb, 10)
+        e = t["x"].element_size()
+        fb_bytes = sum(ssd_bytes(sh, e))
+        ff = ssd_flops(**sh)
+        fbf = ff + ssd_flops(**sh, backward=True)
+        tf_f, tf_fb = ff / (fwd_ms * 1e-3) / 1e12, fbf / (fb_ms * 1e-3) / 1e12
+        r = {
+            "workload": (f"mamba_chunk_scan_combined, {name} x/z/B/C, batch 4, seqlen 2048, 80 heads x "
+                         "headdim 64, 1 group, dstate 128, D + z + dt_bias, softplus"),
+            "fwd_ms": round(fwd_ms, 4),
+            "fwd_bwd_ms": round(fb_ms, 4),
+            "tokens_per_s_fwd_bwd": round(sh["batch"] * sh["seqlen"] / (fb_ms * 1e-3), 1),
+            "roofline": {
+                "bound": "mfma", "unit": "TFLOP/s", "peak": MFMA_F32_PEAK_TFS,
+                "achieved_fwd": round(tf_f, 2), "frac_fwd": round(tf_f / MFMA_F32_PEAK_TFS, 4),
+                "achieved": round(tf_fb, 2), "frac": round(tf_fb / MFMA_F32_PEAK_TFS, 4),
+                "matrix_flops": {"fwd": int(ff), "fwd_bwd": int(fbf)},
+                "hbm_GBps": round(fb_bytes / (fb_ms * 1e-3) / 1e9, 1),
+                "hbm_frac": round(fb_bytes / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes_fwd_bwd": int(fb_bytes),
+            },
+        }
+        if cpu and name == "fp32":
+            r["cpu_baseline"] = cpu_ssd(torch, t)
+            r["speedup_vs_cpu_port"] = round(
+                r["tokens_per_s_fwd_bwd"] / r["cpu_baseline"]["value"], 1)
+        res[f"ssd_{name}_b4_l2048_h80_p64_n128"] = r
+        del t, leaves, gout
+    return res
+
+
+def cpu_ssd(torch, t, steps=128):
+    """The float64 numpy restatement of the SSD scan (the reference has no
+    SSD path), forward and backward on one host thread, over the first
+    `steps` steps of batch row 0 of the same inputs; tokens/s."""
+    from oracle import ssd as S
+
+    c = {k: (v[:1, :steps] if v.dim() >= 3 else v).detach().cpu() for k, v in t.items()}
+    dout = torch.randn(c["x"].shape)
+    t0 = time.perf_counter()
+    S.ssd_fwd(**c, dt_softplus=True)
+    S.ssd_bwd(**c, dt_softplus=True, dout=dout)
+    sec = time.perf_counter() - t0
+    return {"value": round(steps / sec, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"batch row 0, first {steps} steps, forward + backward in float64 numpy"}
+
+
 MAMBA130M = dict(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2, conv_kernel=4,
                  vocab_size=50280)
 
@@ -722,6 +824,22 @@ def counter_pass(torch, dev, inputs, gout, which):
     print(f"counter pass ({which}) done", flush=True)
 
 
+def ssd_pass(torch, dev):
+    """Three forward+backward passes of the bf16 SSD workload, for
+    rocprofv3 --kernel-trace."""
+    from mamba_cpu import mamba_chunk_scan_combined
+
+    t = _ssd_inputs(torch, dev, torch.bfloat16, SSD_SHAPE)
+    leaves = {k: v.requires_grad_() for k, v in t.items()}
+    gout = torch.randn(t["x"].shape, device=dev).to(torch.bfloat16)
+    for i in range(3):
+        out = mamba_chunk_scan_combined(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 256,
+                                        D=leaves["D"], z=leaves["z"], dt_bias=leaves["dt_bias"], dt_softplus=True)
+        out.backward(gout)
+        torch.cuda.synchronize()
+        print(f"ssd pass {i} done", flush=True)
+
+
 def model_pass(torch, dev, what):
     """A short fixed run of the Mamba-130M architecture for kernel traces
     (rocprofv3 --kernel-trace): `train` = 3 warm-up + 5 training steps at
@@ -762,6 +880,8 @@ def main():
     ap.add_argument("--counter-pass", nargs="?", const="train", choices=["train", "fwd", "long"],
                     help="only run 3 x (one workload's scan ops, 256 MiB copy) for rocprofv3 --pmc: "
                          "train (default), fwd or long")
+    ap.add_argument("--ssd-pass", action="store_true",
+                    help="only run 3 forward+backward passes of the bf16 SSD workload for kernel traces")
     ap.add_argument("--model-pass", choices=["train", "decode"],
                     help="only run a short Mamba-130M train or graph-decode sequence for kernel traces")
     args = ap.parse_args()
@@ -779,6 +899,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.model_pass:
         model_pass(torch, dev, args.model_pass)
+        return
+    if args.ssd_pass:
+        ssd_pass(torch, dev)
         return
     inputs, gout = make_inputs(torch, dev)
     if args.counter_pass:
@@ -893,6 +1016,7 @@ def main():
         del keep
     if not args.no_configs:
         extra["workloads"] = other_configs(torch, dev, stream, not args.no_cpu_baseline)
+        extra["workloads"].update(ssd_workloads(torch, dev, stream, not args.no_cpu_baseline))
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes, extra)
     extra["host_cpus"] = host_cpus()

@@ -293,6 +293,69 @@ typedef struct mcpu_state_update_args {
 
 int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Mamba-2 SSD scan.                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* mamba_ssm's mamba_chunk_scan_combined (mamba_ssm/ops/triton/ssd_combined.py),
+ * which the reference lists as roadmap (README.md:7, 94) and does not have.
+ * Per batch row and head h (heads split into ngroups contiguous groups that
+ * share B and C):
+ *   step_t = clamp(softplus?(dt_t + dt_bias_h), dt_limit_lo, dt_limit_hi)
+ *   h_t = exp(step_t A_h) h_{t-1} + step_t x_t B_t^T      (headdim x dstate,
+ *                                                          h_{-1} = initial state or 0)
+ *   y_t = h_t C_t + D x_t ;  out_t = y_t silu(z_t) when z is given
+ * All tensors contiguous. headdim a multiple of 16 up to 64, dstate a multiple
+ * of 16 up to 128. The forward fills a caller-owned "saved" buffer of
+ * mcpu_ssd_saved_size() bytes (per-chunk decays and states) that the backward
+ * reads; the chunking is internal (64 steps) and does not change the result
+ * beyond float32 rounding. */
+typedef struct mcpu_ssd_args {
+  const void* x;                /* (batch, seqlen, nheads, headdim), dtype */
+  const float* dt;              /* (batch, seqlen, nheads), before dt_bias and softplus */
+  const float* A;               /* (nheads) */
+  const void* B;                /* (batch, seqlen, ngroups, dstate), dtype */
+  const void* C;                /* same as B */
+  const float* D;               /* (nheads, headdim), optional */
+  const void* z;                /* like x, optional */
+  const float* dt_bias;         /* (nheads), optional */
+  const float* initial_states;  /* (batch, nheads, headdim, dstate), optional */
+  int64_t batch, seqlen, nheads, headdim, ngroups, dstate;
+  int32_t dtype;                /* storage type of x, z, B, C, out, ysave, dout, dx, dz */
+  int32_t dt_softplus;
+  float dt_limit_lo, dt_limit_hi; /* clamp of the step; lo <= 0 and hi = +inf: none */
+  /* forward outputs */
+  void* out;                    /* like x */
+  float* final_states;          /* (batch, nheads, headdim, dstate), optional */
+  void* ysave;                  /* like x: y before the z gate; the forward writes it when
+                                   given (needed by the backward when z is given) */
+  /* backward inputs */
+  const void* dout;             /* like x */
+  const float* dfinal_states;   /* like final_states, optional */
+  /* backward outputs */
+  void* dx;                     /* like x */
+  float* ddt;                   /* (batch, seqlen, nheads): gradient of the raw dt */
+  float* dA;                    /* (nheads) */
+  float* dB;                    /* (batch, seqlen, ngroups, dstate) float32 */
+  float* dC;
+  float* dD;                    /* (nheads, headdim); required iff D != NULL */
+  void* dz;                     /* like x; required iff z != NULL */
+  float* ddt_bias;              /* (nheads); required iff dt_bias != NULL */
+  float* dinitial_states;       /* required iff initial_states != NULL */
+} mcpu_ssd_args;
+
+/* Bytes of the buffer the forward fills for the backward (0 for an empty
+ * batch or sequence, where the buffer may be NULL; 0 too for arguments the
+ * entry points reject, which then say why). */
+size_t mcpu_ssd_saved_size(const mcpu_ssd_args* a);
+/* Forward. Replaces nothing in the reference (see above). */
+int mcpu_ssd_fwd(const mcpu_ssd_args* a, void* saved, size_t saved_bytes, void* stream);
+/* Workspace bytes of the backward (0, and NULL allowed, when empty). */
+size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a);
+/* Backward, given the forward's saved buffer (and ysave when z is given). */
+int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

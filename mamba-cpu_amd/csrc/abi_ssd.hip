@@ -1,0 +1,237 @@
+// C-ABI entry points of the Mamba-2 SSD scan: argument checks, the layout of
+// the saved buffer and of the backward's workspace, and kernel sequencing.
+// Nothing is allocated here.
+#include <cmath>
+#include <cstring>
+
+#include "abi_util.h"
+#include "scan_common.h"
+#include "ssd_params.h"
+
+namespace mcpu {
+namespace {
+
+int check_ssd(const mcpu_ssd_args* a) {
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "ssd: null argument block");
+  if (a->batch < 0 || a->seqlen < 0 || a->nheads < 1 || a->ngroups < 1)
+    return fail(MCPU_ERR_INVALID, "ssd: bad sizes");
+  // Per-step tensors may be NULL (empty) when there are no steps.
+  const bool steps = a->batch > 0 && a->seqlen > 0;
+  if (a->A == nullptr || (steps && (a->x == nullptr || a->dt == nullptr || a->B == nullptr || a->C == nullptr)))
+    return fail(MCPU_ERR_INVALID, "ssd: x, dt, A, B and C are required");
+  if (a->nheads % a->ngroups != 0)
+    return fail(MCPU_ERR_INVALID, "ssd: nheads (%lld) must be divisible by ngroups (%lld)",
+                (long long)a->nheads, (long long)a->ngroups);
+  if (a->headdim < 16 || a->headdim > kSsdMaxP || a->headdim % 16 != 0)
+    return fail(MCPU_ERR_UNSUPPORTED, "ssd: headdim must be a multiple of 16 up to %d, got %lld", kSsdMaxP,
+                (long long)a->headdim);
+  if (a->dstate < 16 || a->dstate > kSsdMaxN || a->dstate % 16 != 0)
+    return fail(MCPU_ERR_UNSUPPORTED, "ssd: dstate must be a multiple of 16 up to %d, got %lld", kSsdMaxN,
+                (long long)a->dstate);
+  if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "ssd: bad dtype %d", a->dtype);
+  if (!(a->dt_limit_lo <= a->dt_limit_hi))
+    return fail(MCPU_ERR_INVALID, "ssd: dt_limit must be an interval (lo <= hi)");
+  const int64_t nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
+  if (nchunks > 0x7fffffffll || a->nheads > 65535 || a->batch > 65535)
+    return fail(MCPU_ERR_UNSUPPORTED, "ssd: grid too large");
+  return MCPU_OK;
+}
+
+SsdParams make_ssd(const mcpu_ssd_args* a) {
+  SsdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.x = a->x;
+  p.dt = a->dt;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.D = a->D;
+  p.z = a->z;
+  p.dt_bias = a->dt_bias;
+  p.init = a->initial_states;
+  p.batch = a->batch;
+  p.seqlen = a->seqlen;
+  p.nheads = a->nheads;
+  p.headdim = a->headdim;
+  p.ngroups = a->ngroups;
+  p.dstate = a->dstate;
+  p.nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
+  p.nslices = (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
+  p.softplus = a->dt_softplus != 0;
+  p.clamp = (a->dt_limit_lo > 0.f || !std::isinf(a->dt_limit_hi)) ? 1 : 0;
+  p.dt_lo = a->dt_limit_lo;
+  p.dt_hi = a->dt_limit_hi;
+  return p;
+}
+
+// The saved buffer: cs, cs_lo and step (batch, nheads, nchunks, 64), then
+// states (batch, nchunks, nheads, headdim, dstate), all float32.
+struct SavedLayout {
+  size_t cs = 0, cs_lo = 0, step = 0, states = 0, total = 0;
+};
+SavedLayout saved_layout(const SsdParams& p) {
+  SavedLayout w;
+  const size_t chunk = sizeof(float) * p.batch * p.nheads * p.nchunks * kSsdQ;
+  w.cs = 0;
+  w.cs_lo = align_up(chunk);
+  w.step = w.cs_lo + align_up(chunk);
+  w.states = w.step + align_up(chunk);
+  w.total = w.states + align_up(sizeof(float) * p.batch * p.nchunks * p.nheads * p.headdim * p.dstate);
+  return w;
+}
+
+// The backward's workspace.
+struct BwdLayout {
+  size_t dstates = 0, dxt = 0, dB = 0, dC = 0, dcs = 0, dcsL = 0, dA = 0, dbias = 0, dD = 0, total = 0;
+};
+BwdLayout bwd_layout(const SsdParams& p) {
+  BwdLayout w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  const size_t f = sizeof(float);
+  w.dstates = take(f * p.batch * p.nchunks * p.nheads * p.headdim * p.dstate);
+  w.dxt = take(f * p.batch * p.seqlen * p.nheads * p.headdim);
+  w.dB = take(f * p.batch * p.seqlen * p.nheads * p.dstate);
+  w.dC = take(f * p.batch * p.seqlen * p.nheads * p.dstate);
+  w.dcs = take(f * p.batch * p.nheads * p.nchunks * kSsdQ);
+  w.dcsL = take(f * p.batch * p.nheads * p.nchunks * p.nslices);
+  w.dA = take(f * p.batch * p.nchunks * p.nheads);
+  w.dbias = take(f * p.batch * p.nchunks * p.nheads);
+  w.dD = take(f * p.batch * p.nchunks * p.nheads * p.headdim);
+  w.total = off;
+  return w;
+}
+
+void bind_saved(SsdParams& p, const void* saved) {
+  const SavedLayout w = saved_layout(p);
+  char* s = static_cast<char*>(const_cast<void*>(saved));
+  p.cs = reinterpret_cast<float*>(s + w.cs);
+  p.cs_lo = reinterpret_cast<float*>(s + w.cs_lo);
+  p.step = reinterpret_cast<float*>(s + w.step);
+  p.states = reinterpret_cast<float*>(s + w.states);
+}
+
+}  // namespace
+}  // namespace mcpu
+
+using namespace mcpu;
+
+extern "C" size_t mcpu_ssd_saved_size(const mcpu_ssd_args* a) {
+  if (check_ssd(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  return saved_layout(make_ssd(a)).total;
+}
+
+extern "C" int mcpu_ssd_fwd(const mcpu_ssd_args* a, void* saved, size_t saved_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_ssd(a)) return rc;
+  if (a->out == nullptr && a->batch > 0 && a->seqlen > 0) return fail(MCPU_ERR_INVALID, "ssd_fwd: out is required");
+  SsdParams p = make_ssd(a);
+  const size_t need = saved_layout(p).total;
+  if (need > 0 && (saved == nullptr || saved_bytes < need))
+    return fail(MCPU_ERR_INVALID, "ssd_fwd: saved buffer of %zu bytes needed, got %zu", need, saved_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  if (a->batch == 0 || a->seqlen == 0) {
+    // Nothing to scan: the final state is the initial state (or 0).
+    if (a->final_states != nullptr && a->batch > 0) {
+      const int64_t n = a->batch * a->nheads * a->headdim * a->dstate;
+      if (a->initial_states != nullptr)
+        return hip_status(hipMemcpyAsync(a->final_states, a->initial_states, sizeof(float) * n,
+                                         hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)),
+                          "ssd_fwd copy");
+      return zero_f32(a->final_states, n, static_cast<hipStream_t>(stream));
+    }
+    return MCPU_OK;
+  }
+  bind_saved(p, saved);
+  p.out = a->out;
+  p.final_states = a->final_states;
+  p.ysave = a->ysave;
+  return hip_status(ssd_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)), "ssd_fwd launch");
+}
+
+extern "C" size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a) {
+  if (check_ssd(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  return bwd_layout(make_ssd(a)).total;
+}
+
+extern "C" int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_ssd(a)) return rc;
+  if (a->dA == nullptr || (a->batch > 0 && a->seqlen > 0 &&
+                           (a->dout == nullptr || a->dx == nullptr || a->ddt == nullptr || a->dB == nullptr ||
+                            a->dC == nullptr)))
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: dout, dx, ddt, dA, dB and dC are required");
+  if (a->z != nullptr && (a->dz == nullptr || a->ysave == nullptr))
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: dz and the forward's ysave are required when z is given");
+  if (a->D != nullptr && a->dD == nullptr)
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: dD is required when D is given");
+  if (a->dt_bias != nullptr && a->ddt_bias == nullptr)
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: ddt_bias is required when dt_bias is given");
+  if (a->initial_states != nullptr && a->dinitial_states == nullptr)
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: dinitial_states is required when initial_states is given");
+  SsdParams p = make_ssd(a);
+  const size_t need_saved = saved_layout(p).total;
+  if (need_saved > 0 && (saved == nullptr || saved_bytes < need_saved))
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: the forward's saved buffer of %zu bytes is needed, got %zu",
+                need_saved, saved_bytes);
+  const BwdLayout w = bwd_layout(p);
+  if (w.total > 0 && (workspace == nullptr || workspace_bytes < w.total))
+    return fail(MCPU_ERR_INVALID, "ssd_bwd: workspace of %zu bytes needed, got %zu", w.total, workspace_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->batch == 0 || a->seqlen == 0) {
+    // Parameter gradients are zero; the initial state's is the final state's.
+    if (int rc = zero_f32(a->dA, a->nheads, st)) return rc;
+    if (a->dD) if (int rc = zero_f32(a->dD, a->nheads * a->headdim, st)) return rc;
+    if (a->ddt_bias) if (int rc = zero_f32(a->ddt_bias, a->nheads, st)) return rc;
+    if (a->dinitial_states && a->batch > 0) {
+      const int64_t n = a->batch * a->nheads * a->headdim * a->dstate;
+      if (a->dfinal_states)
+        return hip_status(hipMemcpyAsync(a->dinitial_states, a->dfinal_states, sizeof(float) * n,
+                                         hipMemcpyDeviceToDevice, st),
+                          "ssd_bwd copy");
+      return zero_f32(a->dinitial_states, n, st);
+    }
+    return MCPU_OK;
+  }
+  bind_saved(p, saved);
+  char* ws = static_cast<char*>(workspace);
+  p.ysave = a->ysave;
+  p.dout = a->dout;
+  p.dfinal = a->dfinal_states;
+  p.dx = a->dx;
+  p.ddt = a->ddt;
+  p.dz = a->dz;
+  p.dinit = a->dinitial_states;
+  p.dstates = reinterpret_cast<float*>(ws + w.dstates);
+  p.dxt = reinterpret_cast<float*>(ws + w.dxt);
+  p.dB_head = reinterpret_cast<float*>(ws + w.dB);
+  p.dC_head = reinterpret_cast<float*>(ws + w.dC);
+  p.dcs = reinterpret_cast<float*>(ws + w.dcs);
+  p.dcsL = reinterpret_cast<float*>(ws + w.dcsL);
+  p.dA_part = reinterpret_cast<float*>(ws + w.dA);
+  p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
+  p.dD_part = reinterpret_cast<float*>(ws + w.dD);
+  if (int rc = hip_status(ssd_bwd_launch(p, a->dtype, st), "ssd_bwd launch")) return rc;
+  // dB/dC summed over each group's heads; dA / dD / ddt_bias over (batch, chunk).
+  const int64_t hpg = p.nheads / p.ngroups;
+  const PartialSum sums[5] = {
+      {p.dB_head, a->dB, p.batch * p.seqlen * p.ngroups, hpg, p.dstate},
+      {p.dC_head, a->dC, p.batch * p.seqlen * p.ngroups, hpg, p.dstate},
+      {p.dA_part, a->dA, 1, p.batch * p.nchunks, p.nheads},
+      {a->ddt_bias ? p.dbias_part : nullptr, a->ddt_bias, 1, p.batch * p.nchunks, p.nheads},
+      {a->dD ? p.dD_part : nullptr, a->dD, 1, p.batch * p.nchunks, p.nheads * p.headdim},
+  };
+  return hip_status(partial_sums_launch(sums, 5, st), "ssd_bwd reduce");
+}

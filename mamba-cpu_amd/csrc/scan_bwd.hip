@@ -678,6 +678,32 @@ static unsigned grid_for(int64_t n) {
   return static_cast<unsigned>(g < 1 ? 1 : g);
 }
 
+// Sums up to five partial arrays in one launch: out[s, e] = sum over c of
+// part[s, c, e] (outer slices s, nsum terms c, per elements e), each in the
+// fixed order c = 0, 1, ... Entries with part == nullptr are skipped.
+hipError_t partial_sums_launch(const PartialSum* sums, int n, hipStream_t stream) {
+  ReduceJobs jobs{};
+  int64_t total = 0;
+  for (int i = 0; i < n && jobs.njobs < 5; ++i) {
+    const PartialSum& ps = sums[i];
+    if (ps.part == nullptr || ps.outer * ps.per == 0) continue;
+    ReduceJob& j = jobs.job[jobs.njobs++];
+    j.part = ps.part;
+    j.out = ps.out;
+    j.outer = ps.outer;
+    j.nsum = ps.nsum;
+    j.per = ps.per;
+    const bool aligned = reinterpret_cast<uintptr_t>(ps.part) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(ps.out) % 16 == 0;
+    j.vec = ps.per % 4 == 0 && aligned ? 4 : 1;
+    j.items = ps.outer * ps.per / j.vec;
+    total += j.items;
+  }
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(reduce_jobs_kernel, dim3(grid_for(total)), dim3(256), 0, stream, jobs, total);
+  return hipGetLastError();
+}
+
 // Sums the backward's partials: dB/dC over channel blocks (`slices` slices of
 // `per_slice` elements, `nblk_c` blocks each; skipped when dB_part is null),
 // and dA / dD / ddelta_bias over the batch (each skipped when its part is null).

@@ -217,6 +217,15 @@ struct BCStage {
   }
 };
 
+// One partial array to sum: out[s, e] = sum over c < nsum of
+// part[(s * nsum + c) * per + e], for s < outer, e < per.
+struct PartialSum {
+  const float* part;
+  float* out;
+  int64_t outer, nsum, per;
+};
+hipError_t partial_sums_launch(const PartialSum* sums, int n, hipStream_t stream);
+
 // Reads the 16 steps of state lane n from a transposed B/C tile.
 __device__ __forceinline__ void read_bc_row(const float (*tile)[kBCPad], int n, float (&v)[kScanBlockT]) {
   const float4* row = reinterpret_cast<const float4*>(tile[n]);

@@ -1066,10 +1066,154 @@ Tensor selective_state_update_inplace(Tensor& state, const Tensor& x, const Tens
   return out;
 }
 
+// ---- Mamba-2 SSD scan ------------------------------------------------------------
+//
+// mamba_chunk_scan_combined's forward and backward over mcpu_ssd_fwd / _bwd.
+// Layouts as the C ABI takes them (all contiguous): x, z (batch, seqlen,
+// nheads, headdim) in one storage type; dt (batch, seqlen, nheads) float32;
+// A, dt_bias (nheads) float32; B, C (batch, seqlen, ngroups, dstate) in x's
+// type; D (nheads, headdim) float32; initial_states (batch, nheads, headdim,
+// dstate) float32. The Python wrapper (mamba_cpu/ops/ssd_combined.py) brings
+// its arguments to these.
+
+mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, const Tensor& A,
+                       const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                       const optional<Tensor>& z, const optional<Tensor>& dt_bias,
+                       const optional<Tensor>& init, bool softplus, double lo, double hi) {
+  for (const optional<Tensor>& t : {opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias, init})
+    check_gpu(name, t);
+  TORCH_CHECK_VALUE(x.dim() == 4 && x_dtype(x.scalar_type()) && x.is_contiguous(), name,
+                    " expects a contiguous x (batch, seqlen, nheads, headdim) in float32, bfloat16 or float16");
+  const int64_t b = x.size(0), l = x.size(1), h = x.size(2), p = x.size(3);
+  TORCH_CHECK_VALUE(dt.scalar_type() == at::kFloat && dt.is_contiguous() && dt.dim() == 3 &&
+                        dt.size(0) == b && dt.size(1) == l && dt.size(2) == h,
+                    name, " expects a contiguous float32 dt (batch, seqlen, nheads)");
+  TORCH_CHECK_VALUE(A.scalar_type() == at::kFloat && A.dim() == 1 && A.size(0) == h && A.is_contiguous(), name,
+                    " expects a float32 A of shape (nheads,)");
+  for (const Tensor* X : {&B, &C})
+    TORCH_CHECK_VALUE(X->dim() == 4 && X->size(0) == b && X->size(1) == l && X->scalar_type() == x.scalar_type() &&
+                          X->is_contiguous(),
+                      name, " expects contiguous B and C (batch, seqlen, ngroups, dstate) in x's dtype");
+  TORCH_CHECK_VALUE(B.sizes() == C.sizes(), name, " expects B and C of one shape");
+  TORCH_CHECK_VALUE(!has(D) || (D->scalar_type() == at::kFloat && D->dim() == 2 && D->size(0) == h &&
+                                D->size(1) == p && D->is_contiguous()),
+                    name, " expects a float32 D of shape (nheads, headdim)");
+  TORCH_CHECK_VALUE(!has(z) || (z->sizes() == x.sizes() && z->scalar_type() == x.scalar_type() && z->is_contiguous()),
+                    name, " expects a contiguous z like x");
+  TORCH_CHECK_VALUE(!has(dt_bias) || (dt_bias->scalar_type() == at::kFloat && dt_bias->dim() == 1 &&
+                                      dt_bias->size(0) == h && dt_bias->is_contiguous()),
+                    name, " expects a float32 dt_bias of shape (nheads,)");
+  TORCH_CHECK_VALUE(!has(init) || (init->scalar_type() == at::kFloat && init->dim() == 4 && init->size(0) == b &&
+                                   init->size(1) == h && init->size(2) == p && init->size(3) == B.size(3) &&
+                                   init->is_contiguous()),
+                    name, " expects float32 initial_states (batch, nheads, headdim, dstate)");
+  mcpu_ssd_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x.data_ptr();
+  a.dt = static_cast<const float*>(dt.data_ptr());
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.B = B.data_ptr();
+  a.C = C.data_ptr();
+  a.D = fptr(D);
+  a.z = ptr(z);
+  a.dt_bias = fptr(dt_bias);
+  a.initial_states = fptr(init);
+  a.batch = b;
+  a.seqlen = l;
+  a.nheads = h;
+  a.headdim = p;
+  a.ngroups = B.size(2);
+  a.dstate = B.size(3);
+  a.dtype = dtype_tag(x.scalar_type());
+  a.dt_softplus = softplus ? 1 : 0;
+  a.dt_limit_lo = static_cast<float>(lo);
+  a.dt_limit_hi = static_cast<float>(hi);
+  return a;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> ssd_fwd(const Tensor& x, const Tensor& dt, const Tensor& A,
+                                                   const Tensor& B, const Tensor& C, const optional<Tensor>& D,
+                                                   const optional<Tensor>& z, const optional<Tensor>& dt_bias,
+                                                   const optional<Tensor>& init, bool softplus, double lo,
+                                                   double hi, bool save_for_backward) {
+  const char* name = "mamba_cpu::ssd_fwd";
+  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi);
+  c10::DeviceGuard guard(x.device());
+  Tensor out = at::empty(x.sizes(), x.options());
+  Tensor fin = at::empty({a.batch, a.nheads, a.headdim, a.dstate}, x.options().dtype(at::kFloat));
+  Tensor ysave = (save_for_backward && has(z)) ? at::empty(x.sizes(), x.options()) : x.new_empty({0});
+  // 0 for an empty sequence; for arguments the library rejects, the
+  // forward call below reports why.
+  const size_t nsaved = mcpu_ssd_saved_size(&a);
+  Tensor saved = at::empty({static_cast<int64_t>(nsaved)}, x.options().dtype(at::kByte));
+  a.out = out.data_ptr();
+  a.final_states = static_cast<float*>(fin.data_ptr());
+  a.ysave = ysave.numel() ? ysave.data_ptr() : nullptr;
+  check_rc(mcpu_ssd_fwd(&a, saved.data_ptr(), nsaved, stream_of(x)), name);
+  return {out, fin, saved, ysave};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> ssd_bwd(
+    const Tensor& dout, const optional<Tensor>& dfinal, const Tensor& x, const Tensor& dt, const Tensor& A,
+    const Tensor& B, const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
+    const optional<Tensor>& dt_bias, const optional<Tensor>& init, bool softplus, double lo, double hi,
+    const Tensor& saved, const Tensor& ysave) {
+  const char* name = "mamba_cpu::ssd_bwd";
+  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi);
+  check_gpu(name, opt(dout));
+  check_gpu(name, dfinal);
+  TORCH_CHECK_VALUE(dout.sizes() == x.sizes() && dout.scalar_type() == x.scalar_type() && dout.is_contiguous(),
+                    name, " expects a contiguous dout like x");
+  TORCH_CHECK_VALUE(!has(dfinal) || (dfinal->scalar_type() == at::kFloat && dfinal->is_contiguous() &&
+                                     dfinal->dim() == 4 && dfinal->size(0) == a.batch &&
+                                     dfinal->size(1) == a.nheads && dfinal->size(2) == a.headdim &&
+                                     dfinal->size(3) == a.dstate),
+                    name, " expects a float32 dfinal_states (batch, nheads, headdim, dstate)");
+  const size_t nsaved = mcpu_ssd_saved_size(&a);
+  TORCH_CHECK_VALUE(saved.scalar_type() == at::kByte && static_cast<size_t>(saved.numel()) >= nsaved && saved.is_cuda(),
+                    name, " expects the forward's saved buffer");
+  TORCH_CHECK_VALUE(!has(z) || (ysave.sizes() == x.sizes() && ysave.scalar_type() == x.scalar_type()), name,
+                    " expects the forward's ysave when z is given");
+  c10::DeviceGuard guard(x.device());
+  const auto f32 = x.options().dtype(at::kFloat);
+  Tensor dx = at::empty(x.sizes(), x.options());
+  Tensor ddt = at::empty(dt.sizes(), f32);
+  Tensor dA = at::empty({a.nheads}, f32);
+  Tensor dB = at::empty(B.sizes(), f32);
+  Tensor dC = at::empty(C.sizes(), f32);
+  Tensor dD = has(D) ? at::empty(D->sizes(), f32) : A.new_empty({0});
+  Tensor dz = has(z) ? at::empty(x.sizes(), x.options()) : x.new_empty({0});
+  Tensor dbias = has(dt_bias) ? at::empty({a.nheads}, f32) : A.new_empty({0});
+  Tensor dinit = has(init) ? at::empty(init->sizes(), f32) : A.new_empty({0});
+  a.ysave = has(z) ? ysave.data_ptr() : nullptr;
+  a.dout = dout.data_ptr();
+  a.dfinal_states = fptr(dfinal);
+  a.dx = dx.data_ptr();
+  a.ddt = static_cast<float*>(ddt.data_ptr());
+  a.dA = static_cast<float*>(dA.data_ptr());
+  a.dB = static_cast<float*>(dB.data_ptr());
+  a.dC = static_cast<float*>(dC.data_ptr());
+  a.dD = has(D) ? static_cast<float*>(dD.data_ptr()) : nullptr;
+  a.dz = has(z) ? dz.data_ptr() : nullptr;
+  a.ddt_bias = has(dt_bias) ? static_cast<float*>(dbias.data_ptr()) : nullptr;
+  a.dinitial_states = has(init) ? static_cast<float*>(dinit.data_ptr()) : nullptr;
+  const size_t nws = mcpu_ssd_bwd_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(nws)}, x.options().dtype(at::kByte));
+  check_rc(mcpu_ssd_bwd(&a, saved.data_ptr(), saved.numel(), ws.data_ptr(), nws, stream_of(x)), name);
+  return {dx, ddt, dA, dB, dC, dD, dz, dbias, dinit};
+}
+
 }  // namespace
 }  // namespace mcpu_torch
 
 TORCH_LIBRARY(mamba_cpu, m) {
+  m.def("ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
+        "Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, float dt_hi, "
+        "bool save_for_backward) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("ssd_bwd(Tensor dout, Tensor? dfinal_states, Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, "
+        "Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, "
+        "float dt_hi, Tensor saved, Tensor ysave) -> "
+        "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("selective_scan_fwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
         "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor)");
   m.def("selective_scan_bwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
@@ -1120,6 +1264,8 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("causal_conv1d_bwd", &causal_conv1d_bwd);
   m.impl("causal_conv1d_update", &causal_conv1d_update);
   m.impl("selective_state_update", &selective_state_update);
+  m.impl("ssd_fwd", &ssd_fwd);
+  m.impl("ssd_bwd", &ssd_bwd);
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {

@@ -101,9 +101,24 @@ class StateUpdateArgs(ctypes.Structure):
     ]
 
 
+class SsdArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _P), ("dt", _P), ("A", _P), ("B", _P), ("C", _P), ("D", _P), ("z", _P), ("dt_bias", _P),
+        ("initial_states", _P),
+        ("batch", _I64), ("seqlen", _I64), ("nheads", _I64), ("headdim", _I64), ("ngroups", _I64),
+        ("dstate", _I64),
+        ("dtype", _I32), ("dt_softplus", _I32), ("dt_limit_lo", ctypes.c_float),
+        ("dt_limit_hi", ctypes.c_float),
+        ("out", _P), ("final_states", _P), ("ysave", _P),
+        ("dout", _P), ("dfinal_states", _P),
+        ("dx", _P), ("ddt", _P), ("dA", _P), ("dB", _P), ("dC", _P), ("dD", _P), ("dz", _P),
+        ("ddt_bias", _P), ("dinitial_states", _P),
+    ]
+
+
 _ARGP = {n: ctypes.POINTER(c) for n, c in
          (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-          ("state_update", StateUpdateArgs))}
+          ("state_update", StateUpdateArgs), ("ssd", SsdArgs))}
 
 lib.mcpu_last_error.restype = ctypes.c_char_p
 lib.mcpu_version.restype = ctypes.c_char_p
@@ -132,9 +147,17 @@ lib.mcpu_causal_conv1d_update.argtypes = [_ARGP["conv_update"], _P]
 lib.mcpu_causal_conv1d_update.restype = ctypes.c_int
 lib.mcpu_selective_state_update.argtypes = [_ARGP["state_update"], _P]
 lib.mcpu_selective_state_update.restype = ctypes.c_int
+lib.mcpu_ssd_saved_size.argtypes = [_ARGP["ssd"]]
+lib.mcpu_ssd_saved_size.restype = ctypes.c_size_t
+lib.mcpu_ssd_fwd.argtypes = [_ARGP["ssd"], _P, ctypes.c_size_t, _P]
+lib.mcpu_ssd_fwd.restype = ctypes.c_int
+lib.mcpu_ssd_bwd_workspace_size.argtypes = [_ARGP["ssd"]]
+lib.mcpu_ssd_bwd_workspace_size.restype = ctypes.c_size_t
+lib.mcpu_ssd_bwd.argtypes = [_ARGP["ssd"], _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]
+lib.mcpu_ssd_bwd.restype = ctypes.c_int
 
 for _name, _cls in (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-                    ("state_update", StateUpdateArgs)):
+                    ("state_update", StateUpdateArgs), ("ssd", SsdArgs)):
     _want = lib.mcpu_args_size(_name.encode())
     if _want != ctypes.sizeof(_cls):
         raise ImportError(f"mamba_cpu: {_name} argument block is {ctypes.sizeof(_cls)} bytes here "

@@ -1,0 +1,155 @@
+"""mamba_chunk_scan_combined on MI355X: Mamba-2's SSD scan over the gfx950
+kernels (csrc/ssd.hip), forward and backward.
+
+The reference lists Mamba-2 SSD as roadmap (README.md:7, 94) and has no
+implementation; this follows the public function of the mamba_ssm package
+(mamba_ssm/ops/triton/ssd_combined.py, 2.x): the same signature, argument
+layouts and results. Per batch row and head h (heads split into ngroups
+contiguous groups that share B and C):
+
+    dt_t = clamp(softplus?(dt_t + dt_bias_h), dt_limit)
+    h_t  = exp(dt_t A_h) h_{t-1} + dt_t x_t B_t^T    (headdim x dstate state,
+                                                      h_{-1} = initial_states or 0)
+    y_t  = h_t C_t + D x_t ;  out = y silu(z) when z is given
+
+The kernels scan 64-step chunks whatever `chunk_size` says (it is accepted for
+compatibility; the result does not depend on it beyond float32 rounding).
+Arithmetic and states are float32 for every storage type; the chunk-local
+contractions run on the matrix cores.
+"""
+
+import math
+
+import torch
+
+from mamba_cpu import _C  # noqa: F401  (loads the operator library)
+
+_X_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+_CHUNK = 64
+
+
+def _align(n):
+    return (n + 255) // 256 * 256
+
+
+def _saved_bytes(b, l, h, p, n):
+    """Bytes of the forward's saved buffer (the C ABI's layout): per-chunk
+    running decays (a float pair) and steps, then per-chunk states, float32."""
+    nch = (l + _CHUNK - 1) // _CHUNK
+    chunk = 4 * b * h * nch * _CHUNK
+    return 3 * _align(chunk) + _align(4 * b * nch * h * p * n)
+
+
+@torch.library.register_fake("mamba_cpu::ssd_fwd")
+def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, save_for_backward):
+    b, l, h, p = x.shape
+    n = B.shape[-1]
+    ysave = x.new_empty(x.shape) if (save_for_backward and z is not None) else x.new_empty(0)
+    return (x.new_empty(x.shape), x.new_empty(b, h, p, n, dtype=torch.float32),
+            x.new_empty(_saved_bytes(b, l, h, p, n), dtype=torch.uint8), ysave)
+
+
+@torch.library.register_fake("mamba_cpu::ssd_bwd")
+def _(dout, dfinal_states, x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi,
+      saved, ysave):
+    f32 = dict(dtype=torch.float32)
+    return (x.new_empty(x.shape), dt.new_empty(dt.shape, **f32), A.new_empty(A.shape, **f32),
+            B.new_empty(B.shape, **f32), C.new_empty(C.shape, **f32),
+            A.new_empty(D.shape, **f32) if D is not None else A.new_empty(0),
+            x.new_empty(x.shape) if z is not None else x.new_empty(0),
+            A.new_empty(A.shape, **f32) if dt_bias is not None else A.new_empty(0),
+            A.new_empty(initial_states.shape, **f32) if initial_states is not None else A.new_empty(0))
+
+
+class _SsdScan(torch.autograd.Function):
+    """Autograd of the SSD scan: the forward keeps its per-chunk decays and
+    states (and y before the z gate), the backward reads them."""
+
+    @staticmethod
+    def forward(ctx, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi):
+        out, final, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(
+            x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, True)
+        ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, initial_states, saved, ysave)
+        ctx.cfg = (softplus, lo, hi)
+        ctx.set_materialize_grads(False)
+        return out, final
+
+    @staticmethod
+    def backward(ctx, dout, dfinal):
+        x, dt, A, B, C, D, z, dt_bias, init, saved, ysave = ctx.saved_tensors
+        dout = torch.zeros_like(x) if dout is None else dout.to(x.dtype).contiguous()
+        dfinal = None if dfinal is None else dfinal.float().contiguous()
+        dx, ddt, dA, dB, dC, dD, dz, dbias, dinit = torch.ops.mamba_cpu.ssd_bwd(
+            dout, dfinal, x, dt, A, B, C, D, z, dt_bias, init, *ctx.cfg, saved, ysave)
+        return (dx, ddt, dA, dB.to(B.dtype), dC.to(C.dtype), dD if D is not None else None,
+                dz if z is not None else None, dbias if dt_bias is not None else None,
+                dinit if init is not None else None, None, None, None)
+
+
+def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                              initial_states=None, seq_idx=None, cu_seqlens=None, dt_softplus=False,
+                              dt_limit=(0.0, float("inf")), return_final_states=False,
+                              return_varlen_states=False):
+    """Drop-in for mamba_ssm.ops.triton.ssd_combined.mamba_chunk_scan_combined
+    on ROCm GPU tensors.
+
+    x: (batch, seqlen, nheads, headdim); dt: (batch, seqlen, nheads);
+    A: (nheads,); B, C: (batch, seqlen, ngroups, dstate); D: (nheads, headdim)
+    or (nheads,); z: like x; dt_bias: (nheads,); initial_states:
+    (batch, nheads, headdim, dstate). headdim a multiple of 16 up to 64,
+    dstate a multiple of 16 up to 128.
+    Returns out (like x, in x's dtype) [, final_states (batch, nheads, headdim,
+    dstate) float32]. Packed sequences (seq_idx, cu_seqlens,
+    return_varlen_states) are not supported yet and raise NotImplementedError.
+    """
+    if x.device.type != "cuda":
+        raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
+    if seq_idx is not None or cu_seqlens is not None or return_varlen_states:
+        raise NotImplementedError("mamba_chunk_scan_combined: seq_idx / cu_seqlens / return_varlen_states "
+                                  "are not supported")
+    if int(chunk_size) < 1:
+        raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+    if x.dim() != 4 or dt.dim() != 3 or B.dim() != 4 or C.dim() != 4 or A.dim() != 1:
+        raise ValueError("mamba_chunk_scan_combined expects x (b, l, h, p), dt (b, l, h), A (h,), "
+                         "B and C (b, l, g, n)")
+    b, l, h, p = x.shape
+    if h % B.shape[2] != 0:
+        raise ValueError(f"nheads ({h}) must be divisible by ngroups ({B.shape[2]})")
+    xdt = x.dtype if x.dtype in _X_DTYPES else torch.float32
+    lo, hi = float(dt_limit[0]), float(dt_limit[1])
+    if D is not None:
+        D = D.float()
+        D = (D[:, None].expand(h, p) if D.dim() == 1 else D).contiguous()
+    args = (
+        x.to(xdt).contiguous(), dt.float().contiguous(), A.float().contiguous(),
+        B.to(xdt).contiguous(), C.to(xdt).contiguous(), D,
+        None if z is None else z.to(xdt).contiguous(),
+        None if dt_bias is None else dt_bias.float().contiguous(),
+        None if initial_states is None else initial_states.float().contiguous(),
+        bool(dt_softplus), lo, hi,
+    )
+    needs_grad = torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in args)
+    if needs_grad:
+        out, final = _SsdScan.apply(*args)
+    else:
+        out, final, _, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False)
+    out = out.to(x.dtype)
+    return (out, final) if return_final_states else out
+
+
+def ssd_flops(batch, seqlen, nheads, headdim, ngroups, dstate, backward=False):
+    """Matrix-core FLOPs of the chunked scan (64-step chunks): the products
+    the kernels run, per direction; used to place a timing against the
+    float32 matrix peak."""
+    nch = math.ceil(seqlen / _CHUNK)
+    Q, P, N = _CHUNK, headdim, dstate
+    per = batch * nch * nheads
+    # forward: the chunk state (P x N over Q), C B^T (Q x Q over N), the
+    # intra-chunk output (Q x P over Q) and the state's output (Q x P over N)
+    fwd = per * 2 * (P * N * Q + Q * Q * N + Q * P * Q + Q * P * N)
+    if not backward:
+        return fwd
+    # backward: C B^T, dY (dt x)^T, G^T dY, dCB B, dCB^T C, the seed E (N x P
+    # over Q), then (dt x) dH, dY H and B~ dH^T
+    return per * 2 * (Q * Q * N + Q * Q * P + Q * P * Q + 2 * Q * N * Q + N * P * Q + 3 * Q * N * P)

@@ -59,7 +59,8 @@ def test_argument_blocks_match_the_library():
     from mamba_cpu import _C
 
     for name, cls in (("scan", _C.ScanArgs), ("conv", _C.ConvArgs),
-                      ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs)):
+                      ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs),
+                      ("ssd", _C.SsdArgs)):
         assert _C.lib.mcpu_args_size(name.encode()) == ctypes.sizeof(cls)
     assert _C.lib.mcpu_args_size(b"nonsense") == 0
 
@@ -83,7 +84,8 @@ def _header_field_names(struct):
 @pytest.mark.parametrize("struct,cls_name", [("mcpu_scan_args", "ScanArgs"),
                                              ("mcpu_conv_args", "ConvArgs"),
                                              ("mcpu_conv_update_args", "ConvUpdateArgs"),
-                                             ("mcpu_state_update_args", "StateUpdateArgs")])
+                                             ("mcpu_state_update_args", "StateUpdateArgs"),
+                                             ("mcpu_ssd_args", "SsdArgs")])
 def test_argument_block_fields_follow_the_header(struct, cls_name):
     from mamba_cpu import _C
 
@@ -392,3 +394,58 @@ def test_scan_writes_outputs_through_their_strides():
     for k in ref:
         torch.testing.assert_close(views[k], ref[k], rtol=0, atol=0, msg=lambda m: f"{k}: {m}")
         assert (bufs[k][..., :d] == 7.0).all(), f"{k} wrote outside its view"
+
+
+def _ssd_args(**kw):
+    from mamba_cpu import _C
+
+    a = _C.SsdArgs()
+    a.x = a.dt = a.A = a.B = a.C = a.out = 16  # non-NULL placeholders: never dereferenced
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate = 2, 100, 4, 32, 2, 64
+    a.dtype = _C.MCPU_F32
+    a.dt_limit_lo, a.dt_limit_hi = 0.0, float("inf")
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_ssd_rejects_bad_arguments_before_touching_a_device():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    fwd = lambda a: _rc(L.mcpu_ssd_fwd, ctypes.byref(a), None, 0, None)  # noqa: E731
+    assert _rc(L.mcpu_ssd_fwd, None, None, 0, None)[0] == _C.MCPU_ERR_INVALID
+    for kw, code, word in ((dict(x=None), _C.MCPU_ERR_INVALID, "required"),
+                           (dict(headdim=24), _C.MCPU_ERR_UNSUPPORTED, "headdim"),
+                           (dict(headdim=80), _C.MCPU_ERR_UNSUPPORTED, "headdim"),
+                           (dict(dstate=136), _C.MCPU_ERR_UNSUPPORTED, "dstate"),
+                           (dict(ngroups=3), _C.MCPU_ERR_INVALID, "ngroups"),
+                           (dict(dtype=7), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(dt_limit_lo=1.0, dt_limit_hi=0.5), _C.MCPU_ERR_INVALID, "dt_limit")):
+        rc, msg = fwd(_ssd_args(**kw))
+        assert rc == code and word in msg, (kw, rc, msg)
+    # a saved buffer is needed once there are steps; an empty sequence needs none
+    rc, msg = fwd(_ssd_args())
+    assert rc == _C.MCPU_ERR_INVALID and "saved" in msg
+    rc, msg = _rc(L.mcpu_ssd_bwd, ctypes.byref(_ssd_args()), None, 0, None, 0, None)
+    assert rc == _C.MCPU_ERR_INVALID and "dout" in msg
+
+
+def test_ssd_sizes_follow_the_layout():
+    """The saved buffer holds three float32 (batch, nheads, nchunks, 64) arrays
+    and the per-chunk states, each 256-byte aligned; the Python fake kernel
+    uses the same count; empty inputs need nothing; rejected ones report 0."""
+    from mamba_cpu import _C
+    from mamba_cpu.ops.ssd_combined import _saved_bytes
+
+    L = _C.lib
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    for b, l, h, p, g, n in ((2, 100, 4, 32, 2, 64), (1, 64, 3, 16, 1, 16), (3, 1, 2, 64, 2, 128)):
+        a = _ssd_args(batch=b, seqlen=l, nheads=h, headdim=p, ngroups=g, dstate=n)
+        nch = -(-l // 64)
+        want = 3 * al(4 * b * h * nch * 64) + al(4 * b * nch * h * p * n)
+        assert L.mcpu_ssd_saved_size(ctypes.byref(a)) == want == _saved_bytes(b, l, h, p, n)
+        assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(a)) >= 4 * b * l * h * (p + 2 * n)
+    assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(seqlen=0))) == 0
+    assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(batch=0))) == 0
+    assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(headdim=24))) == 0

@@ -1,0 +1,172 @@
+"""mamba_chunk_scan_combined (Mamba-2's SSD scan) on the GPU against the
+float64 oracle (oracle/ssd.py, pinned by tests/test_oracle_ssd.py).
+
+Cases: sequence lengths that are and are not multiples of the 64-step chunk
+(one chunk, several, a ragged tail, 2048 steps), headdim 16-64, dstate
+16-128, 1, 2 or 4 groups, D per head or per channel, with and without z,
+dt_bias, softplus, a dt_limit clamp, initial states and final states;
+float32, bfloat16 and float16 storage; every gradient; opcheck of the two
+operators; an empty sequence.
+Tolerances (unscaled, |got - want| <= atol + rtol |want|): float32 outputs
+and final states rtol 1e-4 / atol 1e-5; float32 gradients rtol 1e-3 with
+atol 1e-4 for per-element gradients (dx, ddt, dz) and 1e-3 for sums (dA,
+dB, dC, dD, ddt_bias, dinitial_states); 16-bit storage 2e-2 / 2e-2, against
+the oracle on the same rounded inputs and upstream gradients.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_report
+from oracle import ssd as S
+
+import mamba_cpu
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "initial_states")
+
+
+def case(b, l, h, p, g, n, seed=0, D="hp", z=True, bias=True, init=False, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen)  # noqa: E731
+    c = dict(x=r(b, l, h, p).to(dtype), dt=r(b, l, h) * 0.5 - 1.0,
+             A=-torch.exp(torch.rand(h, generator=gen) * math.log(8)),
+             B=r(b, l, g, n).to(dtype), C=r(b, l, g, n).to(dtype))
+    c["D"] = None if D is None else r(*((h, p) if D == "hp" else (h,)))
+    c["z"] = r(b, l, h, p).to(dtype) if z else None
+    c["dt_bias"] = torch.rand(h, generator=gen) * 0.5 if bias else None
+    c["initial_states"] = r(b, h, p, n) if init else None
+    return c
+
+
+def run(c, grads=True, softplus=True, limit=(0.0, float("inf")), seed=1):
+    """out, final states and the gradients of sum(out W) + sum(final V) on
+    the GPU, and W, V."""
+    dev = {k: None if v is None else v.to(DEV).requires_grad_(grads) for k, v in c.items()}
+    out, fin = mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=256, dt_softplus=softplus,
+                                                   dt_limit=limit, return_final_states=True)
+    gen = torch.Generator().manual_seed(seed)
+    W = torch.randn(out.shape, generator=gen).to(out.dtype)
+    V = torch.randn(fin.shape, generator=gen)
+    got = {}
+    if grads:
+        ((out.float() * W.to(DEV).float()).sum() + (fin * V.to(DEV)).sum()).backward()
+        got = {k: v.grad for k, v in dev.items() if v is not None}
+    torch.cuda.synchronize()
+    return out.detach(), fin.detach(), got, W, V
+
+
+def check(c, out, fin, got, W, V, softplus=True, limit=(0.0, float("inf")), low=False):
+    kw = dict(dt_softplus=softplus, dt_limit=limit)
+    want, want_fin = S.ssd_fwd(**c, **kw)
+    o_tol = (2e-2, 2e-2) if low else (1e-4, 1e-5)
+    assert_close_report(out, want, *o_tol, "out")
+    assert_close_report(fin, want_fin, *((2e-2, 2e-2) if low else (1e-4, 1e-5)), "final_states")
+    if not got:
+        return
+    grads = S.ssd_bwd(**c, **kw, dout=W.float(), dfinal_states=V)
+    for name, w in zip(NAMES, grads):
+        if c[name] is None:
+            assert w is None, name
+            continue
+        if low:
+            tol = (2e-2, 2e-2)
+        else:
+            tol = (1e-3, 1e-4) if name in ("x", "dt", "z") else (1e-3, 1e-3)
+        assert_close_report(got[name], w, *tol, f"d{name}")
+
+
+SHAPES = [
+    # b, l, h, p, g, n
+    (2, 64, 2, 16, 1, 16),
+    (1, 100, 4, 32, 2, 32),
+    (2, 130, 4, 64, 1, 128),
+    (1, 200, 8, 16, 4, 64),
+    (1, 37, 2, 64, 2, 48),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "b{}l{}h{}p{}g{}n{}".format(*s))
+def test_forward_and_gradients_match_oracle(shape):
+    c = case(*shape, seed=sum(shape))
+    check(c, *run(c))
+
+
+@pytest.mark.parametrize("opts", [
+    dict(D="h", z=False, bias=False, init=True),
+    dict(D=None, z=True, bias=True, init=True),
+    dict(D="hp", z=False, bias=True, init=False),
+], ids=["Dh-noz-init", "noD-z-init", "noz-bias"])
+@pytest.mark.parametrize("softplus,limit", [(True, (0.0, float("inf"))), (True, (0.05, 0.6)),
+                                            (False, (0.0, float("inf")))], ids=["sp", "sp-clamp", "raw"])
+def test_options_match_oracle(opts, softplus, limit):
+    c = case(2, 90, 4, 32, 2, 32, seed=5, **opts)
+    if not softplus:
+        c["dt"] = c["dt"].abs() * 0.3 + 0.05  # a positive step without softplus
+    check(c, *run(c, softplus=softplus, limit=limit), softplus=softplus, limit=limit)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_low_precision_storage(dtype):
+    c = case(2, 150, 4, 64, 2, 64, seed=9, dtype=dtype)
+    out, fin, got, W, V = run(c)
+    assert out.dtype == dtype and got["x"].dtype == dtype and got["B"].dtype == dtype
+    check(c, out, fin, got, W, V, low=True)
+
+
+def test_long_sequence_2048_steps():
+    """32 chunks: the state passing over many chunks, forward and backward."""
+    c = case(1, 2048, 4, 64, 1, 64, seed=13, init=True)
+    check(c, *run(c))
+
+
+def test_no_grad_forward_equals_training_forward():
+    c = case(1, 130, 4, 32, 2, 32, seed=3)
+    dev = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    with torch.no_grad():
+        a = mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, dt_softplus=True)
+    b = mamba_cpu.mamba_chunk_scan_combined(**{k: None if v is None else v.requires_grad_() for k, v in dev.items()},
+                                            chunk_size=64, dt_softplus=True)
+    assert torch.equal(a, b.detach())
+
+
+def test_empty_sequence_passes_the_initial_state_through():
+    c = case(2, 0, 2, 16, 1, 16, seed=4, init=True)
+    dev = {k: None if v is None else v.to(DEV).requires_grad_() for k, v in c.items()}
+    out, fin = mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, return_final_states=True)
+    assert out.shape == (2, 0, 2, 16)
+    assert torch.equal(fin, dev["initial_states"])
+    V = torch.randn_like(fin)
+    (out.sum() + (fin * V).sum()).backward()
+    assert torch.equal(dev["initial_states"].grad, V)
+    for k in ("A", "D", "dt_bias"):
+        assert torch.count_nonzero(dev[k].grad) == 0, k
+
+
+def test_rejects_unsupported_shapes_and_options():
+    c = case(1, 16, 2, 16, 1, 16)
+    dev = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    with pytest.raises(NotImplementedError):
+        mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64,
+                                            seq_idx=torch.zeros(1, 16, dtype=torch.int32, device=DEV))
+    bad = dict(dev, x=torch.randn(1, 16, 2, 24, device=DEV), z=None, D=None)
+    with pytest.raises(NotImplementedError, match="headdim"):
+        mamba_cpu.mamba_chunk_scan_combined(**bad, chunk_size=64)
+    with pytest.raises(ValueError):
+        mamba_cpu.mamba_chunk_scan_combined(**{k: None if v is None else v.cpu() for k, v in dev.items()},
+                                            chunk_size=64)
+
+
+def test_opcheck_ssd_ops():
+    c = case(1, 70, 2, 16, 1, 16, seed=6, init=True)
+    d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
+            True, 0.0, float("inf"), True)
+    torch.library.opcheck(torch.ops.mamba_cpu.ssd_fwd.default, args)
+    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args)
+    bargs = (torch.randn_like(out), torch.randn_like(fin)) + args[:12] + (saved, ysave)
+    torch.library.opcheck(torch.ops.mamba_cpu.ssd_bwd.default, bargs)
