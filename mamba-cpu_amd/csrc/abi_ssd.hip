@@ -34,7 +34,24 @@ int check_ssd(const mcpu_ssd_args* a) {
   const int64_t nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
   if (nchunks > 0x7fffffffll || a->nheads > 65535 || a->batch > 65535)
     return fail(MCPU_ERR_UNSUPPORTED, "ssd: grid too large");
+  // Tiles move four elements at a time.
+  for (const void* t : {a->x, a->B, a->C, a->z, static_cast<const void*>(a->out), static_cast<const void*>(a->ysave),
+                        a->dout, static_cast<const void*>(a->dx), static_cast<const void*>(a->dz)})
+    if (reinterpret_cast<uintptr_t>(t) % 16 != 0)
+      return fail(MCPU_ERR_INVALID, "ssd: x, z, B, C, out, ysave, dout, dx and dz must be 16-byte aligned");
   return MCPU_OK;
+}
+
+// Heads per workgroup of the chunk kernels: the largest divisor of the
+// heads per group, up to kSsdMaxHeadBlock, that still leaves at least 1024
+// workgroups (four per CU) to spread over the GPU.
+int head_block(const mcpu_ssd_args* a) {
+  const int64_t hpg = a->nheads / a->ngroups;
+  const int64_t chunks = a->batch * ((a->seqlen + kSsdQ - 1) / kSsdQ);
+  int hb = 1;
+  for (int d = 2; d <= kSsdMaxHeadBlock; ++d)
+    if (hpg % d == 0 && chunks * (a->nheads / d) >= 1024) hb = d;
+  return hb;
 }
 
 SsdParams make_ssd(const mcpu_ssd_args* a) {
@@ -57,6 +74,8 @@ SsdParams make_ssd(const mcpu_ssd_args* a) {
   p.dstate = a->dstate;
   p.nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
   p.nslices = (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
+  p.hb = head_block(a);
+  p.nhb = static_cast<int>(a->nheads / p.hb);
   p.softplus = a->dt_softplus != 0;
   p.clamp = (a->dt_limit_lo > 0.f || !std::isinf(a->dt_limit_hi)) ? 1 : 0;
   p.dt_lo = a->dt_limit_lo;
@@ -82,7 +101,7 @@ SavedLayout saved_layout(const SsdParams& p) {
 
 // The backward's workspace.
 struct BwdLayout {
-  size_t dstates = 0, dxt = 0, dB = 0, dC = 0, dcs = 0, dcsL = 0, dA = 0, dbias = 0, dD = 0, total = 0;
+  size_t dstates = 0, dB = 0, dC = 0, dcsL = 0, dA = 0, dbias = 0, dD = 0, total = 0;
 };
 BwdLayout bwd_layout(const SsdParams& p) {
   BwdLayout w;
@@ -94,10 +113,8 @@ BwdLayout bwd_layout(const SsdParams& p) {
   };
   const size_t f = sizeof(float);
   w.dstates = take(f * p.batch * p.nchunks * p.nheads * p.headdim * p.dstate);
-  w.dxt = take(f * p.batch * p.seqlen * p.nheads * p.headdim);
-  w.dB = take(f * p.batch * p.seqlen * p.nheads * p.dstate);
-  w.dC = take(f * p.batch * p.seqlen * p.nheads * p.dstate);
-  w.dcs = take(f * p.batch * p.nheads * p.nchunks * kSsdQ);
+  w.dB = take(f * p.batch * p.seqlen * p.nhb * p.dstate);
+  w.dC = take(f * p.batch * p.seqlen * p.nhb * p.dstate);
   w.dcsL = take(f * p.batch * p.nheads * p.nchunks * p.nslices);
   w.dA = take(f * p.batch * p.nchunks * p.nheads);
   w.dbias = take(f * p.batch * p.nchunks * p.nheads);
@@ -215,20 +232,18 @@ extern "C" int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t sa
   p.dz = a->dz;
   p.dinit = a->dinitial_states;
   p.dstates = reinterpret_cast<float*>(ws + w.dstates);
-  p.dxt = reinterpret_cast<float*>(ws + w.dxt);
-  p.dB_head = reinterpret_cast<float*>(ws + w.dB);
-  p.dC_head = reinterpret_cast<float*>(ws + w.dC);
-  p.dcs = reinterpret_cast<float*>(ws + w.dcs);
+  p.dB_part = reinterpret_cast<float*>(ws + w.dB);
+  p.dC_part = reinterpret_cast<float*>(ws + w.dC);
   p.dcsL = reinterpret_cast<float*>(ws + w.dcsL);
   p.dA_part = reinterpret_cast<float*>(ws + w.dA);
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
   p.dD_part = reinterpret_cast<float*>(ws + w.dD);
   if (int rc = hip_status(ssd_bwd_launch(p, a->dtype, st), "ssd_bwd launch")) return rc;
-  // dB/dC summed over each group's heads; dA / dD / ddt_bias over (batch, chunk).
-  const int64_t hpg = p.nheads / p.ngroups;
+  // dB/dC summed over each group's head blocks; dA / dD / ddt_bias over (batch, chunk).
+  const int64_t blocks_per_group = p.nhb / p.ngroups;
   const PartialSum sums[5] = {
-      {p.dB_head, a->dB, p.batch * p.seqlen * p.ngroups, hpg, p.dstate},
-      {p.dC_head, a->dC, p.batch * p.seqlen * p.ngroups, hpg, p.dstate},
+      {p.dB_part, a->dB, p.batch * p.seqlen * p.ngroups, blocks_per_group, p.dstate},
+      {p.dC_part, a->dC, p.batch * p.seqlen * p.ngroups, blocks_per_group, p.dstate},
       {p.dA_part, a->dA, 1, p.batch * p.nchunks, p.nheads},
       {a->ddt_bias ? p.dbias_part : nullptr, a->ddt_bias, 1, p.batch * p.nchunks, p.nheads},
       {a->dD ? p.dD_part : nullptr, a->dD, 1, p.batch * p.nchunks, p.nheads * p.headdim},

@@ -11,16 +11,19 @@
 //     F3  Y    = (C B^T o M) (dt x) + diag(exp(cs)) C H_c^T + D x,  M[t][s] = exp(cs_t - cs_s) [s <= t]
 //         out  = Y silu(z)
 //   backward (dY the gradient of Y, dH_c^out that of the state leaving chunk c)
-//     K1  intra-chunk: dG = dY (dt x)^T, dCB = dG o M, d(dt x) += (CB o M)^T dY,
-//         dC += dCB B, dB += dCB^T C, dcs from dG o G, and the seed
-//         E_c = (diag(exp(cs)) C)^T dY of dL/dH_c
+//     K1  the seed E_c = (diag(exp(cs)) C)^T dY of dL/dH_c from the chunk's own outputs
 //     K2  dH^out_c = dH^in_{c+1} ; dH^in_c = exp(cs_L) dH^out_c + E_c (reverse over
 //         chunks); dcs_L += <dH^out_c, exp(cs_L) H_c>
-//     K3  state terms: d(dt x) += B~ dH^out^T, dC += diag(exp(cs)) dY H_c,
-//         dB += diag(w) (dt x) dH^out (B~ = diag(w) B, w_s = exp(cs_L - cs_s)),
-//         their dcs terms, then da = suffix sums of dcs, ddt, dx and the
+//     K3  per chunk: dG = dY (dt x)^T, dCB = dG o M, d(dt x) = (CB o M)^T dY
+//         + B~ dH^out^T, dC = dCB B + diag(exp(cs)) dY H_c, dB = dCB^T C +
+//         diag(w) (dt x) dH^out (B~ = diag(w) B, w_s = exp(cs_L - cs_s)), dcs
+//         from all of them, da = suffix sums of dcs, then ddt, dx, dz and the
 //         per-chunk partials of dA, dD, ddt_bias
-//     a fixed-order reduce sums dB/dC over a group's heads and the partials.
+//     a fixed-order reduce sums dB/dC over the head blocks of a group and the
+//     partials.
+// The chunk kernels (F1, F3, K1, K3) give a workgroup one chunk of `hb` heads
+// of one group: B, C and C B^T are staged and formed once and each head reuses
+// them; K3 keeps dB and dC of the block's heads in matrix-core accumulators.
 // Chunks past the sequence end are padded with dt = 0 (no decay, no input).
 #include "mcpu_common.h"
 #include "scan_common.h"
@@ -33,29 +36,62 @@ namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int Q = kSsdQ;
-constexpr int QP = Q + 4;          // padded row lengths of the LDS tiles
+constexpr int QP = Q + 4;          // padded row lengths of the LDS tiles (16-byte multiples)
 constexpr int XP = kSsdMaxP + 4;
 constexpr int NP = kSsdMaxN + 4;
 constexpr int kThreads = 256;
 
-// acc[j] += A(16 x K) B(K x 16 columns 16 j ..) for column tiles j < nt
-// (uniform), operands float32 in LDS: A(i, k) = a[i ai + k ak] (a at the
-// strip's first row), B(k, c) = b[k bk + c bj]. In each
-// v_mfma_f32_16x16x4_f32 lane l supplies A(l % 16, k + l / 16) and
-// B(k + l / 16, l % 16); lane l ends holding D(4 (l / 16) + e, l % 16) in
-// acc[j][e].
-template <int NT>
-__device__ __forceinline__ void mma_strip(v4f (&acc)[NT], int nt, const float* a, int ai, int ak,
-                                          const float* b, int bk, int bj, int K) {
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// acc[j] += A(16 x K) B(K x 16 columns 16 j ..) for column tiles j < NTC,
+// operands float32 in LDS: A(i, k) = a[i ai + k ak] (a at the strip's first
+// row), times `as` when SCALE (the lane's own row factor), B(k, c) = b[k bk +
+// c bj]. K is a multiple of 16: four k-steps of operands are read before
+// their products issue (and no more, to bound the registers). In each
+// v_mfma_f32_16x16x4_f32 lane l supplies A(l % 16, k + l / 16) and B(k + l /
+// 16, l % 16); lane l ends holding D(4 (l / 16) + e, l % 16) in acc[j][e].
+template <int NTC, int NT, bool SCALE>
+__device__ __forceinline__ void mma_n(v4f (&acc)[NT], const float* a, int ai, int ak, const float* b, int bk, int bj,
+                                      int K, float as) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, q = lane >> 4;
   const float* pa = a + r * ai + q * ak;
   const float* pb = b + q * bk + r * bj;
-  for (int k = 0; k < K; k += 4) {
-    const float av = pa[k * ak];
+#pragma clang loop unroll(disable)
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    float av[4], bv[4][NTC];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
-      if (j < nt) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pb[k * bk + 16 * j * bj], acc[j], 0, 0, 0);
+    for (int u = 0; u < 4; ++u) {
+      av[u] = pa[(k0 + 4 * u) * ak];
+      if (SCALE) av[u] *= as;
+#pragma unroll
+      for (int j = 0; j < NTC; ++j) bv[u][j] = pb[(k0 + 4 * u) * bk + 16 * j * bj];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < NTC; ++j) acc[j] = mfma4(av[u], bv[u][j], acc[j]);
+  }
+}
+
+// mma_n for a tile count nt (uniform, 1 <= nt <= NT) known only at run time:
+// one branch picks the compile-time variant, so the products of a k-step
+// issue back to back.
+template <int NT, bool SCALE = false>
+__device__ __forceinline__ void mma(v4f (&acc)[NT], int nt, const float* a, int ai, int ak, const float* b, int bk,
+                                    int bj, int K, float as = 1.f) {
+  static_assert(NT >= 1 && NT <= 8, "tile count");
+  switch (nt) {
+    case 1: mma_n<1, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 2: if constexpr (NT >= 2) mma_n<2, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 3: if constexpr (NT >= 3) mma_n<3, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 4: if constexpr (NT >= 4) mma_n<4, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 5: if constexpr (NT >= 5) mma_n<5, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 6: if constexpr (NT >= 6) mma_n<6, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    case 7: if constexpr (NT >= 7) mma_n<7, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
+    default: if constexpr (NT >= 8) mma_n<8, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
   }
 }
 
@@ -65,15 +101,125 @@ __device__ __forceinline__ void zero(v4f (&acc)[NT]) {
   for (int j = 0; j < NT; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (lane 0 first).
-__device__ __forceinline__ float wave_prefix_sum(float v) {
-  const int lane = threadIdx.x & 63;
+// ---- four consecutive storage elements <-> float4 (16-byte aligned float32,
+// 8-byte aligned 16-bit types) ----
+template <typename Tx> __device__ __forceinline__ float4 ld4(const Tx* p);
+template <> __device__ __forceinline__ float4 ld4<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <> __device__ __forceinline__ float4 ld4<bf16>(const bf16* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
+                     __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
+}
+template <> __device__ __forceinline__ float4 ld4<f16>(const f16* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  auto h = [](uint32_t bits) { return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits))); };
+  return make_float4(h(u.x & 0xffff), h(u.x >> 16), h(u.y & 0xffff), h(u.y >> 16));
+}
+template <typename Tx> __device__ __forceinline__ void st4(Tx* p, float4 v);
+template <> __device__ __forceinline__ void st4<float>(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+template <> __device__ __forceinline__ void st4<bf16>(bf16* p, float4 v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+}
+template <> __device__ __forceinline__ void st4<f16>(f16* p, float4 v) {
+  auto b = [](float f) { return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<f16>(f))); };
+  *reinterpret_cast<uint2*>(p) = make_uint2(b(v.x) | (b(v.y) << 16), b(v.z) | (b(v.w) << 16));
+}
+
+__device__ __forceinline__ float4 scale4(float4 v, float s) { return make_float4(v.x * s, v.y * s, v.z * s, v.w * s); }
+
+// The row of float4 number v of a tile with nv float4 per row: floor((v +
+// 0.5) / nv) in float32 is exact for the tile sizes here (v < 2^11, nv <= 32:
+// the quotient is at least 0.5 / nv away from an integer).
+__device__ __forceinline__ int tile_row(int v, float inv_nv) {
+  return static_cast<int>((static_cast<float>(v) + 0.5f) * inv_nv);
+}
+
+// Largest number of float4 per thread in a staged tile (64 x 128).
+constexpr int kMaxVec = Q * kSsdMaxN / 4 / kThreads;
+
+// LDS tile s (rows of ld floats) = rows r < nrows, columns c < ncols
+// (multiple of 4) of src[r rs + c], times scale[r] when given, rows from
+// nvalid on zero. Every load of the tile issues before the first LDS store.
+template <typename Tx>
+__device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t rs, int nrows, int nvalid, int ncols,
+                                      const float* scale = nullptr) {
+  const int nv = ncols >> 2, total = nrows * nv;
+  const float inv = 1.0f / static_cast<float>(nv);
+  float4 x[kMaxVec];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
+  for (int k = 0; k < kMaxVec; ++k) {
+    const int v = threadIdx.x + k * kThreads;
+    x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (v < total) {
+      const int r = tile_row(v, inv);
+      if (r < nvalid) x[k] = ld4<Tx>(src + r * rs + ((v - r * nv) << 2));
+    }
   }
-  return v;
+#pragma unroll
+  for (int k = 0; k < kMaxVec; ++k) {
+    const int v = threadIdx.x + k * kThreads;
+    if (v < total) {
+      const int r = tile_row(v, inv);
+      const int c = (v - r * nv) << 2;
+      *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(x[k], scale[r]) : x[k];
+    }
+  }
+}
+
+// Largest number of float4 per thread in a (64 x headdim) tile.
+constexpr int kMaxVecX = Q * kSsdMaxP / 4 / kThreads;
+
+// LDS tile of dY = dout silu(z) (dout without z) over a chunk of one head,
+// times scale[r] when given; dz = dout y silu'(z) written on the way when
+// write_dz (y from ysave). `off` is the tile's first element in x layout.
+template <typename Tx, bool HAS_Z>
+__device__ __forceinline__ void stage_dy(float* s, int ld, const SsdParams& p, int64_t off, int64_t rs, int nvalid,
+                                         int ncols, bool write_dz, const float* scale = nullptr) {
+  const int nv = ncols >> 2, total = Q * nv;
+  const float inv = 1.0f / static_cast<float>(nv);
+  const Tx* dout = static_cast<const Tx*>(p.dout) + off;
+  float4 go[kMaxVecX], zz[kMaxVecX], yy[kMaxVecX];
+#pragma unroll
+  for (int k = 0; k < kMaxVecX; ++k) {
+    const int v = threadIdx.x + k * kThreads;
+    go[k] = zz[k] = yy[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (v < total) {
+      const int r = tile_row(v, inv);
+      if (r < nvalid) {
+        const int64_t i = r * rs + ((v - r * nv) << 2);
+        go[k] = ld4<Tx>(dout + i);
+        if (HAS_Z) {
+          zz[k] = ld4<Tx>(static_cast<const Tx*>(p.z) + off + i);
+          if (write_dz) yy[k] = ld4<Tx>(static_cast<const Tx*>(p.ysave) + off + i);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxVecX; ++k) {
+    const int v = threadIdx.x + k * kThreads;
+    if (v >= total) continue;
+    const int r = tile_row(v, inv);
+    const int c = (v - r * nv) << 2;
+    float4 dy = go[k];
+    if (HAS_Z) {
+      const float gx[4] = {go[k].x, go[k].y, go[k].z, go[k].w}, zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
+      const float yv[4] = {yy[k].x, yy[k].y, yy[k].z, yy[k].w};
+      float d[4], dzv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float sg = sigmoid(zx[u]);
+        d[u] = gx[u] * zx[u] * sg;
+        dzv[u] = gx[u] * yv[u] * sg * (1.f + zx[u] * (1.f - sg));
+      }
+      if (write_dz && r < nvalid)
+        st4<Tx>(static_cast<Tx*>(p.dz) + off + r * rs + c, make_float4(dzv[0], dzv[1], dzv[2], dzv[3]));
+      dy = make_float4(d[0], d[1], d[2], d[3]);
+    }
+    *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(dy, scale[r]) : dy;
+  }
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave as a float pair hi + lo:
@@ -150,62 +296,69 @@ __device__ __forceinline__ int64_t state_block(const SsdParams& p, int64_t b, in
   return ((b * p.nchunks + c) * p.nheads + h) * p.headdim * p.dstate;
 }
 
+// Steps of the chunk that exist.
+__device__ __forceinline__ int chunk_steps(const SsdParams& p, int64_t t0) {
+  return static_cast<int>(p.seqlen - t0 < Q ? p.seqlen - t0 : Q);
+}
+
 }  // namespace
 
-// F1: steps and running decays of the chunk (saved for F3 and the backward),
-// and the chunk-end state S(p, n) = sum_s exp(cs_L - cs_s) dt_s x_s(p) B_s(n).
-// Grid (nchunks, nheads, batch); wave w computes state rows p in [16 w, 16 w + 16).
+// F1: steps and running decays of each head's chunk (saved for F3 and the
+// backward), and the chunk-end state S(p, n) = sum_s exp(cs_L - cs_s) dt_s
+// x_s(p) B_s(n). Grid (nchunks, nhb, batch); wave w computes state rows p in
+// [16 w, 16 w + 16).
 template <typename Tx>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdParams p) {
-  __shared__ float s_x[Q][XP];
-  __shared__ float s_B[Q][NP];
-  __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  __shared__ __align__(16) float s_B[Q][NP];
+  __shared__ __align__(16) float s_x[Q][XP];
+  __shared__ float s_sc[Q];
+  const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
-  const int64_t g = h / (H / G);
+  const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
+  const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
-  if (wave == 0) {
-    const float st = ssd_step(p, b, t0 + lane, h, nullptr);
-    float cs, csl;
-    wave_prefix_sum2(st * p.A[h], cs, csl);
-    s_cs[lane] = cs;
-    s_csl[lane] = csl;
-    s_dt[lane] = st;
-    const int64_t row = chunk_row(p, b, h, c);
-    p.cs[row + lane] = cs;
-    p.cs_lo[row + lane] = csl;
-    p.step[row + lane] = st;
-  }
-  __syncthreads();
-  for (int e = tid; e < Q * P; e += kThreads) {
-    const int t = e / P, pp = e % P;
-    const float v = t0 + t < L ? ld<Tx>(p.x, ((b * L + t0 + t) * H + h) * P + pp) : 0.f;
-    s_x[t][pp] = v * s_dt[t] * seg_exp(s_cs, s_csl, Q - 1, t);
-  }
-  for (int e = tid; e < Q * N; e += kThreads) {
-    const int t = e / N, n = e % N;
-    s_B[t][n] = t0 + t < L ? ld<Tx>(p.B, ((b * L + t0 + t) * G + g) * N + n) : 0.f;
-  }
-  __syncthreads();
-  if (16 * wave < P) {
-    v4f acc[kSsdMaxN / 16];
-    zero(acc);
-    mma_strip(acc, static_cast<int>(N / 16), &s_x[0][16 * wave], 1, XP, &s_B[0][0], NP, 1, Q);
-    const int r = lane & 15, q = lane >> 4;
-    float* dst = p.states + state_block(p, b, c, h);
+  const int nvalid = chunk_steps(p, t0);
+  stage<Tx>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
+            static_cast<int>(N));
+  for (int i = 0; i < p.hb; ++i) {
+    const int64_t h = h0 + i;
+    if (wave == 0) {
+      const float st = ssd_step(p, b, t0 + lane, h, nullptr);
+      float cs, csl;
+      wave_prefix_sum2(st * p.A[h], cs, csl);
+      const int64_t row = chunk_row(p, b, h, c);
+      p.cs[row + lane] = cs;
+      p.cs_lo[row + lane] = csl;
+      p.step[row + lane] = st;
+      const float csL = __shfl(cs, Q - 1, 64), cslL = __shfl(csl, Q - 1, 64);
+      s_sc[lane] = st * fast_exp((csL - cs) + (cslL - csl));
+    }
+    __syncthreads();
+    stage<Tx>(&s_x[0][0], XP, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
+              static_cast<int>(P), s_sc);
+    __syncthreads();
+    if (16 * wave < P) {
+      v4f acc[kSsdMaxN / 16];
+      zero(acc);
+      mma(acc, static_cast<int>(N / 16), &s_x[0][16 * wave], 1, XP, &s_B[0][0], NP, 1, Q);
+      float* dst = p.states + state_block(p, b, c, h);
 #pragma unroll
-    for (int j = 0; j < kSsdMaxN / 16; ++j)
-      if (j < N / 16)
+      for (int j = 0; j < kSsdMaxN / 16; ++j)
+        if (j < N / 16)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(16 * wave + 4 * q + e) * N + 16 * j + r] = acc[j][e];
+          for (int e = 0; e < 4; ++e) dst[(16 * wave + 4 * q + e) * N + 16 * j + r] = acc[j][e];
+    }
+    __syncthreads();
   }
 }
 
 // F2: walks the chunks in order, replacing each chunk-end state by the state
 // entering the chunk, H_c = exp(cs_L(c-1)) H_{c-1} + S_{c-1} (H_0 = the
 // initial state or 0), and writes the final state. One thread per state
-// element; grid (nslices, nheads, batch).
+// element; grid (nslices, nheads, batch). The next chunk's loads issue before
+// this chunk's store.
 __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParams p) {
   const int64_t PN = p.headdim * p.dstate, H = p.nheads;
   const int64_t e = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
@@ -215,246 +368,164 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParam
   float* st = p.states + state_block(p, b, 0, h) + e;
   const int64_t cstride = H * PN;
   const float* csl = p.cs + chunk_row(p, b, h, 0) + (Q - 1);
+  float s = st[0], d = csl[0];
   for (int64_t c = 0; c < p.nchunks; ++c) {
-    const float s = st[c * cstride];
-    const float d = fast_exp(csl[c * Q]);
+    const float sc = s, dc = fast_exp(d);
+    if (c + 1 < p.nchunks) {
+      s = st[(c + 1) * cstride];
+      d = csl[(c + 1) * Q];
+    }
     st[c * cstride] = run;
-    run = fmaf(d, run, s);
+    run = fmaf(dc, run, sc);
   }
   if (p.final_states) p.final_states[(b * H + h) * PN + e] = run;
 }
 
 // F3: the chunk's outputs, Y = (C B^T o M) (dt x) + diag(exp(cs)) C H^T + D x,
 // out = Y silu(z) (and Y itself into ysave when the backward needs it).
-// Grid (nchunks, nheads, batch); wave w computes rows t in [16 w, 16 w + 16).
+// Grid (nchunks, nhb, batch); wave w computes rows t in [16 w, 16 w + 16).
+// C B^T is formed once for the block's heads.
 template <typename Tx, bool HAS_Z>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParams p) {
-  __shared__ float s_C[Q][NP];
-  __shared__ float s_BH[Q][NP];     // B (Q x N), then the entering state H (P x N)
-  __shared__ float s_G[Q][QP];
-  __shared__ float s_X[Q][XP];      // dt x
+  __shared__ __align__(16) float s_C[Q][NP];
+  __shared__ __align__(16) float s_BH[Q][NP];     // B (Q x N), then each head's entering state H (P x N)
+  __shared__ __align__(16) float s_G[Q][QP];      // (C B^T o M)[t][s] dt_s
+  __shared__ __align__(16) float s_X[Q][XP];      // x
   __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
-  const int64_t g = h / (H / G);
+  const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
+  const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
-  const int64_t row = chunk_row(p, b, h, c);
-  if (tid < Q) {
-    s_cs[tid] = p.cs[row + tid];
-    s_csl[tid] = p.cs_lo[row + tid];
-    s_dt[tid] = p.step[row + tid];
-  }
-  for (int e = tid; e < Q * N; e += kThreads) {
-    const int t = e / N, n = e % N;
-    const bool ok = t0 + t < L;
-    const int64_t at = ((b * L + t0 + t) * G + g) * N + n;
-    s_C[t][n] = ok ? ld<Tx>(p.C, at) : 0.f;
-    s_BH[t][n] = ok ? ld<Tx>(p.B, at) : 0.f;
+  const int nvalid = chunk_steps(p, t0);
+  const int np = static_cast<int>(P / 16);
+  {
+    const int64_t off = ((b * L + t0) * G + g) * N;
+    stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
   __syncthreads();
-  {
-    v4f cb[Q / 16];
-    zero(cb);
-    mma_strip(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+  v4f cb[Q / 16];
+  zero(cb);
+  mma(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+  for (int i = 0; i < p.hb; ++i) {
+    const int64_t h = h0 + i;
+    const int64_t row = chunk_row(p, b, h, c);
+    const int64_t xoff = ((b * L + t0) * H + h) * P;
+    __syncthreads();  // every wave is done with s_BH, s_G, s_X and s_cs
+    if (tid < Q) {
+      s_cs[tid] = p.cs[row + tid];
+      s_csl[tid] = p.cs_lo[row + tid];
+      s_dt[tid] = p.step[row + tid];
+    }
+    stage<Tx>(&s_X[0][0], XP, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+    stage<float>(&s_BH[0][0], NP, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
+                 static_cast<int>(N));
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < Q / 16; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
-        s_G[t][s] = s <= t ? cb[j][e] * seg_exp(s_cs, s_csl, t, s) : 0.f;
+        s_G[t][s] = s <= t ? cb[j][e] * seg_exp(s_cs, s_csl, t, s) * s_dt[s] : 0.f;
       }
-  }
-  __syncthreads();
-  for (int e = tid; e < Q * P; e += kThreads) {
-    const int t = e / P, pp = e % P;
-    s_X[t][pp] = t0 + t < L ? ld<Tx>(p.x, ((b * L + t0 + t) * H + h) * P + pp) * s_dt[t] : 0.f;
-  }
-  const float* hin = p.states + state_block(p, b, c, h);
-  for (int e = tid; e < P * N; e += kThreads) s_BH[e / N][e % N] = hin[e];
-  __syncthreads();
-  v4f y1[kSsdMaxP / 16], y2[kSsdMaxP / 16];
-  zero(y1);
-  zero(y2);
-  const int np = static_cast<int>(P / 16);
-  mma_strip(y1, np, &s_G[16 * wave][0], QP, 1, &s_X[0][0], XP, 1, Q);
-  mma_strip(y2, np, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
-#pragma unroll
-  for (int j = 0; j < kSsdMaxP / 16; ++j) {
-    if (j >= np) continue;
+    __syncthreads();
+    v4f y1[kSsdMaxP / 16], y2[kSsdMaxP / 16];
+    zero(y1);
+    zero(y2);
+    mma(y1, np, &s_G[16 * wave][0], QP, 1, &s_X[0][0], XP, 1, Q);
+    mma(y2, np, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+    __syncthreads();  // every wave is done reading s_G
+    // Y (float32) into s_G, then out = (Y + D x) silu(z) four elements at a time.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * wave + 4 * q + e;
-      const int64_t pp = 16 * j + r;
-      if (t0 + t >= L) continue;
-      const int64_t at = ((b * L + t0 + t) * H + h) * P + pp;
-      float y = y1[j][e] + fast_exp(s_cs[t]) * y2[j][e];
-      if (p.D) y = fmaf(p.D[h * P + pp], ld<Tx>(p.x, at), y);
-      if (HAS_Z) {
-        if (p.ysave) st<Tx>(p.ysave, at, y);
-        const float zz = ld<Tx>(p.z, at);
-        y *= zz * sigmoid(zz);
+      const float ecs = fast_exp(s_cs[t] + s_csl[t]);
+#pragma unroll
+      for (int j = 0; j < kSsdMaxP / 16; ++j)
+        if (j < np) s_G[t][16 * j + r] = fmaf(ecs, y2[j][e], y1[j][e]);
+    }
+    __syncthreads();
+    {
+      const int nv = np * 4;
+      const float inv = 1.0f / static_cast<float>(nv);
+      float4 zz[kMaxVecX];
+#pragma unroll
+      for (int k = 0; k < kMaxVecX; ++k) {
+        const int v = tid + k * kThreads;
+        zz[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (HAS_Z && v < Q * nv) {
+          const int t = tile_row(v, inv);
+          if (t < nvalid) zz[k] = ld4<Tx>(static_cast<const Tx*>(p.z) + xoff + t * H * P + ((v - t * nv) << 2));
+        }
       }
-      st<Tx>(p.out, at, y);
+#pragma unroll
+      for (int k = 0; k < kMaxVecX; ++k) {
+        const int v = tid + k * kThreads;
+        if (v >= Q * nv) continue;
+        const int t = tile_row(v, inv);
+        if (t >= nvalid) continue;
+        const int pp = (v - t * nv) << 2;
+        const int64_t at = xoff + t * H * P + pp;
+        float y[4] = {s_G[t][pp], s_G[t][pp + 1], s_G[t][pp + 2], s_G[t][pp + 3]};
+        if (p.D) {
+          const float4 d = *reinterpret_cast<const float4*>(p.D + h * P + pp);
+          y[0] = fmaf(d.x, s_X[t][pp], y[0]);
+          y[1] = fmaf(d.y, s_X[t][pp + 1], y[1]);
+          y[2] = fmaf(d.z, s_X[t][pp + 2], y[2]);
+          y[3] = fmaf(d.w, s_X[t][pp + 3], y[3]);
+        }
+        if (HAS_Z) {
+          if (p.ysave) st4<Tx>(static_cast<Tx*>(p.ysave) + at, make_float4(y[0], y[1], y[2], y[3]));
+          const float zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) y[u] *= zx[u] * sigmoid(zx[u]);
+        }
+        st4<Tx>(static_cast<Tx*>(p.out) + at, make_float4(y[0], y[1], y[2], y[3]));
+      }
     }
   }
 }
 
-// dY = dout silu(z) (dout without z) at x-layout index `at`; also dz there.
+// K1: the seed E_c[p][n] = sum_t exp(cs_t) dY[t][p] C[t][n] of dL/dH_c from
+// the chunk's own outputs, for each head of the block, into dstates. Grid
+// (nchunks, nhb, batch); wave w computes rows p in [16 w, 16 w + 16).
 template <typename Tx, bool HAS_Z>
-__device__ __forceinline__ float ssd_dy(const SsdParams& p, int64_t at, bool write_dz) {
-  const float go = ld<Tx>(p.dout, at);
-  if (!HAS_Z) return go;
-  const float zz = ld<Tx>(p.z, at);
-  const float sg = sigmoid(zz);
-  if (write_dz) {
-    const float y = ld<Tx>(p.ysave, at);
-    st<Tx>(p.dz, at, go * y * sg * (1.f + zz * (1.f - sg)));
-  }
-  return go * zz * sg;
-}
-
-// K1: intra-chunk gradients and the seed E_c of dL/dH_c. Grid (nchunks,
-// nheads, batch); wave w owns rows [16 w, 16 w + 16) of every Q-row product.
-template <typename Tx, bool HAS_Z>
-__global__ void __launch_bounds__(kThreads) ssd_bwd_intra_kernel(const SsdParams p) {
-  __shared__ float s_C[Q][NP];
-  __shared__ float s_B[Q][NP];
-  __shared__ float s_X[Q][XP];      // dt x
-  __shared__ float s_dY[Q][XP];
-  __shared__ float s_G[Q][QP];      // G = C B^T o M
-  __shared__ float s_dCB[Q][QP];
-  __shared__ float s_colp[16][Q];   // column sums of dG o G, per (wave, lane quarter)
-  __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+__global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams p) {
+  __shared__ __align__(16) float s_C[Q][NP];
+  __shared__ __align__(16) float s_dY[Q][XP];     // exp(cs_t) dY[t][p]
+  __shared__ float s_ecs[Q];
+  const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
-  const int64_t g = h / (H / G);
+  const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
+  const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
-  const int64_t row = chunk_row(p, b, h, c);
-  if (tid < Q) {
-    s_cs[tid] = p.cs[row + tid];
-    s_csl[tid] = p.cs_lo[row + tid];
-    s_dt[tid] = p.step[row + tid];
-  }
-  __syncthreads();
-  for (int e = tid; e < Q * N; e += kThreads) {
-    const int t = e / N, n = e % N;
-    const bool ok = t0 + t < L;
-    const int64_t at = ((b * L + t0 + t) * G + g) * N + n;
-    s_C[t][n] = ok ? ld<Tx>(p.C, at) : 0.f;
-    s_B[t][n] = ok ? ld<Tx>(p.B, at) : 0.f;
-  }
-  for (int e = tid; e < Q * P; e += kThreads) {
-    const int t = e / P, pp = e % P;
-    const bool ok = t0 + t < L;
-    const int64_t at = ((b * L + t0 + t) * H + h) * P + pp;
-    s_X[t][pp] = ok ? ld<Tx>(p.x, at) * s_dt[t] : 0.f;
-    s_dY[t][pp] = ok ? ssd_dy<Tx, HAS_Z>(p, at, true) : 0.f;
-  }
-  __syncthreads();
-  // CB = C B^T and dG = dY (dt x)^T, rows t of this wave, all columns s.
-  v4f cb[Q / 16], dg[Q / 16];
-  zero(cb);
-  zero(dg);
-  mma_strip(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_B[0][0], 1, NP, static_cast<int>(N));
-  mma_strip(dg, Q / 16, &s_dY[16 * wave][0], XP, 1, &s_X[0][0], 1, XP, static_cast<int>(P));
-  // G = CB o M, dCB = dG o M, R = dG o G: row sums of R in the wave, column
-  // sums through LDS; both in a fixed order.
-  float rowsum[4] = {0.f, 0.f, 0.f, 0.f};
+  const int nvalid = chunk_steps(p, t0);
+  stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
+            static_cast<int>(N));
+  for (int i = 0; i < p.hb; ++i) {
+    const int64_t h = h0 + i;
+    const int64_t row = chunk_row(p, b, h, c);
+    __syncthreads();  // every wave is done with s_dY and s_ecs
+    if (tid < Q) s_ecs[tid] = fast_exp(p.cs[row + tid] + p.cs_lo[row + tid]);
+    __syncthreads();
+    stage_dy<Tx, HAS_Z>(&s_dY[0][0], XP, p, ((b * L + t0) * H + h) * P, H * P, nvalid, static_cast<int>(P), false,
+                        s_ecs);
+    __syncthreads();
+    if (16 * wave < P) {
+      v4f ev[kSsdMaxN / 16];
+      zero(ev);
+      mma(ev, static_cast<int>(N / 16), &s_dY[0][16 * wave], 1, XP, &s_C[0][0], NP, 1, Q);
+      float* dst = p.dstates + state_block(p, b, c, h);
 #pragma unroll
-  for (int j = 0; j < Q / 16; ++j) {
-    float colsum = 0.f;
+      for (int j = 0; j < kSsdMaxN / 16; ++j)
+        if (j < N / 16)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
-      const float m = s <= t ? seg_exp(s_cs, s_csl, t, s) : 0.f;
-      const float gv = cb[j][e] * m, dcb = dg[j][e] * m;
-      const float rv = dg[j][e] * gv;
-      cb[j][e] = gv;
-      dg[j][e] = dcb;
-      rowsum[e] += rv;
-      colsum += rv;
-    }
-    s_colp[4 * wave + q][16 * j + r] = colsum;
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) rowsum[e] = row_allreduce16(rowsum[e]);
-  __syncthreads();
-  // dcs_intra[t] = sum_s R[t][s] - sum_s R[s][t]; lane r == e of quarter q holds row t.
-  {
-    float mine = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (r == e) mine = rowsum[e];
-    if (r < 4) {
-      const int t = 16 * wave + 4 * q + r;
-      float col = 0.f;
-      for (int k = 0; k < 16; ++k) col += s_colp[k][t];
-      p.dcs[row + t] = mine - col;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < Q / 16; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
-      s_G[t][s] = cb[j][e];
-      s_dCB[t][s] = dg[j][e];
-    }
-  __syncthreads();
-  const int np = static_cast<int>(P / 16), nn = static_cast<int>(N / 16);
-  {
-    // d(dt x)[s][p] += sum_t G[t][s] dY[t][p]: rows s of this wave.
-    v4f dx[kSsdMaxP / 16];
-    zero(dx);
-    mma_strip(dx, np, &s_G[0][16 * wave], 1, QP, &s_dY[0][0], XP, 1, Q);
-#pragma unroll
-    for (int j = 0; j < kSsdMaxP / 16; ++j) {
-      if (j >= np) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = 16 * wave + 4 * q + e;
-        if (t0 + s < L) p.dxt[((b * L + t0 + s) * H + h) * P + 16 * j + r] = dx[j][e];
-      }
-    }
-  }
-  {
-    // dC[t][n] = sum_s dCB[t][s] B[s][n] ; dB[s][n] = sum_t dCB[t][s] C[t][n].
-    v4f dcv[kSsdMaxN / 16], dbv[kSsdMaxN / 16];
-    zero(dcv);
-    zero(dbv);
-    mma_strip(dcv, nn, &s_dCB[16 * wave][0], QP, 1, &s_B[0][0], NP, 1, Q);
-    mma_strip(dbv, nn, &s_dCB[0][16 * wave], 1, QP, &s_C[0][0], NP, 1, Q);
-#pragma unroll
-    for (int j = 0; j < kSsdMaxN / 16; ++j) {
-      if (j >= nn) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * wave + 4 * q + e;
-        if (t0 + t >= L) continue;
-        const int64_t at = ((b * L + t0 + t) * H + h) * N + 16 * j + r;
-        p.dC_head[at] = dcv[j][e];
-        p.dB_head[at] = dbv[j][e];
-      }
-    }
-  }
-  __syncthreads();
-  // E_c[n][p] = sum_t exp(cs_t) C[t][n] dY[t][p], stored like a state (p, n).
-  for (int e = tid; e < Q * N; e += kThreads) s_C[e / N][e % N] *= fast_exp(s_cs[e / N]);
-  __syncthreads();
-  float* dst = p.dstates + state_block(p, b, c, h);
-  for (int strip = wave; strip < N / 16; strip += 4) {
-    v4f ev[kSsdMaxP / 16];
-    zero(ev);
-    mma_strip(ev, np, &s_C[0][16 * strip], 1, NP, &s_dY[0][0], XP, 1, Q);
-#pragma unroll
-    for (int j = 0; j < kSsdMaxP / 16; ++j) {
-      if (j >= np) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[(16 * j + r) * N + 16 * strip + 4 * q + e] = ev[j][e];
+          for (int e = 0; e < 4; ++e) dst[(16 * wave + 4 * q + e) * N + 16 * j + r] = ev[j][e];
     }
   }
 }
@@ -463,7 +534,8 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_intra_kernel(const SsdParams
 // chunk c) replaces E_c in dstates, dH^in_c = exp(cs_L) dH^out_c + E_c
 // carries on, and <dH^out_c, exp(cs_L) H_c> (this slice's share of dL/dcs_L)
 // goes to dcsL. The gradient of the initial state is what is left after
-// chunk 0. Grid (nslices, nheads, batch).
+// chunk 0. Grid (nslices, nheads, batch). The next chunk's loads issue before
+// this chunk's store.
 __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams p) {
   __shared__ float s_part[kThreads / 64];
   const int64_t PN = p.headdim * p.dstate, H = p.nheads;
@@ -475,199 +547,295 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams 
   const int64_t base = state_block(p, b, 0, h) + (ok ? e : 0);
   const int64_t cstride = H * PN;
   const float* csl = p.cs + chunk_row(p, b, h, 0) + (Q - 1);
-  for (int64_t c = p.nchunks - 1; c >= 0; --c) {
-    const float ec = ok ? p.dstates[base + c * cstride] : 0.f;
-    const float hin = ok ? p.states[base + c * cstride] : 0.f;
-    const float d = fast_exp(csl[c * Q]);
+  float* dcsl = p.dcsL + (chunk_row(p, b, h, 0) / Q) * p.nslices + blockIdx.x;
+  const int64_t last = p.nchunks - 1;
+  float ec = ok ? p.dstates[base + last * cstride] : 0.f;
+  float hin = ok ? p.states[base + last * cstride] : 0.f;
+  float dl = csl[last * Q];
+  for (int64_t c = last; c >= 0; --c) {
+    const float ecc = ec, hc = hin, d = fast_exp(dl);
+    if (c > 0) {
+      ec = ok ? p.dstates[base + (c - 1) * cstride] : 0.f;
+      hin = ok ? p.states[base + (c - 1) * cstride] : 0.f;
+      dl = csl[(c - 1) * Q];
+    }
     if (ok) p.dstates[base + c * cstride] = run;
-    const float part = wave_total(run * d * hin);
+    const float part = wave_total(run * d * hc);
     if (lane == 0) s_part[wave] = part;
     __syncthreads();
-    if (threadIdx.x == 0)
-      p.dcsL[(chunk_row(p, b, h, 0) / Q + c) * p.nslices + blockIdx.x] =
-          (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    if (threadIdx.x == 0) dcsl[c * p.nslices] = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
     __syncthreads();
-    run = fmaf(d, run, ec);
+    run = fmaf(d, run, ecc);
   }
   if (ok && p.dinit) p.dinit[(b * H + h) * PN + e] = run;
 }
 
-// K3: the state terms and the combine. Grid (nchunks, nheads, batch); wave w
-// owns rows [16 w, 16 w + 16) of every Q-row product.
+// K3: every gradient of a chunk, for each head of the block. Grid (nchunks,
+// nhb, batch); wave w owns rows [16 w, 16 w + 16) of every Q-row product.
+// dB and dC of the block's heads stay in accumulators and are written once,
+// as the block's partial sums.
 template <typename Tx, bool HAS_Z>
-__global__ void __launch_bounds__(kThreads) ssd_bwd_state_kernel(const SsdParams p) {
-  __shared__ float s_X[Q][XP];      // dt x
-  __shared__ float s_dY[Q][XP];
-  __shared__ float s_dH[kSsdMaxP][NP];
-  __shared__ float s_H[kSsdMaxP][NP];
-  __shared__ float s_Bt[Q][NP];     // exp(cs_L - cs_s) B
-  __shared__ float s_dcs[Q];
-  __shared__ float s_tot[4];
+__global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdParams p) {
+  __shared__ __align__(16) float s_C[Q][NP];
+  __shared__ __align__(16) float s_B[Q][NP];
+  __shared__ __align__(16) float s_X[Q][XP];      // x
+  __shared__ __align__(16) float s_dY[Q][XP];     // dY
+  __shared__ __align__(16) float s_U[Q][QP];      // G = C B^T o M, then dH^out (P x 64-state half)
+  __shared__ __align__(16) float s_V[Q][QP];      // dCB, then H (P x 64-state half)
+  __shared__ float s_colp[16][Q];                 // column sums of dG o G, per (wave, lane quarter)
   __shared__ float s_dD[16][kSsdMaxP];
-  __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
-  __shared__ float s_w[Q];          // exp(cs_L - cs_s)
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  __shared__ float s_cs[Q], s_csl[Q], s_dt[Q], s_w[Q], s_ecs[Q], s_dcs[Q];
+  __shared__ float s_tot[4], s_wa[4], s_wb[4];
+  const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
-  const int64_t g = h / (H / G);
+  const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
+  const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
-  const int64_t row = chunk_row(p, b, h, c);
-  if (tid < Q) {
-    s_cs[tid] = p.cs[row + tid];
-    s_csl[tid] = p.cs_lo[row + tid];
-    s_dt[tid] = p.step[row + tid];
-  }
-  __syncthreads();
-  if (tid < Q) s_w[tid] = seg_exp(s_cs, s_csl, Q - 1, tid);
-  for (int e = tid; e < Q * P; e += kThreads) {
-    const int t = e / P, pp = e % P;
-    const bool ok = t0 + t < L;
-    const int64_t at = ((b * L + t0 + t) * H + h) * P + pp;
-    s_X[t][pp] = ok ? ld<Tx>(p.x, at) * s_dt[t] : 0.f;
-    s_dY[t][pp] = ok ? ssd_dy<Tx, HAS_Z>(p, at, false) : 0.f;
-  }
-  const int64_t sb = state_block(p, b, c, h);
-  for (int e = tid; e < P * N; e += kThreads) {
-    s_dH[e / N][e % N] = p.dstates[sb + e];
-    s_H[e / N][e % N] = p.states[sb + e];
-  }
-  __syncthreads();
-  for (int e = tid; e < Q * N; e += kThreads) {
-    const int t = e / N, n = e % N;
-    s_Bt[t][n] = t0 + t < L ? ld<Tx>(p.B, ((b * L + t0 + t) * G + g) * N + n) * s_w[t] : 0.f;
-  }
-  __syncthreads();
+  const int nvalid = chunk_steps(p, t0);
   const int np = static_cast<int>(P / 16), nn = static_cast<int>(N / 16);
-  // T = (dt x) dH^out (rows s), dYH = dY H (rows t): both Q x N.
-  v4f tv[kSsdMaxN / 16], yh[kSsdMaxN / 16];
-  zero(tv);
-  zero(yh);
-  mma_strip(tv, nn, &s_X[16 * wave][0], XP, 1, &s_dH[0][0], NP, 1, static_cast<int>(P));
-  mma_strip(yh, nn, &s_dY[16 * wave][0], XP, 1, &s_H[0][0], NP, 1, static_cast<int>(P));
-  float a_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n C dC_state
-  float b_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n B~ T
+  {
+    const int64_t off = ((b * L + t0) * G + g) * N;
+    stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
+  }
+  __syncthreads();
+  v4f cb[Q / 16];
+  zero(cb);
+  mma(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_B[0][0], 1, NP, static_cast<int>(N));
+  v4f dBa[kSsdMaxN / 16], dCa[kSsdMaxN / 16];
+  zero(dBa);
+  zero(dCa);
+  for (int i = 0; i < p.hb; ++i) {
+    const int64_t h = h0 + i;
+    const int64_t row = chunk_row(p, b, h, c);
+    const int64_t xoff = ((b * L + t0) * H + h) * P;
+    const int64_t sb = state_block(p, b, c, h);
+    __syncthreads();  // every wave is done with the previous head's tiles
+    if (tid < Q) {
+      const float cs = p.cs[row + tid], csl = p.cs_lo[row + tid];
+      const float csL = p.cs[row + Q - 1], cslL = p.cs_lo[row + Q - 1];
+      s_cs[tid] = cs;
+      s_csl[tid] = csl;
+      s_dt[tid] = p.step[row + tid];
+      s_w[tid] = fast_exp((csL - cs) + (cslL - csl));
+      s_ecs[tid] = fast_exp(cs + csl);
+    }
+    stage<Tx>(&s_X[0][0], XP, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+    stage_dy<Tx, HAS_Z>(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
+    __syncthreads();
+    // dGraw = dY x^T (rows t of this wave, all columns s); then with M and dt:
+    // G = CB o M, dCB = dt_s dGraw o M, R = dCB o CB (= dG o G); the row sums
+    // of R in the wave, its column sums through LDS, both in a fixed order.
+    float rowsum[4] = {0.f, 0.f, 0.f, 0.f};
+    {
+      v4f dg[Q / 16];
+      zero(dg);
+      mma(dg, Q / 16, &s_dY[16 * wave][0], XP, 1, &s_X[0][0], 1, XP, static_cast<int>(P));
 #pragma unroll
-  for (int j = 0; j < kSsdMaxN / 16; ++j) {
-    if (j >= nn) continue;
+      for (int j = 0; j < Q / 16; ++j) {
+        float colsum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
+          const float m = s <= t ? seg_exp(s_cs, s_csl, t, s) : 0.f;
+          const float dcb = dg[j][e] * s_dt[s] * m;
+          const float rv = dcb * cb[j][e];
+          s_U[t][s] = cb[j][e] * m;
+          s_V[t][s] = dcb;
+          rowsum[e] += rv;
+          colsum += rv;
+        }
+        s_colp[4 * wave + q][16 * j + r] = colsum;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rowsum[e] = row_allreduce16(rowsum[e]);
+    __syncthreads();
+    // dcs_intra[t] = sum_s R[t][s] - sum_s R[s][t]; lane r == e of quarter q has row t.
+    if (r < 4) {
+      float mine = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r == e) mine = rowsum[e];
+      const int t = 16 * wave + 4 * q + r;
+      float col = 0.f;
+      for (int k = 0; k < 16; ++k) col += s_colp[k][t];
+      s_dcs[t] = mine - col;
+    }
+    // d(dt x)[s][p] = sum_t G[t][s] dY[t][p] (rows s of this wave), then the state part below.
+    v4f dxa[kSsdMaxP / 16];
+    zero(dxa);
+    mma(dxa, np, &s_U[0][16 * wave], 1, QP, &s_dY[0][0], XP, 1, Q);
+    // dC[t][n] += sum_s dCB[t][s] B[s][n] ; dB[s][n] += sum_t dCB[t][s] C[t][n].
+    mma(dCa, nn, &s_V[16 * wave][0], QP, 1, &s_B[0][0], NP, 1, Q);
+    mma(dBa, nn, &s_V[0][16 * wave], 1, QP, &s_C[0][0], NP, 1, Q);
+    // State terms, over 64-state halves of dH^out and H.
+    float a_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n C[t][n] exp(cs_t) (dY H)[t][n]
+    float b_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n w_s B[s][n] ((dt x) dH)[s][n]
+    const float dt_row = s_dt[16 * wave + r], w_row = s_w[16 * wave + r];
+#pragma unroll
+    for (int half = 0; half < kSsdMaxN / 64; ++half) {
+      const int n0 = 64 * half;
+      if (n0 >= N) break;
+      const int nw = static_cast<int>(N - n0 < 64 ? N - n0 : 64);
+      const int nt = nw / 16;
+      __syncthreads();  // every wave is done reading s_U / s_V
+      stage<float>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      stage<float>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      __syncthreads();
+      v4f tv[4], yh[4];
+      zero(tv);
+      zero(yh);
+      // tv[s][n] = sum_p dt_s x[s][p] dH[p][n] ; yh[t][n] = sum_p dY[t][p] H[p][n]
+      mma<4, true>(tv, nt, &s_X[16 * wave][0], XP, 1, &s_U[0][0], QP, 1, static_cast<int>(P), dt_row);
+      mma(yh, nt, &s_dY[16 * wave][0], XP, 1, &s_V[0][0], QP, 1, static_cast<int>(P));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j >= nt) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = 16 * wave + 4 * q + e;
+          const int n = n0 + 16 * j + r;
+          const float wt = s_w[t] * tv[j][e];
+          const float ys = s_ecs[t] * yh[j][e];
+          dBa[4 * half + j][e] += wt;
+          dCa[4 * half + j][e] += ys;
+          b_row[e] = fmaf(s_B[t][n], wt, b_row[e]);
+          a_row[e] = fmaf(s_C[t][n], ys, a_row[e]);
+        }
+      }
+      // d(dt x)[s][p] += sum_n w_s B[s][n] dH[p][n]
+      mma<kSsdMaxP / 16, true>(dxa, np, &s_B[16 * wave][n0], NP, 1, &s_U[0][0], 1, QP, nw, w_row);
+    }
+    // sum_p d(dt x) x (for dstep) ; dD partial sums (rows past the sequence are 0).
+    float c_row[4] = {0.f, 0.f, 0.f, 0.f};
+    float dD_col[kSsdMaxP / 16];
+#pragma unroll
+    for (int j = 0; j < kSsdMaxP / 16; ++j) dD_col[j] = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * q + e;
-      const int64_t n = 16 * j + r;
-      const float bt = s_Bt[t][n];
-      b_row[e] = fmaf(bt, tv[j][e], b_row[e]);
-      if (t0 + t >= L) continue;
-      const float ecs = fast_exp(s_cs[t]);
-      const float dcs_state = ecs * yh[j][e];
-      const int64_t at = ((b * L + t0 + t) * H + h) * N + n;
-      a_row[e] = fmaf(ld<Tx>(p.C, ((b * L + t0 + t) * G + g) * N + n), dcs_state, a_row[e]);
-      p.dC_head[at] += dcs_state;
-      p.dB_head[at] += s_w[t] * tv[j][e];
-    }
-  }
-  // d(dt x) state part: B~ dH^out^T (rows s, columns p).
-  v4f dxs[kSsdMaxP / 16];
-  zero(dxs);
-  mma_strip(dxs, np, &s_Bt[16 * wave][0], NP, 1, &s_dH[0][0], 1, NP, static_cast<int>(N));
-  float c_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_p d(dt x) x
-  float dD_col[kSsdMaxP / 16];
+      const int s = 16 * wave + 4 * q + e;
 #pragma unroll
-  for (int j = 0; j < kSsdMaxP / 16; ++j) {
-    dD_col[j] = 0.f;
-    if (j >= np) continue;
+      for (int j = 0; j < kSsdMaxP / 16; ++j) {
+        if (j >= np) continue;
+        const int pp = 16 * j + r;
+        const float xv = s_X[s][pp];
+        c_row[e] = fmaf(dxa[j][e], xv, c_row[e]);
+        dD_col[j] = fmaf(s_dY[s][pp], xv, dD_col[j]);
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * q + e;
-      if (t0 + t >= L) continue;
-      const int64_t pp = 16 * j + r;
-      const int64_t at = ((b * L + t0 + t) * H + h) * P + pp;
-      const float dxt = p.dxt[at] + dxs[j][e];
-      const float xv = ld<Tx>(p.x, at);
-      const float dy = s_dY[t][pp];
-      c_row[e] = fmaf(dxt, xv, c_row[e]);
-      dD_col[j] = fmaf(dy, xv, dD_col[j]);
-      float dxv = dxt * s_dt[t];
-      if (p.D) dxv = fmaf(p.D[h * P + pp], dy, dxv);
-      st<Tx>(p.dx, at, dxv);
+      a_row[e] = row_allreduce16(a_row[e]);
+      b_row[e] = row_allreduce16(b_row[e]);
+      c_row[e] = row_allreduce16(c_row[e]);
+    }
+#pragma unroll
+    for (int j = 0; j < kSsdMaxP / 16; ++j)
+      if (j < np) s_dD[4 * wave + q][16 * j + r] = dD_col[j];
+    // the chunk's sum of b_row is the cs_L term of the states' dependence on w
+    float bsum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bsum += b_row[e];  // this quarter's 4 rows, alike in every lane of the row
+    bsum = wave_total(r == 0 ? bsum : 0.f);
+    if (lane == 0) s_tot[wave] = bsum;
+    float c_mine = 0.f;
+    if (r < 4) {
+      float av = 0.f, bv = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r == e) {
+          av = a_row[e];
+          bv = b_row[e];
+          c_mine = c_row[e];
+        }
+      s_dcs[16 * wave + 4 * q + r] += av - bv;
+    }
+    __syncthreads();  // every wave is done reading s_U / s_V
+    // dx = dt d(dt x) + D dY into s_V, stored below four elements at a time
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = 16 * wave + 4 * q + e;
+#pragma unroll
+      for (int j = 0; j < kSsdMaxP / 16; ++j) {
+        if (j >= np) continue;
+        const int pp = 16 * j + r;
+        float dxv = dxa[j][e] * s_dt[s];
+        if (p.D) dxv = fmaf(p.D[h * P + pp], s_dY[s][pp], dxv);
+        s_V[s][pp] = dxv;
+      }
+    }
+    if (wave == 0) {
+      // add the cs_L terms, then da = suffix sums of dcs over the chunk
+      float v = s_dcs[lane];
+      if (lane == Q - 1) {
+        float l = (s_tot[0] + s_tot[1]) + (s_tot[2] + s_tot[3]);
+        const float* dl = p.dcsL + (row / Q) * p.nslices;
+        for (int64_t k = 0; k < p.nslices; ++k) l += dl[k];
+        v += l;
+      }
+      s_dcs[lane] = wave_suffix_sum(v);
+    }
+    __syncthreads();
+    // dstep = sum_p d(dt x) x + da A, then through softplus / clamp / bias.
+    float ddt_raw = 0.f, dA_term = 0.f;
+    if (r < 4) {
+      const int t = 16 * wave + 4 * q + r;
+      if (t < nvalid) {
+        float gfac;
+        ssd_step(p, b, t0 + t, h, &gfac);
+        const float da = s_dcs[t];
+        ddt_raw = fmaf(da, p.A[h], c_mine) * gfac;
+        dA_term = da * s_dt[t];
+        p.ddt[(b * L + t0 + t) * H + h] = ddt_raw;
+      }
+    }
+    {
+      const int nv = np * 4;
+      const float inv = 1.0f / static_cast<float>(nv);
+#pragma unroll
+      for (int k = 0; k < kMaxVecX; ++k) {
+        const int v = tid + k * kThreads;
+        if (v >= Q * nv) continue;
+        const int s = tile_row(v, inv);
+        if (s >= nvalid) continue;
+        const int pp = (v - s * nv) << 2;
+        st4<Tx>(static_cast<Tx*>(p.dx) + xoff + s * H * P + pp,
+                *reinterpret_cast<const float4*>(&s_V[s][pp]));
+      }
+    }
+    const float wa = wave_total(dA_term), wb = wave_total(ddt_raw);
+    if (lane == 0) {
+      s_wa[wave] = wa;
+      s_wb[wave] = wb;
+    }
+    __syncthreads();
+    const int64_t prt = (b * p.nchunks + c) * H + h;
+    if (tid == 0) {
+      p.dA_part[prt] = (s_wa[0] + s_wa[1]) + (s_wa[2] + s_wa[3]);
+      p.dbias_part[prt] = (s_wb[0] + s_wb[1]) + (s_wb[2] + s_wb[3]);
+    }
+    if (tid < P) {
+      float v = 0.f;
+      for (int k = 0; k < 16; ++k) v += s_dD[k][tid];
+      p.dD_part[prt * P + tid] = v;
     }
   }
+  // the block's dB and dC partial sums
+  const int64_t hbk = blockIdx.y;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    a_row[e] = row_allreduce16(a_row[e]);
-    b_row[e] = row_allreduce16(b_row[e]);
-    c_row[e] = row_allreduce16(c_row[e]);
-  }
+    const int t = 16 * wave + 4 * q + e;
+    if (t >= nvalid) continue;
+    const int64_t at = ((b * L + t0 + t) * p.nhb + hbk) * N;
 #pragma unroll
-  for (int j = 0; j < kSsdMaxP / 16; ++j)
-    if (j < np) s_dD[4 * wave + q][16 * j + r] = dD_col[j];
-  // sum over the chunk of sum_n B~ T (the cs_L term), in a fixed order
-  float bsum = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) bsum += b_row[e];  // this quarter's 4 rows, every lane of the row alike
-  bsum = (r == 0) ? bsum : 0.f;
-  bsum = wave_total(bsum);
-  if (lane == 0) s_tot[wave] = bsum;
-  // dcs (without the cs_L terms) for the 4 rows this lane quarter holds
-  if (r < 4) {
-    float av = 0.f, bv = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (r == e) {
-        av = a_row[e];
-        bv = b_row[e];
-      }
-    const int t = 16 * wave + 4 * q + r;
-    s_dcs[t] = p.dcs[row + t] + av - bv;
-  }
-  __syncthreads();
-  float c_mine = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    if (r == e) c_mine = c_row[e];
-  if (wave == 0) {
-    // add the cs_L terms, then da = suffix sums of dcs over the chunk
-    float v = s_dcs[lane];
-    if (lane == Q - 1) {
-      float l = (s_tot[0] + s_tot[1]) + (s_tot[2] + s_tot[3]);
-      const float* dl = p.dcsL + (chunk_row(p, b, h, 0) / Q + c) * p.nslices;
-      for (int64_t k = 0; k < p.nslices; ++k) l += dl[k];
-      v += l;
+    for (int j = 0; j < kSsdMaxN / 16; ++j) {
+      if (j >= nn) continue;
+      p.dC_part[at + 16 * j + r] = dCa[j][e];
+      p.dB_part[at + 16 * j + r] = dBa[j][e];
     }
-    const float da = wave_suffix_sum(v);
-    s_dcs[lane] = da;
-  }
-  __syncthreads();
-  // dstep = sum_p d(dt x) x + da A, then through softplus / clamp / bias.
-  float ddt_raw = 0.f, dA_term = 0.f;
-  if (r < 4) {
-    const int t = 16 * wave + 4 * q + r;
-    if (t0 + t < L) {
-      float gfac;
-      ssd_step(p, b, t0 + t, h, &gfac);
-      const float da = s_dcs[t];
-      const float dstep = fmaf(da, p.A[h], c_mine);
-      ddt_raw = dstep * gfac;
-      dA_term = da * s_dt[t];
-      p.ddt[(b * L + t0 + t) * H + h] = ddt_raw;
-    }
-  }
-  // per-chunk partials: dA, ddt_bias (wave sums, then the 4 waves), dD (columns)
-  const float wa = wave_total(dA_term), wb = wave_total(ddt_raw);
-  __syncthreads();
-  if (lane == 0) {
-    s_dcs[wave] = wa;
-    s_dcs[4 + wave] = wb;
-  }
-  __syncthreads();
-  const int64_t prt = (b * p.nchunks + c) * H + h;
-  if (tid == 0) {
-    p.dA_part[prt] = (s_dcs[0] + s_dcs[1]) + (s_dcs[2] + s_dcs[3]);
-    p.dbias_part[prt] = (s_dcs[4] + s_dcs[5]) + (s_dcs[6] + s_dcs[7]);
-  }
-  if (tid < P) {
-    float v = 0.f;
-    for (int k = 0; k < 16; ++k) v += s_dD[k][tid];
-    p.dD_part[prt * P + tid] = v;
   }
 }
 
@@ -675,8 +843,7 @@ namespace {
 
 template <typename Tx>
 hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
-  const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nheads),
-                    static_cast<unsigned>(p.batch));
+  const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
   hipLaunchKernelGGL(ssd_chunk_state_kernel<Tx>, chunks, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError()) return e;
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
@@ -690,17 +857,16 @@ hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
 
 template <typename Tx>
 hipError_t bwd_t(const SsdParams& p, hipStream_t st) {
-  const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nheads),
-                    static_cast<unsigned>(p.batch));
+  const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
                     static_cast<unsigned>(p.batch));
-  if (p.z) hipLaunchKernelGGL((ssd_bwd_intra_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((ssd_bwd_intra_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError()) return e;
   hipLaunchKernelGGL(ssd_bwd_pass_kernel, slices, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError()) return e;
-  if (p.z) hipLaunchKernelGGL((ssd_bwd_state_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((ssd_bwd_state_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 

@@ -11,12 +11,15 @@ constexpr int kSsdQ = 64;         // steps per chunk
 constexpr int kSsdMaxP = 64;      // largest headdim
 constexpr int kSsdMaxN = 128;     // largest dstate
 constexpr int kSsdSlice = 256;    // state elements per workgroup of the chunk-passing kernels
+constexpr int kSsdMaxHeadBlock = 8;  // heads one workgroup of the chunk kernels walks through
 
 // Layouts (all contiguous): x, z, out, ysave, dx, dz (batch, seqlen, nheads,
 // headdim) in the storage type; dt, ddt (batch, seqlen, nheads) float32;
 // B, C (batch, seqlen, ngroups, dstate) in the storage type; states
 // (batch, nheads, headdim, dstate) float32; heads split into ngroups
-// contiguous groups sharing B and C.
+// contiguous groups sharing B and C. The chunk kernels give each workgroup
+// one chunk of `hb` consecutive heads of one group (head block; nhb = nheads
+// / hb of them), so B, C and C B^T are staged and formed once per block.
 struct SsdParams {
   const void* x;
   const float* dt;
@@ -46,15 +49,14 @@ struct SsdParams {
   float* dinit;
   float* dstates;           // like states: first the chunk's seed dL/dH_in from its own outputs,
                             // then dL/d(state leaving the chunk)
-  float* dxt;               // (batch, seqlen, nheads, headdim): intra-chunk dL/d(dt x)
-  float* dB_head;           // (batch, seqlen, nheads, dstate): per-head dB, summed over a group later
-  float* dC_head;
-  float* dcs;               // (batch, nheads, nchunks, Q): intra-chunk dL/dcs
+  float* dB_part;           // (batch, seqlen, nhb, dstate): dB summed over a head block
+  float* dC_part;
   float* dcsL;              // (batch, nheads, nchunks, nslices): dL/dcs_last from the passing, per slice
   float* dA_part;           // (batch * nchunks, nheads)
   float* dbias_part;        // (batch * nchunks, nheads)
   float* dD_part;           // (batch * nchunks, nheads, headdim)
   int64_t batch, seqlen, nheads, headdim, ngroups, dstate, nchunks, nslices;
+  int hb, nhb;              // heads per block, blocks over the heads
   int softplus;
   int clamp;                // the step is clamped to [dt_lo, dt_hi]
   float dt_lo, dt_hi;

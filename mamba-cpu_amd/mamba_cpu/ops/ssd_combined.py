@@ -32,6 +32,12 @@ def _align(n):
     return (n + 255) // 256 * 256
 
 
+def _aligned(t):
+    """t, copied when its data does not start on a 16-byte boundary (the
+    kernels move four elements at a time)."""
+    return t if t is None or t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _saved_bytes(b, l, h, p, n):
     """Bytes of the forward's saved buffer (the C ABI's layout): per-chunk
     running decays (a float pair) and steps, then per-chunk states, float32."""
@@ -77,7 +83,7 @@ class _SsdScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, dfinal):
         x, dt, A, B, C, D, z, dt_bias, init, saved, ysave = ctx.saved_tensors
-        dout = torch.zeros_like(x) if dout is None else dout.to(x.dtype).contiguous()
+        dout = torch.zeros_like(x) if dout is None else _aligned(dout.to(x.dtype).contiguous())
         dfinal = None if dfinal is None else dfinal.float().contiguous()
         dx, ddt, dA, dB, dC, dD, dz, dbias, dinit = torch.ops.mamba_cpu.ssd_bwd(
             dout, dfinal, x, dt, A, B, C, D, z, dt_bias, init, *ctx.cfg, saved, ysave)
@@ -121,9 +127,9 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
         D = D.float()
         D = (D[:, None].expand(h, p) if D.dim() == 1 else D).contiguous()
     args = (
-        x.to(xdt).contiguous(), dt.float().contiguous(), A.float().contiguous(),
-        B.to(xdt).contiguous(), C.to(xdt).contiguous(), D,
-        None if z is None else z.to(xdt).contiguous(),
+        _aligned(x.to(xdt).contiguous()), dt.float().contiguous(), A.float().contiguous(),
+        _aligned(B.to(xdt).contiguous()), _aligned(C.to(xdt).contiguous()), D,
+        None if z is None else _aligned(z.to(xdt).contiguous()),
         None if dt_bias is None else dt_bias.float().contiguous(),
         None if initial_states is None else initial_states.float().contiguous(),
         bool(dt_softplus), lo, hi,
@@ -139,17 +145,20 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
 
 
 def ssd_flops(batch, seqlen, nheads, headdim, ngroups, dstate, backward=False):
-    """Matrix-core FLOPs of the chunked scan (64-step chunks): the products
-    the kernels run, per direction; used to place a timing against the
-    float32 matrix peak."""
+    """Matrix FLOPs of the chunked algorithm (64-step chunks), per direction,
+    counting C B^T once per group and chunk (the heads of a group share it);
+    used to place a timing against the float32 matrix peak. The kernels form
+    C B^T once per head block, so they run somewhat more than this."""
     nch = math.ceil(seqlen / _CHUNK)
     Q, P, N = _CHUNK, headdim, dstate
-    per = batch * nch * nheads
-    # forward: the chunk state (P x N over Q), C B^T (Q x Q over N), the
-    # intra-chunk output (Q x P over Q) and the state's output (Q x P over N)
-    fwd = per * 2 * (P * N * Q + Q * Q * N + Q * P * Q + Q * P * N)
+    per_head = batch * nch * nheads
+    per_group = batch * nch * ngroups
+    cbt = per_group * 2 * Q * Q * N
+    # forward: the chunk state (P x N over Q), the intra-chunk output (Q x P
+    # over Q) and the state's output (Q x P over N)
+    fwd = cbt + per_head * 2 * (P * N * Q + Q * P * Q + Q * P * N)
     if not backward:
         return fwd
-    # backward: C B^T, dY (dt x)^T, G^T dY, dCB B, dCB^T C, the seed E (N x P
-    # over Q), then (dt x) dH, dY H and B~ dH^T
-    return per * 2 * (Q * Q * N + Q * Q * P + Q * P * Q + 2 * Q * N * Q + N * P * Q + 3 * Q * N * P)
+    # backward: the seed E (P x N over Q), dY x^T (Q x Q over P), G^T dY, dCB B
+    # and dCB^T C (over Q), then (dt x) dH, dY H and B~ dH^T (over the state)
+    return cbt + per_head * 2 * (P * N * Q + Q * Q * P + Q * P * Q + 2 * Q * N * Q + 3 * Q * N * P)

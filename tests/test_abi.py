@@ -429,6 +429,9 @@ def test_ssd_rejects_bad_arguments_before_touching_a_device():
     assert rc == _C.MCPU_ERR_INVALID and "saved" in msg
     rc, msg = _rc(L.mcpu_ssd_bwd, ctypes.byref(_ssd_args()), None, 0, None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "dout" in msg
+    # tiles move four elements at a time: storage must start on 16 bytes
+    rc, msg = fwd(_ssd_args(B=24))
+    assert rc == _C.MCPU_ERR_INVALID and "aligned" in msg
 
 
 def test_ssd_sizes_follow_the_layout():
@@ -445,7 +448,7 @@ def test_ssd_sizes_follow_the_layout():
         nch = -(-l // 64)
         want = 3 * al(4 * b * h * nch * 64) + al(4 * b * nch * h * p * n)
         assert L.mcpu_ssd_saved_size(ctypes.byref(a)) == want == _saved_bytes(b, l, h, p, n)
-        assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(a)) >= 4 * b * l * h * (p + 2 * n)
+        assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(a)) >= 4 * b * nch * h * p * n
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(seqlen=0))) == 0
     assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(batch=0))) == 0
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(headdim=24))) == 0
