@@ -136,20 +136,22 @@ __device__ __forceinline__ int tile_row(int v, float inv_nv) {
   return static_cast<int>((static_cast<float>(v) + 0.5f) * inv_nv);
 }
 
-// Largest number of float4 per thread in a staged tile (64 x 128).
-constexpr int kMaxVec = Q * kSsdMaxN / 4 / kThreads;
+// float4 per thread of the staged tiles: (64 x dstate) and (headdim x
+// dstate) tiles, (64 x headdim) tiles and (headdim x 64-state half) tiles.
+constexpr int kVecN = Q * kSsdMaxN / 4 / kThreads;
+constexpr int kVecX = Q * kSsdMaxP / 4 / kThreads;
 
-// LDS tile s (rows of ld floats) = rows r < nrows, columns c < ncols
-// (multiple of 4) of src[r rs + c], times scale[r] when given, rows from
-// nvalid on zero. Every load of the tile issues before the first LDS store.
-template <typename Tx>
-__device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t rs, int nrows, int nvalid, int ncols,
-                                      const float* scale = nullptr) {
+// Registers x = rows r < nrows, columns c < ncols (multiple of 4) of
+// src[r rs + c], four elements per float4, rows from nvalid on zero; thread
+// tid holds float4 number tid + k kThreads of the row-major tile. The loads
+// are issued here and waited for where the registers are used.
+template <typename Tx, int V>
+__device__ __forceinline__ void tile_load(float4 (&x)[V], const Tx* src, int64_t rs, int nrows, int nvalid,
+                                          int ncols) {
   const int nv = ncols >> 2, total = nrows * nv;
   const float inv = 1.0f / static_cast<float>(nv);
-  float4 x[kMaxVec];
 #pragma unroll
-  for (int k = 0; k < kMaxVec; ++k) {
+  for (int k = 0; k < V; ++k) {
     const int v = threadIdx.x + k * kThreads;
     x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (v < total) {
@@ -157,8 +159,17 @@ __device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t r
       if (r < nvalid) x[k] = ld4<Tx>(src + r * rs + ((v - r * nv) << 2));
     }
   }
+}
+
+// LDS tile s (rows of ld floats) from registers filled by tile_load with the
+// same nrows / ncols, times scale[r] when given.
+template <int V>
+__device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V], int nrows, int ncols,
+                                           const float* scale = nullptr) {
+  const int nv = ncols >> 2, total = nrows * nv;
+  const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
-  for (int k = 0; k < kMaxVec; ++k) {
+  for (int k = 0; k < V; ++k) {
     const int v = threadIdx.x + k * kThreads;
     if (v < total) {
       const int r = tile_row(v, inv);
@@ -168,59 +179,61 @@ __device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t r
   }
 }
 
-// Largest number of float4 per thread in a (64 x headdim) tile.
-constexpr int kMaxVecX = Q * kSsdMaxP / 4 / kThreads;
-
-// LDS tile of dY = dout silu(z) (dout without z) over a chunk of one head,
-// times scale[r] when given; dz = dout y silu'(z) written on the way when
-// write_dz (y from ysave). `off` is the tile's first element in x layout.
-template <typename Tx, bool HAS_Z>
-__device__ __forceinline__ void stage_dy(float* s, int ld, const SsdParams& p, int64_t off, int64_t rs, int nvalid,
-                                         int ncols, bool write_dz, const float* scale = nullptr) {
-  const int nv = ncols >> 2, total = Q * nv;
-  const float inv = 1.0f / static_cast<float>(nv);
-  const Tx* dout = static_cast<const Tx*>(p.dout) + off;
-  float4 go[kMaxVecX], zz[kMaxVecX], yy[kMaxVecX];
-#pragma unroll
-  for (int k = 0; k < kMaxVecX; ++k) {
-    const int v = threadIdx.x + k * kThreads;
-    go[k] = zz[k] = yy[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (v < total) {
-      const int r = tile_row(v, inv);
-      if (r < nvalid) {
-        const int64_t i = r * rs + ((v - r * nv) << 2);
-        go[k] = ld4<Tx>(dout + i);
-        if (HAS_Z) {
-          zz[k] = ld4<Tx>(static_cast<const Tx*>(p.z) + off + i);
-          if (write_dz) yy[k] = ld4<Tx>(static_cast<const Tx*>(p.ysave) + off + i);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < kMaxVecX; ++k) {
-    const int v = threadIdx.x + k * kThreads;
-    if (v >= total) continue;
-    const int r = tile_row(v, inv);
-    const int c = (v - r * nv) << 2;
-    float4 dy = go[k];
-    if (HAS_Z) {
-      const float gx[4] = {go[k].x, go[k].y, go[k].z, go[k].w}, zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
-      const float yv[4] = {yy[k].x, yy[k].y, yy[k].z, yy[k].w};
-      float d[4], dzv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float sg = sigmoid(zx[u]);
-        d[u] = gx[u] * zx[u] * sg;
-        dzv[u] = gx[u] * yv[u] * sg * (1.f + zx[u] * (1.f - sg));
-      }
-      if (write_dz && r < nvalid)
-        st4<Tx>(static_cast<Tx*>(p.dz) + off + r * rs + c, make_float4(dzv[0], dzv[1], dzv[2], dzv[3]));
-      dy = make_float4(d[0], d[1], d[2], d[3]);
-    }
-    *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(dy, scale[r]) : dy;
-  }
+// tile_load then tile_store.
+template <typename Tx, int V>
+__device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t rs, int nrows, int nvalid, int ncols,
+                                      const float* scale = nullptr) {
+  float4 x[V];
+  tile_load<Tx, V>(x, src, rs, nrows, nvalid, ncols);
+  tile_store<V>(s, ld, x, nrows, ncols, scale);
 }
+
+// The dout, z and ysave tiles of one head's chunk (x layout from `off`, z and
+// ysave only when HAS_Z and, for ysave, want_y).
+template <typename Tx, bool HAS_Z>
+struct DyTiles {
+  float4 go[kVecX], zz[kVecX], yy[kVecX];
+
+  __device__ __forceinline__ void load(const SsdParams& p, int64_t off, int64_t rs, int nvalid, int ncols,
+                                       bool want_y) {
+    tile_load<Tx, kVecX>(go, static_cast<const Tx*>(p.dout) + off, rs, Q, nvalid, ncols);
+    if (HAS_Z) {
+      tile_load<Tx, kVecX>(zz, static_cast<const Tx*>(p.z) + off, rs, Q, nvalid, ncols);
+      if (want_y) tile_load<Tx, kVecX>(yy, static_cast<const Tx*>(p.ysave) + off, rs, Q, nvalid, ncols);
+    }
+  }
+
+  // LDS tile of dY = dout silu(z) (dout without z), times scale[r] when
+  // given; dz = dout y silu'(z) written to rows below nvalid when write_dz.
+  __device__ __forceinline__ void store(float* s, int ld, const SsdParams& p, int64_t off, int64_t rs, int nvalid,
+                                        int ncols, bool write_dz, const float* scale = nullptr) const {
+    const int nv = ncols >> 2, total = Q * nv;
+    const float inv = 1.0f / static_cast<float>(nv);
+#pragma unroll
+    for (int k = 0; k < kVecX; ++k) {
+      const int v = threadIdx.x + k * kThreads;
+      if (v >= total) continue;
+      const int r = tile_row(v, inv);
+      const int c = (v - r * nv) << 2;
+      float4 dy = go[k];
+      if (HAS_Z) {
+        const float gx[4] = {go[k].x, go[k].y, go[k].z, go[k].w}, zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
+        const float yv[4] = {yy[k].x, yy[k].y, yy[k].z, yy[k].w};
+        float d[4], dzv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float sg = sigmoid(zx[u]);
+          d[u] = gx[u] * zx[u] * sg;
+          dzv[u] = gx[u] * yv[u] * sg * (1.f + zx[u] * (1.f - sg));
+        }
+        if (write_dz && r < nvalid)
+          st4<Tx>(static_cast<Tx*>(p.dz) + off + r * rs + c, make_float4(dzv[0], dzv[1], dzv[2], dzv[3]));
+        dy = make_float4(d[0], d[1], d[2], d[3]);
+      }
+      *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(dy, scale[r]) : dy;
+    }
+  }
+};
 
 // Inclusive prefix sum over the 64 lanes of a wave as a float pair hi + lo:
 // each addition keeps its rounding error (Knuth's TwoSum) in lo, so a
@@ -320,7 +333,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdPara
   const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
   const int nvalid = chunk_steps(p, t0);
-  stage<Tx>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
+  stage<Tx, kVecN>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
             static_cast<int>(N));
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
@@ -336,7 +349,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdPara
       s_sc[lane] = st * fast_exp((csL - cs) + (cslL - csl));
     }
     __syncthreads();
-    stage<Tx>(&s_x[0][0], XP, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
+    stage<Tx, kVecX>(&s_x[0][0], XP, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
               static_cast<int>(P), s_sc);
     __syncthreads();
     if (16 * wave < P) {
@@ -403,27 +416,45 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
   const int np = static_cast<int>(P / 16);
   {
     const int64_t off = ((b * L + t0) * G + g) * N;
-    stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
-    stage<Tx>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, kVecN>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
   __syncthreads();
   v4f cb[Q / 16];
   zero(cb);
   mma(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+  // The next head's x tile, entering state and decays load into registers
+  // while this head's products run.
+  float4 rx[kVecX], rh[kVecN], zc[kVecX];
+  float rcs = 0.f, rcsl = 0.f, rdt = 0.f;
+  auto fetch = [&](int64_t h) {
+    const int64_t row = chunk_row(p, b, h, c);
+    if (tid < Q) {
+      rcs = p.cs[row + tid];
+      rcsl = p.cs_lo[row + tid];
+      rdt = p.step[row + tid];
+    }
+    tile_load<Tx, kVecX>(rx, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
+                         static_cast<int>(P));
+    tile_load<float, kVecN>(rh, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
+                            static_cast<int>(N));
+  };
+  fetch(h0);
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
-    const int64_t row = chunk_row(p, b, h, c);
     const int64_t xoff = ((b * L + t0) * H + h) * P;
     __syncthreads();  // every wave is done with s_BH, s_G, s_X and s_cs
     if (tid < Q) {
-      s_cs[tid] = p.cs[row + tid];
-      s_csl[tid] = p.cs_lo[row + tid];
-      s_dt[tid] = p.step[row + tid];
+      s_cs[tid] = rcs;
+      s_csl[tid] = rcsl;
+      s_dt[tid] = rdt;
     }
-    stage<Tx>(&s_X[0][0], XP, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
-    stage<float>(&s_BH[0][0], NP, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
-                 static_cast<int>(N));
+    tile_store<kVecX>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    tile_store<kVecN>(&s_BH[0][0], NP, rh, static_cast<int>(P), static_cast<int>(N));
     __syncthreads();
+    if (HAS_Z)
+      tile_load<Tx, kVecX>(zc, static_cast<const Tx*>(p.z) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+    if (i + 1 < p.hb) fetch(h + 1);
 #pragma unroll
     for (int j = 0; j < Q / 16; ++j)
 #pragma unroll
@@ -451,18 +482,8 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
     {
       const int nv = np * 4;
       const float inv = 1.0f / static_cast<float>(nv);
-      float4 zz[kMaxVecX];
 #pragma unroll
-      for (int k = 0; k < kMaxVecX; ++k) {
-        const int v = tid + k * kThreads;
-        zz[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (HAS_Z && v < Q * nv) {
-          const int t = tile_row(v, inv);
-          if (t < nvalid) zz[k] = ld4<Tx>(static_cast<const Tx*>(p.z) + xoff + t * H * P + ((v - t * nv) << 2));
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kMaxVecX; ++k) {
+      for (int k = 0; k < kVecX; ++k) {
         const int v = tid + k * kThreads;
         if (v >= Q * nv) continue;
         const int t = tile_row(v, inv);
@@ -479,7 +500,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
         }
         if (HAS_Z) {
           if (p.ysave) st4<Tx>(static_cast<Tx*>(p.ysave) + at, make_float4(y[0], y[1], y[2], y[3]));
-          const float zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
+          const float zx[4] = {zc[k].x, zc[k].y, zc[k].z, zc[k].w};
 #pragma unroll
           for (int u = 0; u < 4; ++u) y[u] *= zx[u] * sigmoid(zx[u]);
         }
@@ -505,7 +526,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams 
   const int64_t g = h0 / (H / G);
   const int64_t t0 = c * Q;
   const int nvalid = chunk_steps(p, t0);
-  stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
+  stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
             static_cast<int>(N));
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
@@ -513,8 +534,12 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams 
     __syncthreads();  // every wave is done with s_dY and s_ecs
     if (tid < Q) s_ecs[tid] = fast_exp(p.cs[row + tid] + p.cs_lo[row + tid]);
     __syncthreads();
-    stage_dy<Tx, HAS_Z>(&s_dY[0][0], XP, p, ((b * L + t0) * H + h) * P, H * P, nvalid, static_cast<int>(P), false,
-                        s_ecs);
+    {
+      const int64_t off = ((b * L + t0) * H + h) * P;
+      DyTiles<Tx, HAS_Z> dyt;
+      dyt.load(p, off, H * P, nvalid, static_cast<int>(P), false);
+      dyt.store(&s_dY[0][0], XP, p, off, H * P, nvalid, static_cast<int>(P), false, s_ecs);
+    }
     __syncthreads();
     if (16 * wave < P) {
       v4f ev[kSsdMaxN / 16];
@@ -597,8 +622,8 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
   const int np = static_cast<int>(P / 16), nn = static_cast<int>(N / 16);
   {
     const int64_t off = ((b * L + t0) * G + g) * N;
-    stage<Tx>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
-    stage<Tx>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, kVecN>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
   __syncthreads();
   v4f cb[Q / 16];
@@ -607,6 +632,25 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
   v4f dBa[kSsdMaxN / 16], dCa[kSsdMaxN / 16];
   zero(dBa);
   zero(dCa);
+  // The next head's x, dout, z and ysave tiles and decays load into
+  // registers while this head's products run.
+  float4 rx[kVecX];
+  DyTiles<Tx, HAS_Z> rdy;
+  float rcs = 0.f, rcsl = 0.f, rdt = 0.f, rcsL = 0.f, rcslL = 0.f;
+  auto fetch = [&](int64_t h) {
+    const int64_t row = chunk_row(p, b, h, c);
+    const int64_t xoff = ((b * L + t0) * H + h) * P;
+    if (tid < Q) {
+      rcs = p.cs[row + tid];
+      rcsl = p.cs_lo[row + tid];
+      rdt = p.step[row + tid];
+      rcsL = p.cs[row + Q - 1];
+      rcslL = p.cs_lo[row + Q - 1];
+    }
+    tile_load<Tx, kVecX>(rx, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+    rdy.load(p, xoff, H * P, nvalid, static_cast<int>(P), true);
+  };
+  fetch(h0);
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
     const int64_t row = chunk_row(p, b, h, c);
@@ -614,17 +658,16 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
     const int64_t sb = state_block(p, b, c, h);
     __syncthreads();  // every wave is done with the previous head's tiles
     if (tid < Q) {
-      const float cs = p.cs[row + tid], csl = p.cs_lo[row + tid];
-      const float csL = p.cs[row + Q - 1], cslL = p.cs_lo[row + Q - 1];
-      s_cs[tid] = cs;
-      s_csl[tid] = csl;
-      s_dt[tid] = p.step[row + tid];
-      s_w[tid] = fast_exp((csL - cs) + (cslL - csl));
-      s_ecs[tid] = fast_exp(cs + csl);
+      s_cs[tid] = rcs;
+      s_csl[tid] = rcsl;
+      s_dt[tid] = rdt;
+      s_w[tid] = fast_exp((rcsL - rcs) + (rcslL - rcsl));
+      s_ecs[tid] = fast_exp(rcs + rcsl);
     }
-    stage<Tx>(&s_X[0][0], XP, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
-    stage_dy<Tx, HAS_Z>(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
+    tile_store<kVecX>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    rdy.store(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
     __syncthreads();
+    if (i + 1 < p.hb) fetch(h + 1);
     // dGraw = dY x^T (rows t of this wave, all columns s); then with M and dt:
     // G = CB o M, dCB = dt_s dGraw o M, R = dCB o CB (= dG o G); the row sums
     // of R in the wave, its column sums through LDS, both in a fixed order.
@@ -682,8 +725,8 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       const int nw = static_cast<int>(N - n0 < 64 ? N - n0 : 64);
       const int nt = nw / 16;
       __syncthreads();  // every wave is done reading s_U / s_V
-      stage<float>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
-      stage<float>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      stage<float, kVecX>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      stage<float, kVecX>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
       __syncthreads();
       v4f tv[4], yh[4];
       zero(tv);
@@ -796,7 +839,7 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       const int nv = np * 4;
       const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
-      for (int k = 0; k < kMaxVecX; ++k) {
+      for (int k = 0; k < kVecX; ++k) {
         const int v = tid + k * kThreads;
         if (v >= Q * nv) continue;
         const int s = tile_row(v, inv);
