@@ -44,7 +44,8 @@ int mcpu_check_device(void);
 const char* mcpu_version(void);
 
 /* sizeof() of an argument block ("scan", "conv", "conv_update",
- * "state_update"), 0 for an unknown name; lets bindings check their layout. */
+ * "state_update", "ssd", "mixer_step"), 0 for an unknown name; lets bindings
+ * check their layout. */
 size_t mcpu_args_size(const char* name);
 
 /* ------------------------------------------------------------------------ */
@@ -355,6 +356,60 @@ size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a);
 /* Backward, given the forward's saved buffer (and ysave when z is given). */
 int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes, void* workspace,
                  size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused single-token Mamba block step (decode).                             */
+/* ------------------------------------------------------------------------ */
+
+/* One decode step of a Mamba-1 block for a batch of single tokens: what the
+ * reference's patched transformers MambaBlock computes for one token with a
+ * cache (src/mamba_cpu/hf.py:26-112 routes its pieces: causal_conv1d_update,
+ * selective_state_update), in four launches instead of a dozen:
+ *   u    = RMSNorm(hidden) when norm_weight != NULL (else hidden), in dtype
+ *   x, z = in_proj(u)                    (2 d_inner)
+ *   x    = silu(conv1d_update(conv_state, x))   conv_state shifted in place
+ *   dt, B, C = x_proj(x)                 (dt_rank, dstate, dstate)
+ *   dt   = dt_proj.weight dt             (no bias here)
+ *   y    = selective_state_update(ssm_state, x, dt, A, B, C, D, z, dt_bias, softplus)
+ *   out  = out_proj(y) [+ hidden, the residual, when add_residual]
+ * Rounding follows transformers: each stage's result is stored in dtype
+ * before the next reads it; arithmetic is float32. No counterpart in the
+ * reference (it has no fused decode path). All tensors contiguous, 16-byte
+ * aligned; batch <= 8; d_model and d_inner multiples of 4; conv width and
+ * state length at most 8; with batch rounded up to a power of two, (batch + 1)
+ * x d_model and batch x d_inner at most 32768. */
+typedef struct mcpu_mixer_step_args {
+  const void* hidden;       /* (batch, d_model), hidden_dtype */
+  const void* norm_weight;  /* (d_model), dtype, optional */
+  const void* in_w;         /* (2 d_inner, d_model), dtype */
+  const void* in_b;         /* (2 d_inner), dtype, optional */
+  const void* conv_w;       /* (d_inner, width), dtype */
+  const void* conv_b;       /* (d_inner), dtype, optional */
+  void* conv_state;         /* (batch, d_inner, state_len), dtype, state_len >= width - 1 */
+  const void* x_w;          /* (dt_rank + 2 dstate, d_inner), dtype */
+  const void* dt_w;         /* (d_inner, dt_rank), dtype */
+  const float* dt_b;        /* (d_inner), optional */
+  const float* A;           /* (d_inner, dstate): -exp(A_log) */
+  const float* D;           /* (d_inner), optional */
+  void* ssm_state;          /* (batch, d_inner, dstate), state_dtype */
+  const void* out_w;        /* (d_model, d_inner), dtype */
+  const void* out_b;        /* (d_model), dtype, optional */
+  void* out;                /* (batch, d_model), out_dtype */
+  int64_t batch, d_model, d_inner, dt_rank, dstate, width, state_len;
+  float norm_eps;
+  int32_t add_residual;     /* out = residual + out_proj(y) */
+  int32_t residual_in_fp32; /* the residual is hidden in float32 */
+  int32_t dtype;            /* weights, activations, conv state */
+  int32_t hidden_dtype;     /* dtype or MCPU_F32 */
+  int32_t state_dtype;      /* ssm_state */
+  int32_t out_dtype;        /* dtype, or MCPU_F32 with a float32 residual */
+  int32_t _pad;
+} mcpu_mixer_step_args;
+
+/* Workspace bytes of mcpu_mixer_step (the step's intermediate vectors). */
+size_t mcpu_mixer_step_workspace_size(const mcpu_mixer_step_args* a);
+/* One step. Updates conv_state and ssm_state in place and writes out. */
+int mcpu_mixer_step(const mcpu_mixer_step_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1203,6 +1203,119 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tenso
   return {dx, ddt, dA, dB, dC, dD, dz, dbias, dinit};
 }
 
+// ---- fused single-token block step ----------------------------------------------
+
+// One decode step of a Mamba-1 block (mcpu_mixer_step): hidden (batch,
+// d_model) -> out (batch, d_model), conv_state (batch, d_inner, state_len) and
+// ssm_state (batch, d_inner, dstate) updated in place. Weights as nn.Linear /
+// nn.Conv1d hold them (conv weight (d_inner, width)); dt_bias, A (= -exp(A_log))
+// and D float32. out is float32 when the residual is (add_residual with a
+// float32 residual), else the weights' dtype.
+Tensor mixer_step(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, bool add_residual,
+                  bool residual_in_fp32, const Tensor& in_w, const optional<Tensor>& in_b, const Tensor& conv_w,
+                  const optional<Tensor>& conv_b, Tensor& conv_state, const Tensor& x_w, const Tensor& dt_w,
+                  const optional<Tensor>& dt_b, const Tensor& A, const optional<Tensor>& D, Tensor& ssm_state,
+                  const Tensor& out_w, const optional<Tensor>& out_b) {
+  const char* name = "mamba_cpu::mixer_step";
+  for (const optional<Tensor>& t : {opt(hidden), norm_weight, opt(in_w), in_b, opt(conv_w), conv_b,
+                                    opt(conv_state), opt(x_w), opt(dt_w), dt_b, opt(A), D, opt(ssm_state),
+                                    opt(out_w), out_b})
+    check_gpu(name, t);
+  const auto T = in_w.scalar_type();
+  TORCH_CHECK_VALUE(x_dtype(T), name, " expects float32, bfloat16 or float16 weights");
+  for (const optional<Tensor>& t : {norm_weight, in_b, opt(conv_w), conv_b, opt(conv_state), opt(x_w),
+                                    opt(dt_w), opt(out_w), out_b})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == T && t->is_contiguous()), name,
+                      " expects contiguous weights, biases and conv state of one dtype");
+  for (const optional<Tensor>& t : {dt_b, opt(A), D})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == at::kFloat && t->is_contiguous()), name,
+                      " expects contiguous float32 dt_bias, A and D");
+  TORCH_CHECK_VALUE(hidden.dim() == 2 && hidden.is_contiguous() &&
+                        (hidden.scalar_type() == T || hidden.scalar_type() == at::kFloat),
+                    name, " expects a contiguous hidden (batch, d_model) in the weights' dtype or float32");
+  const int64_t b = hidden.size(0), dm = hidden.size(1);
+  TORCH_CHECK_VALUE(in_w.dim() == 2 && in_w.size(1) == dm && in_w.size(0) % 2 == 0, name,
+                    " expects in_proj weight (2 d_inner, d_model)");
+  const int64_t di = in_w.size(0) / 2;
+  TORCH_CHECK_VALUE(conv_w.dim() == 2 && conv_w.size(0) == di, name, " expects conv weight (d_inner, width)");
+  TORCH_CHECK_VALUE(conv_state.dim() == 3 && conv_state.size(0) == b && conv_state.size(1) == di, name,
+                    " expects conv_state (batch, d_inner, state_len)");
+  TORCH_CHECK_VALUE(A.dim() == 2 && A.size(0) == di, name, " expects A (d_inner, dstate)");
+  const int64_t N = A.size(1);
+  TORCH_CHECK_VALUE(dt_w.dim() == 2 && dt_w.size(0) == di, name, " expects dt_proj weight (d_inner, dt_rank)");
+  const int64_t R = dt_w.size(1);
+  TORCH_CHECK_VALUE(x_w.dim() == 2 && x_w.size(0) == R + 2 * N && x_w.size(1) == di, name,
+                    " expects x_proj weight (dt_rank + 2 dstate, d_inner)");
+  TORCH_CHECK_VALUE(out_w.dim() == 2 && out_w.size(0) == dm && out_w.size(1) == di, name,
+                    " expects out_proj weight (d_model, d_inner)");
+  TORCH_CHECK_VALUE(ssm_state.dim() == 3 && ssm_state.size(0) == b && ssm_state.size(1) == di &&
+                        ssm_state.size(2) == N && ssm_state.is_contiguous() && x_dtype(ssm_state.scalar_type()),
+                    name, " expects a contiguous ssm_state (batch, d_inner, dstate)");
+  TORCH_CHECK_VALUE((!has(norm_weight) || norm_weight->numel() == dm) && (!has(in_b) || in_b->numel() == 2 * di) &&
+                        (!has(conv_b) || conv_b->numel() == di) && (!has(dt_b) || dt_b->numel() == di) &&
+                        (!has(D) || D->numel() == di) && (!has(out_b) || out_b->numel() == dm),
+                    name, " expects bias and norm vectors of their layer's width");
+  const bool res32 = add_residual && (residual_in_fp32 || hidden.scalar_type() == at::kFloat);
+  c10::DeviceGuard guard(hidden.device());
+  Tensor out = at::empty({b, dm}, hidden.options().dtype(res32 ? at::kFloat : T));
+  mcpu_mixer_step_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.hidden = hidden.data_ptr();
+  a.norm_weight = ptr(norm_weight);
+  a.in_w = in_w.data_ptr();
+  a.in_b = ptr(in_b);
+  a.conv_w = conv_w.data_ptr();
+  a.conv_b = ptr(conv_b);
+  a.conv_state = conv_state.data_ptr();
+  a.x_w = x_w.data_ptr();
+  a.dt_w = dt_w.data_ptr();
+  a.dt_b = fptr(dt_b);
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.D = fptr(D);
+  a.ssm_state = ssm_state.data_ptr();
+  a.out_w = out_w.data_ptr();
+  a.out_b = ptr(out_b);
+  a.out = out.data_ptr();
+  a.batch = b;
+  a.d_model = dm;
+  a.d_inner = di;
+  a.dt_rank = R;
+  a.dstate = N;
+  a.width = conv_w.size(1);
+  a.state_len = conv_state.size(2);
+  a.norm_eps = static_cast<float>(eps);
+  a.add_residual = add_residual ? 1 : 0;
+  a.residual_in_fp32 = residual_in_fp32 ? 1 : 0;
+  a.dtype = dtype_tag(T);
+  a.hidden_dtype = dtype_tag(hidden.scalar_type());
+  a.state_dtype = dtype_tag(ssm_state.scalar_type());
+  a.out_dtype = dtype_tag(out.scalar_type());
+  const size_t nws = mcpu_mixer_step_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(nws)}, hidden.options().dtype(at::kByte));
+  check_rc(mcpu_mixer_step(&a, ws.data_ptr(), nws, stream_of(hidden)), name);
+  return out;
+}
+
+Tensor mixer_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, bool add_residual,
+                          bool residual_in_fp32, const Tensor& in_w, const optional<Tensor>& in_b,
+                          const Tensor& conv_w, const optional<Tensor>& conv_b, Tensor& conv_state,
+                          const Tensor& x_w, const Tensor& dt_w, const optional<Tensor>& dt_b, const Tensor& A,
+                          const optional<Tensor>& D, Tensor& ssm_state, const Tensor& out_w,
+                          const optional<Tensor>& out_b) {
+  Tensor out;
+  {
+    at::AutoDispatchBelowADInplaceOrView below;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::mixer_step", "")
+                         .typed<decltype(mixer_step)>();
+    out = op.call(hidden, norm_weight, eps, add_residual, residual_in_fp32, in_w, in_b, conv_w, conv_b, conv_state,
+                  x_w, dt_w, dt_b, A, D, ssm_state, out_w, out_b);
+  }
+  conv_state.unsafeGetTensorImpl()->bump_version();
+  ssm_state.unsafeGetTensorImpl()->bump_version();
+  return out;
+}
+
 }  // namespace
 }  // namespace mcpu_torch
 
@@ -1248,6 +1361,10 @@ TORCH_LIBRARY(mamba_cpu, m) {
   m.def("selective_state_update(Tensor(a!) state, Tensor x, Tensor dt, Tensor A, Tensor B, "
         "Tensor C, Tensor? D, Tensor? z, Tensor? dt_bias, bool dt_softplus, "
         "Tensor? state_batch_indices=None) -> Tensor");
+  m.def("mixer_step(Tensor hidden, Tensor? norm_weight, float eps, bool add_residual, bool residual_in_fp32, "
+        "Tensor in_w, Tensor? in_b, Tensor conv_w, Tensor? conv_b, Tensor(a!) conv_state, Tensor x_w, "
+        "Tensor dt_w, Tensor? dt_b, Tensor A, Tensor? D, Tensor(b!) ssm_state, Tensor out_w, "
+        "Tensor? out_b) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
@@ -1266,6 +1383,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("selective_state_update", &selective_state_update);
   m.impl("ssd_fwd", &ssd_fwd);
   m.impl("ssd_bwd", &ssd_bwd);
+  m.impl("mixer_step", &mixer_step);
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
@@ -1273,10 +1391,13 @@ TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
   m.impl("selective_scan_fwd", &selective_scan_fwd_autograd);
   m.impl("selective_scan_fwd_ckpt", &selective_scan_fwd_ckpt_autograd);
   m.impl("causal_conv1d_fwd", &causal_conv1d_fwd_autograd);
+  // One decode step: no gradient flows through it.
+  m.impl("mixer_step", torch::CppFunction::makeFallthrough());
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, ADInplaceOrView, m) {
   using namespace mcpu_torch;
   m.impl("causal_conv1d_update", &causal_conv1d_update_inplace);
   m.impl("selective_state_update", &selective_state_update_inplace);
+  m.impl("mixer_step", &mixer_step_inplace);
 }

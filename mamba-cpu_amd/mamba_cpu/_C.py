@@ -116,9 +116,21 @@ class SsdArgs(ctypes.Structure):
     ]
 
 
+class MixerStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _P), ("norm_weight", _P), ("in_w", _P), ("in_b", _P), ("conv_w", _P), ("conv_b", _P),
+        ("conv_state", _P), ("x_w", _P), ("dt_w", _P), ("dt_b", _P), ("A", _P), ("D", _P),
+        ("ssm_state", _P), ("out_w", _P), ("out_b", _P), ("out", _P),
+        ("batch", _I64), ("d_model", _I64), ("d_inner", _I64), ("dt_rank", _I64), ("dstate", _I64),
+        ("width", _I64), ("state_len", _I64),
+        ("norm_eps", ctypes.c_float), ("add_residual", _I32), ("residual_in_fp32", _I32), ("dtype", _I32),
+        ("hidden_dtype", _I32), ("state_dtype", _I32), ("out_dtype", _I32), ("_pad", _I32),
+    ]
+
+
 _ARGP = {n: ctypes.POINTER(c) for n, c in
          (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-          ("state_update", StateUpdateArgs), ("ssd", SsdArgs))}
+          ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs))}
 
 lib.mcpu_last_error.restype = ctypes.c_char_p
 lib.mcpu_version.restype = ctypes.c_char_p
@@ -155,9 +167,13 @@ lib.mcpu_ssd_bwd_workspace_size.argtypes = [_ARGP["ssd"]]
 lib.mcpu_ssd_bwd_workspace_size.restype = ctypes.c_size_t
 lib.mcpu_ssd_bwd.argtypes = [_ARGP["ssd"], _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]
 lib.mcpu_ssd_bwd.restype = ctypes.c_int
+lib.mcpu_mixer_step_workspace_size.argtypes = [_ARGP["mixer_step"]]
+lib.mcpu_mixer_step_workspace_size.restype = ctypes.c_size_t
+lib.mcpu_mixer_step.argtypes = [_ARGP["mixer_step"], _P, ctypes.c_size_t, _P]
+lib.mcpu_mixer_step.restype = ctypes.c_int
 
 for _name, _cls in (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-                    ("state_update", StateUpdateArgs), ("ssd", SsdArgs)):
+                    ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs)):
     _want = lib.mcpu_args_size(_name.encode())
     if _want != ctypes.sizeof(_cls):
         raise ImportError(f"mamba_cpu: {_name} argument block is {ctypes.sizeof(_cls)} bytes here "

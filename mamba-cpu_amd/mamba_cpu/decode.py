@@ -10,19 +10,103 @@ the host: every layer issues a dozen small kernels through Python, each one
 dispatched on its own. A Mamba decode step is shape-static once the prompt has
 been consumed: the cache holds one conv window and one state per layer, and
 both are updated in place (transformers allocates them once, at fixed
-addresses, and the conv update and state update ops write them in place). So
-the whole step, from the token embedding to the last-position logits, is
-captured once into a HIP graph (torch.cuda.CUDAGraph) and replayed per token;
-only the argmax and the token copies run eagerly between replays.
+addresses). So the whole step, from the token embedding to the last-position
+logits, is captured once into a HIP graph (torch.cuda.CUDAGraph) and replayed
+per token; only the argmax and the token copies run eagerly between replays.
 
-The result is the token sequence `model.generate` returns for greedy decoding
-with no logits processors: the replayed kernels are the eager step's kernels
-on the same inputs.
+For Mamba (not FalconMamba, whose mixer normalises dt, B and C) the captured
+step runs each block as one fused operator, mamba_cpu::mixer_step: RMSNorm,
+in_proj, conv update, x_proj, dt_proj, state update, out_proj and the
+residual in four kernels, with the small-batch products as matrix-vector
+kernels that read each weight once. It computes what the block computes;
+the products sum in another order than the GEMM library's, so logits agree
+to float32 rounding and greedy tokens match `model.generate`'s.
 """
 
 import torch
 
+from mamba_cpu import _C  # noqa: F401  (loads the operator library)
+
 _GRAPH_MODELS = ("mamba", "falcon_mamba")
+_MAX_FUSED_BATCH = 8
+
+
+@torch.library.register_fake("mamba_cpu::mixer_step")
+def _(hidden, norm_weight, eps, add_residual, residual_in_fp32, in_w, in_b, conv_w, conv_b, conv_state, x_w,
+      dt_w, dt_b, A, D, ssm_state, out_w, out_b):
+    f32 = add_residual and (residual_in_fp32 or hidden.dtype == torch.float32)
+    return hidden.new_empty(hidden.shape, dtype=torch.float32 if f32 else in_w.dtype)
+
+
+def _block_constants(mixer):
+    """float32 dt_proj bias, A = -exp(A_log) and D of a Mamba mixer, computed
+    once and kept on the module until one of the parameters changes."""
+    params = (mixer.A_log, mixer.D, mixer.dt_proj.bias)
+    key = tuple((t.data_ptr(), t._version) for t in params if t is not None)
+    cached = getattr(mixer, "_mamba_cpu_step_constants", None)
+    if cached is None or cached[0] != key:
+        with torch.no_grad():
+            A = -torch.exp(mixer.A_log.float())
+            D = mixer.D.float().contiguous()
+            dtb = None if mixer.dt_proj.bias is None else mixer.dt_proj.bias.float().contiguous()
+        cached = (key, A.contiguous(), D, dtb)
+        mixer._mamba_cpu_step_constants = cached
+    return cached[1:]
+
+
+def fused_step_supported(model, cache, batch_size):
+    """Whether `model`'s decode step can run as fused block steps: a
+    transformers Mamba model on a ROCm GPU, one weight dtype, silu, at most 8
+    batch rows, widths the fused kernels take, and a cache whose conv windows
+    are not recording past inputs."""
+    if model.config.model_type != "mamba" or batch_size > _MAX_FUSED_BATCH:
+        return False
+    layers = getattr(getattr(model, "backbone", None), "layers", None)
+    if not layers:
+        return False
+    for blk in layers:
+        mx = blk.mixer
+        w = mx.in_proj.weight
+        if w.device.type != "cuda" or mx.activation != "silu":
+            return False
+        tensors = [blk.norm.weight, w, mx.in_proj.bias, mx.conv1d.weight, mx.conv1d.bias, mx.x_proj.weight,
+                   mx.dt_proj.weight, mx.out_proj.weight, mx.out_proj.bias]
+        if any(t is not None and (t.dtype != w.dtype or not t.is_contiguous()) for t in tensors):
+            return False
+        if w.shape[1] % 4 or mx.intermediate_size % 4 or mx.ssm_state_size > 128:
+            return False
+        layer = cache.layers[blk.layer_idx]
+        conv, ssm = layer.conv_states[0], layer.recurrent_states[0]
+        if layer.record_past or conv is None or ssm is None or not conv.is_contiguous() \
+                or not ssm.is_contiguous() or conv.dtype != w.dtype or conv.shape[2] > 8:
+            return False
+    return True
+
+
+def fused_block_step(block, hidden, cache):
+    """One decode step of a transformers MambaBlock: hidden (batch, d_model)
+    -> the block's output (batch, d_model), the layer's conv window and SSM
+    state in `cache` advanced in place."""
+    mx = block.mixer
+    layer = cache.layers[block.layer_idx]
+    A, D, dtb = _block_constants(mx)
+    conv_w = mx.conv1d.weight.view(mx.intermediate_size, -1)
+    return torch.ops.mamba_cpu.mixer_step(
+        hidden, block.norm.weight, float(block.norm.variance_epsilon), True, bool(block.residual_in_fp32),
+        mx.in_proj.weight, mx.in_proj.bias, conv_w, mx.conv1d.bias, layer.conv_states[0], mx.x_proj.weight,
+        mx.dt_proj.weight, dtb, A, D, layer.recurrent_states[0], mx.out_proj.weight, mx.out_proj.bias)
+
+
+def fused_model_step(model, token, cache):
+    """A transformers MambaForCausalLM decode step with fused blocks: token
+    (batch, 1) -> last-position logits (batch, vocab) float32, the cache
+    advanced in place."""
+    bb = model.backbone
+    h = bb.embeddings(token)[:, 0]
+    for blk in bb.layers:
+        h = fused_block_step(blk, h, cache)
+    h = bb.norm_f(h)
+    return model.lm_head(h.to(model.lm_head.weight.dtype)).float()
 
 
 def _cache_tensors(cache):
@@ -42,9 +126,11 @@ class GraphedDecodeStep:
     `cache` is the model's cache after the prompt (the `cache_params` a
     `use_cache=True` forward returns). `token` is the (batch, 1) int64 tensor
     the graph reads; `logits` the (batch, vocab) tensor it writes. Each
-    `replay()` advances the cache by the token in `token`."""
+    `replay()` advances the cache by the token in `token`. With `fused`
+    (the default) a Mamba model's blocks run as fused block steps where
+    fused_step_supported() allows; `self.fused` says whether they do."""
 
-    def __init__(self, model, cache, batch_size, warmup=2):
+    def __init__(self, model, cache, batch_size, warmup=2, fused=True):
         if model.config.model_type not in _GRAPH_MODELS:
             raise NotImplementedError(
                 f"graph-captured decoding supports {', '.join(_GRAPH_MODELS)} models, "
@@ -53,6 +139,7 @@ class GraphedDecodeStep:
         if dev.type != "cuda":
             raise ValueError(f"graph-captured decoding runs on ROCm GPU models, got device {dev}")
         self.model, self.cache = model, cache
+        self.fused = bool(fused) and fused_step_supported(model, cache, batch_size)
         self.token = torch.zeros(batch_size, 1, dtype=torch.long, device=dev)
         states = _cache_tensors(cache)
         saved = [t.clone() for t in states]
@@ -74,6 +161,8 @@ class GraphedDecodeStep:
             self.logits = self._step()
 
     def _step(self):
+        if self.fused:
+            return fused_model_step(self.model, self.token, self.cache)
         out = self.model(input_ids=self.token, cache_params=self.cache, use_cache=True)
         return out.logits[:, -1]
 
@@ -83,7 +172,7 @@ class GraphedDecodeStep:
 
 
 @torch.no_grad()
-def greedy_generate(model, input_ids, max_new_tokens):
+def greedy_generate(model, input_ids, max_new_tokens, fused=True):
     """Greedy decoding: the prompt in one eager forward, then `max_new_tokens`
     - 1 graph-replayed steps. Returns (batch, prompt + max_new_tokens) int64
     token ids, as `model.generate(input_ids, max_new_tokens=max_new_tokens,
@@ -93,7 +182,7 @@ def greedy_generate(model, input_ids, max_new_tokens):
     new = torch.empty(b, max_new_tokens, dtype=torch.long, device=input_ids.device)
     new[:, :1] = out.logits[:, -1].argmax(-1, keepdim=True)
     if max_new_tokens > 1:
-        step = GraphedDecodeStep(model, out.cache_params, b)
+        step = GraphedDecodeStep(model, out.cache_params, b, fused=fused)
         for i in range(1, max_new_tokens):
             step.token.copy_(new[:, i - 1:i])
             new[:, i:i + 1] = step.replay().argmax(-1, keepdim=True)

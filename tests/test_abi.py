@@ -60,7 +60,7 @@ def test_argument_blocks_match_the_library():
 
     for name, cls in (("scan", _C.ScanArgs), ("conv", _C.ConvArgs),
                       ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs),
-                      ("ssd", _C.SsdArgs)):
+                      ("ssd", _C.SsdArgs), ("mixer_step", _C.MixerStepArgs)):
         assert _C.lib.mcpu_args_size(name.encode()) == ctypes.sizeof(cls)
     assert _C.lib.mcpu_args_size(b"nonsense") == 0
 
@@ -85,7 +85,8 @@ def _header_field_names(struct):
                                              ("mcpu_conv_args", "ConvArgs"),
                                              ("mcpu_conv_update_args", "ConvUpdateArgs"),
                                              ("mcpu_state_update_args", "StateUpdateArgs"),
-                                             ("mcpu_ssd_args", "SsdArgs")])
+                                             ("mcpu_ssd_args", "SsdArgs"),
+                                             ("mcpu_mixer_step_args", "MixerStepArgs")])
 def test_argument_block_fields_follow_the_header(struct, cls_name):
     from mamba_cpu import _C
 
@@ -452,3 +453,48 @@ def test_ssd_sizes_follow_the_layout():
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(seqlen=0))) == 0
     assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(batch=0))) == 0
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(headdim=24))) == 0
+
+
+def _step_args(**kw):
+    from mamba_cpu import _C
+
+    a = _C.MixerStepArgs()
+    for f in ("hidden", "in_w", "conv_w", "conv_state", "x_w", "dt_w", "A", "ssm_state", "out_w", "out"):
+        setattr(a, f, 256)  # non-NULL placeholders: never dereferenced
+    a.batch, a.d_model, a.d_inner, a.dt_rank, a.dstate, a.width, a.state_len = 4, 768, 1536, 48, 16, 4, 4
+    a.norm_eps = 1e-5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_mixer_step_rejects_bad_arguments_before_touching_a_device():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    step = lambda a, ws=None, n=0: _rc(L.mcpu_mixer_step, ctypes.byref(a), ws, n, None)  # noqa: E731
+    assert _rc(L.mcpu_mixer_step, None, None, 0, None)[0] == _C.MCPU_ERR_INVALID
+    for kw, code, word in ((dict(hidden=None), _C.MCPU_ERR_INVALID, "required"),
+                           (dict(batch=9), _C.MCPU_ERR_UNSUPPORTED, "batch"),
+                           (dict(d_model=770), _C.MCPU_ERR_UNSUPPORTED, "multiples of 4"),
+                           (dict(state_len=9), _C.MCPU_ERR_UNSUPPORTED, "conv state"),
+                           (dict(width=4, state_len=2), _C.MCPU_ERR_UNSUPPORTED, "conv state"),
+                           (dict(dstate=256), _C.MCPU_ERR_UNSUPPORTED, "dstate"),
+                           (dict(batch=8, d_inner=8192), _C.MCPU_ERR_UNSUPPORTED, "LDS"),
+                           (dict(dtype=5), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(dtype=_C.MCPU_BF16, hidden_dtype=_C.MCPU_F16), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(in_w=260), _C.MCPU_ERR_INVALID, "aligned")):
+        rc, msg = step(_step_args(**kw))
+        assert rc == code and word in msg, (kw, rc, msg)
+    rc, msg = step(_step_args())
+    assert rc == _C.MCPU_ERR_INVALID and "workspace" in msg
+
+
+def test_mixer_step_workspace_holds_the_step_vectors():
+    from mamba_cpu import _C
+
+    a = _step_args()
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    want = 3 * al(4 * 4 * 1536) + al(4 * 4 * (48 + 32))
+    assert _C.lib.mcpu_mixer_step_workspace_size(ctypes.byref(a)) == want
+    assert _C.lib.mcpu_mixer_step_workspace_size(ctypes.byref(_step_args(batch=9))) == 0

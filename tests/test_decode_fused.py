@@ -1,0 +1,141 @@
+"""The fused single-token Mamba block step (mamba_cpu::mixer_step, used by
+mamba_cpu.decode) against transformers' own decode step.
+
+- model level, float32, two layers of the Mamba-130M width (d_model 768,
+  d_inner 1536, dstate 16, dt_rank 48, width 4, vocabulary 50280), batch 4:
+  8 fused decode steps on the GPU against the same model on the CPU through
+  transformers' pure-torch path, logits and every cache tensor (logits reach
+  about 14: rtol 1e-4, atol 1e-4; SSM states reach about 100 after 24 steps
+  and conv windows about 13: rtol 1e-4, atol 1e-3);
+- block level, float32 and bfloat16 (residual in float32), batch 1 to 8:
+  one fused block step against the block's own forward on the GPU (its
+  kernels routed to this package), output and both states (float32: rtol
+  1e-4, atol 1e-5 where outputs stay below 4 (the 32-wide model), atol 1e-3
+  at the 768 width, whose outputs reach about 100 on unit-variance inputs;
+  bfloat16: 2e-2 / 2e-2);
+- the captured graph against eager fused steps, bitwise, and the torch.library
+  opcheck of the operator.
+"""
+
+import copy
+
+import pytest
+import torch
+
+pytest.importorskip("transformers", minversion="5.0")
+
+import transformers
+
+import mamba_cpu.decode as dec
+import mamba_cpu.hf
+from conftest import assert_close_report
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+W130 = dict(num_hidden_layers=2, hidden_size=768, state_size=16, expand=2, conv_kernel=4, vocab_size=50280)
+TINY = dict(vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=8, conv_kernel=4, expand=2)
+
+
+@pytest.fixture(autouse=True)
+def patched():
+    mamba_cpu.hf.patch_transformers()
+    yield
+    mamba_cpu.hf.unpatch_transformers()
+
+
+def mamba(cfg, dtype=torch.float32, seed=0):
+    torch.manual_seed(seed)
+    return transformers.MambaForCausalLM(transformers.MambaConfig(**cfg)).to(DEV, dtype).eval()
+
+
+def ids(shape, vocab, seed=1):
+    return torch.randint(0, vocab, shape, generator=torch.Generator().manual_seed(seed))
+
+
+def states(cache):
+    out = []
+    for layer in cache.layers:
+        out += [layer.conv_states[0], layer.recurrent_states[0]]
+    return out
+
+
+@torch.no_grad()
+def test_fused_decode_matches_transformers_on_the_cpu():
+    model = mamba(W130)
+    cpu_model = copy.deepcopy(model).cpu()
+    prompt, toks = ids((4, 16), 50280), ids((4, 8), 50280, seed=2)
+    cache = model(prompt.to(DEV), use_cache=True).cache_params
+    cpu_cache = cpu_model(prompt, use_cache=True).cache_params
+    assert dec.fused_step_supported(model, cache, 4)
+    for i in range(toks.shape[1]):
+        got = dec.fused_model_step(model, toks[:, i:i + 1].to(DEV), cache)
+        want = cpu_model(input_ids=toks[:, i:i + 1], cache_params=cpu_cache, use_cache=True).logits[:, -1]
+        assert_close_report(got, want, 1e-4, 1e-4, f"logits step {i}")
+    for k, (g, w) in enumerate(zip(states(cache), states(cpu_cache))):
+        assert_close_report(g, w, 1e-4, 1e-3, f"cache tensor {k}")
+
+
+@pytest.mark.parametrize("batch", [1, 3, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@torch.no_grad()
+def test_fused_block_step_matches_the_block(batch, dtype):
+    model = mamba(W130 if batch == 4 else TINY, dtype)
+    vocab = model.config.vocab_size
+    cache = model(ids((batch, 12), vocab).to(DEV), use_cache=True).cache_params
+    ref_cache = copy.deepcopy(cache)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    for blk in model.backbone.layers:
+        h = torch.randn(batch, model.config.hidden_size, generator=gen, device=DEV).to(dtype)
+        got = dec.fused_block_step(blk, h, cache)
+        want = blk(h[:, None], cache_params=ref_cache)[:, 0]
+        assert got.dtype == want.dtype and got.shape == want.shape
+        if dtype == torch.float32:
+            tol = (1e-4, 1e-5) if model.config.hidden_size <= 32 else (1e-4, 1e-3)
+        else:
+            tol = (2e-2, 2e-2)
+        assert_close_report(got, want, *tol, f"layer {blk.layer_idx} out")
+        layer, ref = cache.layers[blk.layer_idx], ref_cache.layers[blk.layer_idx]
+        assert_close_report(layer.conv_states[0], ref.conv_states[0], *tol, "conv state")
+        assert_close_report(layer.recurrent_states[0], ref.recurrent_states[0], *tol, "ssm state")
+
+
+@torch.no_grad()
+def test_graph_replays_equal_eager_fused_steps():
+    model = mamba(TINY)
+    prompt, toks = ids((2, 9), 64).to(DEV), ids((2, 10), 64, seed=2).to(DEV)
+    cache = model(prompt, use_cache=True).cache_params
+    eager = [dec.fused_model_step(model, toks[:, i:i + 1], cache).clone() for i in range(toks.shape[1])]
+    graphed = dec.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 2)
+    assert graphed.fused
+    for i in range(toks.shape[1]):
+        graphed.token.copy_(toks[:, i:i + 1])
+        got = graphed.replay().clone()
+        if i % 3 == 0:
+            torch.cuda.synchronize()
+        assert torch.equal(got, eager[i]), f"replay {i}"
+
+
+@torch.no_grad()
+def test_unsupported_models_keep_the_unfused_step():
+    model = mamba(TINY)
+    cache = model(ids((9, 4), 64).to(DEV), use_cache=True).cache_params
+    assert not dec.fused_step_supported(model, cache, 9)   # more than 8 batch rows
+    falcon = transformers.FalconMambaForCausalLM(transformers.FalconMambaConfig(**TINY)).to(DEV).eval()
+    fcache = falcon(ids((2, 4), 64).to(DEV), use_cache=True).cache_params
+    assert not dec.fused_step_supported(falcon, fcache, 2)
+
+
+def test_opcheck_mixer_step():
+    model = mamba(TINY)
+    with torch.no_grad():
+        cache = model(ids((3, 5), 64).to(DEV), use_cache=True).cache_params
+    blk = model.backbone.layers[0]
+    mx = blk.mixer
+    A, D, dtb = dec._block_constants(mx)
+    layer = cache.layers[0]
+    h = torch.randn(3, 32, device=DEV)
+    args = (h, blk.norm.weight.detach(), 1e-5, True, True, mx.in_proj.weight.detach(), None,
+            mx.conv1d.weight.detach().view(mx.intermediate_size, -1), mx.conv1d.bias.detach(),
+            layer.conv_states[0], mx.x_proj.weight.detach(), mx.dt_proj.weight.detach(), dtb, A, D,
+            layer.recurrent_states[0], mx.out_proj.weight.detach(), None)
+    torch.library.opcheck(torch.ops.mamba_cpu.mixer_step.default, args)

@@ -253,7 +253,9 @@ def test_each_graph_replay_equals_the_eager_step():
         cache = model(prompt, use_cache=True).cache_params
         eager = [model(input_ids=steps[:, i:i + 1], cache_params=cache, use_cache=True).logits[:, -1].clone()
                  for i in range(steps.shape[1])]
-        graphed = mamba_cpu.decode.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 2)
+        # the model's own step, captured (the fused block steps have their own test)
+        graphed = mamba_cpu.decode.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 2,
+                                                     fused=False)
         for i in range(steps.shape[1]):
             graphed.token.copy_(steps[:, i:i + 1])
             got = graphed.replay().clone()
