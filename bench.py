@@ -16,7 +16,8 @@ Also reported, on one JSON line:
   cpu_baseline  the reference's own CPU kernels (oracle/_ref, built from the
                 reference sources) on the same workload on this host's cores;
   extra         forward-only time of the same workload; Mamba-130M (random
-                init) prefill 4 x 1024 tokens/s, 128-step greedy decode and a
+                init) prefill 4 x 1024 tokens/s, 128-step greedy decode
+                (generate, and graph-replayed with fused block steps) and a
                 4 x 256 training step through the patched Hugging Face model;
                 and every other workload of the op set (forward-only scan,
                 long-sequence bf16 scan, complex-A scan, conv1d fp32/bf16,
@@ -668,6 +669,20 @@ def mamba130m(torch, dev, keep, iters=3):
     res["decode_graph_ms_per_step"] = round(sec / 128 * 1e3, 3)
     res["decode_graph_tokens_per_s"] = round(4 * 128 / sec, 1)
     res["decode_graph_tokens_match_generate"] = bool(torch.equal(gout, out))
+    # The captured step alone, replayed back to back: with each block as one
+    # fused step (mamba_cpu::mixer_step, what greedy_generate uses) and with
+    # the model's own step (a dozen kernels per block).
+    with torch.no_grad():
+        for fused in (True, False):
+            step = mamba_cpu.decode.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 4,
+                                                      fused=fused)
+            step.token.copy_(prompt[:, -1:])
+            ms = _events_ms(torch, torch.cuda.current_stream(dev), step.replay, 50)
+            key = "decode_graph_replay_ms_per_step" + ("" if fused else "_model_step")
+            res[key] = round(ms, 4)
+            if fused:
+                res["decode_graph_fused_blocks"] = step.fused
+            del step
 
     model.train()
     tids = ids[:, :256]
