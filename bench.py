@@ -634,6 +634,12 @@ def mamba130m(torch, dev, keep, iters=3):
     ids = _mamba130m_ids(torch).to(dev)
     with torch.no_grad():
         keep["logits"] = model(ids).logits.cpu()
+        # The same prefill through transformers' own torch ops on this GPU (its
+        # GEMMs are the patched model's): how far float32 alone moves the
+        # logits of this 24-layer random model from the CPU leg's.
+        mamba_cpu.hf.unpatch_transformers()
+        keep["logits_torch_gpu"] = model(ids).logits.cpu()
+        mamba_cpu.hf.patch_transformers()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(iters):
@@ -719,8 +725,10 @@ def cpu_mamba130m(torch, keep, decode_steps=16):
     benchmarks/check_hf_model.py:105-121: largest |logit difference| and
     top-1 agreement over all 4 x 1024 prefill positions, whether the sampled
     greedy tokens are identical, the two training losses and the worst
-    per-tensor gradient error max|dg| / max|g|. Returns a dict, or None when
-    the reference kernels are not built."""
+    per-tensor gradient error max|dg| / max|g|; beside them the same logit
+    measures for transformers' own torch ops on the GPU, the float32 spread
+    this 24-layer random model shows without this package's kernels.
+    Returns a dict, or None when the reference kernels are not built."""
     from oracle import cpu_torch as CT
     from oracle import ref as R
 
@@ -744,6 +752,13 @@ def cpu_mamba130m(torch, keep, decode_steps=16):
             agree["max_abs_logit"] = float(logits.abs().max())
             agree["top1_agreement"] = float((keep["logits"].argmax(-1) == logits.argmax(-1)).float().mean())
             agree["positions"] = int(logits.shape[0] * logits.shape[1])
+        if "logits_torch_gpu" in keep:
+            ref = keep["logits_torch_gpu"]
+            agree["float32_floor_transformers_torch_on_gpu"] = {
+                "max_abs_logit_diff": float((ref - logits).abs().max()),
+                "top1_agreement": float((ref.argmax(-1) == logits.argmax(-1)).float().mean()),
+                "vs_this_package_max_abs_logit_diff": float((ref - keep["logits"]).abs().max()),
+            }
         del logits
 
         prompt = ids[:, :16]
