@@ -854,14 +854,14 @@ def counter_pass(torch, dev, inputs, gout, which):
     print(f"counter pass ({which}) done", flush=True)
 
 
-def ssd_pass(torch, dev):
-    """Three forward+backward passes of the bf16 SSD workload, for
-    rocprofv3 --kernel-trace."""
+def ssd_pass(torch, dev, xdt):
+    """Three forward+backward passes of the SSD workload with x/z/B/C in
+    `xdt`, for rocprofv3 runs."""
     from mamba_cpu import mamba_chunk_scan_combined
 
-    t = _ssd_inputs(torch, dev, torch.bfloat16, SSD_SHAPE)
+    t = _ssd_inputs(torch, dev, xdt, SSD_SHAPE)
     leaves = {k: v.requires_grad_() for k, v in t.items()}
-    gout = torch.randn(t["x"].shape, device=dev).to(torch.bfloat16)
+    gout = torch.randn(t["x"].shape, device=dev).to(xdt)
     for i in range(3):
         out = mamba_chunk_scan_combined(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 256,
                                         D=leaves["D"], z=leaves["z"], dt_bias=leaves["dt_bias"], dt_softplus=True)
@@ -910,8 +910,9 @@ def main():
     ap.add_argument("--counter-pass", nargs="?", const="train", choices=["train", "fwd", "long"],
                     help="only run 3 x (one workload's scan ops, 256 MiB copy) for rocprofv3 --pmc: "
                          "train (default), fwd or long")
-    ap.add_argument("--ssd-pass", action="store_true",
-                    help="only run 3 forward+backward passes of the bf16 SSD workload for kernel traces")
+    ap.add_argument("--ssd-pass", nargs="?", const="bf16", choices=["bf16", "fp32"],
+                    help="only run 3 forward+backward passes of the SSD workload (bf16 by default) for "
+                         "kernel traces")
     ap.add_argument("--model-pass", choices=["train", "decode"],
                     help="only run a short Mamba-130M train or graph-decode sequence for kernel traces")
     args = ap.parse_args()
@@ -931,7 +932,7 @@ def main():
         model_pass(torch, dev, args.model_pass)
         return
     if args.ssd_pass:
-        ssd_pass(torch, dev)
+        ssd_pass(torch, dev, torch.bfloat16 if args.ssd_pass == "bf16" else torch.float32)
         return
     inputs, gout = make_inputs(torch, dev)
     if args.counter_pass:

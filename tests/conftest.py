@@ -61,8 +61,9 @@ def assert_close_report(got, want, rtol, atol, name=""):
     if got.size:
         err = np.abs(got - want)
         bound = atol + rtol * np.abs(want)
-        with np.errstate(invalid="ignore"):
-            ratio = np.nanmax(err / bound) if np.isfinite(err).any() else float("nan")
+        with np.errstate(invalid="ignore", divide="ignore"):
+            ratio = np.where(bound > 0, err / np.where(bound > 0, bound, 1.0), np.where(err > 0, np.inf, 0.0))
+            ratio = np.nanmax(ratio) if np.isfinite(err).any() else float("nan")
         print(f"  {name}: max|want| {np.abs(want).max():.3g}  max err {np.nanmax(err):.3g}  "
               f"worst err/bound {ratio:.3g}", flush=True)
     np.testing.assert_allclose(got, want, rtol=rtol, atol=atol, err_msg=name)

@@ -397,6 +397,43 @@ def test_scan_writes_outputs_through_their_strides():
         assert (bufs[k][..., :d] == 7.0).all(), f"{k} wrote outside its view"
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("silu", [0, 1])
+def test_conv_backward_with_initial_states_but_no_dinitial_states(silu):
+    """A C-ABI caller may give initial_states without asking for their
+    gradient. With channel-contiguous x (the layout whose fast kernels take no
+    initial states) dx, dweight and dbias must still see the initial states in
+    the first width-1 taps: checked against the float64 oracle (rtol 1e-4,
+    atol 1e-5)."""
+    from conftest import assert_close_report
+    from mamba_cpu import _C
+    from oracle import numerics as O
+
+    torch.manual_seed(5)
+    b, d, l, w = 2, 64, 37, 4
+    dev = "cuda"
+    x = torch.randn(b, l, d, device=dev).transpose(1, 2)          # channel-contiguous view
+    dout = torch.randn(b, l, d, device=dev).transpose(1, 2)
+    weight, bias = torch.randn(d, w, device=dev), torch.randn(d, device=dev)
+    init = torch.randn(b, d, w - 1, device=dev)
+    dx = torch.empty(b, l, d, device=dev).transpose(1, 2)
+    dweight, dbias = torch.empty(d, w, device=dev), torch.empty(d, device=dev)
+    a = _C.ConvArgs()
+    a.x, a.weight, a.bias, a.initial_states = x.data_ptr(), weight.data_ptr(), bias.data_ptr(), init.data_ptr()
+    a.batch, a.dim, a.seqlen, a.width, a.silu, a.dtype = b, d, l, w, silu, _C.MCPU_F32
+    a.x_stride[:], a.init_stride[:] = x.stride(), init.stride()
+    a.dout, a.dx, a.dweight, a.dbias = dout.data_ptr(), dx.data_ptr(), dweight.data_ptr(), dbias.data_ptr()
+    a.dout_stride[:], a.dx_stride[:] = dout.stride(), dx.stride()
+    n = _C.lib.mcpu_causal_conv1d_bwd_workspace_size(ctypes.byref(a))
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
+    rc = _C.lib.mcpu_causal_conv1d_bwd(ctypes.byref(a), ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _C.lib.mcpu_last_error().decode()
+    torch.cuda.synchronize()
+    want = O.causal_conv1d_bwd(x, weight, bias, init, dout, activation="silu" if silu else None)
+    for name, got, ref in (("dx", dx, want[0]), ("dweight", dweight, want[1]), ("dbias", dbias, want[2])):
+        assert_close_report(got, ref, 1e-4, 1e-5, name)
+
+
 def _ssd_args(**kw):
     from mamba_cpu import _C
 
