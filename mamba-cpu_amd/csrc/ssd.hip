@@ -83,6 +83,7 @@ template <int NT, bool SCALE = false>
 __device__ __forceinline__ void mma(v4f (&acc)[NT], int nt, const float* a, int ai, int ak, const float* b, int bk,
                                     int bj, int K, float as = 1.f) {
   static_assert(NT >= 1 && NT <= 8, "tile count");
+  if (nt <= 0) return;
   switch (nt) {
     case 1: mma_n<1, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
     case 2: if constexpr (NT >= 2) mma_n<2, NT, SCALE>(acc, a, ai, ak, b, bk, bj, K, as); break;
@@ -136,23 +137,30 @@ __device__ __forceinline__ int tile_row(int v, float inv_nv) {
   return static_cast<int>((static_cast<float>(v) + 0.5f) * inv_nv);
 }
 
+// The backward chunk kernel runs 8 waves: two per 16-row strip, splitting
+// each product's column tiles.
+constexpr int kThreads3 = 512;
+
 // float4 per thread of the staged tiles: (64 x dstate) and (headdim x
-// dstate) tiles, (64 x headdim) tiles and (headdim x 64-state half) tiles.
-constexpr int kVecN = Q * kSsdMaxN / 4 / kThreads;
-constexpr int kVecX = Q * kSsdMaxP / 4 / kThreads;
+// dstate) tiles, (64 x headdim) tiles and (headdim x 64-state half) tiles,
+// for a workgroup of TPB threads.
+template <int TPB = kThreads> constexpr int vec_n() { return Q * kSsdMaxN / 4 / TPB; }
+template <int TPB = kThreads> constexpr int vec_x() { return Q * kSsdMaxP / 4 / TPB; }
+constexpr int kVecN = vec_n();
+constexpr int kVecX = vec_x();
 
 // Registers x = rows r < nrows, columns c < ncols (multiple of 4) of
 // src[r rs + c], four elements per float4, rows from nvalid on zero; thread
-// tid holds float4 number tid + k kThreads of the row-major tile. The loads
-// are issued here and waited for where the registers are used.
-template <typename Tx, int V>
+// tid holds float4 number tid + k TPB of the row-major tile. The loads are
+// issued here and waited for where the registers are used.
+template <typename Tx, int V, int TPB = kThreads>
 __device__ __forceinline__ void tile_load(float4 (&x)[V], const Tx* src, int64_t rs, int nrows, int nvalid,
                                           int ncols) {
   const int nv = ncols >> 2, total = nrows * nv;
   const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    const int v = threadIdx.x + k * kThreads;
+    const int v = threadIdx.x + k * TPB;
     x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (v < total) {
       const int r = tile_row(v, inv);
@@ -163,14 +171,14 @@ __device__ __forceinline__ void tile_load(float4 (&x)[V], const Tx* src, int64_t
 
 // LDS tile s (rows of ld floats) from registers filled by tile_load with the
 // same nrows / ncols, times scale[r] when given.
-template <int V>
+template <int V, int TPB = kThreads>
 __device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V], int nrows, int ncols,
                                            const float* scale = nullptr) {
   const int nv = ncols >> 2, total = nrows * nv;
   const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    const int v = threadIdx.x + k * kThreads;
+    const int v = threadIdx.x + k * TPB;
     if (v < total) {
       const int r = tile_row(v, inv);
       const int c = (v - r * nv) << 2;
@@ -180,26 +188,27 @@ __device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V
 }
 
 // tile_load then tile_store.
-template <typename Tx, int V>
+template <typename Tx, int V, int TPB = kThreads>
 __device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t rs, int nrows, int nvalid, int ncols,
                                       const float* scale = nullptr) {
   float4 x[V];
-  tile_load<Tx, V>(x, src, rs, nrows, nvalid, ncols);
-  tile_store<V>(s, ld, x, nrows, ncols, scale);
+  tile_load<Tx, V, TPB>(x, src, rs, nrows, nvalid, ncols);
+  tile_store<V, TPB>(s, ld, x, nrows, ncols, scale);
 }
 
 // The dout, z and ysave tiles of one head's chunk (x layout from `off`, z and
-// ysave only when HAS_Z and, for ysave, want_y).
-template <typename Tx, bool HAS_Z>
+// ysave only when HAS_Z and, for ysave, want_y), for a workgroup of TPB threads.
+template <typename Tx, bool HAS_Z, int TPB = kThreads>
 struct DyTiles {
-  float4 go[kVecX], zz[kVecX], yy[kVecX];
+  static constexpr int V = vec_x<TPB>();
+  float4 go[V], zz[V], yy[V];
 
   __device__ __forceinline__ void load(const SsdParams& p, int64_t off, int64_t rs, int nvalid, int ncols,
                                        bool want_y) {
-    tile_load<Tx, kVecX>(go, static_cast<const Tx*>(p.dout) + off, rs, Q, nvalid, ncols);
+    tile_load<Tx, V, TPB>(go, static_cast<const Tx*>(p.dout) + off, rs, Q, nvalid, ncols);
     if (HAS_Z) {
-      tile_load<Tx, kVecX>(zz, static_cast<const Tx*>(p.z) + off, rs, Q, nvalid, ncols);
-      if (want_y) tile_load<Tx, kVecX>(yy, static_cast<const Tx*>(p.ysave) + off, rs, Q, nvalid, ncols);
+      tile_load<Tx, V, TPB>(zz, static_cast<const Tx*>(p.z) + off, rs, Q, nvalid, ncols);
+      if (want_y) tile_load<Tx, V, TPB>(yy, static_cast<const Tx*>(p.ysave) + off, rs, Q, nvalid, ncols);
     }
   }
 
@@ -210,8 +219,8 @@ struct DyTiles {
     const int nv = ncols >> 2, total = Q * nv;
     const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
-    for (int k = 0; k < kVecX; ++k) {
-      const int v = threadIdx.x + k * kThreads;
+    for (int k = 0; k < V; ++k) {
+      const int v = threadIdx.x + k * TPB;
       if (v >= total) continue;
       const int r = tile_row(v, inv);
       const int c = (v - r * nv) << 2;
@@ -596,23 +605,31 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams 
 }
 
 // K3: every gradient of a chunk, for each head of the block. Grid (nchunks,
-// nhb, batch); wave w owns rows [16 w, 16 w + 16) of every Q-row product.
-// dB and dC of the block's heads stay in accumulators and are written once,
-// as the block's partial sums.
+// nhb, batch), 8 waves: wave w owns rows [16 (w % 4), 16 (w % 4) + 16) of
+// every Q-row product and half h = w / 4 of its column tiles (Q columns:
+// tiles 2h, 2h + 1; headdim columns: the first or second half of the tiles;
+// state columns: tiles 2h, 2h + 1 of each 64-state group). Two waves per SIMD
+// hide each other's LDS and memory latency. Row sums over columns are
+// combined across the two halves through LDS. dB and dC of the block's heads
+// stay in accumulators and are written once, as the block's partial sums.
 template <typename Tx, bool HAS_Z>
-__global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdParams p) {
+__global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdParams p) {
+  constexpr int TPB = kThreads3;
+  constexpr int VX = vec_x<TPB>(), VN = vec_n<TPB>();
   __shared__ __align__(16) float s_C[Q][NP];
   __shared__ __align__(16) float s_B[Q][NP];
   __shared__ __align__(16) float s_X[Q][XP];      // x
   __shared__ __align__(16) float s_dY[Q][XP];     // dY
-  __shared__ __align__(16) float s_U[Q][QP];      // G = C B^T o M, then dH^out (P x 64-state half)
-  __shared__ __align__(16) float s_V[Q][QP];      // dCB, then H (P x 64-state half)
-  __shared__ float s_colp[16][Q];                 // column sums of dG o G, per (wave, lane quarter)
+  __shared__ __align__(16) float s_U[Q][QP];      // G = C B^T o M, then dH^out (P x 64-state group)
+  __shared__ __align__(16) float s_V[Q][QP];      // dCB, then H (P x 64-state group), then dx
+  __shared__ float s_colp[16][Q];                 // column sums of dG o G, per (row strip, lane quarter)
   __shared__ float s_dD[16][kSsdMaxP];
+  __shared__ float s_half[2][4][Q];               // per column half: sum_s R, sum_n C.., sum_n B~.., sum_p ..
   __shared__ float s_cs[Q], s_csl[Q], s_dt[Q], s_w[Q], s_ecs[Q], s_dcs[Q];
-  __shared__ float s_tot[4], s_wa[4], s_wb[4];
+  __shared__ float s_tot[8], s_wa[8], s_wb[8];
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ws = wave & 3, hf = wave >> 2;        // row strip, column half
   const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
   const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
@@ -620,22 +637,35 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
   const int64_t t0 = c * Q;
   const int nvalid = chunk_steps(p, t0);
   const int np = static_cast<int>(P / 16), nn = static_cast<int>(N / 16);
+  // headdim tiles of this wave: [p0, p0 + npw)
+  const int pa = (np + 1) / 2;
+  const int p0 = hf ? pa : 0, npw = hf ? np - pa : pa;
+  // state tiles of this wave in the 64-state group starting at tile 4 grp
+  auto ntw = [&](int grp) {
+    const int nt = nn - 4 * grp < 4 ? nn - 4 * grp : 4;
+    const int k = nt - 2 * hf;
+    return k < 0 ? 0 : (k > 2 ? 2 : k);
+  };
   {
     const int64_t off = ((b * L + t0) * G + g) * N;
-    stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
-    stage<Tx, kVecN>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, VN, TPB>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, VN, TPB>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
   __syncthreads();
-  v4f cb[Q / 16];
+  // C B^T, rows t of this strip, Q-column tiles 2 hf, 2 hf + 1
+  v4f cb[2];
   zero(cb);
-  mma(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_B[0][0], 1, NP, static_cast<int>(N));
-  v4f dBa[kSsdMaxN / 16], dCa[kSsdMaxN / 16];
-  zero(dBa);
-  zero(dCa);
+  mma(cb, 2, &s_C[16 * ws][0], NP, 1, &s_B[32 * hf][0], 1, NP, static_cast<int>(N));
+  v4f dBa[2][2], dCa[2][2];   // [64-state group][tile of this wave]
+#pragma unroll
+  for (int grp = 0; grp < 2; ++grp) {
+    zero(dBa[grp]);
+    zero(dCa[grp]);
+  }
   // The next head's x, dout, z and ysave tiles and decays load into
   // registers while this head's products run.
-  float4 rx[kVecX];
-  DyTiles<Tx, HAS_Z> rdy;
+  float4 rx[VX];
+  DyTiles<Tx, HAS_Z, TPB> rdy;
   float rcs = 0.f, rcsl = 0.f, rdt = 0.f, rcsL = 0.f, rcslL = 0.f;
   auto fetch = [&](int64_t h) {
     const int64_t row = chunk_row(p, b, h, c);
@@ -647,7 +677,7 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       rcsL = p.cs[row + Q - 1];
       rcslL = p.cs_lo[row + Q - 1];
     }
-    tile_load<Tx, kVecX>(rx, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+    tile_load<Tx, VX, TPB>(rx, static_cast<const Tx*>(p.x) + xoff, H * P, Q, nvalid, static_cast<int>(P));
     rdy.load(p, xoff, H * P, nvalid, static_cast<int>(P), true);
   };
   fetch(h0);
@@ -664,24 +694,24 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       s_w[tid] = fast_exp((rcsL - rcs) + (rcslL - rcsl));
       s_ecs[tid] = fast_exp(rcs + rcsl);
     }
-    tile_store<kVecX>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    tile_store<VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
     rdy.store(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
     __syncthreads();
     if (i + 1 < p.hb) fetch(h + 1);
-    // dGraw = dY x^T (rows t of this wave, all columns s); then with M and dt:
-    // G = CB o M, dCB = dt_s dGraw o M, R = dCB o CB (= dG o G); the row sums
-    // of R in the wave, its column sums through LDS, both in a fixed order.
+    // dGraw = dY x^T (rows t of this strip, this half's columns s); with M and
+    // dt: G = CB o M, dCB = dt_s dGraw o M, R = dCB o CB (= dG o G). Row sums
+    // of R per half and column sums per strip through LDS, in a fixed order.
     float rowsum[4] = {0.f, 0.f, 0.f, 0.f};
     {
-      v4f dg[Q / 16];
+      v4f dg[2];
       zero(dg);
-      mma(dg, Q / 16, &s_dY[16 * wave][0], XP, 1, &s_X[0][0], 1, XP, static_cast<int>(P));
+      mma(dg, 2, &s_dY[16 * ws][0], XP, 1, &s_X[32 * hf][0], 1, XP, static_cast<int>(P));
 #pragma unroll
-      for (int j = 0; j < Q / 16; ++j) {
+      for (int j = 0; j < 2; ++j) {
         float colsum = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
+          const int t = 16 * ws + 4 * q + e, s = 32 * hf + 16 * j + r;
           const float m = s <= t ? seg_exp(s_cs, s_csl, t, s) : 0.f;
           const float dcb = dg[j][e] * s_dt[s] * m;
           const float rv = dcb * cb[j][e];
@@ -690,80 +720,86 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
           rowsum[e] += rv;
           colsum += rv;
         }
-        s_colp[4 * wave + q][16 * j + r] = colsum;
+        s_colp[4 * ws + q][32 * hf + 16 * j + r] = colsum;
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) rowsum[e] = row_allreduce16(rowsum[e]);
-    __syncthreads();
-    // dcs_intra[t] = sum_s R[t][s] - sum_s R[s][t]; lane r == e of quarter q has row t.
     if (r < 4) {
       float mine = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (r == e) mine = rowsum[e];
-      const int t = 16 * wave + 4 * q + r;
+      s_half[hf][0][16 * ws + 4 * q + r] = mine;
+    }
+    __syncthreads();
+    // dcs_intra[t] = sum_s R[t][s] - sum_s R[s][t] (half 0's quarter lanes r < 4 own row t).
+    if (hf == 0 && r < 4) {
+      const int t = 16 * ws + 4 * q + r;
       float col = 0.f;
       for (int k = 0; k < 16; ++k) col += s_colp[k][t];
-      s_dcs[t] = mine - col;
+      s_dcs[t] = (s_half[0][0][t] + s_half[1][0][t]) - col;
     }
-    // d(dt x)[s][p] = sum_t G[t][s] dY[t][p] (rows s of this wave), then the state part below.
-    v4f dxa[kSsdMaxP / 16];
+    // d(dt x)[s][p] = sum_t G[t][s] dY[t][p] (rows s of this strip, this half's headdim tiles).
+    v4f dxa[2];
     zero(dxa);
-    mma(dxa, np, &s_U[0][16 * wave], 1, QP, &s_dY[0][0], XP, 1, Q);
-    // dC[t][n] += sum_s dCB[t][s] B[s][n] ; dB[s][n] += sum_t dCB[t][s] C[t][n].
-    mma(dCa, nn, &s_V[16 * wave][0], QP, 1, &s_B[0][0], NP, 1, Q);
-    mma(dBa, nn, &s_V[0][16 * wave], 1, QP, &s_C[0][0], NP, 1, Q);
-    // State terms, over 64-state halves of dH^out and H.
+    mma(dxa, npw, &s_U[0][16 * ws], 1, QP, &s_dY[0][16 * p0], XP, 1, Q);
+    // dC[t][n] += sum_s dCB[t][s] B[s][n] ; dB[s][n] += sum_t dCB[t][s] C[t][n] (this wave's state tiles).
+#pragma unroll
+    for (int grp = 0; grp < 2; ++grp) {
+      const int nt = ntw(grp);
+      const int col = 64 * grp + 32 * hf;
+      mma(dCa[grp], nt, &s_V[16 * ws][0], QP, 1, &s_B[0][col], NP, 1, Q);
+      mma(dBa[grp], nt, &s_V[0][16 * ws], 1, QP, &s_C[0][col], NP, 1, Q);
+    }
+    // State terms, over 64-state groups of dH^out and H.
     float a_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n C[t][n] exp(cs_t) (dY H)[t][n]
     float b_row[4] = {0.f, 0.f, 0.f, 0.f};  // sum_n w_s B[s][n] ((dt x) dH)[s][n]
-    const float dt_row = s_dt[16 * wave + r], w_row = s_w[16 * wave + r];
+    const float dt_row = s_dt[16 * ws + r], w_row = s_w[16 * ws + r];
 #pragma unroll
-    for (int half = 0; half < kSsdMaxN / 64; ++half) {
-      const int n0 = 64 * half;
+    for (int grp = 0; grp < kSsdMaxN / 64; ++grp) {
+      const int n0 = 64 * grp;
       if (n0 >= N) break;
       const int nw = static_cast<int>(N - n0 < 64 ? N - n0 : 64);
-      const int nt = nw / 16;
+      const int nt = ntw(grp);
       __syncthreads();  // every wave is done reading s_U / s_V
-      stage<float, kVecX>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
-      stage<float, kVecX>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      stage<float, VX, TPB>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      stage<float, VX, TPB>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
       __syncthreads();
-      v4f tv[4], yh[4];
+      v4f tv[2], yh[2];
       zero(tv);
       zero(yh);
       // tv[s][n] = sum_p dt_s x[s][p] dH[p][n] ; yh[t][n] = sum_p dY[t][p] H[p][n]
-      mma<4, true>(tv, nt, &s_X[16 * wave][0], XP, 1, &s_U[0][0], QP, 1, static_cast<int>(P), dt_row);
-      mma(yh, nt, &s_dY[16 * wave][0], XP, 1, &s_V[0][0], QP, 1, static_cast<int>(P));
+      mma<2, true>(tv, nt, &s_X[16 * ws][0], XP, 1, &s_U[0][32 * hf], QP, 1, static_cast<int>(P), dt_row);
+      mma(yh, nt, &s_dY[16 * ws][0], XP, 1, &s_V[0][32 * hf], QP, 1, static_cast<int>(P));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         if (j >= nt) continue;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int t = 16 * wave + 4 * q + e;
-          const int n = n0 + 16 * j + r;
+          const int t = 16 * ws + 4 * q + e;
+          const int n = n0 + 32 * hf + 16 * j + r;
           const float wt = s_w[t] * tv[j][e];
           const float ys = s_ecs[t] * yh[j][e];
-          dBa[4 * half + j][e] += wt;
-          dCa[4 * half + j][e] += ys;
+          dBa[grp][j][e] += wt;
+          dCa[grp][j][e] += ys;
           b_row[e] = fmaf(s_B[t][n], wt, b_row[e]);
           a_row[e] = fmaf(s_C[t][n], ys, a_row[e]);
         }
       }
-      // d(dt x)[s][p] += sum_n w_s B[s][n] dH[p][n]
-      mma<kSsdMaxP / 16, true>(dxa, np, &s_B[16 * wave][n0], NP, 1, &s_U[0][0], 1, QP, nw, w_row);
+      // d(dt x)[s][p] += sum_n w_s B[s][n] dH[p][n] (all states of the group, this half's headdim tiles)
+      mma<2, true>(dxa, npw, &s_B[16 * ws][n0], NP, 1, &s_U[16 * p0][0], 1, QP, nw, w_row);
     }
-    // sum_p d(dt x) x (for dstep) ; dD partial sums (rows past the sequence are 0).
+    // sum_p d(dt x) x (for dstep) and dD partial sums over this half's headdim tiles.
     float c_row[4] = {0.f, 0.f, 0.f, 0.f};
-    float dD_col[kSsdMaxP / 16];
-#pragma unroll
-    for (int j = 0; j < kSsdMaxP / 16; ++j) dD_col[j] = 0.f;
+    float dD_col[2] = {0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int s = 16 * wave + 4 * q + e;
+      const int s = 16 * ws + 4 * q + e;
 #pragma unroll
-      for (int j = 0; j < kSsdMaxP / 16; ++j) {
-        if (j >= np) continue;
-        const int pp = 16 * j + r;
+      for (int j = 0; j < 2; ++j) {
+        if (j >= npw) continue;
+        const int pp = 16 * (p0 + j) + r;
         const float xv = s_X[s][pp];
         c_row[e] = fmaf(dxa[j][e], xv, c_row[e]);
         dD_col[j] = fmaf(s_dY[s][pp], xv, dD_col[j]);
@@ -776,45 +812,48 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       c_row[e] = row_allreduce16(c_row[e]);
     }
 #pragma unroll
-    for (int j = 0; j < kSsdMaxP / 16; ++j)
-      if (j < np) s_dD[4 * wave + q][16 * j + r] = dD_col[j];
+    for (int j = 0; j < 2; ++j)
+      if (j < npw) s_dD[4 * ws + q][16 * (p0 + j) + r] = dD_col[j];
     // the chunk's sum of b_row is the cs_L term of the states' dependence on w
     float bsum = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) bsum += b_row[e];  // this quarter's 4 rows, alike in every lane of the row
     bsum = wave_total(r == 0 ? bsum : 0.f);
     if (lane == 0) s_tot[wave] = bsum;
-    float c_mine = 0.f;
     if (r < 4) {
-      float av = 0.f, bv = 0.f;
+      float av = 0.f, bv = 0.f, cv = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (r == e) {
           av = a_row[e];
           bv = b_row[e];
-          c_mine = c_row[e];
+          cv = c_row[e];
         }
-      s_dcs[16 * wave + 4 * q + r] += av - bv;
+      const int t = 16 * ws + 4 * q + r;
+      s_half[hf][1][t] = av;
+      s_half[hf][2][t] = bv;
+      s_half[hf][3][t] = cv;
     }
-    __syncthreads();  // every wave is done reading s_U / s_V
+    __syncthreads();  // every wave is done reading s_U / s_V; halves' row sums are in
     // dx = dt d(dt x) + D dY into s_V, stored below four elements at a time
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int s = 16 * wave + 4 * q + e;
+      const int s = 16 * ws + 4 * q + e;
 #pragma unroll
-      for (int j = 0; j < kSsdMaxP / 16; ++j) {
-        if (j >= np) continue;
-        const int pp = 16 * j + r;
+      for (int j = 0; j < 2; ++j) {
+        if (j >= npw) continue;
+        const int pp = 16 * (p0 + j) + r;
         float dxv = dxa[j][e] * s_dt[s];
         if (p.D) dxv = fmaf(p.D[h * P + pp], s_dY[s][pp], dxv);
         s_V[s][pp] = dxv;
       }
     }
     if (wave == 0) {
-      // add the cs_L terms, then da = suffix sums of dcs over the chunk
-      float v = s_dcs[lane];
+      // dcs with the state terms, the cs_L terms, then da = suffix sums over the chunk
+      float v = s_dcs[lane] + (s_half[0][1][lane] + s_half[1][1][lane]) -
+                (s_half[0][2][lane] + s_half[1][2][lane]);
       if (lane == Q - 1) {
-        float l = (s_tot[0] + s_tot[1]) + (s_tot[2] + s_tot[3]);
+        float l = ((s_tot[0] + s_tot[1]) + (s_tot[2] + s_tot[3])) + ((s_tot[4] + s_tot[5]) + (s_tot[6] + s_tot[7]));
         const float* dl = p.dcsL + (row / Q) * p.nslices;
         for (int64_t k = 0; k < p.nslices; ++k) l += dl[k];
         v += l;
@@ -822,15 +861,16 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       s_dcs[lane] = wave_suffix_sum(v);
     }
     __syncthreads();
-    // dstep = sum_p d(dt x) x + da A, then through softplus / clamp / bias.
+    // dstep = sum_p d(dt x) x + da A, then through softplus / clamp / bias (half 0's quarter lanes).
     float ddt_raw = 0.f, dA_term = 0.f;
-    if (r < 4) {
-      const int t = 16 * wave + 4 * q + r;
+    if (hf == 0 && r < 4) {
+      const int t = 16 * ws + 4 * q + r;
       if (t < nvalid) {
         float gfac;
         ssd_step(p, b, t0 + t, h, &gfac);
         const float da = s_dcs[t];
-        ddt_raw = fmaf(da, p.A[h], c_mine) * gfac;
+        const float c_all = s_half[0][3][t] + s_half[1][3][t];
+        ddt_raw = fmaf(da, p.A[h], c_all) * gfac;
         dA_term = da * s_dt[t];
         p.ddt[(b * L + t0 + t) * H + h] = ddt_raw;
       }
@@ -839,14 +879,13 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       const int nv = np * 4;
       const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
-      for (int k = 0; k < kVecX; ++k) {
-        const int v = tid + k * kThreads;
+      for (int k = 0; k < VX; ++k) {
+        const int v = tid + k * TPB;
         if (v >= Q * nv) continue;
         const int s = tile_row(v, inv);
         if (s >= nvalid) continue;
         const int pp = (v - s * nv) << 2;
-        st4<Tx>(static_cast<Tx*>(p.dx) + xoff + s * H * P + pp,
-                *reinterpret_cast<const float4*>(&s_V[s][pp]));
+        st4<Tx>(static_cast<Tx*>(p.dx) + xoff + s * H * P + pp, *reinterpret_cast<const float4*>(&s_V[s][pp]));
       }
     }
     const float wa = wave_total(dA_term), wb = wave_total(ddt_raw);
@@ -857,8 +896,8 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
     __syncthreads();
     const int64_t prt = (b * p.nchunks + c) * H + h;
     if (tid == 0) {
-      p.dA_part[prt] = (s_wa[0] + s_wa[1]) + (s_wa[2] + s_wa[3]);
-      p.dbias_part[prt] = (s_wb[0] + s_wb[1]) + (s_wb[2] + s_wb[3]);
+      p.dA_part[prt] = ((s_wa[0] + s_wa[1]) + (s_wa[2] + s_wa[3])) + ((s_wa[4] + s_wa[5]) + (s_wa[6] + s_wa[7]));
+      p.dbias_part[prt] = ((s_wb[0] + s_wb[1]) + (s_wb[2] + s_wb[3])) + ((s_wb[4] + s_wb[5]) + (s_wb[6] + s_wb[7]));
     }
     if (tid < P) {
       float v = 0.f;
@@ -866,18 +905,23 @@ __global__ void __launch_bounds__(kThreads, 1) ssd_bwd_chunk_kernel(const SsdPar
       p.dD_part[prt * P + tid] = v;
     }
   }
-  // the block's dB and dC partial sums
+  // the block's dB and dC partial sums (this wave's rows and state tiles)
   const int64_t hbk = blockIdx.y;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int t = 16 * wave + 4 * q + e;
+    const int t = 16 * ws + 4 * q + e;
     if (t >= nvalid) continue;
     const int64_t at = ((b * L + t0 + t) * p.nhb + hbk) * N;
 #pragma unroll
-    for (int j = 0; j < kSsdMaxN / 16; ++j) {
-      if (j >= nn) continue;
-      p.dC_part[at + 16 * j + r] = dCa[j][e];
-      p.dB_part[at + 16 * j + r] = dBa[j][e];
+    for (int grp = 0; grp < 2; ++grp) {
+      const int nt = ntw(grp);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (j >= nt) continue;
+        const int n = 64 * grp + 32 * hf + 16 * j + r;
+        p.dC_part[at + n] = dCa[grp][j][e];
+        p.dB_part[at + n] = dBa[grp][j][e];
+      }
     }
   }
 }
@@ -908,8 +952,8 @@ hipError_t bwd_t(const SsdParams& p, hipStream_t st) {
   if (hipError_t e = hipGetLastError()) return e;
   hipLaunchKernelGGL(ssd_bwd_pass_kernel, slices, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError()) return e;
-  if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
+  else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);
   return hipGetLastError();
 }
 
