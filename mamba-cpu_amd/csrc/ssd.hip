@@ -405,17 +405,22 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParam
 
 // F3: the chunk's outputs, Y = (C B^T o M) (dt x) + diag(exp(cs)) C H^T + D x,
 // out = Y silu(z) (and Y itself into ysave when the backward needs it).
-// Grid (nchunks, nhb, batch); wave w computes rows t in [16 w, 16 w + 16).
-// C B^T is formed once for the block's heads.
+// Grid (nchunks, nhb, batch), 8 waves: wave w computes rows t in
+// [16 (w % 4), 16 (w % 4) + 16) and half w / 4 of the column tiles (C B^T:
+// tiles 2h, 2h + 1; Y: the first or second half of the headdim tiles), so each
+// SIMD runs two waves. C B^T is formed once for the block's heads.
 template <typename Tx, bool HAS_Z>
-__global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParams p) {
+__global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdParams p) {
+  constexpr int TPB = kThreads3;
+  constexpr int VX = vec_x<TPB>(), VN = vec_n<TPB>();
   __shared__ __align__(16) float s_C[Q][NP];
   __shared__ __align__(16) float s_BH[Q][NP];     // B (Q x N), then each head's entering state H (P x N)
-  __shared__ __align__(16) float s_G[Q][QP];      // (C B^T o M)[t][s] dt_s
+  __shared__ __align__(16) float s_G[Q][QP];      // (C B^T o M)[t][s] dt_s, then Y
   __shared__ __align__(16) float s_X[Q][XP];      // x
   __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ws = wave & 3, hf = wave >> 2;        // row strip, column half
   const int r = lane & 15, q = lane >> 4;
   const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
   const int64_t h0 = static_cast<int64_t>(blockIdx.y) * p.hb;
@@ -423,18 +428,20 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
   const int64_t t0 = c * Q;
   const int nvalid = chunk_steps(p, t0);
   const int np = static_cast<int>(P / 16);
+  const int pa = (np + 1) / 2;
+  const int p0 = hf ? pa : 0, npw = hf ? np - pa : pa;   // this wave's headdim tiles
   {
     const int64_t off = ((b * L + t0) * G + g) * N;
-    stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
-    stage<Tx, kVecN>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, VN, TPB>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
+    stage<Tx, VN, TPB>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
   __syncthreads();
-  v4f cb[Q / 16];
+  v4f cb[2];
   zero(cb);
-  mma(cb, Q / 16, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+  mma(cb, 2, &s_C[16 * ws][0], NP, 1, &s_BH[32 * hf][0], 1, NP, static_cast<int>(N));
   // The next head's x tile, entering state and decays load into registers
   // while this head's products run.
-  float4 rx[kVecX], rh[kVecN], zc[kVecX];
+  float4 rx[VX], rh[VN], zc[VX];
   float rcs = 0.f, rcsl = 0.f, rdt = 0.f;
   auto fetch = [&](int64_t h) {
     const int64_t row = chunk_row(p, b, h, c);
@@ -443,10 +450,10 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
       rcsl = p.cs_lo[row + tid];
       rdt = p.step[row + tid];
     }
-    tile_load<Tx, kVecX>(rx, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
-                         static_cast<int>(P));
-    tile_load<float, kVecN>(rh, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
-                            static_cast<int>(N));
+    tile_load<Tx, VX, TPB>(rx, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
+                           static_cast<int>(P));
+    tile_load<float, VN, TPB>(rh, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
+                              static_cast<int>(N));
   };
   fetch(h0);
   for (int i = 0; i < p.hb; ++i) {
@@ -458,42 +465,42 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_scan_kernel(const SsdParam
       s_csl[tid] = rcsl;
       s_dt[tid] = rdt;
     }
-    tile_store<kVecX>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
-    tile_store<kVecN>(&s_BH[0][0], NP, rh, static_cast<int>(P), static_cast<int>(N));
+    tile_store<VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    tile_store<VN, TPB>(&s_BH[0][0], NP, rh, static_cast<int>(P), static_cast<int>(N));
     __syncthreads();
     if (HAS_Z)
-      tile_load<Tx, kVecX>(zc, static_cast<const Tx*>(p.z) + xoff, H * P, Q, nvalid, static_cast<int>(P));
+      tile_load<Tx, VX, TPB>(zc, static_cast<const Tx*>(p.z) + xoff, H * P, Q, nvalid, static_cast<int>(P));
     if (i + 1 < p.hb) fetch(h + 1);
 #pragma unroll
-    for (int j = 0; j < Q / 16; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int t = 16 * wave + 4 * q + e, s = 16 * j + r;
+        const int t = 16 * ws + 4 * q + e, s = 32 * hf + 16 * j + r;
         s_G[t][s] = s <= t ? cb[j][e] * seg_exp(s_cs, s_csl, t, s) * s_dt[s] : 0.f;
       }
     __syncthreads();
-    v4f y1[kSsdMaxP / 16], y2[kSsdMaxP / 16];
+    v4f y1[2], y2[2];
     zero(y1);
     zero(y2);
-    mma(y1, np, &s_G[16 * wave][0], QP, 1, &s_X[0][0], XP, 1, Q);
-    mma(y2, np, &s_C[16 * wave][0], NP, 1, &s_BH[0][0], 1, NP, static_cast<int>(N));
+    mma(y1, npw, &s_G[16 * ws][0], QP, 1, &s_X[0][16 * p0], XP, 1, Q);
+    mma(y2, npw, &s_C[16 * ws][0], NP, 1, &s_BH[16 * p0][0], 1, NP, static_cast<int>(N));
     __syncthreads();  // every wave is done reading s_G
     // Y (float32) into s_G, then out = (Y + D x) silu(z) four elements at a time.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * q + e;
+      const int t = 16 * ws + 4 * q + e;
       const float ecs = fast_exp(s_cs[t] + s_csl[t]);
 #pragma unroll
-      for (int j = 0; j < kSsdMaxP / 16; ++j)
-        if (j < np) s_G[t][16 * j + r] = fmaf(ecs, y2[j][e], y1[j][e]);
+      for (int j = 0; j < 2; ++j)
+        if (j < npw) s_G[t][16 * (p0 + j) + r] = fmaf(ecs, y2[j][e], y1[j][e]);
     }
     __syncthreads();
     {
       const int nv = np * 4;
       const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
-      for (int k = 0; k < kVecX; ++k) {
-        const int v = tid + k * kThreads;
+      for (int k = 0; k < VX; ++k) {
+        const int v = tid + k * TPB;
         if (v >= Q * nv) continue;
         const int t = tile_row(v, inv);
         if (t >= nvalid) continue;
@@ -937,8 +944,8 @@ hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
                     static_cast<unsigned>(p.batch));
   hipLaunchKernelGGL(ssd_state_pass_kernel, slices, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError()) return e;
-  if (p.z) hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
+  else hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);
   return hipGetLastError();
 }
 
