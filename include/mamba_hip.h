@@ -343,6 +343,13 @@ typedef struct mcpu_ssd_args {
   void* dz;                     /* like x; required iff z != NULL */
   float* ddt_bias;              /* (nheads); required iff dt_bias != NULL */
   float* dinitial_states;       /* required iff initial_states != NULL */
+  /* Heads one workgroup of the chunk kernels walks through: 0 = chosen by
+     the library from the shape (the production setting); otherwise a divisor
+     of nheads / ngroups, at most 8, which pins it, so tests can cover every
+     head-block size on small shapes. The backward's workspace size query
+     must see the same value as the call. */
+  int32_t head_block;
+  int32_t _pad;
 } mcpu_ssd_args;
 
 /* Bytes of the buffer the forward fills for the backward (0 for an empty

@@ -31,6 +31,10 @@ int check_ssd(const mcpu_ssd_args* a) {
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "ssd: bad dtype %d", a->dtype);
   if (!(a->dt_limit_lo <= a->dt_limit_hi))
     return fail(MCPU_ERR_INVALID, "ssd: dt_limit must be an interval (lo <= hi)");
+  if (a->head_block != 0 &&
+      (a->head_block < 1 || a->head_block > kSsdMaxHeadBlock || (a->nheads / a->ngroups) % a->head_block != 0))
+    return fail(MCPU_ERR_INVALID, "ssd: head_block %d must be 0 or a divisor of nheads / ngroups up to %d",
+                a->head_block, kSsdMaxHeadBlock);
   const int64_t nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
   if (nchunks > 0x7fffffffll || a->nheads > 65535 || a->batch > 65535)
     return fail(MCPU_ERR_UNSUPPORTED, "ssd: grid too large");
@@ -74,7 +78,7 @@ SsdParams make_ssd(const mcpu_ssd_args* a) {
   p.dstate = a->dstate;
   p.nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
   p.nslices = (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
-  p.hb = head_block(a);
+  p.hb = a->head_block != 0 ? a->head_block : head_block(a);
   p.nhb = static_cast<int>(a->nheads / p.hb);
   p.softplus = a->dt_softplus != 0;
   p.clamp = (a->dt_limit_lo > 0.f || !std::isinf(a->dt_limit_hi)) ? 1 : 0;

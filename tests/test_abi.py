@@ -459,7 +459,9 @@ def test_ssd_rejects_bad_arguments_before_touching_a_device():
                            (dict(dstate=136), _C.MCPU_ERR_UNSUPPORTED, "dstate"),
                            (dict(ngroups=3), _C.MCPU_ERR_INVALID, "ngroups"),
                            (dict(dtype=7), _C.MCPU_ERR_INVALID, "dtype"),
-                           (dict(dt_limit_lo=1.0, dt_limit_hi=0.5), _C.MCPU_ERR_INVALID, "dt_limit")):
+                           (dict(dt_limit_lo=1.0, dt_limit_hi=0.5), _C.MCPU_ERR_INVALID, "dt_limit"),
+                           (dict(head_block=3), _C.MCPU_ERR_INVALID, "head_block"),
+                           (dict(head_block=16), _C.MCPU_ERR_INVALID, "head_block")):
         rc, msg = fwd(_ssd_args(**kw))
         assert rc == code and word in msg, (kw, rc, msg)
     # a saved buffer is needed once there are steps; an empty sequence needs none
@@ -487,6 +489,10 @@ def test_ssd_sizes_follow_the_layout():
         want = 3 * al(4 * b * h * nch * 64) + al(4 * b * nch * h * p * n)
         assert L.mcpu_ssd_saved_size(ctypes.byref(a)) == want == _saved_bytes(b, l, h, p, n)
         assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(a)) >= 4 * b * nch * h * p * n
+    # dB/dC partials are per head block: pinning 2 heads per block halves them
+    one = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(head_block=1)))
+    two = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(head_block=2)))
+    assert one - two == 2 * (al(4 * 2 * 100 * 4 * 64) - al(4 * 2 * 100 * 2 * 64))
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(seqlen=0))) == 0
     assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(batch=0))) == 0
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(headdim=24))) == 0

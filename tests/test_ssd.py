@@ -5,8 +5,9 @@ Cases: sequence lengths that are and are not multiples of the 64-step chunk
 (one chunk, several, a ragged tail, 2048 steps), headdim 16-64, dstate
 16-128, 1, 2 or 4 groups, D per head or per channel, with and without z,
 dt_bias, softplus, a dt_limit clamp, initial states and final states;
-float32, bfloat16 and float16 storage; every gradient; opcheck of the two
-operators; an empty sequence.
+float32, bfloat16 and float16 storage; every gradient; workgroups walking
+1, 2, 4 or 8 heads of a group; opcheck of the two operators; an empty
+sequence.
 Tolerances (unscaled, |got - want| <= atol + rtol |want|): float32 outputs
 and final states rtol 1e-4 / atol 1e-5; float32 gradients rtol 1e-3 with
 atol 1e-4 for per-element gradients (dx, ddt, dz) and 1e-3 for sums (dA,
@@ -159,6 +160,56 @@ def test_rejects_unsupported_shapes_and_options():
     with pytest.raises(ValueError):
         mamba_cpu.mamba_chunk_scan_combined(**{k: None if v is None else v.cpu() for k, v in dev.items()},
                                             chunk_size=64)
+
+
+def run_ops(c, head_block, softplus=True, limit=(0.0, float("inf")), seed=1):
+    """Forward and backward through the operators with the chunk kernels'
+    head block pinned: out, final states, the nine gradients of
+    sum(out W) + sum(final V), and W, V."""
+    d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
+            softplus, float(limit[0]), float(limit[1]))
+    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, head_block)
+    gen = torch.Generator().manual_seed(seed)
+    W = torch.randn(out.shape, generator=gen).to(out.dtype)
+    V = torch.randn(fin.shape, generator=gen)
+    g = torch.ops.mamba_cpu.ssd_bwd(W.to(DEV), V.to(DEV), *args, saved, ysave, head_block)
+    torch.cuda.synchronize()
+    return out, fin, g, W, V
+
+
+@pytest.mark.parametrize("shape,blocks", [
+    ((2, 130, 8, 32, 1, 64), (1, 2, 4, 8)),
+    ((1, 200, 8, 16, 2, 32), (2, 4)),
+    ((3, 70, 4, 64, 1, 128), (2, 4)),
+], ids=["h8g1", "h8g2", "h4n128"])
+def test_head_blocks_match_oracle(shape, blocks):
+    """Workgroups walking 2, 4 or 8 heads of a group (C B^T shared, dB/dC
+    summed over the block's heads in the accumulators, partials per head
+    block): every head-block size against the oracle, and the forward
+    bitwise equal across sizes (each head's arithmetic is the same)."""
+    c = case(*shape, seed=sum(shape) + 1, init=True)
+    want = S.ssd_fwd(**c, dt_softplus=True)
+    first = None
+    for hb in blocks:
+        out, fin, g, W, V = run_ops(c, hb)
+        print(f" head_block {hb}")
+        assert_close_report(out, want[0], 1e-4, 1e-5, "out")
+        assert_close_report(fin, want[1], 1e-4, 1e-5, "final_states")
+        wg = S.ssd_bwd(**c, dt_softplus=True, dout=W.float(), dfinal_states=V)
+        for name, got, w in zip(NAMES, g, wg):
+            tol = (1e-3, 1e-4) if name in ("x", "dt", "z") else (1e-3, 1e-3)
+            assert_close_report(got, w, *tol, f"d{name}")
+        if first is None:
+            first = (out, fin)
+        else:
+            assert torch.equal(out, first[0]) and torch.equal(fin, first[1])
+
+
+def test_head_block_must_divide_the_group():
+    c = case(1, 64, 6, 16, 2, 16)
+    with pytest.raises(ValueError, match="head_block"):
+        run_ops(c, 2)   # 3 heads per group
 
 
 def test_opcheck_ssd_ops():
