@@ -349,7 +349,14 @@ typedef struct mcpu_ssd_args {
      head-block size on small shapes. The backward's workspace size query
      must see the same value as the call. */
   int32_t head_block;
-  int32_t _pad;
+  /* How the chunk states are carried from chunk to chunk: 0 = chosen by the
+     library from the shape (the production setting); 1 = chunk-end states
+     computed for every chunk at once, then passed on in a second launch;
+     2 = one launch per (batch, head, 64-state column block) that walks the
+     chunks in order and never stores the chunk-end states. Both give the
+     same result up to float32 rounding; pinning one lets tests cover both.
+     The size queries must see the same value as the calls. */
+  int32_t chunk_pass;
 } mcpu_ssd_args;
 
 /* Bytes of the buffer the forward fills for the backward (0 for an empty

@@ -35,6 +35,8 @@ int check_ssd(const mcpu_ssd_args* a) {
       (a->head_block < 1 || a->head_block > kSsdMaxHeadBlock || (a->nheads / a->ngroups) % a->head_block != 0))
     return fail(MCPU_ERR_INVALID, "ssd: head_block %d must be 0 or a divisor of nheads / ngroups up to %d",
                 a->head_block, kSsdMaxHeadBlock);
+  if (a->chunk_pass < 0 || a->chunk_pass > 2)
+    return fail(MCPU_ERR_INVALID, "ssd: chunk_pass %d must be 0, 1 or 2", a->chunk_pass);
   const int64_t nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
   if (nchunks > 0x7fffffffll || a->nheads > 65535 || a->batch > 65535)
     return fail(MCPU_ERR_UNSUPPORTED, "ssd: grid too large");
@@ -58,6 +60,16 @@ int head_block(const mcpu_ssd_args* a) {
   return hb;
 }
 
+// Whether the chunk states are carried by the in-order kernels: they run one
+// workgroup per (batch, head, 64-state column block) through every chunk, so
+// they need at least 512 of those (two per CU) to fill the GPU; below that the
+// two-launch form, parallel over chunks, is used.
+bool in_order(const mcpu_ssd_args* a) {
+  if (a->chunk_pass != 0) return a->chunk_pass == 2;
+  const int64_t cols = (a->dstate + kSsdPassCols - 1) / kSsdPassCols;
+  return a->batch * a->nheads * cols >= 512;
+}
+
 SsdParams make_ssd(const mcpu_ssd_args* a) {
   SsdParams p;
   std::memset(&p, 0, sizeof(p));
@@ -77,7 +89,9 @@ SsdParams make_ssd(const mcpu_ssd_args* a) {
   p.ngroups = a->ngroups;
   p.dstate = a->dstate;
   p.nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
-  p.nslices = (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
+  p.in_order = in_order(a) ? 1 : 0;
+  p.nslices = p.in_order ? (a->dstate + kSsdPassCols - 1) / kSsdPassCols
+                         : (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
   p.hb = a->head_block != 0 ? a->head_block : head_block(a);
   p.nhb = static_cast<int>(a->nheads / p.hb);
   p.softplus = a->dt_softplus != 0;

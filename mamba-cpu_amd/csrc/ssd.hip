@@ -104,17 +104,25 @@ __device__ __forceinline__ void zero(v4f (&acc)[NT]) {
 
 // ---- four consecutive storage elements <-> float4 (16-byte aligned float32,
 // 8-byte aligned 16-bit types) ----
-template <typename Tx> __device__ __forceinline__ float4 ld4(const Tx* p);
-template <> __device__ __forceinline__ float4 ld4<float>(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
+// As loaded: float4 for float32, the raw 16-bit pairs otherwise. Prefetched
+// tiles stay raw in registers and are widened where they are parked in LDS:
+// widening next to the load would make the wave wait for the load there.
+template <typename Tx> struct Raw4 { using type = uint2; };
+template <> struct Raw4<float> { using type = float4; };
+template <typename Tx> using raw4 = typename Raw4<Tx>::type;
+
+template <typename Tx> __device__ __forceinline__ raw4<Tx> ld_raw(const Tx* p) {
+  return *reinterpret_cast<const raw4<Tx>*>(p);
 }
-template <> __device__ __forceinline__ float4 ld4<bf16>(const bf16* p) {
-  const uint2 u = *reinterpret_cast<const uint2*>(p);
+template <typename Tx> __device__ __forceinline__ raw4<Tx> raw_zero() { return make_uint2(0u, 0u); }
+template <> __device__ __forceinline__ float4 raw_zero<float>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+template <typename Tx> __device__ __forceinline__ float4 widen(raw4<Tx> u);
+template <> __device__ __forceinline__ float4 widen<float>(float4 u) { return u; }
+template <> __device__ __forceinline__ float4 widen<bf16>(uint2 u) {
   return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
                      __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
 }
-template <> __device__ __forceinline__ float4 ld4<f16>(const f16* p) {
-  const uint2 u = *reinterpret_cast<const uint2*>(p);
+template <> __device__ __forceinline__ float4 widen<f16>(uint2 u) {
   auto h = [](uint32_t bits) { return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits))); };
   return make_float4(h(u.x & 0xffff), h(u.x >> 16), h(u.y & 0xffff), h(u.y >> 16));
 }
@@ -150,29 +158,29 @@ constexpr int kVecN = vec_n();
 constexpr int kVecX = vec_x();
 
 // Registers x = rows r < nrows, columns c < ncols (multiple of 4) of
-// src[r rs + c], four elements per float4, rows from nvalid on zero; thread
-// tid holds float4 number tid + k TPB of the row-major tile. The loads are
+// src[r rs + c], four elements per entry, rows from nvalid on zero; thread
+// tid holds entry number tid + k TPB of the row-major tile. The loads are
 // issued here and waited for where the registers are used.
 template <typename Tx, int V, int TPB = kThreads>
-__device__ __forceinline__ void tile_load(float4 (&x)[V], const Tx* src, int64_t rs, int nrows, int nvalid,
+__device__ __forceinline__ void tile_load(raw4<Tx> (&x)[V], const Tx* src, int64_t rs, int nrows, int nvalid,
                                           int ncols) {
   const int nv = ncols >> 2, total = nrows * nv;
   const float inv = 1.0f / static_cast<float>(nv);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     const int v = threadIdx.x + k * TPB;
-    x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    x[k] = raw_zero<Tx>();
     if (v < total) {
       const int r = tile_row(v, inv);
-      if (r < nvalid) x[k] = ld4<Tx>(src + r * rs + ((v - r * nv) << 2));
+      if (r < nvalid) x[k] = ld_raw<Tx>(src + r * rs + ((v - r * nv) << 2));
     }
   }
 }
 
 // LDS tile s (rows of ld floats) from registers filled by tile_load with the
-// same nrows / ncols, times scale[r] when given.
-template <int V, int TPB = kThreads>
-__device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V], int nrows, int ncols,
+// same nrows / ncols, widened to float32, times scale[r] when given.
+template <typename Tx, int V, int TPB = kThreads>
+__device__ __forceinline__ void tile_store(float* s, int ld, const raw4<Tx> (&x)[V], int nrows, int ncols,
                                            const float* scale = nullptr) {
   const int nv = ncols >> 2, total = nrows * nv;
   const float inv = 1.0f / static_cast<float>(nv);
@@ -182,7 +190,24 @@ __device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V
     if (v < total) {
       const int r = tile_row(v, inv);
       const int c = (v - r * nv) << 2;
-      *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(x[k], scale[r]) : x[k];
+      const float4 f = widen<Tx>(x[k]);
+      *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(f, scale[r]) : f;
+    }
+  }
+}
+
+// The same with entry k times sc[k].
+template <typename Tx, int V, int TPB = kThreads>
+__device__ __forceinline__ void tile_store_scaled(float* s, int ld, const raw4<Tx> (&x)[V], int nrows, int ncols,
+                                                  const float (&sc)[V]) {
+  const int nv = ncols >> 2, total = nrows * nv;
+  const float inv = 1.0f / static_cast<float>(nv);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int v = threadIdx.x + k * TPB;
+    if (v < total) {
+      const int r = tile_row(v, inv);
+      *reinterpret_cast<float4*>(s + r * ld + ((v - r * nv) << 2)) = scale4(widen<Tx>(x[k]), sc[k]);
     }
   }
 }
@@ -191,9 +216,9 @@ __device__ __forceinline__ void tile_store(float* s, int ld, const float4 (&x)[V
 template <typename Tx, int V, int TPB = kThreads>
 __device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t rs, int nrows, int nvalid, int ncols,
                                       const float* scale = nullptr) {
-  float4 x[V];
+  raw4<Tx> x[V];
   tile_load<Tx, V, TPB>(x, src, rs, nrows, nvalid, ncols);
-  tile_store<V, TPB>(s, ld, x, nrows, ncols, scale);
+  tile_store<Tx, V, TPB>(s, ld, x, nrows, ncols, scale);
 }
 
 // The dout, z and ysave tiles of one head's chunk (x layout from `off`, z and
@@ -201,7 +226,7 @@ __device__ __forceinline__ void stage(float* s, int ld, const Tx* src, int64_t r
 template <typename Tx, bool HAS_Z, int TPB = kThreads>
 struct DyTiles {
   static constexpr int V = vec_x<TPB>();
-  float4 go[V], zz[V], yy[V];
+  raw4<Tx> go[V], zz[V], yy[V];
 
   __device__ __forceinline__ void load(const SsdParams& p, int64_t off, int64_t rs, int nvalid, int ncols,
                                        bool want_y) {
@@ -224,23 +249,47 @@ struct DyTiles {
       if (v >= total) continue;
       const int r = tile_row(v, inv);
       const int c = (v - r * nv) << 2;
-      float4 dy = go[k];
-      if (HAS_Z) {
-        const float gx[4] = {go[k].x, go[k].y, go[k].z, go[k].w}, zx[4] = {zz[k].x, zz[k].y, zz[k].z, zz[k].w};
-        const float yv[4] = {yy[k].x, yy[k].y, yy[k].z, yy[k].w};
-        float d[4], dzv[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float sg = sigmoid(zx[u]);
-          d[u] = gx[u] * zx[u] * sg;
-          dzv[u] = gx[u] * yv[u] * sg * (1.f + zx[u] * (1.f - sg));
-        }
-        if (write_dz && r < nvalid)
-          st4<Tx>(static_cast<Tx*>(p.dz) + off + r * rs + c, make_float4(dzv[0], dzv[1], dzv[2], dzv[3]));
-        dy = make_float4(d[0], d[1], d[2], d[3]);
-      }
+      float4 dz = make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 dy = dy_of(k, write_dz ? &dz : nullptr);
+      if (HAS_Z && write_dz && r < nvalid) st4<Tx>(static_cast<Tx*>(p.dz) + off + r * rs + c, dz);
       *reinterpret_cast<float4*>(s + r * ld + c) = scale ? scale4(dy, scale[r]) : dy;
     }
+  }
+
+  // The same LDS tile (no dz) with float4 number k scaled by sc[k].
+  __device__ __forceinline__ void store_scaled(float* s, int ld, int ncols, const float (&sc)[V]) const {
+    const int nv = ncols >> 2, total = Q * nv;
+    const float inv = 1.0f / static_cast<float>(nv);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const int v = threadIdx.x + k * TPB;
+      if (v >= total) continue;
+      const int r = tile_row(v, inv);
+      *reinterpret_cast<float4*>(s + r * ld + ((v - r * nv) << 2)) = scale4(dy_of(k, nullptr), sc[k]);
+    }
+  }
+
+  // dY of float4 number k, and dz into *dzp when given (HAS_Z).
+  __device__ __forceinline__ float4 dy_of(int k, float4* dzp) const {
+    const float4 g4 = widen<Tx>(go[k]);
+    if (!HAS_Z) return g4;
+    const float4 z4 = widen<Tx>(zz[k]);
+    const float gx[4] = {g4.x, g4.y, g4.z, g4.w}, zx[4] = {z4.x, z4.y, z4.z, z4.w};
+    float d[4], sg[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sg[u] = sigmoid(zx[u]);
+      d[u] = gx[u] * zx[u] * sg[u];
+    }
+    if (dzp) {
+      const float4 y4 = widen<Tx>(yy[k]);
+      const float yv[4] = {y4.x, y4.y, y4.z, y4.w};
+      float dzv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dzv[u] = gx[u] * yv[u] * sg[u] * (1.f + zx[u] * (1.f - sg[u]));
+      *dzp = make_float4(dzv[0], dzv[1], dzv[2], dzv[3]);
+    }
+    return make_float4(d[0], d[1], d[2], d[3]);
   }
 };
 
@@ -288,14 +337,9 @@ __device__ __forceinline__ float wave_total(float v) {
   return swap_sum<16>(v, v);
 }
 
-// The effective step of (b, t, h) and, when grad, d(step)/d(raw dt): the
-// softplus derivative, zero where the clamp is active. 0 past the sequence.
-__device__ __forceinline__ float ssd_step(const SsdParams& p, int64_t b, int64_t t, int64_t h, float* grad) {
-  if (t >= p.seqlen) {
-    if (grad) *grad = 0.f;
-    return 0.f;
-  }
-  const float pre = p.dt[(b * p.seqlen + t) * p.nheads + h] + (p.dt_bias ? p.dt_bias[h] : 0.f);
+// The effective step for dt + dt_bias = pre and, when grad, d(step)/d(raw
+// dt): the softplus derivative, zero where the clamp is active.
+__device__ __forceinline__ float step_of(const SsdParams& p, float pre, float* grad) {
   float sg = 1.f;
   float st = pre;
   if (p.softplus) st = softplus_sigmoid(pre, sg);
@@ -306,6 +350,14 @@ __device__ __forceinline__ float ssd_step(const SsdParams& p, int64_t b, int64_t
   }
   if (grad) *grad = sg;
   return st;
+}
+// The same for (b, t, h); 0 past the sequence.
+__device__ __forceinline__ float ssd_step(const SsdParams& p, int64_t b, int64_t t, int64_t h, float* grad) {
+  if (t >= p.seqlen) {
+    if (grad) *grad = 0.f;
+    return 0.f;
+  }
+  return step_of(p, p.dt[(b * p.seqlen + t) * p.nheads + h] + (p.dt_bias ? p.dt_bias[h] : 0.f), grad);
 }
 
 // Chunk row (b, h, c) of the cs / step arrays.
@@ -403,6 +455,111 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParam
   if (p.final_states) p.final_states[(b * H + h) * PN + e] = run;
 }
 
+// Row scales of the float4 numbers a thread holds of a (64 x ncols) tile
+// (tile_load's mapping): v[row] from the wave lane that owns the row.
+template <int V>
+__device__ __forceinline__ void row_scales(float (&sc)[V], float v, int ncols) {
+  const int nv = ncols >> 2;
+  const float inv = 1.0f / static_cast<float>(nv);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int r = tile_row(static_cast<int>(threadIdx.x) + k * kThreads, inv);
+    sc[k] = __shfl(v, r < Q ? r : Q - 1, 64);
+  }
+}
+
+// F1 and F2 in one launch: the workgroup of (b, h, column block) walks the
+// chunks in order, holding state columns [64 x, 64 x + 64) of every row in
+// matrix-core accumulators. Per chunk c it stores H_c (the state entering c)
+// and forms H_{c+1} = exp(cs_L) H_c + sum_s exp(cs_L - cs_s) dt_s x_s B_s^T by
+// starting the products from the scaled H_c, so chunk-end states never reach
+// memory. Column block 0 also saves the chunk's steps and running decays.
+// The next chunk's x, B and dt load while the current chunk's products run.
+// Grid (column blocks, nheads, batch); wave w owns state rows [16 w, 16 w + 16).
+// Three waves per SIMD, as the backward's.
+template <typename Tx>
+__global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdParams p) {
+  constexpr int VX = vec_x();
+  constexpr int VB = Q * kSsdPassCols / 4 / kThreads;
+  constexpr int BP = kSsdPassCols + 4;
+  __shared__ __align__(16) float s_x[Q][XP];    // dt_s exp(cs_L - cs_s) x_s
+  __shared__ __align__(16) float s_B[Q][BP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kSsdPassCols;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t g = h / (H / G);
+  const int ncol = static_cast<int>(N - n0 < kSsdPassCols ? N - n0 : kSsdPassCols);
+  const int nt = ncol >> 4;
+  const bool act = 16 * wave < P;
+  const float Ah = p.A[h];
+  const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
+  // Accumulator element (j, e) of this lane: state row 16 wave + 4 q + e,
+  // column n0 + 16 j + r, at offset eo + e N + 16 j of a (headdim x dstate) block.
+  const int64_t eo = (16 * wave + 4 * q) * N + n0 + r;
+  v4f acc[kSsdPassCols / 16];
+#pragma unroll
+  for (int j = 0; j < kSsdPassCols / 16; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      acc[j][e] = (act && j < nt && p.init) ? p.init[(b * H + h) * P * N + eo + e * N + 16 * j] : 0.f;
+
+  const Tx* xh = static_cast<const Tx*>(p.x) + b * L * H * P + h * P;
+  const Tx* Bg = static_cast<const Tx*>(p.B) + b * L * G * N + g * N + n0;
+  raw4<Tx> nx[VX], nB[VB];
+  float ndt = 0.f;
+  auto fetch = [&](int64_t c) {
+    const int64_t t0 = c * Q;
+    const int nv = chunk_steps(p, t0);
+    tile_load<Tx, VX>(nx, xh + t0 * H * P, H * P, Q, nv, static_cast<int>(P));
+    tile_load<Tx, VB>(nB, Bg + t0 * G * N, G * N, Q, nv, ncol);
+    ndt = lane < nv ? p.dt[(b * L + t0 + lane) * H + h] : 0.f;
+  };
+  fetch(0);
+  for (int64_t c = 0; c < p.nchunks; ++c) {
+    const bool tv = c * Q + lane < L;
+    const float st = tv ? step_of(p, ndt + bias, nullptr) : 0.f;
+    float cs, csl;
+    wave_prefix_sum2(st * Ah, cs, csl);
+    const float csL = __shfl(cs, Q - 1, 64), cslL = __shfl(csl, Q - 1, 64);
+    const float decay = fast_exp(csL + cslL);
+    if (blockIdx.x == 0 && wave == 0) {
+      const int64_t row = chunk_row(p, b, h, c);
+      p.cs[row + lane] = cs;
+      p.cs_lo[row + lane] = csl;
+      p.step[row + lane] = st;
+    }
+    float sc[VX];
+    row_scales(sc, st * fast_exp((csL - cs) + (cslL - csl)), static_cast<int>(P));
+    __syncthreads();  // the previous chunk's products are done with s_x and s_B
+    tile_store_scaled<Tx, VX>(&s_x[0][0], XP, nx, Q, static_cast<int>(P), sc);
+    tile_store<Tx, VB>(&s_B[0][0], BP, nB, Q, ncol);
+    if (c + 1 < p.nchunks) fetch(c + 1);
+    __syncthreads();
+    if (act) {
+      float* dst = p.states + state_block(p, b, c, h) + eo;
+#pragma unroll
+      for (int j = 0; j < kSsdPassCols / 16; ++j)
+        if (j < nt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dst[e * N + 16 * j] = acc[j][e];
+            acc[j][e] *= decay;
+          }
+      mma(acc, nt, &s_x[0][16 * wave], 1, XP, &s_B[0][0], BP, 1, Q);
+    }
+  }
+  if (p.final_states && act) {
+    float* dst = p.final_states + (b * H + h) * P * N + eo;
+#pragma unroll
+    for (int j = 0; j < kSsdPassCols / 16; ++j)
+      if (j < nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e * N + 16 * j] = acc[j][e];
+  }
+}
+
 // F3: the chunk's outputs, Y = (C B^T o M) (dt x) + diag(exp(cs)) C H^T + D x,
 // out = Y silu(z) (and Y itself into ysave when the backward needs it).
 // Grid (nchunks, nhb, batch), 8 waves: wave w computes rows t in
@@ -441,7 +598,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
   mma(cb, 2, &s_C[16 * ws][0], NP, 1, &s_BH[32 * hf][0], 1, NP, static_cast<int>(N));
   // The next head's x tile, entering state and decays load into registers
   // while this head's products run.
-  float4 rx[VX], rh[VN], zc[VX];
+  raw4<Tx> rx[VX], zc[VX];
+  float4 rh[VN];
   float rcs = 0.f, rcsl = 0.f, rdt = 0.f;
   auto fetch = [&](int64_t h) {
     const int64_t row = chunk_row(p, b, h, c);
@@ -465,8 +623,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
       s_csl[tid] = rcsl;
       s_dt[tid] = rdt;
     }
-    tile_store<VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
-    tile_store<VN, TPB>(&s_BH[0][0], NP, rh, static_cast<int>(P), static_cast<int>(N));
+    tile_store<Tx, VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    tile_store<float, VN, TPB>(&s_BH[0][0], NP, rh, static_cast<int>(P), static_cast<int>(N));
     __syncthreads();
     if (HAS_Z)
       tile_load<Tx, VX, TPB>(zc, static_cast<const Tx*>(p.z) + xoff, H * P, Q, nvalid, static_cast<int>(P));
@@ -516,7 +674,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
         }
         if (HAS_Z) {
           if (p.ysave) st4<Tx>(static_cast<Tx*>(p.ysave) + at, make_float4(y[0], y[1], y[2], y[3]));
-          const float zx[4] = {zc[k].x, zc[k].y, zc[k].z, zc[k].w};
+          const float4 z4 = widen<Tx>(zc[k]);
+          const float zx[4] = {z4.x, z4.y, z4.z, z4.w};
 #pragma unroll
           for (int u = 0; u < 4; ++u) y[u] *= zx[u] * sigmoid(zx[u]);
         }
@@ -611,6 +770,110 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams 
   if (ok && p.dinit) p.dinit[(b * H + h) * PN + e] = run;
 }
 
+// K1 and K2 in one launch: the workgroup of (b, h, column block) walks the
+// chunks from the last, holding columns [64 x, 64 x + 64) of dL/d(state
+// leaving the chunk) in matrix-core accumulators. Per chunk c it stores
+// dH^out_c, adds <dH^out_c, exp(cs_L) H_c> over its columns to dcsL (slice x),
+// and forms dH^in_c = exp(cs_L) dH^out_c + (diag(exp(cs)) C)^T dY by starting
+// the products from the scaled dH^out_c, so the seeds never reach memory.
+// What is left after chunk 0 is the initial state's gradient. The next
+// chunk's dout, z, C, running decays and H load while the current chunk's
+// products run. Grid (column blocks, nheads, batch); wave w owns rows
+// [16 w, 16 w + 16). Three waves per SIMD: 640 workgroups (the Mamba-2 2.7B
+// layer at batch 4) run in one round.
+template <typename Tx, bool HAS_Z>
+__global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const SsdParams p) {
+  constexpr int VB = Q * kSsdPassCols / 4 / kThreads;
+  constexpr int BP = kSsdPassCols + 4;
+  using Dy = DyTiles<Tx, HAS_Z>;
+  __shared__ __align__(16) float s_dY[Q][XP];   // exp(cs_t) dY[t][p]
+  __shared__ __align__(16) float s_C[Q][BP];
+  __shared__ float s_part[kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kSsdPassCols;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t g = h / (H / G);
+  const int ncol = static_cast<int>(N - n0 < kSsdPassCols ? N - n0 : kSsdPassCols);
+  const int nt = ncol >> 4;
+  const bool act = 16 * wave < P;
+  const int64_t eo = (16 * wave + 4 * q) * N + n0 + r;
+  v4f acc[kSsdPassCols / 16];
+#pragma unroll
+  for (int j = 0; j < kSsdPassCols / 16; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      acc[j][e] = (act && j < nt && p.dfinal) ? p.dfinal[(b * H + h) * P * N + eo + e * N + 16 * j] : 0.f;
+
+  const Tx* Cg = static_cast<const Tx*>(p.C) + b * L * G * N + g * N + n0;
+  Dy dyt;
+  raw4<Tx> nC[VB];
+  float ncs = 0.f, nlo = 0.f, nH[kSsdPassCols / 16][4];
+  auto fetch = [&](int64_t c) {
+    const int64_t t0 = c * Q;
+    const int nv = chunk_steps(p, t0);
+    dyt.load(p, ((b * L + t0) * H + h) * P, H * P, nv, static_cast<int>(P), false);
+    tile_load<Tx, VB>(nC, Cg + t0 * G * N, G * N, Q, nv, ncol);
+    const int64_t row = chunk_row(p, b, h, c);
+    ncs = p.cs[row + lane];
+    nlo = p.cs_lo[row + lane];
+    const float* hs = p.states + state_block(p, b, c, h) + eo;
+#pragma unroll
+    for (int j = 0; j < kSsdPassCols / 16; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nH[j][e] = (act && j < nt) ? hs[e * N + 16 * j] : 0.f;
+  };
+  float* dcsl = p.dcsL + (chunk_row(p, b, h, 0) / Q) * p.nslices + blockIdx.x;
+  int64_t pend = -1;        // chunk whose dcsL share awaits the cross-wave sum
+  float pend_decay = 0.f;
+  fetch(p.nchunks - 1);
+  for (int64_t c = p.nchunks - 1; c >= 0; --c) {
+    const float ecs = fast_exp(ncs + nlo);
+    const float decay = __shfl(ecs, Q - 1, 64);
+    // dH^out_c out, its share of dL/dcs_L, and the decayed carry, before the
+    // next chunk's H_c loads into the same registers.
+    float part = 0.f;
+    if (act) {
+      float* dst = p.dstates + state_block(p, b, c, h) + eo;
+#pragma unroll
+      for (int j = 0; j < kSsdPassCols / 16; ++j)
+        if (j < nt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dst[e * N + 16 * j] = acc[j][e];
+            part = fmaf(acc[j][e], nH[j][e], part);
+            acc[j][e] *= decay;
+          }
+    }
+    part = wave_total(part);
+    float sc[Dy::V];
+    row_scales(sc, ecs, static_cast<int>(P));
+    __syncthreads();  // the previous chunk's products are done with s_dY and s_C; its parts are in
+    if (pend >= 0 && tid == 0)
+      dcsl[pend * p.nslices] = pend_decay * ((s_part[0] + s_part[1]) + (s_part[2] + s_part[3]));
+    dyt.store_scaled(&s_dY[0][0], XP, static_cast<int>(P), sc);
+    tile_store<Tx, VB>(&s_C[0][0], BP, nC, Q, ncol);
+    if (c > 0) fetch(c - 1);
+    __syncthreads();
+    if (lane == 0) s_part[wave] = part;
+    pend = c;
+    pend_decay = decay;
+    if (act) mma(acc, nt, &s_dY[0][16 * wave], 1, XP, &s_C[0][0], BP, 1, Q);
+  }
+  __syncthreads();
+  if (pend >= 0 && tid == 0)
+    dcsl[pend * p.nslices] = pend_decay * ((s_part[0] + s_part[1]) + (s_part[2] + s_part[3]));
+  if (p.dinit && act) {
+    float* dst = p.dinit + (b * H + h) * P * N + eo;
+#pragma unroll
+    for (int j = 0; j < kSsdPassCols / 16; ++j)
+      if (j < nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e * N + 16 * j] = acc[j][e];
+  }
+}
+
 // K3: every gradient of a chunk, for each head of the block. Grid (nchunks,
 // nhb, batch), 8 waves: wave w owns rows [16 (w % 4), 16 (w % 4) + 16) of
 // every Q-row product and half h = w / 4 of its column tiles (Q columns:
@@ -671,7 +934,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
   }
   // The next head's x, dout, z and ysave tiles and decays load into
   // registers while this head's products run.
-  float4 rx[VX];
+  raw4<Tx> rx[VX];
   DyTiles<Tx, HAS_Z, TPB> rdy;
   float rcs = 0.f, rcsl = 0.f, rdt = 0.f, rcsL = 0.f, rcslL = 0.f;
   auto fetch = [&](int64_t h) {
@@ -701,7 +964,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
       s_w[tid] = fast_exp((rcsL - rcs) + (rcslL - rcsl));
       s_ecs[tid] = fast_exp(rcs + rcsl);
     }
-    tile_store<VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
+    tile_store<Tx, VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
     rdy.store(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
     __syncthreads();
     if (i + 1 < p.hb) fetch(h + 1);
@@ -938,11 +1201,15 @@ namespace {
 template <typename Tx>
 hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
   const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
-  hipLaunchKernelGGL(ssd_chunk_state_kernel<Tx>, chunks, dim3(kThreads), 0, st, p);
-  if (hipError_t e = hipGetLastError()) return e;
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
                     static_cast<unsigned>(p.batch));
-  hipLaunchKernelGGL(ssd_state_pass_kernel, slices, dim3(kThreads), 0, st, p);
+  if (p.in_order) {
+    hipLaunchKernelGGL(ssd_state_scan_kernel<Tx>, slices, dim3(kThreads), 0, st, p);
+  } else {
+    hipLaunchKernelGGL(ssd_chunk_state_kernel<Tx>, chunks, dim3(kThreads), 0, st, p);
+    if (hipError_t e = hipGetLastError()) return e;
+    hipLaunchKernelGGL(ssd_state_pass_kernel, slices, dim3(kThreads), 0, st, p);
+  }
   if (hipError_t e = hipGetLastError()) return e;
   if (p.z) hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
   else hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);
@@ -954,10 +1221,15 @@ hipError_t bwd_t(const SsdParams& p, hipStream_t st) {
   const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
                     static_cast<unsigned>(p.batch));
-  if (p.z) hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
-  if (hipError_t e = hipGetLastError()) return e;
-  hipLaunchKernelGGL(ssd_bwd_pass_kernel, slices, dim3(kThreads), 0, st, p);
+  if (p.in_order) {
+    if (p.z) hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, true>), slices, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, false>), slices, dim3(kThreads), 0, st, p);
+  } else {
+    if (p.z) hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+    if (hipError_t e = hipGetLastError()) return e;
+    hipLaunchKernelGGL(ssd_bwd_pass_kernel, slices, dim3(kThreads), 0, st, p);
+  }
   if (hipError_t e = hipGetLastError()) return e;
   if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
   else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);

@@ -12,6 +12,7 @@ constexpr int kSsdMaxP = 64;      // largest headdim
 constexpr int kSsdMaxN = 128;     // largest dstate
 constexpr int kSsdSlice = 256;    // state elements per workgroup of the chunk-passing kernels
 constexpr int kSsdMaxHeadBlock = 8;  // heads one workgroup of the chunk kernels walks through
+constexpr int kSsdPassCols = 64;  // state columns per workgroup of the in-order passing kernels
 
 // Layouts (all contiguous): x, z, out, ysave, dx, dz (batch, seqlen, nheads,
 // headdim) in the storage type; dt, ddt (batch, seqlen, nheads) float32;
@@ -52,11 +53,15 @@ struct SsdParams {
   float* dB_part;           // (batch, seqlen, nhb, dstate): dB summed over a head block
   float* dC_part;
   float* dcsL;              // (batch, nheads, nchunks, nslices): dL/dcs_last from the passing, per slice
+                            // (slices of kSsdSlice state elements, or of kSsdPassCols columns when
+                            // the passing walks the chunks in order)
   float* dA_part;           // (batch * nchunks, nheads)
   float* dbias_part;        // (batch * nchunks, nheads)
   float* dD_part;           // (batch * nchunks, nheads, headdim)
   int64_t batch, seqlen, nheads, headdim, ngroups, dstate, nchunks, nslices;
   int hb, nhb;              // heads per block, blocks over the heads
+  int in_order;             // chunk states carried by the in-order kernels (one launch per
+                            // direction, no chunk-end states stored) instead of two launches
   int softplus;
   int clamp;                // the step is clamped to [dt_lo, dt_hi]
   float dt_lo, dt_hi;

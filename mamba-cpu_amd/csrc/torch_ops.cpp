@@ -1080,7 +1080,7 @@ mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, cons
                        const Tensor& B, const Tensor& C, const optional<Tensor>& D,
                        const optional<Tensor>& z, const optional<Tensor>& dt_bias,
                        const optional<Tensor>& init, bool softplus, double lo, double hi,
-                       int64_t head_block) {
+                       int64_t head_block, int64_t chunk_pass) {
   for (const optional<Tensor>& t : {opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias, init})
     check_gpu(name, t);
   TORCH_CHECK_VALUE(x.dim() == 4 && x_dtype(x.scalar_type()) && x.is_contiguous(), name,
@@ -1130,6 +1130,7 @@ mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, cons
   a.dt_limit_lo = static_cast<float>(lo);
   a.dt_limit_hi = static_cast<float>(hi);
   a.head_block = static_cast<int32_t>(head_block);
+  a.chunk_pass = static_cast<int32_t>(chunk_pass);
   return a;
 }
 
@@ -1137,9 +1138,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> ssd_fwd(const Tensor& x, const Tensor
                                                    const Tensor& B, const Tensor& C, const optional<Tensor>& D,
                                                    const optional<Tensor>& z, const optional<Tensor>& dt_bias,
                                                    const optional<Tensor>& init, bool softplus, double lo,
-                                                   double hi, bool save_for_backward, int64_t head_block) {
+                                                   double hi, bool save_for_backward, int64_t head_block,
+                                                   int64_t chunk_pass) {
   const char* name = "mamba_cpu::ssd_fwd";
-  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block);
+  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass);
   c10::DeviceGuard guard(x.device());
   Tensor out = at::empty(x.sizes(), x.options());
   Tensor fin = at::empty({a.batch, a.nheads, a.headdim, a.dstate}, x.options().dtype(at::kFloat));
@@ -1159,9 +1161,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tenso
     const Tensor& dout, const optional<Tensor>& dfinal, const Tensor& x, const Tensor& dt, const Tensor& A,
     const Tensor& B, const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
     const optional<Tensor>& dt_bias, const optional<Tensor>& init, bool softplus, double lo, double hi,
-    const Tensor& saved, const Tensor& ysave, int64_t head_block) {
+    const Tensor& saved, const Tensor& ysave, int64_t head_block, int64_t chunk_pass) {
   const char* name = "mamba_cpu::ssd_bwd";
-  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block);
+  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass);
   check_gpu(name, opt(dout));
   check_gpu(name, dfinal);
   TORCH_CHECK_VALUE(dout.sizes() == x.sizes() && dout.scalar_type() == x.scalar_type() && dout.is_contiguous(),
@@ -1324,10 +1326,10 @@ Tensor mixer_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_wei
 TORCH_LIBRARY(mamba_cpu, m) {
   m.def("ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
         "Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, float dt_hi, "
-        "bool save_for_backward, int head_block=0) -> (Tensor, Tensor, Tensor, Tensor)");
+        "bool save_for_backward, int head_block=0, int chunk_pass=0) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("ssd_bwd(Tensor dout, Tensor? dfinal_states, Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, "
         "Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, "
-        "float dt_hi, Tensor saved, Tensor ysave, int head_block=0) -> "
+        "float dt_hi, Tensor saved, Tensor ysave, int head_block=0, int chunk_pass=0) -> "
         "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("selective_scan_fwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
         "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor)");

@@ -48,7 +48,7 @@ def _saved_bytes(b, l, h, p, n):
 
 @torch.library.register_fake("mamba_cpu::ssd_fwd")
 def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, save_for_backward,
-      head_block=0):
+      head_block=0, chunk_pass=0):
     b, l, h, p = x.shape
     n = B.shape[-1]
     ysave = x.new_empty(x.shape) if (save_for_backward and z is not None) else x.new_empty(0)
@@ -58,7 +58,7 @@ def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, 
 
 @torch.library.register_fake("mamba_cpu::ssd_bwd")
 def _(dout, dfinal_states, x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi,
-      saved, ysave, head_block=0):
+      saved, ysave, head_block=0, chunk_pass=0):
     f32 = dict(dtype=torch.float32)
     return (x.new_empty(x.shape), dt.new_empty(dt.shape, **f32), A.new_empty(A.shape, **f32),
             B.new_empty(B.shape, **f32), C.new_empty(C.shape, **f32),

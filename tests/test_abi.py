@@ -461,7 +461,9 @@ def test_ssd_rejects_bad_arguments_before_touching_a_device():
                            (dict(dtype=7), _C.MCPU_ERR_INVALID, "dtype"),
                            (dict(dt_limit_lo=1.0, dt_limit_hi=0.5), _C.MCPU_ERR_INVALID, "dt_limit"),
                            (dict(head_block=3), _C.MCPU_ERR_INVALID, "head_block"),
-                           (dict(head_block=16), _C.MCPU_ERR_INVALID, "head_block")):
+                           (dict(head_block=16), _C.MCPU_ERR_INVALID, "head_block"),
+                           (dict(chunk_pass=3), _C.MCPU_ERR_INVALID, "chunk_pass"),
+                           (dict(chunk_pass=-1), _C.MCPU_ERR_INVALID, "chunk_pass")):
         rc, msg = fwd(_ssd_args(**kw))
         assert rc == code and word in msg, (kw, rc, msg)
     # a saved buffer is needed once there are steps; an empty sequence needs none
@@ -493,6 +495,13 @@ def test_ssd_sizes_follow_the_layout():
     one = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(head_block=1)))
     two = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(head_block=2)))
     assert one - two == 2 * (al(4 * 2 * 100 * 4 * 64) - al(4 * 2 * 100 * 2 * 64))
+    # dL/dcs_last shares per chunk: 8 slices of 256 state elements in the
+    # two-launch form, one column block of 64 states in the in-order one
+    sep = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(chunk_pass=1)))
+    ino = L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(chunk_pass=2)))
+    assert sep - ino == al(4 * 2 * 4 * 2 * 8) - al(4 * 2 * 4 * 2 * 1)
+    assert (L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(chunk_pass=1)))
+            == L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(chunk_pass=2))))
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(seqlen=0))) == 0
     assert L.mcpu_ssd_bwd_workspace_size(ctypes.byref(_ssd_args(batch=0))) == 0
     assert L.mcpu_ssd_saved_size(ctypes.byref(_ssd_args(headdim=24))) == 0

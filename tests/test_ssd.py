@@ -6,8 +6,8 @@ Cases: sequence lengths that are and are not multiples of the 64-step chunk
 16-128, 1, 2 or 4 groups, D per head or per channel, with and without z,
 dt_bias, softplus, a dt_limit clamp, initial states and final states;
 float32, bfloat16 and float16 storage; every gradient; workgroups walking
-1, 2, 4 or 8 heads of a group; opcheck of the two operators; an empty
-sequence.
+1, 2, 4 or 8 heads of a group; chunk states carried by two launches or by
+the in-order kernels; opcheck of the two operators; an empty sequence.
 Tolerances (unscaled, |got - want| <= atol + rtol |want|): float32 outputs
 and final states rtol 1e-4 / atol 1e-5; float32 gradients rtol 1e-3 with
 atol 1e-4 for per-element gradients (dx, ddt, dz) and 1e-3 for sums (dA,
@@ -162,18 +162,20 @@ def test_rejects_unsupported_shapes_and_options():
                                             chunk_size=64)
 
 
-def run_ops(c, head_block, softplus=True, limit=(0.0, float("inf")), seed=1):
+def run_ops(c, head_block=0, chunk_pass=0, softplus=True, limit=(0.0, float("inf")), seed=1):
     """Forward and backward through the operators with the chunk kernels'
-    head block pinned: out, final states, the nine gradients of
-    sum(out W) + sum(final V), and W, V."""
+    head block and the way chunk states are carried pinned: out, final
+    states, the nine gradients of sum(out W) + sum(final V), and W, V."""
     d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    if d["D"] is not None and d["D"].dim() == 1:   # the operator takes D per channel
+        d["D"] = d["D"][:, None].expand(d["x"].shape[2:]).contiguous()
     args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
             softplus, float(limit[0]), float(limit[1]))
-    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, head_block)
+    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, head_block, chunk_pass)
     gen = torch.Generator().manual_seed(seed)
     W = torch.randn(out.shape, generator=gen).to(out.dtype)
     V = torch.randn(fin.shape, generator=gen)
-    g = torch.ops.mamba_cpu.ssd_bwd(W.to(DEV), V.to(DEV), *args, saved, ysave, head_block)
+    g = torch.ops.mamba_cpu.ssd_bwd(W.to(DEV), V.to(DEV), *args, saved, ysave, head_block, chunk_pass)
     torch.cuda.synchronize()
     return out, fin, g, W, V
 
@@ -192,7 +194,7 @@ def test_head_blocks_match_oracle(shape, blocks):
     want = S.ssd_fwd(**c, dt_softplus=True)
     first = None
     for hb in blocks:
-        out, fin, g, W, V = run_ops(c, hb)
+        out, fin, g, W, V = run_ops(c, head_block=hb)
         print(f" head_block {hb}")
         assert_close_report(out, want[0], 1e-4, 1e-5, "out")
         assert_close_report(fin, want[1], 1e-4, 1e-5, "final_states")
@@ -206,15 +208,68 @@ def test_head_blocks_match_oracle(shape, blocks):
             assert torch.equal(out, first[0]) and torch.equal(fin, first[1])
 
 
+def check_ops(c, got, softplus=True, limit=(0.0, float("inf")), low=False):
+    out, fin, g, W, V = got
+    kw = dict(dt_softplus=softplus, dt_limit=limit)
+    want = S.ssd_fwd(**c, **kw)
+    tol = (2e-2, 2e-2) if low else (1e-4, 1e-5)
+    assert_close_report(out, want[0], *tol, "out")
+    assert_close_report(fin, want[1], *tol, "final_states")
+    wg = S.ssd_bwd(**c, **kw, dout=W.float(), dfinal_states=V)
+    for name, got_g, w in zip(NAMES, g, wg):
+        if c[name] is None:
+            continue
+        if name == "D" and c["D"].dim() == 1:   # per-channel dD back to the per-head D
+            got_g = got_g.sum(-1)
+        if low:
+            tol = (2e-2, 2e-2)
+        else:
+            tol = (1e-3, 1e-4) if name in ("x", "dt", "z") else (1e-3, 1e-3)
+        assert_close_report(got_g, w, *tol, f"d{name}")
+
+
+@pytest.mark.parametrize("shape,opts", [
+    ((2, 130, 4, 64, 1, 128), dict(init=True)),
+    ((1, 200, 8, 16, 4, 64), dict(z=False)),
+    ((3, 70, 4, 32, 2, 48), dict(init=True, D="h")),
+    ((1, 37, 2, 64, 2, 16), dict(bias=False)),
+    ((2, 300, 4, 48, 1, 32), dict(init=True, z=False, D=None)),
+], ids=["n128-init", "p16-noz", "n48-init", "n16-short", "p48-noD"])
+@pytest.mark.parametrize("chunk_pass", [1, 2], ids=["two-launch", "in-order"])
+def test_chunk_passes_match_oracle(shape, opts, chunk_pass):
+    """Chunk states carried by the two-launch form (chunk-end states for
+    every chunk, then a passing launch) and by the in-order kernels (one
+    workgroup per batch row, head and 64-state column block walking the
+    chunks, column blocks of 64, 48 and 16 states): forward, final states and
+    every gradient against the oracle, with and without initial states, z,
+    D and dt_bias."""
+    c = case(*shape, seed=sum(shape) + chunk_pass, **opts)
+    check_ops(c, run_ops(c, chunk_pass=chunk_pass))
+
+
+def test_chunk_passes_in_bf16_and_clamped():
+    c = case(2, 130, 8, 64, 2, 64, seed=5, init=True, dtype=torch.bfloat16)
+    for cp in (1, 2):
+        check_ops(c, run_ops(c, chunk_pass=cp, limit=(0.05, 2.0)), limit=(0.05, 2.0), low=True)
+
+
+def test_chunk_pass_must_be_known():
+    c = case(1, 64, 2, 16, 1, 16)
+    with pytest.raises(ValueError, match="chunk_pass"):
+        run_ops(c, chunk_pass=3)
+
+
 def test_head_block_must_divide_the_group():
     c = case(1, 64, 6, 16, 2, 16)
     with pytest.raises(ValueError, match="head_block"):
-        run_ops(c, 2)   # 3 heads per group
+        run_ops(c, head_block=2)   # 3 heads per group
 
 
 def test_opcheck_ssd_ops():
     c = case(1, 70, 2, 16, 1, 16, seed=6, init=True)
     d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    if d["D"] is not None and d["D"].dim() == 1:   # the operator takes D per channel
+        d["D"] = d["D"][:, None].expand(d["x"].shape[2:]).contiguous()
     args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
             True, 0.0, float("inf"), True)
     torch.library.opcheck(torch.ops.mamba_cpu.ssd_fwd.default, args)
