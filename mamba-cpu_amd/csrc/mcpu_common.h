@@ -69,6 +69,29 @@ template <> __device__ __forceinline__ float buf_ld<f16>(__amdgpu_buffer_rsrc_t 
   return to_f32(__builtin_bit_cast(f16, static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0))));
 }
 
+// The element's bits as a buffer load returns them (16-bit types in the low
+// half, zero-extended), and their float32 value. Prefetch registers hold the
+// bits and are widened where the value is consumed: widening next to the load
+// would make the wave wait for the load there.
+template <typename T> __device__ __forceinline__ uint32_t buf_ld_raw(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ uint32_t buf_ld_raw<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+template <> __device__ __forceinline__ uint32_t buf_ld_raw<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ uint32_t buf_ld_raw<f16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+template <typename T> __device__ __forceinline__ float raw_f32(uint32_t bits);
+template <> __device__ __forceinline__ float raw_f32<float>(uint32_t bits) { return __builtin_bit_cast(float, bits); }
+template <> __device__ __forceinline__ float raw_f32<bf16>(uint32_t bits) {
+  return __builtin_bit_cast(float, bits << 16);
+}
+template <> __device__ __forceinline__ float raw_f32<f16>(uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits)));
+}
+
 template <typename T> __device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v);
 template <> __device__ __forceinline__ void buf_st<float>(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);

@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     o_poff[q] = static_cast<uint32_t>(sizeof(float) * (tt * N + n));
   }
 
-  float nu = 0.f, nd = 0.f, no = 0.f, nz = 0.f, ny = 0.f;
+  uint32_t nu = 0u, nd = 0u, no = 0u, nz = 0u, ny = 0u;  // raw bits, widened at the park
   float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
   float nh0[SPL];
   // Checkpointed state lanes past dstate load lane 0's entry and read as 0.
@@ -185,11 +185,11 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     ck_base -= stay ? 0 : sizeof(float) * N;
   };
   auto park = [&](int buf) {
-    (&s_x[buf][0][0][0])[xu.slot] = nu;
-    (&s_x[buf][1][0][0])[xd.slot] = nd;
-    (&s_x[buf][2][0][0])[xo.slot] = has_dout ? no : 0.f;
-    if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = nz;
-    if (HAS_Y) (&s_x[buf][4][0][0])[xy.slot] = ny;
+    (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
+    (&s_x[buf][1][0][0])[xd.slot] = raw_f32<Tx>(nd);
+    (&s_x[buf][2][0][0])[xo.slot] = has_dout ? raw_f32<Tx>(no) : 0.f;
+    if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = raw_f32<Tx>(nz);
+    if (HAS_Y) (&s_x[buf][4][0][0])[xy.slot] = raw_f32<Tx>(ny);
     tb.park(s_B[buf], nB);
     tc.park(s_C[buf], nC);
   };
@@ -440,7 +440,8 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   BC tc;
   tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, t_last);
 
-  float nd = 0.f, no = 0.f, nz = 0.f, nC[BC::PER_THREAD];
+  uint32_t nd = 0u, no = 0u, nz = 0u;  // raw bits, widened at the park
+  float nC[BC::PER_THREAD];
   auto fetch = [&](auto GUARD, int64_t t0, bool stay) {
     if constexpr (decltype(GUARD)::value) {
       nd = xd.template load_guarded<Tx>(t0, L);
@@ -459,9 +460,9 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
     tc.advance_unless(-1, stay);
   };
   auto park = [&](int buf) {
-    (&s_x[buf][0][0][0])[xd.slot] = nd;
-    (&s_x[buf][1][0][0])[xo.slot] = has_dout ? no : 0.f;
-    if (HAS_Z) (&s_x[buf][2][0][0])[xz.slot] = nz;
+    (&s_x[buf][0][0][0])[xd.slot] = raw_f32<Tx>(nd);
+    (&s_x[buf][1][0][0])[xo.slot] = has_dout ? raw_f32<Tx>(no) : 0.f;
+    if (HAS_Z) (&s_x[buf][2][0][0])[xz.slot] = raw_f32<Tx>(nz);
     tc.park(s_C[buf], nC);
   };
 

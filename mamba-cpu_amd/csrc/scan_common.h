@@ -131,9 +131,11 @@ struct XStage {
     off = static_cast<uint32_t>(sz * (ce * s[1] + t * s[2]));
     step = static_cast<int32_t>(sz * kScanBlockT * s[2]);
   }
+  // The element's bits (buf_ld_raw); raw_f32<Tx> widens them where they are
+  // parked, after the block the prefetch runs under.
   template <typename Tx>
-  __device__ __forceinline__ float load() const {
-    return buf_ld<Tx>(wave_rsrc(base), off);
+  __device__ __forceinline__ uint32_t load() const {
+    return buf_ld_raw<Tx>(wave_rsrc(base), off);
   }
   // For a block that may extend past the sequence end: steps past the end
   // load the tile's first element (always in range) and read as 0. The load
@@ -141,10 +143,10 @@ struct XStage {
   // lane mask (which would make the compiler drain every outstanding memory
   // operation before reusing it).
   template <typename Tx>
-  __device__ __forceinline__ float load_guarded(int64_t t0, int64_t L) const {
+  __device__ __forceinline__ uint32_t load_guarded(int64_t t0, int64_t L) const {
     const bool ok = t0 + t < L;
-    const float x = buf_ld<Tx>(wave_rsrc(base), ok ? off : 0u);
-    return ok ? x : 0.f;
+    const uint32_t x = buf_ld_raw<Tx>(wave_rsrc(base), ok ? off : 0u);
+    return ok ? x : 0u;
   }
   __device__ __forceinline__ void advance(int dir) { base += dir * step; }
   // Moves one block in direction dir unless `stay` (uniform).

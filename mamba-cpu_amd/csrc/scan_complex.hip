@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
   }
   const int64_t t_full = L - L % T;
 
-  float nu = 0.f, nd = 0.f, nz = 0.f;
+  uint32_t nu = 0u, nd = 0u, nz = 0u;  // raw bits, widened at the park
   float nBr[BC::PER_THREAD], nBi[BC::PER_THREAD], nCr[BC::PER_THREAD], nCi[BC::PER_THREAD];
   // Loads the block at t0 and moves the cursors one block on, except from the
   // last block (`last`), which re-reads itself: no load is conditional.
@@ -133,9 +133,9 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
     }
   };
   auto park = [&](int buf) {
-    (&s_x[buf][0][0][0])[xu.slot] = nu;
-    (&s_x[buf][1][0][0])[xd.slot] = nd;
-    if (HAS_Z && WRITE_OUT) (&s_x[buf][2][0][0])[xz.slot] = nz;
+    (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
+    (&s_x[buf][1][0][0])[xd.slot] = raw_f32<Tx>(nd);
+    if (HAS_Z && WRITE_OUT) (&s_x[buf][2][0][0])[xz.slot] = raw_f32<Tx>(nz);
     tbr.park(s_B[buf][0], nBr);
     tbi.park(s_B[buf][1], nBi);
     if (WRITE_OUT) {
@@ -343,7 +343,7 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
     o_poff[q] = static_cast<uint32_t>(sizeof(float) * ((tt * N + n) * 2 + (arr & 1)));
   }
 
-  float nu = 0.f, nd = 0.f, no = 0.f, nz = 0.f;
+  uint32_t nu = 0u, nd = 0u, no = 0u, nz = 0u;  // raw bits, widened at the park
   float nBr[BC::PER_THREAD], nBi[BC::PER_THREAD], nCr[BC::PER_THREAD], nCi[BC::PER_THREAD];
   float nh0r[SPL], nh0i[SPL];
   // Loads the operands of the block at t0 (full unless GUARD) and moves every
@@ -385,10 +385,10 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
     ck_base -= stay ? 0 : sizeof(float) * N * 2;
   };
   auto park = [&](int buf) {
-    (&s_x[buf][0][0][0])[xu.slot] = nu;
-    (&s_x[buf][1][0][0])[xd.slot] = nd;
-    (&s_x[buf][2][0][0])[xo.slot] = has_dout ? no : 0.f;
-    if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = nz;
+    (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
+    (&s_x[buf][1][0][0])[xd.slot] = raw_f32<Tx>(nd);
+    (&s_x[buf][2][0][0])[xo.slot] = has_dout ? raw_f32<Tx>(no) : 0.f;
+    if (HAS_Z) (&s_x[buf][3][0][0])[xz.slot] = raw_f32<Tx>(nz);
     tbr.park(s_B[buf][0], nBr);
     tbi.park(s_B[buf][1], nBi);
     tcr.park(s_C[buf][0], nCr);

@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   const int64_t t_full = L - L % kScanBlockT;
 
   // Registers holding the next block's operands between fetch and park.
-  float nu = 0.f, nd = 0.f, nz = 0.f;
+  uint32_t nu = 0u, nd = 0u, nz = 0u;  // raw bits, widened at the park
   float nB[BC::PER_THREAD], nC[BC::PER_THREAD];
   // Loads the block at t0 and moves the cursors to the next block, except
   // from the chunk's last block (`last`), where they stay: the loop fetches
@@ -130,9 +130,9 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     if (WRITE_OUT) tc.advance_unless(1, last);
   };
   auto park = [&](int buf) {
-    (&s_x[buf][0][0][0])[xu.slot] = nu;
-    (&s_x[buf][1][0][0])[xd.slot] = nd;
-    if (HAS_Z && WRITE_OUT) (&s_x[buf][2][0][0])[xz.slot] = nz;
+    (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
+    (&s_x[buf][1][0][0])[xd.slot] = raw_f32<Tx>(nd);
+    if (HAS_Z && WRITE_OUT) (&s_x[buf][2][0][0])[xz.slot] = raw_f32<Tx>(nz);
     tb.park(s_B[buf], nB);
     if (WRITE_OUT) tc.park(s_C[buf], nC);
   };
