@@ -147,12 +147,13 @@ def cpu_baseline(inputs, gout, fwd_bytes, bwd_bytes, extra):
     }
 
 
-def valu_roofline(launch_ms, counters):
-    """The vector-ALU ceiling of the backward launch: the issue slots it
-    needs per launch (VALU wave-instructions from the committed counters,
-    plus one more slot per v_exp_f32, which issues at half rate) over the
-    launch time measured in this run, against VALU_PEAK_G. Also the slots per
-    (batch, channel, step, state) element. None without committed counters."""
+def valu_roofline(launch_ms, counters, elements=None, source=COUNTERS_JSON):
+    """The vector-ALU ceiling of a launch (or call): the issue slots it needs
+    (VALU wave-instructions from the committed counters, plus one more slot
+    per v_exp_f32, which issues at half rate) over the time measured in this
+    run, against VALU_PEAK_G. Also the instructions per (batch, channel, step,
+    state) element (`elements`, the training-step shape's by default). None
+    without committed counters."""
     slots = counters.get("valu_issue_slots_per_launch")
     if not slots:
         return None
@@ -165,11 +166,29 @@ def valu_roofline(launch_ms, counters):
         "unit": "G wave-instructions/s",
         "frac": round(rate / VALU_PEAK_G, 4),
         "per_state_step": round(counters.get("valu_wave_instructions_per_launch", 0) * 64
-                                / (B_ * D_ * L_ * N_), 2),
+                                / (elements or B_ * D_ * L_ * N_), 2),
         "note": "peak at the 2.4 GHz peak clock; the chip runs at about 2.1 GHz under this load, "
                 "so the attainable fraction is about 0.88",
-        "source": "profiles/" + COUNTERS_JSON,
+        "source": "profiles/" + source,
     }
+
+
+def _counters(name):
+    """A committed counter summary under profiles/ ({} when absent)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+def _bind_valu(r, ms, name, elements):
+    """Marks a scan workload VALU-bound, with its VALU ceiling from the
+    committed counters of that workload (name under profiles/)."""
+    v = valu_roofline(ms, _counters(name), elements, name)
+    if v is not None:
+        r["bound"] = "valu"
+        r["valu"] = v
 
 
 def _events_ms(torch, stream, fn, iters):
@@ -297,6 +316,7 @@ def other_configs(torch, dev, stream, cpu):
                           fwd_only=True)
         if cms is not None:
             _attach_cpu(r, cms, "the full workload on the reference's C++ kernels, 1 warm-up + 3 timed calls")
+    _bind_valu(r, ms, "scan_fwd_b1_d1536_l2048_n16_counters.json", b * d * l * n)
     res["scan_fwd_b1_d1536_l2048"] = r
     del u, delta, Bm, Cm
 
@@ -330,6 +350,7 @@ def other_configs(torch, dev, stream, cpu):
         if cms is not None:
             _attach_cpu(r, cms, "the full workload (fp32 copies of the bf16 inputs) on the reference's "
                                 "C++ kernels, 1 warm-up + 1 timed fwd+bwd")
+    _bind_valu(r, ms, "scan_fwd_bwd_b1_d5120_l16384_n16_bf16_counters.json", b * d * l * n)
     res["scan_fwdbwd_b1_d5120_l16384_bf16"] = r
     del leaves, gout
 
