@@ -1014,6 +1014,17 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
     v4f dxa[2];
     zero(dxa);
     mma(dxa, npw, &s_U[0][16 * ws], 1, QP, &s_dY[0][16 * p0], XP, 1, Q);
+    // dH^out and H of a 64-state group into registers, parked in s_U / s_V
+    // once the products reading them are done: group 0's load under the dC /
+    // dB products, group 1's under group 0's state products.
+    float4 su[VX], sv[VX];
+    auto load_states = [&](int grp) {
+      const int n0 = 64 * grp;
+      const int nw = static_cast<int>(N - n0 < 64 ? N - n0 : 64);
+      tile_load<float, VX, TPB>(su, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      tile_load<float, VX, TPB>(sv, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+    };
+    load_states(0);
     // dC[t][n] += sum_s dCB[t][s] B[s][n] ; dB[s][n] += sum_t dCB[t][s] C[t][n] (this wave's state tiles).
 #pragma unroll
     for (int grp = 0; grp < 2; ++grp) {
@@ -1033,9 +1044,10 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
       const int nw = static_cast<int>(N - n0 < 64 ? N - n0 : 64);
       const int nt = ntw(grp);
       __syncthreads();  // every wave is done reading s_U / s_V
-      stage<float, VX, TPB>(&s_U[0][0], QP, p.dstates + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
-      stage<float, VX, TPB>(&s_V[0][0], QP, p.states + sb + n0, N, static_cast<int>(P), static_cast<int>(P), nw);
+      tile_store<float, VX, TPB>(&s_U[0][0], QP, su, static_cast<int>(P), nw);
+      tile_store<float, VX, TPB>(&s_V[0][0], QP, sv, static_cast<int>(P), nw);
       __syncthreads();
+      if (n0 + 64 < N) load_states(grp + 1);
       v4f tv[2], yh[2];
       zero(tv);
       zero(yh);
