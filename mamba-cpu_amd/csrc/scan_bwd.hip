@@ -69,16 +69,9 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     // Carry the adjoint state over the summary units after this chunk:
     // through unit u it maps gh to exp(A * sum_dt[u]) * gh + sum_h[u]
     // (sum_h[u] = the adjoint at u's start from a zero adjoint at its end).
-    const float* sh = p.sum_h + row * p.nsum * N;
-    const float* sd = p.sum_dt + row * p.nsum;
-    for (int64_t c = p.nsum - 1; c >= (chunk + 1) * p.sum_per_chunk; --c) {
-      const float ds = sd[c];
-#pragma unroll
-      for (int s = 0; s < SPL; ++s) {
-        const int n = j + 16 * s;
-        if (n < N) gh[s] = fmaf(fast_exp2(A2[s] * ds), gh[s], sh[c * N + n]);
-      }
-    }
+    const int64_t last_unit = (chunk + 1) * p.sum_per_chunk;
+    fold_summaries<SPL>(gh, A2, p.sum_h + row * p.nsum * N, p.sum_dt + row * p.nsum, p.nsum - 1,
+                        p.nsum - last_unit, -1, j, N);
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;

@@ -228,6 +228,38 @@ struct PartialSum {
 };
 hipError_t partial_sums_launch(const PartialSum* sums, int n, hipStream_t stream);
 
+// Folds chunk summaries into a state, in order: for k = 0 .. count-1 and
+// c = first + dir * k, h <- exp2(A2 * sd[c]) h + sh[c * N + n] for each of
+// this lane's states n = j + 16 s < N. The summaries of a few chunks load
+// together and then fold in the same order (the same arithmetic as one chunk
+// at a time, without a memory round trip per chunk).
+template <int SPL>
+__device__ __forceinline__ void fold_summaries(float (&h)[SPL], const float (&A2)[SPL], const float* sh,
+                                               const float* sd, int64_t first, int64_t count, int dir, int j,
+                                               int64_t N) {
+  constexpr int U = SPL == 1 ? 8 : (SPL == 2 ? 4 : 2);
+  for (int64_t k0 = 0; k0 < count; k0 += U) {
+    float ds[U], hv[U][SPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = first + dir * (k0 + u < count ? k0 + u : count - 1);
+      ds[u] = sd[c];
+#pragma unroll
+      for (int s = 0; s < SPL; ++s) {
+        const int n = j + 16 * s;
+        hv[u][s] = sh[c * N + (n < N ? n : 0)];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k0 + u >= count) break;
+#pragma unroll
+      for (int s = 0; s < SPL; ++s)
+        if (j + 16 * s < N) h[s] = fmaf(fast_exp2(A2[s] * ds[u]), h[s], hv[u][s]);
+    }
+  }
+}
+
 // Reads the 16 steps of state lane n from a transposed B/C tile.
 __device__ __forceinline__ void read_bc_row(const float (*tile)[kBCPad], int n, float (&v)[kScanBlockT]) {
   const float4* row = reinterpret_cast<const float4*>(tile[n]);

@@ -64,16 +64,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   }
   if (MODE != kFwdSummary && chunk > 0) {
     // Carry the state over the chunks before this one.
-    const float* sh = p.sum_h + row * p.nchunk * N;
-    const float* sd = p.sum_dt + row * p.nchunk;
-    for (int64_t c = 0; c < chunk; ++c) {
-      const float ds = sd[c];
-#pragma unroll
-      for (int s = 0; s < SPL; ++s) {
-        const int n = j + 16 * s;
-        if (n < N) h[s] = fmaf(fast_exp2(A2[s] * ds), h[s], sh[c * N + n]);
-      }
-    }
+    fold_summaries<SPL>(h, A2, p.sum_h + row * p.nchunk * N, p.sum_dt + row * p.nchunk, 0, chunk, 1, j, N);
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
