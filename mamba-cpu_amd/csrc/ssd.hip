@@ -455,16 +455,32 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParam
   if (p.final_states) p.final_states[(b * H + h) * PN + e] = run;
 }
 
-// Row scales of the float4 numbers a thread holds of a (64 x ncols) tile
-// (tile_load's mapping): v[row] from the wave lane that owns the row.
+// The steps and running decays of every chunk, for the in-order kernels:
+// one wave per (b, h, chunk), lane t owning step t. Grid (ceil(nchunks / 4),
+// nheads, batch).
+__global__ void __launch_bounds__(kThreads) ssd_chunk_decay_kernel(const SsdParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  if (c >= p.nchunks) return;
+  const float st = ssd_step(p, b, c * Q + lane, h, nullptr);
+  float cs, csl;
+  wave_prefix_sum2(st * p.A[h], cs, csl);
+  const int64_t row = chunk_row(p, b, h, c);
+  p.cs[row + lane] = cs;
+  p.cs_lo[row + lane] = csl;
+  p.step[row + lane] = st;
+}
+
+// Rows of the float4 entries a thread holds of a (64 x ncols) tile
+// (tile_load's mapping), clamped to the tile.
 template <int V>
-__device__ __forceinline__ void row_scales(float (&sc)[V], float v, int ncols) {
-  const int nv = ncols >> 2;
-  const float inv = 1.0f / static_cast<float>(nv);
+__device__ __forceinline__ void tile_rows(int (&rows)[V], int ncols) {
+  const float inv = 1.0f / static_cast<float>(ncols >> 2);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     const int r = tile_row(static_cast<int>(threadIdx.x) + k * kThreads, inv);
-    sc[k] = __shfl(v, r < Q ? r : Q - 1, 64);
+    rows[k] = r < Q ? r : Q - 1;
   }
 }
 
@@ -473,8 +489,9 @@ __device__ __forceinline__ void row_scales(float (&sc)[V], float v, int ncols) {
 // matrix-core accumulators. Per chunk c it stores H_c (the state entering c)
 // and forms H_{c+1} = exp(cs_L) H_c + sum_s exp(cs_L - cs_s) dt_s x_s B_s^T by
 // starting the products from the scaled H_c, so chunk-end states never reach
-// memory. Column block 0 also saves the chunk's steps and running decays.
-// The next chunk's x, B and dt load while the current chunk's products run.
+// memory. The chunks' steps and running decays come from
+// ssd_chunk_decay_kernel; each thread loads those of its own x rows with the
+// next chunk's x and B while the current chunk's products run.
 // Grid (column blocks, nheads, batch); wave w owns state rows [16 w, 16 w + 16).
 // Three waves per SIMD, as the backward's.
 template <typename Tx>
@@ -493,8 +510,6 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdPa
   const int ncol = static_cast<int>(N - n0 < kSsdPassCols ? N - n0 : kSsdPassCols);
   const int nt = ncol >> 4;
   const bool act = 16 * wave < P;
-  const float Ah = p.A[h];
-  const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
   // Accumulator element (j, e) of this lane: state row 16 wave + 4 q + e,
   // column n0 + 16 j + r, at offset eo + e N + 16 j of a (headdim x dstate) block.
   const int64_t eo = (16 * wave + 4 * q) * N + n0 + r;
@@ -508,30 +523,30 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdPa
   const Tx* xh = static_cast<const Tx*>(p.x) + b * L * H * P + h * P;
   const Tx* Bg = static_cast<const Tx*>(p.B) + b * L * G * N + g * N + n0;
   raw4<Tx> nx[VX], nB[VB];
-  float ndt = 0.f;
+  int rows[VX];
+  tile_rows(rows, static_cast<int>(P));
+  float ncs[VX], nlo[VX], nst[VX], ncsL = 0.f, nloL = 0.f;
   auto fetch = [&](int64_t c) {
     const int64_t t0 = c * Q;
     const int nv = chunk_steps(p, t0);
     tile_load<Tx, VX>(nx, xh + t0 * H * P, H * P, Q, nv, static_cast<int>(P));
     tile_load<Tx, VB>(nB, Bg + t0 * G * N, G * N, Q, nv, ncol);
-    ndt = lane < nv ? p.dt[(b * L + t0 + lane) * H + h] : 0.f;
+    const int64_t row = chunk_row(p, b, h, c);
+#pragma unroll
+    for (int k = 0; k < VX; ++k) {
+      ncs[k] = p.cs[row + rows[k]];
+      nlo[k] = p.cs_lo[row + rows[k]];
+      nst[k] = p.step[row + rows[k]];
+    }
+    ncsL = p.cs[row + Q - 1];
+    nloL = p.cs_lo[row + Q - 1];
   };
   fetch(0);
   for (int64_t c = 0; c < p.nchunks; ++c) {
-    const bool tv = c * Q + lane < L;
-    const float st = tv ? step_of(p, ndt + bias, nullptr) : 0.f;
-    float cs, csl;
-    wave_prefix_sum2(st * Ah, cs, csl);
-    const float csL = __shfl(cs, Q - 1, 64), cslL = __shfl(csl, Q - 1, 64);
-    const float decay = fast_exp(csL + cslL);
-    if (blockIdx.x == 0 && wave == 0) {
-      const int64_t row = chunk_row(p, b, h, c);
-      p.cs[row + lane] = cs;
-      p.cs_lo[row + lane] = csl;
-      p.step[row + lane] = st;
-    }
-    float sc[VX];
-    row_scales(sc, st * fast_exp((csL - cs) + (cslL - csl)), static_cast<int>(P));
+    const float decay = fast_exp(ncsL + nloL);
+    float sc[VX];  // dt_s exp(cs_L - cs_s) of this thread's rows s
+#pragma unroll
+    for (int k = 0; k < VX; ++k) sc[k] = nst[k] * fast_exp((ncsL - ncs[k]) + (nloL - nlo[k]));
     __syncthreads();  // the previous chunk's products are done with s_x and s_B
     tile_store_scaled<Tx, VX>(&s_x[0][0], XP, nx, Q, static_cast<int>(P), sc);
     tile_store<Tx, VB>(&s_B[0][0], BP, nB, Q, ncol);
@@ -847,8 +862,13 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const S
           }
     }
     part = wave_total(part);
-    float sc[Dy::V];
-    row_scales(sc, ecs, static_cast<int>(P));
+    float sc[Dy::V];  // exp(cs_t) of this thread's dY rows t, from the lanes that own them
+    {
+      int rows[Dy::V];
+      tile_rows(rows, static_cast<int>(P));
+#pragma unroll
+      for (int k = 0; k < Dy::V; ++k) sc[k] = __shfl(ecs, rows[k], 64);
+    }
     __syncthreads();  // the previous chunk's products are done with s_dY and s_C; its parts are in
     if (pend >= 0 && tid == 0)
       dcsl[pend * p.nslices] = pend_decay * ((s_part[0] + s_part[1]) + (s_part[2] + s_part[3]));
@@ -1216,6 +1236,10 @@ hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
                     static_cast<unsigned>(p.batch));
   if (p.in_order) {
+    const dim3 rows(static_cast<unsigned>((p.nchunks + kThreads / 64 - 1) / (kThreads / 64)),
+                    static_cast<unsigned>(p.nheads), static_cast<unsigned>(p.batch));
+    hipLaunchKernelGGL(ssd_chunk_decay_kernel, rows, dim3(kThreads), 0, st, p);
+    if (hipError_t e = hipGetLastError()) return e;
     hipLaunchKernelGGL(ssd_state_scan_kernel<Tx>, slices, dim3(kThreads), 0, st, p);
   } else {
     hipLaunchKernelGGL(ssd_chunk_state_kernel<Tx>, chunks, dim3(kThreads), 0, st, p);
