@@ -614,8 +614,19 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
   // The next head's x tile, entering state and decays load into registers
   // while this head's products run.
   raw4<Tx> rx[VX], zc[VX];
-  float4 rh[VN];
+  float4 rh[VN], rD[VX];
   float rcs = 0.f, rcsl = 0.f, rdt = 0.f;
+  // The headdim column of this thread's output entries (fixed over heads).
+  int ocol[VX];
+  {
+    const float inv = 1.0f / static_cast<float>(np * 4);
+#pragma unroll
+    for (int k = 0; k < VX; ++k) {
+      const int v = tid + k * TPB;
+      const int t = tile_row(v, inv);
+      ocol[k] = v < Q * np * 4 ? (v - t * np * 4) << 2 : 0;
+    }
+  }
   auto fetch = [&](int64_t h) {
     const int64_t row = chunk_row(p, b, h, c);
     if (tid < Q) {
@@ -627,11 +638,17 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
                            static_cast<int>(P));
     tile_load<float, VN, TPB>(rh, p.states + state_block(p, b, c, h), N, static_cast<int>(P), static_cast<int>(P),
                               static_cast<int>(N));
+#pragma unroll
+    for (int k = 0; k < VX; ++k)
+      rD[k] = p.D ? *reinterpret_cast<const float4*>(p.D + h * P + ocol[k]) : make_float4(0.f, 0.f, 0.f, 0.f);
   };
   fetch(h0);
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
     const int64_t xoff = ((b * L + t0) * H + h) * P;
+    float4 dcol[VX];  // this head's D at the output columns (rD moves on to the next head below)
+#pragma unroll
+    for (int k = 0; k < VX; ++k) dcol[k] = rD[k];
     __syncthreads();  // every wave is done with s_BH, s_G, s_X and s_cs
     if (tid < Q) {
       s_cs[tid] = rcs;
@@ -681,7 +698,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
         const int64_t at = xoff + t * H * P + pp;
         float y[4] = {s_G[t][pp], s_G[t][pp + 1], s_G[t][pp + 2], s_G[t][pp + 3]};
         if (p.D) {
-          const float4 d = *reinterpret_cast<const float4*>(p.D + h * P + pp);
+          const float4 d = dcol[k];
           y[0] = fmaf(d.x, s_X[t][pp], y[0]);
           y[1] = fmaf(d.y, s_X[t][pp + 1], y[1]);
           y[2] = fmaf(d.z, s_X[t][pp + 2], y[2]);
@@ -973,8 +990,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
   fetch(h0);
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
-    const int64_t row = chunk_row(p, b, h, c);
     const int64_t xoff = ((b * L + t0) * H + h) * P;
+    const int64_t row = chunk_row(p, b, h, c);
     const int64_t sb = state_block(p, b, c, h);
     __syncthreads();  // every wave is done with the previous head's tiles
     if (tid < Q) {
