@@ -357,6 +357,11 @@ typedef struct mcpu_ssd_args {
      same result up to float32 rounding; pinning one lets tests cover both.
      The size queries must see the same value as the calls. */
   int32_t chunk_pass;
+  /* (batch, seqlen) int32, optional: ids of packed sequences, non-decreasing
+     along each row. The state does not carry across a change of id (the
+     decay is 0 there), and the initial state belongs to id 0, as mamba_ssm's
+     seq_idx. */
+  const int32_t* seq_idx;
 } mcpu_ssd_args;
 
 /* Bytes of the buffer the forward fills for the backward (0 for an empty

@@ -82,6 +82,7 @@ SsdParams make_ssd(const mcpu_ssd_args* a) {
   p.z = a->z;
   p.dt_bias = a->dt_bias;
   p.init = a->initial_states;
+  p.seq_idx = a->seq_idx;
   p.batch = a->batch;
   p.seqlen = a->seqlen;
   p.nheads = a->nheads;

@@ -375,13 +375,45 @@ __device__ __forceinline__ int chunk_steps(const SsdParams& p, int64_t t0) {
   return static_cast<int>(p.seqlen - t0 < Q ? p.seqlen - t0 : Q);
 }
 
+// Packed sequences. Kernels built with SEQ read p.seq_idx; without it every
+// helper below folds to a constant (one sequence, id 0).
+//
+// Id of step t of batch row b: 0 before the first step (the initial state's
+// id); steps past the sequence (a chunk's padding) take the last step's id.
+template <bool SEQ>
+__device__ __forceinline__ int32_t seq_of(const SsdParams& p, int64_t b, int64_t t) {
+  if constexpr (!SEQ) return 0;
+  if (t < 0) return 0;
+  return p.seq_idx[b * p.seqlen + (t < p.seqlen ? t : p.seqlen - 1)];
+}
+
+// Ids do not decrease, so the steps of a chunk that share an id form a run.
+// For the wave whose lane l stands for step t0 + l: the first step (in the
+// chunk) of lane l's run.
+template <bool SEQ>
+__device__ __forceinline__ int run_first(const SsdParams& p, int64_t b, int64_t t0, int lane) {
+  if constexpr (!SEQ) return 0;
+  const bool starts = lane == 0 || seq_of<SEQ>(p, b, t0 + lane) != seq_of<SEQ>(p, b, t0 + lane - 1);
+  const unsigned long long upto = __ballot(starts) & (~0ull >> (63 - lane));
+  return 63 - __clzll(upto);
+}
+
+// Whether the state entering chunk c carries through it: the ids at the ends
+// of chunks c - 1 and c agree (ids do not decrease, so none changes between).
+template <bool SEQ>
+__device__ __forceinline__ bool carries(const SsdParams& p, int64_t b, int64_t c) {
+  if constexpr (!SEQ) return true;
+  const int64_t end = (c + 1) * Q < p.seqlen ? (c + 1) * Q - 1 : p.seqlen - 1;
+  return seq_of<SEQ>(p, b, end) == seq_of<SEQ>(p, b, c * Q - 1);
+}
+
 }  // namespace
 
 // F1: steps and running decays of each head's chunk (saved for F3 and the
 // backward), and the chunk-end state S(p, n) = sum_s exp(cs_L - cs_s) dt_s
 // x_s(p) B_s(n). Grid (nchunks, nhb, batch); wave w computes state rows p in
 // [16 w, 16 w + 16).
-template <typename Tx>
+template <typename Tx, bool SEQ>
 __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdParams p) {
   __shared__ __align__(16) float s_B[Q][NP];
   __shared__ __align__(16) float s_x[Q][XP];
@@ -407,7 +439,9 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdPara
       p.cs_lo[row + lane] = csl;
       p.step[row + lane] = st;
       const float csL = __shfl(cs, Q - 1, 64), cslL = __shfl(csl, Q - 1, 64);
-      s_sc[lane] = st * fast_exp((csL - cs) + (cslL - csl));
+      // steps of another sequence than the chunk's last do not reach its end state
+      const bool reach = seq_of<SEQ>(p, b, t0 + lane) == seq_of<SEQ>(p, b, t0 + nvalid - 1);
+      s_sc[lane] = reach ? st * fast_exp((csL - cs) + (cslL - csl)) : 0.f;
     }
     __syncthreads();
     stage<Tx, kVecX>(&s_x[0][0], XP, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nvalid,
@@ -433,6 +467,7 @@ __global__ void __launch_bounds__(kThreads) ssd_chunk_state_kernel(const SsdPara
 // initial state or 0), and writes the final state. One thread per state
 // element; grid (nslices, nheads, batch). The next chunk's loads issue before
 // this chunk's store.
+template <bool SEQ>
 __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParams p) {
   const int64_t PN = p.headdim * p.dstate, H = p.nheads;
   const int64_t e = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
@@ -444,7 +479,7 @@ __global__ void __launch_bounds__(kThreads) ssd_state_pass_kernel(const SsdParam
   const float* csl = p.cs + chunk_row(p, b, h, 0) + (Q - 1);
   float s = st[0], d = csl[0];
   for (int64_t c = 0; c < p.nchunks; ++c) {
-    const float sc = s, dc = fast_exp(d);
+    const float sc = s, dc = carries<SEQ>(p, b, c) ? fast_exp(d) : 0.f;
     if (c + 1 < p.nchunks) {
       s = st[(c + 1) * cstride];
       d = csl[(c + 1) * Q];
@@ -494,7 +529,7 @@ __device__ __forceinline__ void tile_rows(int (&rows)[V], int ncols) {
 // next chunk's x and B while the current chunk's products run.
 // Grid (column blocks, nheads, batch); wave w owns state rows [16 w, 16 w + 16).
 // Three waves per SIMD, as the backward's.
-template <typename Tx>
+template <typename Tx, bool SEQ>
 __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdParams p) {
   constexpr int VX = vec_x();
   constexpr int VB = Q * kSsdPassCols / 4 / kThreads;
@@ -526,6 +561,10 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdPa
   int rows[VX];
   tile_rows(rows, static_cast<int>(P));
   float ncs[VX], nlo[VX], nst[VX], ncsL = 0.f, nloL = 0.f;
+  // packed sequences: the chunk's last run starts at step nlast (its steps
+  // reach the chunk's end state); H_c carries through the chunk
+  int nlast = 0;
+  bool ncarry = true;
   auto fetch = [&](int64_t c) {
     const int64_t t0 = c * Q;
     const int nv = chunk_steps(p, t0);
@@ -540,13 +579,18 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdPa
     }
     ncsL = p.cs[row + Q - 1];
     nloL = p.cs_lo[row + Q - 1];
+    if constexpr (SEQ) {  // the last run's first step, from a ballot over the chunk's steps
+      nlast = __ffsll(static_cast<long long>(
+                  __ballot(seq_of<SEQ>(p, b, t0 + lane) == seq_of<SEQ>(p, b, t0 + nv - 1)))) - 1;
+      ncarry = carries<SEQ>(p, b, c);
+    }
   };
   fetch(0);
   for (int64_t c = 0; c < p.nchunks; ++c) {
-    const float decay = fast_exp(ncsL + nloL);
+    const float decay = ncarry ? fast_exp(ncsL + nloL) : 0.f;
     float sc[VX];  // dt_s exp(cs_L - cs_s) of this thread's rows s
 #pragma unroll
-    for (int k = 0; k < VX; ++k) sc[k] = nst[k] * fast_exp((ncsL - ncs[k]) + (nloL - nlo[k]));
+    for (int k = 0; k < VX; ++k) sc[k] = rows[k] >= nlast ? nst[k] * fast_exp((ncsL - ncs[k]) + (nloL - nlo[k])) : 0.f;
     __syncthreads();  // the previous chunk's products are done with s_x and s_B
     tile_store_scaled<Tx, VX>(&s_x[0][0], XP, nx, Q, static_cast<int>(P), sc);
     tile_store<Tx, VB>(&s_B[0][0], BP, nB, Q, ncol);
@@ -581,7 +625,7 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_state_scan_kernel(const SsdPa
 // [16 (w % 4), 16 (w % 4) + 16) and half w / 4 of the column tiles (C B^T:
 // tiles 2h, 2h + 1; Y: the first or second half of the headdim tiles), so each
 // SIMD runs two waves. C B^T is formed once for the block's heads.
-template <typename Tx, bool HAS_Z>
+template <typename Tx, bool HAS_Z, bool SEQ>
 __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdParams p) {
   constexpr int TPB = kThreads3;
   constexpr int VX = vec_x<TPB>(), VN = vec_n<TPB>();
@@ -590,6 +634,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
   __shared__ __align__(16) float s_G[Q][QP];      // (C B^T o M)[t][s] dt_s, then Y
   __shared__ __align__(16) float s_X[Q][XP];      // x
   __shared__ float s_cs[Q], s_csl[Q], s_dt[Q];
+  __shared__ __align__(4) uint8_t s_first[Q];     // first step of each step's sequence run in the chunk
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ws = wave & 3, hf = wave >> 2;        // row strip, column half
@@ -607,7 +652,12 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
     stage<Tx, VN, TPB>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
     stage<Tx, VN, TPB>(&s_BH[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
+  if (SEQ && wave == 0) s_first[lane] = static_cast<uint8_t>(run_first<SEQ>(p, b, t0, lane));
+  // the entering state reaches the chunk's first run
+  const bool enter = seq_of<SEQ>(p, b, t0) == seq_of<SEQ>(p, b, t0 - 1);
   __syncthreads();
+  // runs of this thread's rows t = 16 ws + 4 q + e: M[t][s] needs first_t <= s <= t
+  const uint32_t firsts = SEQ ? *reinterpret_cast<const uint32_t*>(&s_first[16 * ws + 4 * q]) : 0u;
   v4f cb[2];
   zero(cb);
   mma(cb, 2, &s_C[16 * ws][0], NP, 1, &s_BH[32 * hf][0], 1, NP, static_cast<int>(N));
@@ -666,7 +716,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = 16 * ws + 4 * q + e, s = 32 * hf + 16 * j + r;
-        s_G[t][s] = s <= t ? cb[j][e] * seg_exp(s_cs, s_csl, t, s) * s_dt[s] : 0.f;
+        const int ft = (firsts >> (8 * e)) & 0xff;
+        s_G[t][s] = (s <= t && s >= ft) ? cb[j][e] * seg_exp(s_cs, s_csl, t, s) * s_dt[s] : 0.f;
       }
     __syncthreads();
     v4f y1[2], y2[2];
@@ -679,7 +730,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * ws + 4 * q + e;
-      const float ecs = fast_exp(s_cs[t] + s_csl[t]);
+      const bool from = enter && ((firsts >> (8 * e)) & 0xff) == 0;
+      const float ecs = from ? fast_exp(s_cs[t] + s_csl[t]) : 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         if (j < npw) s_G[t][16 * (p0 + j) + r] = fmaf(ecs, y2[j][e], y1[j][e]);
@@ -720,7 +772,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_chunk_scan_kernel(const SsdP
 // K1: the seed E_c[p][n] = sum_t exp(cs_t) dY[t][p] C[t][n] of dL/dH_c from
 // the chunk's own outputs, for each head of the block, into dstates. Grid
 // (nchunks, nhb, batch); wave w computes rows p in [16 w, 16 w + 16).
-template <typename Tx, bool HAS_Z>
+template <typename Tx, bool HAS_Z, bool SEQ>
 __global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams p) {
   __shared__ __align__(16) float s_C[Q][NP];
   __shared__ __align__(16) float s_dY[Q][XP];     // exp(cs_t) dY[t][p]
@@ -735,11 +787,13 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams 
   const int nvalid = chunk_steps(p, t0);
   stage<Tx, kVecN>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + ((b * L + t0) * G + g) * N, G * N, Q, nvalid,
             static_cast<int>(N));
+  // packed sequences: step tid reads the entering state only within its sequence
+  const bool from = tid < Q && seq_of<SEQ>(p, b, t0 + tid) == seq_of<SEQ>(p, b, t0 - 1);
   for (int i = 0; i < p.hb; ++i) {
     const int64_t h = h0 + i;
     const int64_t row = chunk_row(p, b, h, c);
     __syncthreads();  // every wave is done with s_dY and s_ecs
-    if (tid < Q) s_ecs[tid] = fast_exp(p.cs[row + tid] + p.cs_lo[row + tid]);
+    if (tid < Q) s_ecs[tid] = from ? fast_exp(p.cs[row + tid] + p.cs_lo[row + tid]) : 0.f;
     __syncthreads();
     {
       const int64_t off = ((b * L + t0) * H + h) * P;
@@ -768,6 +822,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_seed_kernel(const SsdParams 
 // goes to dcsL. The gradient of the initial state is what is left after
 // chunk 0. Grid (nslices, nheads, batch). The next chunk's loads issue before
 // this chunk's store.
+template <bool SEQ>
 __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams p) {
   __shared__ float s_part[kThreads / 64];
   const int64_t PN = p.headdim * p.dstate, H = p.nheads;
@@ -785,7 +840,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams 
   float hin = ok ? p.states[base + last * cstride] : 0.f;
   float dl = csl[last * Q];
   for (int64_t c = last; c >= 0; --c) {
-    const float ecc = ec, hc = hin, d = fast_exp(dl);
+    const float ecc = ec, hc = hin, d = carries<SEQ>(p, b, c) ? fast_exp(dl) : 0.f;
     if (c > 0) {
       ec = ok ? p.dstates[base + (c - 1) * cstride] : 0.f;
       hin = ok ? p.states[base + (c - 1) * cstride] : 0.f;
@@ -813,7 +868,7 @@ __global__ void __launch_bounds__(kThreads) ssd_bwd_pass_kernel(const SsdParams 
 // products run. Grid (column blocks, nheads, batch); wave w owns rows
 // [16 w, 16 w + 16). Three waves per SIMD: 640 workgroups (the Mamba-2 2.7B
 // layer at batch 4) run in one round.
-template <typename Tx, bool HAS_Z>
+template <typename Tx, bool HAS_Z, bool SEQ>
 __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const SsdParams p) {
   constexpr int VB = Q * kSsdPassCols / 4 / kThreads;
   constexpr int BP = kSsdPassCols + 4;
@@ -842,6 +897,7 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const S
   Dy dyt;
   raw4<Tx> nC[VB];
   float ncs = 0.f, nlo = 0.f, nH[kSsdPassCols / 16][4];
+  bool nfrom = true, ncarry = true;  // packed sequences: step lane reads H_c; H_c carries through the chunk
   auto fetch = [&](int64_t c) {
     const int64_t t0 = c * Q;
     const int nv = chunk_steps(p, t0);
@@ -850,6 +906,8 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const S
     const int64_t row = chunk_row(p, b, h, c);
     ncs = p.cs[row + lane];
     nlo = p.cs_lo[row + lane];
+    nfrom = seq_of<SEQ>(p, b, t0 + lane) == seq_of<SEQ>(p, b, t0 - 1);
+    ncarry = carries<SEQ>(p, b, c);
     const float* hs = p.states + state_block(p, b, c, h) + eo;
 #pragma unroll
     for (int j = 0; j < kSsdPassCols / 16; ++j)
@@ -861,8 +919,9 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const S
   float pend_decay = 0.f;
   fetch(p.nchunks - 1);
   for (int64_t c = p.nchunks - 1; c >= 0; --c) {
-    const float ecs = fast_exp(ncs + nlo);
-    const float decay = __shfl(ecs, Q - 1, 64);
+    const float ecs_all = fast_exp(ncs + nlo);
+    const float decay = ncarry ? __shfl(ecs_all, Q - 1, 64) : 0.f;
+    const float ecs = nfrom ? ecs_all : 0.f;
     // dH^out_c out, its share of dL/dcs_L, and the decayed carry, before the
     // next chunk's H_c loads into the same registers.
     float part = 0.f;
@@ -919,7 +978,7 @@ __global__ void __launch_bounds__(kThreads, 3) ssd_bwd_state_scan_kernel(const S
 // hide each other's LDS and memory latency. Row sums over columns are
 // combined across the two halves through LDS. dB and dC of the block's heads
 // stay in accumulators and are written once, as the block's partial sums.
-template <typename Tx, bool HAS_Z>
+template <typename Tx, bool HAS_Z, bool SEQ>
 __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdParams p) {
   constexpr int TPB = kThreads3;
   constexpr int VX = vec_x<TPB>(), VN = vec_n<TPB>();
@@ -934,6 +993,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
   __shared__ float s_half[2][4][Q];               // per column half: sum_s R, sum_n C.., sum_n B~.., sum_p ..
   __shared__ float s_cs[Q], s_csl[Q], s_dt[Q], s_w[Q], s_ecs[Q], s_dcs[Q];
   __shared__ float s_tot[8], s_wa[8], s_wb[8];
+  __shared__ __align__(4) uint8_t s_first[Q];     // first step of each step's sequence run in the chunk
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ws = wave & 3, hf = wave >> 2;        // row strip, column half
@@ -958,7 +1018,18 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
     stage<Tx, VN, TPB>(&s_C[0][0], NP, static_cast<const Tx*>(p.C) + off, G * N, Q, nvalid, static_cast<int>(N));
     stage<Tx, VN, TPB>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + off, G * N, Q, nvalid, static_cast<int>(N));
   }
+  // Packed sequences: step tid reaches the chunk's end state (w) and reads the
+  // entering state (exp(cs)) only within one sequence.
+  bool reach = true, from = true;
+  if (wave == 0) {
+    if (SEQ) s_first[lane] = static_cast<uint8_t>(run_first<SEQ>(p, b, t0, lane));
+    const int32_t id = seq_of<SEQ>(p, b, t0 + lane);
+    reach = id == seq_of<SEQ>(p, b, t0 + nvalid - 1);
+    from = id == seq_of<SEQ>(p, b, t0 - 1);
+  }
   __syncthreads();
+  // runs of this thread's rows t = 16 ws + 4 q + e: M[t][s] needs first_t <= s <= t
+  const uint32_t firsts = SEQ ? *reinterpret_cast<const uint32_t*>(&s_first[16 * ws + 4 * q]) : 0u;
   // C B^T, rows t of this strip, Q-column tiles 2 hf, 2 hf + 1
   v4f cb[2];
   zero(cb);
@@ -998,8 +1069,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
       s_cs[tid] = rcs;
       s_csl[tid] = rcsl;
       s_dt[tid] = rdt;
-      s_w[tid] = fast_exp((rcsL - rcs) + (rcslL - rcsl));
-      s_ecs[tid] = fast_exp(rcs + rcsl);
+      s_w[tid] = reach ? fast_exp((rcsL - rcs) + (rcslL - rcsl)) : 0.f;
+      s_ecs[tid] = from ? fast_exp(rcs + rcsl) : 0.f;
     }
     tile_store<Tx, VX, TPB>(&s_X[0][0], XP, rx, Q, static_cast<int>(P));
     rdy.store(&s_dY[0][0], XP, p, xoff, H * P, nvalid, static_cast<int>(P), true);
@@ -1019,7 +1090,8 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int t = 16 * ws + 4 * q + e, s = 32 * hf + 16 * j + r;
-          const float m = s <= t ? seg_exp(s_cs, s_csl, t, s) : 0.f;
+          const float m = (s <= t && s >= static_cast<int>((firsts >> (8 * e)) & 0xff)) ? seg_exp(s_cs, s_csl, t, s)
+                                                                                     : 0.f;
           const float dcb = dg[j][e] * s_dt[s] * m;
           const float rv = dcb * cb[j][e];
           s_U[t][s] = cb[j][e] * m;
@@ -1247,7 +1319,7 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
 
 namespace {
 
-template <typename Tx>
+template <typename Tx, bool SEQ>
 hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
   const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
@@ -1257,53 +1329,55 @@ hipError_t fwd_t(const SsdParams& p, hipStream_t st) {
                     static_cast<unsigned>(p.nheads), static_cast<unsigned>(p.batch));
     hipLaunchKernelGGL(ssd_chunk_decay_kernel, rows, dim3(kThreads), 0, st, p);
     if (hipError_t e = hipGetLastError()) return e;
-    hipLaunchKernelGGL(ssd_state_scan_kernel<Tx>, slices, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((ssd_state_scan_kernel<Tx, SEQ>), slices, dim3(kThreads), 0, st, p);
   } else {
-    hipLaunchKernelGGL(ssd_chunk_state_kernel<Tx>, chunks, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((ssd_chunk_state_kernel<Tx, SEQ>), chunks, dim3(kThreads), 0, st, p);
     if (hipError_t e = hipGetLastError()) return e;
-    hipLaunchKernelGGL(ssd_state_pass_kernel, slices, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL(ssd_state_pass_kernel<SEQ>, slices, dim3(kThreads), 0, st, p);
   }
   if (hipError_t e = hipGetLastError()) return e;
-  if (p.z) hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
-  else hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, true, SEQ>), chunks, dim3(kThreads3), 0, st, p);
+  else hipLaunchKernelGGL((ssd_chunk_scan_kernel<Tx, false, SEQ>), chunks, dim3(kThreads3), 0, st, p);
   return hipGetLastError();
 }
 
-template <typename Tx>
+template <typename Tx, bool SEQ>
 hipError_t bwd_t(const SsdParams& p, hipStream_t st) {
   const dim3 chunks(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(p.nhb), static_cast<unsigned>(p.batch));
   const dim3 slices(static_cast<unsigned>(p.nslices), static_cast<unsigned>(p.nheads),
                     static_cast<unsigned>(p.batch));
   if (p.in_order) {
-    if (p.z) hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, true>), slices, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, false>), slices, dim3(kThreads), 0, st, p);
+    if (p.z) hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, true, SEQ>), slices, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((ssd_bwd_state_scan_kernel<Tx, false, SEQ>), slices, dim3(kThreads), 0, st, p);
   } else {
-    if (p.z) hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, true>), chunks, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, false>), chunks, dim3(kThreads), 0, st, p);
+    if (p.z) hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, true, SEQ>), chunks, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((ssd_bwd_seed_kernel<Tx, false, SEQ>), chunks, dim3(kThreads), 0, st, p);
     if (hipError_t e = hipGetLastError()) return e;
-    hipLaunchKernelGGL(ssd_bwd_pass_kernel, slices, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL(ssd_bwd_pass_kernel<SEQ>, slices, dim3(kThreads), 0, st, p);
   }
   if (hipError_t e = hipGetLastError()) return e;
-  if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true>), chunks, dim3(kThreads3), 0, st, p);
-  else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false>), chunks, dim3(kThreads3), 0, st, p);
+  if (p.z) hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, true, SEQ>), chunks, dim3(kThreads3), 0, st, p);
+  else hipLaunchKernelGGL((ssd_bwd_chunk_kernel<Tx, false, SEQ>), chunks, dim3(kThreads3), 0, st, p);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t ssd_fwd_launch(const SsdParams& p, int dtype, hipStream_t st) {
+  const bool seq = p.seq_idx != nullptr;
   switch (dtype) {
-    case MCPU_F32: return fwd_t<float>(p, st);
-    case MCPU_BF16: return fwd_t<bf16>(p, st);
-    default: return fwd_t<f16>(p, st);
+    case MCPU_F32: return seq ? fwd_t<float, true>(p, st) : fwd_t<float, false>(p, st);
+    case MCPU_BF16: return seq ? fwd_t<bf16, true>(p, st) : fwd_t<bf16, false>(p, st);
+    default: return seq ? fwd_t<f16, true>(p, st) : fwd_t<f16, false>(p, st);
   }
 }
 
 hipError_t ssd_bwd_launch(const SsdParams& p, int dtype, hipStream_t st) {
+  const bool seq = p.seq_idx != nullptr;
   switch (dtype) {
-    case MCPU_F32: return bwd_t<float>(p, st);
-    case MCPU_BF16: return bwd_t<bf16>(p, st);
-    default: return bwd_t<f16>(p, st);
+    case MCPU_F32: return seq ? bwd_t<float, true>(p, st) : bwd_t<float, false>(p, st);
+    case MCPU_BF16: return seq ? bwd_t<bf16, true>(p, st) : bwd_t<bf16, false>(p, st);
+    default: return seq ? bwd_t<f16, true>(p, st) : bwd_t<f16, false>(p, st);
   }
 }
 

@@ -31,6 +31,7 @@ struct SsdParams {
   const void* z;
   const float* dt_bias;
   const float* init;
+  const int32_t* seq_idx;   // (batch, seqlen) packed-sequence ids, or null
   void* out;
   float* final_states;
   void* ysave;              // y before the z gate, written when the backward will need it

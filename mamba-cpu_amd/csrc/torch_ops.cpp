@@ -1073,15 +1073,16 @@ Tensor selective_state_update_inplace(Tensor& state, const Tensor& x, const Tens
 // nheads, headdim) in one storage type; dt (batch, seqlen, nheads) float32;
 // A, dt_bias (nheads) float32; B, C (batch, seqlen, ngroups, dstate) in x's
 // type; D (nheads, headdim) float32; initial_states (batch, nheads, headdim,
-// dstate) float32. The Python wrapper (mamba_cpu/ops/ssd_combined.py) brings
-// its arguments to these.
+// dstate) float32; seq_idx (batch, seqlen) int32 packed-sequence ids, not
+// decreasing along the sequence. The Python wrapper
+// (mamba_cpu/ops/ssd_combined.py) brings its arguments to these.
 
 mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, const Tensor& A,
                        const Tensor& B, const Tensor& C, const optional<Tensor>& D,
                        const optional<Tensor>& z, const optional<Tensor>& dt_bias,
                        const optional<Tensor>& init, bool softplus, double lo, double hi,
-                       int64_t head_block, int64_t chunk_pass) {
-  for (const optional<Tensor>& t : {opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias, init})
+                       int64_t head_block, int64_t chunk_pass, const optional<Tensor>& seq_idx) {
+  for (const optional<Tensor>& t : {opt(x), opt(dt), opt(A), opt(B), opt(C), D, z, dt_bias, init, seq_idx})
     check_gpu(name, t);
   TORCH_CHECK_VALUE(x.dim() == 4 && x_dtype(x.scalar_type()) && x.is_contiguous(), name,
                     " expects a contiguous x (batch, seqlen, nheads, headdim) in float32, bfloat16 or float16");
@@ -1108,6 +1109,9 @@ mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, cons
                                    init->size(1) == h && init->size(2) == p && init->size(3) == B.size(3) &&
                                    init->is_contiguous()),
                     name, " expects float32 initial_states (batch, nheads, headdim, dstate)");
+  TORCH_CHECK_VALUE(!has(seq_idx) || (seq_idx->scalar_type() == at::kInt && seq_idx->dim() == 2 &&
+                                      seq_idx->size(0) == b && seq_idx->size(1) == l && seq_idx->is_contiguous()),
+                    name, " expects a contiguous int32 seq_idx (batch, seqlen)");
   mcpu_ssd_args a;
   std::memset(&a, 0, sizeof(a));
   a.x = x.data_ptr();
@@ -1131,6 +1135,7 @@ mcpu_ssd_args ssd_args(const char* name, const Tensor& x, const Tensor& dt, cons
   a.dt_limit_hi = static_cast<float>(hi);
   a.head_block = static_cast<int32_t>(head_block);
   a.chunk_pass = static_cast<int32_t>(chunk_pass);
+  a.seq_idx = has(seq_idx) ? static_cast<const int32_t*>(seq_idx->data_ptr()) : nullptr;
   return a;
 }
 
@@ -1139,9 +1144,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> ssd_fwd(const Tensor& x, const Tensor
                                                    const optional<Tensor>& z, const optional<Tensor>& dt_bias,
                                                    const optional<Tensor>& init, bool softplus, double lo,
                                                    double hi, bool save_for_backward, int64_t head_block,
-                                                   int64_t chunk_pass) {
+                                                   int64_t chunk_pass, const optional<Tensor>& seq_idx) {
   const char* name = "mamba_cpu::ssd_fwd";
-  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass);
+  mcpu_ssd_args a =
+      ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass, seq_idx);
   c10::DeviceGuard guard(x.device());
   Tensor out = at::empty(x.sizes(), x.options());
   Tensor fin = at::empty({a.batch, a.nheads, a.headdim, a.dstate}, x.options().dtype(at::kFloat));
@@ -1161,9 +1167,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tenso
     const Tensor& dout, const optional<Tensor>& dfinal, const Tensor& x, const Tensor& dt, const Tensor& A,
     const Tensor& B, const Tensor& C, const optional<Tensor>& D, const optional<Tensor>& z,
     const optional<Tensor>& dt_bias, const optional<Tensor>& init, bool softplus, double lo, double hi,
-    const Tensor& saved, const Tensor& ysave, int64_t head_block, int64_t chunk_pass) {
+    const Tensor& saved, const Tensor& ysave, int64_t head_block, int64_t chunk_pass,
+    const optional<Tensor>& seq_idx) {
   const char* name = "mamba_cpu::ssd_bwd";
-  mcpu_ssd_args a = ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass);
+  mcpu_ssd_args a =
+      ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass, seq_idx);
   check_gpu(name, opt(dout));
   check_gpu(name, dfinal);
   TORCH_CHECK_VALUE(dout.sizes() == x.sizes() && dout.scalar_type() == x.scalar_type() && dout.is_contiguous(),
@@ -1326,10 +1334,11 @@ Tensor mixer_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_wei
 TORCH_LIBRARY(mamba_cpu, m) {
   m.def("ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
         "Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, float dt_hi, "
-        "bool save_for_backward, int head_block=0, int chunk_pass=0) -> (Tensor, Tensor, Tensor, Tensor)");
+        "bool save_for_backward, int head_block=0, int chunk_pass=0, Tensor? seq_idx=None) -> "
+        "(Tensor, Tensor, Tensor, Tensor)");
   m.def("ssd_bwd(Tensor dout, Tensor? dfinal_states, Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, "
         "Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, "
-        "float dt_hi, Tensor saved, Tensor ysave, int head_block=0, int chunk_pass=0) -> "
+        "float dt_hi, Tensor saved, Tensor ysave, int head_block=0, int chunk_pass=0, Tensor? seq_idx=None) -> "
         "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("selective_scan_fwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
         "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor)");

@@ -112,7 +112,7 @@ class SsdArgs(ctypes.Structure):
         ("out", _P), ("final_states", _P), ("ysave", _P),
         ("dout", _P), ("dfinal_states", _P),
         ("dx", _P), ("ddt", _P), ("dA", _P), ("dB", _P), ("dC", _P), ("dD", _P), ("dz", _P),
-        ("ddt_bias", _P), ("dinitial_states", _P), ("head_block", _I32), ("chunk_pass", _I32),
+        ("ddt_bias", _P), ("dinitial_states", _P), ("head_block", _I32), ("chunk_pass", _I32), ("seq_idx", _P),
     ]
 
 

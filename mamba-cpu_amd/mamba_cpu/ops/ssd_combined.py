@@ -12,6 +12,10 @@ contiguous groups that share B and C):
                                                       h_{-1} = initial_states or 0)
     y_t  = h_t C_t + D x_t ;  out = y silu(z) when z is given
 
+With seq_idx (packed sequences: non-decreasing ids along each batch row) the
+state does not cross a change of id: exp(dt_t A_h) is taken as 0 at the first
+step of each new id, and the initial state belongs to id 0.
+
 The kernels scan 64-step chunks whatever `chunk_size` says (it is accepted for
 compatibility; the result does not depend on it beyond float32 rounding).
 Arithmetic and states are float32 for every storage type; the chunk-local
@@ -48,7 +52,7 @@ def _saved_bytes(b, l, h, p, n):
 
 @torch.library.register_fake("mamba_cpu::ssd_fwd")
 def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, save_for_backward,
-      head_block=0, chunk_pass=0):
+      head_block=0, chunk_pass=0, seq_idx=None):
     b, l, h, p = x.shape
     n = B.shape[-1]
     ysave = x.new_empty(x.shape) if (save_for_backward and z is not None) else x.new_empty(0)
@@ -58,7 +62,7 @@ def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, 
 
 @torch.library.register_fake("mamba_cpu::ssd_bwd")
 def _(dout, dfinal_states, x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi,
-      saved, ysave, head_block=0, chunk_pass=0):
+      saved, ysave, head_block=0, chunk_pass=0, seq_idx=None):
     f32 = dict(dtype=torch.float32)
     return (x.new_empty(x.shape), dt.new_empty(dt.shape, **f32), A.new_empty(A.shape, **f32),
             B.new_empty(B.shape, **f32), C.new_empty(C.shape, **f32),
@@ -73,24 +77,24 @@ class _SsdScan(torch.autograd.Function):
     states (and y before the z gate), the backward reads them."""
 
     @staticmethod
-    def forward(ctx, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi):
+    def forward(ctx, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, seq_idx):
         out, final, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(
-            x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, True)
-        ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, initial_states, saved, ysave)
+            x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, True, seq_idx=seq_idx)
+        ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, initial_states, saved, ysave, seq_idx)
         ctx.cfg = (softplus, lo, hi)
         ctx.set_materialize_grads(False)
         return out, final
 
     @staticmethod
     def backward(ctx, dout, dfinal):
-        x, dt, A, B, C, D, z, dt_bias, init, saved, ysave = ctx.saved_tensors
+        x, dt, A, B, C, D, z, dt_bias, init, saved, ysave, seq_idx = ctx.saved_tensors
         dout = torch.zeros_like(x) if dout is None else _aligned(dout.to(x.dtype).contiguous())
         dfinal = None if dfinal is None else dfinal.float().contiguous()
         dx, ddt, dA, dB, dC, dD, dz, dbias, dinit = torch.ops.mamba_cpu.ssd_bwd(
-            dout, dfinal, x, dt, A, B, C, D, z, dt_bias, init, *ctx.cfg, saved, ysave)
+            dout, dfinal, x, dt, A, B, C, D, z, dt_bias, init, *ctx.cfg, saved, ysave, seq_idx=seq_idx)
         return (dx, ddt, dA, dB.to(B.dtype), dC.to(C.dtype), dD if D is not None else None,
                 dz if z is not None else None, dbias if dt_bias is not None else None,
-                dinit if init is not None else None, None, None, None)
+                dinit if init is not None else None, None, None, None, None)
 
 
 def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
@@ -103,16 +107,17 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
     x: (batch, seqlen, nheads, headdim); dt: (batch, seqlen, nheads);
     A: (nheads,); B, C: (batch, seqlen, ngroups, dstate); D: (nheads, headdim)
     or (nheads,); z: like x; dt_bias: (nheads,); initial_states:
-    (batch, nheads, headdim, dstate). headdim a multiple of 16 up to 64,
-    dstate a multiple of 16 up to 128.
+    (batch, nheads, headdim, dstate); seq_idx: (batch, seqlen) integer ids,
+    non-decreasing along each row (not checked, as in mamba_ssm). headdim a
+    multiple of 16 up to 64, dstate a multiple of 16 up to 128.
     Returns out (like x, in x's dtype) [, final_states (batch, nheads, headdim,
-    dstate) float32]. Packed sequences (seq_idx, cu_seqlens,
+    dstate) float32]. Per-sequence final states (cu_seqlens,
     return_varlen_states) are not supported yet and raise NotImplementedError.
     """
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
-    if seq_idx is not None or cu_seqlens is not None or return_varlen_states:
-        raise NotImplementedError("mamba_chunk_scan_combined: seq_idx / cu_seqlens / return_varlen_states "
+    if cu_seqlens is not None or return_varlen_states:
+        raise NotImplementedError("mamba_chunk_scan_combined: cu_seqlens / return_varlen_states "
                                   "are not supported")
     if int(chunk_size) < 1:
         raise ValueError(f"chunk_size must be positive, got {chunk_size}")
@@ -135,12 +140,17 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
         None if initial_states is None else initial_states.float().contiguous(),
         bool(dt_softplus), lo, hi,
     )
+    if seq_idx is not None:
+        if seq_idx.shape != (b, l) or seq_idx.dtype.is_floating_point:
+            raise ValueError(f"seq_idx must hold integer ids of shape ({b}, {l}), got {tuple(seq_idx.shape)} "
+                             f"{seq_idx.dtype}")
+        seq_idx = seq_idx.to(device=x.device, dtype=torch.int32).contiguous()
     needs_grad = torch.is_grad_enabled() and any(
         isinstance(t, torch.Tensor) and t.requires_grad for t in args)
     if needs_grad:
-        out, final = _SsdScan.apply(*args)
+        out, final = _SsdScan.apply(*args, seq_idx)
     else:
-        out, final, _, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False)
+        out, final, _, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False, seq_idx=seq_idx)
     out = out.to(x.dtype)
     return (out, final) if return_final_states else out
 

@@ -12,6 +12,12 @@ contiguous groups that share B and C):
                                                        h_{-1} = initial_states or 0
     y_t  = h_t C_t + D x_t ;  out_t = y_t silu(z_t) when z is given
 
+With seq_idx (batch, seqlen) of non-decreasing sequence ids (packed
+sequences), the state does not carry across a change of id: the decay
+exp(dt_t A_h) is replaced by 0 where seq_idx[t] != seq_idx[t-1], and the
+initial state belongs to sequence id 0 (it is dropped when seq_idx[0] != 0),
+as mamba_ssm's kernels mask it (its state passing starts from sequence id 0).
+
 Layouts (mamba_ssm's): x, z, out (batch, seqlen, nheads, headdim); dt
 (batch, seqlen, nheads); A, dt_bias (nheads,); B, C (batch, seqlen, ngroups,
 dstate); D (nheads, headdim) or (nheads,); states (batch, nheads, headdim,
@@ -20,7 +26,8 @@ depend on a chunk size.
 
 Pinned by tests/test_oracle_ssd.py against the Mamba-1 oracle (A broadcast
 over each head's channels and states), a quadratic direct sum, and
-torch.autograd through that direct sum.
+torch.autograd through that direct sum; seq_idx by running each packed
+sequence on its own.
 """
 
 import numpy as np
@@ -53,8 +60,17 @@ def _D_full(D, nheads, headdim):
     return np.broadcast_to(D[:, None] if D.ndim == 1 else D, (nheads, headdim))
 
 
+def _keep(seq_idx, batch, seqlen):
+    """(batch, seqlen) 1.0 where the state carries into step t, else 0.0."""
+    if seq_idx is None:
+        return np.ones((batch, seqlen))
+    sq = np.asarray(seq_idx, dtype=np.int64).reshape(batch, seqlen)
+    prev = np.concatenate([np.zeros((batch, 1), dtype=np.int64), sq[:, :-1]], axis=1)
+    return (sq == prev).astype(np.float64)
+
+
 def ssd_fwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, dt_softplus=False,
-            dt_limit=(0.0, float("inf"))):
+            dt_limit=(0.0, float("inf")), seq_idx=None):
     """Forward. Returns (out (b, l, h, p), final_states (b, h, p, n))."""
     x, dt, A, B, C = map(_f64, (x, dt, A, B, C))
     D, z, dt_bias, init = map(_f64, (D, z, dt_bias, initial_states))
@@ -65,9 +81,10 @@ def ssd_fwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, d
     Dh = _D_full(D, nheads, headdim)
     h = np.zeros((batch, nheads, headdim, dstate)) if init is None else init.copy()
     y = np.zeros_like(x)
+    keep = _keep(seq_idx, batch, seqlen)
     with np.errstate(over="ignore", invalid="ignore"):
         for t in range(seqlen):
-            a = np.exp(step[:, t] * A[None])                               # (b, h)
+            a = np.exp(step[:, t] * A[None]) * keep[:, t, None]            # (b, h)
             h = a[..., None, None] * h + (step[:, t, :, None] * x[:, t])[..., None] * Bh[:, t, :, None, :]
             y[:, t] = (h * Ch[:, t, :, None, :]).sum(-1) + Dh[None] * x[:, t]
         out = y if z is None else y * z * sigmoid(z)
@@ -75,14 +92,14 @@ def ssd_fwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, d
 
 
 def ssd_bwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, dt_softplus=False,
-            dt_limit=(0.0, float("inf")), dout=None, dfinal_states=None):
+            dt_limit=(0.0, float("inf")), dout=None, dfinal_states=None, seq_idx=None):
     """Backward by the chain rule on the recurrence, walking t = L-1 .. 0 with
     G = dLoss/dh_t (headdim x dstate per head), started from dfinal_states:
         dy = dout silu(z) ; dz = dout y silu'(z)            (dy = dout without z)
         G += dy_t C_t^T ;  dC_t = sum over the group's heads of h_t^T dy_t
         dB_t = sum over the group's heads of (dt_t x_t)^T G ;  dx_t = dt_t G B_t + D dy_t
         dstep_t = <G, x_t B_t^T> + A <G, a_t h_{t-1}> ;  dA += dt_t <G, a_t h_{t-1}>
-        G <- a_t G     (a_t = exp(dt_t A))
+        G <- a_t G     (a_t = exp(dt_t A), or 0 where seq_idx starts a sequence)
     then dinitial_states = G, draw dt = dstep * softplus' * [inside dt_limit],
     ddt_bias = its sum over batch and sequence, and dD = sum of dy x.
     Returns (dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinitial_states); entries
@@ -101,7 +118,7 @@ def ssd_bwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, d
     with np.errstate(over="ignore", invalid="ignore"):
         hs = np.zeros((seqlen + 1, batch, nheads, headdim, dstate))       # hs[t + 1] = h_t
         hs[0] = 0.0 if init is None else init
-        a_all = np.exp(step * A[None, None])                                # (b, l, h)
+        a_all = np.exp(step * A[None, None]) * _keep(seq_idx, batch, seqlen)[..., None]  # (b, l, h)
         for t in range(seqlen):
             hs[t + 1] = a_all[:, t, :, None, None] * hs[t] + \
                 (step[:, t, :, None] * x[:, t])[..., None] * Bh[:, t, :, None, :]

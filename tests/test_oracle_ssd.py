@@ -13,7 +13,8 @@ CPU, so the GPU tests of the SSD kernels check against something known:
 - torch.autograd through that direct sum: every gradient of ssd_bwd,
   including the initial states';
 - a planted mistake in a copy of ssd_bwd (the decay term's dt dropped) fails
-  the autograd check.
+  the autograd check;
+- packed sequences (seq_idx) against each sequence run on its own.
 """
 
 import inspect
@@ -159,3 +160,61 @@ def test_planted_mistake_in_backward_is_caught():
     want.backward(torch.tensor(dout))
     dA = ns["ssd_bwd"](**c, dt_softplus=True, dout=dout)[2]
     assert not np.allclose(dA, t["A"].grad.numpy(), rtol=1e-6, atol=1e-8)
+
+
+def _segments(ids):
+    """[(start, end, id)] of the runs of equal ids in a 1-D array."""
+    out, s0 = [], 0
+    for t in range(1, len(ids) + 1):
+        if t == len(ids) or ids[t] != ids[s0]:
+            out.append((s0, t, int(ids[s0])))
+            s0 = t
+    return out
+
+
+def test_seq_idx_equals_separate_sequences():
+    """Packed sequences (seq_idx) give, on each sequence, what that sequence
+    gives run alone from a zero state (the one with id 0 from the initial
+    state): outputs and the gradients of x, dt, B, C, z on its steps, the final
+    state and its gradient on the last one, the initial state's gradient from
+    the id-0 one (zero when a row starts above id 0); dA, dD, ddt_bias are the
+    sums over sequences."""
+    b, l, h, p, n, g = 2, 50, 4, 8, 6, 2
+    c = ssd_case(b, l, h, p, n, g, seed=3, init=True)
+    seq = np.array([[0] * 13 + [1] * 20 + [2] * 17, [1] * 25 + [3] * 24 + [4]], dtype=np.int32)
+    kw = dict(dt_softplus=True, dt_limit=(0.0, float("inf")))
+    rng = np.random.default_rng(4)
+    dout, dfin = rng.standard_normal(c["x"].shape), rng.standard_normal(c["initial_states"].shape)
+    out, fin = S.ssd_fwd(**c, **kw, seq_idx=seq)
+    got = S.ssd_bwd(**c, **kw, dout=dout, dfinal_states=dfin, seq_idx=seq)
+    names = ("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "initial_states")
+    g_ = dict(zip(names, got))
+    per_step = ("x", "dt", "B", "C", "z")
+    sums = {k: 0.0 for k in ("A", "D", "dt_bias")}
+    for r in range(b):
+        segs = _segments(seq[r])
+        dinit_want = np.zeros((h, p, n))
+        for i, (s0, s1, sid) in enumerate(segs):
+            last = i == len(segs) - 1
+            sub = {k: c[k][r:r + 1, s0:s1] for k in per_step}
+            sub.update(A=c["A"], D=c["D"], dt_bias=c["dt_bias"],
+                       initial_states=c["initial_states"][r:r + 1] if sid == 0 else None)
+            o, f = S.ssd_fwd(**sub, **kw)
+            np.testing.assert_allclose(out[r, s0:s1], o[0], rtol=1e-12, atol=1e-12)
+            if last:
+                np.testing.assert_allclose(fin[r], f[0], rtol=1e-12, atol=1e-12)
+            sg = dict(zip(names, S.ssd_bwd(**sub, **kw, dout=dout[r:r + 1, s0:s1],
+                                           dfinal_states=dfin[r:r + 1] if last else None)))
+            for k in per_step:
+                np.testing.assert_allclose(g_[k][r, s0:s1], sg[k][0], rtol=1e-10, atol=1e-12, err_msg=k)
+            for k in sums:
+                sums[k] = sums[k] + sg[k]
+            if sid == 0:
+                dinit_want = sg["initial_states"][0]
+        np.testing.assert_allclose(g_["initial_states"][r], dinit_want, rtol=1e-10, atol=1e-12)
+    for k in sums:
+        np.testing.assert_allclose(g_[k], sums[k], rtol=1e-10, atol=1e-10, err_msg=k)
+    # all ids equal to 0 is the unpacked scan
+    o0, f0 = S.ssd_fwd(**c, **kw)
+    o1, f1 = S.ssd_fwd(**c, **kw, seq_idx=np.zeros((b, l), dtype=np.int32))
+    assert np.array_equal(o0, o1) and np.array_equal(f0, f1)

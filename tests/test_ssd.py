@@ -151,9 +151,11 @@ def test_empty_sequence_passes_the_initial_state_through():
 def test_rejects_unsupported_shapes_and_options():
     c = case(1, 16, 2, 16, 1, 16)
     dev = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    seq = torch.zeros(1, 16, dtype=torch.int32, device=DEV)
     with pytest.raises(NotImplementedError):
-        mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64,
-                                            seq_idx=torch.zeros(1, 16, dtype=torch.int32, device=DEV))
+        mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, seq_idx=seq, return_varlen_states=True)
+    with pytest.raises(ValueError, match="seq_idx"):
+        mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, seq_idx=seq[:, :8])
     bad = dict(dev, x=torch.randn(1, 16, 2, 24, device=DEV), z=None, D=None)
     with pytest.raises(NotImplementedError, match="headdim"):
         mamba_cpu.mamba_chunk_scan_combined(**bad, chunk_size=64)
@@ -162,20 +164,23 @@ def test_rejects_unsupported_shapes_and_options():
                                             chunk_size=64)
 
 
-def run_ops(c, head_block=0, chunk_pass=0, softplus=True, limit=(0.0, float("inf")), seed=1):
+def run_ops(c, head_block=0, chunk_pass=0, softplus=True, limit=(0.0, float("inf")), seed=1, seq=None):
     """Forward and backward through the operators with the chunk kernels'
     head block and the way chunk states are carried pinned: out, final
-    states, the nine gradients of sum(out W) + sum(final V), and W, V."""
+    states, the nine gradients of sum(out W) + sum(final V), and W, V.
+    seq: packed-sequence ids (batch, seqlen) or None."""
     d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
     if d["D"] is not None and d["D"].dim() == 1:   # the operator takes D per channel
         d["D"] = d["D"][:, None].expand(d["x"].shape[2:]).contiguous()
     args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
             softplus, float(limit[0]), float(limit[1]))
-    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, head_block, chunk_pass)
+    sq = None if seq is None else torch.as_tensor(seq, dtype=torch.int32).to(DEV)
+    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, head_block, chunk_pass, seq_idx=sq)
     gen = torch.Generator().manual_seed(seed)
     W = torch.randn(out.shape, generator=gen).to(out.dtype)
     V = torch.randn(fin.shape, generator=gen)
-    g = torch.ops.mamba_cpu.ssd_bwd(W.to(DEV), V.to(DEV), *args, saved, ysave, head_block, chunk_pass)
+    g = torch.ops.mamba_cpu.ssd_bwd(W.to(DEV), V.to(DEV), *args, saved, ysave, head_block, chunk_pass,
+                                    seq_idx=sq)
     torch.cuda.synchronize()
     return out, fin, g, W, V
 
@@ -208,9 +213,9 @@ def test_head_blocks_match_oracle(shape, blocks):
             assert torch.equal(out, first[0]) and torch.equal(fin, first[1])
 
 
-def check_ops(c, got, softplus=True, limit=(0.0, float("inf")), low=False):
+def check_ops(c, got, softplus=True, limit=(0.0, float("inf")), low=False, seq=None):
     out, fin, g, W, V = got
-    kw = dict(dt_softplus=softplus, dt_limit=limit)
+    kw = dict(dt_softplus=softplus, dt_limit=limit, seq_idx=seq)
     want = S.ssd_fwd(**c, **kw)
     tol = (2e-2, 2e-2) if low else (1e-4, 1e-5)
     assert_close_report(out, want[0], *tol, "out")
