@@ -375,6 +375,17 @@ size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a);
 /* Backward, given the forward's saved buffer (and ysave when z is given). */
 int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes, void* workspace,
                  size_t workspace_bytes, void* stream);
+/* Per-sequence final states of packed sequences (mamba_ssm's
+ * return_varlen_states with cu_seqlens; none in the reference), after
+ * mcpu_ssd_fwd with the same arguments, on the same stream, given the saved
+ * buffer it filled. batch must be 1. cu_seqlens: nseqs + 1 int32 offsets into
+ * the sequence, non-decreasing from 0 to seqlen. varlen_states (nseqs,
+ * nheads, headdim, dstate) float32: entry i is the scan's state after step
+ * cu_seqlens[i + 1] - 1, with seq_idx as given (pass ids that mark the same
+ * sequences so that each state is its own sequence's); zeros for an empty
+ * sequence or offsets outside [0, seqlen]. No gradient. */
+int mcpu_ssd_varlen_states(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes,
+                           const int32_t* cu_seqlens, int64_t nseqs, float* varlen_states, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused single-token Mamba block step (decode).                             */

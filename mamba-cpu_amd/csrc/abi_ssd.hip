@@ -192,6 +192,30 @@ extern "C" int mcpu_ssd_fwd(const mcpu_ssd_args* a, void* saved, size_t saved_by
   return hip_status(ssd_fwd_launch(p, a->dtype, static_cast<hipStream_t>(stream)), "ssd_fwd launch");
 }
 
+extern "C" int mcpu_ssd_varlen_states(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes,
+                                      const int32_t* cu_seqlens, int64_t nseqs, float* varlen_states, void* stream) {
+  clear_error();
+  if (int rc = check_ssd(a)) return rc;
+  if (a->batch != 1)
+    return fail(MCPU_ERR_INVALID, "ssd_varlen_states: packed sequences need batch 1, got %lld", (long long)a->batch);
+  if (nseqs < 0 || nseqs > 0x7fffffffll)
+    return fail(MCPU_ERR_INVALID, "ssd_varlen_states: bad sequence count %lld", (long long)nseqs);
+  if (nseqs == 0) return MCPU_OK;
+  if (cu_seqlens == nullptr || varlen_states == nullptr)
+    return fail(MCPU_ERR_INVALID, "ssd_varlen_states: cu_seqlens and varlen_states are required");
+  SsdParams p = make_ssd(a);
+  const size_t need = saved_layout(p).total;
+  if (need > 0 && (saved == nullptr || saved_bytes < need))
+    return fail(MCPU_ERR_INVALID, "ssd_varlen_states: the forward's saved buffer of %zu bytes is needed, got %zu",
+                need, saved_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->seqlen == 0)  // every sequence is empty
+    return zero_f32(varlen_states, nseqs * a->nheads * a->headdim * a->dstate, st);
+  bind_saved(p, saved);
+  return hip_status(ssd_varlen_launch(p, cu_seqlens, nseqs, varlen_states, a->dtype, st), "ssd_varlen_states launch");
+}
+
 extern "C" size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a) {
   if (check_ssd(a) != MCPU_OK) {
     clear_error();

@@ -1317,6 +1317,74 @@ __global__ void __launch_bounds__(kThreads3, 2) ssd_bwd_chunk_kernel(const SsdPa
   }
 }
 
+// Per-sequence final states of packed sequences in batch row 0 (mamba_ssm's
+// varlen states): entry i is the state after step e = cu[i + 1] - 1. From the
+// chunk c holding e, h_e = exp(cs_e) H_c (when step e is in the entering
+// state's sequence) + sum_s exp(cs_e - cs_s) dt_s x_s B_s^T over the steps
+// s <= e of e's sequence in the chunk: one product on the matrix cores,
+// started from the decayed entering state. Empty sequences, and offsets
+// outside [0, seqlen], give zeros. Grid (nseqs, nheads); wave w computes state
+// rows [16 w, 16 w + 16).
+template <typename Tx, bool SEQ>
+__global__ void __launch_bounds__(kThreads) ssd_varlen_state_kernel(const SsdParams p, const int32_t* cu,
+                                                                     float* out) {
+  __shared__ __align__(16) float s_B[Q][NP];
+  __shared__ __align__(16) float s_x[Q][XP];
+  __shared__ float s_sc[Q];
+  const int64_t i = blockIdx.x, h = blockIdx.y, b = 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t L = p.seqlen, H = p.nheads, P = p.headdim, N = p.dstate, G = p.ngroups;
+  const int64_t g = h / (H / G);
+  const int nt = static_cast<int>(N / 16);
+  const bool act = 16 * wave < P;
+  const int64_t eo = (16 * wave + 4 * q) * N + r;   // accumulator (j, e) at eo + e N + 16 j of a block
+  float* dst = out + (i * H + h) * P * N + eo;
+  v4f acc[kSsdMaxN / 16];
+  zero(acc);
+  const int64_t start = cu[i], end = cu[i + 1];
+  if (start < 0 || end > L || end <= start) {  // the same for the whole workgroup
+    if (act)
+#pragma unroll
+      for (int j = 0; j < kSsdMaxN / 16; ++j)
+        if (j < nt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[e * N + 16 * j] = 0.f;
+    return;
+  }
+  const int64_t last = end - 1, c = last / Q, t0 = c * Q;
+  const int nv = static_cast<int>(last - t0 + 1);
+  const int64_t row = chunk_row(p, b, h, c);
+  const float cse = p.cs[row + nv - 1], loe = p.cs_lo[row + nv - 1];
+  stage<Tx, kVecN>(&s_B[0][0], NP, static_cast<const Tx*>(p.B) + ((b * L + t0) * G + g) * N, G * N, Q, nv,
+                   static_cast<int>(N));
+  if (wave == 0) {
+    const bool in = lane < nv && seq_of<SEQ>(p, b, t0 + lane) == seq_of<SEQ>(p, b, last);
+    s_sc[lane] = in ? p.step[row + lane] * fast_exp((cse - p.cs[row + lane]) + (loe - p.cs_lo[row + lane])) : 0.f;
+  }
+  __syncthreads();
+  stage<Tx, kVecX>(&s_x[0][0], XP, static_cast<const Tx*>(p.x) + ((b * L + t0) * H + h) * P, H * P, Q, nv,
+                   static_cast<int>(P), s_sc);
+  if (act && seq_of<SEQ>(p, b, last) == seq_of<SEQ>(p, b, t0 - 1)) {
+    const float hd = fast_exp(cse + loe);
+    const float* hs = p.states + state_block(p, b, c, h) + eo;
+#pragma unroll
+    for (int j = 0; j < kSsdMaxN / 16; ++j)
+      if (j < nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j][e] = hd * hs[e * N + 16 * j];
+  }
+  __syncthreads();
+  if (act) {
+    mma(acc, nt, &s_x[0][16 * wave], 1, XP, &s_B[0][0], NP, 1, Q);
+#pragma unroll
+    for (int j = 0; j < kSsdMaxN / 16; ++j)
+      if (j < nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e * N + 16 * j] = acc[j][e];
+  }
+}
+
 namespace {
 
 template <typename Tx, bool SEQ>
@@ -1370,6 +1438,26 @@ hipError_t ssd_fwd_launch(const SsdParams& p, int dtype, hipStream_t st) {
     case MCPU_BF16: return seq ? fwd_t<bf16, true>(p, st) : fwd_t<bf16, false>(p, st);
     default: return seq ? fwd_t<f16, true>(p, st) : fwd_t<f16, false>(p, st);
   }
+}
+
+hipError_t ssd_varlen_launch(const SsdParams& p, const int32_t* cu, int64_t nseqs, float* out, int dtype,
+                             hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(nseqs), static_cast<unsigned>(p.nheads));
+  const bool seq = p.seq_idx != nullptr;
+  switch (dtype) {
+    case MCPU_F32:
+      if (seq) hipLaunchKernelGGL((ssd_varlen_state_kernel<float, true>), grid, dim3(kThreads), 0, st, p, cu, out);
+      else hipLaunchKernelGGL((ssd_varlen_state_kernel<float, false>), grid, dim3(kThreads), 0, st, p, cu, out);
+      break;
+    case MCPU_BF16:
+      if (seq) hipLaunchKernelGGL((ssd_varlen_state_kernel<bf16, true>), grid, dim3(kThreads), 0, st, p, cu, out);
+      else hipLaunchKernelGGL((ssd_varlen_state_kernel<bf16, false>), grid, dim3(kThreads), 0, st, p, cu, out);
+      break;
+    default:
+      if (seq) hipLaunchKernelGGL((ssd_varlen_state_kernel<f16, true>), grid, dim3(kThreads), 0, st, p, cu, out);
+      else hipLaunchKernelGGL((ssd_varlen_state_kernel<f16, false>), grid, dim3(kThreads), 0, st, p, cu, out);
+  }
+  return hipGetLastError();
 }
 
 hipError_t ssd_bwd_launch(const SsdParams& p, int dtype, hipStream_t st) {

@@ -70,5 +70,9 @@ struct SsdParams {
 
 hipError_t ssd_fwd_launch(const SsdParams& p, int dtype, hipStream_t st);
 hipError_t ssd_bwd_launch(const SsdParams& p, int dtype, hipStream_t st);
+// Per-sequence final states (nseqs, nheads, headdim, dstate) of batch row 0
+// after the forward; cu holds nseqs + 1 sequence offsets.
+hipError_t ssd_varlen_launch(const SsdParams& p, const int32_t* cu, int64_t nseqs, float* out, int dtype,
+                             hipStream_t st);
 
 }  // namespace mcpu

@@ -1215,6 +1215,32 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tenso
   return {dx, ddt, dA, dB, dC, dD, dz, dbias, dinit};
 }
 
+// Per-sequence final states (nseqs, nheads, headdim, dstate) float32 of the
+// packed sequences of batch row 0, from the forward's saved buffer;
+// cu_seqlens (nseqs + 1) int32 offsets.
+Tensor ssd_varlen_states(const Tensor& x, const Tensor& dt, const Tensor& A, const Tensor& B, const Tensor& C,
+                         const optional<Tensor>& D, const optional<Tensor>& z, const optional<Tensor>& dt_bias,
+                         const optional<Tensor>& init, bool softplus, double lo, double hi, const Tensor& saved,
+                         const Tensor& cu_seqlens, int64_t head_block, int64_t chunk_pass,
+                         const optional<Tensor>& seq_idx) {
+  const char* name = "mamba_cpu::ssd_varlen_states";
+  mcpu_ssd_args a =
+      ssd_args(name, x, dt, A, B, C, D, z, dt_bias, init, softplus, lo, hi, head_block, chunk_pass, seq_idx);
+  check_gpu(name, opt(cu_seqlens));
+  TORCH_CHECK_VALUE(cu_seqlens.scalar_type() == at::kInt && cu_seqlens.dim() == 1 && cu_seqlens.numel() >= 1 &&
+                        cu_seqlens.is_contiguous(),
+                    name, " expects contiguous int32 cu_seqlens (nseqs + 1)");
+  TORCH_CHECK_VALUE(saved.scalar_type() == at::kByte && saved.is_cuda(), name, " expects the forward's saved buffer");
+  c10::DeviceGuard guard(x.device());
+  const int64_t nseqs = cu_seqlens.numel() - 1;
+  Tensor out = at::empty({nseqs, a.nheads, a.headdim, a.dstate}, x.options().dtype(at::kFloat));
+  check_rc(mcpu_ssd_varlen_states(&a, saved.data_ptr(), saved.numel(),
+                                  static_cast<const int32_t*>(cu_seqlens.data_ptr()), nseqs,
+                                  static_cast<float*>(out.data_ptr()), stream_of(x)),
+           name);
+  return out;
+}
+
 // ---- fused single-token block step ----------------------------------------------
 
 // One decode step of a Mamba-1 block (mcpu_mixer_step): hidden (batch,
@@ -1340,6 +1366,9 @@ TORCH_LIBRARY(mamba_cpu, m) {
         "Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, "
         "float dt_hi, Tensor saved, Tensor ysave, int head_block=0, int chunk_pass=0, Tensor? seq_idx=None) -> "
         "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("ssd_varlen_states(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
+        "Tensor? dt_bias, Tensor? initial_states, bool dt_softplus, float dt_lo, float dt_hi, Tensor saved, "
+        "Tensor cu_seqlens, int head_block=0, int chunk_pass=0, Tensor? seq_idx=None) -> Tensor");
   m.def("selective_scan_fwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
         "Tensor? z, Tensor? delta_bias, bool delta_softplus) -> (Tensor, Tensor)");
   m.def("selective_scan_bwd(Tensor u, Tensor delta, Tensor A, Tensor B, Tensor C, Tensor? D, "
@@ -1396,6 +1425,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("selective_state_update", &selective_state_update);
   m.impl("ssd_fwd", &ssd_fwd);
   m.impl("ssd_bwd", &ssd_bwd);
+  m.impl("ssd_varlen_states", &ssd_varlen_states);
   m.impl("mixer_step", &mixer_step);
 }
 

@@ -167,6 +167,8 @@ lib.mcpu_ssd_bwd_workspace_size.argtypes = [_ARGP["ssd"]]
 lib.mcpu_ssd_bwd_workspace_size.restype = ctypes.c_size_t
 lib.mcpu_ssd_bwd.argtypes = [_ARGP["ssd"], _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]
 lib.mcpu_ssd_bwd.restype = ctypes.c_int
+lib.mcpu_ssd_varlen_states.argtypes = [_ARGP["ssd"], _P, ctypes.c_size_t, _P, ctypes.c_int64, _P, _P]
+lib.mcpu_ssd_varlen_states.restype = ctypes.c_int
 lib.mcpu_mixer_step_workspace_size.argtypes = [_ARGP["mixer_step"]]
 lib.mcpu_mixer_step_workspace_size.restype = ctypes.c_size_t
 lib.mcpu_mixer_step.argtypes = [_ARGP["mixer_step"], _P, ctypes.c_size_t, _P]

@@ -72,21 +72,35 @@ def _(dout, dfinal_states, x, dt, A, B, C, D, z, dt_bias, initial_states, dt_sof
             A.new_empty(initial_states.shape, **f32) if initial_states is not None else A.new_empty(0))
 
 
+@torch.library.register_fake("mamba_cpu::ssd_varlen_states")
+def _(x, dt, A, B, C, D, z, dt_bias, initial_states, dt_softplus, dt_lo, dt_hi, saved, cu_seqlens,
+      head_block=0, chunk_pass=0, seq_idx=None):
+    return x.new_empty(cu_seqlens.shape[0] - 1, x.shape[2], x.shape[3], B.shape[-1], dtype=torch.float32)
+
+
+def _varlen(args, saved, cu_seqlens, seq_idx):
+    return torch.ops.mamba_cpu.ssd_varlen_states(*args, saved, cu_seqlens, seq_idx=seq_idx)
+
+
 class _SsdScan(torch.autograd.Function):
     """Autograd of the SSD scan: the forward keeps its per-chunk decays and
-    states (and y before the z gate), the backward reads them."""
+    states (and y before the z gate), the backward reads them. Per-sequence
+    final states, when asked for, carry no gradient (as in mamba_ssm)."""
 
     @staticmethod
-    def forward(ctx, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, seq_idx):
-        out, final, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(
-            x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, True, seq_idx=seq_idx)
+    def forward(ctx, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi, seq_idx, cu_seqlens):
+        args = (x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, lo, hi)
+        out, final, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, seq_idx=seq_idx)
+        varlen = x.new_empty(0, dtype=torch.float32) if cu_seqlens is None else _varlen(args, saved, cu_seqlens,
+                                                                                         seq_idx)
+        ctx.mark_non_differentiable(varlen)
         ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, initial_states, saved, ysave, seq_idx)
         ctx.cfg = (softplus, lo, hi)
         ctx.set_materialize_grads(False)
-        return out, final
+        return out, final, varlen
 
     @staticmethod
-    def backward(ctx, dout, dfinal):
+    def backward(ctx, dout, dfinal, _dvarlen):
         x, dt, A, B, C, D, z, dt_bias, init, saved, ysave, seq_idx = ctx.saved_tensors
         dout = torch.zeros_like(x) if dout is None else _aligned(dout.to(x.dtype).contiguous())
         dfinal = None if dfinal is None else dfinal.float().contiguous()
@@ -94,7 +108,7 @@ class _SsdScan(torch.autograd.Function):
             dout, dfinal, x, dt, A, B, C, D, z, dt_bias, init, *ctx.cfg, saved, ysave, seq_idx=seq_idx)
         return (dx, ddt, dA, dB.to(B.dtype), dC.to(C.dtype), dD if D is not None else None,
                 dz if z is not None else None, dbias if dt_bias is not None else None,
-                dinit if init is not None else None, None, None, None, None)
+                dinit if init is not None else None, None, None, None, None, None)
 
 
 def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
@@ -111,14 +125,24 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
     non-decreasing along each row (not checked, as in mamba_ssm). headdim a
     multiple of 16 up to 64, dstate a multiple of 16 up to 128.
     Returns out (like x, in x's dtype) [, final_states (batch, nheads, headdim,
-    dstate) float32]. Per-sequence final states (cu_seqlens,
-    return_varlen_states) are not supported yet and raise NotImplementedError.
+    dstate) float32] [, varlen_states (nseqs, nheads, headdim, dstate)
+    float32]. varlen_states (return_varlen_states, batch 1, cu_seqlens the
+    nseqs + 1 offsets of the packed sequences, seq_idx marking the same
+    sequences): the state after each sequence's last step, zeros for an empty
+    sequence, without gradient.
     """
     if x.device.type != "cuda":
         raise ValueError(f"mamba_cpu (MI355X build) runs on ROCm GPU tensors, got device {x.device}")
-    if cu_seqlens is not None or return_varlen_states:
-        raise NotImplementedError("mamba_chunk_scan_combined: cu_seqlens / return_varlen_states "
-                                  "are not supported")
+    if return_varlen_states:
+        if cu_seqlens is None or seq_idx is None:
+            raise ValueError("return_varlen_states needs cu_seqlens and the seq_idx of the same sequences")
+        if x.shape[0] != 1:
+            raise ValueError(f"return_varlen_states needs batch 1, got {x.shape[0]}")
+        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1 or cu_seqlens.dtype.is_floating_point:
+            raise ValueError("cu_seqlens must be a 1-D integer tensor of nseqs + 1 offsets")
+        cu_seqlens = cu_seqlens.to(device=x.device, dtype=torch.int32).contiguous()
+    else:
+        cu_seqlens = None   # accepted and unused, as mamba_ssm computes and drops the states
     if int(chunk_size) < 1:
         raise ValueError(f"chunk_size must be positive, got {chunk_size}")
     if x.dim() != 4 or dt.dim() != 3 or B.dim() != 4 or C.dim() != 4 or A.dim() != 1:
@@ -148,11 +172,15 @@ def mamba_chunk_scan_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bia
     needs_grad = torch.is_grad_enabled() and any(
         isinstance(t, torch.Tensor) and t.requires_grad for t in args)
     if needs_grad:
-        out, final = _SsdScan.apply(*args, seq_idx)
+        out, final, varlen = _SsdScan.apply(*args, seq_idx, cu_seqlens)
     else:
-        out, final, _, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False, seq_idx=seq_idx)
+        out, final, saved, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False, seq_idx=seq_idx)
+        varlen = None if cu_seqlens is None else _varlen(args, saved, cu_seqlens, seq_idx)
     out = out.to(x.dtype)
-    return (out, final) if return_final_states else out
+    res = (out, final) if return_final_states else (out,)
+    if return_varlen_states:
+        res = res + (varlen,)
+    return res if len(res) > 1 else out
 
 
 def ssd_flops(batch, seqlen, nheads, headdim, ngroups, dstate, backward=False):

@@ -91,6 +91,33 @@ def ssd_fwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, d
     return out, h
 
 
+def ssd_varlen_states(x, dt, A, B, C, cu_seqlens, dt_bias=None, initial_states=None, dt_softplus=False,
+                      dt_limit=(0.0, float("inf")), seq_idx=None):
+    """Per-sequence final states of packed sequences in batch row 0 (the
+    result of mamba_ssm's return_varlen_states): (nseqs, h, p, n), entry i
+    the recurrence's state after step cu_seqlens[i + 1] - 1, zeros for an
+    empty sequence. The same recurrence as ssd_fwd (seq_idx included)."""
+    x, dt, A, B = map(_f64, (x, dt, A, B))
+    dt_bias, init = map(_f64, (dt_bias, initial_states))
+    batch, seqlen, nheads, headdim = x.shape
+    step, _ = _dt(dt, dt_bias, dt_softplus, dt_limit)
+    Bh = _per_head(B, nheads)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    h = np.zeros((nheads, headdim, B.shape[-1])) if init is None else init[0].copy()
+    keep = _keep(seq_idx, batch, seqlen)[0]
+    after = [h.copy()]                                                      # after[t + 1] = h_t
+    with np.errstate(over="ignore", invalid="ignore"):
+        for t in range(seqlen):
+            h = np.exp(step[0, t] * A) [:, None, None] * keep[t] * h + \
+                (step[0, t, :, None] * x[0, t])[..., None] * Bh[0, t, :, None, :]
+            after.append(h)
+    out = np.zeros((len(cu) - 1,) + h.shape)
+    for i in range(len(cu) - 1):
+        if cu[i + 1] > cu[i]:
+            out[i] = after[cu[i + 1]]
+    return out
+
+
 def ssd_bwd(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, dt_softplus=False,
             dt_limit=(0.0, float("inf")), dout=None, dfinal_states=None, seq_idx=None):
     """Backward by the chain rule on the recurrence, walking t = L-1 .. 0 with

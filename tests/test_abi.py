@@ -476,6 +476,29 @@ def test_ssd_rejects_bad_arguments_before_touching_a_device():
     assert rc == _C.MCPU_ERR_INVALID and "aligned" in msg
 
 
+def test_ssd_varlen_states_rejects_bad_arguments_before_touching_a_device():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    var = lambda a, cu=16, n=2, out=16, saved=None, nbytes=0: _rc(  # noqa: E731
+        L.mcpu_ssd_varlen_states, ctypes.byref(a), saved, nbytes, cu, n, out, None)
+    rc, msg = var(_ssd_args())
+    assert rc == _C.MCPU_ERR_INVALID and "batch 1" in msg
+    one = _ssd_args(batch=1)
+    rc, msg = var(one, n=-1)
+    assert rc == _C.MCPU_ERR_INVALID and "count" in msg
+    rc, msg = var(one, cu=None)
+    assert rc == _C.MCPU_ERR_INVALID and "cu_seqlens" in msg
+    rc, msg = var(one, out=None)
+    assert rc == _C.MCPU_ERR_INVALID and "varlen_states" in msg
+    rc, msg = var(one)
+    assert rc == _C.MCPU_ERR_INVALID and "saved" in msg
+    rc, msg = var(_ssd_args(batch=1, headdim=24))
+    assert rc == _C.MCPU_ERR_UNSUPPORTED and "headdim" in msg
+    # no sequences: nothing to do, nothing touched
+    assert var(one, cu=None, n=0, out=None)[0] == _C.MCPU_OK
+
+
 def test_ssd_sizes_follow_the_layout():
     """The saved buffer holds three float32 (batch, nheads, nchunks, 64) arrays
     and the per-chunk states, each 256-byte aligned; the Python fake kernel

@@ -218,3 +218,33 @@ def test_seq_idx_equals_separate_sequences():
     o0, f0 = S.ssd_fwd(**c, **kw)
     o1, f1 = S.ssd_fwd(**c, **kw, seq_idx=np.zeros((b, l), dtype=np.int32))
     assert np.array_equal(o0, o1) and np.array_equal(f0, f1)
+
+
+def test_varlen_states_equal_each_sequence_alone():
+    """ssd_varlen_states: entry i is the final state of sequence i run alone
+    (from the initial state when it is the id-0 first sequence), zeros for an
+    empty sequence; without seq_idx, the final state of the prefix up to the
+    sequence's last step; the last entry is ssd_fwd's final state when the last
+    sequence ends the row."""
+    l, h, p, n, g = 60, 4, 8, 6, 2
+    c = ssd_case(1, l, h, p, n, g, seed=5, init=True)
+    kw = dict(dt_softplus=True, dt_limit=(0.0, float("inf")))
+    cu = np.array([0, 9, 9, 31, 60])
+    seq = np.repeat(np.arange(4), np.diff(cu))[None].astype(np.int32)
+    args = {k: c[k] for k in ("x", "dt", "A", "B", "C", "dt_bias", "initial_states")}
+    got = S.ssd_varlen_states(**args, cu_seqlens=cu, seq_idx=seq, **kw)
+    assert got.shape == (4, h, p, n)
+    for i in range(4):
+        s0, s1 = cu[i], cu[i + 1]
+        if s1 == s0:
+            assert not got[i].any()
+            continue
+        sub = {k: c[k][:, s0:s1] for k in ("x", "dt", "B", "C", "z")}
+        sub.update(A=c["A"], D=c["D"], dt_bias=c["dt_bias"], initial_states=c["initial_states"] if s0 == 0 else None)
+        np.testing.assert_allclose(got[i], S.ssd_fwd(**sub, **kw)[1][0], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got[-1], S.ssd_fwd(**c, **kw, seq_idx=seq)[1][0], rtol=1e-12, atol=1e-12)
+    plain = S.ssd_varlen_states(**args, cu_seqlens=cu, **kw)
+    for i in (0, 2, 3):
+        pre = {k: c[k][:, :cu[i + 1]] for k in ("x", "dt", "B", "C", "z")}
+        pre.update(A=c["A"], D=c["D"], dt_bias=c["dt_bias"], initial_states=c["initial_states"])
+        np.testing.assert_allclose(plain[i], S.ssd_fwd(**pre, **kw)[1][0], rtol=1e-12, atol=1e-12)

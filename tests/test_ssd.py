@@ -152,7 +152,7 @@ def test_rejects_unsupported_shapes_and_options():
     c = case(1, 16, 2, 16, 1, 16)
     dev = {k: None if v is None else v.to(DEV) for k, v in c.items()}
     seq = torch.zeros(1, 16, dtype=torch.int32, device=DEV)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="cu_seqlens"):
         mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, seq_idx=seq, return_varlen_states=True)
     with pytest.raises(ValueError, match="seq_idx"):
         mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, seq_idx=seq[:, :8])

@@ -9,9 +9,14 @@ the two ways chunk states are carried; 16-bit storage; the autograd path
 through mamba_chunk_scan_combined with int64 ids. At 2048 steps (beyond
 what the oracle finishes quickly) a packed run is checked against the same
 sequences run one at a time on the GPU. Ids that are all 0 give the result
-without seq_idx bit for bit (every mask is open). Tolerances as in
-tests/test_ssd.py: float32 outputs rtol 1e-4 / atol 1e-5, gradients rtol
-1e-3 with atol 1e-4 (dx, ddt, dz) or 1e-3 (sums); 16-bit storage 2e-2.
+without seq_idx bit for bit (every mask is open). Per-sequence final states
+(cu_seqlens, return_varlen_states) against oracle.ssd_varlen_states: empty
+and one-step sequences, ends on chunk edges, a first sequence that ends
+inside the first chunk with an initial state, both ways of carrying chunk
+states, 16-bit storage, and through mamba_chunk_scan_combined with autograd.
+Tolerances as in tests/test_ssd.py: float32 outputs and states rtol 1e-4 /
+atol 1e-5, gradients rtol 1e-3 with atol 1e-4 (dx, ddt, dz) or 1e-3 (sums);
+16-bit storage 2e-2.
 """
 
 import numpy as np
@@ -19,6 +24,7 @@ import pytest
 import torch
 
 from conftest import assert_close_report
+from oracle import ssd as S
 from test_ssd import DEV, NAMES, case, check_ops, run_ops
 
 import mamba_cpu
@@ -147,3 +153,86 @@ def test_packed_equals_separate_at_2048_steps(chunk_pass):
             sums[k] += gs[NAMES.index(k)]
     for k, v in sums.items():
         assert_close_report(g[NAMES.index(k)], v, 1e-3, 1e-3, f"d{k}")
+
+
+VARLEN = {
+    # name: (seqlen, cu_seqlens)
+    "inside-chunks": (200, [0, 30, 100, 150, 200]),
+    "chunk-edges": (260, [0, 64, 128, 192, 260]),
+    "empty-and-one-step": (130, [0, 0, 1, 65, 65, 130]),
+    "first-ends-in-chunk-0": (150, [0, 20, 150]),
+}
+
+
+def _varlen_ops(c, cu, seq, chunk_pass=0, softplus=True):
+    d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    if d["D"] is not None and d["D"].dim() == 1:
+        d["D"] = d["D"][:, None].expand(d["x"].shape[2:]).contiguous()
+    args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
+            softplus, 0.0, float("inf"))
+    sq = torch.as_tensor(seq, dtype=torch.int32).to(DEV)
+    out, fin, saved, _ = torch.ops.mamba_cpu.ssd_fwd(*args, False, 0, chunk_pass, seq_idx=sq)
+    var = torch.ops.mamba_cpu.ssd_varlen_states(*args, saved, torch.as_tensor(cu, dtype=torch.int32).to(DEV), 0,
+                                                chunk_pass, seq_idx=sq)
+    torch.cuda.synchronize()
+    return var, fin
+
+
+@pytest.mark.parametrize("layout", list(VARLEN), ids=list(VARLEN))
+@pytest.mark.parametrize("chunk_pass", [1, 2], ids=["two-launch", "in-order"])
+def test_varlen_states_match_oracle(layout, chunk_pass):
+    """Per-sequence final states (return_varlen_states) against the oracle:
+    zeros for empty sequences; the initial state reaches the id-0 first
+    sequence, also when it ends inside the first chunk; the last entry is
+    the final state."""
+    l, cu = VARLEN[layout]
+    seq = np.repeat(np.arange(len(cu) - 1), np.diff(cu))[None].astype(np.int32)
+    c = case(1, l, 4, 32, 2, 64, seed=7 + l, init=True)
+    print(f" {layout} chunk_pass {chunk_pass} cu {cu}", flush=True)
+    var, fin = _varlen_ops(c, cu, seq, chunk_pass)
+    want = S.ssd_varlen_states(c["x"], c["dt"], c["A"], c["B"], c["C"], cu, dt_bias=c["dt_bias"],
+                               initial_states=c["initial_states"], dt_softplus=True, seq_idx=seq)
+    assert_close_report(var, want, 1e-4, 1e-5, "varlen_states")
+    for i in np.flatnonzero(np.diff(cu) == 0):
+        assert not var[i].any()
+    assert_close_report(var[-1], fin[0], 1e-4, 1e-5, "last = final")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_states_low_precision(dtype):
+    cu = [0, 50, 64, 190, 300]
+    seq = np.repeat(np.arange(4), np.diff(cu))[None].astype(np.int32)
+    c = case(1, 300, 8, 64, 1, 128, seed=3, init=True, dtype=dtype)
+    want = S.ssd_varlen_states(c["x"], c["dt"], c["A"], c["B"], c["C"], cu, dt_bias=c["dt_bias"],
+                               initial_states=c["initial_states"], dt_softplus=True, seq_idx=seq)
+    for cp in (1, 2):
+        var, _ = _varlen_ops(c, cu, seq, cp)
+        assert_close_report(var, want, 2e-2, 2e-2, f"varlen_states cp{cp}")
+
+
+def test_varlen_states_through_the_function():
+    """mamba_chunk_scan_combined(..., return_final_states=True,
+    return_varlen_states=True) returns (out, final, varlen) with autograd on
+    the inputs; varlen carries no gradient; the same results without
+    autograd; out and final as without cu_seqlens."""
+    cu = [0, 40, 41, 140]
+    seq = torch.as_tensor(np.repeat(np.arange(3), np.diff(cu))[None], device=DEV)
+    c = case(1, 140, 4, 32, 1, 32, seed=12, init=True)
+    dev = {k: None if v is None else v.to(DEV).requires_grad_(True) for k, v in c.items()}
+    kw = dict(chunk_size=256, dt_softplus=True, seq_idx=seq, return_final_states=True)
+    out, fin, var = mamba_cpu.mamba_chunk_scan_combined(
+        **dev, cu_seqlens=torch.as_tensor(cu, device=DEV), return_varlen_states=True, **kw)
+    assert not var.requires_grad and out.requires_grad
+    (out.sum() + fin.sum()).backward()
+    with torch.no_grad():
+        out2, fin2, var2 = mamba_cpu.mamba_chunk_scan_combined(
+            **dev, cu_seqlens=torch.as_tensor(cu, device=DEV), return_varlen_states=True, **kw)
+        out3, fin3 = mamba_cpu.mamba_chunk_scan_combined(**dev, **kw)
+    assert torch.equal(out, out2) and torch.equal(fin, fin2) and torch.equal(var, var2)
+    assert torch.equal(out, out3) and torch.equal(fin, fin3)
+    want = S.ssd_varlen_states(c["x"], c["dt"], c["A"], c["B"], c["C"], cu, dt_bias=c["dt_bias"],
+                               initial_states=c["initial_states"], dt_softplus=True, seq_idx=seq.cpu().numpy())
+    assert_close_report(var, want, 1e-4, 1e-5, "varlen_states")
+    with pytest.raises(ValueError, match="seq_idx"):
+        mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, cu_seqlens=torch.as_tensor(cu, device=DEV),
+                                            return_varlen_states=True)
