@@ -13,7 +13,8 @@ without seq_idx bit for bit (every mask is open). Per-sequence final states
 (cu_seqlens, return_varlen_states) against oracle.ssd_varlen_states: empty
 and one-step sequences, ends on chunk edges, a first sequence that ends
 inside the first chunk with an initial state, both ways of carrying chunk
-states, 16-bit storage, and through mamba_chunk_scan_combined with autograd.
+states, 16-bit storage, and through mamba_chunk_scan_combined with autograd;
+opcheck of the operators with seq_idx and of ssd_varlen_states.
 Tolerances as in tests/test_ssd.py: float32 outputs and states rtol 1e-4 /
 atol 1e-5, gradients rtol 1e-3 with atol 1e-4 (dx, ddt, dz) or 1e-3 (sums);
 16-bit storage 2e-2.
@@ -236,3 +237,19 @@ def test_varlen_states_through_the_function():
     with pytest.raises(ValueError, match="seq_idx"):
         mamba_cpu.mamba_chunk_scan_combined(**dev, chunk_size=64, cu_seqlens=torch.as_tensor(cu, device=DEV),
                                             return_varlen_states=True)
+
+
+def test_opcheck_with_seq_idx_and_varlen_states():
+    """opcheck of ssd_fwd / ssd_bwd with seq_idx and of ssd_varlen_states."""
+    cu = [0, 30, 31, 70]
+    c = case(1, 70, 2, 16, 1, 16, seed=9, init=True)
+    d = {k: None if v is None else v.to(DEV) for k, v in c.items()}
+    seq = torch.as_tensor(np.repeat(np.arange(3), np.diff(cu))[None], dtype=torch.int32, device=DEV)
+    args = (d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["z"], d["dt_bias"], d["initial_states"],
+            True, 0.0, float("inf"))
+    torch.library.opcheck(torch.ops.mamba_cpu.ssd_fwd.default, args + (True,), dict(seq_idx=seq))
+    out, fin, saved, ysave = torch.ops.mamba_cpu.ssd_fwd(*args, True, seq_idx=seq)
+    bargs = (torch.randn_like(out), torch.randn_like(fin)) + args + (saved, ysave)
+    torch.library.opcheck(torch.ops.mamba_cpu.ssd_bwd.default, bargs, dict(seq_idx=seq))
+    cut = torch.as_tensor(cu, dtype=torch.int32, device=DEV)
+    torch.library.opcheck(torch.ops.mamba_cpu.ssd_varlen_states.default, args + (saved, cut), dict(seq_idx=seq))
