@@ -12,6 +12,15 @@ reference hooks the same five globals (src/mamba_cpu/hf.py:63-112), which is
 why the hook points, the three public names and the parameter lists below are
 what they are.
 
+Mamba-2 models (modeling_mamba2) look up their own set the same way:
+mamba2_chunk_scan (mamba_ssm's mamba_chunk_scan_combined),
+mamba2_selective_state_update, causal_conv1d_fn and causal_conv1d_update,
+routed here to mamba_chunk_scan_combined and the ops above. Their fifth,
+mamba2_split_conv1d_scan_combined (the fused layer), is left alone: without
+mamba_ssm it answers None and the mixer takes its unfused path through the
+four routed functions. Following mamba_ssm, a seq_idx that reaches these
+functions packs sequences (transformers' own torch functions ignore it).
+
 patch_transformers() puts a DeviceRoute in each global: a call whose leading
 tensor is on a ROCm GPU (torch's "cuda" device type) runs this package's op,
 any other call the function the route replaced, so CPU models keep
@@ -28,12 +37,15 @@ import torch
 from mamba_cpu.ops import (
     causal_conv1d_fn,
     causal_conv1d_update,
+    mamba_chunk_scan_combined,
     selective_scan_fn,
     selective_state_update,
 )
 from mamba_cpu.ops.mamba_inner import fused_path_supported, mamba_inner_fn
 
-SUPPORTED_MODELS = ("mamba", "falcon_mamba", "jamba")
+MAMBA1_FAMILIES = ("mamba", "falcon_mamba", "jamba")
+MAMBA2_FAMILIES = ("mamba2",)
+SUPPORTED_MODELS = MAMBA1_FAMILIES + MAMBA2_FAMILIES
 
 
 # GPU bodies of transformers' kernel globals. Each takes the parameter list of
@@ -56,8 +68,8 @@ def gpu_selective_state_update(state, hidden_states, dt, A, B, C, D=None, dt_bia
                                   dt_softplus=dt_softplus)
 
 
-def gpu_causal_conv1d(hidden_states, weight, bias=None, activation=None, **options):
-    return causal_conv1d_fn(hidden_states, weight, bias, activation=activation)
+def gpu_causal_conv1d(hidden_states, weight, bias=None, activation=None, seq_idx=None, **options):
+    return causal_conv1d_fn(hidden_states, weight, bias, seq_idx=seq_idx, activation=activation)
 
 
 def gpu_causal_conv1d_update(hidden_states, conv_state, weight, bias=None, activation=None, **options):
@@ -85,7 +97,21 @@ def gpu_mamba_inner(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_we
                           delta_softplus=delta_softplus)
 
 
-# transformers global -> the GPU body that routes take for it
+def gpu_chunk_scan(hidden_states, dt, A, B, C, chunk_size, D=None, dt_bias=None, initial_states=None,
+                   dt_softplus=False, dt_limit=(0.0, float("inf")), return_final_states=False, z=None,
+                   seq_idx=None, cu_seqlens=None, return_varlen_states=False, **options):
+    """mamba2_chunk_scan: (batch, seqlen, nheads, headdim) x, (batch, seqlen,
+    nheads) dt, (nheads,) A and D, (batch, seqlen, ngroups, dstate) B and C;
+    out in x's dtype (transformers' torch function returns float32)."""
+    return mamba_chunk_scan_combined(hidden_states, dt, A, B, C, chunk_size, D=D, z=z, dt_bias=dt_bias,
+                                     initial_states=initial_states, seq_idx=seq_idx, cu_seqlens=cu_seqlens,
+                                     dt_softplus=dt_softplus, dt_limit=dt_limit,
+                                     return_final_states=return_final_states,
+                                     return_varlen_states=return_varlen_states)
+
+
+# transformers global -> the GPU body that routes take for it: Mamba-1
+# families, then Mamba-2 families
 KERNEL_GLOBALS = {
     "mamba_selective_scan": gpu_selective_scan,
     "mamba_selective_state_update": gpu_selective_state_update,
@@ -93,6 +119,17 @@ KERNEL_GLOBALS = {
     "causal_conv1d_update": gpu_causal_conv1d_update,
     "mamba_inner_fn": gpu_mamba_inner,
 }
+MAMBA2_KERNEL_GLOBALS = {
+    "mamba2_chunk_scan": gpu_chunk_scan,
+    "mamba2_selective_state_update": gpu_selective_state_update,
+    "causal_conv1d_fn": gpu_causal_conv1d,
+    "causal_conv1d_update": gpu_causal_conv1d_update,
+}
+
+
+def kernel_globals(family):
+    """The globals table of a model family."""
+    return MAMBA2_KERNEL_GLOBALS if family in MAMBA2_FAMILIES else KERNEL_GLOBALS
 
 
 class DeviceRoute:
@@ -124,19 +161,19 @@ def _modeling(family):
 def patch_transformers(models=SUPPORTED_MODELS):
     """Route ROCm-GPU calls of the given model families' kernels to this
     package. Calling it again changes nothing. Raises RuntimeError, and
-    patches nothing, if a family's modeling module lacks one of the five
-    globals (transformers older than 5)."""
-    modules = [_modeling(family) for family in models]
+    patches nothing, if a family's modeling module lacks one of the globals
+    of its table (transformers older than 5)."""
+    modules = [(_modeling(family), kernel_globals(family)) for family in models]
     gaps = []
-    for module in modules:
-        absent = [name for name in KERNEL_GLOBALS if not hasattr(module, name)]
+    for module, table in modules:
+        absent = [name for name in table if not hasattr(module, name)]
         if absent:
             gaps.append(f"{module.__name__} ({', '.join(absent)})")
     if gaps:
         raise RuntimeError("mamba_cpu.hf works with transformers >= 5, whose Mamba modeling modules "
                            "define the kernel globals it routes; missing in " + "; ".join(gaps))
-    for module in modules:
-        for name, body in KERNEL_GLOBALS.items():
+    for module, table in modules:
+        for name, body in table.items():
             current = getattr(module, name)
             if not isinstance(current, DeviceRoute):
                 setattr(module, name, DeviceRoute(current, body))
@@ -146,7 +183,7 @@ def unpatch_transformers(models=SUPPORTED_MODELS):
     """Put back the functions patch_transformers() replaced."""
     for family in models:
         module = _modeling(family)
-        for name in KERNEL_GLOBALS:
+        for name in kernel_globals(family):
             current = getattr(module, name, None)
             if isinstance(current, DeviceRoute):
                 setattr(module, name, current.fallback)

@@ -1,4 +1,4 @@
-"""mamba_cpu.hf on small random Mamba, FalconMamba and Jamba models.
+"""mamba_cpu.hf on small random Mamba, FalconMamba, Jamba and Mamba-2 models.
 
 Each check runs one model twice on the GPU: first on transformers' own
 pure-torch kernel functions (the functions the routes replace, reached
@@ -11,7 +11,9 @@ graph-replayed greedy decoder (mamba_cpu.decode) against model.generate, and
 a two-layer model of the Mamba-130M width (d_model 768, vocabulary 50280)
 checked with the reference's model-level measures (largest logit
 difference, top-1 agreement, greedy identity, per-tensor gradient error:
-benchmarks/check_hf_model.py:105-121).
+benchmarks/check_hf_model.py:105-121). Mamba-2 (which the reference does not
+route) takes the same cases through mamba_chunk_scan_combined, plus a two-layer
+model at the Mamba-2 2.7B layer's head shape (headdim 64, dstate 128).
 """
 
 import contextlib
@@ -37,6 +39,10 @@ def tiny_model(family, device=DEV):
         model = transformers.MambaForCausalLM(transformers.MambaConfig(**TINY))
     elif family == "falcon_mamba":
         model = transformers.FalconMambaForCausalLM(transformers.FalconMambaConfig(**TINY))
+    elif family == "mamba2":  # 4 heads of 16 channels, 2 groups
+        model = transformers.Mamba2ForCausalLM(transformers.Mamba2Config(
+            vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=16, conv_kernel=4, expand=2,
+            num_heads=4, head_dim=16, n_groups=2, chunk_size=16))
     else:  # a Mamba layer then an attention layer, one expert
         model = transformers.JambaForCausalLM(transformers.JambaConfig(
             vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=2,
@@ -51,7 +57,9 @@ def token_ids(shape, device=DEV, vocab=64, seed=1):
 
 
 def _modules():
-    return [importlib.import_module(f".modeling_{f}", f"transformers.models.{f}") for f in FAMILIES]
+    """(modeling module, its kernel-globals table) of every family."""
+    return [(importlib.import_module(f".modeling_{f}", f"transformers.models.{f}"), mamba_cpu.hf.kernel_globals(f))
+            for f in FAMILIES]
 
 
 @contextlib.contextmanager
@@ -60,8 +68,8 @@ def torch_kernels():
     (the plain functions its hub/fallback decorator wraps), restored after."""
     mamba_cpu.hf.unpatch_transformers()
     saved = []
-    for module in _modules():
-        for name in mamba_cpu.hf.KERNEL_GLOBALS:
+    for module, table in _modules():
+        for name in table:
             fn = getattr(module, name)
             saved.append((module, name, fn))
             setattr(module, name, getattr(fn, "__wrapped__", fn))
@@ -104,14 +112,16 @@ def calls(monkeypatch):
             return body(*args, **kwargs)
         return run
 
-    for name, body in list(mamba_cpu.hf.KERNEL_GLOBALS.items()):
-        monkeypatch.setitem(mamba_cpu.hf.KERNEL_GLOBALS, name, counted(name, body))
+    for table in (mamba_cpu.hf.KERNEL_GLOBALS, mamba_cpu.hf.MAMBA2_KERNEL_GLOBALS):
+        for name, body in list(table.items()):
+            monkeypatch.setitem(table, name, counted(name, body))
     return seen
 
 
 def used_the_scan(seen):
-    # the scan itself, or the fused mixer (which runs it) in training
-    return "mamba_selective_scan" in seen or "mamba_inner_fn" in seen
+    # the scan itself, the fused mixer (which runs it) in training, or the
+    # Mamba-2 chunked scan
+    return any(name in seen for name in ("mamba_selective_scan", "mamba_inner_fn", "mamba2_chunk_scan"))
 
 
 per_family = pytest.mark.parametrize("family", FAMILIES)
@@ -133,7 +143,8 @@ def test_greedy_generation_matches(family, calls):
     model = tiny_model(family)
     ids = token_ids((2, 11))
     got, want = torch_then_gpu(lambda: model.generate(ids, max_new_tokens=12, do_sample=False))
-    assert used_the_scan(calls) and "mamba_selective_state_update" in calls
+    assert used_the_scan(calls)
+    assert "mamba_selective_state_update" in calls or "mamba2_selective_state_update" in calls
     assert torch.equal(got, want)
 
 
@@ -301,3 +312,46 @@ def test_mamba_130m_width_two_layers_agrees_with_transformers():
     print(f"  train loss {loss:.6f} vs {loss_want:.6f}, worst per-tensor gradient error {worst:.3g}")
     assert abs(loss - loss_want) <= 1e-5 * abs(loss_want)
     assert worst < 1e-4
+
+
+@pytest.mark.gpu
+def test_mamba2_head_shape_two_layers_agrees_with_transformers():
+    """Two Mamba-2 layers with the 2.7B model's head shape (headdim 64,
+    dstate 128, one group; 16 heads of d_model 512), random init, float32:
+    prefill logits of 2 x 300 tokens, 16 greedy steps (the decode path:
+    selective_state_update in the head layout and the conv update), and a
+    training step of 2 x 200, on this package against transformers' torch
+    kernels (which chunk by 256 where the package's kernels chunk by 64).
+    Bounds: largest |logit difference| 1e-3, top-1 agreement at every
+    position, identical greedy tokens, worst per-tensor gradient error
+    max|dg| / max|g| of 1e-3."""
+    torch.manual_seed(0)
+    cfg = transformers.Mamba2Config(num_hidden_layers=2, hidden_size=512, num_heads=16, head_dim=64,
+                                    state_size=128, n_groups=1, expand=2, conv_kernel=4, vocab_size=1000,
+                                    chunk_size=256)
+    model = transformers.Mamba2ForCausalLM(cfg).to(DEV).eval()
+    ids = token_ids((2, 300), vocab=1000)
+    got, want = torch_then_gpu(lambda: model(ids).logits.detach())
+    dlogit = (got - want).abs().max().item()
+    top1 = (got.argmax(-1) == want.argmax(-1)).float().mean().item()
+    print(f"  max|dlogit| {dlogit:.3g} (max|logit| {want.abs().max().item():.3g}), top-1 agreement {top1}")
+    assert dlogit < 1e-3 and top1 == 1.0
+    gen, gen_want = torch_then_gpu(lambda: model.generate(ids[:, :40], max_new_tokens=16,
+                                                          min_new_tokens=16, do_sample=False))
+    assert torch.equal(gen, gen_want)
+    model.train()
+    train_ids = ids[:, :200]
+
+    def step():
+        model.zero_grad()
+        loss = model(train_ids, labels=train_ids).loss
+        loss.backward()
+        return loss.item(), {k: p.grad.clone() for k, p in model.named_parameters() if p.grad is not None}
+
+    (loss, grads), (loss_want, grads_want) = torch_then_gpu(step)
+    worst = max(((grads[k] - g).abs().max() / g.abs().max().clamp_min(1e-12)).item()
+                for k, g in grads_want.items())
+    print(f"  train loss {loss:.6f} vs {loss_want:.6f}, worst per-tensor gradient error {worst:.3g}")
+    assert grads.keys() == grads_want.keys()
+    assert abs(loss - loss_want) <= 1e-5 * abs(loss_want)
+    assert worst < 1e-3
