@@ -19,7 +19,9 @@ Also reported, on one JSON line:
                 init) prefill 4 x 1024 tokens/s, 128-step greedy decode
                 (generate, and graph-replayed with fused block steps) and a
                 4 x 256 training step through the patched Hugging Face model;
-                and every other workload of the op set (forward-only scan,
+                the same prefill and training step for the Mamba-2 130M
+                architecture, beside transformers' own torch kernels on the
+                GPU; and every other workload of the op set (forward-only scan,
                 long-sequence bf16 scan, complex-A scan, conv1d fp32/bf16,
                 conv1d over packed sequences, conv update, conv update through
                 ring buffers and state indices, state update), each with time,
@@ -639,6 +641,70 @@ def _mamba130m_ids(torch):
     return torch.randint(0, MAMBA130M["vocab_size"], (4, 1024), generator=torch.Generator().manual_seed(1))
 
 
+MAMBA2_130M = dict(num_hidden_layers=24, hidden_size=768, num_heads=24, head_dim=64, state_size=128,
+                   n_groups=1, expand=2, conv_kernel=4, vocab_size=50280, chunk_size=256)
+
+
+def mamba2_130m(torch, dev, iters=3):
+    """Random-init Mamba-2 130M architecture (24 layers, d_model 768, 24 heads
+    x headdim 64, dstate 128, one group, conv width 4, vocab 50280), fp32,
+    through the patched Hugging Face model: prefill 4 x 1024 tokens on this
+    package's kernels, the same prefill through transformers' own torch
+    kernels on this GPU (one pass: they build (chunk x chunk x heads x dstate)
+    intermediates), the largest logit difference between the two, and one
+    training step at 4 x 256. The reference has no Mamba-2 path, so there is
+    no CPU leg."""
+    import transformers
+
+    import mamba_cpu.hf
+
+    torch.manual_seed(0)
+    model = transformers.Mamba2ForCausalLM(transformers.Mamba2Config(**MAMBA2_130M)).to(dev).eval()
+    ids = torch.randint(0, MAMBA2_130M["vocab_size"], (4, 1024), generator=torch.Generator().manual_seed(1))
+    ids = ids.to(dev)
+    res = {"workload": "Mamba-2 130M architecture (24 layers, d_model 768, 24 heads x 64, dstate 128), "
+                       "random init, fp32, prefill 4 x 1024 and a 4 x 256 training step"}
+    mamba_cpu.hf.patch_transformers()
+    try:
+        with torch.no_grad():
+            got = model(ids).logits
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                model(ids)
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t0) / iters
+        res["prefill_ms"] = round(sec * 1e3, 2)
+        res["prefill_tokens_per_s"] = round(4 * 1024 / sec, 1)
+        model.train()
+        train_ids = ids[:, :256]
+        model(train_ids, labels=train_ids).loss.backward()
+        model.zero_grad(set_to_none=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            model(train_ids, labels=train_ids).loss.backward()
+            model.zero_grad(set_to_none=True)
+        torch.cuda.synchronize()
+        res["train_step_ms_4x256"] = round((time.perf_counter() - t0) / iters * 1e3, 2)
+        model.eval()
+    finally:
+        mamba_cpu.hf.unpatch_transformers()
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        want = model(ids).logits
+        torch.cuda.synchronize()
+        sec_torch = time.perf_counter() - t0
+    res["torch_kernels_prefill_ms"] = round(sec_torch * 1e3, 2)
+    res["prefill_speedup_vs_torch_kernels"] = round(sec_torch / sec, 1)
+    res["max_abs_logit_diff_vs_torch_kernels"] = float((got - want).abs().max())
+    res["max_abs_logit"] = float(want.abs().max())
+    del got, want, model
+    torch.cuda.empty_cache()
+    return res
+
+
 def mamba130m(torch, dev, keep, iters=3):
     """Random-init Mamba-1 130M architecture (24 layers, d_model 768, d_inner
     1536, dstate 16, dt_rank 48, conv width 4, vocab 50280), fp32, through the
@@ -1066,6 +1132,10 @@ def main():
             except Exception as exc:  # reported, not hidden
                 extra["mamba130m_cpu_error"] = repr(exc)
         del keep
+        try:
+            extra["mamba2_130m"] = mamba2_130m(torch, dev)
+        except Exception as exc:  # reported, not hidden
+            extra["mamba2_130m_error"] = repr(exc)
     if not args.no_configs:
         extra["workloads"] = other_configs(torch, dev, stream, not args.no_cpu_baseline)
         extra["workloads"].update(ssd_workloads(torch, dev, stream, not args.no_cpu_baseline))
