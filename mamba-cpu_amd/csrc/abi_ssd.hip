@@ -48,29 +48,44 @@ int check_ssd(const mcpu_ssd_args* a) {
   return MCPU_OK;
 }
 
-// Heads per workgroup of the chunk kernels: the largest divisor of the
-// heads per group, up to kSsdMaxHeadBlock, that still leaves at least 1024
-// workgroups (four per CU) to spread over the GPU.
+// Heads per workgroup of the chunk kernels. Their LDS holds one workgroup
+// per CU, so a launch takes ceil(workgroups / CUs) rounds, each as long as one
+// workgroup: a part shared by its heads (staging B and C, forming C B^T) plus
+// a part per head, the shared part about 0.4 of a head's in both directions.
+// The divisor of the heads per group, up to kSsdMaxHeadBlock, with the least
+// rounds x (0.4 + heads) is chosen; against timings of both directions at
+// batch 1-8, 24-80 heads, seqlen 256-4096 this picks the fastest block or one
+// within 3 % of it.
 int head_block(const mcpu_ssd_args* a) {
   const int64_t hpg = a->nheads / a->ngroups;
   const int64_t chunks = a->batch * ((a->seqlen + kSsdQ - 1) / kSsdQ);
   int hb = 1;
-  for (int d = 2; d <= kSsdMaxHeadBlock; ++d)
-    if (hpg % d == 0 && chunks * (a->nheads / d) >= 1024) hb = d;
+  int64_t best = -1;
+  for (int d = 1; d <= kSsdMaxHeadBlock; ++d) {
+    if (hpg % d != 0) continue;
+    const int64_t rounds = (chunks * (a->nheads / d) + kSsdCUs - 1) / kSsdCUs;
+    const int64_t cost = rounds * (4 + 10 * d);
+    if (best < 0 || cost < best) {
+      best = cost;
+      hb = d;
+    }
+  }
   return hb;
 }
 
-// Whether the chunk states are carried by the in-order kernels: they run one
-// workgroup per (batch, head, 64-state column block) through every chunk, so
-// they need at least 512 of those (two per CU) to fill the GPU; below that the
-// two-launch form, parallel over chunks, is used.
-bool in_order(const mcpu_ssd_args* a) {
+// Whether the chunk states are carried by the in-order kernels, one
+// workgroup per (batch, head, 64-state column block) walking every chunk, or
+// by the two-launch form, parallel over chunks. The in-order forward is the
+// faster from about 256 such workgroups, the in-order backward from about
+// 160 (measured at 48-640 of them); the two directions choose on their own
+// (the saved buffer is the same for both forms).
+bool in_order(const mcpu_ssd_args* a, bool bwd) {
   if (a->chunk_pass != 0) return a->chunk_pass == 2;
   const int64_t cols = (a->dstate + kSsdPassCols - 1) / kSsdPassCols;
-  return a->batch * a->nheads * cols >= 512;
+  return a->batch * a->nheads * cols >= (bwd ? 160 : 256);
 }
 
-SsdParams make_ssd(const mcpu_ssd_args* a) {
+SsdParams make_ssd(const mcpu_ssd_args* a, bool bwd = false) {
   SsdParams p;
   std::memset(&p, 0, sizeof(p));
   p.x = a->x;
@@ -90,7 +105,7 @@ SsdParams make_ssd(const mcpu_ssd_args* a) {
   p.ngroups = a->ngroups;
   p.dstate = a->dstate;
   p.nchunks = (a->seqlen + kSsdQ - 1) / kSsdQ;
-  p.in_order = in_order(a) ? 1 : 0;
+  p.in_order = in_order(a, bwd) ? 1 : 0;
   p.nslices = p.in_order ? (a->dstate + kSsdPassCols - 1) / kSsdPassCols
                          : (a->headdim * a->dstate + kSsdSlice - 1) / kSsdSlice;
   p.hb = a->head_block != 0 ? a->head_block : head_block(a);
@@ -221,7 +236,7 @@ extern "C" size_t mcpu_ssd_bwd_workspace_size(const mcpu_ssd_args* a) {
     clear_error();
     return 0;
   }
-  return bwd_layout(make_ssd(a)).total;
+  return bwd_layout(make_ssd(a, true)).total;
 }
 
 extern "C" int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t saved_bytes, void* workspace,
@@ -240,7 +255,7 @@ extern "C" int mcpu_ssd_bwd(const mcpu_ssd_args* a, const void* saved, size_t sa
     return fail(MCPU_ERR_INVALID, "ssd_bwd: ddt_bias is required when dt_bias is given");
   if (a->initial_states != nullptr && a->dinitial_states == nullptr)
     return fail(MCPU_ERR_INVALID, "ssd_bwd: dinitial_states is required when initial_states is given");
-  SsdParams p = make_ssd(a);
+  SsdParams p = make_ssd(a, true);
   const size_t need_saved = saved_layout(p).total;
   if (need_saved > 0 && (saved == nullptr || saved_bytes < need_saved))
     return fail(MCPU_ERR_INVALID, "ssd_bwd: the forward's saved buffer of %zu bytes is needed, got %zu",

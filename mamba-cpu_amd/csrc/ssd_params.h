@@ -13,6 +13,7 @@ constexpr int kSsdMaxN = 128;     // largest dstate
 constexpr int kSsdSlice = 256;    // state elements per workgroup of the chunk-passing kernels
 constexpr int kSsdMaxHeadBlock = 8;  // heads one workgroup of the chunk kernels walks through
 constexpr int kSsdPassCols = 64;  // state columns per workgroup of the in-order passing kernels
+constexpr int kSsdCUs = 256;      // compute units of an MI355X (workgroups of the chunk kernels per round)
 
 // Layouts (all contiguous): x, z, out, ysave, dx, dz (batch, seqlen, nheads,
 // headdim) in the storage type; dt, ddt (batch, seqlen, nheads) float32;
