@@ -20,14 +20,16 @@ in_proj, conv update, x_proj, dt_proj, state update, out_proj and the
 residual in four kernels, with the small-batch products as matrix-vector
 kernels that read each weight once. It computes what the block computes;
 the products sum in another order than the GEMM library's, so logits agree
-to float32 rounding and greedy tokens match `model.generate`'s.
+to float32 rounding and greedy tokens match `model.generate`'s. FalconMamba
+and Mamba-2 models replay their own decode step (on this package's conv
+update and state update once mamba_cpu.hf is patched).
 """
 
 import torch
 
 from mamba_cpu import _C  # noqa: F401  (loads the operator library)
 
-_GRAPH_MODELS = ("mamba", "falcon_mamba")
+_GRAPH_MODELS = ("mamba", "falcon_mamba", "mamba2")
 _MAX_FUSED_BATCH = 8
 
 
@@ -120,8 +122,9 @@ def _cache_tensors(cache):
 
 
 class GraphedDecodeStep:
-    """One decode step of `model` (a transformers MambaForCausalLM or
-    FalconMambaForCausalLM on a ROCm GPU) captured as a HIP graph.
+    """One decode step of `model` (a transformers MambaForCausalLM,
+    FalconMambaForCausalLM or Mamba2ForCausalLM on a ROCm GPU) captured as a
+    HIP graph.
 
     `cache` is the model's cache after the prompt (the `cache_params` a
     `use_cache=True` forward returns). `token` is the (batch, 1) int64 tensor

@@ -239,26 +239,29 @@ def test_patched_model_used_as_installed(family, calls):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("family", ["mamba", "falcon_mamba"])
+@pytest.mark.parametrize("family", ["mamba", "falcon_mamba", "mamba2"])
 def test_graph_replayed_greedy_equals_generate(family):
     import mamba_cpu.decode
 
     model = tiny_model(family)
     ids = token_ids((3, 7))
     with gpu_kernels():
-        want = model.generate(ids, max_new_tokens=20, min_new_tokens=20, do_sample=False)
+        # an explicit mask: generate would otherwise mask prompt tokens equal to the pad id
+        want = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=20,
+                              min_new_tokens=20, do_sample=False)
         got = mamba_cpu.decode.greedy_generate(model, ids, 20)
     assert torch.equal(got, want)
 
 
 @pytest.mark.gpu
-def test_each_graph_replay_equals_the_eager_step():
+@pytest.mark.parametrize("family", ["mamba", "mamba2"])
+def test_each_graph_replay_equals_the_eager_step(family):
     """Every replay of the captured decode step against the eager step on the
     same token and cache, with eager work and synchronisations between
     replays."""
     import mamba_cpu.decode
 
-    model = tiny_model("mamba")
+    model = tiny_model(family)
     prompt, steps = token_ids((2, 9)), token_ids((2, 12), seed=2)
     with gpu_kernels(), torch.no_grad():
         cache = model(prompt, use_cache=True).cache_params
@@ -321,7 +324,8 @@ def test_mamba2_head_shape_two_layers_agrees_with_transformers():
     prefill logits of 2 x 300 tokens, 16 greedy steps (the decode path:
     selective_state_update in the head layout and the conv update), and a
     training step of 2 x 200, on this package against transformers' torch
-    kernels (which chunk by 256 where the package's kernels chunk by 64).
+    kernels (which chunk by 256 where the package's kernels chunk by 64);
+    the graph-replayed greedy decoder gives the same tokens.
     Bounds: largest |logit difference| 1e-3, top-1 agreement at every
     position, identical greedy tokens, worst per-tensor gradient error
     max|dg| / max|g| of 1e-3."""
@@ -336,9 +340,15 @@ def test_mamba2_head_shape_two_layers_agrees_with_transformers():
     top1 = (got.argmax(-1) == want.argmax(-1)).float().mean().item()
     print(f"  max|dlogit| {dlogit:.3g} (max|logit| {want.abs().max().item():.3g}), top-1 agreement {top1}")
     assert dlogit < 1e-3 and top1 == 1.0
-    gen, gen_want = torch_then_gpu(lambda: model.generate(ids[:, :40], max_new_tokens=16,
-                                                          min_new_tokens=16, do_sample=False))
+    prompt = ids[:, :40]
+    gen, gen_want = torch_then_gpu(lambda: model.generate(prompt, attention_mask=torch.ones_like(prompt),
+                                                          max_new_tokens=16, min_new_tokens=16,
+                                                          do_sample=False))
     assert torch.equal(gen, gen_want)
+    import mamba_cpu.decode
+
+    with gpu_kernels():  # the decode step replayed from a HIP graph gives the same tokens
+        assert torch.equal(mamba_cpu.decode.greedy_generate(model, prompt, 16), gen)
     model.train()
     train_ids = ids[:, :200]
 
