@@ -651,9 +651,10 @@ def mamba2_130m(torch, dev, iters=3):
     through the patched Hugging Face model: prefill 4 x 1024 tokens on this
     package's kernels, the same prefill through transformers' own torch
     kernels on this GPU (one pass: they build (chunk x chunk x heads x dstate)
-    intermediates), the largest logit difference between the two, and one
-    training step at 4 x 256. The reference has no Mamba-2 path, so there is
-    no CPU leg."""
+    intermediates), the largest logit difference between the two, one
+    training step at 4 x 256, and 128 greedy decode steps at batch 4 through
+    generate and graph-replayed (prompt and capture included). The reference
+    has no Mamba-2 path, so there is no CPU leg."""
     import transformers
 
     import mamba_cpu.hf
@@ -663,7 +664,7 @@ def mamba2_130m(torch, dev, iters=3):
     ids = torch.randint(0, MAMBA2_130M["vocab_size"], (4, 1024), generator=torch.Generator().manual_seed(1))
     ids = ids.to(dev)
     res = {"workload": "Mamba-2 130M architecture (24 layers, d_model 768, 24 heads x 64, dstate 128), "
-                       "random init, fp32, prefill 4 x 1024 and a 4 x 256 training step"}
+                       "random init, fp32, prefill 4 x 1024, a 4 x 256 training step, 128 decode steps at batch 4"}
     mamba_cpu.hf.patch_transformers()
     try:
         with torch.no_grad():
@@ -688,6 +689,25 @@ def mamba2_130m(torch, dev, iters=3):
         torch.cuda.synchronize()
         res["train_step_ms_4x256"] = round((time.perf_counter() - t0) / iters * 1e3, 2)
         model.eval()
+        # 128 greedy decode steps from a 4 x 16 prompt: generate, and the
+        # step replayed from a HIP graph (mamba_cpu.decode)
+        import mamba_cpu.decode
+
+        prompt = ids[:, :16]
+        mask = torch.ones_like(prompt)
+        with torch.no_grad():
+            model.generate(prompt, attention_mask=mask, max_new_tokens=4, min_new_tokens=4, do_sample=False)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            model.generate(prompt, attention_mask=mask, max_new_tokens=128, min_new_tokens=128, do_sample=False)
+            torch.cuda.synchronize()
+            res["decode_ms_per_step"] = round((time.perf_counter() - t0) / 128 * 1e3, 3)
+            mamba_cpu.decode.greedy_generate(model, prompt, 4)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            mamba_cpu.decode.greedy_generate(model, prompt, 128)
+            torch.cuda.synchronize()
+            res["decode_graph_ms_per_step"] = round((time.perf_counter() - t0) / 128 * 1e3, 3)
     finally:
         mamba_cpu.hf.unpatch_transformers()
     with torch.no_grad():
