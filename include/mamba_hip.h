@@ -290,6 +290,16 @@ typedef struct mcpu_state_update_args {
      selective_state_update. state_batch: rows of state (0 = batch). */
   const int32_t* state_batch_indices;
   int64_t state_batch;
+  /* 0: A is (nheads, headdim, dstate) and D, dt_bias (nheads, headdim),
+     contiguous, and the strides below are ignored. 1: they are read through
+     the strides below, in elements, 0 for a broadcast dimension (the Mamba-2
+     decode step passes A, D and dt_bias expanded from per-head values).
+     No counterpart in the reference, whose op materialises them. */
+  int32_t param_strides;
+  int32_t _pad2;
+  int64_t A_stride[3];     /* over (head, headdim, dstate) */
+  int64_t D_stride[2];     /* over (head, headdim) */
+  int64_t dt_bias_stride[2];
 } mcpu_state_update_args;
 
 int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream);

@@ -259,6 +259,8 @@ extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void
     return fail(MCPU_ERR_INVALID, "selective_state_update: bad dtype");
   if (a->nheads * a->headdim > 0xffff0000ll)
     return fail(MCPU_ERR_UNSUPPORTED, "selective_state_update: nheads * headdim too large");
+  if (a->param_strides != 0 && a->param_strides != 1)
+    return fail(MCPU_ERR_INVALID, "selective_state_update: param_strides must be 0 or 1");
   if (int rc = mcpu_check_device()) return rc;
   StateUpdateParams p;
   std::memset(&p, 0, sizeof(p));
@@ -286,6 +288,19 @@ extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void
   for (int i = 0; i < 2; ++i) {
     p.sB[i] = a->B_stride[i];
     p.sC[i] = a->C_stride[i];
+  }
+  if (a->param_strides) {
+    for (int i = 0; i < 3; ++i) p.sA[i] = a->A_stride[i];
+    for (int i = 0; i < 2; ++i) {
+      p.sD[i] = a->D_stride[i];
+      p.sbias[i] = a->dt_bias_stride[i];
+    }
+  } else {
+    p.sA[0] = a->headdim * a->dstate;
+    p.sA[1] = a->dstate;
+    p.sA[2] = 1;
+    p.sD[0] = p.sbias[0] = a->headdim;
+    p.sD[1] = p.sbias[1] = 1;
   }
   if (a->state_batch < 0) return fail(MCPU_ERR_INVALID, "selective_state_update: negative state_batch");
   p.state_idx = a->state_batch_indices;

@@ -72,6 +72,7 @@ struct StateUpdateParams {
   void* out;
   int64_t batch, nheads, headdim, dstate, ngroups;
   int64_t sst[3], sx[3], sdt[3], sz[3], sB[2], sC[2];
+  int64_t sA[3], sD[2], sbias[2];  // A over (head, headdim, dstate); D, dt_bias over (head, headdim)
   int softplus;
   const int32_t* state_idx;  // state row per batch row, or null
   int64_t state_batch;       // rows of state

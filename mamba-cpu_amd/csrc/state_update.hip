@@ -30,7 +30,7 @@ __global__ void __launch_bounds__(256) state_update_kernel(const StateUpdatePara
     const int64_t rowid = b * p.nheads * p.headdim + hp;
     const float x = ld<Tx>(p.x, b * p.sx[0] + h * p.sx[1] + pp * p.sx[2]);
     float dt = ld<Tx>(p.dt, b * p.sdt[0] + h * p.sdt[1] + pp * p.sdt[2]);
-    if (p.dt_bias != nullptr) dt += p.dt_bias[hp];
+    if (p.dt_bias != nullptr) dt += p.dt_bias[h * p.sbias[0] + pp * p.sbias[1]];
     if (p.softplus) dt = softplus(dt);
     const float dtx = dt * x;
     int64_t srow = b;
@@ -42,22 +42,35 @@ __global__ void __launch_bounds__(256) state_update_kernel(const StateUpdatePara
       }
     }
     const int64_t sbase = srow * p.sst[0] + h * p.sst[1] + pp * p.sst[2];
+    const float* Arow = p.A + h * p.sA[0] + pp * p.sA[1];
+    const float* Brow = p.B + b * p.sB[0] + g * p.sB[1];
+    const float* Crow = p.C + b * p.sC[0] + g * p.sC[1];
+    // Every load of the lane's states first: a load after a store to the
+    // state could not be moved above it, which would make each state a
+    // memory round trip of its own.
+    float sv[SPL], av[SPL], bv[SPL], cv[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) {
+      const int n = j + 16 * s;
+      const bool ok = n < N;
+      sv[s] = ok ? ld<Ts>(p.state, sbase + n) : 0.f;
+      av[s] = ok ? Arow[n * p.sA[2]] : 0.f;
+      bv[s] = ok ? Brow[n] : 0.f;
+      cv[s] = ok ? Crow[n] : 0.f;
+    }
     float acc = 0.f;
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {
       const int n = j + 16 * s;
       if (n < N) {
-        const float a = fast_exp(dt * p.A[hp * N + n]);
-        const float Bn = p.B[b * p.sB[0] + g * p.sB[1] + n];
-        const float Cn = p.C[b * p.sC[0] + g * p.sC[1] + n];
-        const float sv = fmaf(ld<Ts>(p.state, sbase + n), a, dtx * Bn);
-        st<Ts>(p.state, sbase + n, sv);
-        acc = fmaf(sv, Cn, acc);
+        const float v = fmaf(sv[s], fast_exp(dt * av[s]), dtx * bv[s]);
+        st<Ts>(p.state, sbase + n, v);
+        acc = fmaf(v, cv[s], acc);
       }
     }
     float y = row_allreduce16(acc);
     if (j == 0) {
-      if (p.D != nullptr) y = fmaf(x, p.D[hp], y);
+      if (p.D != nullptr) y = fmaf(x, p.D[h * p.sD[0] + pp * p.sD[1]], y);
       if (p.z != nullptr) {
         const float zz = ld<Tx>(p.z, b * p.sz[0] + h * p.sz[1] + pp * p.sz[2]);
         y *= zz * sigmoid(zz);
@@ -77,6 +90,8 @@ static hipError_t launch_su(const StateUpdateParams& p, hipStream_t st) {
     hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 2>), dim3(blocks), dim3(256), 0, st, p);
   else if (p.dstate <= 64)
     hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 4>), dim3(blocks), dim3(256), 0, st, p);
+  else if (p.dstate <= 128)
+    hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 8>), dim3(blocks), dim3(256), 0, st, p);
   else
     hipLaunchKernelGGL((state_update_kernel<Tx, Ts, 16>), dim3(blocks), dim3(256), 0, st, p);
   return hipGetLastError();

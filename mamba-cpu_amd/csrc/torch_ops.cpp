@@ -972,8 +972,12 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
     const Tensor f = t.to(at::kFloat);
     return (f.stride(-1) == 1 || f.size(-1) == 1) ? f : f.contiguous();
   };
-  const Tensor A = f32c(A_in), B = unit_last(B_in), C = unit_last(C_in);
-  const optional<Tensor> D = f32c(D_in), dt_bias = f32c(dt_bias_in);
+  // float32 parameters are read through their own strides (the Mamba-2 step
+  // passes A, D and dt_bias expanded from per-head values); others are cast.
+  auto f32 = [](const Tensor& t) { return t.scalar_type() == at::kFloat ? t : t.to(at::kFloat); };
+  auto f32o = [&](const optional<Tensor>& t) { return has(t) ? optional<Tensor>(f32(*t)) : optional<Tensor>(); };
+  const Tensor A = f32(A_in), B = unit_last(B_in), C = unit_last(C_in);
+  const optional<Tensor> D = f32o(D_in), dt_bias = f32o(dt_bias_in);
   TORCH_CHECK_VALUE(heads ? (A.dim() == 3 && A.size(0) == h && A.size(1) == p && A.size(2) == n)
                           : (A.dim() == 2 && A.size(0) == p && A.size(1) == n),
                     name, " expects A of shape (dim, dstate) or (nheads, headdim, dstate)");
@@ -1027,6 +1031,17 @@ Tensor selective_state_update(Tensor& state, const Tensor& x, const Tensor& dt, 
   a.state_batch_indices =
       has(state_batch_indices) ? static_cast<const int32_t*>(state_batch_indices->data_ptr()) : nullptr;
   a.state_batch = state.size(0);
+  a.param_strides = 1;
+  a.A_stride[0] = heads ? A.stride(0) : 0;
+  a.A_stride[1] = A.stride(heads ? 1 : 0);
+  a.A_stride[2] = A.stride(heads ? 2 : 1);
+  auto s2 = [&](int64_t (&d)[2], const optional<Tensor>& t) {
+    if (!has(t)) return;
+    d[0] = heads ? t->stride(0) : 0;
+    d[1] = t->stride(heads ? 1 : 0);
+  };
+  s2(a.D_stride, D);
+  s2(a.dt_bias_stride, dt_bias);
   check_rc(mcpu_selective_state_update(&a, stream_of(x)), name);
   return out;
 }

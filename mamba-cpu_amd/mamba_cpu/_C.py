@@ -98,6 +98,8 @@ class StateUpdateArgs(ctypes.Structure):
         ("state_stride", _S3), ("x_stride", _S3), ("dt_stride", _S3), ("z_stride", _S3),
         ("B_stride", _S2), ("C_stride", _S2),
         ("state_batch_indices", _P), ("state_batch", _I64),
+        ("param_strides", _I32), ("_pad2", _I32), ("A_stride", _S3), ("D_stride", _S2),
+        ("dt_bias_stride", _S2),
     ]
 
 

@@ -200,6 +200,11 @@ def test_conv_and_state_update_reject_bad_arguments():
     assert _rc(L.mcpu_causal_conv1d_update, ctypes.byref(u), None)[0] == _C.MCPU_ERR_INVALID
     s = _C.StateUpdateArgs()
     assert _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)[0] == _C.MCPU_ERR_INVALID
+    s.state = s.x = s.dt = s.A = s.B = s.C = s.out = 16  # non-NULL placeholders: never dereferenced
+    s.batch, s.nheads, s.headdim, s.dstate, s.ngroups = 1, 2, 4, 16, 1
+    s.param_strides = 2
+    rc, msg = _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)
+    assert rc == _C.MCPU_ERR_INVALID and "param_strides" in msg
 
 
 def test_conv_workspace_depends_only_on_the_shape():
