@@ -981,7 +981,9 @@ def model_pass(torch, dev, what):
     """A short fixed run of the Mamba-130M architecture for kernel traces
     (rocprofv3 --kernel-trace): `train` = 3 warm-up + 5 training steps at
     4 x 256; `decode` = the 4 x 16 prompt, then 64 graph-replayed greedy
-    steps."""
+    steps. `mamba2-prefill` = 4 prefills of 4 x 1024 tokens and
+    `mamba2-decode` = the 4 x 16 prompt then 32 graph-replayed greedy steps,
+    on the Mamba-2 130M architecture."""
     import transformers
 
     import mamba_cpu.decode
@@ -989,6 +991,18 @@ def model_pass(torch, dev, what):
 
     mamba_cpu.hf.patch_transformers()
     torch.manual_seed(0)
+    if what.startswith("mamba2"):
+        model = transformers.Mamba2ForCausalLM(transformers.Mamba2Config(**MAMBA2_130M)).to(dev).eval()
+        with torch.no_grad():
+            if what == "mamba2-prefill":
+                ids = torch.randint(0, 50280, (4, 1024), device=dev)
+                for _ in range(4):
+                    model(ids)
+            else:
+                mamba_cpu.decode.greedy_generate(model, torch.randint(0, 50280, (4, 16), device=dev), 33)
+        torch.cuda.synchronize()
+        print(f"model pass ({what}) done", flush=True)
+        return
     cfg = transformers.MambaConfig(num_hidden_layers=24, hidden_size=768, state_size=16, expand=2,
                                    conv_kernel=4, vocab_size=50280)
     model = transformers.MambaForCausalLM(cfg).to(dev)
@@ -1020,8 +1034,9 @@ def main():
     ap.add_argument("--ssd-pass", nargs="?", const="bf16", choices=["bf16", "fp32"],
                     help="only run 3 forward+backward passes of the SSD workload (bf16 by default) for "
                          "kernel traces")
-    ap.add_argument("--model-pass", choices=["train", "decode"],
-                    help="only run a short Mamba-130M train or graph-decode sequence for kernel traces")
+    ap.add_argument("--model-pass", choices=["train", "decode", "mamba2-prefill", "mamba2-decode"],
+                    help="only run a short Mamba-130M train or graph-decode sequence, or a Mamba-2 130M "
+                         "prefill or graph-decode sequence, for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
