@@ -14,7 +14,8 @@ without seq_idx bit for bit (every mask is open). Per-sequence final states
 and one-step sequences, ends on chunk edges, a first sequence that ends
 inside the first chunk with an initial state, both ways of carrying chunk
 states, 16-bit storage, and through mamba_chunk_scan_combined with autograd;
-opcheck of the operators with seq_idx and of ssd_varlen_states.
+head blocks of 1, 2 and 4 heads; opcheck of the operators with seq_idx and
+of ssd_varlen_states.
 Tolerances as in tests/test_ssd.py: float32 outputs and states rtol 1e-4 /
 atol 1e-5, gradients rtol 1e-3 with atol 1e-4 (dx, ddt, dz) or 1e-3 (sums);
 16-bit storage 2e-2.
@@ -79,6 +80,18 @@ def test_seq_idx_shapes_match_oracle(shape, opts, chunk_pass):
                         int(rng.integers(0, 2))) for _ in range(b)])
     c = case(*shape, seed=sum(shape) + 3, **opts)
     check_ops(c, run_ops(c, chunk_pass=chunk_pass, seq=seq), seq=seq)
+
+
+@pytest.mark.parametrize("chunk_pass", [1, 2], ids=["two-launch", "in-order"])
+def test_seq_idx_head_blocks(chunk_pass):
+    """Packed sequences with the chunk kernels' head block pinned to 1, 2 and
+    4 heads (8 heads, 2 groups): each against the oracle."""
+    b, l = 2, 170
+    seq = _seq(b, l, [([20, 64, 120], 0), ([100], 1)])
+    c = case(b, l, 8, 32, 2, 64, seed=17, init=True)
+    for hb in (1, 2, 4):
+        print(f" head_block {hb}", flush=True)
+        check_ops(c, run_ops(c, head_block=hb, chunk_pass=chunk_pass, seq=seq), seq=seq)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
