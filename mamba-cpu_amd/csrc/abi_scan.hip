@@ -160,7 +160,10 @@ int bwd_waves(const mcpu_scan_args* a) {
 // (at least four 16-step blocks each) so that about four waves per SIMD run,
 // the most that fit at the backward's register use, and chunks hold at most
 // 64 blocks (measured: batch 1, dim 5120, seqlen 16384 bf16 takes 1.33 ms at
-// 16 chunks against 1.40 ms at 3). Sets p.nchunk / p.chunk_blocks.
+// 16 chunks against 1.40 ms at 3). Two chunks of a sequence of at most 16
+// blocks are not worth their summary pass (batch 4, dim 1536, 256 steps fp32
+// with z: 49.8 us in one chunk against 53.0 us in two). Sets p.nchunk /
+// p.chunk_blocks.
 void bwd_chunks(ScanParams& p, int waves) {
   int64_t n = 1;
   const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves;
@@ -169,6 +172,7 @@ void bwd_chunks(ScanParams& p, int waves) {
     if (n < p.nblk / 64) n = p.nblk / 64;  // chunks of at most 64 blocks
     if (n > p.nblk / 4) n = p.nblk / 4;
     if (n < 1) n = 1;
+    if (n == 2 && p.nblk <= 16) n = 1;
   }
   p.chunk_blocks = n > 1 ? (p.nblk + n - 1) / n : (p.nblk > 0 ? p.nblk : 1);
   p.nchunk = n > 1 ? (p.nblk + p.chunk_blocks - 1) / p.chunk_blocks : 1;

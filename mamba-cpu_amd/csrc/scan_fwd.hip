@@ -266,11 +266,18 @@ int scan_fwd_waves() { return kFwdWaves; }
 // seqlen 2048 fp32 runs fastest at 13 chunks (40 us against 44 us at 11);
 // batch 1, dim 5120, seqlen 16384 bf16 at 16-24 chunks (0.73 ms against
 // 0.83 ms at 4), although the summary pass then covers 15/16 of the sequence.
-// Sets p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone fill the GPU.
+// Short sequences over at least half the GPU's compute units are not cut: the
+// summary pass costs more than the parallelism gains there (dim 1536 fp32
+// with z: batch 4 x 256 steps 21.9 us unchunked against 29.0 us in 4 chunks,
+// batch 4 x 1024 68.1 against 72.7, batch 2 x 512 29.9 against 31.2; but
+// batch 2 x 1024 54.3 against 49.3, so 128-255 workgroups keep chunks beyond
+// 32 blocks). Sets p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone
+// fill the GPU.
 void scan_fwd_chunks(ScanParams& p) {
   const int64_t wgs = p.batch * p.ngroups * p.nblk_c;
+  const bool short_rows = (wgs >= 256 && p.nblk <= 64) || (wgs >= 128 && p.nblk <= 32);
   int64_t n = 1;
-  if (wgs > 0 && wgs < 512 && p.nblk >= 4) {
+  if (wgs > 0 && wgs < 512 && p.nblk >= 4 && !short_rows) {
     n = (1280 + wgs - 1) / wgs;
     if (n < p.nblk / 64) n = p.nblk / 64;
     if (n > p.nblk / 2) n = p.nblk / 2;
