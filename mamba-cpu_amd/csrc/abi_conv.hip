@@ -12,10 +12,11 @@ namespace {
 
 int check_conv(const mcpu_conv_args* a) {
   if (a == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d: null argument block");
-  if (a->x == nullptr || a->weight == nullptr)
-    return fail(MCPU_ERR_INVALID, "causal_conv1d: x and weight are required");
   if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
     return fail(MCPU_ERR_INVALID, "causal_conv1d: negative size");
+  // A tensor with no elements may come as NULL (torch's empty tensors do).
+  if ((a->x == nullptr && a->batch * a->dim * a->seqlen > 0) || (a->weight == nullptr && a->dim > 0))
+    return fail(MCPU_ERR_INVALID, "causal_conv1d: x and weight are required");
   if (a->width < 1 || a->width > kConvMaxW)
     return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d: width must be in [1, %lld], got %lld",
                 (long long)kConvMaxW, (long long)a->width);
@@ -144,7 +145,8 @@ using namespace mcpu;
 extern "C" int mcpu_causal_conv1d_fwd(const mcpu_conv_args* a, void* stream) {
   clear_error();
   if (int rc = check_conv(a)) return rc;
-  if (a->out == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d_fwd: out is required");
+  if (a->out == nullptr && a->batch * a->dim * a->seqlen > 0)
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_fwd: out is required");
   if (int rc = mcpu_check_device()) return rc;
   ConvParams p = make_conv(a);
   p.out = a->out;
@@ -169,7 +171,8 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
                                       size_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_conv(a)) return rc;
-  if (a->dout == nullptr || a->dx == nullptr || a->dweight == nullptr)
+  if (((a->dout == nullptr || a->dx == nullptr) && a->batch * a->dim * a->seqlen > 0) ||
+      (a->dweight == nullptr && a->dim > 0))
     return fail(MCPU_ERR_INVALID, "causal_conv1d_bwd: dout, dx and dweight are required");
   if (a->bias != nullptr && a->dbias == nullptr)
     return fail(MCPU_ERR_INVALID, "causal_conv1d_bwd: dbias is required when bias is given");
@@ -201,10 +204,12 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
 extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* stream) {
   clear_error();
   if (a == nullptr) return fail(MCPU_ERR_INVALID, "causal_conv1d_update: null argument block");
-  if (a->x == nullptr || a->conv_state == nullptr || a->weight == nullptr || a->out == nullptr)
-    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: x, conv_state, weight and out are required");
   if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
     return fail(MCPU_ERR_INVALID, "causal_conv1d_update: negative size");
+  // With no rows (or channels) the tensors may come as NULL.
+  if (a->batch * a->dim > 0 &&
+      (a->x == nullptr || a->conv_state == nullptr || a->weight == nullptr || a->out == nullptr))
+    return fail(MCPU_ERR_INVALID, "causal_conv1d_update: x, conv_state, weight and out are required");
   if (a->width < 1 || a->width > kConvMaxW)
     return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d_update: width must be in [1, %lld]",
                 (long long)kConvMaxW);
@@ -246,11 +251,13 @@ extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* s
 extern "C" int mcpu_selective_state_update(const mcpu_state_update_args* a, void* stream) {
   clear_error();
   if (a == nullptr) return fail(MCPU_ERR_INVALID, "selective_state_update: null argument block");
-  if (a->state == nullptr || a->x == nullptr || a->dt == nullptr || a->A == nullptr ||
-      a->B == nullptr || a->C == nullptr || a->out == nullptr)
-    return fail(MCPU_ERR_INVALID, "selective_state_update: state, x, dt, A, B, C and out are required");
   if (a->batch < 0 || a->nheads < 0 || a->headdim < 0)
     return fail(MCPU_ERR_INVALID, "selective_state_update: negative size");
+  // With no rows (or channels) the tensors may come as NULL.
+  if (a->batch * a->nheads * a->headdim > 0 &&
+      (a->state == nullptr || a->x == nullptr || a->dt == nullptr || a->A == nullptr || a->B == nullptr ||
+       a->C == nullptr || a->out == nullptr))
+    return fail(MCPU_ERR_INVALID, "selective_state_update: state, x, dt, A, B, C and out are required");
   if (a->dstate < 1 || a->dstate > 256)
     return fail(MCPU_ERR_UNSUPPORTED, "selective_state_update: dstate must be in [1, 256]");
   if (a->ngroups < 1 || (a->nheads > 0 && a->nheads % a->ngroups != 0))

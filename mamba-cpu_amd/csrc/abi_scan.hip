@@ -36,11 +36,13 @@ void out_strides(const int64_t (&given)[3], int64_t dim, int64_t seqlen, int64_t
 
 int check_scan(const mcpu_scan_args* a) {
   if (a == nullptr) return fail(MCPU_ERR_INVALID, "selective_scan: null argument block");
-  if (a->u == nullptr || a->delta == nullptr || a->A == nullptr || a->B == nullptr ||
-      a->C == nullptr)
-    return fail(MCPU_ERR_INVALID, "selective_scan: u, delta, A, B and C are required");
   if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
     return fail(MCPU_ERR_INVALID, "selective_scan: negative size");
+  // A tensor with no elements may come as NULL (torch's empty tensors do).
+  const bool has_steps = a->batch > 0 && a->dim > 0 && a->seqlen > 0;
+  if ((has_steps && (a->u == nullptr || a->delta == nullptr || a->B == nullptr || a->C == nullptr)) ||
+      (a->dim > 0 && a->A == nullptr))
+    return fail(MCPU_ERR_INVALID, "selective_scan: u, delta, A, B and C are required");
   if (a->ngroups < 1 || (a->dim > 0 && a->dim % a->ngroups != 0))
     return fail(MCPU_ERR_INVALID, "selective_scan: dim (%lld) must be divisible by ngroups (%lld)",
                 (long long)a->dim, (long long)a->ngroups);
@@ -346,6 +348,11 @@ extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
   if (int rc = check_scan(a)) return rc;
   if (int rc = mcpu_check_device()) return rc;
   if (a->batch == 0 || a->dim == 0) return MCPU_OK;
+  if (a->seqlen == 0) {  // no steps: the state stays at its zero start
+    if (a->last_state == nullptr) return MCPU_OK;
+    return zero_f32(a->last_state, (a->complex_a ? 2 : 1) * a->batch * a->dim * a->dstate,
+                    static_cast<hipStream_t>(stream));
+  }
   if (a->complex_a) return complex_fwd(a, static_cast<hipStream_t>(stream));
   ScanParams p = make_params(a, scan_fwd_waves());
   scan_fwd_chunks(p);
@@ -380,8 +387,9 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
                                        size_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_scan(a)) return rc;
-  if (a->du == nullptr || a->ddelta == nullptr || a->dA == nullptr || a->dB == nullptr ||
-      a->dC == nullptr)
+  const bool has_steps = a->batch > 0 && a->dim > 0 && a->seqlen > 0;
+  if ((has_steps && (a->du == nullptr || a->ddelta == nullptr || a->dB == nullptr || a->dC == nullptr)) ||
+      (a->dim > 0 && a->dA == nullptr))
     return fail(MCPU_ERR_INVALID, "selective_scan_bwd: du, ddelta, dA, dB and dC are required");
   if (a->z != nullptr && a->dz == nullptr)
     return fail(MCPU_ERR_INVALID, "selective_scan_bwd: dz is required when z is given");
@@ -396,8 +404,9 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
                 w.total, workspace_bytes);
   if (int rc = mcpu_check_device()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (a->batch == 0 || a->dim == 0) {
-    // Empty batch/channel set: parameter grads are zero.
+  if (!has_steps) {
+    // No steps or rows: every per-step gradient is empty and the parameter
+    // gradients are zero.
     if (int rc = zero_f32(a->dA, a->dim * a->dstate, st)) return rc;
     if (a->dD) if (int rc = zero_f32(a->dD, a->dim, st)) return rc;
     if (a->ddelta_bias) if (int rc = zero_f32(a->ddelta_bias, a->dim, st)) return rc;

@@ -4,7 +4,7 @@ The four ops are torch.library custom ops over hand-written HIP kernels in
 libmamba_hip.so; they take ROCm GPU tensors. `mamba_chunk_scan_combined` is
 Mamba-2's SSD scan (mamba_ssm's function of that name) over the same library. `mamba_inner_fn` is the fused
 Mamba-1 mixer over them (transformers' training path). `mamba_cpu.hf.patch_transformers()`
-routes Hugging Face Mamba / FalconMamba / Jamba models on the GPU to them.
+routes Hugging Face Mamba / FalconMamba / Jamba / Mamba-2 models on the GPU to them.
 """
 
 from mamba_cpu.ops import (

@@ -139,6 +139,12 @@ def test_scan_rejects_bad_arguments_before_touching_a_device():
     # backward: required outputs
     rc, msg = _rc(L.mcpu_selective_scan_bwd, ctypes.byref(_scan_args()), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "du" in msg
+    # with no steps the per-step tensors may be NULL (torch's empty tensors
+    # are): the forward gets past the argument checks (to the device check on
+    # a host without a GPU; with one, it has nothing to write)
+    empty = _scan_args(u=None, delta=None, B=None, C=None, seqlen=0)
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(empty), None, 0, None)
+    assert "required" not in msg
 
 
 def test_scan_sizes():
@@ -191,15 +197,26 @@ def test_conv_and_state_update_reject_bad_arguments():
     L = _C.lib
     c = _C.ConvArgs()
     rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
-    assert rc == _C.MCPU_ERR_INVALID and msg
-    c.x = c.weight = c.out = 16
-    c.batch, c.dim, c.seqlen, c.width = 1, 4, 8, 17
+    assert rc != _C.MCPU_OK and msg  # width 0
+    # NULL tensors are accepted only where they hold no elements
+    c.batch, c.dim, c.seqlen, c.width = 1, 4, 8, 4
+    rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
+    assert rc == _C.MCPU_ERR_INVALID and "required" in msg
+    c.x = c.weight = 16
+    rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
+    assert rc == _C.MCPU_ERR_INVALID and "out is required" in msg
+    c.out = 16
+    c.width = 17
     rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
     assert rc in (_C.MCPU_ERR_INVALID, _C.MCPU_ERR_UNSUPPORTED) and "width" in msg
     u = _C.ConvUpdateArgs()
-    assert _rc(L.mcpu_causal_conv1d_update, ctypes.byref(u), None)[0] == _C.MCPU_ERR_INVALID
+    u.batch, u.dim, u.seqlen, u.width, u.state_len = 2, 8, 1, 4, 3
+    rc, msg = _rc(L.mcpu_causal_conv1d_update, ctypes.byref(u), None)
+    assert rc == _C.MCPU_ERR_INVALID and "required" in msg
     s = _C.StateUpdateArgs()
-    assert _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)[0] == _C.MCPU_ERR_INVALID
+    s.batch, s.nheads, s.headdim, s.dstate, s.ngroups = 1, 2, 4, 16, 1
+    rc, msg = _rc(L.mcpu_selective_state_update, ctypes.byref(s), None)
+    assert rc == _C.MCPU_ERR_INVALID and "required" in msg
     s.state = s.x = s.dt = s.A = s.B = s.C = s.out = 16  # non-NULL placeholders: never dereferenced
     s.batch, s.nheads, s.headdim, s.dstate, s.ngroups = 1, 2, 4, 16, 1
     s.param_strides = 2
