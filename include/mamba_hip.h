@@ -6,7 +6,8 @@
  * returns MCPU_OK or an error code; mcpu_last_error() then describes it.
  * The caller owns every buffer, including workspaces sized by the matching
  * *_workspace_size query (the reference's caller-owns-memory rule,
- * csrc/selective_scan.h:14-20, 42-50).
+ * csrc/selective_scan.h:14-20, 42-50). A tensor with no elements (zero steps,
+ * rows or channels) may be passed as NULL, as torch's empty tensors are.
  *
  * Storage types: "x-group" tensors (u, delta, z, out, dout, du, ddelta, dz for
  * the scan; x, out, states for the conv; x, dt, z, out for the state update)
