@@ -532,15 +532,27 @@ struct ReduceJobs {
   int njobs;
 };
 
-// The terms are loaded sixteen at a time (sixteen loads in flight instead of
-// a load-add chain) and added in the same fixed order c = 0, 1, ...
+// The terms are loaded 32 (then 16) at a time, so a launch that has about
+// one wave per SIMD waits for one or two memory round trips per item instead
+// of a load-add chain, and added in the same fixed order c = 0, 1, ...
+template <int U, typename V, typename Ld, typename Add>
+__device__ __forceinline__ void sum_terms(int64_t& c, int64_t nsum, Ld ld, Add add) {
+  for (; c + U <= nsum; c += U) {
+    V v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld(c + u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) add(v[u]);
+  }
+}
+
 __device__ __forceinline__ void reduce_item(const ReduceJob& j, int64_t i) {
-  constexpr int U = 16;
   if (j.vec == 4) {
     const int64_t per4 = j.per / 4;
     const int64_t sl = i / per4, e = (i % per4) * 4;
     const float* src = j.part + sl * j.nsum * j.per + e;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto ld = [&](int64_t c) { return *reinterpret_cast<const float4*>(src + c * j.per); };
     auto add = [&](const float4 v) {
       acc.x += v.x;
       acc.y += v.y;
@@ -548,28 +560,20 @@ __device__ __forceinline__ void reduce_item(const ReduceJob& j, int64_t i) {
       acc.w += v.w;
     };
     int64_t c = 0;
-    for (; c + U <= j.nsum; c += U) {
-      float4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = *reinterpret_cast<const float4*>(src + (c + u) * j.per);
-#pragma unroll
-      for (int u = 0; u < U; ++u) add(v[u]);
-    }
-    for (; c < j.nsum; ++c) add(*reinterpret_cast<const float4*>(src + c * j.per));
+    sum_terms<32, float4>(c, j.nsum, ld, add);
+    sum_terms<16, float4>(c, j.nsum, ld, add);
+    for (; c < j.nsum; ++c) add(ld(c));
     *reinterpret_cast<float4*>(j.out + sl * j.per + e) = acc;
   } else {
     const int64_t sl = i / j.per, e = i % j.per;
     const float* src = j.part + sl * j.nsum * j.per + e;
     float acc = 0.f;
+    auto ld = [&](int64_t c) { return src[c * j.per]; };
+    auto add = [&](const float v) { acc += v; };
     int64_t c = 0;
-    for (; c + U <= j.nsum; c += U) {
-      float v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = src[(c + u) * j.per];
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc += v[u];
-    }
-    for (; c < j.nsum; ++c) acc += src[c * j.per];
+    sum_terms<32, float>(c, j.nsum, ld, add);
+    sum_terms<16, float>(c, j.nsum, ld, add);
+    for (; c < j.nsum; ++c) add(ld(c));
     j.out[sl * j.per + e] = acc;
   }
 }
