@@ -1039,7 +1039,7 @@ def main():
                          "prefill or graph-decode sequence, for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
+        print("bench.py measures one GPU only; runs over several GPUs are not supported "
               f"(got --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
 
