@@ -2,8 +2,8 @@
 vectors produced by the reference's own CPU kernels (csrc/selective_scan.cpp,
 compiled from the reference sources into oracle/_ref/libmcpu_ref.so by
 oracle/Makefile). The reference ships no data files, so these are the
-known-answer vectors for the scan; the GPU box, which has no reference
-checkout, checks against them.
+known-answer vectors for the scan; a machine without the reference sources
+checks against them.
 
     make -C oracle REF=/root/reference && python tests/golden/make_golden.py
 
