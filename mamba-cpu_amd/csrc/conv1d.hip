@@ -493,33 +493,48 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
   float dwk[W + 1];  // dweight[0..W), dbias
 #pragma unroll
   for (int k = 0; k <= W; ++k) dwk[k] = 0.f;
+  const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
+  const int64_t orow = c.b * p.sdo[0] + c.d * p.sdo[1];
+  float xv[4 + VT + 4];  // X[t0 - 4 .. t0 + VT + 4)
+  float go[VT + 4];      // dout[t0 .. t0 + VT + 4)
+#pragma unroll
+  for (int i = 0; i < 4 + VT + 4; ++i) xv[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < VT + 4; ++i) go[i] = 0.f;
   if (g.active) {
-    float w[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) w[k] = p.w[c.d * W + k];
-    const float bias = p.bias ? p.bias[c.d] : 0.f;
-    const int64_t xrow = c.b * p.sx[0] + c.d * p.sx[1];
-    const int64_t orow = c.b * p.sdo[0] + c.d * p.sdo[1];
-    const bool tail = g.t0 + VT < L;  // the next VT steps exist
-    float xv[4 + VT + 4];              // X[t0 - 4 .. t0 + VT + 4)
-    float go[VT + 4];                  // dout[t0 .. t0 + VT + 4)
-    if (g.t0 > 0) {
-      ld4<T>(p.x, xrow + g.t0 - 4, xv);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
-    }
 #pragma unroll
     for (int q = 0; q < VT; q += 4) {
       ld4<T>(p.x, xrow + g.t0 + q, xv + 4 + q);
       ld4<T>(p.dout, orow + g.t0 + q, go + q);
     }
-    if (tail) {
+  }
+  // The halos are the neighbouring lanes' own steps: a wave's lanes hold
+  // consecutive VT-step pieces of one row, so lane l's four steps before t0
+  // are lane l - 1's last four and its four after are lane l + 1's first
+  // four (every lane runs the shifts; inactive lanes hold zeros). Only the
+  // wave's end lanes read them from memory.
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xv[i] = dpp<kWaveShr1>(xv[VT + i]);
+    xv[4 + VT + i] = dpp<kWaveShl1>(xv[4 + i]);
+    go[VT + i] = dpp<kWaveShl1>(go[i]);
+  }
+  if (g.active) {
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = p.w[c.d * W + k];
+    const float bias = p.bias ? p.bias[c.d] : 0.f;
+    const bool tail = g.t0 + VT < L;  // the next VT steps exist
+    if (g.t0 == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[i] = conv_x<T>(p, c, i - 4);
+    } else if (lane == 0) {
+      ld4<T>(p.x, xrow + g.t0 - 4, xv);
+    }
+    if (tail && lane == 63) {
       ld4<T>(p.x, xrow + g.t0 + VT, xv + 4 + VT);
       ld4<T>(p.dout, orow + g.t0 + VT, go + VT);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[4 + VT + i] = go[VT + i] = 0.f;
     }
     // dpre[t0 + i] for i < VT + W - 1 (zero past the sequence end).
     float dp[VT + W - 1];

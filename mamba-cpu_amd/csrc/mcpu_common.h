@@ -133,13 +133,18 @@ __device__ __forceinline__ float softplus(float x) {
 // Lanes are numbered l = 16 * row + j. DPP control codes (gfx9 encoding):
 //   0x00-0xFF quad_perm, 0x120+n row_ror:n, 0x140 row_mirror (j -> 15 - j),
 //   0x141 row_half_mirror (j -> 7 - j within each 8), 0x150+n row_newbcast:n
-//   (every lane of a row reads lane n of that row).
+//   (every lane of a row reads lane n of that row), 0x130 / 0x138 wave_shl:1 /
+//   wave_shr:1 (across the whole wave).
 
 template <int CTRL> __device__ __forceinline__ float dpp(float x) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
+// Whole-wave shifts: lane l reads lane l + 1 (kWaveShl1) or l - 1 (kWaveShr1);
+// lane 63 (resp. 0), whose source is outside the wave, reads 0.
+constexpr int kWaveShl1 = 0x130;
+constexpr int kWaveShr1 = 0x138;
 constexpr int kRowMirror = 0x140;
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kQuadXor3 = 0x1B;   // quad_perm [3,2,1,0]
