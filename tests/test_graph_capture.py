@@ -105,3 +105,67 @@ def test_training_calls_replay_from_a_graph():
         print(f"replay with inputs of seed {seed}", flush=True)
         for k, v in want.items():
             torch.testing.assert_close(got[k], v, rtol=0, atol=0, msg=lambda m, k=k: f"seed {seed}, {k}: {m}")
+
+
+def _mixer_draw(seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    b, d, l, N, R, Dm, width = 2, 64, 300, 16, 8, 32, 4
+    r = lambda *s, sc=1.0: torch.randn(*s, device=DEV, generator=g) * sc  # noqa: E731
+    return {
+        "xz": r(b, l, 2 * d).transpose(1, 2), "conv_w": r(d, 1, width, sc=0.5), "conv_b": r(d, sc=0.3),
+        "x_proj_w": r(R + 2 * N, d, sc=d ** -0.5), "dt_proj_w": r(d, R, sc=R ** -0.5),
+        "out_proj_w": r(Dm, d, sc=d ** -0.5), "out_proj_b": r(Dm, sc=0.1),
+        "A": -torch.exp(2 * torch.rand(d, N, device=DEV, generator=g)), "D": r(d),
+        "delta_bias": torch.rand(d, device=DEV, generator=g) - 3, "dout": r(b, l, Dm),
+    }
+
+
+MIXER = ("xz", "conv_w", "conv_b", "x_proj_w", "dt_proj_w", "out_proj_w", "out_proj_b", "A", "D", "delta_bias")
+
+
+def _mixer_step(t):
+    from mamba_cpu import mamba_inner_fn
+
+    out = mamba_inner_fn(t["xz"], t["conv_w"], t["conv_b"], t["x_proj_w"], t["dt_proj_w"], t["out_proj_w"],
+                         t["out_proj_b"], t["A"], D=t["D"], delta_bias=t["delta_bias"], delta_softplus=True)
+    out.backward(t["dout"])
+    return out
+
+
+def test_fused_mixer_replays_from_a_graph():
+    """The fused Mamba-1 mixer (its x_proj / dt_proj / out_proj products go
+    through rocBLAS from C++) captured forward + backward and replayed."""
+    static = _mixer_draw(0)
+    for k in MIXER:
+        static[k] = static[k].detach().requires_grad_()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for k in MIXER:
+                static[k].grad = None
+            _mixer_step(static)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for k in MIXER:
+        static[k].grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = _mixer_step(static)
+    torch.cuda.synchronize()
+    for seed in (1, 2, 3):
+        fresh = _mixer_draw(seed)
+        with torch.no_grad():
+            for k, v in fresh.items():
+                static[k].copy_(v)
+        graph.replay()
+        got = {"out": out.detach().clone(), **{"d" + k: static[k].grad.clone() for k in MIXER}}
+        torch.cuda.synchronize()
+        eager = _mixer_draw(seed)
+        for k in MIXER:
+            eager[k] = eager[k].detach().requires_grad_()
+        want = {"out": _mixer_step(eager).detach(), **{"d" + k: eager[k].grad for k in MIXER}}
+        torch.cuda.synchronize()
+        print(f"mixer replay with inputs of seed {seed}", flush=True)
+        for k, v in want.items():
+            torch.testing.assert_close(got[k], v, rtol=0, atol=0, msg=lambda m, k=k: f"seed {seed}, {k}: {m}")
