@@ -100,8 +100,8 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // from the chunk's last block (`last`), where they stay: the loop fetches
   // in every iteration, the last one re-reading its own block, so no load or
   // park is ever conditional.
-  auto fetch = [&](int64_t t0, bool last) {
-    if (t0 < t_full) {
+  auto fetch = [&](auto GUARD, int64_t t0, bool last) {
+    if (!decltype(GUARD)::value || t0 < t_full) {
       nu = xu.template load<Tx>();
       nd = xd.template load<Tx>();
       if (HAS_Z && WRITE_OUT) nz = xz.template load<Tx>();
@@ -129,7 +129,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   };
 
   if (kb0 < kb1) {
-    fetch(tb0, kb0 + 1 >= kb1);
+    fetch(std::true_type{}, tb0, kb0 + 1 >= kb1);
     park(static_cast<int>(kb0 & 1));
   }
   __syncthreads();
@@ -146,12 +146,15 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
 
   // Per block: prefetch the next block, compute this one, park the prefetch,
   // then store. Stores come last so that waiting for the prefetched loads
-  // never waits for this block's stores as well.
-  for (int64_t k = kb0; k < kb1; ++k) {
+  // never waits for this block's stores as well. Only the chunk's last block
+  // can be partial, so every fetch but the one of that block is unguarded:
+  // the loop runs the blocks before the last two with plain fetches, then
+  // the last two with guarded ones.
+  auto block = [&](auto GUARD, int64_t k) {
     const int buf = static_cast<int>(k & 1);
     const int64_t t0 = k * kScanBlockT;
     const bool has_next = k + 1 < kb1;
-    fetch(has_next ? t0 + kScanBlockT : t0, k + 2 >= kb1);
+    fetch(GUARD, has_next ? t0 + kScanBlockT : t0, k + 2 >= kb1);
 
     const int64_t t = t0 + j;
     const bool tv = t < L;
@@ -186,7 +189,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       }
       pacc[i] = acc;
     };
-    if (nvalid == kScanBlockT) {
+    if (!decltype(GUARD)::value || nvalid == kScanBlockT) {
       static_for<kScanBlockT>(step);
     } else {
       static_for<kScanBlockT>([&](auto I) {
@@ -216,7 +219,10 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
           buf_st<float>(wave_rsrc(p.ckpt + (row0 * p.nblk + k + 1) * N), ck_off + 64 * s, h[s]);
     }
     __syncthreads();
-  }
+  };
+  const int64_t kg = kb1 - 2 > kb0 ? kb1 - 2 : kb0;  // first block whose fetch may be guarded
+  for (int64_t k = kb0; k < kg; ++k) block(std::false_type{}, k);
+  for (int64_t k = kg; k < kb1; ++k) block(std::true_type{}, k);
   if (MODE == kFwdSummary) {
     dts = row_allreduce16(dts);
     if (rc.active) {

@@ -30,7 +30,21 @@ import torch
 from mamba_cpu import _C  # noqa: F401  (loads the operator library)
 
 _GRAPH_MODELS = ("mamba", "falcon_mamba", "mamba2")
+# Limits of mcpu_mixer_step (csrc/mixer_step.hip, check_step): batch rows,
+# conv window length, state size, and the float32 LDS budget that holds the
+# batch rows (padded to a power of two) of one workgroup.
 _MAX_FUSED_BATCH = 8
+_MAX_FUSED_CONV_STATE = 8
+_MAX_FUSED_DSTATE = 128
+_FUSED_LDS_FLOATS = 32768
+
+
+def _fused_lds_fits(batch_size, d_model, d_inner):
+    """Whether the fused step's workgroups can hold `batch_size` rows of the
+    normed hidden state (plus one row of scratch) and of the conv outputs in
+    LDS, as check_step requires."""
+    rows = 1 if batch_size <= 1 else 2 if batch_size <= 2 else 4 if batch_size <= 4 else 8
+    return (rows + 1) * d_model <= _FUSED_LDS_FLOATS and rows * d_inner <= _FUSED_LDS_FLOATS
 
 
 @torch.library.register_fake("mamba_cpu::mixer_step")
@@ -60,7 +74,8 @@ def fused_step_supported(model, cache, batch_size):
     """Whether `model`'s decode step can run as fused block steps: a
     transformers Mamba model on a ROCm GPU, one weight dtype, silu, at most 8
     batch rows, widths the fused kernels take, and a cache whose conv windows
-    are not recording past inputs."""
+    are not recording past inputs. Shapes the kernels would refuse keep the
+    unfused step."""
     if model.config.model_type != "mamba" or batch_size > _MAX_FUSED_BATCH:
         return False
     layers = getattr(getattr(model, "backbone", None), "layers", None)
@@ -75,12 +90,14 @@ def fused_step_supported(model, cache, batch_size):
                    mx.dt_proj.weight, mx.out_proj.weight, mx.out_proj.bias]
         if any(t is not None and (t.dtype != w.dtype or not t.is_contiguous()) for t in tensors):
             return False
-        if w.shape[1] % 4 or mx.intermediate_size % 4 or mx.ssm_state_size > 128:
+        if w.shape[1] % 4 or mx.intermediate_size % 4 or mx.ssm_state_size > _MAX_FUSED_DSTATE \
+                or mx.conv_kernel_size > _MAX_FUSED_CONV_STATE \
+                or not _fused_lds_fits(batch_size, w.shape[1], mx.intermediate_size):
             return False
         layer = cache.layers[blk.layer_idx]
         conv, ssm = layer.conv_states[0], layer.recurrent_states[0]
         if layer.record_past or conv is None or ssm is None or not conv.is_contiguous() \
-                or not ssm.is_contiguous() or conv.dtype != w.dtype or conv.shape[2] > 8:
+                or not ssm.is_contiguous() or conv.dtype != w.dtype or conv.shape[2] > _MAX_FUSED_CONV_STATE:
             return False
     return True
 
