@@ -41,12 +41,16 @@ const char* mcpu_last_error(void);
  * (result cached per device); exported so callers can fail early. */
 int mcpu_check_device(void);
 
-/* Library version string. */
+/* Library version string. 0.3.0: the argument blocks have grown fields since
+ * 0.1.0 (mcpu_scan_args.bwd_waves; mcpu_state_update_args.param_strides and
+ * the A, D and dt_bias strides), so a binding built against an older header
+ * passes a shorter block: check mcpu_args_size() first. */
 const char* mcpu_version(void);
 
 /* sizeof() of an argument block ("scan", "conv", "conv_update",
- * "state_update", "ssd", "mixer_step"), 0 for an unknown name; lets bindings
- * check their layout. */
+ * "state_update", "ssd", "mixer_step"), 0 for an unknown name. A binding must
+ * compare it with its own sizeof of each block it uses before its first call:
+ * the library reads a whole block, whatever the caller allocated. */
 size_t mcpu_args_size(const char* name);
 
 /* ------------------------------------------------------------------------ */
@@ -156,7 +160,10 @@ size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);
 int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
                             void* stream);
 
-/* Bytes of the per-device scratch array behind mcpu_selective_scan_bwd_noalloc. */
+/* Bytes of the per-device scratch array behind mcpu_selective_scan_bwd_noalloc.
+ * The array is a file-scope __device__ object: every device the library's code
+ * object is loaded on reserves it (in any process that uses any entry point
+ * there) until the process ends, whether or not this entry point is called. */
 #define MCPU_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* Backward that allocates nothing and takes no workspace. No counterpart in
@@ -164,8 +171,8 @@ int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t wor
  * under HIP graph capture, serving loops that forbid allocation). It runs
  * the kernels of mcpu_selective_scan_bwd with their scratch (partial sums,
  * chunk summaries, and block checkpoints when ckpt is NULL) in a fixed
- * library array of MCPU_NOALLOC_SCRATCH_BYTES per device, which each device
- * holds from the first call on it until the process ends. Results equal
+ * library array of MCPU_NOALLOC_SCRATCH_BYTES per device (reserved wherever
+ * the library is loaded, see above). Results equal
  * mcpu_selective_scan_bwd's. Returns MCPU_ERR_UNSUPPORTED, before any device
  * work, when mcpu_selective_scan_bwd_workspace_size(a) exceeds the array
  * (the training-step shape batch 8, dim 1536, seqlen 1024, dstate 16 needs
@@ -335,7 +342,8 @@ typedef struct mcpu_ssd_args {
   int64_t batch, seqlen, nheads, headdim, ngroups, dstate;
   int32_t dtype;                /* storage type of x, z, B, C, out, ysave, dout, dx, dz */
   int32_t dt_softplus;
-  float dt_limit_lo, dt_limit_hi; /* clamp of the step; lo <= 0 and hi = +inf: none */
+  float dt_limit_lo, dt_limit_hi; /* clamp of the step, always applied (mamba_ssm's default is 0, +inf,
+                                    which makes a negative raw step 0); the raw-dt gradient is 0 outside */
   /* forward outputs */
   void* out;                    /* like x */
   float* final_states;          /* (batch, nheads, headdim, dstate), optional */

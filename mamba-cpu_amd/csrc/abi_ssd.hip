@@ -111,7 +111,6 @@ SsdParams make_ssd(const mcpu_ssd_args* a, bool bwd = false) {
   p.hb = a->head_block != 0 ? a->head_block : head_block(a);
   p.nhb = static_cast<int>(a->nheads / p.hb);
   p.softplus = a->dt_softplus != 0;
-  p.clamp = (a->dt_limit_lo > 0.f || !std::isinf(a->dt_limit_hi)) ? 1 : 0;
   p.dt_lo = a->dt_limit_lo;
   p.dt_hi = a->dt_limit_hi;
   return p;

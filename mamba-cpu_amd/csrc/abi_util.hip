@@ -47,7 +47,7 @@ int zero_f32(float* p, int64_t n, hipStream_t stream) {
 
 extern "C" const char* mcpu_last_error(void) { return mcpu::g_err; }
 
-extern "C" const char* mcpu_version(void) { return "mamba_hip 0.1.0 (gfx950)"; }
+extern "C" const char* mcpu_version(void) { return "mamba_hip 0.3.0 (gfx950)"; }
 
 extern "C" size_t mcpu_args_size(const char* name) {
   if (name == nullptr) return 0;

@@ -338,16 +338,16 @@ __device__ __forceinline__ float wave_total(float v) {
 }
 
 // The effective step for dt + dt_bias = pre and, when grad, d(step)/d(raw
-// dt): the softplus derivative, zero where the clamp is active.
+// dt): the softplus derivative, zero where the clamp to [dt_lo, dt_hi] is
+// active. The clamp always applies, as in mamba_ssm (its default (0, inf)
+// makes a negative raw step 0), and keeps a NaN step NaN, as torch.clamp does.
 __device__ __forceinline__ float step_of(const SsdParams& p, float pre, float* grad) {
   float sg = 1.f;
   float st = pre;
   if (p.softplus) st = softplus_sigmoid(pre, sg);
-  if (p.clamp) {
-    const bool inside = st >= p.dt_lo && st <= p.dt_hi;
-    st = fminf(fmaxf(st, p.dt_lo), p.dt_hi);
-    if (!inside) sg = 0.f;
-  }
+  const bool inside = st >= p.dt_lo && st <= p.dt_hi;
+  st = st < p.dt_lo ? p.dt_lo : (st > p.dt_hi ? p.dt_hi : st);
+  if (!inside) sg = 0.f;
   if (grad) *grad = sg;
   return st;
 }

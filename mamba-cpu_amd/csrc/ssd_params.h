@@ -65,8 +65,7 @@ struct SsdParams {
   int in_order;             // chunk states carried by the in-order kernels (one launch per
                             // direction, no chunk-end states stored) instead of two launches
   int softplus;
-  int clamp;                // the step is clamped to [dt_lo, dt_hi]
-  float dt_lo, dt_hi;
+  float dt_lo, dt_hi;       // the step is clamped to [dt_lo, dt_hi]
 };
 
 hipError_t ssd_fwd_launch(const SsdParams& p, int dtype, hipStream_t st);

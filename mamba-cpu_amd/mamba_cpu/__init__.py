@@ -17,7 +17,7 @@ from mamba_cpu.ops import (
 )
 from mamba_cpu.reference import causal_conv1d_ref, selective_scan_ref
 
-__version__ = "0.1.0"
+__version__ = "0.3.0"
 
 __all__ = [
     "causal_conv1d_fn",

@@ -42,10 +42,11 @@ def _dt(dt, dt_bias, dt_softplus, dt_limit):
     step = softplus(pre) if dt_softplus else pre
     grad = sigmoid(pre) if dt_softplus else np.ones_like(pre)
     lo, hi = dt_limit
-    if lo > 0.0 or hi < np.inf:
-        inside = (step >= lo) & (step <= hi)
-        step = np.clip(step, lo, hi)
-        grad = grad * inside
+    # Always clamped, as mamba_ssm's _chunk_cumsum kernels and transformers'
+    # mamba2_chunk_scan do: with the default (0, inf) a negative raw step is 0.
+    inside = (step >= lo) & (step <= hi)
+    step = np.clip(step, lo, hi)
+    grad = grad * inside
     return step, grad
 
 

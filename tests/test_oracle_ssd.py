@@ -248,3 +248,42 @@ def test_varlen_states_equal_each_sequence_alone():
         pre = {k: c[k][:, :cu[i + 1]] for k in ("x", "dt", "B", "C", "z")}
         pre.update(A=c["A"], D=c["D"], dt_bias=c["dt_bias"], initial_states=c["initial_states"])
         np.testing.assert_allclose(plain[i], S.ssd_fwd(**pre, **kw)[1][0], rtol=1e-12, atol=1e-12)
+
+
+def test_raw_negative_steps_clamp_like_transformers():
+    """Without softplus, a negative dt + dt_bias is clamped to the default
+    dt_limit (0, inf), so that step is 0 and its raw-dt gradient 0, as
+    mamba_ssm's kernels and transformers' pure-torch mamba2_chunk_scan do
+    (torch.clamp in its first lines). About half of the raw steps here are
+    negative; the oracle's outputs, final states and every gradient match
+    autograd through transformers' function (float32, so rtol 1e-4)."""
+    transformers = pytest.importorskip("transformers", minversion="5.0")
+    from transformers.models.mamba2 import modeling_mamba2 as M2
+
+    fn = getattr(M2.mamba2_chunk_scan, "__wrapped__", M2.mamba2_chunk_scan)
+    rng = np.random.default_rng(3)
+    b, l, h, p, g, n = 2, 70, 4, 8, 2, 8
+    c = dict(x=rng.standard_normal((b, l, h, p)), dt=rng.standard_normal((b, l, h)) * 0.5,
+             A=-np.exp(rng.random(h) * math.log(8)), B=rng.standard_normal((b, l, g, n)),
+             C=rng.standard_normal((b, l, g, n)), D=rng.standard_normal(h), dt_bias=rng.random(h) * 0.2,
+             initial_states=rng.standard_normal((b, h, p, n)))
+    assert 0.3 < ((c["dt"] + c["dt_bias"]) < 0).mean() < 0.7
+    t = {k: torch.tensor(v, dtype=torch.float32, requires_grad=True) for k, v in c.items()}
+    out, fin = fn(t["x"], t["dt"], t["A"], t["B"], t["C"], 32, D=t["D"], dt_bias=t["dt_bias"],
+                  initial_states=t["initial_states"], dt_softplus=False, return_final_states=True)
+    W, V = rng.standard_normal(out.shape), rng.standard_normal(fin.shape)
+    ((out * torch.tensor(W, dtype=torch.float32)).sum() + (fin * torch.tensor(V, dtype=torch.float32)).sum()).backward()
+    want, want_fin = S.ssd_fwd(**c, dt_softplus=False)
+    np.testing.assert_allclose(want, out.detach().numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(want_fin, fin.detach().numpy(), rtol=1e-4, atol=1e-5)
+    grads = S.ssd_bwd(**c, z=None, dt_softplus=False, dout=W, dfinal_states=V)
+    names = ("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "initial_states")
+    for name, gw in zip(names, grads):
+        if name == "z":
+            assert gw is None
+            continue
+        ref = t[name].grad.numpy()
+        scale = max(np.abs(ref).max(), 1.0)
+        np.testing.assert_allclose(gw / scale, ref / scale, rtol=1e-4, atol=1e-5, err_msg=name)
+    # the clamped steps pass no gradient to the raw dt
+    assert np.all(grads[1][(c["dt"] + c["dt_bias"][None, None]) < 0] == 0)

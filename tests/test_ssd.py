@@ -111,6 +111,20 @@ def test_options_match_oracle(opts, softplus, limit):
     check(c, *run(c, softplus=softplus, limit=limit), softplus=softplus, limit=limit)
 
 
+def test_raw_negative_steps_are_clamped():
+    """Without softplus, a negative raw step is clamped to the default
+    dt_limit (0, inf): step 0 and no raw-dt gradient there (mamba_ssm's and
+    transformers' semantics; the oracle is pinned against transformers'
+    mamba2_chunk_scan in tests/test_oracle_ssd.py)."""
+    c = case(2, 150, 4, 32, 2, 32, seed=6, init=True)
+    c["dt"] = c["dt"] + 0.8  # about half of dt + dt_bias below 0
+    out, fin, got, W, V = run(c, softplus=False)
+    check(c, out, fin, got, W, V, softplus=False)
+    neg = (c["dt"] + c["dt_bias"][None, None]) < 0
+    assert 0.2 < neg.float().mean().item() < 0.8
+    assert torch.all(got["dt"].cpu()[neg] == 0)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_low_precision_storage(dtype):
     c = case(2, 150, 4, 64, 2, 64, seed=9, dtype=dtype)
