@@ -13,6 +13,19 @@
 // at the start of every block (checkpoints for the backward), and y before the
 // z gate (lets the backward skip recomputing it).
 //
+// Precision of long runs: v_exp_f32 is correctly rounded for about 95 % of
+// arguments and otherwise mostly one ulp low (mean error -0.04 ulp, measured
+// over [-8, 0]), so a slowly decaying state carried through hundreds of
+// serial steps drifts low by that bias times the step count. Time-chunked
+// runs (CORR) therefore carry each 16-step block's start state with one
+// exponential of the block's summed step instead of the product of its 16
+// per-step factors: h_end += (exp(A sum dt) - prod a) h_start. At batch 1,
+// dim 1536, seqlen 2048 with A = -U(0, 1) that takes the largest output error
+// against float64 from 5.4e-4 to 2.0e-4 (the reference's kernels: 2.6e-4);
+// it costs one multiply per state-step (about 10 % of the forward), which
+// unchunked runs (rows that fill the GPU, typically short or fast-decaying)
+// do not pay.
+//
 // Time chunks (when there are too few rows to fill the GPU): a summary pass
 // scans every chunk but the last from a zero state and records the state at
 // its end and its sum of dt; the main pass then starts chunk c from
@@ -29,7 +42,7 @@ constexpr int kFwdWaves = 4;
 // (ckpt / last_state), or the chunk summaries of the chunked scan.
 enum FwdMode { kFwdOut = 0, kFwdStates = 1, kFwdSummary = 2 };
 
-template <typename Tx, int SPL, bool HAS_Z, int MODE>
+template <typename Tx, int SPL, bool HAS_Z, int MODE, bool CORR>
 __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanParams p) {
   constexpr bool WRITE_OUT = MODE == kFwdOut;
   constexpr int W = kFwdWaves;
@@ -176,6 +189,13 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     if (MODE == kFwdSummary && tv) dts += dt;
 
     float pacc[kScanBlockT];
+    // CORR: the block's start state and the product of its decay factors.
+    float hstart[SPL], prod[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) {
+      hstart[s] = h[s];
+      prod[s] = 1.f;
+    }
     auto step = [&](auto I) {
       constexpr int i = decltype(I)::value;
       const float dti = row_bcast<i>(dt);
@@ -185,6 +205,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       for (int s = 0; s < SPL; ++s) {
         const float a = fast_exp2(dti * A2[s]);
         h[s] = fmaf(a, h[s], dtui * Bv[s][i]);
+        if (CORR) prod[s] *= a;
         if (WRITE_OUT) acc = fmaf(h[s], Cv[s][i], acc);
       }
       pacc[i] = acc;
@@ -198,6 +219,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       });
     }
 
+    if (CORR) {
+      // The start state decays by exp(A * the block's summed step).
+      const float bdt = row_allreduce16(j < nvalid ? dt : 0.f);
+#pragma unroll
+      for (int s = 0; s < SPL; ++s) h[s] = fmaf(fast_exp2(A2[s] * bdt) - prod[s], hstart[s], h[s]);
+    }
     float y = 0.f, yg = 0.f;
     if (WRITE_OUT) {
       y = row_reduce_scatter16(pacc, j);
@@ -241,8 +268,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
 template <typename Tx, int SPL, bool HAS_Z, int MODE>
 static hipError_t launch_fwd(const ScanParams& p, hipStream_t stream) {
   const int64_t blocks = p.batch * p.ngroups * p.nblk_c * p.nchunk;
-  hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, MODE>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(64 * kFwdWaves), 0, stream, p);
+  if (p.nchunk > 1)
+    hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, MODE, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(64 * kFwdWaves), 0, stream, p);
+  else
+    hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, MODE, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(64 * kFwdWaves), 0, stream, p);
   return hipGetLastError();
 }
 

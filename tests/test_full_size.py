@@ -134,13 +134,13 @@ def test_forward_fp32_b1_d1536_l2048():
     values near zero: float32 cannot meet atol 1e-5 there. The reference's
     own kernels miss it against float64 on 27 of 3.1 M elements (largest error
     2.6e-4 at |out| up to 309). So the float32 check is: the GPU's error
-    against float64 is within three times the reference kernels' own (the
+    against float64 is within 1.5 times the reference kernels' own (the
     largest error, and the count of elements beyond rtol 1e-4 / atol 1e-5),
     and every element meets rtol 1e-4 / atol 1e-3 against both. Measured on
-    an MI355X: largest error 5.4e-4 against the reference's 2.6e-4, 52
-    elements beyond against its 27; the time-chunked forward composes
-    independently scanned chunks, another summation order than one serial
-    pass."""
+    an MI355X: largest error 2.0e-4, 18 elements beyond (v_exp_f32's slight
+    low bias, compounded over the slowly decaying steps, gave 5.4e-4 and 52
+    before the chunked forward carried each block's start state with one
+    exponential of its summed step)."""
     need_ref()
     inp = scan_c1()
     note("scan fwd fp32 (1, 1536, 2048, 16): GPU")
@@ -163,8 +163,8 @@ def test_forward_fp32_b1_d1536_l2048():
     g_over, r_over = int((gerr > bound).sum()), int((rerr > bound).sum())
     note(f"  largest error vs float64: GPU {gerr.max():.3g}, reference {rerr.max():.3g}; elements beyond "
          f"rtol 1e-4 / atol 1e-5: GPU {g_over}, reference {r_over} of {out.size}")
-    assert gerr.max() <= 3 * rerr.max()
-    assert g_over <= 3 * max(r_over, 1)
+    assert gerr.max() <= 1.5 * rerr.max()
+    assert g_over <= 1.5 * max(r_over, 1)
 
 
 def test_training_step_fp32_b8_d1536_l1024():
