@@ -8,6 +8,8 @@
 
 namespace mcpu {
 
+int64_t conv_wide_nseg(int64_t seqlen);
+
 namespace {
 
 int check_conv(const mcpu_conv_args* a) {
@@ -17,9 +19,9 @@ int check_conv(const mcpu_conv_args* a) {
   // A tensor with no elements may come as NULL (torch's empty tensors do).
   if ((a->x == nullptr && a->batch * a->dim * a->seqlen > 0) || (a->weight == nullptr && a->dim > 0))
     return fail(MCPU_ERR_INVALID, "causal_conv1d: x and weight are required");
-  if (a->width < 1 || a->width > kConvMaxW)
+  if (a->width < 1 || a->width > kConvWideMaxW)
     return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d: width must be in [1, %lld], got %lld",
-                (long long)kConvMaxW, (long long)a->width);
+                (long long)kConvWideMaxW, (long long)a->width);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "causal_conv1d: bad dtype %d", a->dtype);
   if (a->seq_idx != nullptr &&
       (a->initial_states != nullptr || a->final_states != nullptr || a->dfinal_states != nullptr ||
@@ -128,7 +130,12 @@ bool cl_ok(const ConvParams& p, int dtype, bool bwd) {
   return cl_operand(p.out, p.sout, dtype);
 }
 
+// Bytes of the backward's workspace: the dweight/dbias partials, and for
+// widths above kConvMaxW the per-element dout * act'(pre) after them.
 size_t conv_ws(const ConvParams& p) {
+  if (p.width > kConvMaxW)
+    return align_up(sizeof(float) * p.batch * conv_wide_nseg(p.seqlen) * p.dim * (p.width + 1)) +
+           align_up(sizeof(float) * p.batch * p.dim * p.seqlen);
   ConvParams q = p;
   conv_vt_shape(q, kConvVTSteps);  // the fewest steps per thread: the most segments
   conv_cl_shape(q);
@@ -187,6 +194,10 @@ extern "C" int mcpu_causal_conv1d_bwd(const mcpu_conv_args* a, void* workspace,
   p.dx = a->dx;
   p.dinit = a->dinitial_states;
   p.dw_part = static_cast<float*>(workspace);
+  if (p.width > kConvMaxW)
+    p.dpre = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      align_up(sizeof(float) * p.batch * conv_wide_nseg(p.seqlen) * p.dim *
+                                               (p.width + 1)));
   p.vt = vt_ok(p, a->dtype, true);
   if (p.vt) conv_vt_shape(p, p.vt);
   conv_cl_shape(p);
@@ -210,9 +221,9 @@ extern "C" int mcpu_causal_conv1d_update(const mcpu_conv_update_args* a, void* s
   if (a->batch * a->dim > 0 &&
       (a->x == nullptr || a->conv_state == nullptr || a->weight == nullptr || a->out == nullptr))
     return fail(MCPU_ERR_INVALID, "causal_conv1d_update: x, conv_state, weight and out are required");
-  if (a->width < 1 || a->width > kConvMaxW)
+  if (a->width < 1 || a->width > kConvWideMaxW)
     return fail(MCPU_ERR_UNSUPPORTED, "causal_conv1d_update: width must be in [1, %lld]",
-                (long long)kConvMaxW);
+                (long long)kConvWideMaxW);
   if (a->state_len < a->width - 1)
     return fail(MCPU_ERR_INVALID, "conv_state length (%lld) must be at least width - 1 (%lld)",
                 (long long)a->state_len, (long long)(a->width - 1));

@@ -209,6 +209,128 @@ __global__ void __launch_bounds__(256) conv_bwd_kernel(const ConvParams p) {
   part[W] = dbias;
 }
 
+// Widths above kConvMaxW (the reference's F.conv1d takes any width): per-element
+// kernels whose tap loops read the weights from memory. Forward: one thread per
+// output. Backward: dpre = dout * act'(pre) per element into the workspace,
+// then dX per input position (W taps of dpre, plus dfinal_states), and
+// dweight/dbias partials over segments of kConvWideSeg steps, summed by
+// conv_reduce_dw_kernel. Threads run along the contiguous dimension (channel
+// or time) of x.
+
+// (b, d, i) of thread tid over a (batch, dim, span) index space.
+__device__ __forceinline__ ConvRow wide_index(const ConvParams& p, int64_t tid, int64_t span, int64_t& i) {
+  ConvRow c;
+  c.r = 0;
+  if (p.channels_last) {
+    c.d = tid % p.dim;
+    tid /= p.dim;
+    i = tid % span;
+    c.b = tid / span;
+  } else {
+    i = tid % span;
+    tid /= span;
+    c.d = tid % p.dim;
+    c.b = tid / p.dim;
+  }
+  return c;
+}
+
+// The pre-activation at step t: bias + sum_k w[k] X[t-(W-1)+k], taps from
+// another packed sequence counting as zero.
+template <typename T, bool SEQ>
+__device__ float wide_pre(const ConvParams& p, const ConvRow& c, int64_t t) {
+  const int64_t W = p.width;
+  const float* w = p.w + c.d * W;
+  const int64_t sid = SEQ ? conv_seq(p, c.b, t) : 0;
+  float acc = p.bias ? p.bias[c.d] : 0.f;
+  for (int64_t k = 0; k < W; ++k) {
+    const int64_t s = t - (W - 1) + k;
+    if (SEQ && conv_seq(p, c.b, s) != sid) continue;
+    acc = fmaf(w[k], conv_x<T>(p, c, s), acc);
+  }
+  return acc;
+}
+
+template <typename T, bool SEQ>
+__global__ void __launch_bounds__(256) conv_fwd_wide_kernel(const ConvParams p) {
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
+  if (tid >= p.batch * p.dim * p.seqlen) return;
+  int64_t t;
+  const ConvRow c = wide_index(p, tid, p.seqlen, t);
+  float acc = wide_pre<T, SEQ>(p, c, t);
+  if (p.silu) acc = acc * sigmoid(acc);
+  st<T>(p.out, c.b * p.sout[0] + c.d * p.sout[1] + t * p.sout[2], acc);
+}
+
+template <typename T, bool SEQ>
+__global__ void __launch_bounds__(256) conv_dpre_wide_kernel(const ConvParams p) {
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
+  if (tid >= p.batch * p.dim * p.seqlen) return;
+  int64_t t;
+  const ConvRow c = wide_index(p, tid, p.seqlen, t);
+  const float go = ld<T>(p.dout, c.b * p.sdo[0] + c.d * p.sdo[1] + t * p.sdo[2]);
+  float v = go;
+  if (p.silu) {
+    const float pre = wide_pre<T, SEQ>(p, c, t);
+    const float sg = sigmoid(pre);
+    v = go * sg * (1.f + pre * (1.f - sg));
+  }
+  p.dpre[(c.b * p.dim + c.d) * p.seqlen + t] = v;
+}
+
+// dX[s] for s in [-(W-1), L): to dx (s >= 0) or dinitial_states (s < 0).
+template <typename T, bool SEQ>
+__global__ void __launch_bounds__(256) conv_dx_wide_kernel(const ConvParams p) {
+  const int64_t W = p.width, W1 = W - 1, L = p.seqlen, span = L + W1;
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
+  if (tid >= p.batch * p.dim * span) return;
+  int64_t i;
+  const ConvRow c = wide_index(p, tid, span, i);
+  const int64_t s = i - W1;
+  if (s < 0 && p.dinit == nullptr) return;
+  const float* w = p.w + c.d * W;
+  const float* dp = p.dpre + (c.b * p.dim + c.d) * L;
+  const int64_t sid = SEQ ? conv_seq(p, c.b, s) : 0;
+  float acc = 0.f;
+  for (int64_t k = 0; k < W; ++k) {
+    const int64_t t = s + W1 - k;  // the output that reads X[s] through tap k
+    if (t < 0 || t >= L) continue;
+    if (SEQ && conv_seq(p, c.b, t) != sid) continue;
+    acc = fmaf(w[k], dp[t], acc);
+  }
+  if (p.dfinal != nullptr && s >= L - W1) acc += ld<T>(p.dfinal, (c.b * p.dim + c.d) * W1 + (s - (L - W1)));
+  if (s >= 0) st<T>(p.dx, c.b * p.sdx[0] + c.d * p.sdx[1] + s * p.sdx[2], acc);
+  else st<T>(p.dinit, (c.b * p.dim + c.d) * W1 + (s + W1), acc);
+}
+
+// part[((b * nseg + g) * dim + d) * (W+1) + k]: over the steps t of segment g,
+// sum dpre[t] X[t-(W-1)+k] (k < W) or dpre[t] (k = W).
+template <typename T, bool SEQ>
+__global__ void __launch_bounds__(256) conv_dw_wide_kernel(const ConvParams p, int64_t nseg) {
+  const int64_t W = p.width, W1 = W - 1, L = p.seqlen, per = p.dim * (W + 1);
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
+  if (tid >= p.batch * nseg * per) return;
+  const int64_t e = tid % per, bg = tid / per;
+  ConvRow c;
+  c.r = 0;
+  c.d = e / (W + 1);
+  c.b = bg / nseg;
+  const int64_t k = e % (W + 1), g = bg % nseg;
+  const int64_t t0 = g * kConvWideSeg, t1 = t0 + kConvWideSeg < L ? t0 + kConvWideSeg : L;
+  const float* dp = p.dpre + (c.b * p.dim + c.d) * L;
+  float acc = 0.f;
+  for (int64_t t = t0; t < t1; ++t) {
+    if (k == W) {
+      acc += dp[t];
+      continue;
+    }
+    const int64_t s = t - W1 + k;
+    if (SEQ && conv_seq(p, c.b, s) != conv_seq(p, c.b, t)) continue;
+    acc = fmaf(dp[t], conv_x<T>(p, c, s), acc);
+  }
+  p.dw_part[tid] = acc;
+}
+
 // dweight[d, k] / dbias[d] = sum over the (batch, R or segment) partials.
 // A workgroup covers 64 consecutive (d, k) entries; its four waves each sum
 // every fourth partial (four loads in flight per lane), then combine in LDS.
@@ -249,7 +371,7 @@ __global__ void __launch_bounds__(256) conv_reduce_dw_kernel(const float* __rest
 // state is a ring buffer (the upstream causal_conv1d package's semantics): the
 // W-1 inputs before x sit at (cs - (W-1) + k) mod state_len, and x[s] is
 // written at (cs + s) mod state_len after every output has been computed.
-template <typename T>
+template <typename T, bool WIDE>
 __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams p) {
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x;
   if (tid >= p.batch * p.dim) return;
@@ -276,15 +398,22 @@ __global__ void __launch_bounds__(256) conv_update_kernel(const ConvUpdateParams
     const int64_t pos = ring ? wrap(cs - S + i) : i;
     return ld<T>(p.state, sb + pos * p.sst[2]);
   };
-  float w[kConvMaxW];
+  // WIDE (widths above kConvMaxW): the taps read the weights from memory.
+  float w[WIDE ? 1 : kConvMaxW];
+  if constexpr (!WIDE) {
 #pragma unroll
-  for (int k = 0; k < kConvMaxW; ++k) w[k] = k < W ? p.w[d * W + k] : 0.f;
+    for (int k = 0; k < kConvMaxW; ++k) w[k] = k < W ? p.w[d * W + k] : 0.f;
+  }
   const float bias = p.bias ? p.bias[d] : 0.f;
   for (int64_t s = 0; s < L; ++s) {
     float acc = bias;
+    if constexpr (WIDE) {
+      for (int k = 0; k < W; ++k) acc = fmaf(p.w[d * W + k], full(S - (W - 1) + s + k), acc);
+    } else {
 #pragma unroll
-    for (int k = 0; k < kConvMaxW; ++k)
-      if (k < W) acc = fmaf(w[k], full(S - (W - 1) + s + k), acc);
+      for (int k = 0; k < kConvMaxW; ++k)
+        if (k < W) acc = fmaf(w[k], full(S - (W - 1) + s + k), acc);
+    }
     if (p.silu) acc = acc * sigmoid(acc);
     st<T>(p.out, ob + s * p.sout[2], acc);
   }
@@ -960,6 +1089,44 @@ static hipError_t launch_vt_dtype(const ConvParams& p, int dtype, bool bwd, hipS
 
 static unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
+// Segments of the per-element backward's dweight partials.
+int64_t conv_wide_nseg(int64_t seqlen) { return seqlen > 0 ? (seqlen + kConvWideSeg - 1) / kConvWideSeg : 1; }
+
+template <typename T, bool SEQ>
+static hipError_t launch_wide_seq(const ConvParams& p, bool bwd, float* dweight, float* dbias, hipStream_t st) {
+  const int64_t n = p.batch * p.dim * p.seqlen;
+  if (!bwd) {
+    if (n > 0) hipLaunchKernelGGL((conv_fwd_wide_kernel<T, SEQ>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+    return hipGetLastError();
+  }
+  if (n > 0) hipLaunchKernelGGL((conv_dpre_wide_kernel<T, SEQ>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+  const int64_t nx = p.batch * p.dim * (p.seqlen + p.width - 1);
+  if (nx > 0) hipLaunchKernelGGL((conv_dx_wide_kernel<T, SEQ>), dim3(blocks_for(nx)), dim3(256), 0, st, p);
+  const int64_t nseg = conv_wide_nseg(p.seqlen), per = p.dim * (p.width + 1);
+  if (p.batch * nseg * per > 0)
+    hipLaunchKernelGGL((conv_dw_wide_kernel<T, SEQ>), dim3(blocks_for(p.batch * nseg * per)), dim3(256), 0, st,
+                       p, nseg);
+  hipLaunchKernelGGL(conv_reduce_dw_kernel, dim3(static_cast<unsigned>((per + 63) / 64)), dim3(256), 0, st,
+                     p.dw_part, dweight, dbias, p.batch * nseg, p.dim, p.width);
+  return hipGetLastError();
+}
+
+static hipError_t launch_wide(const ConvParams& p, int dtype, bool bwd, float* dweight, float* dbias,
+                              hipStream_t st) {
+  const bool seq = p.seq_idx != nullptr;
+  switch (dtype) {
+    case MCPU_F32:
+      return seq ? launch_wide_seq<float, true>(p, bwd, dweight, dbias, st)
+                 : launch_wide_seq<float, false>(p, bwd, dweight, dbias, st);
+    case MCPU_BF16:
+      return seq ? launch_wide_seq<bf16, true>(p, bwd, dweight, dbias, st)
+                 : launch_wide_seq<bf16, false>(p, bwd, dweight, dbias, st);
+    default:
+      return seq ? launch_wide_seq<f16, true>(p, bwd, dweight, dbias, st)
+                 : launch_wide_seq<f16, false>(p, bwd, dweight, dbias, st);
+  }
+}
+
 // The chunked kernels, specialised for widths 2..5 (Mamba's is 4).
 template <typename T, bool SEQ>
 static hipError_t launch_generic_seq(const ConvParams& p, bool bwd, unsigned grid, hipStream_t st) {
@@ -998,7 +1165,9 @@ static hipError_t launch_generic_dtype(const ConvParams& p, int dtype, bool bwd,
 
 hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
-  if (n > 0 && p.vt) {
+  if (p.width > kConvMaxW) {
+    if (hipError_t e = launch_wide(p, dtype, false, nullptr, nullptr, st)) return e;
+  } else if (n > 0 && p.vt) {
     if (hipError_t e = launch_vt_dtype(p, dtype, false, st)) return e;
   } else if (n > 0 && p.cl) {
     if (hipError_t e = launch_cl_dtype(p, dtype, false, st)) return e;
@@ -1019,6 +1188,7 @@ hipError_t conv_fwd_launch(const ConvParams& p, int dtype, hipStream_t st) {
 
 hipError_t conv_bwd_launch(const ConvParams& p, int dtype, float* dweight, float* dbias, hipStream_t st) {
   const int64_t n = p.batch * p.dim * p.R;
+  if (p.width > kConvMaxW) return launch_wide(p, dtype, true, dweight, dbias, st);
   if (n > 0 && p.vt) {
     if (hipError_t e = launch_vt_dtype(p, dtype, true, st)) return e;
     const int64_t per = p.dim * (p.width + 1);
@@ -1071,10 +1241,20 @@ hipError_t conv_update_launch(const ConvUpdateParams& p, int dtype, hipStream_t 
     }
     if (done) return hipGetLastError();
   }
+  const bool wide = p.width > kConvMaxW;
   switch (dtype) {
-    case MCPU_F32: hipLaunchKernelGGL(conv_update_kernel<float>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-    case MCPU_BF16: hipLaunchKernelGGL(conv_update_kernel<bf16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
-    default: hipLaunchKernelGGL(conv_update_kernel<f16>, dim3(blocks_for(n)), dim3(256), 0, st, p); break;
+    case MCPU_F32:
+      if (wide) hipLaunchKernelGGL((conv_update_kernel<float, true>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((conv_update_kernel<float, false>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      break;
+    case MCPU_BF16:
+      if (wide) hipLaunchKernelGGL((conv_update_kernel<bf16, true>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((conv_update_kernel<bf16, false>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      break;
+    default:
+      if (wide) hipLaunchKernelGGL((conv_update_kernel<f16, true>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((conv_update_kernel<f16, false>), dim3(blocks_for(n)), dim3(256), 0, st, p);
+      break;
   }
   return hipGetLastError();
 }

@@ -9,7 +9,9 @@
 namespace mcpu {
 
 constexpr int kConvT = 8;      // conv steps per chunk
-constexpr int kConvMaxW = 16;  // largest supported conv width
+constexpr int kConvMaxW = 16;  // widest conv of the register-window kernels
+constexpr int64_t kConvWideMaxW = 1 << 16;  // widest conv (the per-element kernels above kConvMaxW)
+constexpr int kConvWideSeg = 256;  // steps per dweight partial of the per-element backward
 constexpr int kConvRMax = 16;  // most threads walking one (batch, channel) row
 constexpr int kConvVTSteps = 8;  // steps per thread of the time-contiguous fast path
 constexpr int kConvClG = 8;      // unrolled steps per group of the channel-contiguous fast path
@@ -26,6 +28,7 @@ struct ConvParams {
   void* dx;
   void* dinit;
   float* dw_part;   // (batch, R, dim, W + 1): per-thread partial dw and dbias
+  float* dpre;      // widths above kConvMaxW: (batch, dim, seqlen) float32 dout * act'(pre)
   int64_t batch, dim, seqlen, width;
   int64_t nchunks, R;
   int64_t sx[3], sinit[3], sout[3], sdo[3], sdx[3];

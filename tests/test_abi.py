@@ -206,7 +206,7 @@ def test_conv_and_state_update_reject_bad_arguments():
     rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
     assert rc == _C.MCPU_ERR_INVALID and "out is required" in msg
     c.out = 16
-    c.width = 17
+    c.width = (1 << 16) + 1  # widths up to 65536 run (above 16 on the per-element kernels)
     rc, msg = _rc(L.mcpu_causal_conv1d_fwd, ctypes.byref(c), None)
     assert rc in (_C.MCPU_ERR_INVALID, _C.MCPU_ERR_UNSUPPORTED) and "width" in msg
     u = _C.ConvUpdateArgs()

@@ -25,7 +25,7 @@ def close(got, want, rtol, atol, name=""):
                                rtol=rtol, atol=atol, err_msg=name)
 
 
-@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7])
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7, 16, 17, 40])
 @pytest.mark.parametrize("activation", [None, "silu"])
 @pytest.mark.parametrize("has_bias", [False, True])
 def test_matches_oracle(width, activation, has_bias):
@@ -181,7 +181,7 @@ def test_update_continuous_batching_matches_oracle(seqlen, state_len, mode, widt
             cs = cs + (1 if seqlen is None else seqlen)
 
 
-@pytest.mark.parametrize("width", [1, 2, 4, 7])
+@pytest.mark.parametrize("width", [1, 2, 4, 7, 17, 33, 60])
 @pytest.mark.parametrize("activation", [None, "silu"])
 @pytest.mark.parametrize("with_init", [False, True])
 @pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
@@ -421,3 +421,58 @@ def test_channel_contiguous_long_segments_match_time_contiguous(packed):
     torch.testing.assert_close(dx1, dx2, rtol=1e-6, atol=1e-6)
     torch.testing.assert_close(dw1, dw2, rtol=1e-5, atol=1e-2)
     torch.testing.assert_close(db1, db2, rtol=1e-5, atol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["contiguous", "channels_last"])
+def test_wide_width_packed_sequences_and_long_rows(dtype, layout):
+    """Widths above 16 run per-element kernels (the reference's F.conv1d takes
+    any width): forward, final states and every gradient against the oracle
+    with packed sequences (seq_idx, cuts inside and across the taps' reach),
+    and over 700 steps (three dweight segments of 256 steps), in float32 and
+    bfloat16."""
+    torch.manual_seed(3)
+    b, d, l, width = 2, 12, 700, 24
+    if layout == "contiguous":
+        x = torch.randn(b, d, l, device=DEV).to(dtype)
+    else:
+        x = torch.randn(b, l, d, device=DEV).to(dtype).transpose(1, 2)
+    x.requires_grad_()
+    w = torch.randn(d, width, device=DEV, requires_grad=True)
+    bias = torch.randn(d, device=DEV, requires_grad=True)
+    seq = torch.zeros(b, l, dtype=torch.int32)
+    for r, cuts in enumerate([[5, 30, 31, 400], [300]]):
+        for c in cuts:
+            seq[r, c:] += 1
+    seq = seq.to(DEV)
+    out = causal_conv1d_fn(x, w, bias, seq_idx=seq, activation="silu")
+    want, _ = O.causal_conv1d_fwd(x.float(), w, bias, None, "silu", seq_idx=seq.cpu().numpy())
+    tol = (1e-5, 1e-5) if dtype == torch.float32 else (2e-2, 2e-2)
+    close(out, want, *tol, "out")
+    G = torch.randn(b, d, l, device=DEV).to(dtype)
+    (out.float() * G.float()).sum().backward()
+    dx, dw, db, _ = O.causal_conv1d_bwd(x.float(), w, bias, None, G.float(), "silu", None,
+                                        seq_idx=seq.cpu().numpy())
+    gtol = (1e-4, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)
+    close(x.grad, dx, *gtol, "dx")
+    scale = max(np.abs(dw).max(), 1.0)
+    close(w.grad / scale, dw / scale, *gtol, "dweight")
+    close(bias.grad / max(np.abs(db).max(), 1.0), db / max(np.abs(db).max(), 1.0), *gtol, "dbias")
+
+
+@pytest.mark.parametrize("seqlen", [None, 3])
+def test_wide_width_update_matches_oracle(seqlen):
+    """The decode update at width 20 (taps read from memory), several steps,
+    against the oracle, output and state."""
+    torch.manual_seed(5)
+    b, d, width, state_len = 3, 10, 20, 22
+    w = torch.randn(d, width, device=DEV)
+    bias = torch.randn(d, device=DEV)
+    state = torch.randn(b, d, state_len, device=DEV)
+    want_state = state.cpu().double().numpy()
+    for step in range(3):
+        x = torch.randn(b, d, device=DEV) if seqlen is None else torch.randn(b, d, seqlen, device=DEV)
+        out = causal_conv1d_update(x, state, w, bias, "silu")
+        want, want_state = O.causal_conv1d_update(x, want_state, w, bias, "silu")
+        close(out, want, 1e-5, 1e-5, f"out step {step}")
+        close(state, want_state, 0, 0, f"state step {step}")
