@@ -15,6 +15,7 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate);
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
 hipError_t scan_bwd_summary_launch(const ScanParams& p, int dtype, hipStream_t stream);
+hipError_t scan_bwd_finish_launch(const ScanParams& p, int dtype, hipStream_t stream);
 int scan_complex_waves();
 hipError_t scan_cfwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_cbwd_launch(const ScanParams& p, int dtype, hipStream_t stream);
@@ -25,6 +26,28 @@ hipError_t scan_reduce_launch(const float* dB_part, float* dB, const float* dC_p
                               int64_t batch, hipStream_t stream);
 
 namespace {
+
+// State slices: above kSliceAbove states (what one lane group of the kernels
+// holds in registers) the states are cut into slices that the grid scans side
+// by side: 64 states per forward slice (four per lane), 16 per backward slice
+// (the backward's fastest form). Up to kMaxSlicedDstate states.
+constexpr int64_t kSliceAbove = 64;
+constexpr int64_t kFwdSlice = 64;
+constexpr int64_t kBwdSlice = 16;
+constexpr int64_t kMaxSlicedDstate = 4096;
+
+int64_t slices_of(int64_t dstate, int64_t slice) {
+  return dstate > kSliceAbove ? (dstate + slice - 1) / slice : 1;
+}
+
+// Cuts p (made for all states) into slices of `slice` states when sliced.
+void slice_params(ScanParams& p, int64_t slice) {
+  const int64_t ns = slices_of(p.ntotal, slice);
+  if (ns > 1) {
+    p.dstate = slice;
+    p.nslices = ns;
+  }
+}
 
 // An output's strides as given, or contiguous (batch, dim, seqlen) when all zero.
 void out_strides(const int64_t (&given)[3], int64_t dim, int64_t seqlen, int64_t (&s)[3]) {
@@ -46,7 +69,7 @@ int check_scan(const mcpu_scan_args* a) {
   if (a->ngroups < 1 || (a->dim > 0 && a->dim % a->ngroups != 0))
     return fail(MCPU_ERR_INVALID, "selective_scan: dim (%lld) must be divisible by ngroups (%lld)",
                 (long long)a->dim, (long long)a->ngroups);
-  const int64_t max_dstate = a->complex_a ? 32 : 64;
+  const int64_t max_dstate = a->complex_a ? 32 : kMaxSlicedDstate;
   if (a->dstate < 1 || a->dstate > max_dstate)
     return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, %lld]%s, got %lld",
                 (long long)max_dstate, a->complex_a ? " with complex A" : "", (long long)a->dstate);
@@ -56,7 +79,7 @@ int check_scan(const mcpu_scan_args* a) {
     return fail(MCPU_ERR_INVALID, "selective_scan: bwd_waves must be 0, or 4, 8 or 12 with real A "
                 "and dstate <= 16, got %d", a->bwd_waves);
   const int64_t dpg = a->dim / a->ngroups;
-  const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16);
+  const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16) * slices_of(a->dstate, kBwdSlice);
   if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
   for (int i = 0; i < 3; ++i)
     if (a->u_stride[i] < 0 || a->delta_stride[i] < 0 || a->z_stride[i] < 0 || a->dout_stride[i] < 0 ||
@@ -133,28 +156,49 @@ ScanParams make_params(const mcpu_scan_args* a, int waves) {
   p.softplus = a->delta_softplus != 0;
   p.nchunk = 1;
   p.chunk_blocks = p.nblk > 0 ? p.nblk : 1;
+  p.nslices = 1;
+  p.nstride = p.ntotal = a->dstate;
   return p;
 }
 
-// Workspace of a chunked forward: chunk-end states and chunk sums of dt.
+// Forward parameters: sliced when dstate needs it, chunked by the shape.
+ScanParams fwd_params(const mcpu_scan_args* a) {
+  ScanParams p = make_params(a, scan_fwd_waves());
+  slice_params(p, kFwdSlice);
+  scan_fwd_chunks(p);
+  return p;
+}
+
+// Workspace of a forward: chunk-end states and chunk sums of dt when
+// chunked; each slice's share of y when sliced and writing outputs.
 struct FwdLayout {
-  size_t sum_h = 0, sum_dt = 0, total = 0;
+  size_t sum_h = 0, sum_dt = 0, ypart = 0, total = 0;
 };
 
-FwdLayout fwd_layout(const ScanParams& p) {
+FwdLayout fwd_layout(const ScanParams& p, bool write_out) {
   FwdLayout w;
-  if (p.nchunk <= 1) return w;
-  w.sum_h = 0;
-  w.sum_dt = align_up(sizeof(float) * p.batch * p.dim * p.nchunk * p.dstate);
-  w.total = w.sum_dt + align_up(sizeof(float) * p.batch * p.dim * p.nchunk);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  if (p.nchunk > 1) {
+    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nchunk * p.ntotal);
+    w.sum_dt = take(sizeof(float) * p.batch * p.dim * p.nchunk);
+  }
+  if (p.nslices > 1 && write_out) w.ypart = take(sizeof(float) * p.nslices * p.batch * p.dim * p.seqlen);
+  w.total = off;
   return w;
 }
 
 // The backward's workgroup width: pinned by the caller (bwd_waves, checked by
-// check_scan) or chosen from the shape.
+// check_scan) or chosen from the shape (a sliced backward's slices count as
+// more batch rows of kBwdSlice states).
 int bwd_waves(const mcpu_scan_args* a) {
   if (a->bwd_waves != 0) return a->bwd_waves;
-  return scan_bwd_waves(a->batch, a->ngroups, a->dim / a->ngroups, a->dstate);
+  const int64_t ns = slices_of(a->dstate, kBwdSlice);
+  return scan_bwd_waves(a->batch * ns, a->ngroups, a->dim / a->ngroups, ns > 1 ? kBwdSlice : a->dstate);
 }
 
 // Time chunks of a backward with these parameters: when the rows give fewer
@@ -168,7 +212,7 @@ int bwd_waves(const mcpu_scan_args* a) {
 // p.chunk_blocks.
 void bwd_chunks(ScanParams& p, int waves) {
   int64_t n = 1;
-  const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves;
+  const int64_t wv = p.batch * p.ngroups * p.nblk_c * waves * p.nslices;
   if (wv > 0 && wv < 2048 && p.nblk >= 8) {
     n = 4096 / wv;  // about four waves per SIMD, the register limit of the kernel
     if (n < p.nblk / 64) n = p.nblk / 64;  // chunks of at most 64 blocks
@@ -195,14 +239,20 @@ void bwd_chunks(ScanParams& p, int waves) {
   }
 }
 
+// A sliced backward also needs: each slice's <ga, A> and <g, B> shares
+// (rpart), y before the gate when z is given and the caller saved none
+// (ysave, the input dtype), and for the forward that makes it (or the
+// checkpoints), that forward's own workspace (fwd).
 struct BwdLayout {
-  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, sum_h = 0, sum_dt = 0, total = 0;
-  bool own_ckpt = false, part_bc = false, part_dA = false;
+  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, sum_h = 0, sum_dt = 0;
+  size_t rpart = 0, ysave = 0, fwd = 0, fwd_bytes = 0, total = 0;
+  bool own_ckpt = false, part_bc = false, part_dA = false, own_ysave = false, sliced = false;
   int64_t nchunk = 1, chunk_blocks = 1, nsum = 1, sum_blocks = 1, sum_per_chunk = 1;
 };
 
 BwdLayout bwd_layout(const mcpu_scan_args* a) {
   ScanParams p = make_params(a, bwd_waves(a));
+  slice_params(p, kBwdSlice);
   bwd_chunks(p, bwd_waves(a));
   BwdLayout w;
   w.nchunk = p.nchunk;
@@ -217,22 +267,33 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
     return at;
   };
   w.own_ckpt = a->ckpt == nullptr;
-  if (w.own_ckpt) w.ckpt = take(sizeof(float) * p.batch * p.dim * p.nblk * p.dstate);
+  if (w.own_ckpt) w.ckpt = take(sizeof(float) * p.batch * p.dim * p.nblk * p.ntotal);
   w.part_bc = p.nblk_c > 1;
   if (w.part_bc) {
-    const size_t bc = sizeof(float) * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.dstate;
+    const size_t bc = sizeof(float) * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.ntotal;
     w.dB = take(bc);
     w.dC = take(bc);
   }
   // dA, dD and ddelta_bias partials per (chunk, batch).
   const int64_t parts = p.batch * p.nchunk;
   w.part_dA = parts > 1;
-  if (w.part_dA) w.dA = take(sizeof(float) * parts * p.dim * p.dstate);
+  if (w.part_dA) w.dA = take(sizeof(float) * parts * p.dim * p.ntotal);
   w.dD = take(sizeof(float) * parts * p.dim);
   w.dbias = take(sizeof(float) * parts * p.dim);
   if (p.nchunk > 1) {
-    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nsum * p.dstate);
+    w.sum_h = take(sizeof(float) * p.batch * p.dim * p.nsum * p.ntotal);
     w.sum_dt = take(sizeof(float) * p.batch * p.dim * p.nsum);
+  }
+  w.sliced = p.nslices > 1;
+  if (w.sliced) {
+    const int64_t n = p.batch * p.dim * p.seqlen;
+    w.rpart = take(sizeof(float) * 2 * p.nslices * n);
+    w.own_ysave = a->z != nullptr && (a->ckpt == nullptr || a->ysave == nullptr);
+    if (w.own_ysave) w.ysave = take(dtype_size(a->dtype) * n);
+    if (w.own_ckpt || w.own_ysave) {
+      w.fwd_bytes = fwd_layout(fwd_params(a), w.own_ysave).total;
+      w.fwd = take(w.fwd_bytes);
+    }
   }
   w.total = off;
   return w;
@@ -337,9 +398,7 @@ extern "C" size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a
     return 0;
   }
   if (a->complex_a) return 0;
-  ScanParams p = make_params(a, scan_fwd_waves());
-  scan_fwd_chunks(p);
-  return fwd_layout(p).total;
+  return fwd_layout(fwd_params(a), a->out != nullptr).total;
 }
 
 extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
@@ -354,11 +413,18 @@ extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
                     static_cast<hipStream_t>(stream));
   }
   if (a->complex_a) return complex_fwd(a, static_cast<hipStream_t>(stream));
-  ScanParams p = make_params(a, scan_fwd_waves());
-  scan_fwd_chunks(p);
-  const FwdLayout w = fwd_layout(p);
+  ScanParams p = fwd_params(a);
+  const bool write_out = a->out != nullptr;
+  FwdLayout w = fwd_layout(p, write_out);
+  char* ws = static_cast<char*>(workspace);
+  if (p.nslices > 1 && write_out) {
+    // A sliced forward cannot do without the slices' shares of y.
+    if (workspace == nullptr || workspace_bytes < w.total)
+      return fail(MCPU_ERR_INVALID, "selective_scan_fwd: dstate %lld needs a workspace of %zu bytes, got %zu",
+                  (long long)a->dstate, w.total, workspace_bytes);
+    p.ypart = reinterpret_cast<float*>(ws + w.ypart);
+  }
   if (p.nchunk > 1 && workspace != nullptr && workspace_bytes >= w.total) {
-    char* ws = static_cast<char*>(workspace);
     p.sum_h = reinterpret_cast<float*>(ws + w.sum_h);
     p.sum_dt = reinterpret_cast<float*>(ws + w.sum_dt);
   } else {
@@ -415,9 +481,30 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   char* ws = static_cast<char*>(workspace);
   const int waves = bwd_waves(a);
   ScanParams p = make_params(a, waves);
+  slice_params(p, kBwdSlice);
   p.ckpt = w.own_ckpt ? reinterpret_cast<float*>(ws + w.ckpt) : a->ckpt;
   p.ysave = (a->z != nullptr && a->ckpt != nullptr) ? a->ysave : nullptr;
-  if (w.own_ckpt) {
+  if (w.sliced) {
+    if (a->z != nullptr && w.own_ysave) p.ysave = ws + w.ysave;
+    p.rpart = reinterpret_cast<float*>(ws + w.rpart);
+    if (w.own_ckpt || w.own_ysave) {
+      // The sliced forward for the checkpoints and/or y before the gate.
+      ScanParams pf = fwd_params(a);
+      const FwdLayout fw = fwd_layout(pf, w.own_ysave);
+      char* fws = ws + w.fwd;
+      if (pf.nchunk > 1) {
+        pf.sum_h = reinterpret_cast<float*>(fws + fw.sum_h);
+        pf.sum_dt = reinterpret_cast<float*>(fws + fw.sum_dt);
+      }
+      if (w.own_ysave) {
+        pf.ypart = reinterpret_cast<float*>(fws + fw.ypart);
+        pf.ysave = p.ysave;
+      }
+      pf.ckpt = w.own_ckpt ? p.ckpt : nullptr;
+      if (int rc = hip_status(scan_fwd_launch(pf, a->dtype, w.own_ysave, st), "selective_scan_bwd fwd launch"))
+        return rc;
+    }
+  } else if (w.own_ckpt) {
     ScanParams pf = make_params(a, scan_fwd_waves());  // states-only forward: block checkpoints
     pf.ckpt = p.ckpt;
     if (int rc = hip_status(scan_fwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
@@ -451,12 +538,31 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
   }
   if (int rc = hip_status(scan_bwd_launch(p, a->dtype, waves, st), "selective_scan_bwd launch"))
     return rc;
+  if (w.sliced) {
+    // du, ddelta, dz and the dD / ddelta_bias batch partials from the slices'
+    // shares; then dB/dC over channel blocks, dA over (chunk, batch) and
+    // dD / ddelta_bias over the batch.
+    if (int rc = hip_status(scan_bwd_finish_launch(p, a->dtype, st), "selective_scan_bwd finish launch"))
+      return rc;
+    if (int rc = hip_status(
+            scan_reduce_launch(w.part_bc ? p.dB_part : nullptr, a->dB, w.part_bc ? p.dC_part : nullptr, a->dC,
+                               p.batch * p.ngroups, p.nblk_c, p.seqlen * p.ntotal,
+                               w.part_dA ? p.dA_part : nullptr, a->dA, p.dim * p.ntotal, nullptr, nullptr,
+                               nullptr, nullptr, p.dim, p.batch * p.nchunk, st),
+            "selective_scan_bwd reduce"))
+      return rc;
+    return hip_status(scan_reduce_launch(nullptr, nullptr, nullptr, nullptr, 0, 1, 0, nullptr, nullptr, 0,
+                                         a->dD ? p.dD_part : nullptr, a->dD,
+                                         a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim,
+                                         p.batch, st),
+                      "selective_scan_bwd reduce");
+  }
   // One launch sums every partial: dB/dC over channel blocks (when there is
   // more than one), dA/dD/ddelta_bias over the batch.
   return hip_status(
       scan_reduce_launch(w.part_bc ? p.dB_part : nullptr, a->dB, w.part_bc ? p.dC_part : nullptr,
-                         a->dC, p.batch * p.ngroups, p.nblk_c, p.seqlen * p.dstate,
-                         w.part_dA ? p.dA_part : nullptr, a->dA, p.dim * p.dstate,
+                         a->dC, p.batch * p.ngroups, p.nblk_c, p.seqlen * p.ntotal,
+                         w.part_dA ? p.dA_part : nullptr, a->dA, p.dim * p.ntotal,
                          a->dD ? p.dD_part : nullptr, a->dD,
                          a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim,
                          p.batch * p.nchunk, st),

@@ -25,7 +25,9 @@
 
 namespace mcpu {
 
-template <typename Tx, int W, int SPL, bool HAS_Z, bool HAS_Y>
+// SLICED: one state slice of a sliced backward, which writes its <ga, A> and
+// <g, B> shares (rpart) in place of du, ddelta, dz, dD and ddelta_bias.
+template <typename Tx, int W, int SPL, bool HAS_Z, bool HAS_Y, bool SLICED>
 __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
@@ -45,9 +47,12 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
   // Time chunk of this workgroup: blocks [kb0, kb1), walked from kb1 - 1 down.
-  const int64_t chunk = blockIdx.x % p.nchunk;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
-  const int64_t N = p.dstate, L = p.seqlen;
+  const SliceCtx sc = scan_slice(p);
+  const int64_t chunk = sc.bx % p.nchunk;
+  const RowCtx rc = scan_row_ctx<W>(p, sc.bx / p.nchunk, wave, r);
+  // This slice's states, n0 .. n0 + N - 1 of the NS per row of A, dlast_state,
+  // the checkpoints, the chunk summaries and the dA/dB/dC layouts.
+  const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
   const int64_t kb0 = chunk * p.chunk_blocks;
   const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
@@ -60,9 +65,9 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
 #pragma unroll
   for (int s = 0; s < SPL; ++s) {
     const int n = j + 16 * s;
-    Av[s] = n < N ? p.A[rc.d * N + n] : 0.f;
+    Av[s] = n < N ? p.A[rc.d * NS + n0 + n] : 0.f;
     A2[s] = Av[s] * kLog2e;
-    gh[s] = (n < N && p.dlast_state != nullptr) ? p.dlast_state[row * N + n] : 0.f;
+    gh[s] = (n < N && p.dlast_state != nullptr) ? p.dlast_state[row * NS + n0 + n] : 0.f;
     dA_acc[s] = 0.f;
   }
   if (chunk < p.nchunk - 1) {
@@ -70,8 +75,8 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     // through unit u it maps gh to exp(A * sum_dt[u]) * gh + sum_h[u]
     // (sum_h[u] = the adjoint at u's start from a zero adjoint at its end).
     const int64_t last_unit = (chunk + 1) * p.sum_per_chunk;
-    fold_summaries<SPL>(gh, A2, p.sum_h + row * p.nsum * N, p.sum_dt + row * p.nsum, p.nsum - 1,
-                        p.nsum - last_unit, -1, j, N);
+    fold_summaries<SPL>(gh, A2, p.sum_h + row * p.nsum * NS + n0, p.sum_dt + row * p.nsum, p.nsum - 1,
+                        p.nsum - last_unit, -1, j, N, NS);
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
@@ -89,16 +94,16 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   const int64_t sy[3] = {p.dim * L, L, 1};
   if (HAS_Y) xy.template init<Tx>(tid, p.ysave, sy, p, rc, t_last);
   BC tb, tc;
-  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, t_last);
-  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, t_last);
+  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1] + n0 * p.sB[3], p.sB, N, t_last);
+  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1] + n0 * p.sC[3], p.sC, N, t_last);
 
   // Rows of the workgroup: uniform first row + per-lane offsets (rows past the
   // slice end use the last channel for loads and store nothing).
   const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
   const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);  // this lane's row within the workgroup
   // Checkpointed state lane j of the current block.
-  const char* ck_base = reinterpret_cast<const char*>(p.ckpt + (row0 * p.nblk + kl) * N);
-  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
+  const char* ck_base = reinterpret_cast<const char*>(p.ckpt + (row0 * p.nblk + kl) * NS + n0);
+  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * NS + j));
   // Per-lane outputs at step t0 + j of the current block, each with its own
   // strides: a uniform base (the workgroup's first channel at t0, moved one
   // block back per block) plus a fixed per-lane offset.
@@ -128,8 +133,8 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     o_t[q] = tt;
     o_red[q] = (arr * W * T + tt) * NW + n;  // index of (arr, wave 0, tt, n) in s_red[buf]
     o_ok[q] = e < 2 * T * NW && n < N;
-    o_part[q] = reinterpret_cast<char*>((arr == 0 ? p.dB_part : p.dC_part) + part_row * N);
-    o_poff[q] = static_cast<uint32_t>(sizeof(float) * (tt * N + n));
+    o_part[q] = reinterpret_cast<char*>((arr == 0 ? p.dB_part : p.dC_part) + part_row * NS + n0);
+    o_poff[q] = static_cast<uint32_t>(sizeof(float) * (tt * NS + n));
   }
 
   uint32_t nu = 0u, nd = 0u, no = 0u, nz = 0u, ny = 0u;  // raw bits, widened at the park
@@ -175,7 +180,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     if (HAS_Y) xy.advance_unless(-1, stay);
     tb.advance_unless(-1, stay);
     tc.advance_unless(-1, stay);
-    ck_base -= stay ? 0 : sizeof(float) * N;
+    ck_base -= stay ? 0 : sizeof(float) * NS;
   };
   auto park = [&](int buf) {
     (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
@@ -357,9 +362,17 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     }
     // Stores after the park, so waiting for the prefetch never waits for them.
     if (tv && rc.active) {
-      buf_st<Tx>(wave_rsrc(o_du), off_du, duv);
-      buf_st<Tx>(wave_rsrc(o_dd), off_dd, ddt);
-      if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), off_dz, dzv);
+      if constexpr (SLICED) {
+        // A state slice: its <ga, A> and <g, B> shares, from which
+        // scan_bwd_finish_kernel forms du, ddelta, dz, dD and ddelta_bias.
+        const int64_t at = ((sc.sl * p.batch + rc.b) * p.dim + rc.d) * L + t0 + j;
+        p.rpart[at] = R1;
+        p.rpart[p.nslices * p.batch * p.dim * L + at] = R2;
+      } else {
+        buf_st<Tx>(wave_rsrc(o_du), off_du, duv);
+        buf_st<Tx>(wave_rsrc(o_dd), off_dd, ddt);
+        if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), off_dz, dzv);
+      }
     }
     o_du -= T * esz * p.sdu[2];
     o_dd -= T * esz * p.sdd[2];
@@ -376,7 +389,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
         for (int w = 0; w < W; ++w) acc += src[w * T * NW];
         buf_st<float>(wave_rsrc(o_part[q]), o_poff[q], acc);
       }
-      o_part[q] -= sizeof(float) * T * N;
+      o_part[q] -= sizeof(float) * T * NS;
     }
   };
 
@@ -390,14 +403,92 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   if (rc.active) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) p.dA_part[prow * N + j + 16 * s] = dA_acc[s];
+      if (j + 16 * s < N) p.dA_part[prow * NS + n0 + j + 16 * s] = dA_acc[s];
   }
   dD_acc = row_allreduce16(dD_acc);
   dbias_acc = row_allreduce16(dbias_acc);
-  if (rc.active && j == 0) {
+  if (rc.active && j == 0 && !SLICED) {  // a sliced backward forms them in its finish kernel
     p.dD_part[prow] = dD_acc;
     p.dbias_part[prow] = dbias_acc;
   }
+}
+
+// A sliced backward's per-step gradients, one wave per (batch, channel) row,
+// its lanes walking the steps: R1 = the slices' <ga, A> shares summed, R2 =
+// their <g, B_t>; with dt, dy and dz from the row's inputs as the unsliced
+// kernel forms them,
+//   ddelta = (R1 + u R2) softplus'(pre), du = dy D + dt R2,
+//   dz = dout y s(z) (1 + z (1 - s(z))),
+// and the row's sums dD = sum dy u and ddelta_bias = sum ddelta into the
+// per-(batch, channel) partials.
+template <typename Tx, bool HAS_Z>
+__global__ void __launch_bounds__(256) scan_bwd_finish_kernel(const ScanParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x * 4ll + (threadIdx.x >> 6);
+  if (row >= p.batch * p.dim) return;  // the whole wave
+  const int64_t d = row % p.dim, b = row / p.dim, L = p.seqlen, n = p.batch * p.dim * L;
+  const float Dd = p.D ? p.D[d] : 0.f;
+  const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+  float dD = 0.f, dbias = 0.f;
+  for (int64_t t = lane; t < L; t += 64) {
+    const int64_t i = row * L + t;
+    float R1 = 0.f, R2 = 0.f;
+    for (int64_t s = 0; s < p.nslices; ++s) {
+      R1 += p.rpart[s * n + i];
+      R2 += p.rpart[(p.nslices + s) * n + i];
+    }
+    const float uu = ld<Tx>(p.u, b * p.su[0] + d * p.su[1] + t * p.su[2]);
+    const float dl = ld<Tx>(p.delta, b * p.sdl[0] + d * p.sdl[1] + t * p.sdl[2]);
+    const float go = p.dout ? ld<Tx>(p.dout, b * p.sdo[0] + d * p.sdo[1] + t * p.sdo[2]) : 0.f;
+    const float pre = dl + bias;
+    float dt = pre, sg_pre = 1.f;
+    if (p.softplus) dt = softplus_sigmoid(pre, sg_pre);
+    float dy = go;
+    if (HAS_Z) {
+      const float zz = ld<Tx>(p.z, b * p.sz[0] + d * p.sz[1] + t * p.sz[2]);
+      const float y = ld<Tx>(p.ysave, i);
+      const float sg = sigmoid(zz);
+      st<Tx>(p.dz, b * p.sdz[0] + d * p.sdz[1] + t * p.sdz[2], go * y * sg * (1.f + zz * (1.f - sg)));
+      dy = go * zz * sg;
+    }
+    float ddt = fmaf(uu, R2, R1);
+    const float duv = fmaf(dy, Dd, dt * R2);
+    if (p.softplus) ddt *= sg_pre;
+    dD = fmaf(dy, uu, dD);
+    dbias += ddt;
+    st<Tx>(p.du, b * p.sdu[0] + d * p.sdu[1] + t * p.sdu[2], duv);
+    st<Tx>(p.ddelta, b * p.sdd[0] + d * p.sdd[1] + t * p.sdd[2], ddt);
+  }
+  dD = row_allreduce16(dD);
+  dD = swap_sum<16>(dD, dD);
+  dD = swap_sum<32>(dD, dD);
+  dbias = row_allreduce16(dbias);
+  dbias = swap_sum<16>(dbias, dbias);
+  dbias = swap_sum<32>(dbias, dbias);
+  if (lane == 0) {
+    p.dD_part[row] = dD;
+    p.dbias_part[row] = dbias;
+  }
+}
+
+hipError_t scan_bwd_finish_launch(const ScanParams& p, int dtype, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((p.batch * p.dim + 3) / 4));
+  const bool z = p.z != nullptr;
+  switch (dtype) {
+    case MCPU_F32:
+      if (z) hipLaunchKernelGGL((scan_bwd_finish_kernel<float, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_bwd_finish_kernel<float, false>), grid, dim3(256), 0, stream, p);
+      break;
+    case MCPU_BF16:
+      if (z) hipLaunchKernelGGL((scan_bwd_finish_kernel<bf16, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_bwd_finish_kernel<bf16, false>), grid, dim3(256), 0, stream, p);
+      break;
+    default:
+      if (z) hipLaunchKernelGGL((scan_bwd_finish_kernel<f16, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_bwd_finish_kernel<f16, false>), grid, dim3(256), 0, stream, p);
+      break;
+  }
+  return hipGetLastError();
 }
 
 // Adjoint summaries of a time-chunked backward. For every summary unit u
@@ -418,15 +509,16 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   __shared__ __align__(16) float s_x[2][3][CH][T];  // delta, dout, z
   __shared__ __align__(16) float s_C[2][NW][kBCPad];
 
-  const int64_t unit = blockIdx.x % p.nsum;
+  const SliceCtx sc = scan_slice(p);
+  const int64_t unit = sc.bx % p.nsum;
   if (unit < p.sum_per_chunk) return;  // the first chunk's units feed no carry
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nsum, wave, r);
-  const int64_t N = p.dstate, L = p.seqlen;
+  const RowCtx rc = scan_row_ctx<W>(p, sc.bx / p.nsum, wave, r);
+  const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
   const int64_t kb0 = unit * p.sum_blocks;
   const int64_t kb1 = kb0 + p.sum_blocks < p.nblk ? kb0 + p.sum_blocks : p.nblk;
@@ -437,7 +529,7 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
 #pragma unroll
   for (int s = 0; s < SPL; ++s) {
     const int n = j + 16 * s;
-    A2[s] = n < N ? p.A[rc.d * N + n] * kLog2e : 0.f;
+    A2[s] = n < N ? p.A[rc.d * NS + n0 + n] * kLog2e : 0.f;
     gh[s] = 0.f;
   }
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
@@ -450,7 +542,7 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   xo.template init<Tx>(tid, has_dout ? p.dout : p.delta, p.sdo, p, rc, t_last);
   if (HAS_Z) xz.template init<Tx>(tid, p.z, p.sz, p, rc, t_last);
   BC tc;
-  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, t_last);
+  tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1] + n0 * p.sC[3], p.sC, N, t_last);
 
   uint32_t nd = 0u, no = 0u, nz = 0u;  // raw bits, widened at the park
   float nC[BC::PER_THREAD];
@@ -532,7 +624,7 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   if (rc.active) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) p.sum_h[(row * p.nsum + unit) * N + j + 16 * s] = gh[s];
+      if (j + 16 * s < N) p.sum_h[(row * p.nsum + unit) * NS + n0 + j + 16 * s] = gh[s];
     if (j == 0) p.sum_dt[row * p.nsum + unit] = dts;
   }
 }
@@ -617,17 +709,26 @@ __global__ void __launch_bounds__(256) reduce_jobs_kernel(const ReduceJobs jobs,
   }
 }
 
-template <typename Tx, int W, int SPL>
-static hipError_t launch_bwd_zy(const ScanParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nchunk));
+template <typename Tx, int W, int SPL, bool SLICED>
+static hipError_t launch_bwd_zys(const ScanParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nchunk * p.nslices));
   const dim3 block(64 * W);
   if (p.z != nullptr && p.ysave != nullptr)
-    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, true, SLICED>), grid, block, 0, stream, p);
   else if (p.z != nullptr)
-    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, true, false, SLICED>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, false, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_bwd_kernel<Tx, W, SPL, false, false, SLICED>), grid, block, 0, stream, p);
   return hipGetLastError();
+}
+
+// Sliced backwards (p.rpart set) run 16-state slices, so only SPL 1 has a
+// sliced form.
+template <typename Tx, int W, int SPL>
+static hipError_t launch_bwd_zy(const ScanParams& p, hipStream_t stream) {
+  if constexpr (SPL == 1)
+    if (p.rpart != nullptr) return launch_bwd_zys<Tx, W, SPL, true>(p, stream);
+  return launch_bwd_zys<Tx, W, SPL, false>(p, stream);
 }
 
 // Wider workgroups (8 or 12 waves) only for dstate <= 16, where their LDS fits.
@@ -663,7 +764,7 @@ int scan_bwd_waves(int64_t batch, int64_t ngroups, int64_t dpg, int64_t dstate) 
 
 template <typename Tx, int SPL>
 static hipError_t launch_bwd_summary(const ScanParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nsum));
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nsum * p.nslices));
   const dim3 block(64 * kScanSumWaves);
   if (p.z != nullptr)
     hipLaunchKernelGGL((scan_bwd_summary_kernel<Tx, SPL, true>), grid, block, 0, stream, p);

@@ -73,7 +73,31 @@ struct ScanParams {
   int64_t nsum;
   int64_t sum_blocks;
   int64_t sum_per_chunk;
+  // State slices (dstate above what one lane group holds): the grid holds
+  // nslices copies of the launch, copy s scanning states [s * dstate,
+  // s * dstate + dstate) of the ntotal states (the last slice may be short).
+  // A, ckpt, last_state, dlast_state, sum_h and the dA/dB/dC layouts keep all
+  // ntotal states (nstride per row). Unsliced: nslices 1, nstride = ntotal =
+  // dstate.
+  int64_t nslices, nstride, ntotal;
+  float* ypart;   // sliced forward: (nslices, batch, dim, seqlen) y of each slice's states
+  float* rpart;   // sliced backward: (2, nslices, batch, dim, seqlen) <ga, A> and <g, B> per slice
 };
+
+// This workgroup's state slice: its index, first state and state count.
+struct SliceCtx {
+  int64_t sl, n0, N;
+  int64_t bx;  // the workgroup's index within its slice's copy of the grid
+};
+__device__ __forceinline__ SliceCtx scan_slice(const ScanParams& p) {
+  SliceCtx s;
+  const int64_t per = gridDim.x / p.nslices;
+  s.sl = blockIdx.x / per;
+  s.bx = blockIdx.x % per;
+  s.n0 = s.sl * p.dstate;
+  s.N = p.ntotal - s.n0 < p.dstate ? p.ntotal - s.n0 : p.dstate;
+  return s;
+}
 
 struct RowCtx {
   int64_t b, g, d;     // batch, group, channel (clamped into range)
@@ -229,14 +253,14 @@ struct PartialSum {
 hipError_t partial_sums_launch(const PartialSum* sums, int n, hipStream_t stream);
 
 // Folds chunk summaries into a state, in order: for k = 0 .. count-1 and
-// c = first + dir * k, h <- exp2(A2 * sd[c]) h + sh[c * N + n] for each of
+// c = first + dir * k, h <- exp2(A2 * sd[c]) h + sh[c * NS + n] for each of
 // this lane's states n = j + 16 s < N. The summaries of a few chunks load
 // together and then fold in the same order (the same arithmetic as one chunk
 // at a time, without a memory round trip per chunk).
 template <int SPL>
 __device__ __forceinline__ void fold_summaries(float (&h)[SPL], const float (&A2)[SPL], const float* sh,
                                                const float* sd, int64_t first, int64_t count, int dir, int j,
-                                               int64_t N) {
+                                               int64_t N, int64_t NS) {
   constexpr int U = SPL == 1 ? 8 : (SPL == 2 ? 4 : 2);
   for (int64_t k0 = 0; k0 < count; k0 += U) {
     float ds[U], hv[U][SPL];
@@ -247,7 +271,7 @@ __device__ __forceinline__ void fold_summaries(float (&h)[SPL], const float (&A2
 #pragma unroll
       for (int s = 0; s < SPL; ++s) {
         const int n = j + 16 * s;
-        hv[u][s] = sh[c * N + (n < N ? n : 0)];
+        hv[u][s] = sh[c * NS + (n < N ? n : 0)];
       }
     }
 #pragma unroll

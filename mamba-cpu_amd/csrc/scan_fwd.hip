@@ -39,12 +39,13 @@ namespace mcpu {
 constexpr int kFwdWaves = 4;
 
 // MODE: outputs (out, optional ysave / ckpt / last_state), states only
-// (ckpt / last_state), or the chunk summaries of the chunked scan.
-enum FwdMode { kFwdOut = 0, kFwdStates = 1, kFwdSummary = 2 };
+// (ckpt / last_state), the chunk summaries of the chunked scan, or a state
+// slice's share of y (ypart; optional ckpt / last_state).
+enum FwdMode { kFwdOut = 0, kFwdStates = 1, kFwdSummary = 2, kFwdPart = 3 };
 
 template <typename Tx, int SPL, bool HAS_Z, int MODE, bool CORR>
 __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanParams p) {
-  constexpr bool WRITE_OUT = MODE == kFwdOut;
+  constexpr bool WRITE_OUT = MODE == kFwdOut || MODE == kFwdPart;
   constexpr int W = kFwdWaves;
   constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
@@ -59,11 +60,14 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const int64_t chunk = blockIdx.x % p.nchunk;
+  const SliceCtx sc = scan_slice(p);
+  const int64_t chunk = sc.bx % p.nchunk;
   // The summary pass has nothing to record for the last chunk.
   if (MODE == kFwdSummary && chunk == p.nchunk - 1) return;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x / p.nchunk, wave, r);
-  const int64_t N = p.dstate, L = p.seqlen;
+  const RowCtx rc = scan_row_ctx<W>(p, sc.bx / p.nchunk, wave, r);
+  // This slice's states, n0 .. n0 + N - 1 of the NS per row of A, the
+  // checkpoints, the last state and the chunk summaries.
+  const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
   const int64_t kb0 = chunk * p.chunk_blocks;  // this chunk's blocks: [kb0, kb1)
   const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
@@ -72,16 +76,17 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
 #pragma unroll
   for (int s = 0; s < SPL; ++s) {
     const int n = j + 16 * s;
-    A2[s] = n < N ? p.A[rc.d * N + n] * kLog2e : 0.f;
+    A2[s] = n < N ? p.A[rc.d * NS + n0 + n] * kLog2e : 0.f;
     h[s] = 0.f;
   }
   if (MODE != kFwdSummary && chunk > 0) {
     // Carry the state over the chunks before this one.
-    fold_summaries<SPL>(h, A2, p.sum_h + row * p.nchunk * N, p.sum_dt + row * p.nchunk, 0, chunk, 1, j, N);
+    fold_summaries<SPL>(h, A2, p.sum_h + row * p.nchunk * NS + n0, p.sum_dt + row * p.nchunk, 0, chunk, 1, j,
+                        N, NS);
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
-  float* ck = (MODE != kFwdSummary && p.ckpt) ? p.ckpt + row * p.nblk * N : nullptr;
+  float* ck = (MODE != kFwdSummary && p.ckpt) ? p.ckpt + row * p.nblk * NS + n0 : nullptr;
   // Per-step outputs and checkpoints as a uniform base (the workgroup's first
   // row, moved one block at a time) plus a fixed 32-bit per-lane offset.
   const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
@@ -92,7 +97,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       static_cast<int64_t>(sizeof(Tx)) * (rc.b * p.sout[0] + (rc.g * p.dpg + rc.cl0) * p.sout[1]);
   const int64_t out_ts = static_cast<int64_t>(sizeof(Tx)) * p.sout[2];
   const uint32_t out_off = static_cast<uint32_t>(sizeof(Tx) * (crow * p.sout[1] + j * p.sout[2]));
-  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * N + j));
+  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * NS + j));
   float dts = 0.f;  // sum of dt over this lane's steps (summary pass)
 
   const int64_t tb0 = kb0 * kScanBlockT;
@@ -101,8 +106,8 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, tb0);
   if (HAS_Z && WRITE_OUT) xz.template init<Tx>(tid, p.z, p.sz, p, rc, tb0);
   BC tb, tc;
-  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1], p.sB, N, tb0);
-  if (WRITE_OUT) tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1], p.sC, N, tb0);
+  tb.init(tid, p.B + rc.b * p.sB[0] + rc.g * p.sB[1] + n0 * p.sB[3], p.sB, N, tb0);
+  if (WRITE_OUT) tc.init(tid, p.C + rc.b * p.sC[0] + rc.g * p.sC[1] + n0 * p.sC[3], p.sC, N, tb0);
   // Only the last block can extend past the sequence end.
   const int64_t t_full = L - L % kScanBlockT;
 
@@ -154,7 +159,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   if (ck != nullptr && rc.active && kb0 < kb1) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) ck[kb0 * N + j + 16 * s] = h[s];
+      if (j + 16 * s < N) ck[kb0 * NS + j + 16 * s] = h[s];
   }
 
   // Per block: prefetch the next block, compute this one, park the prefetch,
@@ -235,15 +240,21 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     park(buf ^ 1);  // in the last iteration a harmless copy into the idle buffer
 
     if (WRITE_OUT && tv && rc.active) {
-      const int64_t o_pos = (row0 * L + t0) * static_cast<int64_t>(sizeof(Tx));
-      if (p.ysave != nullptr) buf_st<Tx>(wave_rsrc(static_cast<char*>(p.ysave) + o_pos), o_off, y);
-      buf_st<Tx>(wave_rsrc(out0 + t0 * out_ts), out_off, yg);
+      if constexpr (MODE == kFwdPart) {
+        // A state slice: its share of y, summed with the others (and D u
+        // added, the gate applied) by scan_fwd_finish_kernel.
+        p.ypart[((sc.sl * p.batch + rc.b) * p.dim + rc.d) * L + t] = y;
+      } else {
+        const int64_t o_pos = (row0 * L + t0) * static_cast<int64_t>(sizeof(Tx));
+        if (p.ysave != nullptr) buf_st<Tx>(wave_rsrc(static_cast<char*>(p.ysave) + o_pos), o_off, y);
+        buf_st<Tx>(wave_rsrc(out0 + t0 * out_ts), out_off, yg);
+      }
     }
     if (ck != nullptr && rc.active && k + 1 < kb1) {
 #pragma unroll
       for (int s = 0; s < SPL; ++s)
         if (j + 16 * s < N)
-          buf_st<float>(wave_rsrc(p.ckpt + (row0 * p.nblk + k + 1) * N), ck_off + 64 * s, h[s]);
+          buf_st<float>(wave_rsrc(p.ckpt + (row0 * p.nblk + k + 1) * NS + n0), ck_off + 64 * s, h[s]);
     }
     __syncthreads();
   };
@@ -255,19 +266,40 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     if (rc.active) {
 #pragma unroll
       for (int s = 0; s < SPL; ++s)
-        if (j + 16 * s < N) p.sum_h[(row * p.nchunk + chunk) * N + j + 16 * s] = h[s];
+        if (j + 16 * s < N) p.sum_h[(row * p.nchunk + chunk) * NS + n0 + j + 16 * s] = h[s];
       if (j == 0) p.sum_dt[row * p.nchunk + chunk] = dts;
     }
   } else if (p.last_state != nullptr && rc.active && kb1 == p.nblk) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
-      if (j + 16 * s < N) p.last_state[row * N + j + 16 * s] = h[s];
+      if (j + 16 * s < N) p.last_state[row * NS + n0 + j + 16 * s] = h[s];
   }
+}
+
+// A sliced forward's outputs, per (batch, channel, step): y = the slices'
+// shares + D u, ysave = y, out = y silu(z) (or y), with the arithmetic of the
+// unsliced kernel's epilogue.
+template <typename Tx, bool HAS_Z>
+__global__ void __launch_bounds__(256) scan_fwd_finish_kernel(const ScanParams p) {
+  const int64_t L = p.seqlen, n = p.batch * p.dim * L;
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= n) return;
+  const int64_t t = i % L, row = i / L, d = row % p.dim, b = row / p.dim;
+  float y = 0.f;
+  for (int64_t s = 0; s < p.nslices; ++s) y += p.ypart[s * n + i];
+  if (p.D != nullptr) y = fmaf(p.D[d], ld<Tx>(p.u, b * p.su[0] + d * p.su[1] + t * p.su[2]), y);
+  if (p.ysave != nullptr) st<Tx>(p.ysave, i, y);
+  float o = y;
+  if (HAS_Z) {
+    const float zz = ld<Tx>(p.z, b * p.sz[0] + d * p.sz[1] + t * p.sz[2]);
+    o = y * (zz * sigmoid(zz));
+  }
+  if (p.out != nullptr) st<Tx>(p.out, b * p.sout[0] + d * p.sout[1] + t * p.sout[2], o);
 }
 
 template <typename Tx, int SPL, bool HAS_Z, int MODE>
 static hipError_t launch_fwd(const ScanParams& p, hipStream_t stream) {
-  const int64_t blocks = p.batch * p.ngroups * p.nblk_c * p.nchunk;
+  const int64_t blocks = p.batch * p.ngroups * p.nblk_c * p.nchunk * p.nslices;
   if (p.nchunk > 1)
     hipLaunchKernelGGL((scan_fwd_kernel<Tx, SPL, HAS_Z, MODE, true>), dim3(static_cast<unsigned>(blocks)),
                        dim3(64 * kFwdWaves), 0, stream, p);
@@ -283,6 +315,7 @@ static hipError_t dispatch_fwd_flags(const ScanParams& p, bool write_out, hipStr
     if (hipError_t e = launch_fwd<Tx, SPL, false, kFwdSummary>(p, stream)) return e;
   }
   if (!write_out) return launch_fwd<Tx, SPL, false, kFwdStates>(p, stream);
+  if (p.ypart != nullptr) return launch_fwd<Tx, SPL, false, kFwdPart>(p, stream);
   if (p.z != nullptr) return launch_fwd<Tx, SPL, true, kFwdOut>(p, stream);
   return launch_fwd<Tx, SPL, false, kFwdOut>(p, stream);
 }
@@ -292,6 +325,23 @@ static hipError_t dispatch_fwd_spl(const ScanParams& p, bool write_out, hipStrea
   if (p.dstate <= 16) return dispatch_fwd_flags<Tx, 1>(p, write_out, stream);
   if (p.dstate <= 32) return dispatch_fwd_flags<Tx, 2>(p, write_out, stream);
   return dispatch_fwd_flags<Tx, 4>(p, write_out, stream);
+}
+
+// Sliced (p.nslices > 1, p.ypart set when write_out): the slices' kernels
+// without D and the gate, then the outputs from their shares.
+template <typename Tx>
+static hipError_t dispatch_fwd_sliced(const ScanParams& p, bool write_out, hipStream_t stream) {
+  if (!write_out) return dispatch_fwd_spl<Tx>(p, false, stream);
+  ScanParams ps = p;
+  ps.D = nullptr;
+  ps.z = nullptr;
+  ps.ysave = nullptr;
+  if (hipError_t e = dispatch_fwd_spl<Tx>(ps, true, stream)) return e;
+  const int64_t n = p.batch * p.dim * p.seqlen;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  if (p.z != nullptr) hipLaunchKernelGGL((scan_fwd_finish_kernel<Tx, true>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((scan_fwd_finish_kernel<Tx, false>), grid, dim3(256), 0, stream, p);
+  return hipGetLastError();
 }
 
 int scan_fwd_waves() { return kFwdWaves; }
@@ -311,7 +361,7 @@ int scan_fwd_waves() { return kFwdWaves; }
 // 32 blocks). Sets p.nchunk / p.chunk_blocks; nchunk == 1 when the rows alone
 // fill the GPU.
 void scan_fwd_chunks(ScanParams& p) {
-  const int64_t wgs = p.batch * p.ngroups * p.nblk_c;
+  const int64_t wgs = p.batch * p.ngroups * p.nblk_c * p.nslices;
   const bool short_rows = (wgs >= 256 && p.nblk <= 64) || (wgs >= 128 && p.nblk <= 32);
   int64_t n = 1;
   if (wgs > 0 && wgs < 512 && p.nblk >= 4 && !short_rows) {
@@ -327,6 +377,13 @@ void scan_fwd_chunks(ScanParams& p) {
 // write_out = false computes states only (checkpoints and/or last_state),
 // skipping C, z and the outputs.
 hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream) {
+  if (p.nslices > 1) {
+    switch (dtype) {
+      case MCPU_F32: return dispatch_fwd_sliced<float>(p, write_out, stream);
+      case MCPU_BF16: return dispatch_fwd_sliced<bf16>(p, write_out, stream);
+      default: return dispatch_fwd_sliced<f16>(p, write_out, stream);
+    }
+  }
   switch (dtype) {
     case MCPU_F32: return dispatch_fwd_spl<float>(p, write_out, stream);
     case MCPU_BF16: return dispatch_fwd_spl<bf16>(p, write_out, stream);

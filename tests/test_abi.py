@@ -122,7 +122,8 @@ def test_scan_rejects_bad_arguments_before_touching_a_device():
     assert _rc(L.mcpu_selective_scan_fwd, None, None, 0, None)[0] == _C.MCPU_ERR_INVALID
     rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(u=None)), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "required" in msg
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=65)), None, 0, None)
+    # dstate above 64 runs in state slices, up to 4096
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=4097)), None, 0, None)
     assert rc == _C.MCPU_ERR_UNSUPPORTED and "dstate" in msg
     rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(ngroups=3)), None, 0, None)
     assert rc == _C.MCPU_ERR_INVALID and "ngroups" in msg

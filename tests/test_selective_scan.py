@@ -359,6 +359,65 @@ def test_larger_dstate(dstate):
     check_grads(got, oracle_grads(inp, True, W, None))
 
 
+@pytest.mark.parametrize("dstate", [65, 96, 128, 256])
+@pytest.mark.parametrize("ngroups", [None, 2])
+def test_dstate_above_64_matches_oracle(dstate, ngroups):
+    """Above 64 states the scan runs in state slices (64 states per forward
+    slice, 16 per backward slice; mamba_ssm's kernel takes up to 256, the
+    reference's any): outputs, last state and every gradient against the
+    oracle, with D, z, delta_bias, a ragged last slice (65) and groups."""
+    inp = make_inputs(2, 16, 70, dstate, ngroups, True, True, True, torch.float32, requires_grad=True)
+    g = torch.Generator().manual_seed(1)
+    W = torch.randn(2, 16, 70, generator=g).to(DEV)
+    V = torch.randn(2, 16, dstate, generator=g).to(DEV)
+    out, last = selective_scan_fn(**inp, delta_softplus=True, return_last_state=True)
+    out_ref, last_ref = O.selective_scan_fwd(**inp, delta_softplus=True)
+    close(out, out_ref, 1e-4, 1e-5, "out")
+    close(last, last_ref, 1e-4, 1e-5, "last_state")
+    got = grads_of(inp, True, W, V)
+    check_grads(got, oracle_grads(inp, True, W, V))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dstate_128_long_sequence_time_chunks(dtype):
+    """State slices and time chunks together (batch 1, 3000 steps): forward
+    summaries and adjoint summaries per slice, against the oracle."""
+    inp = make_inputs(1, 24, 3000, 128, None, True, True, True, dtype, requires_grad=True)
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(1, 24, 3000, generator=g).to(DEV)
+    V = torch.randn(1, 24, 128, generator=g).to(DEV)
+    out, last = selective_scan_fn(**inp, delta_softplus=True, return_last_state=True)
+    out_ref, last_ref = O.selective_scan_fwd(**inp, delta_softplus=True)
+    tol = (1e-4, 1e-5) if dtype == torch.float32 else (1e-2, 1e-2)
+    close(out, out_ref, *tol, "out")
+    close(last, last_ref, 1e-4 if dtype == torch.float32 else 1e-2, 1e-5, "last_state")
+    got = grads_of(inp, True, W, V)
+    want = oracle_grads(inp, True, W.to(dtype).float(), V)
+    if dtype == torch.float32:
+        check_grads(got, want)
+    else:
+        check_grads(got, want, 2e-2, 2e-2)
+
+
+def test_dstate_256_reference_schema_backward_agrees_with_ckpt_path():
+    """The reference-schema backward op (no checkpoints or saved y: the sliced
+    backward runs its own forward for both) against the checkpointed
+    training-path pair, at dstate 256 with z."""
+    inp = make_inputs(2, 8, 50, 256, None, True, True, True, torch.float32)
+    Bk = inp["B"][:, None].transpose(-1, -2).contiguous()
+    Ck = inp["C"][:, None].transpose(-1, -2).contiguous()
+    args = (inp["u"], inp["delta"], inp["A"], Bk, Ck, inp["D"], inp["z"], inp["delta_bias"], True)
+    out, last, ckpt, ysave = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
+    out2, last2 = torch.ops.mamba_cpu.selective_scan_fwd(*args)
+    assert torch.equal(out, out2) and torch.equal(last, last2)
+    dout = torch.randn_like(out)
+    dlast = torch.randn_like(last)
+    g1 = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave)
+    g2 = torch.ops.mamba_cpu.selective_scan_bwd(*args, dout, dlast)
+    for a, b in zip(g1, g2):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
 def test_version_and_device_check():
     from mamba_cpu import _C
 
