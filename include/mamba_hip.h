@@ -413,7 +413,8 @@ int mcpu_ssd_varlen_states(const mcpu_ssd_args* a, const void* saved, size_t sav
 /* One decode step of a Mamba-1 block for a batch of single tokens: what the
  * reference's patched transformers MambaBlock computes for one token with a
  * cache (src/mamba_cpu/hf.py:26-112 routes its pieces: causal_conv1d_update,
- * selective_state_update), in four launches instead of a dozen:
+ * selective_state_update), in three launches instead of a dozen (four for
+ * blocks of Mamba-790M width and up, whose x_proj runs as its own product):
  *   u    = RMSNorm(hidden) when norm_weight != NULL (else hidden), in dtype
  *   x, z = in_proj(u)                    (2 d_inner)
  *   x    = silu(conv1d_update(conv_state, x))   conv_state shifted in place

@@ -1,20 +1,32 @@
 // One decode step of a Mamba-1 block for a batch of single tokens (batch <=
-// 8), in four launches:
+// 8), in three launches:
 //   1. block_in_kernel: RMSNorm of the hidden rows (every workgroup, into
-//      LDS), the in_proj rows of this workgroup (one wave per row, the batch
+//      LDS), the in_proj rows of this workgroup (RW rows per wave, the batch
 //      rows at once), and for the x half the depthwise conv update of that
-//      channel (conv state shifted in place) with silu;
-//   2. gemv_kernel: x_proj over the conv outputs (dt, B, C);
-//   3. block_ssm_kernel: dt_proj row, softplus, the selective state update
-//      (state in place), D skip and the silu(z) gate;
-//   4. gemv_kernel: out_proj, plus the residual.
+//      channel (conv state shifted in place) with silu. A workgroup of x rows
+//      then multiplies its channels' conv outputs by the matching x_proj
+//      columns: a partial x_proj sum over those channels, for every output
+//      (dt, B, C) and batch row;
+//   2. block_ssm_kernel: x_proj = those partial sums added in a fixed order,
+//      then dt_proj, softplus, the selective state update (state in place),
+//      the D skip and the silu(z) gate;
+//   3. gemv_kernel: out_proj, plus the residual.
+// Where adding the partial sums would cost block_ssm_kernel more than a
+// separate product (wide blocks: many x workgroups times many x_proj
+// outputs), x_proj runs as a gemv_kernel between 1 and 2 instead.
 // The in_proj, x_proj and out_proj products are matrix-vector products over
 // a handful of rows: they read each weight once, four elements per lane
 // (coalesced rows), against the batch rows held in LDS, and reduce across
 // the wave with DPP and permlane swaps. Intermediate vectors live in a small
 // float32 workspace holding values already rounded to the storage type, as
 // transformers' separate ops would have stored them.
+// Each kernel requests all of its global loads before it waits on any, and
+// keeps the values as stored (a float4, or two 32-bit words holding four
+// 16-bit values) until then: a conversion next to a conditional load makes
+// the compiler wait for that load on the spot, which turns a kernel's
+// prologue into a chain of memory round trips.
 #include <cstring>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "mcpu_common.h"
@@ -24,9 +36,14 @@ namespace mcpu {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kSsmThreads = 1024;                  // block_ssm_kernel: 64 channels x 16 lanes
+constexpr int kSsmChannels = kSsmThreads / 16;
 constexpr int kMaxBatch = 8;
 constexpr int kMaxLdsFloats = 32768;
 constexpr int kMaxConvState = 8;
+constexpr int kMaxXdb = 2048;                      // dt_rank + 2 dstate
+constexpr int kPartLoads = 16;                     // partial sums one block_ssm thread adds
+constexpr int kDtLoads = 8;                        // dt_proj weights per lane requested at once
 
 struct MixerParams {
   const void* hidden;
@@ -45,11 +62,15 @@ struct MixerParams {
   const void* out_w;
   const void* out_b;
   void* out;
-  float* xc;    // (batch, d_inner): silu(conv) of the x half
-  float* zg;    // (batch, d_inner): the z half
-  float* xdb;   // (batch, dt_rank + 2 dstate): x_proj
-  float* yv;    // (batch, d_inner): gated scan output
+  float* xc;     // (batch, d_inner): silu(conv) of the x half
+  float* zg;     // (batch, d_inner): the z half
+  float* xdb;    // (batch, dt_rank + 2 dstate): x_proj, when it runs as its own product
+  float* xpart;  // (batch, xpp, dt_rank + 2 dstate): partial x_proj sums, or null
+  float* yv;     // (batch, d_inner): gated scan output
   int64_t batch, dm, di, R, N, W, S;
+  int nxwg;      // block_in workgroups holding x rows: partial sums 0 .. nxwg - 1
+  int xq, xs;    // block_ssm_kernel adds xq groups of xs partial sums per output
+  int xpp;       // = xq xs >= nxwg: partial sums per output, nxwg .. xpp - 1 zero
   float eps;
   int add_residual, hidden_dtype, state_dtype, out_dtype;
 };
@@ -57,31 +78,41 @@ struct MixerParams {
 // v rounded to the storage type T (exact in float32).
 template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f32(from_f32<T>(v)); }
 
-template <typename T> __device__ __forceinline__ float4 ld4t(const void* base, int64_t i);
-template <> __device__ __forceinline__ float4 ld4t<float>(const void* base, int64_t i) {
-  return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+// Four consecutive elements of a T tensor as stored: a float4 for float32,
+// two 32-bit words for the 16-bit types.
+template <typename T> struct Raw4 { using type = uint2; };
+template <> struct Raw4<float> { using type = float4; };
+template <typename T> using raw4 = typename Raw4<T>::type;
+
+template <typename T> __device__ __forceinline__ raw4<T> ld_raw4(const void* base, int64_t i) {
+  return *reinterpret_cast<const raw4<T>*>(static_cast<const T*>(base) + i);
 }
-template <> __device__ __forceinline__ float4 ld4t<bf16>(const void* base, int64_t i) {
-  const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+template <typename T> __device__ __forceinline__ float4 cvt4(const raw4<T>& r);
+template <> __device__ __forceinline__ float4 cvt4<float>(const float4& r) { return r; }
+template <> __device__ __forceinline__ float4 cvt4<bf16>(const uint2& u) {
   return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
                      __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
 }
-template <> __device__ __forceinline__ float4 ld4t<f16>(const void* base, int64_t i) {
-  const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+template <> __device__ __forceinline__ float4 cvt4<f16>(const uint2& u) {
   auto h = [](uint32_t bits) { return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits))); };
   return make_float4(h(u.x & 0xffff), h(u.x >> 16), h(u.y & 0xffff), h(u.y >> 16));
 }
 
-// Element i of a tensor of storage type dt (float32, bf16 or f16) as float.
-__device__ __forceinline__ float ld_any(const void* base, int64_t i, int dt) {
-  if (dt == MCPU_F32) return static_cast<const float*>(base)[i];
-  if (dt == MCPU_BF16) return ld<bf16>(base, i);
-  return ld<f16>(base, i);
+// Element i of a T tensor as stored, in the low bits of a 32-bit word: each
+// 16-bit element gets a register of its own (two 16-bit loads into halves of
+// one register would make the second wait for the first).
+template <typename T> __device__ __forceinline__ uint32_t ld_bits(const T* base, int64_t i) {
+  if constexpr (std::is_same_v<T, float>) return __builtin_bit_cast(uint32_t, base[i]);
+  else return *reinterpret_cast<const uint16_t*>(base + i);
 }
-__device__ __forceinline__ void st_any(void* base, int64_t i, float v, int dt) {
-  if (dt == MCPU_F32) static_cast<float*>(base)[i] = v;
-  else if (dt == MCPU_BF16) st<bf16>(base, i, v);
-  else st<f16>(base, i, v);
+template <typename T> __device__ __forceinline__ float bits_f32(uint32_t b) {
+  if constexpr (std::is_same_v<T, float>) return __builtin_bit_cast(float, b);
+  else if constexpr (std::is_same_v<T, bf16>) return __builtin_bit_cast(float, b << 16);
+  else return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(b)));
+}
+template <typename T> __device__ __forceinline__ void st_bits(T* base, int64_t i, uint32_t b) {
+  if constexpr (std::is_same_v<T, float>) base[i] = __builtin_bit_cast(float, b);
+  else *reinterpret_cast<uint16_t*>(base + i) = static_cast<uint16_t>(b);
 }
 
 // Sum over the 64 lanes of a wave, in a fixed order, in every lane.
@@ -94,20 +125,23 @@ __device__ __forceinline__ float wave_sum(float v) {
 // float4 chunks (256 elements of a row per wave) each lane loads per pass.
 constexpr int kChunks = 8;
 
-// This wave's weight rows row0 .. row0 + RW - 1 (rows from nrows on, and
-// columns past K, read as 0), chunk u of pass k0 at k = k0 + 4 lane + 256 u.
+// This wave's weight rows row0 .. row0 + RW - 1 of a matrix with rows
+// 0 .. last, as stored, chunk u of pass k0 at k = k0 + 4 lane + 256 u. The
+// loads are unconditional, from addresses clamped into the matrix (row last,
+// columns K - 4 ..): rows past last and columns past K hold copies whose
+// products are never used.
 template <typename T, int RW>
 struct RowTiles {
-  float4 w[RW][kChunks];
+  raw4<T> w[RW][kChunks];
 
-  __device__ __forceinline__ void load(const void* wt, int64_t row0, int nrows, int K, int k0) {
+  __device__ __forceinline__ void load(const void* wt, int64_t row0, int64_t last, int K, int k0) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
       for (int u = 0; u < kChunks; ++u) {
-        const int k = k0 + 4 * lane + 256 * u;
-        w[rr][u] = (rr < nrows && k < K) ? ld4t<T>(wt, (row0 + rr) * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int k = min(k0 + 4 * lane + 256 * u, K - 4);
+        w[rr][u] = ld_raw4<T>(wt, (row0 + rr < last ? row0 + rr : last) * K + k);
       }
   }
 
@@ -124,11 +158,12 @@ struct RowTiles {
         const float4 xv = *reinterpret_cast<const float4*>(sx + m * K + k);
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr) {
+          const float4 wv = cvt4<T>(w[rr][u]);
           float a = acc[rr][m];
-          a = fmaf(w[rr][u].x, xv.x, a);
-          a = fmaf(w[rr][u].y, xv.y, a);
-          a = fmaf(w[rr][u].z, xv.z, a);
-          a = fmaf(w[rr][u].w, xv.w, a);
+          a = fmaf(wv.x, xv.x, a);
+          a = fmaf(wv.y, xv.y, a);
+          a = fmaf(wv.z, xv.z, a);
+          a = fmaf(wv.w, xv.w, a);
           acc[rr][m] = a;
         }
       }
@@ -138,18 +173,18 @@ struct RowTiles {
 
 // acc[r][m] = sum_k X[m][k] W[row0 + r][k], summed over the wave: every lane
 // ends with every row's sums. `tiles` holds the first pass's weights,
-// loaded before X was staged (so their latency overlapped the staging);
+// requested before X was staged (so their latency overlapped the staging);
 // further passes (K > 2048) load and multiply in turn.
 template <typename T, int MT, int RW>
 __device__ __forceinline__ void rows_dot(float (&acc)[RW][MT], RowTiles<T, RW>& tiles, const float* sx,
-                                         const void* w, int64_t row0, int nrows, int K) {
+                                         const void* w, int64_t row0, int64_t last, int K) {
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[rr][m] = 0.f;
   tiles.template fma<MT>(acc, sx, K, 0);
   for (int k0 = 256 * kChunks; k0 < K; k0 += 256 * kChunks) {
-    tiles.load(w, row0, nrows, K, k0);
+    tiles.load(w, row0, last, K, k0);
     tiles.template fma<MT>(acc, sx, K, k0);
   }
 #pragma unroll
@@ -158,84 +193,117 @@ __device__ __forceinline__ void rows_dot(float (&acc)[RW][MT], RowTiles<T, RW>& 
     for (int m = 0; m < MT; ++m) acc[rr][m] = wave_sum(acc[rr][m]);
 }
 
-// LDS rows sx[m][k] (m < MT; rows past batch are 0) = float32 vectors of
-// length K from a float32 workspace.
+// Lane m's value of a wave-uniform array indexed by lane (m < MT).
 template <int MT>
-__device__ __forceinline__ void load_rows(float* sx, const float* src, int64_t batch, int K) {
-  for (int i = 4 * threadIdx.x; i < MT * K; i += 4 * kThreads) {
-    const int m = i / K;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < batch) v = *reinterpret_cast<const float4*>(src + i);
-    *reinterpret_cast<float4*>(sx + i) = v;
-  }
+__device__ __forceinline__ float pick_lane(const float (&v)[MT], int lane) {
+  float y = 0.f;
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    if (lane == m) y = v[m];
+  return y;
 }
 
 }  // namespace
 
-// 1. RMSNorm (optional) + in_proj + conv update. Grid: ceil(2 d_inner / (4 RW))
-// workgroups; wave w handles in_proj rows (4 blockIdx.x + w) RW + rr.
-template <typename T, int MT, int RW>
+// 1. RMSNorm (optional) + in_proj + conv update + partial x_proj. Grid:
+// ceil(2 d_inner / (4 RW)) workgroups; wave w handles in_proj rows
+// (4 blockIdx.x + w) RW + rr, so workgroups 0 .. nxwg - 1 hold the x rows
+// (channels 4 RW blockIdx.x onwards). HF: the hidden rows are float32 (else T).
+template <typename T, int MT, int RW, bool HF>
 __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p) {
+  using TH = std::conditional_t<HF, float, T>;
   extern __shared__ __align__(16) float s_u[];   // (MT, d_model) rows, then the norm weight
   __shared__ float s_red[MT][kThreads / 64];
+  __shared__ float s_xc[MT][4 * RW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = static_cast<int>(p.dm);
   float* s_nw = s_u + MT * K;
   const int64_t nout = 2 * p.di;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RW;
   const int nrows = row0 >= nout ? 0 : static_cast<int>(nout - row0 < RW ? nout - row0 : RW);
-  // Everything this wave reads from memory is requested up front: its
-  // in_proj rows, then what its epilogue needs (lane m < batch: the bias and,
-  // for x rows, batch row m's conv window, weights and bias).
-  RowTiles<T, RW> tiles;
-  tiles.load(p.in_w, row0, nrows, K, 0);
-  const T* tb = static_cast<const T*>(p.in_b);
-  float eb[RW], ecb[RW], est[RW][kMaxConvState], ecw[RW][kMaxConvState];
+  const int nbk = static_cast<int>(p.batch) * K;
+  // Loads: first the hidden rows and the norm weight; once the rows are in,
+  // what the epilogue needs (lane m < batch: the bias and, for x rows, batch
+  // row m's conv window, weights and bias) and, in an x workgroup, the x_proj
+  // columns of its channels (thread j: output j); after the first barrier
+  // this wave's in_proj rows, which stream in while the norm runs. Requested
+  // before the rows arrive, the in_proj rows of every workgroup delay them
+  // (by about 1.4 us at Mamba-130M widths) more than issuing them later
+  // costs. Every load is unconditional, from an index clamped into its
+  // tensor (an absent optional tensor reads another one of its type); values
+  // read for positions outside it are never used. The scheduling barriers
+  // keep the groups in this order.
+  constexpr int kStage = 8, kNorm = 4;
+  raw4<TH> hv[kStage];
 #pragma unroll
-  for (int rr = 0; rr < RW; ++rr) {
-    const int64_t n = row0 + rr;
-    const bool mine = rr < nrows && lane < p.batch;
-    const bool xrow = mine && n < p.di;
-    eb[rr] = (mine && tb) ? to_f32(tb[n]) : 0.f;
-    ecb[rr] = (xrow && p.conv_b) ? to_f32(static_cast<const T*>(p.conv_b)[n]) : 0.f;
-    const T* stt = static_cast<const T*>(p.conv_state) + (lane * p.di + n) * p.S;
-    const T* cw = static_cast<const T*>(p.conv_w) + n * p.W;
+  for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(p.hidden, min(4 * (tid + kThreads * u), nbk - 4));
+  raw4<T> nv[kNorm];
 #pragma unroll
-    for (int i = 0; i < kMaxConvState; ++i) {
-      est[rr][i] = (xrow && i < p.S) ? to_f32(stt[i]) : 0.f;
-      ecw[rr][i] = (xrow && i < p.W) ? to_f32(cw[i]) : 0.f;
-    }
-  }
+  for (int u = 0; u < kNorm; ++u)
+    nv[u] = ld_raw4<T>(p.norm_w ? p.norm_w : p.in_w, min(4 * (tid + kThreads * u), K - 4));
+  __builtin_amdgcn_sched_barrier(0);
   // The block's input rows, rounded to T as transformers casts them for the
-  // norm, four elements per thread-step, loads first; the norm weight beside them.
-  constexpr int kStage = 4;
+  // norm, with each batch row's sum of squares.
   float ss[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) ss[m] = 0.f;
-  for (int base = 4 * tid; base < MT * K; base += 4 * kThreads * kStage) {
-    float4 hv[kStage];
+  for (int base = 0; base < MT * K; base += 4 * kThreads * kStage) {
+    if (base > 0) {
 #pragma unroll
-    for (int u = 0; u < kStage; ++u) {
-      const int i = base + 4 * kThreads * u;
-      hv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (i < MT * K && i / K < p.batch)
-        hv[u] = p.hidden_dtype == MCPU_F32 ? ld4t<float>(p.hidden, i) : ld4t<T>(p.hidden, i);
+      for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(p.hidden, min(base + 4 * (tid + kThreads * u), nbk - 4));
     }
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
-      const int i = base + 4 * kThreads * u;
+      const int i = base + 4 * (tid + kThreads * u);
       if (i >= MT * K) break;
       const int m = i / K;
-      const float4 v = make_float4(rnd<T>(hv[u].x), rnd<T>(hv[u].y), rnd<T>(hv[u].z), rnd<T>(hv[u].w));
+      const float4 h = i < nbk ? cvt4<TH>(hv[u]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 v = make_float4(rnd<T>(h.x), rnd<T>(h.y), rnd<T>(h.z), rnd<T>(h.w));
 #pragma unroll
       for (int mm = 0; mm < MT; ++mm)
         if (mm == m) ss[mm] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
       *reinterpret_cast<float4*>(s_u + i) = v;
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  const T* tb = static_cast<const T*>(p.in_b);
+  const T* cb = static_cast<const T*>(p.conv_b ? p.conv_b : p.conv_w);
+  const T* tbl = tb ? tb : static_cast<const T*>(p.in_w);
+  const int64_t ml = lane < p.batch ? lane : p.batch - 1;
+  uint32_t eb[RW], ecb[RW], est[RW][kMaxConvState], ecw[RW][kMaxConvState];
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) {
+    const int64_t n = row0 + rr < nout ? row0 + rr : nout - 1;
+    const int64_t nx = n < p.di ? n : p.di - 1;
+    eb[rr] = ld_bits(tbl, n);
+    ecb[rr] = ld_bits(cb, nx);
+    const T* stt = static_cast<const T*>(p.conv_state) + (ml * p.di + nx) * p.S;
+    const T* cw = static_cast<const T*>(p.conv_w) + nx * p.W;
+#pragma unroll
+    for (int i = 0; i < kMaxConvState; ++i) {
+      est[rr][i] = ld_bits(stt, min(i, static_cast<int>(p.S) - 1));
+      ecw[rr][i] = ld_bits(cw, min(i, static_cast<int>(p.W) - 1));
+    }
+  }
+  const int64_t J = p.R + 2 * p.N;
+  const bool xpart = p.xpart != nullptr && static_cast<int>(blockIdx.x) < p.nxwg;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 4 * RW;
+  const int cw = xpart ? static_cast<int>(p.di - c0 < 4 * RW ? p.di - c0 : 4 * RW) : 0;
+  raw4<T> xw[RW];
+  if (xpart) {
+    const int64_t jl = tid < J ? tid : J - 1;
+#pragma unroll
+    for (int u = 0; u < RW; ++u) xw[u] = ld_raw4<T>(p.x_w, jl * p.di + c0 + min(4 * u, cw - 4));
+  }
+  __builtin_amdgcn_sched_barrier(0);
   if (p.norm_w) {
-    for (int i = 4 * tid; i < K; i += 4 * kThreads)
-      *reinterpret_cast<float4*>(s_nw + i) = ld4t<T>(p.norm_w, i);
+#pragma unroll
+    for (int u = 0; u < kNorm; ++u) {
+      const int i = 4 * (tid + kThreads * u);
+      if (i < K) *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(nv[u]);
+    }
+    for (int i = 4 * (tid + kThreads * kNorm); i < K; i += 4 * kThreads)
+      *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(ld_raw4<T>(p.norm_w, i));
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float t = wave_sum(ss[m]);
@@ -243,6 +311,9 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
     }
   }
   __syncthreads();
+  RowTiles<T, RW> tiles;
+  tiles.load(p.in_w, row0, nout - 1, K, 0);
+  __builtin_amdgcn_sched_barrier(0);
   if (p.norm_w) {
     // u = w * round_T(x * rsqrt(mean(x^2) + eps)), rounded to T.
     for (int i = 4 * tid; i < MT * K; i += 4 * kThreads) {
@@ -260,128 +331,251 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
     }
     __syncthreads();
   }
-  if (nrows == 0) return;
-  float acc[RW][MT];
-  rows_dot<T, MT, RW>(acc, tiles, s_u, p.in_w, row0, nrows, K);
-  // Lane m finishes batch row m of each of the wave's rows.
+  if (nrows > 0) {
+    float acc[RW][MT];
+    rows_dot<T, MT, RW>(acc, tiles, s_u, p.in_w, row0, nout - 1, K);
+    // Lane m finishes batch row m of each of the wave's rows.
 #pragma unroll
-  for (int rr = 0; rr < RW; ++rr) {
-    const int64_t n = row0 + rr;
-    if (rr >= nrows) continue;
-    float y = 0.f;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      if (lane == m) y = acc[rr][m];
-    if (lane >= p.batch) continue;
-    const int64_t m = lane;
-    y = rnd<T>(y + eb[rr]);
-    if (n >= p.di) {
-      p.zg[m * p.di + (n - p.di)] = y;
-      continue;
-    }
-    // Depthwise conv update of channel n: taps 0 .. W-2 read the newest W-1
-    // state entries, tap W-1 reads y; the state shifts left by one and y
-    // becomes its newest entry.
-    float c = ecb[rr];
-    for (int k = 0; k < p.W - 1; ++k) {
-      float v = 0.f, wk = 0.f;
-#pragma unroll
-      for (int i = 0; i < kMaxConvState; ++i) {
-        if (i == p.S - (p.W - 1) + k) v = est[rr][i];
-        if (i == k) wk = ecw[rr][i];
+    for (int rr = 0; rr < RW; ++rr) {
+      const int64_t n = row0 + rr;
+      float y = pick_lane<MT>(acc[rr], lane);
+      if (rr >= nrows || lane >= p.batch) continue;
+      const int64_t m = lane;
+      y = rnd<T>(tb ? y + bits_f32<T>(eb[rr]) : y);
+      if (n >= p.di) {
+        p.zg[m * p.di + (n - p.di)] = y;
+        continue;
       }
-      c = fmaf(wk, v, c);
+      // Depthwise conv update of channel n: taps 0 .. W-2 read the newest W-1
+      // state entries, tap W-1 reads y; the state shifts left by one and y
+      // becomes its newest entry.
+      float c = p.conv_b ? bits_f32<T>(ecb[rr]) : 0.f;
+      for (int k = 0; k < p.W - 1; ++k) {
+        uint32_t v = 0, wk = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxConvState; ++i) {
+          if (i == p.S - (p.W - 1) + k) v = est[rr][i];
+          if (i == k) wk = ecw[rr][i];
+        }
+        c = fmaf(bits_f32<T>(wk), bits_f32<T>(v), c);
+      }
+      uint32_t wl = 0;
+#pragma unroll
+      for (int i = 0; i < kMaxConvState; ++i)
+        if (i == p.W - 1) wl = ecw[rr][i];
+      c = fmaf(bits_f32<T>(wl), y, c);
+      c = c * sigmoid(c);
+      T* stt = static_cast<T*>(p.conv_state) + (m * p.di + n) * p.S;
+#pragma unroll
+      for (int i = 0; i < kMaxConvState - 1; ++i)
+        if (i < p.S - 1) st_bits(stt, i, est[rr][i + 1]);
+      stt[p.S - 1] = from_f32<T>(y);
+      c = rnd<T>(c);
+      p.xc[m * p.di + n] = c;
+      s_xc[m][wave * RW + rr] = c;
     }
-    float wl = 0.f;
+  }
+  if (!xpart) return;  // uniform across the workgroup
+  // Partial x_proj over this workgroup's channels c0 .. c0 + cw - 1: thread j
+  // sums output j for every batch row, into partial-sum row blockIdx.x (rows
+  // of the outputs, so consecutive threads store consecutive words); the last
+  // x workgroup also zeroes the padding rows.
+  __syncthreads();
+  for (int64_t j = tid; j < J; j += kThreads) {
+    raw4<T> wr[RW];
 #pragma unroll
-    for (int i = 0; i < kMaxConvState; ++i)
-      if (i == p.W - 1) wl = ecw[rr][i];
-    c = fmaf(wl, y, c);
-    c = c * sigmoid(c);
-    T* stt = static_cast<T*>(p.conv_state) + (m * p.di + n) * p.S;
+    for (int u = 0; u < RW; ++u) {
+      wr[u] = xw[u];
+      if (j != tid) {
+        wr[u] = raw4<T>{};
+        if (4 * u < cw) wr[u] = ld_raw4<T>(p.x_w, j * p.di + c0 + 4 * u);
+      }
+    }
+    float acc[MT];
 #pragma unroll
-    for (int i = 0; i < kMaxConvState - 1; ++i)
-      if (i < p.S - 1) stt[i] = from_f32<T>(est[rr][i + 1]);
-    stt[p.S - 1] = from_f32<T>(y);
-    p.xc[m * p.di + n] = rnd<T>(c);
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < RW; ++u) {
+      if (4 * u >= cw) break;
+      const float4 w = cvt4<T>(wr[u]);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float a = acc[m];
+        a = fmaf(s_xc[m][4 * u], w.x, a);
+        a = fmaf(s_xc[m][4 * u + 1], w.y, a);
+        a = fmaf(s_xc[m][4 * u + 2], w.z, a);
+        a = fmaf(s_xc[m][4 * u + 3], w.w, a);
+        acc[m] = a;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= p.batch) break;
+      float* dst = p.xpart + m * p.xpp * J + j;
+      dst[blockIdx.x * J] = acc[m];
+      if (static_cast<int>(blockIdx.x) == p.nxwg - 1)
+        for (int q = p.nxwg; q < p.xpp; ++q) dst[q * J] = 0.f;
+    }
   }
 }
 
-// 2 / 4. Rows n of y[m][n] = round_T(sum_k x[m][k] W[n][k] + bias[n]) for
-// x (batch, K) float32 from the workspace: into outf (batch, nout) float32
-// when given, else out (out_dtype) = residual + y when add_residual, else y.
-template <typename T, int MT, int RW>
+// 3 (and x_proj where it runs alone). Rows n of y[m][n] = round_T(sum_k
+// x[m][k] W[n][k] + bias[n]) for x (batch, K) float32 from the workspace:
+// into outf (batch, nout) float32 when given, else out (out_dtype) =
+// residual + y when add_residual (residual: the hidden rows, float32 when HF,
+// else T), else y.
+template <typename T, int MT, int RW, bool HF>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(const MixerParams p, const float* x, const void* w,
                                                         const void* bias, int64_t nout, int K, float* outf) {
+  using TH = std::conditional_t<HF, float, T>;
   extern __shared__ __align__(16) float s_x[];   // (MT, K)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RW;
   const int nrows = row0 >= nout ? 0 : static_cast<int>(nout - row0 < RW ? nout - row0 : RW);
+  const int nbk = static_cast<int>(p.batch) * K;
+  // Loads: the x rows (staged into LDS first), this wave's weight rows, the
+  // epilogue's bias and residual.
+  // Unconditional, from indexes clamped into each tensor.
+  // An absent bias reads the weights; the residual is read from the hidden
+  // rows (batch, nout) of an out_proj, from x itself (float32, HF) for an
+  // x_proj, whose result takes none.
+  constexpr int kStage = 16;
+  float4 xv[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u)
+    xv[u] = *reinterpret_cast<const float4*>(x + min(4 * (tid + kThreads * u), nbk - 4));
+  __builtin_amdgcn_sched_barrier(0);
   RowTiles<T, RW> tiles;
-  tiles.load(w, row0, nrows, K, 0);
-  // the epilogue's bias and residual, requested with the weights
-  float eb[RW], er[RW];
+  tiles.load(w, row0, nout - 1, K, 0);
+  const int64_t ml = lane < p.batch ? lane : p.batch - 1;
+  const T* bl = static_cast<const T*>(bias ? bias : w);
+  const TH* hb = outf ? reinterpret_cast<const TH*>(x) : static_cast<const TH*>(p.hidden);
+  const int64_t hmax = outf ? nbk - 1 : p.batch * nout - 1;
+  uint32_t eb[RW], er[RW];
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
-    const int64_t n = row0 + rr;
-    const bool mine = rr < nrows && lane < p.batch;
-    eb[rr] = (mine && bias) ? to_f32(static_cast<const T*>(bias)[n]) : 0.f;
-    er[rr] = (mine && !outf && p.add_residual) ? ld_any(p.hidden, lane * nout + n, p.hidden_dtype) : 0.f;
+    const int64_t n = row0 + rr < nout ? row0 + rr : nout - 1;
+    eb[rr] = ld_bits(bl, n);
+    er[rr] = ld_bits(hb, min(ml * nout + n, hmax));
   }
-  load_rows<MT>(s_x, x, p.batch, K);
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int i = 4 * (tid + kThreads * u);
+    if (i < MT * K) *reinterpret_cast<float4*>(s_x + i) = i < nbk ? xv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int i = 4 * (tid + kThreads * kStage); i < MT * K; i += 4 * kThreads) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < nbk) v = *reinterpret_cast<const float4*>(x + i);
+    *reinterpret_cast<float4*>(s_x + i) = v;
+  }
   __syncthreads();
   if (nrows == 0) return;
   float acc[RW][MT];
-  rows_dot<T, MT, RW>(acc, tiles, s_x, w, row0, nrows, K);
+  rows_dot<T, MT, RW>(acc, tiles, s_x, w, row0, nout - 1, K);
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
     const int64_t n = row0 + rr;
-    if (rr >= nrows) continue;
-    float y = 0.f;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      if (lane == m) y = acc[rr][m];
-    if (lane >= p.batch) continue;
+    float y = pick_lane<MT>(acc[rr], lane);
+    if (rr >= nrows || lane >= p.batch) continue;
     const int64_t m = lane;
-    y = rnd<T>(y + eb[rr]);
+    y = rnd<T>(bias ? y + bits_f32<T>(eb[rr]) : y);
     if (outf) {
       outf[m * nout + n] = y;
     } else {
-      if (p.add_residual) y = er[rr] + y;
-      st_any(p.out, m * nout + n, y, p.out_dtype);
+      if (p.add_residual) y = bits_f32<TH>(er[rr]) + y;
+      if (p.out_dtype == MCPU_F32) static_cast<float*>(p.out)[m * nout + n] = y;
+      else st<T>(p.out, m * nout + n, y);
     }
   }
 }
 
-// 3. dt_proj + softplus + selective state update + D skip + silu(z) gate.
-// 16 lanes per channel (state n = lane + 16 s), 16 channels per workgroup;
-// grid (ceil(d_inner / 16), batch). The arithmetic of each channel is the
+// 2. x_proj (the partial sums added, FUSED, or the finished row) + dt_proj +
+// softplus + selective state update + D skip + silu(z) gate. 16 lanes per
+// channel (state n = lane + 16 s), 64 channels per workgroup; grid
+// (ceil(d_inner / 64), batch). The arithmetic of each channel is the
 // selective state update kernel's.
-template <typename T, typename Ts, int SPL>
-__global__ void __launch_bounds__(kThreads) block_ssm_kernel(const MixerParams p) {
-  const int j = threadIdx.x & 15;
-  const int64_t d = blockIdx.x * 16ll + (threadIdx.x >> 4);
+template <typename T, typename Ts, int SPL, bool FUSED>
+__global__ void __launch_bounds__(kSsmThreads) block_ssm_kernel(const MixerParams p) {
+  __shared__ float s_red[kSsmThreads];
+  __shared__ float s_xdb[kMaxXdb];
+  const int tid = threadIdx.x, j = tid & 15;
+  const int64_t d = blockIdx.x * static_cast<int64_t>(kSsmChannels) + (tid >> 4);
   const int64_t m = blockIdx.y;
-  if (d >= p.di) return;  // whole 16-lane rows leave together
-  const int64_t R = p.R, N = p.N;
-  const float* xdb = p.xdb + m * (R + 2 * N);
-  const T* dtw = static_cast<const T*>(p.dt_w) + d * R;
-  Ts* state = static_cast<Ts*>(p.ssm_state) + (m * p.di + d) * N;
-  // Every load of the channel first: none of them waits on another.
-  float sv0[SPL], av[SPL], bv[SPL], cv[SPL];
+  const int64_t R = p.R, N = p.N, J = R + 2 * N;
+  const bool live = d < p.di;
+  // Loads first. x_proj of batch row m: thread (q, oj) = (tid / J, tid % J)
+  // reads partial sums q xs .. q xs + xs - 1 of output oj (a wave reads
+  // consecutive words of a partial-sum row).
+  // All loads are unconditional, from indexes clamped into each tensor;
+  // values read for positions outside it are never used.
+  const int pq = FUSED ? tid / static_cast<int>(J) : 0;
+  const int pj = FUSED ? tid - pq * static_cast<int>(J) : 0;
+  const bool pa = FUSED && pq < p.xq;
+  float pv[FUSED ? kPartLoads : 1];
+  constexpr int kXr = kMaxXdb / kSsmThreads;
+  float xr[FUSED ? 1 : kXr];
+  if constexpr (FUSED) {
+    const float* src = p.xpart + (m * p.xpp + (pa ? pq : p.xq - 1) * p.xs) * J + pj;
+#pragma unroll
+    for (int u = 0; u < kPartLoads; ++u) pv[u] = src[min(u, p.xs - 1) * J];
+  } else {
+#pragma unroll
+    for (int u = 0; u < kXr; ++u) xr[u] = p.xdb[m * J + min(static_cast<int64_t>(tid + kSsmThreads * u), J - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // This channel: its dt_proj row (lane j: r = j + 16 i), state, A, x, z, D
+  // and dt bias.
+  const int64_t dl = live ? d : p.di - 1;
+  const T* dtw = static_cast<const T*>(p.dt_w) + dl * R;
+  Ts* state = static_cast<Ts*>(p.ssm_state) + (m * p.di + dl) * N;
+  uint32_t dw[kDtLoads];
+#pragma unroll
+  for (int i = 0; i < kDtLoads; ++i) dw[i] = ld_bits(dtw, min(static_cast<int64_t>(j + 16 * i), R - 1));
+  uint32_t sv0[SPL];
+  float av[SPL];
 #pragma unroll
   for (int s = 0; s < SPL; ++s) {
-    const int64_t n = j + 16 * s;
-    const bool ok = n < N;
-    sv0[s] = ok ? to_f32(state[n]) : 0.f;
-    av[s] = ok ? p.A[d * N + n] : 0.f;
-    bv[s] = ok ? xdb[R + n] : 0.f;
-    cv[s] = ok ? xdb[R + N + n] : 0.f;
+    const int64_t n = min(static_cast<int64_t>(j + 16 * s), N - 1);
+    sv0[s] = ld_bits(state, n);
+    av[s] = p.A[dl * N + n];
   }
-  const float x = p.xc[m * p.di + d], zz = p.zg[m * p.di + d];
-  const float Dd = p.D ? p.D[d] : 0.f, bias = p.dt_b ? p.dt_b[d] : 0.f;
+  const float x = p.xc[m * p.di + dl], zz = p.zg[m * p.di + dl];
+  const float Dd = (p.D ? p.D : p.A)[dl], bias = (p.dt_b ? p.dt_b : p.A)[dl];
+  __builtin_amdgcn_sched_barrier(0);
+  // x_proj into LDS, rounded to T as the product's output.
+  if constexpr (FUSED) {
+    // Selects, not a loop bound: a load used only under a condition would
+    // be moved next to its use.
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kPartLoads; ++u) sum = u < p.xs ? sum + pv[u] : sum;
+    if (pa) s_red[pq * J + pj] = sum;
+    __syncthreads();
+    for (int t = tid; t < J; t += kSsmThreads) {
+      float a = 0.f;
+      for (int q = 0; q < p.xq; ++q) a += s_red[q * J + t];
+      s_xdb[t] = rnd<T>(a);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kXr; ++u) {
+      const int t = tid + kSsmThreads * u;
+      if (t < J) s_xdb[t] = xr[u];
+    }
+  }
+  __syncthreads();
+  if (!live) return;  // whole 16-lane rows leave together, after the last barrier
   float part = 0.f;
-  for (int64_t r = j; r < R; r += 16) part = fmaf(xdb[r], to_f32(dtw[r]), part);
+#pragma unroll
+  for (int i = 0; i < kDtLoads; ++i)
+    if (j + 16 * i < R) part = fmaf(s_xdb[j + 16 * i], bits_f32<T>(dw[i]), part);
+  for (int64_t r0 = 16 * kDtLoads; r0 < R; r0 += 16 * kDtLoads) {  // dt_rank > 128: one round trip per 128
+#pragma unroll
+    for (int i = 0; i < kDtLoads; ++i) dw[i] = ld_bits(dtw, min(r0 + j + 16 * i, R - 1));
+#pragma unroll
+    for (int i = 0; i < kDtLoads; ++i)
+      if (r0 + j + 16 * i < R) part = fmaf(s_xdb[r0 + j + 16 * i], bits_f32<T>(dw[i]), part);
+  }
   float dt = rnd<T>(row_allreduce16(part));
   if (p.dt_b) dt += bias;
   dt = softplus(dt);
@@ -392,9 +586,9 @@ __global__ void __launch_bounds__(kThreads) block_ssm_kernel(const MixerParams p
     const int64_t n = j + 16 * s;
     if (n < N) {
       const float a = fast_exp(dt * av[s]);
-      const float sv = fmaf(sv0[s], a, dtx * bv[s]);
+      const float sv = fmaf(bits_f32<Ts>(sv0[s]), a, dtx * s_xdb[R + n]);
       state[n] = from_f32<Ts>(sv);
-      acc = fmaf(sv, cv[s], acc);
+      acc = fmaf(sv, s_xdb[R + N + n], acc);
     }
   }
   float y = row_allreduce16(acc);
@@ -414,56 +608,86 @@ int rows_per_wave(int64_t nout) {
   return 1;
 }
 
+// How block_ssm_kernel adds the partial x_proj sums of nxwg workgroups for
+// J outputs: xq groups of xs (at most kPartLoads) per output, xq J <=
+// kSsmThreads. Returns false where that does not fit: then x_proj runs as
+// its own product.
+bool partial_plan(int64_t nxwg, int64_t J, int* xq, int* xs) {
+  if (J > kSsmThreads) return false;
+  int64_t q = kSsmThreads / J;
+  if (q > nxwg) q = nxwg;
+  const int64_t s = (nxwg + q - 1) / q;
+  if (s > kPartLoads) return false;
+  *xq = static_cast<int>(q);
+  *xs = static_cast<int>(s);
+  return true;
+}
+
 template <typename T, int MT, int RW>
-hipError_t launch_rw(const MixerParams& p, hipStream_t st) {
+hipError_t launch_in(const MixerParams& p, bool hf, hipStream_t st) {
   const int64_t nin = 2 * p.di;
-  hipLaunchKernelGGL((block_in_kernel<T, MT, RW>), dim3(static_cast<unsigned>((nin + 4 * RW - 1) / (4 * RW))),
-                     dim3(kThreads), sizeof(float) * (MT + 1) * p.dm, st, p);
+  const dim3 grid(static_cast<unsigned>((nin + 4 * RW - 1) / (4 * RW)));
+  const size_t lds = sizeof(float) * (MT + 1) * p.dm;
+  if (hf || std::is_same_v<T, float>)
+    hipLaunchKernelGGL((block_in_kernel<T, MT, RW, true>), grid, dim3(kThreads), lds, st, p);
+  else
+    hipLaunchKernelGGL((block_in_kernel<T, MT, RW, false>), grid, dim3(kThreads), lds, st, p);
   return hipGetLastError();
 }
 
-template <typename T, int MT>
+template <typename T, int MT, int RW, bool HF>
+void launch_gemv(const MixerParams& p, const float* x, const void* w, const void* bias, int64_t nout, int64_t K,
+                 float* outf, hipStream_t st) {
+  const size_t lds = sizeof(float) * MT * K;
+  hipLaunchKernelGGL((gemv_kernel<T, MT, RW, HF>), dim3(static_cast<unsigned>((nout + 4 * RW - 1) / (4 * RW))),
+                     dim3(kThreads), lds, st, p, x, w, bias, nout, static_cast<int>(K), outf);
+}
+
+template <typename T, int MT, bool HF>
 hipError_t gemv(const MixerParams& p, const float* x, const void* w, const void* bias, int64_t nout, int64_t K,
                 float* outf, hipStream_t st) {
   const int rw = rows_per_wave(nout);
-  const size_t lds = sizeof(float) * MT * K;
-  auto grid = [&](int r) { return dim3(static_cast<unsigned>((nout + 4 * r - 1) / (4 * r))); };
-  if (rw == 4)
-    hipLaunchKernelGGL((gemv_kernel<T, MT, 4>), grid(4), dim3(kThreads), lds, st, p, x, w, bias, nout,
-                       static_cast<int>(K), outf);
-  else if (rw == 2)
-    hipLaunchKernelGGL((gemv_kernel<T, MT, 2>), grid(2), dim3(kThreads), lds, st, p, x, w, bias, nout,
-                       static_cast<int>(K), outf);
-  else
-    hipLaunchKernelGGL((gemv_kernel<T, MT, 1>), grid(1), dim3(kThreads), lds, st, p, x, w, bias, nout,
-                       static_cast<int>(K), outf);
+  if (rw == 4) launch_gemv<T, MT, 4, HF>(p, x, w, bias, nout, K, outf, st);
+  else if (rw == 2) launch_gemv<T, MT, 2, HF>(p, x, w, bias, nout, K, outf, st);
+  else launch_gemv<T, MT, 1, HF>(p, x, w, bias, nout, K, outf, st);
   return hipGetLastError();
 }
 
-template <typename T, typename Ts>
+template <typename T, typename Ts, bool FUSED>
 hipError_t launch_ssm(const MixerParams& p, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((p.di + 15) / 16), static_cast<unsigned>(p.batch));
-  if (p.N <= 16) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 1>), grid, dim3(kThreads), 0, st, p);
-  else if (p.N <= 32) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 2>), grid, dim3(kThreads), 0, st, p);
-  else if (p.N <= 64) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 4>), grid, dim3(kThreads), 0, st, p);
-  else hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 8>), grid, dim3(kThreads), 0, st, p);
+  const dim3 grid(static_cast<unsigned>((p.di + kSsmChannels - 1) / kSsmChannels), static_cast<unsigned>(p.batch));
+  if (p.N <= 16) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 1, FUSED>), grid, dim3(kSsmThreads), 0, st, p);
+  else if (p.N <= 32) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 2, FUSED>), grid, dim3(kSsmThreads), 0, st, p);
+  else if (p.N <= 64) hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 4, FUSED>), grid, dim3(kSsmThreads), 0, st, p);
+  else hipLaunchKernelGGL((block_ssm_kernel<T, Ts, 8, FUSED>), grid, dim3(kSsmThreads), 0, st, p);
   return hipGetLastError();
+}
+
+template <typename T, bool FUSED>
+hipError_t launch_ssm_state(const MixerParams& p, hipStream_t st) {
+  switch (p.state_dtype) {
+    case MCPU_F32: return launch_ssm<T, float, FUSED>(p, st);
+    case MCPU_BF16: return launch_ssm<T, bf16, FUSED>(p, st);
+    default: return launch_ssm<T, f16, FUSED>(p, st);
+  }
 }
 
 template <typename T, int MT>
 hipError_t step_t(const MixerParams& p, hipStream_t st) {
   const int rw = rows_per_wave(2 * p.di);
-  hipError_t e = rw == 4 ? launch_rw<T, MT, 4>(p, st) : rw == 2 ? launch_rw<T, MT, 2>(p, st)
-                                                                : launch_rw<T, MT, 1>(p, st);
+  const bool hf = p.hidden_dtype == MCPU_F32;
+  hipError_t e = rw == 4 ? launch_in<T, MT, 4>(p, hf, st) : rw == 2 ? launch_in<T, MT, 2>(p, hf, st)
+                                                                    : launch_in<T, MT, 1>(p, hf, st);
   if (e != hipSuccess) return e;
-  if ((e = gemv<T, MT>(p, p.xc, p.x_w, nullptr, p.R + 2 * p.N, p.di, p.xdb, st)) != hipSuccess) return e;
-  switch (p.state_dtype) {
-    case MCPU_F32: e = launch_ssm<T, float>(p, st); break;
-    case MCPU_BF16: e = launch_ssm<T, bf16>(p, st); break;
-    default: e = launch_ssm<T, f16>(p, st); break;
+  if (p.xpart) {
+    e = launch_ssm_state<T, true>(p, st);
+  } else {
+    if ((e = gemv<T, MT, true>(p, p.xc, p.x_w, nullptr, p.R + 2 * p.N, p.di, p.xdb, st)) != hipSuccess) return e;
+    e = launch_ssm_state<T, false>(p, st);
   }
   if (e != hipSuccess) return e;
-  return gemv<T, MT>(p, p.yv, p.out_w, p.out_b, p.dm, p.di, nullptr, st);
+  return hf || std::is_same_v<T, float> ? gemv<T, MT, true>(p, p.yv, p.out_w, p.out_b, p.dm, p.di, nullptr, st)
+                                        : gemv<T, MT, false>(p, p.yv, p.out_w, p.out_b, p.dm, p.di, nullptr, st);
 }
 
 template <typename T>
@@ -477,7 +701,9 @@ hipError_t step_dtype(const MixerParams& p, hipStream_t st) {
 int pow2_batch(int64_t b) { return b <= 1 ? 1 : b <= 2 ? 2 : b <= 4 ? 4 : 8; }
 
 struct StepLayout {
-  size_t xc = 0, zg = 0, xdb = 0, yv = 0, total = 0;
+  size_t xc = 0, zg = 0, xdb = 0, xpart = 0, yv = 0, total = 0;
+  int nxwg = 0, xq = 0, xs = 0;
+  bool fused = false;
 };
 StepLayout step_layout(const mcpu_mixer_step_args* a) {
   StepLayout w;
@@ -487,9 +713,14 @@ StepLayout step_layout(const mcpu_mixer_step_args* a) {
     off += align_up(sizeof(float) * n);
     return at;
   };
+  const int64_t J = a->dt_rank + 2 * a->dstate;
+  const int rw = rows_per_wave(2 * a->d_inner);
+  w.nxwg = static_cast<int>((a->d_inner + 4 * rw - 1) / (4 * rw));
+  w.fused = partial_plan(w.nxwg, J, &w.xq, &w.xs);
   w.xc = take(a->batch * a->d_inner);
   w.zg = take(a->batch * a->d_inner);
-  w.xdb = take(a->batch * (a->dt_rank + 2 * a->dstate));
+  if (w.fused) w.xpart = take(a->batch * J * w.xq * w.xs);
+  else w.xdb = take(a->batch * J);
   w.yv = take(a->batch * a->d_inner);
   w.total = off;
   return w;
@@ -509,6 +740,9 @@ int check_step(const mcpu_mixer_step_args* a) {
   if (a->d_model % 4 != 0 || a->d_inner % 4 != 0)
     return fail(MCPU_ERR_UNSUPPORTED, "mixer_step: d_model and d_inner must be multiples of 4");
   if (a->dstate > 128) return fail(MCPU_ERR_UNSUPPORTED, "mixer_step: dstate %lld > 128", (long long)a->dstate);
+  if (a->dt_rank + 2 * a->dstate > kMaxXdb)
+    return fail(MCPU_ERR_UNSUPPORTED, "mixer_step: dt_rank + 2 dstate = %lld > %d",
+                (long long)(a->dt_rank + 2 * a->dstate), kMaxXdb);
   if (a->state_len < a->width - 1 || a->state_len < 1 || a->state_len > kMaxConvState)
     return fail(MCPU_ERR_UNSUPPORTED, "mixer_step: conv state length must be in [max(1, width - 1), %d]",
                 kMaxConvState);
@@ -570,7 +804,15 @@ extern "C" int mcpu_mixer_step(const mcpu_mixer_step_args* a, void* workspace, s
   char* ws = static_cast<char*>(workspace);
   p.xc = reinterpret_cast<float*>(ws + w.xc);
   p.zg = reinterpret_cast<float*>(ws + w.zg);
-  p.xdb = reinterpret_cast<float*>(ws + w.xdb);
+  if (w.fused) {
+    p.xpart = reinterpret_cast<float*>(ws + w.xpart);
+    p.nxwg = w.nxwg;
+    p.xq = w.xq;
+    p.xs = w.xs;
+    p.xpp = w.xq * w.xs;
+  } else {
+    p.xdb = reinterpret_cast<float*>(ws + w.xdb);
+  }
   p.yv = reinterpret_cast<float*>(ws + w.yv);
   p.batch = a->batch;
   p.dm = a->d_model;

@@ -17,7 +17,7 @@ per token; only the argmax and the token copies run eagerly between replays.
 For Mamba (not FalconMamba, whose mixer normalises dt, B and C) the captured
 step runs each block as one fused operator, mamba_cpu::mixer_step: RMSNorm,
 in_proj, conv update, x_proj, dt_proj, state update, out_proj and the
-residual in four kernels, with the small-batch products as matrix-vector
+residual in three kernels, with the small-batch products as matrix-vector
 kernels that read each weight once. It computes what the block computes;
 the products sum in another order than the GEMM library's, so logits agree
 to float32 rounding and greedy tokens match `model.generate`'s. FalconMamba

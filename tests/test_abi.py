@@ -578,6 +578,7 @@ def test_mixer_step_rejects_bad_arguments_before_touching_a_device():
                            (dict(state_len=9), _C.MCPU_ERR_UNSUPPORTED, "conv state"),
                            (dict(width=4, state_len=2), _C.MCPU_ERR_UNSUPPORTED, "conv state"),
                            (dict(dstate=256), _C.MCPU_ERR_UNSUPPORTED, "dstate"),
+                           (dict(dt_rank=1793, dstate=128), _C.MCPU_ERR_UNSUPPORTED, "dt_rank"),
                            (dict(batch=8, d_inner=8192), _C.MCPU_ERR_UNSUPPORTED, "LDS"),
                            (dict(dtype=5), _C.MCPU_ERR_INVALID, "dtype"),
                            (dict(dtype=_C.MCPU_BF16, hidden_dtype=_C.MCPU_F16), _C.MCPU_ERR_INVALID, "dtype"),
@@ -589,10 +590,16 @@ def test_mixer_step_rejects_bad_arguments_before_touching_a_device():
 
 
 def test_mixer_step_workspace_holds_the_step_vectors():
+    """Three (batch, d_inner) float32 vectors (conv outputs, z, gated
+    output) plus x_proj's inputs to the state update: at Mamba-130M widths
+    the partial x_proj sums of the 192 in_proj workgroups holding x rows
+    (8 channels each) for the 80 outputs (dt_rank 48 + 2 x dstate 16), at
+    Mamba-2.8B widths (320 such workgroups of 16 channels, 192 outputs: more
+    than the state-update workgroup adds at once) the finished x_proj rows."""
     from mamba_cpu import _C
 
-    a = _step_args()
     al = lambda n: (n + 255) // 256 * 256  # noqa: E731
-    want = 3 * al(4 * 4 * 1536) + al(4 * 4 * (48 + 32))
-    assert _C.lib.mcpu_mixer_step_workspace_size(ctypes.byref(a)) == want
-    assert _C.lib.mcpu_mixer_step_workspace_size(ctypes.byref(_step_args(batch=9))) == 0
+    size = lambda **kw: _C.lib.mcpu_mixer_step_workspace_size(ctypes.byref(_step_args(**kw)))  # noqa: E731
+    assert size() == 3 * al(4 * 4 * 1536) + al(4 * 4 * 80 * 192)
+    assert size(batch=2, d_model=2560, d_inner=5120, dt_rank=160) == 3 * al(2 * 4 * 5120) + al(2 * 4 * 192)
+    assert size(batch=9) == 0
