@@ -48,7 +48,7 @@ int mcpu_check_device(void);
 const char* mcpu_version(void);
 
 /* sizeof() of an argument block ("scan", "conv", "conv_update",
- * "state_update", "ssd", "mixer_step"), 0 for an unknown name. A binding must
+ * "state_update", "ssd", "mixer_step", "norm_linear"), 0 for an unknown name. A binding must
  * compare it with its own sizeof of each block it uses before its first call:
  * the library reads a whole block, whatever the caller allocated. */
 size_t mcpu_args_size(const char* name);
@@ -460,6 +460,38 @@ typedef struct mcpu_mixer_step_args {
 size_t mcpu_mixer_step_workspace_size(const mcpu_mixer_step_args* a);
 /* One step. Updates conv_state and ssm_state in place and writes out. */
 int mcpu_mixer_step(const mcpu_mixer_step_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Final norm and output head of a decode step.                              */
+/* ------------------------------------------------------------------------ */
+
+/* out = Linear(RMSNorm(hidden)) for a batch of single tokens: a Mamba
+ * model's last step after its blocks (transformers' MambaRMSNorm norm_f,
+ * then lm_head on the result cast to the weights' dtype, logits .float()):
+ *   r   = hidden * rsqrt(mean(hidden^2) + norm_eps)     (float32)
+ *   u   = round_dtype(norm_weight * round_hidden(r))    (round_dtype(hidden)
+ *                                                        without a norm weight)
+ *   out = round_dtype(weight u + bias)                  stored as out_dtype
+ * round_hidden rounds to hidden_dtype (nothing for float32 rows); arithmetic
+ * is float32. No counterpart in the reference (it has no fused decode path):
+ * one launch for callers that replay a whole decode step. All tensors
+ * contiguous; hidden, weight and norm_weight 16-byte aligned; batch <= 8;
+ * d_in a multiple of 4; with batch rounded up to a power of two,
+ * (batch + 1) x d_in at most 32768. */
+typedef struct mcpu_norm_linear_args {
+  const void* hidden;       /* (batch, d_in), hidden_dtype */
+  const void* norm_weight;  /* (d_in), dtype, optional */
+  const void* weight;       /* (d_out, d_in), dtype */
+  const void* bias;         /* (d_out), dtype, optional */
+  void* out;                /* (batch, d_out), out_dtype */
+  int64_t batch, d_in, d_out;
+  float norm_eps;
+  int32_t dtype;            /* weights */
+  int32_t hidden_dtype;     /* dtype or MCPU_F32 */
+  int32_t out_dtype;        /* dtype or MCPU_F32 */
+} mcpu_norm_linear_args;
+
+int mcpu_norm_linear(const mcpu_norm_linear_args* a, void* stream);
 
 #ifdef __cplusplus
 }

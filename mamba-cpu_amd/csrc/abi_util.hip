@@ -57,6 +57,7 @@ extern "C" size_t mcpu_args_size(const char* name) {
   if (std::strcmp(name, "state_update") == 0) return sizeof(mcpu_state_update_args);
   if (std::strcmp(name, "ssd") == 0) return sizeof(mcpu_ssd_args);
   if (std::strcmp(name, "mixer_step") == 0) return sizeof(mcpu_mixer_step_args);
+  if (std::strcmp(name, "norm_linear") == 0) return sizeof(mcpu_norm_linear_args);
   return 0;
 }
 

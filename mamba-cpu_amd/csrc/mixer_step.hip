@@ -75,6 +75,17 @@ struct MixerParams {
   int add_residual, hidden_dtype, state_dtype, out_dtype;
 };
 
+struct NormLinearParams {
+  const void* x;     // (batch, K): float32 when HF, else T
+  const void* nw;    // (K), T, or null
+  const void* w;     // (nout, K), T
+  const void* bias;  // (nout), T, or null
+  void* out;         // (batch, nout): float32 when out_f32, else T
+  int64_t batch, nout, ngroups;
+  int K, out_f32;
+  float eps;
+};
+
 // v rounded to the storage type T (exact in float32).
 template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f32(from_f32<T>(v)); }
 
@@ -126,20 +137,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 constexpr int kChunks = 8;
 
 // This wave's weight rows row0 .. row0 + RW - 1 of a matrix with rows
-// 0 .. last, as stored, chunk u of pass k0 at k = k0 + 4 lane + 256 u. The
-// loads are unconditional, from addresses clamped into the matrix (row last,
-// columns K - 4 ..): rows past last and columns past K hold copies whose
-// products are never used.
-template <typename T, int RW>
+// 0 .. last, as stored, chunk u of pass k0 at k = k0 + 4 lane + 256 u
+// (u < KC). The loads are unconditional, from addresses clamped into the
+// matrix (row last, columns K - 4 ..): rows past last and columns past K
+// hold copies whose products are never used.
+template <typename T, int RW, int KC = kChunks>
 struct RowTiles {
-  raw4<T> w[RW][kChunks];
+  static constexpr int kc = KC;
+  raw4<T> w[RW][KC];
 
   __device__ __forceinline__ void load(const void* wt, int64_t row0, int64_t last, int K, int k0) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
-      for (int u = 0; u < kChunks; ++u) {
+      for (int u = 0; u < KC; ++u) {
         const int k = min(k0 + 4 * lane + 256 * u, K - 4);
         w[rr][u] = ld_raw4<T>(wt, (row0 + rr < last ? row0 + rr : last) * K + k);
       }
@@ -150,7 +162,7 @@ struct RowTiles {
   __device__ __forceinline__ void fma(float (&acc)[RW][MT], const float* sx, int K, int k0) const {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int u = 0; u < kChunks; ++u) {
+    for (int u = 0; u < KC; ++u) {
       const int k = k0 + 4 * lane + 256 * u;
       if (k >= K) break;
 #pragma unroll
@@ -174,16 +186,16 @@ struct RowTiles {
 // acc[r][m] = sum_k X[m][k] W[row0 + r][k], summed over the wave: every lane
 // ends with every row's sums. `tiles` holds the first pass's weights,
 // requested before X was staged (so their latency overlapped the staging);
-// further passes (K > 2048) load and multiply in turn.
-template <typename T, int MT, int RW>
-__device__ __forceinline__ void rows_dot(float (&acc)[RW][MT], RowTiles<T, RW>& tiles, const float* sx,
+// further passes (K > 256 KC) load and multiply in turn.
+template <typename T, int MT, int RW, int KC>
+__device__ __forceinline__ void rows_dot(float (&acc)[RW][MT], RowTiles<T, RW, KC>& tiles, const float* sx,
                                          const void* w, int64_t row0, int64_t last, int K) {
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[rr][m] = 0.f;
   tiles.template fma<MT>(acc, sx, K, 0);
-  for (int k0 = 256 * kChunks; k0 < K; k0 += 256 * kChunks) {
+  for (int k0 = 256 * KC; k0 < K; k0 += 256 * KC) {
     tiles.load(w, row0, last, K, k0);
     tiles.template fma<MT>(acc, sx, K, k0);
   }
@@ -203,6 +215,110 @@ __device__ __forceinline__ float pick_lane(const float (&v)[MT], int lane) {
   return y;
 }
 
+// The batch rows of x (batch, K), float32 when HF else T, staged in LDS as
+// s_u (MT, K) and RMS-normalised as transformers' MambaRMSNorm does, with
+// the weight nw (T) when given:
+//   s_u = round_T(nw * round_R(x * rsqrt(mean(x^2) + eps)))
+// where x is the row as given, or rounded to T first (CAST: a Mamba block
+// casts its input to the weights' dtype before its norm), and round_R
+// rounds to the dtype the norm sees (T when CAST or the rows are T, nothing
+// for float32 rows). Without a weight s_u = round_T(x). Rows from batch on
+// are zero. Four steps, so that a kernel can request loads between them:
+// issue() requests the rows and the weight (an absent weight reads alt, any
+// T tensor of at least K elements); stage() waits for the rows, stores them
+// and sums each row's squares; finish() stores the weight and reduces the
+// sums over the workgroup, ending with a barrier; normalize() applies the
+// norm, ending with a barrier.
+template <typename T, int MT, bool HF, bool CAST>
+struct RowStage {
+  using TH = std::conditional_t<HF, float, T>;
+  static constexpr int kStage = 8, kNorm = 4;
+  const void* x;
+  const void* nw;
+  int K, nbk;
+  raw4<TH> hv[kStage];
+  raw4<T> nv[kNorm];
+  float ss[MT];
+
+  __device__ __forceinline__ RowStage(const void* x_, const void* nw_, int64_t batch, int K_)
+      : x(x_), nw(nw_), K(K_), nbk(static_cast<int>(batch) * K_) {}
+
+  __device__ __forceinline__ void issue(const void* alt) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(x, min(4 * (tid + kThreads * u), nbk - 4));
+#pragma unroll
+    for (int u = 0; u < kNorm; ++u) nv[u] = ld_raw4<T>(nw ? nw : alt, min(4 * (tid + kThreads * u), K - 4));
+  }
+
+  __device__ __forceinline__ void stage(float* s_u) {
+    const int tid = threadIdx.x;
+    const bool to_t = CAST || nw == nullptr;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) ss[m] = 0.f;
+    for (int base = 0; base < MT * K; base += 4 * kThreads * kStage) {
+      if (base > 0) {
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(x, min(base + 4 * (tid + kThreads * u), nbk - 4));
+      }
+#pragma unroll
+      for (int u = 0; u < kStage; ++u) {
+        const int i = base + 4 * (tid + kThreads * u);
+        if (i >= MT * K) break;
+        const int m = i / K;
+        float4 v = i < nbk ? cvt4<TH>(hv[u]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (to_t) v = make_float4(rnd<T>(v.x), rnd<T>(v.y), rnd<T>(v.z), rnd<T>(v.w));
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm)
+          if (mm == m) ss[mm] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        *reinterpret_cast<float4*>(s_u + i) = v;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void finish(float* s_nw, float (*s_red)[kThreads / 64]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (nw) {
+#pragma unroll
+      for (int u = 0; u < kNorm; ++u) {
+        const int i = 4 * (tid + kThreads * u);
+        if (i < K) *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(nv[u]);
+      }
+      for (int i = 4 * (tid + kThreads * kNorm); i < K; i += 4 * kThreads)
+        *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(ld_raw4<T>(nw, i));
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float t = wave_sum(ss[m]);
+        if (lane == 0) s_red[m][wave] = t;
+      }
+    }
+    __syncthreads();
+  }
+
+  __device__ __forceinline__ void normalize(float* s_u, const float* s_nw, float (*s_red)[kThreads / 64],
+                                            float eps) {
+    if (!nw) return;
+    for (int i = 4 * threadIdx.x; i < MT * K; i += 4 * kThreads) {
+      const int m = i / K;
+      float tot = 0.f;
+#pragma unroll
+      for (int mm = 0; mm < MT; ++mm)
+        if (mm == m) tot = (s_red[mm][0] + s_red[mm][1]) + (s_red[mm][2] + s_red[mm][3]);
+      const float rs = rsqrtf(tot / static_cast<float>(K) + eps);
+      float4 v = *reinterpret_cast<const float4*>(s_u + i);
+      const float4 w = *reinterpret_cast<const float4*>(s_nw + (i - m * K));
+      if (CAST || !HF)
+        v = make_float4(rnd<T>(w.x * rnd<T>(v.x * rs)), rnd<T>(w.y * rnd<T>(v.y * rs)),
+                        rnd<T>(w.z * rnd<T>(v.z * rs)), rnd<T>(w.w * rnd<T>(v.w * rs)));
+      else
+        v = make_float4(rnd<T>(w.x * (v.x * rs)), rnd<T>(w.y * (v.y * rs)), rnd<T>(w.z * (v.z * rs)),
+                        rnd<T>(w.w * (v.w * rs)));
+      *reinterpret_cast<float4*>(s_u + i) = v;
+    }
+    __syncthreads();
+  }
+};
+
 }  // namespace
 
 // 1. RMSNorm (optional) + in_proj + conv update + partial x_proj. Grid:
@@ -211,7 +327,6 @@ __device__ __forceinline__ float pick_lane(const float (&v)[MT], int lane) {
 // (channels 4 RW blockIdx.x onwards). HF: the hidden rows are float32 (else T).
 template <typename T, int MT, int RW, bool HF>
 __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p) {
-  using TH = std::conditional_t<HF, float, T>;
   extern __shared__ __align__(16) float s_u[];   // (MT, d_model) rows, then the norm weight
   __shared__ float s_red[MT][kThreads / 64];
   __shared__ float s_xc[MT][4 * RW];
@@ -221,7 +336,6 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
   const int64_t nout = 2 * p.di;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RW;
   const int nrows = row0 >= nout ? 0 : static_cast<int>(nout - row0 < RW ? nout - row0 : RW);
-  const int nbk = static_cast<int>(p.batch) * K;
   // Loads: first the hidden rows and the norm weight; once the rows are in,
   // what the epilogue needs (lane m < batch: the bias and, for x rows, batch
   // row m's conv window, weights and bias) and, in an x workgroup, the x_proj
@@ -233,38 +347,10 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
   // tensor (an absent optional tensor reads another one of its type); values
   // read for positions outside it are never used. The scheduling barriers
   // keep the groups in this order.
-  constexpr int kStage = 8, kNorm = 4;
-  raw4<TH> hv[kStage];
-#pragma unroll
-  for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(p.hidden, min(4 * (tid + kThreads * u), nbk - 4));
-  raw4<T> nv[kNorm];
-#pragma unroll
-  for (int u = 0; u < kNorm; ++u)
-    nv[u] = ld_raw4<T>(p.norm_w ? p.norm_w : p.in_w, min(4 * (tid + kThreads * u), K - 4));
+  RowStage<T, MT, HF, true> rows(p.hidden, p.norm_w, p.batch, K);
+  rows.issue(p.in_w);
   __builtin_amdgcn_sched_barrier(0);
-  // The block's input rows, rounded to T as transformers casts them for the
-  // norm, with each batch row's sum of squares.
-  float ss[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) ss[m] = 0.f;
-  for (int base = 0; base < MT * K; base += 4 * kThreads * kStage) {
-    if (base > 0) {
-#pragma unroll
-      for (int u = 0; u < kStage; ++u) hv[u] = ld_raw4<TH>(p.hidden, min(base + 4 * (tid + kThreads * u), nbk - 4));
-    }
-#pragma unroll
-    for (int u = 0; u < kStage; ++u) {
-      const int i = base + 4 * (tid + kThreads * u);
-      if (i >= MT * K) break;
-      const int m = i / K;
-      const float4 h = i < nbk ? cvt4<TH>(hv[u]) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 v = make_float4(rnd<T>(h.x), rnd<T>(h.y), rnd<T>(h.z), rnd<T>(h.w));
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm)
-        if (mm == m) ss[mm] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-      *reinterpret_cast<float4*>(s_u + i) = v;
-    }
-  }
+  rows.stage(s_u);
   __builtin_amdgcn_sched_barrier(0);
   const T* tb = static_cast<const T*>(p.in_b);
   const T* cb = static_cast<const T*>(p.conv_b ? p.conv_b : p.conv_w);
@@ -296,41 +382,11 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
     for (int u = 0; u < RW; ++u) xw[u] = ld_raw4<T>(p.x_w, jl * p.di + c0 + min(4 * u, cw - 4));
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (p.norm_w) {
-#pragma unroll
-    for (int u = 0; u < kNorm; ++u) {
-      const int i = 4 * (tid + kThreads * u);
-      if (i < K) *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(nv[u]);
-    }
-    for (int i = 4 * (tid + kThreads * kNorm); i < K; i += 4 * kThreads)
-      *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(ld_raw4<T>(p.norm_w, i));
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float t = wave_sum(ss[m]);
-      if (lane == 0) s_red[m][wave] = t;
-    }
-  }
-  __syncthreads();
+  rows.finish(s_nw, s_red);
   RowTiles<T, RW> tiles;
   tiles.load(p.in_w, row0, nout - 1, K, 0);
   __builtin_amdgcn_sched_barrier(0);
-  if (p.norm_w) {
-    // u = w * round_T(x * rsqrt(mean(x^2) + eps)), rounded to T.
-    for (int i = 4 * tid; i < MT * K; i += 4 * kThreads) {
-      const int m = i / K;
-      float tot = 0.f;
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm)
-        if (mm == m) tot = (s_red[mm][0] + s_red[mm][1]) + (s_red[mm][2] + s_red[mm][3]);
-      const float rs = rsqrtf(tot / static_cast<float>(K) + p.eps);
-      float4 v = *reinterpret_cast<const float4*>(s_u + i);
-      const float4 w = *reinterpret_cast<const float4*>(s_nw + (i - m * K));
-      v = make_float4(rnd<T>(w.x * rnd<T>(v.x * rs)), rnd<T>(w.y * rnd<T>(v.y * rs)),
-                      rnd<T>(w.z * rnd<T>(v.z * rs)), rnd<T>(w.w * rnd<T>(v.w * rs)));
-      *reinterpret_cast<float4*>(s_u + i) = v;
-    }
-    __syncthreads();
-  }
+  rows.normalize(s_u, s_nw, s_red, p.eps);
   if (nrows > 0) {
     float acc[RW][MT];
     rows_dot<T, MT, RW>(acc, tiles, s_u, p.in_w, row0, nout - 1, K);
@@ -599,6 +655,63 @@ __global__ void __launch_bounds__(kSsmThreads) block_ssm_kernel(const MixerParam
   }
 }
 
+// Final RMSNorm and a wide product for a handful of rows (a decode step's
+// norm_f + lm_head): out[m][n] = round_T(sum_k u[m][k] W[n][k] + bias[n])
+// with u the normalised rows (RowStage, rows as given). Persistent: each of
+// gridDim.x workgroups stages and normalises the rows once, then walks the
+// row groups g = blockIdx.x, blockIdx.x + gridDim.x, ... (RW rows per wave,
+// 4 RW per group), requesting the next group's weights and bias before it
+// multiplies the current one, so a workgroup keeps one group in flight
+// while it computes. The request for a group past the end reads the last
+// group again (unconditional: a conditional request would make the wait
+// for the current group cover it too).
+template <typename T, int MT, int RW, int KC, bool HF>
+__global__ void __launch_bounds__(kThreads) norm_linear_kernel(const NormLinearParams p) {
+  extern __shared__ __align__(16) float s_u[];   // (MT, K) rows, then the norm weight
+  __shared__ float s_red[MT][kThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = p.K;
+  const int64_t last = p.nout - 1;
+  const T* bl = static_cast<const T*>(p.bias ? p.bias : p.w);
+  auto row_of = [&](int64_t g) { return (g * (kThreads / 64) + wave) * RW; };
+  RowStage<T, MT, HF, false> rows(p.x, p.nw, p.batch, K);
+  rows.issue(p.w);
+  __builtin_amdgcn_sched_barrier(0);
+  rows.stage(s_u);
+  __builtin_amdgcn_sched_barrier(0);
+  rows.finish(s_u + MT * K, s_red);
+  int64_t g = blockIdx.x;
+  RowTiles<T, RW, KC> cur, nxt;
+  uint32_t eb[RW], ebn[RW];
+  cur.load(p.w, row_of(g), last, K, 0);
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) eb[rr] = ld_bits(bl, min(row_of(g) + rr, last));
+  __builtin_amdgcn_sched_barrier(0);
+  rows.normalize(s_u, s_u + MT * K, s_red, p.eps);
+  for (; g < p.ngroups; g += gridDim.x) {
+    const int64_t gn = min(g + static_cast<int64_t>(gridDim.x), p.ngroups - 1);
+    nxt.load(p.w, row_of(gn), last, K, 0);
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) ebn[rr] = ld_bits(bl, min(row_of(gn) + rr, last));
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t row0 = row_of(g);
+    float acc[RW][MT];
+    rows_dot<T, MT, RW, KC>(acc, cur, s_u, p.w, row0, last, K);
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int64_t n = row0 + rr;
+      float y = pick_lane<MT>(acc[rr], lane);
+      if (n > last || lane >= p.batch) continue;
+      y = rnd<T>(p.bias ? y + bits_f32<T>(eb[rr]) : y);
+      if (p.out_f32) static_cast<float*>(p.out)[lane * p.nout + n] = y;
+      else st<T>(p.out, lane * p.nout + n, y);
+    }
+    cur = nxt;
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) eb[rr] = ebn[rr];
+  }
+}
+
 namespace {
 
 // Rows per wave: as many as keep at least 256 workgroups.
@@ -834,4 +947,84 @@ extern "C" int mcpu_mixer_step(const mcpu_mixer_step_args* a, void* workspace, s
     default: e = step_dtype<f16>(p, st); break;
   }
   return hip_status(e, "mixer_step launch");
+}
+
+namespace mcpu {
+namespace {
+
+constexpr int kNormLinearRW = 2;
+constexpr int64_t kNormLinearGrid = 1024;   // 4 workgroups per CU on 256 CUs
+
+template <typename T, int MT, int KC>
+void launch_norm_linear(const NormLinearParams& p, bool hf, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(p.ngroups < kNormLinearGrid ? p.ngroups : kNormLinearGrid));
+  const size_t lds = sizeof(float) * (MT + 1) * p.K;
+  if (hf || std::is_same_v<T, float>)
+    hipLaunchKernelGGL((norm_linear_kernel<T, MT, kNormLinearRW, KC, true>), grid, dim3(kThreads), lds, st, p);
+  else
+    hipLaunchKernelGGL((norm_linear_kernel<T, MT, kNormLinearRW, KC, false>), grid, dim3(kThreads), lds, st, p);
+}
+
+template <typename T, int MT>
+void norm_linear_mt(const NormLinearParams& p, bool hf, hipStream_t st) {
+  if (p.K <= 256 * 4) launch_norm_linear<T, MT, 4>(p, hf, st);
+  else launch_norm_linear<T, MT, kChunks>(p, hf, st);
+}
+
+template <typename T>
+void norm_linear_t(const NormLinearParams& p, bool hf, hipStream_t st) {
+  if (p.batch <= 1) norm_linear_mt<T, 1>(p, hf, st);
+  else if (p.batch <= 2) norm_linear_mt<T, 2>(p, hf, st);
+  else if (p.batch <= 4) norm_linear_mt<T, 4>(p, hf, st);
+  else norm_linear_mt<T, 8>(p, hf, st);
+}
+
+int check_norm_linear(const mcpu_norm_linear_args* a) {
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "norm_linear: null argument block");
+  if (a->hidden == nullptr || a->weight == nullptr || a->out == nullptr)
+    return fail(MCPU_ERR_INVALID, "norm_linear: hidden, weight and out are required");
+  if (a->batch < 1 || a->d_in < 4 || a->d_out < 1) return fail(MCPU_ERR_INVALID, "norm_linear: bad sizes");
+  if (a->batch > kMaxBatch)
+    return fail(MCPU_ERR_UNSUPPORTED, "norm_linear: batch %lld > %d", (long long)a->batch, kMaxBatch);
+  if (a->d_in % 4 != 0) return fail(MCPU_ERR_UNSUPPORTED, "norm_linear: d_in must be a multiple of 4");
+  if ((pow2_batch(a->batch) + 1) * a->d_in > kMaxLdsFloats)
+    return fail(MCPU_ERR_UNSUPPORTED, "norm_linear: batch x d_in too large for one workgroup's LDS");
+  if (!valid_dtype(a->dtype) || (a->hidden_dtype != a->dtype && a->hidden_dtype != MCPU_F32) ||
+      (a->out_dtype != a->dtype && a->out_dtype != MCPU_F32))
+    return fail(MCPU_ERR_INVALID, "norm_linear: bad dtype");
+  if (a->norm_eps < 0.f) return fail(MCPU_ERR_INVALID, "norm_linear: norm_eps < 0");
+  for (const void* t : {a->hidden, a->weight, a->norm_weight})
+    if (reinterpret_cast<uintptr_t>(t) % 16 != 0)
+      return fail(MCPU_ERR_INVALID, "norm_linear: hidden, weight and norm_weight must be 16-byte aligned");
+  return MCPU_OK;
+}
+
+}  // namespace
+}  // namespace mcpu
+
+extern "C" int mcpu_norm_linear(const mcpu_norm_linear_args* a, void* stream) {
+  clear_error();
+  if (int rc = check_norm_linear(a)) return rc;
+  if (int rc = mcpu_check_device()) return rc;
+  NormLinearParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.x = a->hidden;
+  p.nw = a->norm_weight;
+  p.w = a->weight;
+  p.bias = a->bias;
+  p.out = a->out;
+  p.batch = a->batch;
+  p.nout = a->d_out;
+  p.ngroups = (a->d_out + 4 * kNormLinearRW - 1) / (4 * kNormLinearRW);
+  p.K = static_cast<int>(a->d_in);
+  p.out_f32 = a->out_dtype == MCPU_F32;
+  p.eps = a->norm_eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool hf = a->hidden_dtype == MCPU_F32;
+  switch (a->dtype) {
+    case MCPU_F32: norm_linear_t<float>(p, hf, st); break;
+    case MCPU_BF16: norm_linear_t<bf16>(p, hf, st); break;
+    default: norm_linear_t<f16>(p, hf, st); break;
+  }
+  return hip_status(hipGetLastError(), "norm_linear launch");
 }

@@ -1349,6 +1349,47 @@ Tensor mixer_step(const Tensor& hidden, const optional<Tensor>& norm_weight, dou
   return out;
 }
 
+// Final norm and output head of a decode step (mcpu_norm_linear): hidden
+// (batch, d_in) in the weights' dtype or float32 -> Linear(RMSNorm(hidden))
+// (batch, d_out), float32 when out_float32, else the weights' dtype.
+Tensor norm_linear(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, const Tensor& weight,
+                   const optional<Tensor>& bias, bool out_float32) {
+  const char* name = "mamba_cpu::norm_linear";
+  for (const optional<Tensor>& t : {opt(hidden), norm_weight, opt(weight), bias}) check_gpu(name, t);
+  const auto T = weight.scalar_type();
+  TORCH_CHECK_VALUE(x_dtype(T), name, " expects float32, bfloat16 or float16 weights");
+  for (const optional<Tensor>& t : {norm_weight, opt(weight), bias})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == T && t->is_contiguous()), name,
+                      " expects contiguous weight, bias and norm weight of one dtype");
+  TORCH_CHECK_VALUE(hidden.dim() == 2 && hidden.is_contiguous() &&
+                        (hidden.scalar_type() == T || hidden.scalar_type() == at::kFloat),
+                    name, " expects a contiguous hidden (batch, d_in) in the weights' dtype or float32");
+  const int64_t b = hidden.size(0), din = hidden.size(1);
+  TORCH_CHECK_VALUE(weight.dim() == 2 && weight.size(1) == din, name, " expects weight (d_out, d_in)");
+  const int64_t dout = weight.size(0);
+  TORCH_CHECK_VALUE((!has(norm_weight) || norm_weight->numel() == din) && (!has(bias) || bias->numel() == dout),
+                    name, " expects norm weight (d_in) and bias (d_out)");
+  c10::DeviceGuard guard(hidden.device());
+  Tensor out = at::empty({b, dout}, hidden.options().dtype(out_float32 ? at::kFloat : T));
+  if (b == 0 || dout == 0) return out;
+  mcpu_norm_linear_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.hidden = hidden.data_ptr();
+  a.norm_weight = ptr(norm_weight);
+  a.weight = weight.data_ptr();
+  a.bias = ptr(bias);
+  a.out = out.data_ptr();
+  a.batch = b;
+  a.d_in = din;
+  a.d_out = dout;
+  a.norm_eps = static_cast<float>(eps);
+  a.dtype = dtype_tag(T);
+  a.hidden_dtype = dtype_tag(hidden.scalar_type());
+  a.out_dtype = dtype_tag(out.scalar_type());
+  check_rc(mcpu_norm_linear(&a, stream_of(hidden)), name);
+  return out;
+}
+
 Tensor mixer_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, bool add_residual,
                           bool residual_in_fp32, const Tensor& in_w, const optional<Tensor>& in_b,
                           const Tensor& conv_w, const optional<Tensor>& conv_b, Tensor& conv_state,
@@ -1422,6 +1463,8 @@ TORCH_LIBRARY(mamba_cpu, m) {
         "Tensor in_w, Tensor? in_b, Tensor conv_w, Tensor? conv_b, Tensor(a!) conv_state, Tensor x_w, "
         "Tensor dt_w, Tensor? dt_b, Tensor A, Tensor? D, Tensor(b!) ssm_state, Tensor out_w, "
         "Tensor? out_b) -> Tensor");
+  m.def("norm_linear(Tensor hidden, Tensor? norm_weight, float eps, Tensor weight, Tensor? bias, "
+        "bool out_float32) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
@@ -1442,6 +1485,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("ssd_bwd", &ssd_bwd);
   m.impl("ssd_varlen_states", &ssd_varlen_states);
   m.impl("mixer_step", &mixer_step);
+  m.impl("norm_linear", &norm_linear);
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
@@ -1451,6 +1495,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
   m.impl("causal_conv1d_fwd", &causal_conv1d_fwd_autograd);
   // One decode step: no gradient flows through it.
   m.impl("mixer_step", torch::CppFunction::makeFallthrough());
+  m.impl("norm_linear", torch::CppFunction::makeFallthrough());
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, ADInplaceOrView, m) {

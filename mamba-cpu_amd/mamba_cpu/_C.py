@@ -130,9 +130,18 @@ class MixerStepArgs(ctypes.Structure):
     ]
 
 
-_ARGP = {n: ctypes.POINTER(c) for n, c in
-         (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-          ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs))}
+class NormLinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _P), ("norm_weight", _P), ("weight", _P), ("bias", _P), ("out", _P),
+        ("batch", _I64), ("d_in", _I64), ("d_out", _I64),
+        ("norm_eps", ctypes.c_float), ("dtype", _I32), ("hidden_dtype", _I32), ("out_dtype", _I32),
+    ]
+
+
+_BLOCKS = (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
+           ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs),
+           ("norm_linear", NormLinearArgs))
+_ARGP = {n: ctypes.POINTER(c) for n, c in _BLOCKS}
 
 lib.mcpu_last_error.restype = ctypes.c_char_p
 lib.mcpu_version.restype = ctypes.c_char_p
@@ -175,9 +184,10 @@ lib.mcpu_mixer_step_workspace_size.argtypes = [_ARGP["mixer_step"]]
 lib.mcpu_mixer_step_workspace_size.restype = ctypes.c_size_t
 lib.mcpu_mixer_step.argtypes = [_ARGP["mixer_step"], _P, ctypes.c_size_t, _P]
 lib.mcpu_mixer_step.restype = ctypes.c_int
+lib.mcpu_norm_linear.argtypes = [_ARGP["norm_linear"], _P]
+lib.mcpu_norm_linear.restype = ctypes.c_int
 
-for _name, _cls in (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
-                    ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs)):
+for _name, _cls in _BLOCKS:
     _want = lib.mcpu_args_size(_name.encode())
     if _want != ctypes.sizeof(_cls):
         raise ImportError(f"mamba_cpu: {_name} argument block is {ctypes.sizeof(_cls)} bytes here "

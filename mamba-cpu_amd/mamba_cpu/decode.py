@@ -18,9 +18,10 @@ For Mamba (not FalconMamba, whose mixer normalises dt, B and C) the captured
 step runs each block as one fused operator, mamba_cpu::mixer_step: RMSNorm,
 in_proj, conv update, x_proj, dt_proj, state update, out_proj and the
 residual in three kernels, with the small-batch products as matrix-vector
-kernels that read each weight once. It computes what the block computes;
-the products sum in another order than the GEMM library's, so logits agree
-to float32 rounding and greedy tokens match `model.generate`'s. FalconMamba
+kernels that read each weight once, and the final norm and lm_head as one
+more, mamba_cpu::norm_linear. It computes what the model computes; the
+products sum in another order than the GEMM library's, so logits agree to
+float32 rounding and greedy tokens match `model.generate`'s. FalconMamba
 and Mamba-2 models replay their own decode step (on this package's conv
 update and state update once mamba_cpu.hf is patched).
 """
@@ -45,6 +46,11 @@ def _fused_lds_fits(batch_size, d_model, d_inner):
     LDS, as check_step requires."""
     rows = 1 if batch_size <= 1 else 2 if batch_size <= 2 else 4 if batch_size <= 4 else 8
     return (rows + 1) * d_model <= _FUSED_LDS_FLOATS and rows * d_inner <= _FUSED_LDS_FLOATS
+
+
+@torch.library.register_fake("mamba_cpu::norm_linear")
+def _(hidden, norm_weight, eps, weight, bias, out_float32):
+    return hidden.new_empty((hidden.shape[0], weight.shape[0]), dtype=torch.float32 if out_float32 else weight.dtype)
 
 
 @torch.library.register_fake("mamba_cpu::mixer_step")
@@ -116,6 +122,19 @@ def fused_block_step(block, hidden, cache):
         mx.dt_proj.weight, dtb, A, D, layer.recurrent_states[0], mx.out_proj.weight, mx.out_proj.bias)
 
 
+def fused_head_supported(model, batch_size):
+    """Whether a Mamba model's final norm and lm_head can run as one
+    mamba_cpu::norm_linear launch (mcpu_norm_linear's limits: at most 8 rows,
+    a width that is a multiple of 4 and fits the LDS budget, one dtype)."""
+    norm, head = model.backbone.norm_f, model.lm_head
+    w = head.weight
+    rows = 1 if batch_size <= 1 else 2 if batch_size <= 2 else 4 if batch_size <= 4 else 8
+    return (batch_size <= _MAX_FUSED_BATCH and w.device.type == "cuda" and w.is_contiguous()
+            and w.shape[1] % 4 == 0 and (rows + 1) * w.shape[1] <= _FUSED_LDS_FLOATS
+            and norm.weight.dtype == w.dtype and norm.weight.is_contiguous()
+            and (head.bias is None or (head.bias.dtype == w.dtype and head.bias.is_contiguous())))
+
+
 def fused_model_step(model, token, cache):
     """A transformers MambaForCausalLM decode step with fused blocks: token
     (batch, 1) -> last-position logits (batch, vocab) float32, the cache
@@ -124,6 +143,10 @@ def fused_model_step(model, token, cache):
     h = bb.embeddings(token)[:, 0]
     for blk in bb.layers:
         h = fused_block_step(blk, h, cache)
+    if fused_head_supported(model, h.shape[0]):
+        head = model.lm_head
+        return torch.ops.mamba_cpu.norm_linear(h, bb.norm_f.weight, float(bb.norm_f.variance_epsilon),
+                                               head.weight, head.bias, True)
     h = bb.norm_f(h)
     return model.lm_head(h.to(model.lm_head.weight.dtype)).float()
 

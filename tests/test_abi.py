@@ -60,7 +60,8 @@ def test_argument_blocks_match_the_library():
 
     for name, cls in (("scan", _C.ScanArgs), ("conv", _C.ConvArgs),
                       ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs),
-                      ("ssd", _C.SsdArgs), ("mixer_step", _C.MixerStepArgs)):
+                      ("ssd", _C.SsdArgs), ("mixer_step", _C.MixerStepArgs),
+                      ("norm_linear", _C.NormLinearArgs)):
         assert _C.lib.mcpu_args_size(name.encode()) == ctypes.sizeof(cls)
     assert _C.lib.mcpu_args_size(b"nonsense") == 0
 
@@ -86,7 +87,8 @@ def _header_field_names(struct):
                                              ("mcpu_conv_update_args", "ConvUpdateArgs"),
                                              ("mcpu_state_update_args", "StateUpdateArgs"),
                                              ("mcpu_ssd_args", "SsdArgs"),
-                                             ("mcpu_mixer_step_args", "MixerStepArgs")])
+                                             ("mcpu_mixer_step_args", "MixerStepArgs"),
+                                             ("mcpu_norm_linear_args", "NormLinearArgs")])
 def test_argument_block_fields_follow_the_header(struct, cls_name):
     from mamba_cpu import _C
 
@@ -603,3 +605,34 @@ def test_mixer_step_workspace_holds_the_step_vectors():
     assert size() == 3 * al(4 * 4 * 1536) + al(4 * 4 * 80 * 192)
     assert size(batch=2, d_model=2560, d_inner=5120, dt_rank=160) == 3 * al(2 * 4 * 5120) + al(2 * 4 * 192)
     assert size(batch=9) == 0
+
+
+def _head_args(**kw):
+    from mamba_cpu import _C
+
+    a = _C.NormLinearArgs()
+    for f in ("hidden", "weight", "out"):
+        setattr(a, f, 256)  # non-NULL placeholders: never dereferenced
+    a.batch, a.d_in, a.d_out, a.norm_eps = 4, 768, 50280, 1e-5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_norm_linear_rejects_bad_arguments_before_touching_a_device():
+    from mamba_cpu import _C
+
+    L = _C.lib
+    call = lambda a: _rc(L.mcpu_norm_linear, ctypes.byref(a), None)  # noqa: E731
+    assert _rc(L.mcpu_norm_linear, None, None)[0] == _C.MCPU_ERR_INVALID
+    for kw, code, word in ((dict(weight=None), _C.MCPU_ERR_INVALID, "required"),
+                           (dict(batch=0), _C.MCPU_ERR_INVALID, "sizes"),
+                           (dict(batch=9), _C.MCPU_ERR_UNSUPPORTED, "batch"),
+                           (dict(d_in=770), _C.MCPU_ERR_UNSUPPORTED, "multiple of 4"),
+                           (dict(batch=8, d_in=4096), _C.MCPU_ERR_UNSUPPORTED, "LDS"),
+                           (dict(dtype=_C.MCPU_BF16, hidden_dtype=_C.MCPU_F16), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(out_dtype=9), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(norm_eps=-1.0), _C.MCPU_ERR_INVALID, "norm_eps"),
+                           (dict(norm_weight=264), _C.MCPU_ERR_INVALID, "aligned")):
+        rc, msg = call(_head_args(**kw))
+        assert rc == code and word in msg, (kw, rc, msg)

@@ -19,8 +19,14 @@ mamba_cpu.decode) against transformers' own decode step.
   in_proj workgroups (32, 768 and 1024, the last with 4 in_proj rows per
   wave) and, at the Mamba-2.8B width (d_inner 5120, dt_rank 160), as its own
   product;
+- the final norm and lm_head as one launch (mamba_cpu::norm_linear) against
+  transformers' MambaRMSNorm and nn.Linear on the GPU: float32 (rtol 1e-5,
+  atol 1e-5 of the largest logit) and bfloat16 weights with float32 or
+  bfloat16 rows (results rounded to bfloat16: rtol 1e-2, atol 1e-2 of the
+  largest), widths 32 to 2560 (one and two passes over d_in), batch 1 to 8,
+  with and without norm weight and bias, at the 50280-word vocabulary;
 - the captured graph against eager fused steps, bitwise, and the torch.library
-  opcheck of the operator.
+  opcheck of both operators.
 """
 
 import copy
@@ -154,3 +160,41 @@ def test_opcheck_mixer_step():
             layer.conv_states[0], mx.x_proj.weight.detach(), mx.dt_proj.weight.detach(), dtb, A, D,
             layer.recurrent_states[0], mx.out_proj.weight.detach(), None)
     torch.library.opcheck(torch.ops.mamba_cpu.mixer_step.default, args)
+
+
+@pytest.mark.parametrize("dtype,hdtype,batch,d_in,d_out,norm,bias", [
+    (torch.float32, torch.float32, 4, 768, 50280, True, False),
+    (torch.float32, torch.float32, 1, 1536, 1000, True, True),
+    (torch.float32, torch.float32, 8, 2560, 333, True, False),
+    (torch.float32, torch.float32, 3, 32, 64, False, True),
+    (torch.bfloat16, torch.float32, 4, 768, 50280, True, False),
+    (torch.bfloat16, torch.bfloat16, 2, 1024, 777, True, True),
+    (torch.bfloat16, torch.bfloat16, 5, 768, 129, False, False),
+], ids=["f32-768-vocab", "f32-1536-bias", "f32-2560-b8", "f32-nonorm", "bf16-f32rows-vocab", "bf16-bf16rows",
+        "bf16-nonorm"])
+@torch.no_grad()
+def test_norm_linear_matches_norm_and_head(dtype, hdtype, batch, d_in, d_out, norm, bias):
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    h = (torch.randn(batch, d_in, generator=gen, device=DEV) * 3).to(hdtype)
+    norm_f = transformers.models.mamba.modeling_mamba.MambaRMSNorm(d_in, eps=1e-5).to(DEV, dtype)
+    norm_f.weight.copy_(1 + 0.1 * torch.randn(d_in, generator=gen, device=DEV))
+    head = torch.nn.Linear(d_in, d_out, bias=bias).to(DEV, dtype)
+    head.weight.copy_(torch.randn(d_out, d_in, generator=gen, device=DEV) * 0.05)
+    if bias:
+        head.bias.copy_(torch.randn(d_out, generator=gen, device=DEV))
+    got = torch.ops.mamba_cpu.norm_linear(h, norm_f.weight if norm else None, 1e-5, head.weight, head.bias, True)
+    u = norm_f(h) if norm else h
+    want = head(u.to(dtype)).float()
+    assert got.dtype == torch.float32 and got.shape == want.shape
+    scale = want.abs().max().item()
+    tol = (1e-5, 1e-5 * scale) if dtype == torch.float32 else (1e-2, 1e-2 * scale)
+    assert_close_report(got, want, *tol, "logits")
+    low = torch.ops.mamba_cpu.norm_linear(h, norm_f.weight if norm else None, 1e-5, head.weight, head.bias, False)
+    assert low.dtype == dtype and torch.equal(low.float(), got)
+
+
+def test_opcheck_norm_linear():
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    args = (torch.randn(3, 32, generator=gen, device=DEV), torch.rand(32, generator=gen, device=DEV) + 0.5, 1e-5,
+            torch.randn(70, 32, generator=gen, device=DEV), None, True)
+    torch.library.opcheck(torch.ops.mamba_cpu.norm_linear.default, args)
