@@ -161,9 +161,10 @@ int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t wor
                             void* stream);
 
 /* Bytes of the per-device scratch array behind mcpu_selective_scan_bwd_noalloc.
- * The array is a file-scope __device__ object: every device the library's code
- * object is loaded on reserves it (in any process that uses any entry point
- * there) until the process ends, whether or not this entry point is called. */
+ * The array is a file-scope __device__ object in a code object of its own: a
+ * device reserves it (with that code object, 68 MiB measured) when the first
+ * mcpu_selective_scan_bwd_noalloc call on it looks up the array's address, and
+ * holds it until the process ends. Other entry points never reserve it. */
 #define MCPU_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* Backward that allocates nothing and takes no workspace. No counterpart in
@@ -171,8 +172,8 @@ int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t wor
  * under HIP graph capture, serving loops that forbid allocation). It runs
  * the kernels of mcpu_selective_scan_bwd with their scratch (partial sums,
  * chunk summaries, and block checkpoints when ckpt is NULL) in a fixed
- * library array of MCPU_NOALLOC_SCRATCH_BYTES per device (reserved wherever
- * the library is loaded, see above). Results equal
+ * library array of MCPU_NOALLOC_SCRATCH_BYTES per device (reserved by the
+ * first call on each device, see above). Results equal
  * mcpu_selective_scan_bwd's. Returns MCPU_ERR_UNSUPPORTED, before any device
  * work, when mcpu_selective_scan_bwd_workspace_size(a) exceeds the array
  * (the training-step shape batch 8, dim 1536, seqlen 1024, dstate 16 needs

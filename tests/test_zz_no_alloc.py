@@ -8,6 +8,12 @@ dstate 16, with the forward's checkpoints and saved y), then a smaller,
 time-chunked one (batch 1, dim 48, seqlen 4000, no checkpoints, so the
 array also holds them), then the first again over the second's leftovers.
 Shapes whose scratch exceeds the array are refused before any device work.
+
+The array lives in a code object of its own, loaded when the first call on
+a device looks up its address: this file's first test measures the device's
+free memory around the first and second calls (64 MiB and more taken by the
+first, nothing by the second), so it runs before any other noalloc call in
+the process.
 """
 
 import ctypes
@@ -36,6 +42,34 @@ def case(batch, dim, seqlen, seed):
     dlast = torch.randn(batch, dim, 16, generator=g).to(dev)
     args = (u, delta, A, B[:, None].transpose(-1, -2), C[:, None].transpose(-1, -2), D, z, bias, True)
     return args, (B, C), dout, dlast
+
+
+SCRATCH_BYTES = 64 << 20  # MCPU_NOALLOC_SCRATCH_BYTES in include/mamba_hip.h
+
+
+@pytest.mark.gpu
+def test_first_call_reserves_the_array():
+    from mamba_cpu import _C
+    from scan_abi import bwd as abi_bwd
+
+    noalloc = _C.lib.mcpu_selective_scan_bwd_noalloc
+    taken = []
+
+    def entry(a, stream):
+        torch.cuda.synchronize()
+        before = torch.cuda.mem_get_info()[0]
+        rc = noalloc(a, stream)
+        torch.cuda.synchronize()
+        taken.append(before - torch.cuda.mem_get_info()[0])
+        return rc
+
+    entry.__name__ = "mcpu_selective_scan_bwd_noalloc"
+    args, _, dout, dlast = case(1, 64, 100, 3)
+    for _ in range(2):
+        abi_bwd(*args, dout, dlast, None, None, entry=entry)
+    print(f"free device memory taken: first call {taken[0] / 2**20:.1f} MiB, second {taken[1] / 2**20:.1f} MiB")
+    assert taken[0] >= SCRATCH_BYTES
+    assert taken[1] == 0
 
 
 @pytest.mark.gpu
