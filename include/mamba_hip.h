@@ -162,7 +162,7 @@ int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t wor
 
 /* Bytes of the per-device scratch array behind mcpu_selective_scan_bwd_noalloc.
  * The array is a file-scope __device__ object in a code object of its own: a
- * device reserves it (with that code object, 68 MiB measured) when the first
+ * device reserves it (with that code object, about 66 MiB measured) when the first
  * mcpu_selective_scan_bwd_noalloc call on it looks up the array's address, and
  * holds it until the process ends. Other entry points never reserve it. */
 #define MCPU_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)

@@ -16,6 +16,7 @@ hipError_t scan_fwd_launch(const ScanParams& p, int dtype, bool write_out, hipSt
 hipError_t scan_bwd_launch(const ScanParams& p, int dtype, int waves, hipStream_t stream);
 hipError_t scan_bwd_summary_launch(const ScanParams& p, int dtype, hipStream_t stream);
 hipError_t scan_bwd_finish_launch(const ScanParams& p, int dtype, hipStream_t stream);
+hipError_t scan_fwd_finish_launch(const ScanParams& p, int dtype, hipStream_t stream);
 int scan_complex_waves();
 hipError_t scan_cfwd_launch(const ScanParams& p, int dtype, bool write_out, hipStream_t stream);
 hipError_t scan_cbwd_launch(const ScanParams& p, int dtype, hipStream_t stream);
@@ -30,19 +31,22 @@ namespace {
 // State slices: above kSliceAbove states (what one lane group of the kernels
 // holds in registers) the states are cut into slices that the grid scans side
 // by side: 64 states per forward slice (four per lane), 16 per backward slice
-// (the backward's fastest form). Up to kMaxSlicedDstate states.
+// (the backward's fastest form). With complex A, whose (re, im) states take
+// twice the registers, above kCSlice states in slices of kCSlice, forward and
+// backward. Up to kMaxSlicedDstate states.
 constexpr int64_t kSliceAbove = 64;
 constexpr int64_t kFwdSlice = 64;
 constexpr int64_t kBwdSlice = 16;
+constexpr int64_t kCSlice = 32;
 constexpr int64_t kMaxSlicedDstate = 4096;
 
-int64_t slices_of(int64_t dstate, int64_t slice) {
-  return dstate > kSliceAbove ? (dstate + slice - 1) / slice : 1;
+int64_t slices_of(int64_t dstate, int64_t slice, int64_t above = kSliceAbove) {
+  return dstate > above ? (dstate + slice - 1) / slice : 1;
 }
 
 // Cuts p (made for all states) into slices of `slice` states when sliced.
-void slice_params(ScanParams& p, int64_t slice) {
-  const int64_t ns = slices_of(p.ntotal, slice);
+void slice_params(ScanParams& p, int64_t slice, int64_t above = kSliceAbove) {
+  const int64_t ns = slices_of(p.ntotal, slice, above);
   if (ns > 1) {
     p.dstate = slice;
     p.nslices = ns;
@@ -69,17 +73,17 @@ int check_scan(const mcpu_scan_args* a) {
   if (a->ngroups < 1 || (a->dim > 0 && a->dim % a->ngroups != 0))
     return fail(MCPU_ERR_INVALID, "selective_scan: dim (%lld) must be divisible by ngroups (%lld)",
                 (long long)a->dim, (long long)a->ngroups);
-  const int64_t max_dstate = a->complex_a ? 32 : kMaxSlicedDstate;
-  if (a->dstate < 1 || a->dstate > max_dstate)
-    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, %lld]%s, got %lld",
-                (long long)max_dstate, a->complex_a ? " with complex A" : "", (long long)a->dstate);
+  if (a->dstate < 1 || a->dstate > kMaxSlicedDstate)
+    return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: dstate must be in [1, %lld], got %lld",
+                (long long)kMaxSlicedDstate, (long long)a->dstate);
   if (!valid_dtype(a->dtype)) return fail(MCPU_ERR_INVALID, "selective_scan: bad dtype %d", a->dtype);
   if (a->bwd_waves != 0 &&
       (a->complex_a || a->dstate > 16 || (a->bwd_waves != 4 && a->bwd_waves != 8 && a->bwd_waves != 12)))
     return fail(MCPU_ERR_INVALID, "selective_scan: bwd_waves must be 0, or 4, 8 or 12 with real A "
                 "and dstate <= 16, got %d", a->bwd_waves);
   const int64_t dpg = a->dim / a->ngroups;
-  const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16) * slices_of(a->dstate, kBwdSlice);
+  const int64_t blocks = a->batch * a->ngroups * ((dpg + 15) / 16) *
+                        (a->complex_a ? slices_of(a->dstate, kCSlice, kCSlice) : slices_of(a->dstate, kBwdSlice));
   if (blocks > 0x7fffffffll) return fail(MCPU_ERR_UNSUPPORTED, "selective_scan: grid too large");
   for (int i = 0; i < 3; ++i)
     if (a->u_stride[i] < 0 || a->delta_stride[i] < 0 || a->z_stride[i] < 0 || a->dout_stride[i] < 0 ||
@@ -299,14 +303,28 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
   return w;
 }
 
-// Complex A: one time chunk, 4-wave workgroups, states as (re, im) pairs.
+// Complex A: one time chunk, 4-wave workgroups, states as (re, im) pairs;
+// above kCSlice states, kCSlice-state slices (the forward's shares of y and
+// the backward's shares of its two state sums go through the workspace and
+// the real scan's finish kernels).
+ScanParams cparams(const mcpu_scan_args* a) {
+  ScanParams p = make_params(a, scan_complex_waves());
+  slice_params(p, kCSlice, kCSlice);
+  return p;
+}
+
+// A sliced complex forward's workspace: the slices' shares of y.
+size_t cfwd_bytes(const ScanParams& p, bool write_out) {
+  return p.nslices > 1 && write_out ? align_up(sizeof(float) * p.nslices * p.batch * p.dim * p.seqlen) : 0;
+}
+
 struct CBwdLayout {
-  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, total = 0;
-  bool own_ckpt = false, part_bc = false, part_dA = false;
+  size_t ckpt = 0, dB = 0, dC = 0, dA = 0, dD = 0, dbias = 0, rpart = 0, ysave = 0, fwd = 0, total = 0;
+  bool own_ckpt = false, part_bc = false, part_dA = false, sliced = false, own_ysave = false;
 };
 
 CBwdLayout cbwd_layout(const mcpu_scan_args* a) {
-  const ScanParams p = make_params(a, scan_complex_waves());
+  const ScanParams p = cparams(a);
   CBwdLayout w;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -315,28 +333,60 @@ CBwdLayout cbwd_layout(const mcpu_scan_args* a) {
     return at;
   };
   w.own_ckpt = a->ckpt == nullptr;
-  if (w.own_ckpt) w.ckpt = take(sizeof(float) * 2 * p.batch * p.dim * p.nblk * p.dstate);
+  if (w.own_ckpt) w.ckpt = take(sizeof(float) * 2 * p.batch * p.dim * p.nblk * p.ntotal);
   w.part_bc = p.nblk_c > 1;
   if (w.part_bc) {
-    const size_t bc = sizeof(float) * 2 * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.dstate;
+    const size_t bc = sizeof(float) * 2 * p.batch * p.ngroups * p.nblk_c * p.seqlen * p.ntotal;
     w.dB = take(bc);
     w.dC = take(bc);
   }
   w.part_dA = p.batch > 1;
-  if (w.part_dA) w.dA = take(sizeof(float) * 2 * p.batch * p.dim * p.dstate);
+  if (w.part_dA) w.dA = take(sizeof(float) * 2 * p.batch * p.dim * p.ntotal);
   w.dD = take(sizeof(float) * p.batch * p.dim);
   w.dbias = take(sizeof(float) * p.batch * p.dim);
+  w.sliced = p.nslices > 1;
+  if (w.sliced) {
+    w.rpart = take(sizeof(float) * 2 * p.nslices * p.batch * p.dim * p.seqlen);
+    // y before the gate for dz: the caller's (with its checkpoints) or made here
+    w.own_ysave = a->z != nullptr && (a->ckpt == nullptr || a->ysave == nullptr);
+    if (w.own_ysave) {
+      w.ysave = take(dtype_size(a->dtype) * p.batch * p.dim * p.seqlen);
+      w.fwd = take(cfwd_bytes(p, true));
+    }
+  }
   w.total = off;
   return w;
 }
 
-int complex_fwd(const mcpu_scan_args* a, hipStream_t st) {
-  ScanParams p = make_params(a, scan_complex_waves());
+// The forward: scan_cfwd_kernel, and for a sliced one writing outputs its
+// slices' shares of y (workspace) and then scan_fwd_finish_kernel.
+int complex_fwd_run(ScanParams p, bool write_out, float* ypart, int dtype, hipStream_t st, const char* what) {
+  if (p.nslices > 1 && write_out) {
+    ScanParams ps = p;
+    ps.ypart = ypart;
+    ps.D = nullptr;
+    ps.z = nullptr;
+    ps.ysave = nullptr;
+    if (int rc = hip_status(scan_cfwd_launch(ps, dtype, true, st), what)) return rc;
+    p.ypart = ypart;
+    return hip_status(scan_fwd_finish_launch(p, dtype, st), what);
+  }
+  return hip_status(scan_cfwd_launch(p, dtype, write_out, st), what);
+}
+
+int complex_fwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  ScanParams p = cparams(a);
   p.out = a->out;
   p.last_state = a->last_state;
   p.ckpt = a->ckpt;
+  p.ysave = a->out != nullptr ? a->ysave : nullptr;
   if (p.out == nullptr && p.last_state == nullptr && p.ckpt == nullptr) return MCPU_OK;
-  return hip_status(scan_cfwd_launch(p, a->dtype, a->out != nullptr, st), "selective_scan_fwd launch");
+  const size_t need = cfwd_bytes(p, a->out != nullptr);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(MCPU_ERR_INVALID, "selective_scan_fwd: complex dstate %lld needs a workspace of %zu bytes, got %zu",
+                (long long)a->dstate, need, workspace_bytes);
+  return complex_fwd_run(p, a->out != nullptr, static_cast<float*>(workspace), a->dtype, st,
+                         "selective_scan_fwd launch");
 }
 
 int complex_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes, hipStream_t st) {
@@ -354,11 +404,16 @@ int complex_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes
     return MCPU_OK;
   }
   char* ws = static_cast<char*>(workspace);
-  ScanParams p = make_params(a, scan_complex_waves());
+  ScanParams p = cparams(a);
   p.ckpt = w.own_ckpt ? reinterpret_cast<float*>(ws + w.ckpt) : a->ckpt;
-  if (w.own_ckpt) {
-    ScanParams pf = p;  // states-only forward: block checkpoints
-    if (int rc = hip_status(scan_cfwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
+  p.ysave = w.sliced && a->z != nullptr ? (w.own_ysave ? ws + w.ysave : a->ysave) : nullptr;
+  if (w.own_ckpt || w.own_ysave) {
+    // The forward for the block checkpoints and/or (sliced, with z) y before
+    // the gate.
+    ScanParams pf = p;
+    pf.ckpt = w.own_ckpt ? p.ckpt : nullptr;
+    if (int rc = complex_fwd_run(pf, w.own_ysave, reinterpret_cast<float*>(ws + w.fwd), a->dtype, st,
+                                 "selective_scan_bwd fwd launch"))
       return rc;
   }
   p.dout = a->dout;
@@ -371,11 +426,18 @@ int complex_bwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes
   p.dA_part = w.part_dA ? reinterpret_cast<float*>(ws + w.dA) : a->dA;
   p.dD_part = reinterpret_cast<float*>(ws + w.dD);
   p.dbias_part = reinterpret_cast<float*>(ws + w.dbias);
+  if (w.sliced) p.rpart = reinterpret_cast<float*>(ws + w.rpart);
   if (int rc = hip_status(scan_cbwd_launch(p, a->dtype, st), "selective_scan_bwd launch")) return rc;
+  if (w.sliced) {
+    // du, ddelta, dz and the dD / ddelta_bias batch partials from the slices'
+    // shares, then the partials as for one slice.
+    if (int rc = hip_status(scan_bwd_finish_launch(p, a->dtype, st), "selective_scan_bwd finish launch"))
+      return rc;
+  }
   return hip_status(
       scan_reduce_launch(w.part_bc ? p.dB_part : nullptr, a->dB, w.part_bc ? p.dC_part : nullptr,
-                         a->dC, p.batch * p.ngroups, p.nblk_c, 2 * p.seqlen * p.dstate,
-                         w.part_dA ? p.dA_part : nullptr, a->dA, 2 * p.dim * p.dstate,
+                         a->dC, p.batch * p.ngroups, p.nblk_c, 2 * p.seqlen * p.ntotal,
+                         w.part_dA ? p.dA_part : nullptr, a->dA, 2 * p.dim * p.ntotal,
                          a->dD ? p.dD_part : nullptr, a->dD,
                          a->ddelta_bias ? p.dbias_part : nullptr, a->ddelta_bias, p.dim, p.batch, st),
       "selective_scan_bwd reduce");
@@ -397,7 +459,7 @@ extern "C" size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a
     clear_error();
     return 0;
   }
-  if (a->complex_a) return 0;
+  if (a->complex_a) return cfwd_bytes(cparams(a), a->out != nullptr);
   return fwd_layout(fwd_params(a), a->out != nullptr).total;
 }
 
@@ -412,7 +474,7 @@ extern "C" int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace,
     return zero_f32(a->last_state, (a->complex_a ? 2 : 1) * a->batch * a->dim * a->dstate,
                     static_cast<hipStream_t>(stream));
   }
-  if (a->complex_a) return complex_fwd(a, static_cast<hipStream_t>(stream));
+  if (a->complex_a) return complex_fwd(a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   ScanParams p = fwd_params(a);
   const bool write_out = a->out != nullptr;
   FwdLayout w = fwd_layout(p, write_out);

@@ -23,6 +23,14 @@
 // summed over the wave's channel rows (permlane swaps), over the workgroup's
 // waves (LDS) into one partial per workgroup, and the partials are summed in a
 // fixed order by the backward's reduce launch.
+//
+// Above 32 states the states are cut into slices of 32 that the grid scans
+// side by side (scan_slice), as for real A: the forward's slices write their
+// shares of 2 Re(sum_n h C) (PART), which scan_fwd_finish_kernel adds with D
+// u and the gate; the backward's slices write their shares of
+// sum_n Re(q conj(A)) and sum_n Re(g conj(B)) (SLICED), from which
+// scan_bwd_finish_kernel forms du, ddelta, dz and the dD / ddelta_bias
+// partials. All other outputs are per state and land in place.
 #include "scan_common.h"
 
 namespace mcpu {
@@ -39,8 +47,8 @@ __device__ __forceinline__ void cexp_step(float x2, float rev, float& ar, float&
 }
 
 // WRITE_OUT = false: states only (checkpoints and/or last_state), no C, z or
-// outputs.
-template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT>
+// outputs. PART: a state slice's share of y into p.ypart (no D, no gate).
+template <typename Tx, int SPL, bool HAS_Z, bool WRITE_OUT, bool PART>
 __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParams p) {
   constexpr int W = kCWaves;
   constexpr int CH = 4 * W;
@@ -58,8 +66,10 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x, wave, r);
-  const int64_t N = p.dstate, L = p.seqlen, nb = p.nblk;
+  const SliceCtx sc = scan_slice(p);
+  const RowCtx rc = scan_row_ctx<W>(p, sc.bx, wave, r);
+  // This slice's states, n0 .. n0 + N - 1 of the NS per row.
+  const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen, nb = p.nblk;
   const int64_t row = rc.b * p.dim + rc.d;
 
   float Ar2[SPL], Air[SPL], hr[SPL], hi[SPL];
@@ -67,14 +77,14 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
   for (int s = 0; s < SPL; ++s) {
     const int n = j + 16 * s;
     const bool ok = n < N;
-    Ar2[s] = ok ? p.A[2 * (rc.d * N + n)] * kLog2e : 0.f;
-    Air[s] = ok ? p.A[2 * (rc.d * N + n) + 1] * kInv2Pi : 0.f;
+    Ar2[s] = ok ? p.A[2 * (rc.d * NS + n0 + n)] * kLog2e : 0.f;
+    Air[s] = ok ? p.A[2 * (rc.d * NS + n0 + n) + 1] * kInv2Pi : 0.f;
     hr[s] = hi[s] = 0.f;
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[rc.d] : 0.f;
-  // Checkpoints (batch, dim, nblk, dstate, 2): the state at each block start.
-  float* ck = p.ckpt ? p.ckpt + row * nb * N * 2 : nullptr;
+  // Checkpoints (batch, dim, nblk, NS, 2): the state at each block start.
+  float* ck = p.ckpt ? p.ckpt + (row * nb * NS + n0) * 2 : nullptr;
   const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);
   char* const out0 = static_cast<char*>(p.out) +
       static_cast<int64_t>(sizeof(Tx)) * (rc.b * p.sout[0] + (rc.g * p.dpg + rc.cl0) * p.sout[1]);
@@ -85,8 +95,8 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
   xu.template init<Tx>(tid, p.u, p.su, p, rc, 0);
   xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, 0);
   if (HAS_Z && WRITE_OUT) xz.template init<Tx>(tid, p.z, p.sz, p, rc, 0);
-  const float* Brow = p.B + rc.b * p.sB[0] + rc.g * p.sB[1];
-  const float* Crow = p.C + rc.b * p.sC[0] + rc.g * p.sC[1];
+  const float* Brow = p.B + rc.b * p.sB[0] + rc.g * p.sB[1] + n0 * p.sB[3];
+  const float* Crow = p.C + rc.b * p.sC[0] + rc.g * p.sC[1] + n0 * p.sC[3];
   BC tbr, tbi, tcr, tci;
   tbr.init(tid, Brow, p.sB, N, 0, true);
   tbi.init(tid, Brow + 1, p.sB, N, 0, true);
@@ -211,21 +221,24 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
       });
     }
 
-    float yg = 0.f;
+    float y = 0.f, yg = 0.f;
     if (WRITE_OUT) {
-      float y = 2.f * row_reduce_scatter16(pacc, j);
-      if (p.D != nullptr) y = fmaf(Dd, uu, y);
-      yg = HAS_Z ? y * (zz * sigmoid(zz)) : y;
+      y = 2.f * row_reduce_scatter16(pacc, j);
+      if (!PART && p.D != nullptr) y = fmaf(Dd, uu, y);
+      yg = (HAS_Z && !PART) ? y * (zz * sigmoid(zz)) : y;
     }
 
     park(buf ^ 1);  // in the last iteration a harmless copy into the idle buffer
 
-    if (WRITE_OUT && tv && rc.active) buf_st<Tx>(wave_rsrc(out0 + t0 * out_ts), out_off, yg);
+    if (WRITE_OUT && tv && rc.active) {
+      if constexpr (PART) p.ypart[((sc.sl * p.batch + rc.b) * p.dim + rc.d) * L + t0 + j] = y;
+      else buf_st<Tx>(wave_rsrc(out0 + t0 * out_ts), out_off, yg);
+    }
     if (ck != nullptr && rc.active && k + 1 < nb) {
 #pragma unroll
       for (int s = 0; s < SPL; ++s)
         if (j + 16 * s < N) {
-          float* c = ck + ((k + 1) * N + j + 16 * s) * 2;
+          float* c = ck + ((k + 1) * NS + j + 16 * s) * 2;
           c[0] = hr[s];
           c[1] = hi[s];
         }
@@ -236,13 +249,16 @@ __global__ void __launch_bounds__(64 * kCWaves) scan_cfwd_kernel(const ScanParam
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
       if (j + 16 * s < N) {
-        p.last_state[(row * N + j + 16 * s) * 2] = hr[s];
-        p.last_state[(row * N + j + 16 * s) * 2 + 1] = hi[s];
+        p.last_state[(row * NS + n0 + j + 16 * s) * 2] = hr[s];
+        p.last_state[(row * NS + n0 + j + 16 * s) * 2 + 1] = hi[s];
       }
   }
 }
 
-template <typename Tx, int W, int SPL, bool HAS_Z>
+// SLICED: one state slice, which writes its sum_n Re(q conj(A)) and
+// sum_n Re(g conj(B)) shares (rpart) in place of du, ddelta, dz and the dD /
+// ddelta_bias partials.
+template <typename Tx, int W, int SPL, bool HAS_Z, bool SLICED>
 __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   constexpr int CH = 4 * W;
   constexpr int NW = 16 * SPL;
@@ -261,8 +277,11 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   const int wave = tid >> 6;
   const int r = lane >> 4, j = lane & 15;
   const int c_local = wave * kScanRowsPerWave + r;
-  const RowCtx rc = scan_row_ctx<W>(p, blockIdx.x, wave, r);
-  const int64_t N = p.dstate, L = p.seqlen, nb = p.nblk;
+  const SliceCtx sc = scan_slice(p);
+  const RowCtx rc = scan_row_ctx<W>(p, sc.bx, wave, r);
+  // This slice's states, n0 .. n0 + N - 1 of the NS per row of A,
+  // dlast_state, the checkpoints and the dA/dB/dC layouts.
+  const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen, nb = p.nblk;
   const int64_t row = rc.b * p.dim + rc.d;
   const int64_t kl = nb - 1;
   const int64_t t_last = kl * T;
@@ -272,12 +291,12 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   for (int s = 0; s < SPL; ++s) {
     const int n = j + 16 * s;
     const bool ok = n < N;
-    Ar[s] = ok ? p.A[2 * (rc.d * N + n)] : 0.f;
-    Ai[s] = ok ? p.A[2 * (rc.d * N + n) + 1] : 0.f;
+    Ar[s] = ok ? p.A[2 * (rc.d * NS + n0 + n)] : 0.f;
+    Ai[s] = ok ? p.A[2 * (rc.d * NS + n0 + n) + 1] : 0.f;
     Ar2[s] = Ar[s] * kLog2e;
     Air[s] = Ai[s] * kInv2Pi;
-    ghr[s] = (ok && p.dlast_state != nullptr) ? p.dlast_state[(row * N + n) * 2] : 0.f;
-    ghi[s] = (ok && p.dlast_state != nullptr) ? p.dlast_state[(row * N + n) * 2 + 1] : 0.f;
+    ghr[s] = (ok && p.dlast_state != nullptr) ? p.dlast_state[(row * NS + n0 + n) * 2] : 0.f;
+    ghi[s] = (ok && p.dlast_state != nullptr) ? p.dlast_state[(row * NS + n0 + n) * 2 + 1] : 0.f;
     dAr[s] = dAi[s] = 0.f;
   }
   const float Dd = p.D ? p.D[rc.d] : 0.f;
@@ -292,8 +311,8 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, t_last);
   xo.template init<Tx>(tid, has_dout ? p.dout : p.u, p.sdo, p, rc, t_last);
   if (HAS_Z) xz.template init<Tx>(tid, p.z, p.sz, p, rc, t_last);
-  const float* Brow = p.B + rc.b * p.sB[0] + rc.g * p.sB[1];
-  const float* Crow = p.C + rc.b * p.sC[0] + rc.g * p.sC[1];
+  const float* Brow = p.B + rc.b * p.sB[0] + rc.g * p.sB[1] + n0 * p.sB[3];
+  const float* Crow = p.C + rc.b * p.sC[0] + rc.g * p.sC[1] + n0 * p.sC[3];
   BC tbr, tbi, tcr, tci;
   tbr.init(tid, Brow, p.sB, N, t_last, true);
   tbi.init(tid, Brow + 1, p.sB, N, t_last, true);
@@ -303,8 +322,8 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   const int64_t row0 = rc.b * p.dim + rc.g * p.dpg + rc.cl0;
   const int64_t crow = rc.d - (rc.g * p.dpg + rc.cl0);
   // Checkpointed state pair of lane j, state j + 16 s, of the current block.
-  const char* ck_base = reinterpret_cast<const char*>(p.ckpt + (row0 * nb + kl) * N * 2);
-  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * nb * N * 2 + 2 * j));
+  const char* ck_base = reinterpret_cast<const char*>(p.ckpt + ((row0 * nb + kl) * NS + n0) * 2);
+  const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * nb * NS * 2 + 2 * j));
   uint32_t ck_lane[SPL];
   bool ck_ok[SPL];
 #pragma unroll
@@ -324,7 +343,7 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
 
   // Cross-wave dB/dC outputs of this thread: element e = (array, step, state);
   // T * NW is a multiple of 64 * W, so the array is uniform over a wave.
-  // Partials are (batch, ngroups, nblk_c, seqlen, dstate, 2).
+  // Partials are (batch, ngroups, nblk_c, seqlen, NS, 2).
   constexpr int NOUT = 4 * T * NW / (64 * W);
   const int64_t part_row = ((rc.b * p.ngroups + rc.g) * p.nblk_c + rc.cblk) * L + t_last;
   char* o_part[NOUT];
@@ -339,8 +358,8 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
     o_t[q] = tt;
     o_red[q] = (arr * W * T + tt) * NW + n;
     o_ok[q] = n < N;
-    o_part[q] = reinterpret_cast<char*>((arr < 2 ? p.dB_part : p.dC_part) + part_row * N * 2);
-    o_poff[q] = static_cast<uint32_t>(sizeof(float) * ((tt * N + n) * 2 + (arr & 1)));
+    o_part[q] = reinterpret_cast<char*>((arr < 2 ? p.dB_part : p.dC_part) + (part_row * NS + n0) * 2);
+    o_poff[q] = static_cast<uint32_t>(sizeof(float) * ((tt * NS + n) * 2 + (arr & 1)));
   }
 
   uint32_t nu = 0u, nd = 0u, no = 0u, nz = 0u;  // raw bits, widened at the park
@@ -382,7 +401,7 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
     tbi.advance_unless(-1, stay);
     tcr.advance_unless(-1, stay);
     tci.advance_unless(-1, stay);
-    ck_base -= stay ? 0 : sizeof(float) * N * 2;
+    ck_base -= stay ? 0 : sizeof(float) * NS * 2;
   };
   auto park = [&](int buf) {
     (&s_x[buf][0][0][0])[xu.slot] = raw_f32<Tx>(nu);
@@ -460,7 +479,7 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
             hsi[s][i] = ni;
             asr[s][i] = ar;
             asi[s][i] = ai;
-            if (HAS_Z) acc = fmaf(nr, Cr[s][i], fmaf(-ni, Ci[s][i], acc));
+            if (HAS_Z && !SLICED) acc = fmaf(nr, Cr[s][i], fmaf(-ni, Ci[s][i], acc));
           }
           pacc[i] = acc;
         } else {
@@ -471,13 +490,16 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
       });
     }
 
-    // Output gating: dy_t and dz_t for the step this lane owns.
+    // Output gating: dy_t and dz_t for the step this lane owns (a slice sees
+    // only its share of y: dz is formed by the finish kernel from ysave).
     float dy = go, dzv = 0.f;
     if (HAS_Z) {
-      float y = 2.f * row_reduce_scatter16(pacc, j);
-      if (has_D) y = fmaf(Dd, uu, y);
       const float sg = sigmoid(zz);
-      dzv = go * y * sg * (1.f + zz * (1.f - sg));
+      if constexpr (!SLICED) {
+        float y = 2.f * row_reduce_scatter16(pacc, j);
+        if (has_D) y = fmaf(Dd, uu, y);
+        dzv = go * y * sg * (1.f + zz * (1.f - sg));
+      }
       dy = go * zz * sg;
     }
 
@@ -570,9 +592,15 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
       h0i[s] = ck_ok[s] ? nh0i[s] : 0.f;
     }
     if (tv && rc.active) {
-      buf_st<Tx>(wave_rsrc(o_du), off_du, duv);
-      buf_st<Tx>(wave_rsrc(o_dd), off_dd, ddt);
-      if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), off_dz, dzv);
+      if constexpr (SLICED) {
+        const int64_t at = ((sc.sl * p.batch + rc.b) * p.dim + rc.d) * L + t0 + j;
+        p.rpart[at] = R1;
+        p.rpart[p.nslices * p.batch * p.dim * L + at] = R2;
+      } else {
+        buf_st<Tx>(wave_rsrc(o_du), off_du, duv);
+        buf_st<Tx>(wave_rsrc(o_dd), off_dd, ddt);
+        if (HAS_Z) buf_st<Tx>(wave_rsrc(o_dz), off_dz, dzv);
+      }
     }
     o_du -= T * esz * p.sdu[2];
     o_dd -= T * esz * p.sdd[2];
@@ -589,7 +617,7 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
         for (int w = 0; w < W; ++w) acc += src[w * T * NW];
         buf_st<float>(wave_rsrc(o_part[q]), o_poff[q], acc);
       }
-      o_part[q] -= sizeof(float) * T * N * 2;
+      o_part[q] -= sizeof(float) * T * NS * 2;
     }
   };
 
@@ -602,10 +630,11 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
 #pragma unroll
     for (int s = 0; s < SPL; ++s)
       if (j + 16 * s < N) {
-        p.dA_part[(row * N + j + 16 * s) * 2] = dAr[s];
-        p.dA_part[(row * N + j + 16 * s) * 2 + 1] = dAi[s];
+        p.dA_part[(row * NS + n0 + j + 16 * s) * 2] = dAr[s];
+        p.dA_part[(row * NS + n0 + j + 16 * s) * 2 + 1] = dAi[s];
       }
   }
+  if constexpr (SLICED) return;
   dD_acc = row_allreduce16(dD_acc);
   dbias_acc = row_allreduce16(dbias_acc);
   if (rc.active && j == 0) {
@@ -614,27 +643,42 @@ __global__ void __launch_bounds__(64 * W) scan_cbwd_kernel(const ScanParams p) {
   }
 }
 
+// A sliced forward (p.nslices > 1) writes the slices' shares of y when
+// p.ypart is set; the caller then runs the finish kernel.
 template <typename Tx, int SPL>
 static hipError_t launch_cfwd(const ScanParams& p, bool write_out, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c));
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nslices));
   const dim3 block(64 * kCWaves);
   if (!write_out)
-    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, false, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, false, false, false>), grid, block, 0, stream, p);
+  else if (p.ypart != nullptr)
+    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, false, true, true>), grid, block, 0, stream, p);
   else if (p.z != nullptr)
-    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, true, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, true, true, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, false, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cfwd_kernel<Tx, SPL, false, true, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
+// Sliced backwards (p.rpart set) run 32-state slices: only SPL 2 has a
+// sliced form.
 template <typename Tx, int W, int SPL>
 static hipError_t launch_cbwd(const ScanParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c));
+  const dim3 grid(static_cast<unsigned>(p.batch * p.ngroups * p.nblk_c * p.nslices));
   const dim3 block(64 * W);
+  if constexpr (SPL == 2) {
+    if (p.rpart != nullptr) {
+      if (p.z != nullptr)
+        hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, true, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, false, true>), grid, block, 0, stream, p);
+      return hipGetLastError();
+    }
+  }
   if (p.z != nullptr)
-    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, true, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((scan_cbwd_kernel<Tx, W, SPL, false, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

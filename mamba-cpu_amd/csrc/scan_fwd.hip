@@ -346,6 +346,29 @@ static hipError_t dispatch_fwd_sliced(const ScanParams& p, bool write_out, hipSt
 
 int scan_fwd_waves() { return kFwdWaves; }
 
+// The outputs of a sliced forward from its slices' shares of y (p.ypart),
+// with D u, ysave and the gate: the complex-A forward's finish.
+hipError_t scan_fwd_finish_launch(const ScanParams& p, int dtype, hipStream_t stream) {
+  const int64_t n = p.batch * p.dim * p.seqlen;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  const bool z = p.z != nullptr;
+  switch (dtype) {
+    case MCPU_F32:
+      if (z) hipLaunchKernelGGL((scan_fwd_finish_kernel<float, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_fwd_finish_kernel<float, false>), grid, dim3(256), 0, stream, p);
+      break;
+    case MCPU_BF16:
+      if (z) hipLaunchKernelGGL((scan_fwd_finish_kernel<bf16, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_fwd_finish_kernel<bf16, false>), grid, dim3(256), 0, stream, p);
+      break;
+    default:
+      if (z) hipLaunchKernelGGL((scan_fwd_finish_kernel<f16, true>), grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL((scan_fwd_finish_kernel<f16, false>), grid, dim3(256), 0, stream, p);
+      break;
+  }
+  return hipGetLastError();
+}
+
 // Time chunks for a forward with these parameters (p.nblk_c set for
 // scan_fwd_waves()): enough chunks to give the GPU's 256 compute units about
 // five workgroups each (the kernel's occupancy), and chunks of at most 64

@@ -458,7 +458,11 @@ std::tuple<Tensor, Tensor, Tensor> selective_scan_cfwd(const Tensor& u, const Te
   strides3(a.out_stride, out);
   a.last_state = static_cast<float*>(last.data_ptr());
   a.ckpt = static_cast<float*>(ckpt.data_ptr());
-  check_rc(mcpu_selective_scan_fwd(&a, nullptr, 0, stream_of(u)), name);
+  // Above 32 states the slices' shares of y need a workspace.
+  const size_t ws_bytes = mcpu_selective_scan_fwd_workspace_size(&a);
+  Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({static_cast<int64_t>(ws_bytes)}, u.options().dtype(at::kByte));
+  check_rc(mcpu_selective_scan_fwd(&a, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(u)), name);
   return {out, last, ckpt};
 }
 

@@ -218,7 +218,7 @@ def selective_scan_fn(
     ROCm GPU tensors.
 
     u, delta, z: (batch, dim, seqlen), float32 / bfloat16 / float16
-    A: (dim, dstate), real-valued, or complex (dstate <= 32)
+    A: (dim, dstate), real-valued, or complex; dstate up to 4096
     B, C: (batch, dstate, seqlen) or (batch, ngroups, dstate, seqlen), input-dependent,
           with their own group counts; or (dim, dstate), input-independent.
           With complex A (mamba_ssm's convention): input-dependent B/C are real

@@ -166,8 +166,10 @@ def test_scan_sizes():
 
 def test_complex_scan_sizes_and_limits():
     """complex_a: checkpoints hold (re, im) pairs, the forward uses no
-    workspace, dstate is at most 32, and the imaginary part of the last B/C
-    element counts in the 32-bit offset check."""
+    workspace up to 32 states and above them (32-state slices) one float per
+    slice and output element (the call refuses a smaller one), dstate is at
+    most 4096, and the imaginary part
+    of the last B/C element counts in the 32-bit offset check."""
     from mamba_cpu import _C
 
     L = _C.lib
@@ -178,9 +180,12 @@ def test_complex_scan_sizes_and_limits():
         ctypes.byref(_scan_args(batch=1, dim=64, seqlen=4096, complex_a=1))) == 0
     assert L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(a)) > \
         L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(seqlen=33)))
-    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=33, complex_a=1)), None, 0, None)
-    assert rc == _C.MCPU_ERR_UNSUPPORTED and "complex" in msg
-    assert L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(dstate=33, complex_a=1))) == 0
+    big = _scan_args(dstate=96, complex_a=1)
+    big.out = 16
+    assert L.mcpu_selective_scan_fwd_workspace_size(ctypes.byref(big)) == 4 * 3 * 2 * 8 * 32
+    assert L.mcpu_selective_scan_bwd_workspace_size(ctypes.byref(_scan_args(dstate=33, complex_a=1))) > 0
+    rc, msg = _rc(L.mcpu_selective_scan_fwd, ctypes.byref(_scan_args(dstate=4097, complex_a=1)), None, 0, None)
+    assert rc == _C.MCPU_ERR_UNSUPPORTED and "dstate" in msg
 
 
 def test_scan_without_gfx950_reports_the_device():

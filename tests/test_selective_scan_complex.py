@@ -11,6 +11,9 @@ scan and torch.autograd. Complex gradients are dLoss/dRe + i dLoss/dIm
 (torch's convention).
 Tolerances: float32 outputs rtol 1e-4 / atol 2e-5, gradients rtol 1e-3 / atol
 1e-4 after scaling by the gradient's magnitude; bf16 inputs 1e-2 / 2e-2.
+Above 32 states the kernels scan 32-state slices side by side and finish
+from their shares (dstate 33 to 128, with groups, z, D, bias, both loss
+terms, a long sequence and bf16 inputs).
 """
 
 import numpy as np
@@ -178,9 +181,6 @@ def test_complex_long_sequence():
 
 
 def test_complex_rejections():
-    inp = make_cinputs(1, 4, 8, 33, None, False, False, False)
-    with pytest.raises(NotImplementedError, match="dstate"):
-        selective_scan_fn(**inp)
     inp = make_cinputs(1, 4, 8, 2, None, False, False, False)
     with pytest.raises(ValueError, match="input-independent"):
         selective_scan_fn(**{**inp, "B": torch.complex(inp["B"], inp["B"])})
@@ -220,3 +220,37 @@ def test_complex_channel_contiguous_inputs():
     for k, w in zip(["u", "delta", "A", "B", "C", "D", "z", "delta_bias"], wants):
         close(cc[k].grad, w, GRAD_RTOL, GRAD_ATOL[k], k)
     assert cc["u"].grad.stride(1) == 1 and cc["z"].grad.stride(1) == 1
+
+
+@pytest.mark.parametrize("batch,dim,seqlen,dstate,ngroups", [(2, 16, 40, 33, None), (1, 20, 70, 48, 2),
+                                                            (2, 8, 100, 64, None), (1, 12, 37, 128, 3)])
+@pytest.mark.parametrize("has_D,has_z,has_bias,softplus", [
+    (False, False, False, False),
+    (True, True, True, True),
+])
+def test_complex_dstate_above_32_matches_oracle(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias,
+                                                softplus):
+    inp = make_cinputs(batch, dim, seqlen, dstate, ngroups, has_D, has_z, has_bias, requires_grad=True,
+                       seed=dstate)
+    with torch.no_grad():
+        out, last = selective_scan_fn(**inp, delta_softplus=softplus, return_last_state=True)
+    want, want_last = O.selective_scan_fwd_complex(**inp, delta_softplus=softplus)
+    close(out, want, 1e-4, 2e-5, "out")
+    close(last, want_last, 1e-4, 2e-5, "last_state")
+    g = torch.Generator().manual_seed(dstate + 1)
+    W = torch.randn(batch, dim, seqlen, generator=g).to(DEV)
+    V = torch.complex(torch.randn(batch, dim, dstate, generator=g), torch.randn(batch, dim, dstate, generator=g))
+    check_grads(inp, softplus, W, V.to(DEV))
+
+
+def test_complex_dstate_above_32_long_sequence_and_bf16():
+    inp = make_cinputs(1, 8, 2000, 80, None, True, True, True, requires_grad=True, seed=11)
+    out = selective_scan_fn(**inp, delta_softplus=True)
+    want, _ = O.selective_scan_fwd_complex(**inp, delta_softplus=True)
+    close(out, want, 1e-4, 5e-5, "out")
+    W = torch.randn(1, 8, 2000, generator=torch.Generator().manual_seed(12)).to(DEV)
+    check_grads(inp, True, W, None)
+    inp = make_cinputs(2, 16, 60, 40, None, True, True, True, dtype=torch.bfloat16, seed=13)
+    out = selective_scan_fn(**inp, delta_softplus=True)
+    want, _ = O.selective_scan_fwd_complex(**inp, delta_softplus=True)
+    close(out.float(), want, 1e-2, 2e-2, "out bf16")
