@@ -48,9 +48,10 @@ int mcpu_check_device(void);
 const char* mcpu_version(void);
 
 /* sizeof() of an argument block ("scan", "conv", "conv_update",
- * "state_update", "ssd", "mixer_step", "norm_linear"), 0 for an unknown name. A binding must
- * compare it with its own sizeof of each block it uses before its first call:
- * the library reads a whole block, whatever the caller allocated. */
+ * "state_update", "ssd", "mixer_step", "norm_linear", "mamba2_step"), 0 for
+ * an unknown name. A binding must compare it with its own sizeof of each
+ * block it uses before its first call: the library reads a whole block,
+ * whatever the caller allocated. */
 size_t mcpu_args_size(const char* name);
 
 /* ------------------------------------------------------------------------ */
@@ -493,6 +494,61 @@ typedef struct mcpu_norm_linear_args {
 } mcpu_norm_linear_args;
 
 int mcpu_norm_linear(const mcpu_norm_linear_args* a, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused single-token Mamba-2 block step (decode).                           */
+/* ------------------------------------------------------------------------ */
+
+/* One decode step of a Mamba-2 block for a batch of single tokens: what a
+ * transformers Mamba2Block computes for one token with a cache (its mixer's
+ * recurrent form, which the reference's patched models route through
+ * causal_conv1d_update and the Mamba-2 form of selective_state_update,
+ * src/mamba_cpu/hf.py), in three launches:
+ *   u         = RMSNorm(hidden) when norm_weight != NULL (else hidden), in dtype
+ *   gate, xBC, dt = in_proj(u)             (d_inner, conv_dim, nheads)
+ *   xBC       = silu(conv1d_update(conv_state, xBC))   conv_state shifted in place
+ *   x, B, C   = xBC                        (d_inner, ngroups dstate, ngroups dstate)
+ *   y         = selective_state_update(ssm_state, x, dt, A, B, C, D, dt_bias, softplus)
+ *               per head h of headdim channels, group h / (nheads / ngroups)
+ *   r         = y silu(gate) ;  y = gate_norm_weight round(r rsqrt(mean(r^2) + gate_norm_eps))
+ *   out       = out_proj(y) [+ hidden, the residual, when add_residual]
+ * conv_dim = d_inner + 2 ngroups dstate. Rounding follows transformers: each
+ * stage's result is stored in dtype before the next reads it; arithmetic is
+ * float32. No counterpart in the reference (it has no fused decode path). All
+ * tensors contiguous, 16-byte aligned; batch <= 8; d_model and d_inner
+ * multiples of 4; dstate <= 128; conv width and state length at most 8; with
+ * batch rounded up to a power of two, (batch + 1) x d_model and (batch + 1) x
+ * d_inner at most 32768. */
+typedef struct mcpu_mamba2_step_args {
+  const void* hidden;           /* (batch, d_model), hidden_dtype */
+  const void* norm_weight;      /* (d_model), dtype, optional */
+  const void* in_w;             /* (d_inner + conv_dim + nheads, d_model), dtype */
+  const void* in_b;             /* (d_inner + conv_dim + nheads), dtype, optional */
+  const void* conv_w;           /* (conv_dim, width), dtype */
+  const void* conv_b;           /* (conv_dim), dtype, optional */
+  void* conv_state;             /* (batch, conv_dim, state_len), dtype */
+  const float* dt_bias;         /* (nheads), optional */
+  const float* A;               /* (nheads): -exp(A_log) */
+  const float* D;               /* (nheads), optional */
+  void* ssm_state;              /* (batch, nheads, headdim, dstate), state_dtype */
+  const void* gate_norm_weight; /* (d_inner), dtype */
+  const void* out_w;            /* (d_model, d_inner), dtype */
+  const void* out_b;            /* (d_model), dtype, optional */
+  void* out;                    /* (batch, d_model), out_dtype */
+  int64_t batch, d_model, d_inner, nheads, headdim, ngroups, dstate, width, state_len;
+  float norm_eps, gate_norm_eps;
+  int32_t add_residual;         /* out = residual + out_proj(y) */
+  int32_t residual_in_fp32;     /* the residual is hidden in float32 */
+  int32_t dtype;                /* weights, activations, conv state */
+  int32_t hidden_dtype;         /* dtype or MCPU_F32 */
+  int32_t state_dtype;          /* ssm_state */
+  int32_t out_dtype;            /* dtype, or MCPU_F32 with a float32 residual */
+} mcpu_mamba2_step_args;
+
+/* Workspace bytes of mcpu_mamba2_step (the step's intermediate vectors). */
+size_t mcpu_mamba2_step_workspace_size(const mcpu_mamba2_step_args* a);
+/* One step. Updates conv_state and ssm_state in place and writes out. */
+int mcpu_mamba2_step(const mcpu_mamba2_step_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,7 @@ extern "C" size_t mcpu_args_size(const char* name) {
   if (std::strcmp(name, "ssd") == 0) return sizeof(mcpu_ssd_args);
   if (std::strcmp(name, "mixer_step") == 0) return sizeof(mcpu_mixer_step_args);
   if (std::strcmp(name, "norm_linear") == 0) return sizeof(mcpu_norm_linear_args);
+  if (std::strcmp(name, "mamba2_step") == 0) return sizeof(mcpu_mamba2_step_args);
   return 0;
 }
 

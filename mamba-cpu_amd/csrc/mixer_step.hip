@@ -68,6 +68,17 @@ struct MixerParams {
   float* xpart;  // (batch, xpp, dt_rank + 2 dstate): partial x_proj sums, or null
   float* yv;     // (batch, d_inner): gated scan output
   int64_t batch, dm, di, R, N, W, S;
+  // in_proj rows: nin of them; rows conv_lo .. conv_lo + nconv - 1 go through
+  // the conv (into xc, (batch, nconv)), the others, in order, into zg
+  // (batch, nin - nconv). Mamba-1: [x | z], conv on x. Mamba-2: [gate | xBC |
+  // dt], conv on xBC.
+  int64_t nin, conv_lo, nconv;
+  int64_t zst;  // zg row stride: nin - nconv rounded up to a multiple of 4
+  // Mamba-2 heads: nh heads of hd channels, ng groups of N states; the gated
+  // norm's weight and epsilon.
+  int64_t nh, hd, ng;
+  const void* gn_w;
+  float gn_eps;
   int nxwg;      // block_in workgroups holding x rows: partial sums 0 .. nxwg - 1
   int xq, xs;    // block_ssm_kernel adds xq groups of xs partial sums per output
   int xpp;       // = xq xs >= nxwg: partial sums per output, nxwg .. xpp - 1 zero
@@ -333,7 +344,7 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = static_cast<int>(p.dm);
   float* s_nw = s_u + MT * K;
-  const int64_t nout = 2 * p.di;
+  const int64_t nout = p.nin, nplain = p.zst;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RW;
   const int nrows = row0 >= nout ? 0 : static_cast<int>(nout - row0 < RW ? nout - row0 : RW);
   // Loads: first the hidden rows and the norm weight; once the rows are in,
@@ -360,10 +371,11 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
     const int64_t n = row0 + rr < nout ? row0 + rr : nout - 1;
-    const int64_t nx = n < p.di ? n : p.di - 1;
+    const int64_t cn = n - p.conv_lo;  // conv channel of the row, clamped into the conv rows
+    const int64_t nx = cn < 0 ? 0 : (cn < p.nconv ? cn : p.nconv - 1);
     eb[rr] = ld_bits(tbl, n);
     ecb[rr] = ld_bits(cb, nx);
-    const T* stt = static_cast<const T*>(p.conv_state) + (ml * p.di + nx) * p.S;
+    const T* stt = static_cast<const T*>(p.conv_state) + (ml * p.nconv + nx) * p.S;
     const T* cw = static_cast<const T*>(p.conv_w) + nx * p.W;
 #pragma unroll
     for (int i = 0; i < kMaxConvState; ++i) {
@@ -398,11 +410,12 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
       if (rr >= nrows || lane >= p.batch) continue;
       const int64_t m = lane;
       y = rnd<T>(tb ? y + bits_f32<T>(eb[rr]) : y);
-      if (n >= p.di) {
-        p.zg[m * p.di + (n - p.di)] = y;
+      const int64_t cn = n - p.conv_lo;
+      if (cn < 0 || cn >= p.nconv) {
+        p.zg[m * nplain + (cn < 0 ? n : n - p.nconv)] = y;
         continue;
       }
-      // Depthwise conv update of channel n: taps 0 .. W-2 read the newest W-1
+      // Depthwise conv update of channel cn: taps 0 .. W-2 read the newest W-1
       // state entries, tap W-1 reads y; the state shifts left by one and y
       // becomes its newest entry.
       float c = p.conv_b ? bits_f32<T>(ecb[rr]) : 0.f;
@@ -421,14 +434,14 @@ __global__ void __launch_bounds__(kThreads) block_in_kernel(const MixerParams p)
         if (i == p.W - 1) wl = ecw[rr][i];
       c = fmaf(bits_f32<T>(wl), y, c);
       c = c * sigmoid(c);
-      T* stt = static_cast<T*>(p.conv_state) + (m * p.di + n) * p.S;
+      T* stt = static_cast<T*>(p.conv_state) + (m * p.nconv + cn) * p.S;
 #pragma unroll
       for (int i = 0; i < kMaxConvState - 1; ++i)
         if (i < p.S - 1) st_bits(stt, i, est[rr][i + 1]);
       stt[p.S - 1] = from_f32<T>(y);
       c = rnd<T>(c);
-      p.xc[m * p.di + n] = c;
-      s_xc[m][wave * RW + rr] = c;
+      p.xc[m * p.nconv + cn] = c;
+      if (p.xpart) s_xc[m][wave * RW + rr] = c;
     }
   }
   if (!xpart) return;  // uniform across the workgroup
@@ -655,6 +668,176 @@ __global__ void __launch_bounds__(kSsmThreads) block_ssm_kernel(const MixerParam
   }
 }
 
+// Mamba-2 step, launch 2: the selective state update of every (head,
+// channel) row, in the state update kernel's layout and arithmetic (16 lanes
+// per row, states n = lane + 16 s, the same fixed-order sums):
+//   dt = softplus(dt_raw[h] + dt_bias[h]),
+//   state = state exp(dt A[h]) + dt x B_g,   y = <state, C_g> + D[h] x,
+// y rounded to T. x, B and C are the conv outputs (xc: x | B | C of every
+// group), dt_raw the in_proj rows after the gate (zg). Grid
+// (ceil(nh hd / 16), batch).
+template <typename T, typename Ts, int SPL>
+__global__ void __launch_bounds__(256) m2_ssm_kernel(const MixerParams p) {
+  const int j = threadIdx.x & 15;
+  const int64_t hp = blockIdx.x * 16ll + (threadIdx.x >> 4);
+  const int64_t m = blockIdx.y;
+  if (hp >= p.nh * p.hd) return;  // whole 16-lane rows leave together
+  const int64_t h = hp / p.hd, g = h / (p.nh / p.ng), N = p.N;
+  const float* xr = p.xc + m * p.nconv;
+  const float* Bg = xr + p.di + g * N;
+  const float* Cg = xr + p.di + p.ng * N + g * N;
+  Ts* state = static_cast<Ts*>(p.ssm_state) + (m * p.nh * p.hd + hp) * N;
+  // Loads first, unconditional from indexes clamped into the row.
+  uint32_t sv[SPL];
+  float bv[SPL], cv[SPL];
+#pragma unroll
+  for (int s = 0; s < SPL; ++s) {
+    const int64_t n = min(static_cast<int64_t>(j + 16 * s), N - 1);
+    sv[s] = ld_bits(state, n);
+    bv[s] = Bg[n];
+    cv[s] = Cg[n];
+  }
+  const float x = xr[hp];
+  float dt = p.zg[m * p.zst + p.di + h];
+  const float Ah = p.A[h];
+  const float bias = (p.dt_b ? p.dt_b : p.A)[h], Dh = (p.D ? p.D : p.A)[h];
+  if (p.dt_b) dt += bias;
+  dt = softplus(dt);
+  const float dtx = dt * x;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < SPL; ++s) {
+    const int64_t n = j + 16 * s;
+    if (n < N) {
+      const float v = fmaf(bits_f32<Ts>(sv[s]), fast_exp(dt * Ah), dtx * bv[s]);
+      state[n] = from_f32<Ts>(v);
+      acc = fmaf(v, cv[s], acc);
+    }
+  }
+  float y = row_allreduce16(acc);
+  if (j == 0) {
+    if (p.D) y = fmaf(x, Dh, y);
+    p.yv[m * p.di + hp] = rnd<T>(y);
+  }
+}
+
+// Mamba-2 step, launch 3: transformers' MambaRMSNormGated of the scan output
+// and out_proj, plus the residual:
+//   r = y silu(gate) (float32),  u = round_T(w round_T(r rsqrt(mean(r^2) + eps))),
+//   out = round_T(out_w u + out_b) [+ residual]
+// y (batch, d_inner) from yv, the gate from the first d_inner plain rows of
+// zg. Every workgroup stages and normalises the rows; its waves then take
+// their out_proj rows as gemv_kernel does. HF: the residual is float32.
+template <typename T, int MT, int RW, bool HF>
+__global__ void __launch_bounds__(kThreads) m2_out_kernel(const MixerParams p) {
+  using TH = std::conditional_t<HF, float, T>;
+  extern __shared__ __align__(16) float s_u[];   // (MT, d_inner) rows, then the norm weight
+  __shared__ float s_red[MT][kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = static_cast<int>(p.di);
+  const int64_t nout = p.dm;
+  float* s_nw = s_u + MT * K;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * RW;
+  const int nrows = row0 >= nout ? 0 : static_cast<int>(nout - row0 < RW ? nout - row0 : RW);
+  const int nbk = static_cast<int>(p.batch) * K;
+  // Loads: the rows and their gates, the norm weight; then the epilogue's
+  // bias and residual; the out_proj rows after the first barrier. All
+  // unconditional, from indexes clamped into their tensors.
+  constexpr int kStage = 8, kNorm = 4;
+  float4 yv4[kStage], gv4[kStage];
+  auto load_rows = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = min(base + 4 * (tid + kThreads * u), nbk - 4);
+      const int m = i / K;
+      yv4[u] = *reinterpret_cast<const float4*>(p.yv + i);
+      gv4[u] = *reinterpret_cast<const float4*>(p.zg + m * p.zst + (i - m * K));
+    }
+  };
+  load_rows(0);
+  raw4<T> nv[kNorm];
+#pragma unroll
+  for (int u = 0; u < kNorm; ++u) nv[u] = ld_raw4<T>(p.gn_w, min(4 * (tid + kThreads * u), K - 4));
+  __builtin_amdgcn_sched_barrier(0);
+  float ss[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) ss[m] = 0.f;
+  for (int base = 0; base < MT * K; base += 4 * kThreads * kStage) {
+    if (base > 0) load_rows(base);
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int i = base + 4 * (tid + kThreads * u);
+      if (i >= MT * K) break;
+      const int m = i / K;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nbk) {
+        const float4 y = yv4[u], gt = gv4[u];
+        v = make_float4(y.x * (gt.x * sigmoid(gt.x)), y.y * (gt.y * sigmoid(gt.y)), y.z * (gt.z * sigmoid(gt.z)),
+                        y.w * (gt.w * sigmoid(gt.w)));
+      }
+#pragma unroll
+      for (int mm = 0; mm < MT; ++mm)
+        if (mm == m) ss[mm] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+      *reinterpret_cast<float4*>(s_u + i) = v;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t ml = lane < p.batch ? lane : p.batch - 1;
+  const T* bl = static_cast<const T*>(p.out_b ? p.out_b : p.out_w);
+  const TH* hb = static_cast<const TH*>(p.hidden);
+  uint32_t eb[RW], er[RW];
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) {
+    const int64_t n = row0 + rr < nout ? row0 + rr : nout - 1;
+    eb[rr] = ld_bits(bl, n);
+    er[rr] = ld_bits(hb, ml * nout + n);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < kNorm; ++u) {
+    const int i = 4 * (tid + kThreads * u);
+    if (i < K) *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(nv[u]);
+  }
+  for (int i = 4 * (tid + kThreads * kNorm); i < K; i += 4 * kThreads)
+    *reinterpret_cast<float4*>(s_nw + i) = cvt4<T>(ld_raw4<T>(p.gn_w, i));
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const float t = wave_sum(ss[m]);
+    if (lane == 0) s_red[m][wave] = t;
+  }
+  __syncthreads();
+  RowTiles<T, RW> tiles;
+  tiles.load(p.out_w, row0, nout - 1, K, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int i = 4 * tid; i < MT * K; i += 4 * kThreads) {
+    const int m = i / K;
+    float tot = 0.f;
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm)
+      if (mm == m) tot = (s_red[mm][0] + s_red[mm][1]) + (s_red[mm][2] + s_red[mm][3]);
+    const float rs = rsqrtf(tot / static_cast<float>(K) + p.gn_eps);
+    float4 v = *reinterpret_cast<const float4*>(s_u + i);
+    const float4 w = *reinterpret_cast<const float4*>(s_nw + (i - m * K));
+    v = make_float4(rnd<T>(w.x * rnd<T>(v.x * rs)), rnd<T>(w.y * rnd<T>(v.y * rs)),
+                    rnd<T>(w.z * rnd<T>(v.z * rs)), rnd<T>(w.w * rnd<T>(v.w * rs)));
+    *reinterpret_cast<float4*>(s_u + i) = v;
+  }
+  __syncthreads();
+  if (nrows == 0) return;
+  float acc[RW][MT];
+  rows_dot<T, MT, RW>(acc, tiles, s_u, p.out_w, row0, nout - 1, K);
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) {
+    const int64_t n = row0 + rr;
+    float y = pick_lane<MT>(acc[rr], lane);
+    if (rr >= nrows || lane >= p.batch) continue;
+    y = rnd<T>(p.out_b ? y + bits_f32<T>(eb[rr]) : y);
+    if (p.add_residual) y = bits_f32<TH>(er[rr]) + y;
+    if (p.out_dtype == MCPU_F32) static_cast<float*>(p.out)[lane * nout + n] = y;
+    else st<T>(p.out, lane * nout + n, y);
+  }
+}
+
 // Final RMSNorm and a wide product for a handful of rows (a decode step's
 // norm_f + lm_head): out[m][n] = round_T(sum_k u[m][k] W[n][k] + bias[n])
 // with u the normalised rows (RowStage, rows as given). Persistent: each of
@@ -738,7 +921,7 @@ bool partial_plan(int64_t nxwg, int64_t J, int* xq, int* xs) {
 
 template <typename T, int MT, int RW>
 hipError_t launch_in(const MixerParams& p, bool hf, hipStream_t st) {
-  const int64_t nin = 2 * p.di;
+  const int64_t nin = p.nin;
   const dim3 grid(static_cast<unsigned>((nin + 4 * RW - 1) / (4 * RW)));
   const size_t lds = sizeof(float) * (MT + 1) * p.dm;
   if (hf || std::is_same_v<T, float>)
@@ -787,7 +970,7 @@ hipError_t launch_ssm_state(const MixerParams& p, hipStream_t st) {
 
 template <typename T, int MT>
 hipError_t step_t(const MixerParams& p, hipStream_t st) {
-  const int rw = rows_per_wave(2 * p.di);
+  const int rw = rows_per_wave(p.nin);
   const bool hf = p.hidden_dtype == MCPU_F32;
   hipError_t e = rw == 4 ? launch_in<T, MT, 4>(p, hf, st) : rw == 2 ? launch_in<T, MT, 2>(p, hf, st)
                                                                     : launch_in<T, MT, 1>(p, hf, st);
@@ -930,6 +1113,10 @@ extern "C" int mcpu_mixer_step(const mcpu_mixer_step_args* a, void* workspace, s
   p.batch = a->batch;
   p.dm = a->d_model;
   p.di = a->d_inner;
+  p.nin = 2 * a->d_inner;
+  p.conv_lo = 0;
+  p.nconv = a->d_inner;
+  p.zst = a->d_inner;
   p.R = a->dt_rank;
   p.N = a->dstate;
   p.W = a->width;
@@ -1027,4 +1214,182 @@ extern "C" int mcpu_norm_linear(const mcpu_norm_linear_args* a, void* stream) {
     default: norm_linear_t<f16>(p, hf, st); break;
   }
   return hip_status(hipGetLastError(), "norm_linear launch");
+}
+
+// ---- Mamba-2 block step --------------------------------------------------------
+
+namespace mcpu {
+namespace {
+
+struct Step2Layout {
+  size_t xc = 0, zg = 0, yv = 0, total = 0;
+  int64_t conv_dim = 0, nin = 0, zst = 0;
+};
+
+Step2Layout step2_layout(const mcpu_mamba2_step_args* a) {
+  Step2Layout w;
+  w.conv_dim = a->d_inner + 2 * a->ngroups * a->dstate;
+  w.nin = a->d_inner + w.conv_dim + a->nheads;
+  w.zst = (a->d_inner + a->nheads + 3) / 4 * 4;
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t at = off;
+    off += align_up(sizeof(float) * n);
+    return at;
+  };
+  w.xc = take(a->batch * w.conv_dim);
+  w.zg = take(a->batch * w.zst);
+  w.yv = take(a->batch * a->d_inner);
+  w.total = off;
+  return w;
+}
+
+int check_step2(const mcpu_mamba2_step_args* a) {
+  if (a == nullptr) return fail(MCPU_ERR_INVALID, "mamba2_step: null argument block");
+  if (a->hidden == nullptr || a->in_w == nullptr || a->conv_w == nullptr || a->conv_state == nullptr ||
+      a->A == nullptr || a->ssm_state == nullptr || a->gate_norm_weight == nullptr || a->out_w == nullptr ||
+      a->out == nullptr)
+    return fail(MCPU_ERR_INVALID, "mamba2_step: hidden, in_w, conv_w, conv_state, A, ssm_state, "
+                                  "gate_norm_weight, out_w and out are required");
+  if (a->batch < 1 || a->d_model < 4 || a->nheads < 1 || a->headdim < 1 || a->ngroups < 1 || a->dstate < 1 ||
+      a->width < 1 || a->d_inner != a->nheads * a->headdim || a->nheads % a->ngroups != 0)
+    return fail(MCPU_ERR_INVALID, "mamba2_step: bad sizes (d_inner must be nheads x headdim, nheads a "
+                                  "multiple of ngroups)");
+  if (a->batch > kMaxBatch)
+    return fail(MCPU_ERR_UNSUPPORTED, "mamba2_step: batch %lld > %d", (long long)a->batch, kMaxBatch);
+  if (a->d_model % 4 != 0 || a->d_inner % 4 != 0)
+    return fail(MCPU_ERR_UNSUPPORTED, "mamba2_step: d_model and d_inner must be multiples of 4");
+  if (a->dstate > 128) return fail(MCPU_ERR_UNSUPPORTED, "mamba2_step: dstate %lld > 128", (long long)a->dstate);
+  if (a->state_len < a->width - 1 || a->state_len < 1 || a->state_len > kMaxConvState || a->width > kMaxConvState)
+    return fail(MCPU_ERR_UNSUPPORTED, "mamba2_step: conv width and state length must be at most %d, "
+                                      "state length at least max(1, width - 1)", kMaxConvState);
+  const int64_t mt = pow2_batch(a->batch);
+  if ((mt + 1) * a->d_model > kMaxLdsFloats || (mt + 1) * a->d_inner > kMaxLdsFloats)
+    return fail(MCPU_ERR_UNSUPPORTED, "mamba2_step: batch x width too large for one workgroup's LDS");
+  if (!valid_dtype(a->dtype) || !valid_dtype(a->state_dtype) ||
+      (a->hidden_dtype != a->dtype && a->hidden_dtype != MCPU_F32) ||
+      (a->out_dtype != a->dtype && a->out_dtype != MCPU_F32))
+    return fail(MCPU_ERR_INVALID, "mamba2_step: bad dtype");
+  if (a->norm_eps < 0.f || a->gate_norm_eps < 0.f) return fail(MCPU_ERR_INVALID, "mamba2_step: eps < 0");
+  for (const void* t : {a->hidden, a->in_w, a->out_w, a->norm_weight, a->gate_norm_weight,
+                        static_cast<const void*>(a->out)})
+    if (reinterpret_cast<uintptr_t>(t) % 16 != 0)
+      return fail(MCPU_ERR_INVALID, "mamba2_step: hidden, weights and out must be 16-byte aligned");
+  return MCPU_OK;
+}
+
+template <typename T, typename Ts>
+void launch_m2_ssm(const MixerParams& p, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((p.nh * p.hd + 15) / 16), static_cast<unsigned>(p.batch));
+  if (p.N <= 16) hipLaunchKernelGGL((m2_ssm_kernel<T, Ts, 1>), grid, dim3(256), 0, st, p);
+  else if (p.N <= 32) hipLaunchKernelGGL((m2_ssm_kernel<T, Ts, 2>), grid, dim3(256), 0, st, p);
+  else if (p.N <= 64) hipLaunchKernelGGL((m2_ssm_kernel<T, Ts, 4>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((m2_ssm_kernel<T, Ts, 8>), grid, dim3(256), 0, st, p);
+}
+
+template <typename T, int MT, int RW>
+void launch_m2_out(const MixerParams& p, bool hf, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((p.dm + 4 * RW - 1) / (4 * RW)));
+  const size_t lds = sizeof(float) * (MT + 1) * p.di;
+  if (hf || std::is_same_v<T, float>)
+    hipLaunchKernelGGL((m2_out_kernel<T, MT, RW, true>), grid, dim3(kThreads), lds, st, p);
+  else
+    hipLaunchKernelGGL((m2_out_kernel<T, MT, RW, false>), grid, dim3(kThreads), lds, st, p);
+}
+
+template <typename T, int MT>
+hipError_t step2_t(const MixerParams& p, hipStream_t st) {
+  const bool hf = p.hidden_dtype == MCPU_F32;
+  const int rw = rows_per_wave(p.nin);
+  hipError_t e = rw == 4 ? launch_in<T, MT, 4>(p, hf, st) : rw == 2 ? launch_in<T, MT, 2>(p, hf, st)
+                                                                    : launch_in<T, MT, 1>(p, hf, st);
+  if (e != hipSuccess) return e;
+  switch (p.state_dtype) {
+    case MCPU_F32: launch_m2_ssm<T, float>(p, st); break;
+    case MCPU_BF16: launch_m2_ssm<T, bf16>(p, st); break;
+    default: launch_m2_ssm<T, f16>(p, st); break;
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int ro = rows_per_wave(p.dm);
+  if (ro == 4) launch_m2_out<T, MT, 4>(p, hf, st);
+  else if (ro == 2) launch_m2_out<T, MT, 2>(p, hf, st);
+  else launch_m2_out<T, MT, 1>(p, hf, st);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t step2_dtype(const MixerParams& p, hipStream_t st) {
+  if (p.batch <= 1) return step2_t<T, 1>(p, st);
+  if (p.batch <= 2) return step2_t<T, 2>(p, st);
+  if (p.batch <= 4) return step2_t<T, 4>(p, st);
+  return step2_t<T, 8>(p, st);
+}
+
+}  // namespace
+}  // namespace mcpu
+
+extern "C" size_t mcpu_mamba2_step_workspace_size(const mcpu_mamba2_step_args* a) {
+  if (check_step2(a) != MCPU_OK) {
+    clear_error();
+    return 0;
+  }
+  return step2_layout(a).total;
+}
+
+extern "C" int mcpu_mamba2_step(const mcpu_mamba2_step_args* a, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  clear_error();
+  if (int rc = check_step2(a)) return rc;
+  const Step2Layout w = step2_layout(a);
+  if (workspace == nullptr || workspace_bytes < w.total)
+    return fail(MCPU_ERR_INVALID, "mamba2_step: workspace of %zu bytes needed, got %zu", w.total, workspace_bytes);
+  if (int rc = mcpu_check_device()) return rc;
+  MixerParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.hidden = a->hidden;
+  p.norm_w = a->norm_weight;
+  p.in_w = a->in_w;
+  p.in_b = a->in_b;
+  p.conv_w = a->conv_w;
+  p.conv_b = a->conv_b;
+  p.conv_state = a->conv_state;
+  p.dt_b = a->dt_bias;
+  p.A = a->A;
+  p.D = a->D;
+  p.ssm_state = a->ssm_state;
+  p.gn_w = a->gate_norm_weight;
+  p.gn_eps = a->gate_norm_eps;
+  p.out_w = a->out_w;
+  p.out_b = a->out_b;
+  p.out = a->out;
+  char* ws = static_cast<char*>(workspace);
+  p.xc = reinterpret_cast<float*>(ws + w.xc);
+  p.zg = reinterpret_cast<float*>(ws + w.zg);
+  p.yv = reinterpret_cast<float*>(ws + w.yv);
+  p.batch = a->batch;
+  p.dm = a->d_model;
+  p.di = a->d_inner;
+  p.N = a->dstate;
+  p.W = a->width;
+  p.S = a->state_len;
+  p.nin = w.nin;
+  p.conv_lo = a->d_inner;
+  p.nconv = w.conv_dim;
+  p.zst = w.zst;
+  p.nh = a->nheads;
+  p.hd = a->headdim;
+  p.ng = a->ngroups;
+  p.eps = a->norm_eps;
+  p.add_residual = a->add_residual != 0;
+  p.hidden_dtype = a->hidden_dtype;
+  p.state_dtype = a->state_dtype;
+  p.out_dtype = a->out_dtype;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (a->dtype) {
+    case MCPU_F32: e = step2_dtype<float>(p, st); break;
+    case MCPU_BF16: e = step2_dtype<bf16>(p, st); break;
+    default: e = step2_dtype<f16>(p, st); break;
+  }
+  return hip_status(e, "mamba2_step launch");
 }

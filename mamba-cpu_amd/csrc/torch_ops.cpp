@@ -1394,6 +1394,119 @@ Tensor norm_linear(const Tensor& hidden, const optional<Tensor>& norm_weight, do
   return out;
 }
 
+// One decode step of a Mamba-2 block (mcpu_mamba2_step): hidden (batch,
+// d_model) -> out (batch, d_model), conv_state (batch, conv_dim, state_len)
+// and ssm_state (batch, nheads, headdim, dstate) updated in place. Sizes come
+// from the tensors: d_inner from the gated norm's weight, nheads from A,
+// headdim and dstate from ssm_state, ngroups from the conv's width
+// conv_dim = d_inner + 2 ngroups dstate. dt_bias, A (= -exp(A_log)) and D
+// float32 per head.
+Tensor mamba2_step(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, bool add_residual,
+                   bool residual_in_fp32, const Tensor& in_w, const optional<Tensor>& in_b, const Tensor& conv_w,
+                   const optional<Tensor>& conv_b, Tensor& conv_state, const optional<Tensor>& dt_bias,
+                   const Tensor& A, const optional<Tensor>& D, Tensor& ssm_state, const Tensor& gate_norm_w,
+                   double gate_eps, const Tensor& out_w, const optional<Tensor>& out_b) {
+  const char* name = "mamba_cpu::mamba2_step";
+  for (const optional<Tensor>& t : {opt(hidden), norm_weight, opt(in_w), in_b, opt(conv_w), conv_b,
+                                    opt(conv_state), dt_bias, opt(A), D, opt(ssm_state), opt(gate_norm_w),
+                                    opt(out_w), out_b})
+    check_gpu(name, t);
+  const auto T = in_w.scalar_type();
+  TORCH_CHECK_VALUE(x_dtype(T), name, " expects float32, bfloat16 or float16 weights");
+  for (const optional<Tensor>& t : {norm_weight, in_b, opt(conv_w), conv_b, opt(conv_state), opt(gate_norm_w),
+                                    opt(out_w), out_b})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == T && t->is_contiguous()), name,
+                      " expects contiguous weights, biases and conv state of one dtype");
+  for (const optional<Tensor>& t : {dt_bias, opt(A), D})
+    TORCH_CHECK_VALUE(!has(t) || (t->scalar_type() == at::kFloat && t->is_contiguous()), name,
+                      " expects contiguous float32 dt_bias, A and D");
+  TORCH_CHECK_VALUE(hidden.dim() == 2 && hidden.is_contiguous() &&
+                        (hidden.scalar_type() == T || hidden.scalar_type() == at::kFloat),
+                    name, " expects a contiguous hidden (batch, d_model) in the weights' dtype or float32");
+  TORCH_CHECK_VALUE(ssm_state.dim() == 4 && ssm_state.is_contiguous() && x_dtype(ssm_state.scalar_type()), name,
+                    " expects a contiguous ssm_state (batch, nheads, headdim, dstate)");
+  const int64_t b = hidden.size(0), dm = hidden.size(1), di = gate_norm_w.numel(), nh = A.numel();
+  const int64_t hd = ssm_state.size(2), N = ssm_state.size(3);
+  TORCH_CHECK_VALUE(conv_w.dim() == 2, name, " expects conv weight (conv_dim, width)");
+  const int64_t conv_dim = conv_w.size(0);
+  TORCH_CHECK_VALUE(conv_dim > di && (conv_dim - di) % (2 * N) == 0, name,
+                    " expects conv_dim = d_inner + 2 ngroups dstate");
+  const int64_t ng = (conv_dim - di) / (2 * N);
+  TORCH_CHECK_VALUE(ssm_state.size(0) == b && ssm_state.size(1) == nh && nh * hd == di, name,
+                    " expects ssm_state (batch, nheads, headdim, dstate) with nheads x headdim = d_inner");
+  TORCH_CHECK_VALUE(in_w.dim() == 2 && in_w.size(1) == dm && in_w.size(0) == di + conv_dim + nh, name,
+                    " expects in_proj weight (d_inner + conv_dim + nheads, d_model)");
+  TORCH_CHECK_VALUE(conv_state.dim() == 3 && conv_state.size(0) == b && conv_state.size(1) == conv_dim, name,
+                    " expects conv_state (batch, conv_dim, state_len)");
+  TORCH_CHECK_VALUE(out_w.dim() == 2 && out_w.size(0) == dm && out_w.size(1) == di, name,
+                    " expects out_proj weight (d_model, d_inner)");
+  TORCH_CHECK_VALUE((!has(norm_weight) || norm_weight->numel() == dm) && (!has(in_b) || in_b->numel() == in_w.size(0)) &&
+                        (!has(conv_b) || conv_b->numel() == conv_dim) && (!has(dt_bias) || dt_bias->numel() == nh) &&
+                        (!has(D) || D->numel() == nh) && (!has(out_b) || out_b->numel() == dm),
+                    name, " expects bias and norm vectors of their layer's width");
+  const bool res32 = add_residual && (residual_in_fp32 || hidden.scalar_type() == at::kFloat);
+  c10::DeviceGuard guard(hidden.device());
+  Tensor out = at::empty({b, dm}, hidden.options().dtype(res32 ? at::kFloat : T));
+  mcpu_mamba2_step_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.hidden = hidden.data_ptr();
+  a.norm_weight = ptr(norm_weight);
+  a.in_w = in_w.data_ptr();
+  a.in_b = ptr(in_b);
+  a.conv_w = conv_w.data_ptr();
+  a.conv_b = ptr(conv_b);
+  a.conv_state = conv_state.data_ptr();
+  a.dt_bias = fptr(dt_bias);
+  a.A = static_cast<const float*>(A.data_ptr());
+  a.D = fptr(D);
+  a.ssm_state = ssm_state.data_ptr();
+  a.gate_norm_weight = gate_norm_w.data_ptr();
+  a.out_w = out_w.data_ptr();
+  a.out_b = ptr(out_b);
+  a.out = out.data_ptr();
+  a.batch = b;
+  a.d_model = dm;
+  a.d_inner = di;
+  a.nheads = nh;
+  a.headdim = hd;
+  a.ngroups = ng;
+  a.dstate = N;
+  a.width = conv_w.size(1);
+  a.state_len = conv_state.size(2);
+  a.norm_eps = static_cast<float>(eps);
+  a.gate_norm_eps = static_cast<float>(gate_eps);
+  a.add_residual = add_residual ? 1 : 0;
+  a.residual_in_fp32 = residual_in_fp32 ? 1 : 0;
+  a.dtype = dtype_tag(T);
+  a.hidden_dtype = dtype_tag(hidden.scalar_type());
+  a.state_dtype = dtype_tag(ssm_state.scalar_type());
+  a.out_dtype = dtype_tag(out.scalar_type());
+  const size_t nws = mcpu_mamba2_step_workspace_size(&a);
+  Tensor ws = at::empty({static_cast<int64_t>(nws > 0 ? nws : 1)}, hidden.options().dtype(at::kByte));
+  check_rc(mcpu_mamba2_step(&a, ws.data_ptr(), nws, stream_of(hidden)), name);
+  return out;
+}
+
+Tensor mamba2_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps,
+                           bool add_residual, bool residual_in_fp32, const Tensor& in_w,
+                           const optional<Tensor>& in_b, const Tensor& conv_w, const optional<Tensor>& conv_b,
+                           Tensor& conv_state, const optional<Tensor>& dt_bias, const Tensor& A,
+                           const optional<Tensor>& D, Tensor& ssm_state, const Tensor& gate_norm_w,
+                           double gate_eps, const Tensor& out_w, const optional<Tensor>& out_b) {
+  Tensor out;
+  {
+    at::AutoDispatchBelowADInplaceOrView below;
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mamba_cpu::mamba2_step", "")
+                         .typed<decltype(mamba2_step)>();
+    out = op.call(hidden, norm_weight, eps, add_residual, residual_in_fp32, in_w, in_b, conv_w, conv_b,
+                  conv_state, dt_bias, A, D, ssm_state, gate_norm_w, gate_eps, out_w, out_b);
+  }
+  conv_state.unsafeGetTensorImpl()->bump_version();
+  ssm_state.unsafeGetTensorImpl()->bump_version();
+  return out;
+}
+
 Tensor mixer_step_inplace(const Tensor& hidden, const optional<Tensor>& norm_weight, double eps, bool add_residual,
                           bool residual_in_fp32, const Tensor& in_w, const optional<Tensor>& in_b,
                           const Tensor& conv_w, const optional<Tensor>& conv_b, Tensor& conv_state,
@@ -1469,6 +1582,10 @@ TORCH_LIBRARY(mamba_cpu, m) {
         "Tensor? out_b) -> Tensor");
   m.def("norm_linear(Tensor hidden, Tensor? norm_weight, float eps, Tensor weight, Tensor? bias, "
         "bool out_float32) -> Tensor");
+  m.def("mamba2_step(Tensor hidden, Tensor? norm_weight, float eps, bool add_residual, bool residual_in_fp32, "
+        "Tensor in_w, Tensor? in_b, Tensor conv_w, Tensor? conv_b, Tensor(a!) conv_state, Tensor? dt_bias, "
+        "Tensor A, Tensor? D, Tensor(b!) ssm_state, Tensor gate_norm_w, float gate_eps, Tensor out_w, "
+        "Tensor? out_b) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
@@ -1490,6 +1607,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, CUDA, m) {
   m.impl("ssd_varlen_states", &ssd_varlen_states);
   m.impl("mixer_step", &mixer_step);
   m.impl("norm_linear", &norm_linear);
+  m.impl("mamba2_step", &mamba2_step);
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
@@ -1500,6 +1618,7 @@ TORCH_LIBRARY_IMPL(mamba_cpu, Autograd, m) {
   // One decode step: no gradient flows through it.
   m.impl("mixer_step", torch::CppFunction::makeFallthrough());
   m.impl("norm_linear", torch::CppFunction::makeFallthrough());
+  m.impl("mamba2_step", torch::CppFunction::makeFallthrough());
 }
 
 TORCH_LIBRARY_IMPL(mamba_cpu, ADInplaceOrView, m) {
@@ -1507,4 +1626,5 @@ TORCH_LIBRARY_IMPL(mamba_cpu, ADInplaceOrView, m) {
   m.impl("causal_conv1d_update", &causal_conv1d_update_inplace);
   m.impl("selective_state_update", &selective_state_update_inplace);
   m.impl("mixer_step", &mixer_step_inplace);
+  m.impl("mamba2_step", &mamba2_step_inplace);
 }

@@ -138,9 +138,22 @@ class NormLinearArgs(ctypes.Structure):
     ]
 
 
+class Mamba2StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _P), ("norm_weight", _P), ("in_w", _P), ("in_b", _P), ("conv_w", _P), ("conv_b", _P),
+        ("conv_state", _P), ("dt_bias", _P), ("A", _P), ("D", _P), ("ssm_state", _P), ("gate_norm_weight", _P),
+        ("out_w", _P), ("out_b", _P), ("out", _P),
+        ("batch", _I64), ("d_model", _I64), ("d_inner", _I64), ("nheads", _I64), ("headdim", _I64),
+        ("ngroups", _I64), ("dstate", _I64), ("width", _I64), ("state_len", _I64),
+        ("norm_eps", ctypes.c_float), ("gate_norm_eps", ctypes.c_float), ("add_residual", _I32),
+        ("residual_in_fp32", _I32), ("dtype", _I32), ("hidden_dtype", _I32), ("state_dtype", _I32),
+        ("out_dtype", _I32),
+    ]
+
+
 _BLOCKS = (("scan", ScanArgs), ("conv", ConvArgs), ("conv_update", ConvUpdateArgs),
            ("state_update", StateUpdateArgs), ("ssd", SsdArgs), ("mixer_step", MixerStepArgs),
-           ("norm_linear", NormLinearArgs))
+           ("norm_linear", NormLinearArgs), ("mamba2_step", Mamba2StepArgs))
 _ARGP = {n: ctypes.POINTER(c) for n, c in _BLOCKS}
 
 lib.mcpu_last_error.restype = ctypes.c_char_p
@@ -186,6 +199,10 @@ lib.mcpu_mixer_step.argtypes = [_ARGP["mixer_step"], _P, ctypes.c_size_t, _P]
 lib.mcpu_mixer_step.restype = ctypes.c_int
 lib.mcpu_norm_linear.argtypes = [_ARGP["norm_linear"], _P]
 lib.mcpu_norm_linear.restype = ctypes.c_int
+lib.mcpu_mamba2_step_workspace_size.argtypes = [_ARGP["mamba2_step"]]
+lib.mcpu_mamba2_step_workspace_size.restype = ctypes.c_size_t
+lib.mcpu_mamba2_step.argtypes = [_ARGP["mamba2_step"], _P, ctypes.c_size_t, _P]
+lib.mcpu_mamba2_step.restype = ctypes.c_int
 
 for _name, _cls in _BLOCKS:
     _want = lib.mcpu_args_size(_name.encode())

@@ -19,11 +19,14 @@ step runs each block as one fused operator, mamba_cpu::mixer_step: RMSNorm,
 in_proj, conv update, x_proj, dt_proj, state update, out_proj and the
 residual in three kernels, with the small-batch products as matrix-vector
 kernels that read each weight once, and the final norm and lm_head as one
-more, mamba_cpu::norm_linear. It computes what the model computes; the
-products sum in another order than the GEMM library's, so logits agree to
-float32 rounding and greedy tokens match `model.generate`'s. FalconMamba
-and Mamba-2 models replay their own decode step (on this package's conv
-update and state update once mamba_cpu.hf is patched).
+more, mamba_cpu::norm_linear. Mamba-2 blocks run as
+mamba_cpu::mamba2_step: RMSNorm, in_proj, the conv update of x, B and C,
+the per-head state update, the gated RMSNorm, out_proj and the residual in
+three kernels. Both compute what the model computes; the products sum in
+another order than the GEMM library's, so logits agree to float32 rounding
+and greedy tokens match `model.generate`'s. FalconMamba models replay their
+own decode step (on this package's conv update and state update once
+mamba_cpu.hf is patched).
 """
 
 import torch
@@ -40,17 +43,25 @@ _MAX_FUSED_DSTATE = 128
 _FUSED_LDS_FLOATS = 32768
 
 
-def _fused_lds_fits(batch_size, d_model, d_inner):
+def _fused_lds_fits(batch_size, d_model, d_inner, gated=False):
     """Whether the fused step's workgroups can hold `batch_size` rows of the
     normed hidden state (plus one row of scratch) and of the conv outputs in
-    LDS, as check_step requires."""
+    LDS, as check_step requires (Mamba-2's gated norm also stages its weight
+    beside the d_inner rows: check_step2)."""
     rows = 1 if batch_size <= 1 else 2 if batch_size <= 2 else 4 if batch_size <= 4 else 8
-    return (rows + 1) * d_model <= _FUSED_LDS_FLOATS and rows * d_inner <= _FUSED_LDS_FLOATS
+    return (rows + 1) * d_model <= _FUSED_LDS_FLOATS and (rows + int(gated)) * d_inner <= _FUSED_LDS_FLOATS
 
 
 @torch.library.register_fake("mamba_cpu::norm_linear")
 def _(hidden, norm_weight, eps, weight, bias, out_float32):
     return hidden.new_empty((hidden.shape[0], weight.shape[0]), dtype=torch.float32 if out_float32 else weight.dtype)
+
+
+@torch.library.register_fake("mamba_cpu::mamba2_step")
+def _(hidden, norm_weight, eps, add_residual, residual_in_fp32, in_w, in_b, conv_w, conv_b, conv_state, dt_bias,
+      A, D, ssm_state, gate_norm_w, gate_eps, out_w, out_b):
+    f32 = add_residual and (residual_in_fp32 or hidden.dtype == torch.float32)
+    return hidden.new_empty(hidden.shape, dtype=torch.float32 if f32 else in_w.dtype)
 
 
 @torch.library.register_fake("mamba_cpu::mixer_step")
@@ -61,16 +72,18 @@ def _(hidden, norm_weight, eps, add_residual, residual_in_fp32, in_w, in_b, conv
 
 
 def _block_constants(mixer):
-    """float32 dt_proj bias, A = -exp(A_log) and D of a Mamba mixer, computed
-    once and kept on the module until one of the parameters changes."""
-    params = (mixer.A_log, mixer.D, mixer.dt_proj.bias)
+    """float32 dt bias (Mamba: dt_proj's, Mamba-2: the per-head dt_bias),
+    A = -exp(A_log) and D of a mixer, computed once and kept on the module
+    until one of the parameters changes."""
+    dt_bias = mixer.dt_bias if hasattr(mixer, "dt_bias") else mixer.dt_proj.bias
+    params = (mixer.A_log, mixer.D, dt_bias)
     key = tuple((t.data_ptr(), t._version) for t in params if t is not None)
     cached = getattr(mixer, "_mamba_cpu_step_constants", None)
     if cached is None or cached[0] != key:
         with torch.no_grad():
             A = -torch.exp(mixer.A_log.float())
             D = mixer.D.float().contiguous()
-            dtb = None if mixer.dt_proj.bias is None else mixer.dt_proj.bias.float().contiguous()
+            dtb = None if dt_bias is None else dt_bias.float().contiguous()
         cached = (key, A.contiguous(), D, dtb)
         mixer._mamba_cpu_step_constants = cached
     return cached[1:]
@@ -78,11 +91,12 @@ def _block_constants(mixer):
 
 def fused_step_supported(model, cache, batch_size):
     """Whether `model`'s decode step can run as fused block steps: a
-    transformers Mamba model on a ROCm GPU, one weight dtype, silu, at most 8
-    batch rows, widths the fused kernels take, and a cache whose conv windows
-    are not recording past inputs. Shapes the kernels would refuse keep the
-    unfused step."""
-    if model.config.model_type != "mamba" or batch_size > _MAX_FUSED_BATCH:
+    transformers Mamba or Mamba-2 model on a ROCm GPU, one weight dtype, silu,
+    at most 8 batch rows, widths the fused kernels take, and a cache whose
+    conv windows are not recording past inputs. Shapes the kernels would
+    refuse keep the unfused step."""
+    kind = model.config.model_type
+    if kind not in ("mamba", "mamba2") or batch_size > _MAX_FUSED_BATCH:
         return False
     layers = getattr(getattr(model, "backbone", None), "layers", None)
     if not layers:
@@ -92,13 +106,17 @@ def fused_step_supported(model, cache, batch_size):
         w = mx.in_proj.weight
         if w.device.type != "cuda" or mx.activation != "silu":
             return False
-        tensors = [blk.norm.weight, w, mx.in_proj.bias, mx.conv1d.weight, mx.conv1d.bias, mx.x_proj.weight,
-                   mx.dt_proj.weight, mx.out_proj.weight, mx.out_proj.bias]
+        if kind == "mamba":
+            own = [mx.x_proj.weight, mx.dt_proj.weight]
+        else:
+            own = [mx.norm.weight]
+        tensors = [blk.norm.weight, w, mx.in_proj.bias, mx.conv1d.weight, mx.conv1d.bias, mx.out_proj.weight,
+                   mx.out_proj.bias] + own
         if any(t is not None and (t.dtype != w.dtype or not t.is_contiguous()) for t in tensors):
             return False
         if w.shape[1] % 4 or mx.intermediate_size % 4 or mx.ssm_state_size > _MAX_FUSED_DSTATE \
                 or mx.conv_kernel_size > _MAX_FUSED_CONV_STATE \
-                or not _fused_lds_fits(batch_size, w.shape[1], mx.intermediate_size):
+                or not _fused_lds_fits(batch_size, w.shape[1], mx.intermediate_size, kind == "mamba2"):
             return False
         layer = cache.layers[blk.layer_idx]
         conv, ssm = layer.conv_states[0], layer.recurrent_states[0]
@@ -109,12 +127,19 @@ def fused_step_supported(model, cache, batch_size):
 
 
 def fused_block_step(block, hidden, cache):
-    """One decode step of a transformers MambaBlock: hidden (batch, d_model)
-    -> the block's output (batch, d_model), the layer's conv window and SSM
-    state in `cache` advanced in place."""
+    """One decode step of a transformers MambaBlock or Mamba2Block: hidden
+    (batch, d_model) -> the block's output (batch, d_model), the layer's conv
+    window and SSM state in `cache` advanced in place."""
     mx = block.mixer
     layer = cache.layers[block.layer_idx]
     A, D, dtb = _block_constants(mx)
+    if hasattr(mx, "dt_bias"):  # Mamba-2
+        conv_w = mx.conv1d.weight.view(mx.conv1d.weight.shape[0], -1)
+        return torch.ops.mamba_cpu.mamba2_step(
+            hidden, block.norm.weight, float(block.norm.variance_epsilon), True, bool(block.residual_in_fp32),
+            mx.in_proj.weight, mx.in_proj.bias, conv_w, mx.conv1d.bias, layer.conv_states[0], dtb, A, D,
+            layer.recurrent_states[0], mx.norm.weight, float(mx.norm.variance_epsilon), mx.out_proj.weight,
+            mx.out_proj.bias)
     conv_w = mx.conv1d.weight.view(mx.intermediate_size, -1)
     return torch.ops.mamba_cpu.mixer_step(
         hidden, block.norm.weight, float(block.norm.variance_epsilon), True, bool(block.residual_in_fp32),
@@ -136,7 +161,7 @@ def fused_head_supported(model, batch_size):
 
 
 def fused_model_step(model, token, cache):
-    """A transformers MambaForCausalLM decode step with fused blocks: token
+    """A transformers MambaForCausalLM or Mamba2ForCausalLM decode step with fused blocks: token
     (batch, 1) -> last-position logits (batch, vocab) float32, the cache
     advanced in place."""
     bb = model.backbone

@@ -61,7 +61,7 @@ def test_argument_blocks_match_the_library():
     for name, cls in (("scan", _C.ScanArgs), ("conv", _C.ConvArgs),
                       ("conv_update", _C.ConvUpdateArgs), ("state_update", _C.StateUpdateArgs),
                       ("ssd", _C.SsdArgs), ("mixer_step", _C.MixerStepArgs),
-                      ("norm_linear", _C.NormLinearArgs)):
+                      ("norm_linear", _C.NormLinearArgs), ("mamba2_step", _C.Mamba2StepArgs)):
         assert _C.lib.mcpu_args_size(name.encode()) == ctypes.sizeof(cls)
     assert _C.lib.mcpu_args_size(b"nonsense") == 0
 
@@ -88,7 +88,8 @@ def _header_field_names(struct):
                                              ("mcpu_state_update_args", "StateUpdateArgs"),
                                              ("mcpu_ssd_args", "SsdArgs"),
                                              ("mcpu_mixer_step_args", "MixerStepArgs"),
-                                             ("mcpu_norm_linear_args", "NormLinearArgs")])
+                                             ("mcpu_norm_linear_args", "NormLinearArgs"),
+                                             ("mcpu_mamba2_step_args", "Mamba2StepArgs")])
 def test_argument_block_fields_follow_the_header(struct, cls_name):
     from mamba_cpu import _C
 
@@ -641,3 +642,43 @@ def test_norm_linear_rejects_bad_arguments_before_touching_a_device():
                            (dict(norm_weight=264), _C.MCPU_ERR_INVALID, "aligned")):
         rc, msg = call(_head_args(**kw))
         assert rc == code and word in msg, (kw, rc, msg)
+
+
+def _m2_args(**kw):
+    from mamba_cpu import _C
+
+    a = _C.Mamba2StepArgs()
+    for f in ("hidden", "in_w", "conv_w", "conv_state", "A", "ssm_state", "gate_norm_weight", "out_w", "out"):
+        setattr(a, f, 256)  # non-NULL placeholders: never dereferenced
+    a.batch, a.d_model, a.d_inner, a.nheads, a.headdim, a.ngroups, a.dstate = 4, 768, 1536, 24, 64, 1, 128
+    a.width, a.state_len, a.norm_eps, a.gate_norm_eps = 4, 4, 1e-5, 1e-5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_mamba2_step_rejects_bad_arguments_before_touching_a_device():
+    """Argument checks of mcpu_mamba2_step, and its workspace: the conv
+    outputs (x, B, C), the gate and dt rows (padded to a multiple of 4) and
+    the scan output, float32 per batch row."""
+    from mamba_cpu import _C
+
+    L = _C.lib
+    step = lambda a: _rc(L.mcpu_mamba2_step, ctypes.byref(a), None, 0, None)  # noqa: E731
+    assert _rc(L.mcpu_mamba2_step, None, None, 0, None)[0] == _C.MCPU_ERR_INVALID
+    for kw, code, word in ((dict(gate_norm_weight=None), _C.MCPU_ERR_INVALID, "required"),
+                           (dict(d_inner=1500), _C.MCPU_ERR_INVALID, "nheads x headdim"),
+                           (dict(ngroups=5), _C.MCPU_ERR_INVALID, "ngroups"),
+                           (dict(batch=9), _C.MCPU_ERR_UNSUPPORTED, "batch"),
+                           (dict(dstate=256), _C.MCPU_ERR_UNSUPPORTED, "dstate"),
+                           (dict(width=9), _C.MCPU_ERR_UNSUPPORTED, "conv width"),
+                           (dict(batch=8, d_model=4096), _C.MCPU_ERR_UNSUPPORTED, "LDS"),
+                           (dict(dtype=5), _C.MCPU_ERR_INVALID, "dtype"),
+                           (dict(out_w=264), _C.MCPU_ERR_INVALID, "aligned")):
+        rc, msg = step(_m2_args(**kw))
+        assert rc == code and word in msg, (kw, rc, msg)
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    want = al(4 * 4 * (1536 + 256)) + al(4 * 4 * 1560) + al(4 * 4 * 1536)
+    assert L.mcpu_mamba2_step_workspace_size(ctypes.byref(_m2_args())) == want
+    rc, msg = step(_m2_args())
+    assert rc == _C.MCPU_ERR_INVALID and "workspace" in msg

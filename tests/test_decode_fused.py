@@ -25,8 +25,14 @@ mamba_cpu.decode) against transformers' own decode step.
   bfloat16 rows (results rounded to bfloat16: rtol 1e-2, atol 1e-2 of the
   largest), widths 32 to 2560 (one and two passes over d_in), batch 1 to 8,
   with and without norm weight and bias, at the 50280-word vocabulary;
-- the captured graph against eager fused steps, bitwise, and the torch.library
-  opcheck of both operators.
+- Mamba-2 (mamba_cpu::mamba2_step): one fused block step against the
+  block's own recurrent step (its kernels routed to this package) at batch 1
+  to 8, float32 and bfloat16, a small model (2 groups, dstate 16) and the
+  Mamba-2 130M width (24 heads x 64, dstate 128; same tolerances as Mamba);
+  8 fused decode steps of a two-layer 130M-width model against transformers
+  on the CPU (logits and every cache tensor, tolerances as Mamba's);
+- the captured graph against eager fused steps, bitwise (Mamba and Mamba-2),
+  and the torch.library opcheck of every operator.
 """
 
 import copy
@@ -49,6 +55,10 @@ TINY = dict(vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=8, co
 W1024 = dict(num_hidden_layers=1, hidden_size=1024, state_size=16, expand=2, conv_kernel=4, vocab_size=64)
 W2560 = dict(num_hidden_layers=1, hidden_size=2560, state_size=16, expand=2, conv_kernel=4, vocab_size=64)
 CFGS = {"tiny": TINY, "768": W130, "1024": W1024, "2560": W2560}
+M2_TINY = dict(vocab_size=64, hidden_size=64, num_hidden_layers=2, num_heads=4, head_dim=32, state_size=16,
+               n_groups=2, expand=2, conv_kernel=4, chunk_size=16)
+M2_130 = dict(vocab_size=50280, hidden_size=768, num_hidden_layers=2, num_heads=24, head_dim=64, state_size=128,
+              n_groups=1, expand=2, conv_kernel=4, chunk_size=256)
 
 
 @pytest.fixture(autouse=True)
@@ -198,3 +208,81 @@ def test_opcheck_norm_linear():
     args = (torch.randn(3, 32, generator=gen, device=DEV), torch.rand(32, generator=gen, device=DEV) + 0.5, 1e-5,
             torch.randn(70, 32, generator=gen, device=DEV), None, True)
     torch.library.opcheck(torch.ops.mamba_cpu.norm_linear.default, args)
+
+
+def mamba2(cfg, dtype=torch.float32, seed=0):
+    torch.manual_seed(seed)
+    return transformers.Mamba2ForCausalLM(transformers.Mamba2Config(**cfg)).to(DEV, dtype).eval()
+
+
+@pytest.mark.parametrize("width,batch", [("tiny", 1), ("tiny", 3), ("130m", 4), ("tiny", 8), ("130m", 8)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@torch.no_grad()
+def test_fused_mamba2_block_step_matches_the_block(width, batch, dtype):
+    model = mamba2(M2_TINY if width == "tiny" else M2_130, dtype)
+    vocab = model.config.vocab_size
+    cache = model(ids((batch, 12), vocab).to(DEV), use_cache=True).cache_params
+    assert dec.fused_step_supported(model, cache, batch)
+    ref_cache = copy.deepcopy(cache)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    for blk in model.backbone.layers:
+        h = torch.randn(batch, model.config.hidden_size, generator=gen, device=DEV).to(dtype)
+        got = dec.fused_block_step(blk, h, cache)
+        want = blk(h[:, None], cache_params=ref_cache)[:, 0]
+        assert got.dtype == want.dtype and got.shape == want.shape
+        if dtype == torch.float32:
+            tol = (1e-4, 1e-5) if model.config.hidden_size <= 64 else (1e-4, 1e-3)
+        else:
+            tol = (2e-2, 2e-2)
+        assert_close_report(got, want, *tol, f"layer {blk.layer_idx} out")
+        layer, ref = cache.layers[blk.layer_idx], ref_cache.layers[blk.layer_idx]
+        assert_close_report(layer.conv_states[0], ref.conv_states[0], *tol, "conv state")
+        assert_close_report(layer.recurrent_states[0], ref.recurrent_states[0], *tol, "ssm state")
+
+
+@torch.no_grad()
+def test_fused_mamba2_decode_matches_transformers_on_the_cpu():
+    model = mamba2(M2_130)
+    cpu_model = copy.deepcopy(model).cpu()
+    prompt, toks = ids((4, 16), 50280), ids((4, 8), 50280, seed=2)
+    cache = model(prompt.to(DEV), use_cache=True).cache_params
+    cpu_cache = cpu_model(prompt, use_cache=True).cache_params
+    assert dec.fused_step_supported(model, cache, 4)
+    for i in range(toks.shape[1]):
+        got = dec.fused_model_step(model, toks[:, i:i + 1].to(DEV), cache)
+        want = cpu_model(input_ids=toks[:, i:i + 1], cache_params=cpu_cache, use_cache=True).logits[:, -1]
+        assert_close_report(got, want, 1e-4, 1e-4, f"logits step {i}")
+    for k, (g, w) in enumerate(zip(states(cache), states(cpu_cache))):
+        assert_close_report(g, w, 1e-4, 1e-3, f"cache tensor {k}")
+
+
+@torch.no_grad()
+def test_mamba2_graph_replays_equal_eager_fused_steps():
+    model = mamba2(M2_TINY)
+    prompt, toks = ids((2, 9), 64).to(DEV), ids((2, 10), 64, seed=2).to(DEV)
+    cache = model(prompt, use_cache=True).cache_params
+    eager = [dec.fused_model_step(model, toks[:, i:i + 1], cache).clone() for i in range(toks.shape[1])]
+    graphed = dec.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 2)
+    assert graphed.fused
+    for i in range(toks.shape[1]):
+        graphed.token.copy_(toks[:, i:i + 1])
+        got = graphed.replay().clone()
+        if i % 3 == 0:
+            torch.cuda.synchronize()
+        assert torch.equal(got, eager[i]), f"replay {i}"
+
+
+def test_opcheck_mamba2_step():
+    model = mamba2(M2_TINY)
+    with torch.no_grad():
+        cache = model(ids((3, 5), 64).to(DEV), use_cache=True).cache_params
+    blk = model.backbone.layers[0]
+    mx = blk.mixer
+    A, D, dtb = dec._block_constants(mx)
+    layer = cache.layers[0]
+    h = torch.randn(3, 64, device=DEV)
+    args = (h, blk.norm.weight.detach(), 1e-5, True, True, mx.in_proj.weight.detach(), None,
+            mx.conv1d.weight.detach().view(mx.conv1d.weight.shape[0], -1), mx.conv1d.bias.detach(),
+            layer.conv_states[0], dtb, A, D, layer.recurrent_states[0], mx.norm.weight.detach(), 1e-5,
+            mx.out_proj.weight.detach(), None)
+    torch.library.opcheck(torch.ops.mamba_cpu.mamba2_step.default, args)
