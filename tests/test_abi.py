@@ -682,3 +682,31 @@ def test_mamba2_step_rejects_bad_arguments_before_touching_a_device():
     assert L.mcpu_mamba2_step_workspace_size(ctypes.byref(_m2_args())) == want
     rc, msg = step(_m2_args())
     assert rc == _C.MCPU_ERR_INVALID and "workspace" in msg
+
+
+def test_fused_step_lds_rule_is_the_librarys():
+    """mamba_cpu.decode sends a model to the fused step only where the
+    library takes its shape, so that shapes the kernels refuse keep the
+    unfused step instead of raising: its LDS rule must accept exactly what
+    check_step (Mamba) and check_step2 (Mamba-2) accept. A workspace size of
+    0 is the library's refusal. Widths of the Mamba family up to 8192 at
+    every batch size up to 8; among them d_inner 4096 at batch 8, exactly
+    at the limit, and 5120 (Mamba-2.8B) at batch 5-8, past it."""
+    from mamba_cpu import _C
+
+    import mamba_cpu.decode as dec
+
+    L = _C.lib
+    seen = set()
+    for batch in range(1, 9):
+        for dm in (256, 768, 1024, 1536, 2048, 2560, 4096):
+            di = 2 * dm
+            a = _step_args(batch=batch, d_model=dm, d_inner=di, dt_rank=(dm + 15) // 16)
+            takes = L.mcpu_mixer_step_workspace_size(ctypes.byref(a)) > 0
+            assert dec._fused_lds_fits(batch, dm, di) == takes, ("mamba", batch, dm)
+            seen.add(takes)
+            m2 = _m2_args(batch=batch, d_model=dm, d_inner=di, nheads=di // 64, headdim=64)
+            takes = L.mcpu_mamba2_step_workspace_size(ctypes.byref(m2)) > 0
+            assert dec._fused_lds_fits(batch, dm, di, gated=True) == takes, ("mamba2", batch, dm)
+    assert seen == {True, False}
+    assert dec._fused_lds_fits(8, 2048, 4096) and not dec._fused_lds_fits(5, 2560, 5120)

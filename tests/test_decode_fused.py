@@ -17,8 +17,10 @@ mamba_cpu.decode) against transformers' own decode step.
   them by 2e-6 of that; bfloat16: 2e-2 / 2e-2).
   The widths cover both ways the step runs x_proj: as partial sums of the
   in_proj workgroups (32, 768 and 1024, the last with 4 in_proj rows per
-  wave) and, at the Mamba-2.8B width (d_inner 5120, dt_rank 160), as its own
-  product;
+  wave) and, at d_inner 4096 and the Mamba-2.8B width (d_inner 5120, dt_rank
+  160), as its own product. d_inner 4096 at batch 8 stages 8 x 4096 floats,
+  the most a workgroup's LDS takes; the 5120 width at batch 8 is past it and
+  keeps the unfused step (tokens equal to transformers' generate);
 - the final norm and lm_head as one launch (mamba_cpu::norm_linear) against
   transformers' MambaRMSNorm and nn.Linear on the GPU: float32 (rtol 1e-5,
   atol 1e-5 of the largest logit) and bfloat16 weights with float32 or
@@ -53,8 +55,9 @@ DEV = "cuda"
 W130 = dict(num_hidden_layers=2, hidden_size=768, state_size=16, expand=2, conv_kernel=4, vocab_size=50280)
 TINY = dict(vocab_size=64, hidden_size=32, num_hidden_layers=2, state_size=8, conv_kernel=4, expand=2)
 W1024 = dict(num_hidden_layers=1, hidden_size=1024, state_size=16, expand=2, conv_kernel=4, vocab_size=64)
+W2048 = dict(num_hidden_layers=1, hidden_size=2048, state_size=16, expand=2, conv_kernel=4, vocab_size=64)
 W2560 = dict(num_hidden_layers=1, hidden_size=2560, state_size=16, expand=2, conv_kernel=4, vocab_size=64)
-CFGS = {"tiny": TINY, "768": W130, "1024": W1024, "2560": W2560}
+CFGS = {"tiny": TINY, "768": W130, "1024": W1024, "2048": W2048, "2560": W2560}
 M2_TINY = dict(vocab_size=64, hidden_size=64, num_hidden_layers=2, num_heads=4, head_dim=32, state_size=16,
                n_groups=2, expand=2, conv_kernel=4, chunk_size=16)
 M2_130 = dict(vocab_size=50280, hidden_size=768, num_hidden_layers=2, num_heads=24, head_dim=64, state_size=128,
@@ -101,7 +104,7 @@ def test_fused_decode_matches_transformers_on_the_cpu():
 
 
 @pytest.mark.parametrize("width,batch", [("tiny", 1), ("tiny", 3), ("768", 4), ("tiny", 8), ("768", 8),
-                                         ("1024", 2), ("2560", 2)])
+                                         ("1024", 2), ("2048", 8), ("2560", 2)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @torch.no_grad()
 def test_fused_block_step_matches_the_block(width, batch, dtype):
@@ -154,6 +157,23 @@ def test_unsupported_models_keep_the_unfused_step():
     falcon = transformers.FalconMambaForCausalLM(transformers.FalconMambaConfig(**TINY)).to(DEV).eval()
     fcache = falcon(ids((2, 4), 64).to(DEV), use_cache=True).cache_params
     assert not dec.fused_step_supported(falcon, fcache, 2)
+
+
+@torch.no_grad()
+def test_widths_past_the_lds_limit_keep_the_unfused_step():
+    """At the Mamba-2.8B width (d_inner 5120) batch 8 needs more LDS than a
+    workgroup holds (8 x 5120 floats), so decoding keeps the unfused step and
+    still matches transformers' own; at batch 2 the same model is fused."""
+    model = mamba(W2560)
+    prompt = ids((8, 5), 64).to(DEV)
+    assert dec.fused_step_supported(model, model(prompt[:2], use_cache=True).cache_params, 2)
+    cache = model(prompt, use_cache=True).cache_params
+    assert not dec.fused_step_supported(model, cache, 8)
+    step = dec.GraphedDecodeStep(model, cache, 8)
+    assert not step.fused
+    toks = dec.greedy_generate(model, prompt, 3)
+    want = model.generate(prompt, max_new_tokens=3, min_new_tokens=3, do_sample=False)
+    assert torch.equal(toks.cpu(), want.cpu())
 
 
 def test_opcheck_mixer_step():
