@@ -196,11 +196,16 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
 
     float pacc[kScanBlockT];
     // CORR: the block's start state and the product of its decay factors.
+    // Without outputs only the block's end state is needed, so the block runs
+    // from a zero state instead and the start state's decay is added at its
+    // end: the same sum without the per-step product.
+    constexpr bool LOCAL = CORR && !WRITE_OUT;
     float hstart[SPL], prod[SPL];
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {
       hstart[s] = h[s];
       prod[s] = 1.f;
+      if (LOCAL) h[s] = 0.f;
     }
     auto step = [&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -211,7 +216,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       for (int s = 0; s < SPL; ++s) {
         const float a = fast_exp2(dti * A2[s]);
         h[s] = fmaf(a, h[s], dtui * Bv[s][i]);
-        if (CORR) prod[s] *= a;
+        if (CORR && !LOCAL) prod[s] *= a;
         if (WRITE_OUT) acc = fmaf(h[s], Cv[s][i], acc);
       }
       pacc[i] = acc;
@@ -229,7 +234,8 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
       // The start state decays by exp(A * the block's summed step).
       const float bdt = row_allreduce16(j < nvalid ? dt : 0.f);
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) h[s] = fmaf(fast_exp2(A2[s] * bdt) - prod[s], hstart[s], h[s]);
+      for (int s = 0; s < SPL; ++s)
+        h[s] = fmaf(LOCAL ? fast_exp2(A2[s] * bdt) : fast_exp2(A2[s] * bdt) - prod[s], hstart[s], h[s]);
     }
     float y = 0.f, yg = 0.f;
     if (WRITE_OUT) {
