@@ -962,9 +962,10 @@ def ssd_pass(torch, dev, xdt):
 
 def model_pass(torch, dev, what):
     """A short fixed run of the Mamba-130M architecture for kernel traces
-    (rocprofv3 --kernel-trace): `train` = 3 warm-up + 5 training steps at
-    4 x 256; `decode` = the 4 x 16 prompt, then 64 graph-replayed greedy
-    steps. `mamba2-prefill` = 4 prefills of 4 x 1024 tokens and
+    (rocprofv3 --kernel-trace): `train` = 8 training steps at 4 x 256;
+    `prefill` = 4 prefills of 4 x 1024 tokens (logits at every position, as
+    the bench's prefill leg); `decode` = the 4 x 16 prompt, then 64
+    graph-replayed greedy steps. `mamba2-prefill` = 4 prefills of 4 x 1024 tokens and
     `mamba2-decode` = the 4 x 16 prompt then 32 graph-replayed greedy steps,
     on the Mamba-2 130M architecture."""
     import transformers
@@ -995,6 +996,12 @@ def model_pass(torch, dev, what):
         for _ in range(8):
             model(ids, labels=ids).loss.backward()
             model.zero_grad(set_to_none=True)
+    elif what == "prefill":
+        model.eval()
+        ids = torch.randint(0, 50280, (4, 1024), device=dev)
+        with torch.no_grad():
+            for _ in range(4):
+                model(ids)
     else:
         model.eval()
         ids = torch.randint(0, 50280, (4, 16), device=dev)
@@ -1017,7 +1024,7 @@ def main():
     ap.add_argument("--ssd-pass", nargs="?", const="bf16", choices=["bf16", "fp32"],
                     help="only run 3 forward+backward passes of the SSD workload (bf16 by default) for "
                          "kernel traces")
-    ap.add_argument("--model-pass", choices=["train", "decode", "mamba2-prefill", "mamba2-decode"],
+    ap.add_argument("--model-pass", choices=["train", "decode", "prefill", "mamba2-prefill", "mamba2-decode"],
                     help="only run a short Mamba-130M train or graph-decode sequence, or a Mamba-2 130M "
                          "prefill or graph-decode sequence, for kernel traces")
     args = ap.parse_args()
