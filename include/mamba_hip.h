@@ -27,7 +27,7 @@ extern "C" {
 enum {
   MCPU_OK = 0,
   MCPU_ERR_INVALID = 1,     /* bad argument: shape, stride, null pointer, size */
-  MCPU_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. dstate > 64) */
+  MCPU_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. dstate > 4096) */
   MCPU_ERR_DEVICE = 3,      /* current device is not gfx950 */
   MCPU_ERR_HIP = 4          /* a HIP runtime call or launch failed */
 };
@@ -123,8 +123,12 @@ typedef struct mcpu_scan_args {
      and the imaginary part is the next float (mamba_ssm's real
      (batch, ngroups, dstate, 2 seqlen) layout, or a complex tensor's view);
      last_state, dlast_state and the checkpoints hold complex pairs; dB/dC are
-     (batch, ngroups, seqlen, dstate, 2) contiguous. dstate <= 32; ysave and
-     the forward workspace are not used. */
+     (batch, ngroups, seqlen, dstate, 2) contiguous. dstate up to 4096:
+     above 32 the states run in 32-state slices, and the forward then needs
+     mcpu_selective_scan_fwd_workspace_size() bytes of workspace and, with z,
+     writes y before the gate to ysave when given (a sliced backward reads
+     it; without it the backward runs that forward itself). At 32 states or
+     fewer, ysave and the forward workspace are not used. */
   int32_t complex_a;
   /* Backward workgroup width in waves: 0 = chosen by the library from the
      shape (the production setting); 4, 8 or 12 pins it (dstate <= 16, real A
