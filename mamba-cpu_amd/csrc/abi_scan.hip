@@ -298,6 +298,12 @@ BwdLayout bwd_layout(const mcpu_scan_args* a) {
       w.fwd_bytes = fwd_layout(fwd_params(a), w.own_ysave).total;
       w.fwd = take(w.fwd_bytes);
     }
+  } else if (w.own_ckpt) {
+    // The states-only forward that makes the checkpoints runs with the
+    // forward's own time chunks (its chunk summaries go here), so that its
+    // checkpoints are bit-identical to those a forward call saves.
+    w.fwd_bytes = fwd_layout(fwd_params(a), false).total;
+    if (w.fwd_bytes > 0) w.fwd = take(w.fwd_bytes);
   }
   w.total = off;
   return w;
@@ -567,8 +573,15 @@ extern "C" int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace,
         return rc;
     }
   } else if (w.own_ckpt) {
-    ScanParams pf = make_params(a, scan_fwd_waves());  // states-only forward: block checkpoints
+    // States-only forward for the block checkpoints, time-chunked as a
+    // forward call is.
+    ScanParams pf = fwd_params(a);
     pf.ckpt = p.ckpt;
+    if (pf.nchunk > 1) {
+      const FwdLayout fw = fwd_layout(pf, false);
+      pf.sum_h = reinterpret_cast<float*>(ws + w.fwd + fw.sum_h);
+      pf.sum_dt = reinterpret_cast<float*>(ws + w.fwd + fw.sum_dt);
+    }
     if (int rc = hip_status(scan_fwd_launch(pf, a->dtype, false, st), "selective_scan_bwd ckpt launch"))
       return rc;
   }

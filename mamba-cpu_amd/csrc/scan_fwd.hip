@@ -196,10 +196,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
 
     float pacc[kScanBlockT];
     // CORR: the block's start state and the product of its decay factors.
-    // Without outputs only the block's end state is needed, so the block runs
-    // from a zero state instead and the start state's decay is added at its
-    // end: the same sum without the per-step product.
-    constexpr bool LOCAL = CORR && !WRITE_OUT;
+    // The summary pass needs only each block's end state, so its blocks run
+    // from a zero state instead and the start state's decay is added at the
+    // end: the same sum without the per-step product. (The states-only mode
+    // keeps the product form, so that its checkpoints are bit-identical to
+    // those of the output mode.)
+    constexpr bool LOCAL = CORR && MODE == kFwdSummary;
     float hstart[SPL], prod[SPL];
 #pragma unroll
     for (int s = 0; s < SPL; ++s) {

@@ -464,6 +464,26 @@ def test_ckpt_and_recompute_backward_agree():
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
 
 
+def test_recompute_checkpoints_equal_a_chunked_forwards():
+    """The reference-schema backward makes its own checkpoints with a
+    states-only forward; on a time-chunked shape with slowly decaying states
+    (A = -U(0, 1), where the chunked forward's per-block decay correction does
+    not round away) they must equal the checkpoints a forward call saves, so
+    both backwards agree bit for bit."""
+    inp = make_inputs(1, 32, 1000, 16, None, True, True, True, torch.float32)
+    inp["A"] = -torch.rand(32, 16, generator=torch.Generator().manual_seed(3)).to(DEV)
+    Bk = inp["B"][:, None].transpose(-1, -2).contiguous()
+    Ck = inp["C"][:, None].transpose(-1, -2).contiguous()
+    args = (inp["u"], inp["delta"], inp["A"], Bk, Ck, inp["D"], inp["z"], inp["delta_bias"], True)
+    out, last, ckpt, ysave = torch.ops.mamba_cpu.selective_scan_fwd_ckpt(*args)
+    dout = torch.randn_like(out)
+    dlast = torch.randn_like(last)
+    g_own = torch.ops.mamba_cpu.selective_scan_bwd(*args, dout, dlast)
+    g_saved = torch.ops.mamba_cpu.selective_scan_bwd_ckpt(*args, dout, dlast, ckpt, ysave.new_empty(0))
+    for a, b in zip(g_own, g_saved):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("seqlen", [100, 1000, 4096])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_long_sequence_time_chunks(seqlen, dtype):
