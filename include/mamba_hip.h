@@ -157,7 +157,12 @@ size_t mcpu_selective_scan_fwd_workspace_size(const mcpu_scan_args* a);
 int mcpu_selective_scan_fwd(const mcpu_scan_args* a, void* workspace, size_t workspace_bytes,
                             void* stream);
 
-/* Workspace bytes needed by mcpu_selective_scan_bwd for these arguments. */
+/* Workspace bytes needed by mcpu_selective_scan_bwd for these arguments:
+ * the dB/dC/dA partial sums, the adjoint's chunk summaries when time-chunked
+ * and, when ckpt is NULL, the block checkpoints and the chunk summaries of
+ * the forward that makes them (that forward is time-chunked as a forward call
+ * given its workspace is, so the checkpoints equal that call's bit for
+ * bit). */
 size_t mcpu_selective_scan_bwd_workspace_size(const mcpu_scan_args* a);
 
 /* Backward. Replaces selective_scan_bwd_f32 (csrc/selective_scan.h:65) as
@@ -176,7 +181,7 @@ int mcpu_selective_scan_bwd(const mcpu_scan_args* a, void* workspace, size_t wor
  * the reference; it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops that forbid allocation). It runs
  * the kernels of mcpu_selective_scan_bwd with their scratch (partial sums,
- * chunk summaries, and block checkpoints when ckpt is NULL) in a fixed
+ * chunk summaries, and when ckpt is NULL the block checkpoints) in a fixed
  * library array of MCPU_NOALLOC_SCRATCH_BYTES per device (reserved by the
  * first call on each device, see above). Results equal
  * mcpu_selective_scan_bwd's. Returns MCPU_ERR_UNSUPPORTED, before any device
