@@ -635,8 +635,10 @@ def mamba2_130m(torch, dev, iters=3):
     package's kernels, the same prefill through transformers' own torch
     kernels on this GPU (one pass: they build (chunk x chunk x heads x dstate)
     intermediates), the largest logit difference between the two, one
-    training step at 4 x 256, and 128 greedy decode steps at batch 4 through
-    generate and graph-replayed (prompt and capture included). The reference
+    training step at 4 x 256, 128 greedy decode steps at batch 4 through
+    generate and graph-replayed (prompt and capture included), and the
+    captured step alone replayed, with fused layer steps and with the model's
+    own step. The reference
     has no Mamba-2 path, so there is no CPU leg."""
     import transformers
 
@@ -691,6 +693,17 @@ def mamba2_130m(torch, dev, iters=3):
             mamba_cpu.decode.greedy_generate(model, prompt, 128)
             torch.cuda.synchronize()
             res["decode_graph_ms_per_step"] = round((time.perf_counter() - t0) / 128 * 1e3, 3)
+            # The captured step alone, replayed back to back: fused layer
+            # steps (mamba_cpu::mamba2_step) and the model's own step.
+            for fused in (True, False):
+                step = mamba_cpu.decode.GraphedDecodeStep(model, model(prompt, use_cache=True).cache_params, 4,
+                                                          fused=fused)
+                step.token.copy_(prompt[:, -1:])
+                ms = _events_ms(torch, torch.cuda.current_stream(dev), step.replay, 50)
+                res["decode_graph_replay_ms_per_step" + ("" if fused else "_model_step")] = round(ms, 4)
+                if fused:
+                    res["decode_graph_fused_blocks"] = step.fused
+                del step
     finally:
         mamba_cpu.hf.unpatch_transformers()
     with torch.no_grad():
