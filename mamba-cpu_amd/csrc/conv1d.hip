@@ -521,31 +521,18 @@ __device__ __forceinline__ void ld4(const void* base, int64_t idx, float* v) {
   }
 }
 
-// NT: a non-temporal store (the line is not kept in the caches). The backward's
-// dx stores take it (measured 114 against 125 us in fp32 at batch 8, dim 3072,
-// seqlen 2048); the forward's output stores were slower with it (78 against 71).
-template <typename T, bool NT = false>
+template <typename T>
 __device__ __forceinline__ void st4(void* base, int64_t idx, const float* v) {
-  typedef float vf4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t vu2 __attribute__((ext_vector_type(2)));
   if constexpr (sizeof(T) == 4) {
-    const vf4 q = {v[0], v[1], v[2], v[3]};
-    vf4* dst = reinterpret_cast<vf4*>(static_cast<float*>(base) + idx);
-    if constexpr (NT) __builtin_nontemporal_store(q, dst);
-    else *dst = q;
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (std::is_same_v<T, bf16>) {
+    *reinterpret_cast<uint2*>(static_cast<T*>(base) + idx) =
+        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   } else {
-    vu2 q;
-    if constexpr (std::is_same_v<T, bf16>) {
-      q = vu2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    } else {
-      uint32_t h[4];
+    uint32_t h[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) h[i] = __builtin_bit_cast(uint16_t, from_f32<T>(v[i]));
-      q = vu2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    }
-    vu2* dst = reinterpret_cast<vu2*>(static_cast<T*>(base) + idx);
-    if constexpr (NT) __builtin_nontemporal_store(q, dst);
-    else *dst = q;
+    for (int i = 0; i < 4; ++i) h[i] = __builtin_bit_cast(uint16_t, from_f32<T>(v[i]));
+    *reinterpret_cast<uint2*>(static_cast<T*>(base) + idx) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
 }
 
@@ -708,7 +695,7 @@ __global__ void __launch_bounds__(256) conv_bwd_vt_kernel(const ConvParams p) {
     }
     const int64_t xr = c.b * p.sdx[0] + c.d * p.sdx[1];
 #pragma unroll
-    for (int q = 0; q < VT; q += 4) st4<T, true>(p.dx, xr + g.t0 + q, dx + q);
+    for (int q = 0; q < VT; q += 4) st4<T>(p.dx, xr + g.t0 + q, dx + q);
     if (g.t0 == 0 && p.dinit != nullptr) {
       // dX[s] for s in [-(W-1), 0): the initial-state columns.
 #pragma unroll
@@ -932,7 +919,7 @@ __device__ __forceinline__ void conv_bwd_cl_step(const ConvParams& p, const Conv
       }
       dx[c] = acc;
     }
-    st4<T, true>(p.dx, g.b * p.sdx[0] + g.d0 + s * p.sdx[2], dx);
+    st4<T>(p.dx, g.b * p.sdx[0] + g.d0 + s * p.sdx[2], dx);
   }
 #pragma unroll
   for (int k = 0; k < W - 1; ++k) {
