@@ -173,8 +173,8 @@ def valu_roofline(launch_ms, counters, elements=None, source=COUNTERS_JSON):
         "frac": round(rate / VALU_PEAK_G, 4),
         "per_state_step": round(counters.get("valu_wave_instructions_per_launch", 0) * 64
                                 / (elements or B_ * D_ * L_ * N_), 2),
-        "note": "peak at the 2.4 GHz peak clock; the chip runs at about 2.1 GHz under this load, "
-                "so the attainable fraction is about 0.88",
+        "note": "peak at the 2.4 GHz peak clock, which settled clocks under sustained load come "
+                "close to; the profiler's counter runs, one kernel at a time, ran at about 2.1 GHz",
         "source": "profiles/" + source,
     }
 
@@ -197,10 +197,19 @@ def _bind_valu(r, ms, name, elements):
         r["valu"] = v
 
 
-def _events_ms(torch, stream, fn, iters):
+def _events_ms(torch, stream, fn, iters, settle_s=0.03):
     """Average GPU time per call of fn() over iters back-to-back calls, from
-    HIP events recorded on the stream the ops launch on."""
+    HIP events recorded on the stream the ops launch on. Untimed calls of
+    fn() run first for at least settle_s seconds (at least one call): the
+    GPU's clocks ramp up over some tens of milliseconds of load, and a leg
+    timed right after the host-side work before it would time the ramp."""
+    t_end = time.perf_counter() + settle_s
     fn()
+    torch.cuda.synchronize()
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
