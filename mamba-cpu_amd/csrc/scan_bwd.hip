@@ -54,10 +54,15 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   // the checkpoints, the chunk summaries and the dA/dB/dC layouts.
   const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t kb0 = chunk * p.chunk_blocks;
-  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
-  const int64_t kl = kb1 - 1;  // the chunk's last block
-  const int64_t t_last = kl * T;
+  // Block indices as uniform 32-bit values: the host's 32-bit tile-offset
+  // check keeps seqlen under 2^32 / (element size * channels per tile), so
+  // they stay far below 2^31, and the loop's tests on them become scalar
+  // compares (the scalar unit has no signed 64-bit compare).
+  const int kb0 = __builtin_amdgcn_readfirstlane(static_cast<int>(chunk * p.chunk_blocks));
+  const int kb1 = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk));
+  const int kl = kb1 - 1;  // the chunk's last block
+  const int64_t t_last = static_cast<int64_t>(kl) * T;
   // Row of the per-(chunk, batch, channel) partials of dA, dD, ddelta_bias.
   const int64_t prow = (chunk * p.batch + rc.b) * p.dim + rc.d;
 
@@ -205,10 +210,10 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
   __builtin_amdgcn_s_waitcnt(0);
 
   // One block; FULL = all 16 steps exist (every block but possibly the last).
-  auto block = [&](auto FULL, int64_t k, int nvalid) {
+  auto block = [&](auto FULL, int k, int nvalid) {
     constexpr bool full = decltype(FULL)::value;
     const int buf = static_cast<int>(k & 1);
-    const int64_t t0 = k * T;
+    const int64_t t0 = static_cast<int64_t>(k) * T;
     // The block before this one (always full), or this block again from the
     // chunk's first block (guarded like this block).
     // Full blocks load at the cursor either way (block k - 1, or block k
@@ -398,7 +403,7 @@ __global__ void __launch_bounds__(64 * W) scan_bwd_kernel(const ScanParams p) {
     if (nlast == T) block(std::true_type{}, kl, T);
     else block(std::false_type{}, kl, nlast);
   }
-  for (int64_t k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
+  for (int k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
 
   if (rc.active) {
 #pragma unroll
@@ -520,10 +525,11 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   const RowCtx rc = scan_row_ctx<W>(p, sc.bx / p.nsum, wave, r);
   const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t kb0 = unit * p.sum_blocks;
-  const int64_t kb1 = kb0 + p.sum_blocks < p.nblk ? kb0 + p.sum_blocks : p.nblk;
-  const int64_t kl = kb1 - 1;
-  const int64_t t_last = kl * T;
+  const int kb0 = __builtin_amdgcn_readfirstlane(static_cast<int>(unit * p.sum_blocks));
+  const int kb1 = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(kb0 + p.sum_blocks < p.nblk ? kb0 + p.sum_blocks : p.nblk));
+  const int kl = kb1 - 1;
+  const int64_t t_last = static_cast<int64_t>(kl) * T;
 
   float A2[SPL], gh[SPL];
 #pragma unroll
@@ -575,10 +581,10 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   __syncthreads();
   __builtin_amdgcn_s_waitcnt(0);
 
-  auto block = [&](auto FULL, int64_t k, int nvalid) {
+  auto block = [&](auto FULL, int k, int nvalid) {
     constexpr bool full = decltype(FULL)::value;
     const int buf = static_cast<int>(k & 1);
-    const int64_t t0 = k * T;
+    const int64_t t0 = static_cast<int64_t>(k) * T;
     // Full blocks load at the cursor either way (block k - 1, or block k
     // again from the chunk's first block, where the cursor stayed), so one
     // branch-free fetch covers both.
@@ -618,7 +624,7 @@ __global__ void __launch_bounds__(64 * kScanSumWaves) scan_bwd_summary_kernel(co
   const int nlast = static_cast<int>(L - t_last < T ? L - t_last : T);
   if (nlast == T) block(std::true_type{}, kl, T);
   else block(std::false_type{}, kl, nlast);
-  for (int64_t k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
+  for (int k = kl - 1; k >= kb0; --k) block(std::true_type{}, k, T);
 
   dts = row_allreduce16(dts);
   if (rc.active) {

@@ -70,8 +70,14 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // checkpoints, the last state and the chunk summaries.
   const int64_t N = sc.N, NS = p.nstride, n0 = sc.n0, L = p.seqlen;
   const int64_t row = rc.b * p.dim + rc.d;
-  const int64_t kb0 = chunk * p.chunk_blocks;  // this chunk's blocks: [kb0, kb1)
-  const int64_t kb1 = kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk;
+  // Block indices as uniform 32-bit values: the host's 32-bit tile-offset
+  // check keeps seqlen under 2^32 / (element size * channels per tile), so
+  // they stay far below 2^31, and the loop's tests on them become scalar
+  // compares (the scalar unit has no signed 64-bit compare).
+  // This chunk's blocks: [kb0, kb1).
+  const int kb0 = __builtin_amdgcn_readfirstlane(static_cast<int>(chunk * p.chunk_blocks));
+  const int kb1 = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(kb0 + p.chunk_blocks < p.nblk ? kb0 + p.chunk_blocks : p.nblk));
 
   float A2[SPL], h[SPL];
 #pragma unroll
@@ -101,7 +107,7 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   const uint32_t ck_off = static_cast<uint32_t>(sizeof(float) * (crow * p.nblk * NS + j));
   float dts = 0.f;  // sum of dt over this lane's steps (summary pass)
 
-  const int64_t tb0 = kb0 * kScanBlockT;
+  const int64_t tb0 = static_cast<int64_t>(kb0) * kScanBlockT;
   XStage<W> xu, xd, xz;
   xu.template init<Tx>(tid, p.u, p.su, p, rc, tb0);
   xd.template init<Tx>(tid, p.delta, p.sdl, p, rc, tb0);
@@ -169,9 +175,9 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
   // can be partial, so every fetch but the one of that block is unguarded:
   // the loop runs the blocks before the last two with plain fetches, then
   // the last two with guarded ones.
-  auto block = [&](auto GUARD, int64_t k) {
+  auto block = [&](auto GUARD, int k) {
     const int buf = static_cast<int>(k & 1);
-    const int64_t t0 = k * kScanBlockT;
+    const int64_t t0 = static_cast<int64_t>(k) * kScanBlockT;
     const bool has_next = k + 1 < kb1;
     fetch(GUARD, has_next ? t0 + kScanBlockT : t0, k + 2 >= kb1);
 
@@ -267,9 +273,9 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     }
     __syncthreads();
   };
-  const int64_t kg = kb1 - 2 > kb0 ? kb1 - 2 : kb0;  // first block whose fetch may be guarded
-  for (int64_t k = kb0; k < kg; ++k) block(std::false_type{}, k);
-  for (int64_t k = kg; k < kb1; ++k) block(std::true_type{}, k);
+  const int kg = kb1 - 2 > kb0 ? kb1 - 2 : kb0;  // first block whose fetch may be guarded
+  for (int k = kb0; k < kg; ++k) block(std::false_type{}, k);
+  for (int k = kg; k < kb1; ++k) block(std::true_type{}, k);
   if (MODE == kFwdSummary) {
     dts = row_allreduce16(dts);
     if (rc.active) {
