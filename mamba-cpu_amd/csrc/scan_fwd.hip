@@ -182,11 +182,12 @@ __global__ void __launch_bounds__(64 * kFwdWaves) scan_fwd_kernel(const ScanPara
     fetch(GUARD, has_next ? t0 + kScanBlockT : t0, k + 2 >= kb1);
 
     const int64_t t = t0 + j;
-    const bool tv = t < L;
+    const int nvalid = static_cast<int>(L - t0 < kScanBlockT ? L - t0 : kScanBlockT);
+    // This lane's step exists; unguarded blocks are always whole.
+    const bool tv = !decltype(GUARD)::value || j < nvalid;
     const float uu = s_x[buf][0][c_local][j];
     const float dl = s_x[buf][1][c_local][j];
     const float zz = (HAS_Z && WRITE_OUT) ? s_x[buf][2][c_local][j] : 0.f;
-    const int nvalid = static_cast<int>(L - t0 < kScanBlockT ? L - t0 : kScanBlockT);
 
     float Bv[SPL][kScanBlockT], Cv[SPL][kScanBlockT];
 #pragma unroll
